@@ -1,0 +1,168 @@
+/*
+ * ssla_hip.h -- C ABI of libssla_hip.so, the MI355X (gfx950) drain of the
+ * SSLA-S s2 + s3 + YOLOX-head path.
+ *
+ * Conventions for every entry point:
+ *   - plain C types and pointers only; no exceptions cross the boundary;
+ *   - int-returning calls return SSLA_OK (0) or a negative SSLA_ERR_* code,
+ *     and ssla_hip_last_error() then holds a message (per thread);
+ *   - "device pointer" means any pointer a gfx950 kernel may dereference:
+ *     memory from ssla_hip_malloc_device (HBM) or ssla_hip_malloc_host
+ *     (fine-grained, coherent, pinned host memory).
+ *
+ * Each entry cites the reference interface it replaces.  The reference
+ * drives its CUDA kernels through cuda-python; a HIP build cannot be driven
+ * that way, so the launches become host C functions with the same argument
+ * meaning, plus the allocation helpers the reference took from cuda-python.
+ */
+#ifndef SSLA_HIP_H
+#define SSLA_HIP_H
+
+#include <stddef.h>
+
+#include "ssla_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SSLA_OK          0
+#define SSLA_ERR_ARG    (-1)   /* bad argument or shape */
+#define SSLA_ERR_HIP    (-2)   /* HIP runtime failure */
+#define SSLA_ERR_IO     (-3)   /* file missing / unreadable */
+#define SSLA_ERR_FORMAT (-4)   /* weight directory does not follow the schema */
+#define SSLA_ERR_STATE  (-5)   /* call out of order */
+
+/* Last error message of the calling thread ("" when none). */
+const char* ssla_hip_last_error(void);
+
+/* Writes {sizeof HybridInputRec, sizeof HybridS2S3Config, offsetof preds,
+ * sizeof HybridS2S3OutputSlot, sizeof GpuTimingSlot, sizeof HybridStrip,
+ * sizeof LayerWeightsS2S3} into out[0..6] (cap >= 7).  Needs no GPU; lets
+ * ctypes mirrors check themselves (hybrid_common.py:30-123 asserts). */
+int ssla_hip_abi_layout(long long* out, int cap);
+
+/* ---- memory helpers --------------------------------------------------
+ * Replace orin/orin/cuda_util.py:39-48 (alloc_managed) and :59-76
+ * (alloc_pinned).  Host memory is hipHostMalloc'd fine-grained and
+ * coherent so the host may write rings / flags while a kernel polls them. */
+int ssla_hip_malloc_device(size_t nbytes, void** out);
+int ssla_hip_malloc_host(size_t nbytes, void** out);
+int ssla_hip_free_device(void* p);
+int ssla_hip_free_host(void* p);
+/* Synchronous copy in any direction (hipMemcpyDefault). */
+int ssla_hip_memcpy(void* dst, const void* src, size_t nbytes);
+int ssla_hip_memset(void* dst, int value, size_t nbytes);
+int ssla_hip_device_synchronize(void);
+
+/* ---- weight directory (tools/make_ssla_stub.py schema) ----------------
+ * Host-only readers (no GPU): replace vendor/src/weights_loader.cpp:162-252
+ * (load_meta) and :255-350 (load_weights_npz).  weights.npz must be stored
+ * (uncompressed) '<f4' C-order; ZIP64 entries are accepted.
+ * ssla_hip_npz_read copies tensor `key` into out (cap floats) and returns
+ * its element count, writing up to 4 dims into shape/ndim when non-NULL. */
+long long ssla_hip_npz_read(const char* weights_dir, const char* key,
+                            float* out, long long cap,
+                            long long* shape, int* ndim);
+/* out[0..3] = height, width, num_classes, ssla_tdrop_window */
+int ssla_hip_meta_read(const char* weights_dir, int* out);
+
+typedef struct SslaHipModel SslaHipModel;
+
+typedef struct SslaHipModelInfo {
+    int height, width;      /* sensor grid of meta.json */
+    int num_classes;
+    int tdrop_window;
+    int H2, W2, H3, W3;     /* s2 / s3 grids (height/4, width/4, /8) */
+    int has_head;           /* 2-branch YOLOX head present */
+} SslaHipModelInfo;
+
+/* Loads layers/4..7 and head level 0 of a weight directory into HBM in the
+ * device layouts of ssla_abi.h (fused q/v/g and gather-o weights, head BN
+ * folded).  Replaces multi_block.build_n_block_random_layers(npz=...)
+ * (orin/orin/multi_block.py:128-210) and hybrid_common.
+ * load_two_layer_head_weights (orin/orin/hybrid_common.py:352-409). */
+int  ssla_hip_model_load(const char* weights_dir, SslaHipModel** out);
+int  ssla_hip_model_info(const SslaHipModel* m, SslaHipModelInfo* out);
+void ssla_hip_model_free(SslaHipModel* m);
+
+/* ---- configuration and per-instance state -----------------------------
+ * ssla_hip_config_bind replaces hybrid_common.build_config
+ * (hybrid_common.py:214-271) / multi_block.build_n_block_config
+ * (multi_block.py:288-340) for weight-directory models: it zeroes *cfg,
+ * sets grid dims, tdrop window and head_out_dim, points every block's
+ * layers[] and the head at the model, and gives every block the whole grid
+ * as its owned strip (one ownership domain per block).  Buffers of
+ * hidden/tdrop/preds/version/timing stay NULL until allocated.
+ * ssla_hip_state_alloc allocates zeroed hidden state and tdrop counters for
+ * block `blk` in HBM (multi_block.py:180-181, alloc_tdrop_n_block :213-226);
+ * ssla_hip_preds_alloc allocates zeroed fine-grained host preds/version for
+ * the block's owned s3 box (alloc_predictions_n_block :229-252). */
+int  ssla_hip_config_bind(const SslaHipModel* m, int n_blocks,
+                          HybridS2S3Config* cfg);
+int  ssla_hip_state_alloc(HybridS2S3Config* cfg, int blk);
+int  ssla_hip_state_reset(const HybridS2S3Config* cfg, int blk);
+/* Same, enqueued on `stream` (hipStream_t or NULL) without waiting. */
+int  ssla_hip_state_reset_async(const HybridS2S3Config* cfg, int blk,
+                                void* stream);
+void ssla_hip_state_free(HybridS2S3Config* cfg, int blk);
+int  ssla_hip_preds_alloc(HybridS2S3Config* cfg, int blk);
+void ssla_hip_preds_free(HybridS2S3Config* cfg, int blk);
+
+/* ---- drain ----------------------------------------------------------
+ * Processes ns[b] pre-filled records of rings[b] for every block b <
+ * cfg->n_blocks, with the per-block hidden state and tdrop counters of
+ * cfg, exactly as if the records were processed one at a time in ring
+ * order: L4, L5, tdrop_s2 at the s2 cell, L6, L7, tdrop_s3 at the s3 cell,
+ * then (when head weights and preds are set) the YOLOX head for owned
+ * pass-3 records, last write per s3 cell winning.
+ * Replaces the kernels k_ssla_s2s3_celled_drain_n_multi
+ * (orin/kernels/ssla_s2_s3_head_celled.cuh:1108-1255) and
+ * k_ssla_s2s3_celled_drain_n (:914-1095).
+ *   cfg        host pointer; its pointer members are device pointers
+ *   rings[b]   device pointer to ns[b] records (x, y in s2 coordinates)
+ *   outs[b]    NULL or device pointer to ns[b] output slots: pass2/pass3 as
+ *              1/0 for owned records and -1 for halo records; s3_feat holds
+ *              the L7 output for pass-3 records and zeros otherwise
+ *   batch_clks must be NULL (per-8-record clock pairs do not exist in the
+ *              whole-ring scan; see ssla_hip_drain_n_ex / timing)
+ * Records outside the s2 grid leave all state untouched and report
+ * pass2 = pass3 = -2.  Synchronous.  Weights must be shared by all blocks. */
+int ssla_hip_drain_n(const HybridS2S3Config* cfg,
+                     const HybridInputRec* const* rings, const int* ns,
+                     HybridS2S3OutputSlot* const* outs,
+                     unsigned long long* const* batch_clks);
+
+/* Two-ring form of the same call (the reference's P1 entry signature). */
+int ssla_hip_drain_n2(const HybridS2S3Config* cfg,
+                      const HybridInputRec* ring0, const HybridInputRec* ring1,
+                      int n0, int n1,
+                      HybridS2S3OutputSlot* out0, HybridS2S3OutputSlot* out1);
+
+#define SSLA_DRAIN_PHASES 15
+/* Phase order of SslaHipDrainOpts.phase_ms: 0 ordering (decode, sorts,
+ * tdrop decisions), then for L4, L5, L6, L7 in turn: projection, per-cell
+ * recurrence, gather + LayerNorm (1..12), 13 head, 14 output slots. */
+
+typedef struct SslaHipDrainOpts {
+    void*         stream;      /* hipStream_t; NULL = default stream */
+    int           sync;        /* nonzero: wait for completion */
+    int           reserved;
+    float* const* head_outs;   /* NULL or [n_blocks] device pointers to
+                                  (ns[b], 7) raw head outputs, written for
+                                  owned pass-3 records, zeros otherwise */
+    float*        phase_ms;    /* NULL or host float[SSLA_DRAIN_PHASES]:
+                                  adds the GPU time of each phase, measured
+                                  with HIP events on `stream` (needs sync) */
+} SslaHipDrainOpts;
+
+int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg,
+                        const HybridInputRec* const* rings, const int* ns,
+                        HybridS2S3OutputSlot* const* outs,
+                        const SslaHipDrainOpts* opts);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SSLA_HIP_H */

@@ -1,0 +1,315 @@
+"""ctypes binding of the CPU oracle (oracle/libssla_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+the cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.
+The product (libssla_hip.so and its Python host side) never imports it.
+
+The C sources (ssla_oracle.c, ssla_oracle_f32.c) list the reference file:line
+each function restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Dict, List, Optional, Sequence
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libssla_oracle.so"
+REF_LIB_PATH = HERE / "_ref" / "libssla_ref.so"
+
+C1, C2, C3 = 24, 48, 96
+GPU_LAYER_IO = ((C1, C2), (C2, C2), (C2, C3), (C3, C3))
+
+_FP = ctypes.POINTER(ctypes.c_float)
+
+
+class OracleLayer(ctypes.Structure):
+    _fields_ = [("qvgIn", _FP), ("goW", _FP), ("input_proj", _FP),
+                ("ln_gamma", _FP), ("ln_beta", _FP),
+                ("in_dim", ctypes.c_int), ("out_dim", ctypes.c_int), ("K", ctypes.c_int)]
+
+
+class OracleHead(ctypes.Structure):
+    _fields_ = [(n, _FP) for n in ("cls_conv_W", "cls_conv_b", "cls_pred_W", "cls_pred_b",
+                                   "reg_conv_W", "reg_conv_b", "reg_pred_W", "reg_pred_b",
+                                   "obj_pred_W", "obj_pred_b")] + [("C", ctypes.c_int)]
+
+
+class OracleS2S3(ctypes.Structure):
+    _fields_ = [("L", OracleLayer * 4), ("H", _FP * 4),
+                ("td2", ctypes.POINTER(ctypes.c_uint8)), ("td3", ctypes.POINTER(ctypes.c_uint8)),
+                ("H2", ctypes.c_int), ("W2", ctypes.c_int), ("H3", ctypes.c_int), ("W3", ctypes.c_int),
+                ("window", ctypes.c_int), ("head", ctypes.POINTER(OracleHead))]
+
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(HERE), "all"], check=True)
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.oracle_reshape_layer.restype = ctypes.c_int
+        L.oracle_reshape_layer.argtypes = [_FP, ctypes.c_int, _FP, ctypes.c_int, _FP, _FP, _FP, _FP,
+                                           ctypes.c_int, ctypes.c_int, _FP, _FP]
+        for nm in ("oracle_layer_step_f64", "oracle_layer_step_f32"):
+            f = getattr(L, nm)
+            f.restype = None
+            f.argtypes = [ctypes.POINTER(OracleLayer), _FP, _FP, ctypes.c_int, ctypes.c_int,
+                          ctypes.c_int, ctypes.c_int, _FP]
+        L.oracle_tdrop.restype = ctypes.c_int
+        L.oracle_tdrop.argtypes = [ctypes.POINTER(ctypes.c_uint8), ctypes.c_int, ctypes.c_int]
+        L.oracle_s2s3_run.restype = ctypes.c_int
+        L.oracle_s2s3_run.argtypes = [ctypes.POINTER(OracleS2S3), ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p]
+        L.oracle_s2s3_decisions.restype = ctypes.c_int
+        L.oracle_s2s3_decisions.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                            ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                            ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                            ctypes.c_void_p]
+        for nm in ("oracle_head_raw_f64", "oracle_head_raw_f32"):
+            f = getattr(L, nm)
+            f.restype = None
+            f.argtypes = [ctypes.POINTER(OracleHead), _FP, _FP]
+        L.oracle_fuse_conv_bn.restype = None
+        L.oracle_fuse_conv_bn.argtypes = [_FP, _FP, _FP, _FP, _FP, _FP, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_float, _FP, _FP]
+        _lib = L
+    return _lib
+
+
+def _fp(a: Optional[np.ndarray]):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_FP)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---- layers -------------------------------------------------------------------
+
+@dataclass
+class Layer:
+    """Fused weights in the oracle layout (qvgIn (A, 3D, in), goW (A, D, D))."""
+    qvgIn: np.ndarray
+    goW: np.ndarray
+    input_proj: Optional[np.ndarray]
+    ln_gamma: np.ndarray
+    ln_beta: np.ndarray
+    K: int = 3
+
+    def c(self) -> OracleLayer:
+        A, three_d, i = self.qvgIn.shape
+        for a in (self.qvgIn, self.goW, self.input_proj, self.ln_gamma, self.ln_beta):
+            if a is not None:
+                assert a.dtype == np.float32 and a.flags.c_contiguous
+        return OracleLayer(_fp(self.qvgIn), _fp(self.goW), _fp(self.input_proj),
+                           _fp(self.ln_gamma), _fp(self.ln_beta), i, three_d // 3, self.K)
+
+
+def reshape(W_in_cat, W_out_cat, qW, vW, gW, oW):
+    """oracle_reshape_layer: returns (qvgIn (A, 3D, in), goW (A, D, D))."""
+    Win, Wout = _f32(W_in_cat), _f32(W_out_cat)
+    q, v, g, o = (_f32(a) for a in (qW, vW, gW, oW))
+    in_dim, D = Win.shape[0], q.shape[0]
+    A = max(Win.shape[1] // D, Wout.shape[0] // D)
+    qvg = np.zeros((A, 3 * D, in_dim), np.float32)
+    go = np.zeros((A, D, D), np.float32)
+    rc = load().oracle_reshape_layer(_fp(Win), Win.shape[1], _fp(Wout), Wout.shape[0],
+                                     _fp(q), _fp(v), _fp(g), _fp(o), in_dim, D, _fp(qvg), _fp(go))
+    if rc < 0:
+        raise ValueError("oracle_reshape_layer rejected the shapes")
+    return qvg, go
+
+
+def layer_from_raw(raw) -> Layer:
+    qvg, go = reshape(raw.W_in_cat, raw.W_out_cat, raw.qW, raw.vW, raw.gW, raw.oW)
+    K = 3 if qvg.shape[0] == 9 else 1
+    ip = None if raw.input_proj is None else _f32(raw.input_proj)
+    return Layer(qvg, go, ip, _f32(raw.ln_gamma), _f32(raw.ln_beta), K)
+
+
+def layer_step(layer: Layer, x: np.ndarray, H: np.ndarray, ev_x: int, ev_y: int,
+               Hl: int, Wl: int, precision: int = 64) -> np.ndarray:
+    out = np.zeros(layer.goW.shape[1], np.float32)
+    x = _f32(x)
+    assert H.dtype == np.float32 and H.flags.c_contiguous
+    L = layer.c()
+    f = load().oracle_layer_step_f64 if precision == 64 else load().oracle_layer_step_f32
+    f(ctypes.byref(L), _fp(x), _fp(H), ev_x, ev_y, Hl, Wl, _fp(out))
+    return out
+
+
+# ---- head -------------------------------------------------------------------
+
+def fuse_conv_bn(W, b_conv, bn_w, bn_b, bn_mu, bn_var, eps: float = 1e-5):
+    W = _f32(W).reshape(W.shape[0], -1)
+    co, ci = W.shape
+    Wo = np.zeros_like(W)
+    bo = np.zeros(co, np.float32)
+    load().oracle_fuse_conv_bn(_fp(W), _fp(None if b_conv is None else _f32(b_conv)), _fp(_f32(bn_w)),
+                               _fp(_f32(bn_b)), _fp(_f32(bn_mu)), _fp(_f32(bn_var)), co, ci, eps,
+                               _fp(Wo), _fp(bo))
+    return Wo, bo
+
+
+@dataclass
+class Head:
+    arrays: Dict[str, np.ndarray]
+
+    def c(self) -> OracleHead:
+        a = self.arrays
+        return OracleHead(*[_fp(a[k]) for k in ("cls_conv_W", "cls_conv_b", "cls_pred_W",
+                                                 "cls_pred_b", "reg_conv_W", "reg_conv_b",
+                                                 "reg_pred_W", "reg_pred_b", "obj_pred_W",
+                                                 "obj_pred_b")], 96)
+
+
+def head_from_npz(w) -> Head:
+    """BN-fold level 0 of a weights.npz mapping (hybrid_common.py:352-409)."""
+    a = {}
+    for br, tag in (("cls_convs", "cls"), ("reg_convs", "reg")):
+        base = f"head/{br}/0"
+        bias_key = f"{base}/0/bias"
+        b = w[bias_key] if bias_key in w else None
+        a[f"{tag}_conv_W"], a[f"{tag}_conv_b"] = fuse_conv_bn(
+            w[f"{base}/0/weight"], b, w[f"{base}/1/weight"], w[f"{base}/1/bias"],
+            w[f"{base}/1/running_mean"], w[f"{base}/1/running_var"])
+    for tag in ("cls", "reg", "obj"):
+        a[f"{tag}_pred_W"] = _f32(w[f"head/{tag}_preds/0/weight"]).reshape(-1, 96).copy()
+        a[f"{tag}_pred_b"] = _f32(w[f"head/{tag}_preds/0/bias"]).copy()
+    return Head(a)
+
+
+def head_raw(head: Head, x: np.ndarray, precision: int = 64) -> np.ndarray:
+    out = np.zeros(7, np.float32)
+    h = head.c()
+    f = load().oracle_head_raw_f64 if precision == 64 else load().oracle_head_raw_f32
+    f(ctypes.byref(h), _fp(_f32(x)), _fp(out))
+    return out
+
+
+# ---- weight directory -------------------------------------------------------------
+
+def load_npz(weights_dir: str) -> Dict[str, np.ndarray]:
+    with np.load(str(Path(weights_dir) / "weights.npz"), allow_pickle=False) as z:
+        return {k: np.array(z[k]) for k in z.files}
+
+
+def layers_from_npz(w) -> List[Layer]:
+    """Layers 4..7 of the sorted SSLA layer indices (ssla_kernels.cpp:178-198)."""
+    idx = sorted(int(k.split("/")[1]) for k in w if k.startswith("layers/") and k.endswith("/W_in_cat"))
+    out = []
+    for li in range(4):
+        p = f"layers/{idx[4 + li]}"
+        qvg, go = reshape(w[f"{p}/W_in_cat"], w[f"{p}/W_out_cat"], w[f"{p}/q_proj/weight"],
+                          w[f"{p}/v_proj/weight"], w[f"{p}/g_proj/weight"], w[f"{p}/o_proj/weight"])
+        ipk = f"{p}/input_proj/weight"
+        out.append(Layer(qvg, go, _f32(w[ipk]) if ipk in w else None,
+                         _f32(w[f"{p}/norm/weight"]), _f32(w[f"{p}/norm/bias"])))
+    return out
+
+
+# ---- the drain schedule ---------------------------------------------------------------
+
+class S2S3:
+    """One drain instance: layers L4..L7, hidden state, tdrop counters."""
+
+    def __init__(self, layers: Sequence[Layer], H2: int, W2: int, window: int,
+                 h_init: Optional[Sequence[np.ndarray]] = None, head: Optional[Head] = None):
+        self.layers = list(layers)
+        self.H2, self.W2, self.H3, self.W3 = H2, W2, H2 >> 1, W2 >> 1
+        self.window = window
+        cells = (H2 * W2, H2 * W2, self.H3 * self.W3, self.H3 * self.W3)
+        self.H = [np.zeros((cells[li], GPU_LAYER_IO[li][1]), np.float32) for li in range(4)]
+        if h_init is not None:
+            for li in range(4):
+                self.H[li][...] = h_init[li]
+        self.td2 = np.zeros(H2 * W2, np.uint8)
+        self.td3 = np.zeros(self.H3 * self.W3, np.uint8)
+        self.head = head
+
+    def run(self, x, y, feat1, owner=None, precision: int = 64, want_feat: bool = True,
+            want_head: bool = False):
+        n = len(x)
+        x = np.ascontiguousarray(x, np.uint16)
+        y = np.ascontiguousarray(y, np.uint16)
+        f = _f32(feat1).reshape(n, C1)
+        own = None if owner is None else np.ascontiguousarray(owner, np.uint8)
+        p2 = np.zeros(n, np.int8)
+        p3 = np.zeros(n, np.int8)
+        feat = np.zeros((n, C3), np.float32) if want_feat else None
+        head7 = np.zeros((n, 7), np.float32) if want_head else None
+        st = OracleS2S3()
+        for li in range(4):
+            st.L[li] = self.layers[li].c()
+            st.H[li] = _fp(self.H[li])
+        st.td2 = self.td2.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8))
+        st.td3 = self.td3.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8))
+        st.H2, st.W2, st.H3, st.W3 = self.H2, self.W2, self.H3, self.W3
+        st.window = self.window
+        hc = None
+        if want_head:
+            if self.head is None:
+                raise ValueError("no head weights")
+            hc = self.head.c()
+            st.head = ctypes.pointer(hc)
+        rc = load().oracle_s2s3_run(ctypes.byref(st), x.ctypes.data, y.ctypes.data, f.ctypes.data,
+                                    None if own is None else own.ctypes.data, n, precision,
+                                    p2.ctypes.data, p3.ctypes.data,
+                                    None if feat is None else feat.ctypes.data,
+                                    None if head7 is None else head7.ctypes.data)
+        if rc < 0:
+            raise ValueError("oracle_s2s3_run rejected its arguments")
+        return p2, p3, feat, head7
+
+
+def decisions(x, y, H2: int, W2: int, window: int, td2=None, td3=None):
+    """Pass flags only (the same tdrop schedule), for full-size checks."""
+    n = len(x)
+    x = np.ascontiguousarray(x, np.uint16)
+    y = np.ascontiguousarray(y, np.uint16)
+    td2 = np.zeros(H2 * W2, np.uint8) if td2 is None else td2
+    td3 = np.zeros((H2 >> 1) * (W2 >> 1), np.uint8) if td3 is None else td3
+    p2 = np.zeros(n, np.int8)
+    p3 = np.zeros(n, np.int8)
+    load().oracle_s2s3_decisions(td2.ctypes.data, td3.ctypes.data, H2, W2, window,
+                                 x.ctypes.data, y.ctypes.data, n, p2.ctypes.data, p3.ctypes.data)
+    return p2, p3, td2, td3
+
+
+# ---- the reference checker (oracle/_ref) ------------------------------------------
+
+def load_ref() -> Optional[ctypes.CDLL]:
+    """libssla_ref.so built from the reference's own CPU sources, or None."""
+    if not REF_LIB_PATH.exists():
+        return None
+    L = ctypes.CDLL(str(REF_LIB_PATH))
+    L.ref_meta.restype = ctypes.c_int
+    L.ref_meta.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)]
+    L.ref_tensor.restype = ctypes.c_int
+    L.ref_tensor.argtypes = [ctypes.c_char_p, ctypes.c_char_p, _FP, ctypes.c_int]
+    L.ref_head_decode.restype = ctypes.c_int
+    L.ref_head_decode.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, _FP, _FP]
+    L.ref_layernorm.restype = ctypes.c_int
+    L.ref_layernorm.argtypes = [_FP, ctypes.c_int, _FP, _FP]
+    L.ref_lru_step.restype = ctypes.c_int
+    L.ref_lru_step.argtypes = [_FP, _FP, _FP, _FP, _FP, ctypes.c_int]
+    L.ref_mm.restype = ctypes.c_int
+    L.ref_mm.argtypes = [_FP, ctypes.c_int, ctypes.c_int, _FP, ctypes.c_int, _FP]
+    return L

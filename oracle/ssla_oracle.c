@@ -1,0 +1,330 @@
+/*
+ * ssla_oracle.c -- CPU restatement of the SSLA-S s2+s3+head drain path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see ssla_oracle.h for the rules and the list of
+ * reference files each function follows).  Built by oracle/Makefile into
+ * oracle/libssla_oracle.so with the reference CPU build's flags
+ * (CMakeLists.txt:18-25: -O3 -march=native -ffast-math) for the fp32 path;
+ * the fp64 path is compiled in a separate translation unit without
+ * -ffast-math so its summation order is the one written here.
+ */
+#include "ssla_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define MAXD 96          /* largest channel count on the path (C3) */
+
+/* ------------------------------------------------------------------------ */
+/* reshape (weights_ssla.py:24-88, ssla_kernels.cpp:73-153)                 */
+/* ------------------------------------------------------------------------ */
+
+/* C = B @ A with B (bo, bi), A (bi, ai); k-outer accumulation in fp32 as in
+ * vendor/openeva/prim/matmul.h:22-38.                                       */
+static void mm_f32(const float* B, int bo, int bi, const float* A, int ai,
+                   float* C) {
+    for (int o = 0; o < bo; ++o) {
+        float* cr = C + (size_t)o * ai;
+        for (int i = 0; i < ai; ++i) cr[i] = 0.0f;
+        for (int k = 0; k < bi; ++k) {
+            const float bv = B[(size_t)o * bi + k];
+            const float* ar = A + (size_t)k * ai;
+            for (int i = 0; i < ai; ++i) cr[i] += bv * ar[i];
+        }
+    }
+}
+
+int oracle_reshape_layer(const float* W_in_cat, int win_cols,
+                         const float* W_out_cat, int wout_rows,
+                         const float* qW, const float* vW,
+                         const float* gW, const float* oW,
+                         int in_dim, int D, float* qvgIn, float* goW) {
+    if (D <= 0 || D > MAXD || in_dim <= 0 || in_dim > MAXD) return -1;
+    if (win_cols % D != 0 || wout_rows % D != 0) return -1;
+    const int n_in = win_cols / D, n_out = wout_rows / D;
+    const int A = n_in > n_out ? n_in : n_out;
+    float* scatter = (float*)malloc(sizeof(float) * D * in_dim);
+    float* gather = (float*)malloc(sizeof(float) * D * D);
+    if (!scatter || !gather) { free(scatter); free(gather); return -1; }
+    for (int p = 0; p < A; ++p) {
+        const int pin = (n_in == 1) ? 0 : p;
+        const int pout = (n_out == 1) ? 0 : p;
+        /* scatter[d, c] = W_in_cat[c, pin*D + d] */
+        for (int d = 0; d < D; ++d)
+            for (int c = 0; c < in_dim; ++c)
+                scatter[(size_t)d * in_dim + c] =
+                    W_in_cat[(size_t)c * win_cols + (size_t)pin * D + d];
+        /* gather[i, j] = W_out_cat[pout*D + j, i] */
+        for (int i = 0; i < D; ++i)
+            for (int j = 0; j < D; ++j)
+                gather[(size_t)i * D + j] =
+                    W_out_cat[((size_t)pout * D + j) * D + i];
+        float* qvg = qvgIn + (size_t)p * 3 * D * in_dim;
+        mm_f32(qW, D, D, scatter, in_dim, qvg);
+        mm_f32(vW, D, D, scatter, in_dim, qvg + (size_t)D * in_dim);
+        mm_f32(gW, D, D, scatter, in_dim, qvg + (size_t)2 * D * in_dim);
+        mm_f32(gather, D, D, oW, D, goW + (size_t)p * D * D);
+    }
+    free(scatter);
+    free(gather);
+    return A;
+}
+
+/* ------------------------------------------------------------------------ */
+/* patch walk shared by both precisions                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Fills (cell index, delta) for the in-bounds patch cells of an event, in
+ * the order the reference visits them: interior events use the fixed
+ * delta 8..0 table (ssla_ref.py:72-77, ssla_kernels.cpp:349-358); events on
+ * the border walk dy, dx = -1..1 with delta = (1-dy)*3 + (1-dx)
+ * (ssla_ref.py:79-86).  K = 1 visits only the centre with delta 0.         */
+static int patch_list(int K, int ev_x, int ev_y, int Hl, int Wl,
+                      int cells[9], int deltas[9]) {
+    if (K == 1) {
+        cells[0] = ev_y * Wl + ev_x;
+        deltas[0] = 0;
+        return 1;
+    }
+    const int base = ev_y * Wl + ev_x;
+    const int interior = ev_x > 0 && ev_x + 1 < Wl && ev_y > 0 && ev_y + 1 < Hl;
+    if (interior) {
+        const int offs[9] = {-Wl - 1, -Wl, -Wl + 1, -1, 0, 1, Wl - 1, Wl, Wl + 1};
+        for (int k = 0; k < 9; ++k) {
+            cells[k] = base + offs[k];
+            deltas[k] = 8 - k;
+        }
+        return 9;
+    }
+    int n = 0;
+    for (int dy = -1; dy <= 1; ++dy) {
+        const int py = ev_y + dy;
+        if (py < 0 || py >= Hl) continue;
+        for (int dx = -1; dx <= 1; ++dx) {
+            const int px = ev_x + dx;
+            if (px < 0 || px >= Wl) continue;
+            cells[n] = py * Wl + px;
+            deltas[n] = (1 - dy) * 3 + (1 - dx);
+            ++n;
+        }
+    }
+    return n;
+}
+
+/* fp64 LayerNorm over OUT values with eps = 1e-5, affine in fp64 then cast
+ * (ssla_ref.py:88-93; layernorm.h:40-60 does the same in fp64).            */
+static void layernorm_f64(const double* y, int D, const float* gamma,
+                          const float* beta, float* out) {
+    double sum = 0.0;
+    for (int i = 0; i < D; ++i) sum += y[i];
+    const double mean = sum / (double)D;
+    double var = 0.0;
+    for (int i = 0; i < D; ++i) {
+        const double d = y[i] - mean;
+        var += d * d;
+    }
+    var /= (double)D;
+    const double inv = 1.0 / sqrt(var + 1e-5);
+    for (int i = 0; i < D; ++i)
+        out[i] = (float)((y[i] - mean) * inv * (double)gamma[i] + (double)beta[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* layer_step, fp64 (ssla_ref.py:17-93)                                     */
+/* ------------------------------------------------------------------------ */
+
+void oracle_layer_step_f64(const OracleLayer* L, const float* in,
+                           float* H_all, int ev_x, int ev_y, int Hl, int Wl,
+                           float* out) {
+    const int IN = L->in_dim, D = L->out_dim;
+    double acc[MAXD], res[MAXD], qvg[3 * MAXD], qh[MAXD];
+    if (L->input_proj) {
+        for (int o = 0; o < D; ++o) {
+            double s = 0.0;
+            const float* w = L->input_proj + (size_t)o * IN;
+            for (int i = 0; i < IN; ++i) s += (double)w[i] * (double)in[i];
+            res[o] = s;
+        }
+    } else {
+        for (int o = 0; o < D; ++o) res[o] = (double)in[o];
+    }
+    for (int o = 0; o < D; ++o) acc[o] = 0.0;
+
+    int cells[9], deltas[9];
+    const int np = patch_list(L->K, ev_x, ev_y, Hl, Wl, cells, deltas);
+    for (int k = 0; k < np; ++k) {
+        const int p = deltas[k];
+        const float* W = L->qvgIn + (size_t)p * 3 * D * IN;
+        for (int r = 0; r < 3 * D; ++r) {
+            double s = 0.0;
+            const float* w = W + (size_t)r * IN;
+            for (int i = 0; i < IN; ++i) s += (double)w[i] * (double)in[i];
+            qvg[r] = s;
+        }
+        float* h = H_all + (size_t)cells[k] * D;
+        for (int o = 0; o < D; ++o) {
+            const double gc = 1.0 / (1.0 + exp(-qvg[2 * D + o]));
+            const double hn = gc * (double)h[o] + qvg[D + o];
+            h[o] = (float)hn;              /* stored back as fp32 */
+            qh[o] = qvg[o] * hn;           /* q * h_new in fp64 */
+        }
+        const float* G = L->goW + (size_t)p * D * D;
+        for (int o = 0; o < D; ++o) {
+            double s = 0.0;
+            const float* g = G + (size_t)o * D;
+            for (int i = 0; i < D; ++i) s += (double)g[i] * qh[i];
+            acc[o] += s;
+        }
+    }
+    for (int o = 0; o < D; ++o) acc[o] += res[o];
+    layernorm_f64(acc, D, L->ln_gamma, L->ln_beta, out);
+}
+
+/* ------------------------------------------------------------------------ */
+/* tdrop (ssla_ref.py:190-195, ssla_kernels.cpp:912-921)                    */
+/* ------------------------------------------------------------------------ */
+
+int oracle_tdrop(uint8_t* counter, int window, int idx) {
+    const uint8_t pre = counter[idx];
+    counter[idx] = (uint8_t)(pre + 1u);
+    if (window <= 1) return 1;
+    return (pre % (unsigned)window) == 0u;
+}
+
+/* ------------------------------------------------------------------------ */
+/* head (…celled.cuh:841-902): y = SiLU(Wc x + bc) -> cls; y' = SiLU(Wr x +
+ * br) -> reg, obj; output [reg0..3, obj, cls0, cls1]                       */
+/* ------------------------------------------------------------------------ */
+
+void oracle_head_raw_f64(const OracleHead* h, const float* x, float out7[7]) {
+    const int C = h->C;
+    double yc[MAXD], yr[MAXD];
+    for (int o = 0; o < C; ++o) {
+        double a = (double)h->cls_conv_b[o], b = (double)h->reg_conv_b[o];
+        const float* wc = h->cls_conv_W + (size_t)o * C;
+        const float* wr = h->reg_conv_W + (size_t)o * C;
+        for (int i = 0; i < C; ++i) {
+            a += (double)wc[i] * (double)x[i];
+            b += (double)wr[i] * (double)x[i];
+        }
+        yc[o] = a / (1.0 + exp(-a));
+        yr[o] = b / (1.0 + exp(-b));
+    }
+    for (int k = 0; k < 4; ++k) {
+        double s = (double)h->reg_pred_b[k];
+        for (int i = 0; i < C; ++i) s += (double)h->reg_pred_W[(size_t)k * C + i] * yr[i];
+        out7[k] = (float)s;
+    }
+    {
+        double s = (double)h->obj_pred_b[0];
+        for (int i = 0; i < C; ++i) s += (double)h->obj_pred_W[i] * yr[i];
+        out7[4] = (float)s;
+    }
+    for (int k = 0; k < 2; ++k) {
+        double s = (double)h->cls_pred_b[k];
+        for (int i = 0; i < C; ++i) s += (double)h->cls_pred_W[(size_t)k * C + i] * yc[i];
+        out7[5 + k] = (float)s;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* decisions (bench_s2_s3_head_celled.py:70-84)                             */
+/* ------------------------------------------------------------------------ */
+
+static int in_grid(int x, int y, int H, int W) {
+    return x >= 0 && x < W && y >= 0 && y < H;
+}
+
+int oracle_s2s3_decisions(uint8_t* td2, uint8_t* td3, int H2, int W2,
+                          int window, const uint16_t* xs, const uint16_t* ys,
+                          int n, int8_t* pass2, int8_t* pass3) {
+    if (n < 0 || H2 <= 0 || W2 <= 0) return -1;
+    const int W3 = W2 >> 1;
+    int n3 = 0;
+    for (int i = 0; i < n; ++i) {
+        const int x = xs[i], y = ys[i];
+        int p2 = -2, p3 = -2;
+        if (in_grid(x, y, H2, W2)) {
+            p2 = oracle_tdrop(td2, window, y * W2 + x);
+            p3 = 0;
+            if (p2) {
+                p3 = oracle_tdrop(td3, window, (y >> 1) * W3 + (x >> 1));
+                n3 += p3;
+            }
+        }
+        if (pass2) pass2[i] = (int8_t)p2;
+        if (pass3) pass3[i] = (int8_t)p3;
+    }
+    return n3;
+}
+
+/* ------------------------------------------------------------------------ */
+/* full schedule, both precisions                                           */
+/* ------------------------------------------------------------------------ */
+
+typedef void (*layer_fn)(const OracleLayer*, const float*, float*, int, int,
+                         int, int, float*);
+
+int oracle_s2s3_run(OracleS2S3* st, const uint16_t* xs, const uint16_t* ys,
+                    const float* feat1, const uint8_t* owner, int n,
+                    int precision, int8_t* pass2, int8_t* pass3,
+                    float* s3_feat, float* head7) {
+    if (!st || n < 0 || (precision != 32 && precision != 64)) return -1;
+    if (st->H2 <= 0 || st->W2 <= 0 || (st->H2 & 1) || (st->W2 & 1)) return -1;
+    if (head7 && !st->head) return -1;
+    const layer_fn step = (precision == 64) ? oracle_layer_step_f64
+                                            : oracle_layer_step_f32;
+    const int H2 = st->H2, W2 = st->W2, H3 = st->H3, W3 = st->W3;
+    float b4[MAXD], b5[MAXD], b6[MAXD], b7[MAXD];
+    int n3 = 0;
+    for (int i = 0; i < n; ++i) {
+        const int x = xs[i], y = ys[i];
+        int p2 = -2, p3 = -2;
+        if (s3_feat) memset(s3_feat + (size_t)i * 96, 0, sizeof(float) * 96);
+        if (head7) memset(head7 + (size_t)i * 7, 0, sizeof(float) * 7);
+        if (in_grid(x, y, H2, W2)) {
+            const float* f = feat1 + (size_t)i * 24;
+            step(&st->L[0], f, st->H[0], x, y, H2, W2, b4);
+            step(&st->L[1], b4, st->H[1], x, y, H2, W2, b5);
+            p2 = oracle_tdrop(st->td2, st->window, y * W2 + x);
+            p3 = 0;
+            if (p2) {
+                const int sx = x >> 1, sy = y >> 1;
+                step(&st->L[2], b5, st->H[2], sx, sy, H3, W3, b6);
+                step(&st->L[3], b6, st->H[3], sx, sy, H3, W3, b7);
+                p3 = oracle_tdrop(st->td3, st->window, sy * W3 + sx);
+                if (p3) {
+                    ++n3;
+                    if (s3_feat) memcpy(s3_feat + (size_t)i * 96, b7, sizeof(float) * 96);
+                    if (head7 && (!owner || owner[i])) {
+                        if (precision == 64) oracle_head_raw_f64(st->head, b7, head7 + (size_t)i * 7);
+                        else oracle_head_raw_f32(st->head, b7, head7 + (size_t)i * 7);
+                    }
+                }
+            }
+        }
+        if (pass2) pass2[i] = (int8_t)p2;
+        if (pass3) pass3[i] = (int8_t)p3;
+    }
+    return n3;
+}
+
+/* ------------------------------------------------------------------------ */
+/* BN fold (hybrid_common.py:327-349)                                       */
+/* ------------------------------------------------------------------------ */
+
+void oracle_fuse_conv_bn(const float* W, const float* b_conv_or_null,
+                         const float* bn_w, const float* bn_b,
+                         const float* bn_mu, const float* bn_var,
+                         int c_out, int c_in, float eps,
+                         float* W_out, float* b_out) {
+    for (int o = 0; o < c_out; ++o) {
+        const float scale = bn_w[o] / sqrtf(bn_var[o] + eps);
+        const float shift = bn_b[o] - scale * bn_mu[o];
+        for (int i = 0; i < c_in; ++i)
+            W_out[(size_t)o * c_in + i] = W[(size_t)o * c_in + i] * scale;
+        const float bc = b_conv_or_null ? b_conv_or_null[o] : 0.0f;
+        b_out[o] = bc * scale + shift;
+    }
+}

@@ -1,0 +1,900 @@
+// drain_scan.hip -- whole-ring drain of SSLA-S s2 + s3 + YOLOX head on gfx950.
+//
+// The reference drains a ring 8 records at a time in one 9-warp block per
+// ring (orin/kernels/ssla_s2_s3_head_celled.cuh:914-1255), so at most 8
+// records are in flight per block.  This file re-derives the same result
+// for a whole pre-filled ring at once, using the structure of one SSLA layer
+// (orin/orin/ssla_ref.py:17-93):
+//
+//   for every in-bounds patch cell c of event e (offset delta):
+//       q, v, g = qvgIn[delta] x_e                    (depends on x_e only)
+//       h_c     = sigmoid(g) * h_c + v                (ordered per cell)
+//       qh      = q * h_c
+//   y_e = LN( sum_delta goW[delta] qh + residual(x_e) )
+//
+// Only the h_c recurrence is ordered, and only among events touching the
+// same cell.  Per layer the drain therefore runs three phases over all
+// records of all rings:
+//   P  (k_qvg)   q, v, g for every (record, delta) pair, written in
+//                per-cell ring order (pair rows sorted by target cell)
+//   S  (k_scan)  one workgroup per cell walks its pairs in ring order and
+//                turns (q, v, g) rows into q*h rows in place
+//   O  (k_out)   per record: gather the <= 9 q*h rows, goW contraction,
+//                residual, fp64 LayerNorm
+// The temporal-dropout decisions (ssla_ref.py:190-195) depend only on the
+// per-cell arrival rank of a record, so they come from a stable sort of
+// records by cell: pass = ((counter + rank) mod 256) % window == 0.
+// Results equal sequential processing in ring order up to fp32 summation
+// order; drop decisions are bit-exact.
+//
+// Device layouts are those of include/ssla_abi.h.
+#include <hip/hip_runtime.h>
+#include <hipcub/hipcub.hpp>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "drain_scan.h"
+
+namespace ssla {
+
+namespace {
+
+constexpr int kPatch = 9;
+constexpr int kTE = 32;              // records per projection / output tile
+
+struct BlockDesc {
+    const HybridInputRec* ring;
+    HybridS2S3OutputSlot* out;
+    float*                head_out;
+    float*                hidden[4];
+    unsigned char*        td2;
+    unsigned char*        td3;
+    float*                preds;
+    unsigned int*         version;
+    HybridStrip           strip;
+    int                   n;
+    int                   offset;
+};
+
+struct Geometry {
+    int H2, W2, H3, W3;
+    int C2, C3;          // cells per block at s2 / s3
+    int nb;              // blocks
+    int window;
+};
+
+__device__ __forceinline__ float sigmoid_fast(float x) {
+    return __fdividef(1.0f, 1.0f + __expf(-x));
+}
+
+__device__ __forceinline__ int find_block(const BlockDesc* bd, int nb, int g) {
+    int b = 0;
+    for (int i = 1; i < nb; ++i)
+        if (g >= bd[i].offset) b = i;
+    return b;
+}
+
+// ---------------------------------------------------------------------------
+// decode: ring records -> compact features, centre cells, sort keys
+// ---------------------------------------------------------------------------
+__global__ void k_decode(int E, const BlockDesc* __restrict__ bd, Geometry G,
+                         float* __restrict__ X0, int* __restrict__ cell2,
+                         unsigned char* __restrict__ owner,
+                         uint32_t* __restrict__ key2, uint32_t* __restrict__ val2) {
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= E) return;
+    const int b = find_block(bd, G.nb, g);
+    const HybridInputRec& r = bd[b].ring[g - bd[b].offset];
+    const int x = r.x, y = r.y;
+    const bool valid = x < G.W2 && y < G.H2;
+    float4* dst = reinterpret_cast<float4*>(X0 + (size_t)g * SSLA_C1);
+    const float4* src = reinterpret_cast<const float4*>(r.feat1);
+    #pragma unroll
+    for (int i = 0; i < SSLA_C1 / 4; ++i)
+        dst[i] = valid ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const HybridStrip& s = bd[b].strip;
+    owner[g] = (valid && x >= s.owned_lo && x < s.owned_hi &&
+                y >= s.owned_y_lo && y < s.owned_y_hi) ? 1 : 0;
+    const uint32_t none = (uint32_t)(G.nb * G.C2);
+    cell2[g] = valid ? y * G.W2 + x : -1;
+    key2[g] = valid ? (uint32_t)(b * G.C2 + y * G.W2 + x) : none;
+    val2[g] = (uint32_t)g;
+}
+
+// s3 centre keys of records that passed tdrop_s2 (sentinel otherwise);
+// key3g keeps a per-record copy for the head, ks/vs feed the sort.
+__global__ void k_keys3(int E, const BlockDesc* __restrict__ bd, Geometry G,
+                        const int* __restrict__ cell2,
+                        const unsigned char* __restrict__ pass2,
+                        uint32_t* __restrict__ key3g, uint32_t* __restrict__ ks,
+                        uint32_t* __restrict__ vs) {
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= E) return;
+    const int b = find_block(bd, G.nb, g);
+    const int c = cell2[g];
+    const bool live = c >= 0 && pass2[g];
+    const int x = (c % G.W2) >> 1, y = (c / G.W2) >> 1;
+    const uint32_t k = live ? (uint32_t)(b * G.C3 + y * G.W3 + x) : (uint32_t)(G.nb * G.C3);
+    key3g[g] = k;
+    ks[g] = k;
+    vs[g] = (uint32_t)g;
+}
+
+// (record, delta) pair keys: the patch cell the pair updates, or the
+// sentinel nb*C when the cell is off the grid or the record does not enter
+// the level (level 3 takes pass2 records only).  delta = (1-dy)*3 + (1-dx).
+__global__ void k_pairs(int E, const BlockDesc* __restrict__ bd, Geometry G,
+                        int level, const int* __restrict__ cell2,
+                        const unsigned char* __restrict__ pass2,
+                        uint32_t* __restrict__ pkey, uint32_t* __restrict__ pval) {
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= E) return;
+    const int b = find_block(bd, G.nb, g);
+    const int c = cell2[g];
+    const bool live = c >= 0 && (level == 2 || pass2[g]);
+    const int sh = level == 2 ? 0 : 1;
+    const int H = level == 2 ? G.H2 : G.H3, W = level == 2 ? G.W2 : G.W3;
+    const int C = H * W;
+    const int x = (c % G.W2) >> sh, y = (c / G.W2) >> sh;
+    const uint32_t none = (uint32_t)(G.nb * C);
+    #pragma unroll
+    for (int d = 0; d < kPatch; ++d) {
+        const int ty = y + 1 - d / 3, tx = x + 1 - d % 3;
+        const bool in = live && ty >= 0 && ty < H && tx >= 0 && tx < W;
+        pkey[(size_t)g * kPatch + d] = in ? (uint32_t)(b * C + ty * W + tx) : none;
+        pval[(size_t)g * kPatch + d] = (uint32_t)(g * kPatch + d);
+    }
+}
+
+__global__ void k_fill_i32(int n, int* __restrict__ p, int v) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// [start, end) of every key present in a sorted key array.
+__global__ void k_runs(int n, const uint32_t* __restrict__ keys, uint32_t nk,
+                       int* __restrict__ start, int* __restrict__ end) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const uint32_t k = keys[p];
+    if (k >= nk) return;
+    if (p == 0 || keys[p - 1] != k) start[k] = p;
+    if (p == n - 1 || keys[p + 1] != k) end[k] = p + 1;
+}
+
+// tdrop decision from the arrival rank inside the cell's run.
+__global__ void k_tdrop(int n, const uint32_t* __restrict__ keys,
+                        const uint32_t* __restrict__ vals, uint32_t nk, int C,
+                        const int* __restrict__ start,
+                        const BlockDesc* __restrict__ bd, int level, int window,
+                        unsigned char* __restrict__ pass) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const uint32_t k = keys[p];
+    const uint32_t g = vals[p];
+    if (k >= nk) { pass[g] = 0; return; }
+    const int b = (int)k / C, cell = (int)k % C;
+    const unsigned char* td = level == 2 ? bd[b].td2 : bd[b].td3;
+    const unsigned pre = ((unsigned)td[cell] + (unsigned)(p - start[k])) & 255u;
+    pass[g] = (window <= 1 || pre % (unsigned)window == 0u) ? 1 : 0;
+}
+
+__global__ void k_tdrop_commit(uint32_t nk, int C, const int* __restrict__ start,
+                               const int* __restrict__ end,
+                               const BlockDesc* __restrict__ bd, int level) {
+    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= nk) return;
+    const int len = end[k] - start[k];
+    if (len <= 0) return;
+    const int b = (int)k / C, cell = (int)k % C;
+    unsigned char* td = level == 2 ? bd[b].td2 : bd[b].td3;
+    td[cell] = (unsigned char)(((unsigned)td[cell] + (unsigned)len) & 255u);
+}
+
+// position of every (record, delta) pair in the sorted pair order, -1 if
+// the patch cell is outside the grid (or the record does not enter).
+__global__ void k_pair_pos(int n, const uint32_t* __restrict__ keys,
+                           const uint32_t* __restrict__ vals, uint32_t nk,
+                           int* __restrict__ pos) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    pos[vals[p]] = keys[p] < nk ? p : -1;
+}
+
+// ---------------------------------------------------------------------------
+// P: q, v, g rows.  One workgroup = kTE records x all 9 deltas; one thread
+// per output column of [q | v | g].  Weight rows (9, IN, 3*OUT) stream from
+// L2 once per tile and feed kTE FMAs each; x comes from LDS as broadcasts.
+// ---------------------------------------------------------------------------
+template <int IN, int OUT>
+__global__ void __launch_bounds__(((3 * OUT + 63) / 64) * 64)
+k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
+      const float* __restrict__ X, const int* __restrict__ pos,
+      const float* __restrict__ W, float* __restrict__ QVG) {
+    constexpr int NC = 3 * OUT;
+    __shared__ float xs[kTE][IN];
+    __shared__ int rows[kTE];
+    const int n = n_dev ? *n_dev : n_max;
+    const int base = blockIdx.x * kTE;
+    if (base >= n) return;
+    const int cnt = min(kTE, n - base);
+    for (int t = threadIdx.x; t < kTE * IN; t += blockDim.x) {
+        const int r = t / IN, i = t % IN;
+        float v = 0.f;
+        if (r < cnt) {
+            const int g = list ? list[base + r] : base + r;
+            v = X[(size_t)g * IN + i];
+        }
+        xs[r][i] = v;
+    }
+    if (threadIdx.x < kTE)
+        rows[threadIdx.x] = threadIdx.x < cnt
+            ? (list ? list[base + threadIdx.x] : base + threadIdx.x) : -1;
+    __syncthreads();
+    const int c = threadIdx.x;
+    if (c >= NC) return;
+    for (int d = 0; d < kPatch; ++d) {
+        const float* w = W + (size_t)d * IN * NC + c;
+        float acc[kTE];
+        #pragma unroll
+        for (int r = 0; r < kTE; ++r) acc[r] = 0.f;
+        for (int i = 0; i < IN; ++i) {
+            const float wi = w[(size_t)i * NC];
+            #pragma unroll
+            for (int r = 0; r < kTE; ++r) acc[r] = fmaf(wi, xs[r][i], acc[r]);
+        }
+        #pragma unroll
+        for (int r = 0; r < kTE; ++r) {
+            const int g = rows[r];
+            if (g < 0) continue;
+            const int pr = pos[(size_t)g * kPatch + d];
+            if (pr >= 0) QVG[(size_t)pr * NC + c] = acc[r];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// S: one workgroup per cell, one lane per channel; walks the cell's pairs in
+// ring order.  h = sigmoid(g) h + v; the q slot of the row becomes q*h.
+// ---------------------------------------------------------------------------
+template <int OUT>
+__global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
+k_scan(int C, const int* __restrict__ start, const int* __restrict__ end,
+       const BlockDesc* __restrict__ bd, int li, float* __restrict__ QVG) {
+    constexpr int NC = 3 * OUT;
+    const int k = blockIdx.x;
+    const int c = threadIdx.x;
+    if (c >= OUT) return;
+    const int s = start[k], e = end[k];
+    if (e <= s) return;
+    const int b = k / C, cell = k % C;
+    float* hp = bd[b].hidden[li] + (size_t)cell * OUT + c;
+    float h = *hp;
+    float* row = QVG + (size_t)s * NC + c;
+    int p = s;
+    for (; p + 4 <= e; p += 4, row += 4 * NC) {
+        float q[4], v[4], gg[4];
+        #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            q[j] = row[j * NC];
+            v[j] = row[j * NC + OUT];
+            gg[j] = row[j * NC + 2 * OUT];
+        }
+        #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h = fmaf(sigmoid_fast(gg[j]), h, v[j]);
+            row[j * NC] = q[j] * h;
+        }
+    }
+    for (; p < e; ++p, row += NC) {
+        const float q = row[0], v = row[OUT], gg = row[2 * OUT];
+        h = fmaf(sigmoid_fast(gg), h, v);
+        row[0] = q * h;
+    }
+    *hp = h;
+}
+
+// ---------------------------------------------------------------------------
+// O: per record y = sum_delta goW[delta]^T qh + residual, fp64 LayerNorm.
+// One workgroup = kTE records; one thread per output channel.
+// ---------------------------------------------------------------------------
+template <int IN, int OUT>
+__global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
+k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
+      const float* __restrict__ X, const int* __restrict__ pos,
+      const float* __restrict__ QVG, const float* __restrict__ goW,
+      const float* __restrict__ ip, const float* __restrict__ gamma,
+      const float* __restrict__ beta, float* __restrict__ Y) {
+    constexpr int NC = 3 * OUT;
+    __shared__ float vs[kTE][OUT > IN ? OUT : IN];
+    __shared__ float ys[kTE][OUT + 1];
+    __shared__ double stat[kTE][2];
+    __shared__ int rows[kTE];
+    const int n = n_dev ? *n_dev : n_max;
+    const int base = blockIdx.x * kTE;
+    if (base >= n) return;
+    const int cnt = min(kTE, n - base);
+    const int o = threadIdx.x;
+    if (threadIdx.x < kTE)
+        rows[threadIdx.x] = threadIdx.x < cnt
+            ? (list ? list[base + threadIdx.x] : base + threadIdx.x) : -1;
+    float acc[kTE];
+    #pragma unroll
+    for (int r = 0; r < kTE; ++r) acc[r] = 0.f;
+    for (int d = 0; d < kPatch; ++d) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < kTE * OUT; t += blockDim.x) {
+            const int r = t / OUT, i = t % OUT;
+            const int g = rows[r];
+            float v = 0.f;
+            if (g >= 0) {
+                const int pr = pos[(size_t)g * kPatch + d];
+                if (pr >= 0) v = QVG[(size_t)pr * NC + i];
+            }
+            vs[r][i] = v;
+        }
+        __syncthreads();
+        if (o < OUT) {
+            const float* w = goW + (size_t)d * OUT * OUT + o;
+            for (int i = 0; i < OUT; ++i) {
+                const float wi = w[(size_t)i * OUT];
+                #pragma unroll
+                for (int r = 0; r < kTE; ++r) acc[r] = fmaf(wi, vs[r][i], acc[r]);
+            }
+        }
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < kTE * IN; t += blockDim.x) {
+        const int r = t / IN, i = t % IN;
+        const int g = rows[r];
+        vs[r][i] = g >= 0 ? X[(size_t)g * IN + i] : 0.f;
+    }
+    __syncthreads();
+    if (o < OUT) {
+        if (ip) {
+            for (int i = 0; i < IN; ++i) {
+                const float wi = ip[(size_t)i * OUT + o];
+                #pragma unroll
+                for (int r = 0; r < kTE; ++r) acc[r] = fmaf(wi, vs[r][i], acc[r]);
+            }
+        } else {
+            #pragma unroll
+            for (int r = 0; r < kTE; ++r) acc[r] += vs[r][o];
+        }
+        #pragma unroll
+        for (int r = 0; r < kTE; ++r) ys[r][o] = acc[r];
+    }
+    __syncthreads();
+    if (threadIdx.x < kTE) {
+        const int r = threadIdx.x;
+        double s = 0.0;
+        for (int i = 0; i < OUT; ++i) s += (double)ys[r][i];
+        const double mean = s / (double)OUT;
+        double var = 0.0;
+        for (int i = 0; i < OUT; ++i) {
+            const double dd = (double)ys[r][i] - mean;
+            var += dd * dd;
+        }
+        var /= (double)OUT;
+        stat[r][0] = mean;
+        stat[r][1] = 1.0 / sqrt(var + 1e-5);
+    }
+    __syncthreads();
+    if (o < OUT) {
+        const double gm = (double)gamma[o], bt = (double)beta[o];
+        for (int r = 0; r < cnt; ++r) {
+            const double v = ((double)ys[r][o] - stat[r][0]) * stat[r][1];
+            Y[(size_t)rows[r] * OUT + o] = (float)(v * gm + bt);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// head: raw [reg0..3, obj, cls0, cls1] for owned pass-3 records
+// (...celled.cuh:841-902).  One workgroup per record, one thread per hidden
+// channel.
+// ---------------------------------------------------------------------------
+struct HeadPtrs {
+    const float *cls_conv_W, *cls_conv_b, *cls_pred_W, *cls_pred_b;
+    const float *reg_conv_W, *reg_conv_b, *reg_pred_W, *reg_pred_b;
+    const float *obj_pred_W, *obj_pred_b;
+};
+
+__global__ void __launch_bounds__(128)
+k_head(const int* __restrict__ n_dev, const int* __restrict__ list,
+       const unsigned char* __restrict__ owner, const float* __restrict__ X,
+       HeadPtrs hp, float* __restrict__ H7) {
+    constexpr int C = SSLA_C3;
+    __shared__ float x[C], yc[C], yr[C];
+    const int j = blockIdx.x;
+    if (j >= *n_dev) return;
+    const int g = list[j];
+    if (!owner[g]) return;
+    const int t = threadIdx.x;
+    if (t < C) x[t] = X[(size_t)g * C + t];
+    __syncthreads();
+    if (t < C) {
+        float a = hp.cls_conv_b[t], b = hp.reg_conv_b[t];
+        for (int i = 0; i < C; ++i) {
+            a = fmaf(hp.cls_conv_W[(size_t)i * C + t], x[i], a);
+            b = fmaf(hp.reg_conv_W[(size_t)i * C + t], x[i], b);
+        }
+        yc[t] = a * sigmoid_fast(a);
+        yr[t] = b * sigmoid_fast(b);
+    }
+    __syncthreads();
+    // outputs 0..3 reg, 4 obj, 5..6 cls: one wave, lane-strided partial sums
+    if (t < 64) {
+        float part[7];
+        #pragma unroll
+        for (int k = 0; k < 7; ++k) part[k] = 0.f;
+        for (int i = t; i < C; i += 64) {
+            #pragma unroll
+            for (int k = 0; k < 4; ++k) part[k] = fmaf(hp.reg_pred_W[(size_t)i * 4 + k], yr[i], part[k]);
+            part[4] = fmaf(hp.obj_pred_W[i], yr[i], part[4]);
+            #pragma unroll
+            for (int k = 0; k < 2; ++k) part[5 + k] = fmaf(hp.cls_pred_W[(size_t)i * 2 + k], yc[i], part[5 + k]);
+        }
+        #pragma unroll
+        for (int k = 0; k < 7; ++k) {
+            float v = part[k];
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+            part[k] = v;
+        }
+        if (t == 0) {
+            float* o = H7 + (size_t)g * 7;
+            #pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = part[k] + hp.reg_pred_b[k];
+            o[4] = part[4] + hp.obj_pred_b[0];
+            o[5] = part[5] + hp.cls_pred_b[0];
+            o[6] = part[6] + hp.cls_pred_b[1];
+        }
+    }
+}
+
+// Last owned pass-3 record per s3 cell and number of such records.
+__global__ void k_pred_last(const int* __restrict__ n_dev, const int* __restrict__ list,
+                            const unsigned char* __restrict__ owner,
+                            const uint32_t* __restrict__ key3_by_g,
+                            int* __restrict__ last, int* __restrict__ count) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= *n_dev) return;
+    const int g = list[j];
+    if (!owner[g]) return;
+    const uint32_t k = key3_by_g[g];
+    atomicMax(&last[k], g);
+    atomicAdd(&count[k], 1);
+}
+
+__global__ void k_pred_write(const int* __restrict__ n_dev, const int* __restrict__ list,
+                             const unsigned char* __restrict__ owner,
+                             const uint32_t* __restrict__ key3_by_g,
+                             const int* __restrict__ last, const int* __restrict__ count,
+                             const BlockDesc* __restrict__ bd, Geometry G,
+                             const float* __restrict__ H7) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= *n_dev) return;
+    const int g = list[j];
+    if (!owner[g]) return;
+    const uint32_t k = key3_by_g[g];
+    if (last[k] != g) return;
+    const int b = (int)k / G.C3, cell = (int)k % G.C3;
+    const HybridStrip& s = bd[b].strip;
+    const int sx = cell % G.W3, sy = cell / G.W3;
+    const int hx = sx - s.s3_owned_lo, hy = sy - s.s3_owned_y_lo;
+    const int w = s.s3_owned_hi - s.s3_owned_lo, h = s.s3_owned_y_hi - s.s3_owned_y_lo;
+    if (hx < 0 || hx >= w || hy < 0 || hy >= h) return;
+    const int idx = hy * w + hx;
+    if (bd[b].preds) {
+        float* dst = bd[b].preds + (size_t)idx * 7;
+        #pragma unroll
+        for (int q = 0; q < 7; ++q) dst[q] = H7[(size_t)g * 7 + q];
+    }
+    if (bd[b].version) bd[b].version[idx] += (unsigned)count[k];
+}
+
+// Output slots (...celled.cuh:1233-1247 conventions) and raw head rows.
+__global__ void k_emit(int E, const BlockDesc* __restrict__ bd, int nb,
+                       const int* __restrict__ cell2,
+                       const unsigned char* __restrict__ owner,
+                       const unsigned char* __restrict__ pass2,
+                       const unsigned char* __restrict__ pass3,
+                       const float* __restrict__ X4, const float* __restrict__ H7,
+                       int have_head) {
+    const int g = blockIdx.x;
+    if (g >= E) return;
+    const int b = find_block(bd, nb, g);
+    const int k = g - bd[b].offset;
+    const bool valid = cell2[g] >= 0;
+    const bool p2 = valid && pass2[g], p3 = p2 && pass3[g], own = owner[g];
+    HybridS2S3OutputSlot* out = bd[b].out;
+    if (out) {
+        HybridS2S3OutputSlot& s = out[k];
+        if (threadIdx.x == 0) {
+            s.pass2 = !valid ? -2 : (own ? (p2 ? 1 : 0) : -1);
+            s.pass3 = !valid ? -2 : (own ? (p3 ? 1 : 0) : -1);
+        }
+        for (int i = threadIdx.x; i < SSLA_C3; i += blockDim.x)
+            s.s3_feat[i] = p3 ? X4[(size_t)g * SSLA_C3 + i] : 0.f;
+    }
+    float* ho = bd[b].head_out;
+    if (ho && threadIdx.x < 7)
+        ho[(size_t)k * 7 + threadIdx.x] =
+            (have_head && p3 && own) ? H7[(size_t)g * 7 + threadIdx.x] : 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// workspace
+// ---------------------------------------------------------------------------
+struct Workspace {
+    int cap = 0;            // records
+    int cap_blocks = 0;
+    int cap_keys = 0;
+    void* base = nullptr;
+    size_t bytes = 0;
+    float *X0, *X1, *X2, *X3, *X4, *QVG, *H7;
+    int *cell2, *pos2, *pos3, *list2, *list3, *counts;
+    int *st2, *en2, *st3, *en3, *pst2, *pen2, *pst3, *pen3, *last3, *cnt3;
+    unsigned char *owner, *pass2, *pass3;
+    uint32_t *ka, *kb, *va, *vb, *key3g;
+    BlockDesc* bd;
+    BlockDesc* bd_host = nullptr;      // pinned staging of the block table
+    hipEvent_t bd_copied = nullptr;    // the last staging copy has been read
+    void* temp;
+    size_t temp_bytes;
+};
+
+std::mutex g_ws_mu;
+Workspace g_ws;
+
+#define HIPCHK(call)                                                          \
+    do {                                                                      \
+        hipError_t e_ = (call);                                               \
+        if (e_ != hipSuccess) {                                               \
+            set_error(std::string(#call) + ": " + hipGetErrorString(e_));    \
+            return SSLA_ERR_HIP;                                              \
+        }                                                                     \
+    } while (0)
+
+size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
+
+int ensure_workspace(int E, int nkeys) {
+    if (E <= g_ws.cap && nkeys <= g_ws.cap_keys) return SSLA_OK;
+    if (g_ws.base) {
+        HIPCHK(hipDeviceSynchronize());
+        HIPCHK(hipFree(g_ws.base));
+        g_ws.base = nullptr;
+        g_ws.cap = 0;
+    }
+    const int cap = std::max(E, std::max(g_ws.cap, 1024));
+    const int ck = std::max(nkeys, g_ws.cap_keys);
+    const size_t P = (size_t)cap * kPatch;
+    // temp storage: radix sort of P pairs and the flagged selections.
+    size_t t_sort = 0, t_sel = 0;
+    HIPCHK(hipcub::DeviceRadixSort::SortPairs(nullptr, t_sort, (uint32_t*)nullptr,
+                                               (uint32_t*)nullptr, (uint32_t*)nullptr,
+                                               (uint32_t*)nullptr, (int)P, 0, 32));
+    HIPCHK(hipcub::DeviceSelect::Flagged(nullptr, t_sel, hipcub::CountingInputIterator<int>(0),
+                                          (unsigned char*)nullptr, (int*)nullptr,
+                                          (int*)nullptr, cap));
+    const size_t temp = std::max(t_sort, t_sel);
+    struct Item { void** dst; size_t bytes; };
+    Workspace& w = g_ws;
+    std::vector<Item> items = {
+        {(void**)&w.X0, sizeof(float) * (size_t)cap * SSLA_C1},
+        {(void**)&w.X1, sizeof(float) * (size_t)cap * SSLA_C2},
+        {(void**)&w.X2, sizeof(float) * (size_t)cap * SSLA_C2},
+        {(void**)&w.X3, sizeof(float) * (size_t)cap * SSLA_C3},
+        {(void**)&w.X4, sizeof(float) * (size_t)cap * SSLA_C3},
+        {(void**)&w.QVG, sizeof(float) * P * 3 * SSLA_C3},
+        {(void**)&w.H7, sizeof(float) * (size_t)cap * 7},
+        {(void**)&w.cell2, sizeof(int) * (size_t)cap},
+        {(void**)&w.pos2, sizeof(int) * P},
+        {(void**)&w.pos3, sizeof(int) * P},
+        {(void**)&w.list2, sizeof(int) * (size_t)cap},
+        {(void**)&w.list3, sizeof(int) * (size_t)cap},
+        {(void**)&w.counts, sizeof(int) * 4},
+        {(void**)&w.st2, sizeof(int) * (size_t)ck},
+        {(void**)&w.en2, sizeof(int) * (size_t)ck},
+        {(void**)&w.st3, sizeof(int) * (size_t)ck},
+        {(void**)&w.en3, sizeof(int) * (size_t)ck},
+        {(void**)&w.pst2, sizeof(int) * (size_t)ck},
+        {(void**)&w.pen2, sizeof(int) * (size_t)ck},
+        {(void**)&w.pst3, sizeof(int) * (size_t)ck},
+        {(void**)&w.pen3, sizeof(int) * (size_t)ck},
+        {(void**)&w.last3, sizeof(int) * (size_t)ck},
+        {(void**)&w.cnt3, sizeof(int) * (size_t)ck},
+        {(void**)&w.owner, (size_t)cap},
+        {(void**)&w.pass2, (size_t)cap},
+        {(void**)&w.pass3, (size_t)cap},
+        {(void**)&w.ka, sizeof(uint32_t) * P},
+        {(void**)&w.kb, sizeof(uint32_t) * P},
+        {(void**)&w.va, sizeof(uint32_t) * P},
+        {(void**)&w.vb, sizeof(uint32_t) * P},
+        {(void**)&w.key3g, sizeof(uint32_t) * (size_t)cap},
+        {(void**)&w.bd, sizeof(BlockDesc) * SSLA_MAX_BLOCKS},
+        {(void**)&w.temp, temp},
+    };
+    size_t total = 0;
+    for (auto& it : items) total += align_up(it.bytes);
+    void* base = nullptr;
+    HIPCHK(hipMalloc(&base, total));
+    char* p = static_cast<char*>(base);
+    for (auto& it : items) {
+        *it.dst = p;
+        p += align_up(it.bytes);
+    }
+    if (!w.bd_host) {
+        HIPCHK(hipHostMalloc((void**)&w.bd_host, sizeof(BlockDesc) * SSLA_MAX_BLOCKS,
+                             hipHostMallocDefault));
+        HIPCHK(hipEventCreateWithFlags(&w.bd_copied, hipEventDisableTiming));
+    }
+    w.base = base;
+    w.bytes = total;
+    w.cap = cap;
+    w.cap_keys = ck;
+    w.temp_bytes = temp;
+    return SSLA_OK;
+}
+
+int bits_for(uint32_t v) {
+    int b = 1;
+    while ((1u << b) <= v && b < 32) ++b;
+    return b;
+}
+
+inline unsigned grid1(long long n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+}  // namespace
+
+int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
+               const int* ns, HybridS2S3OutputSlot* const* outs,
+               float* const* head_outs, hipStream_t st, bool sync,
+               float* phase_ms) {
+    const int nb = cfg->n_blocks;
+    if (nb < 1 || nb > SSLA_MAX_BLOCKS) {
+        set_error("n_blocks must be in [1, 16]");
+        return SSLA_ERR_ARG;
+    }
+    if (cfg->H2 <= 0 || cfg->W2 <= 0 || (cfg->H2 & 1) || (cfg->W2 & 1) ||
+        cfg->H3 != cfg->H2 / 2 || cfg->W3 != cfg->W2 / 2 ||
+        cfg->H2 > 65535 || cfg->W2 > 65535) {
+        set_error("grid must have even H2, W2 and H3 = H2/2, W3 = W2/2");
+        return SSLA_ERR_ARG;
+    }
+    for (int b = 0; b < nb; ++b) {
+        for (int li = 0; li < 4; ++li) {
+            const LayerWeightsS2S3& L = cfg->layers[b][li];
+            const LayerWeightsS2S3& L0 = cfg->layers[0][li];
+            if (!L.qvgIn || !L.goW || !L.ln_gamma || !L.ln_beta) {
+                set_error("layer weights not bound for block " + std::to_string(b));
+                return SSLA_ERR_ARG;
+            }
+            if (L.qvgIn != L0.qvgIn || L.goW != L0.goW || L.input_proj != L0.input_proj ||
+                L.ln_gamma != L0.ln_gamma || L.ln_beta != L0.ln_beta) {
+                set_error("all blocks must share one set of layer weights");
+                return SSLA_ERR_ARG;
+            }
+            if (!cfg->hidden[b][li]) {
+                set_error("hidden state not allocated for block " + std::to_string(b));
+                return SSLA_ERR_ARG;
+            }
+        }
+        if (!cfg->tdrop_s2[b] || !cfg->tdrop_s3[b]) {
+            set_error("tdrop counters not allocated for block " + std::to_string(b));
+            return SSLA_ERR_ARG;
+        }
+        if (ns[b] < 0 || (ns[b] > 0 && !rings[b])) {
+            set_error("bad ring / count for block " + std::to_string(b));
+            return SSLA_ERR_ARG;
+        }
+    }
+    if ((cfg->layers[0][0].input_proj == nullptr) || (cfg->layers[0][2].input_proj == nullptr) ||
+        cfg->layers[0][1].input_proj != nullptr || cfg->layers[0][3].input_proj != nullptr) {
+        set_error("L4/L6 need input_proj and L5/L7 must not have one");
+        return SSLA_ERR_ARG;
+    }
+    long long E64 = 0;
+    for (int b = 0; b < nb; ++b) E64 += ns[b];
+    if (E64 * kPatch > 0x7fffffffLL) {
+        set_error("too many records in one call");
+        return SSLA_ERR_ARG;
+    }
+    const int E = (int)E64;
+    Geometry G;
+    G.H2 = cfg->H2; G.W2 = cfg->W2; G.H3 = cfg->H3; G.W3 = cfg->W3;
+    G.C2 = G.H2 * G.W2; G.C3 = G.H3 * G.W3; G.nb = nb; G.window = cfg->tdrop_window;
+    const uint32_t nk2 = (uint32_t)(nb * G.C2), nk3 = (uint32_t)(nb * G.C3);
+    const bool have_head = cfg->head_cls_conv_W != nullptr;
+
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if (E == 0) return SSLA_OK;
+    {
+        const int rc = ensure_workspace(E, (int)nk2 + 1);
+        if (rc) return rc;
+    }
+    Workspace& w = g_ws;
+
+    BlockDesc hbd[SSLA_MAX_BLOCKS] = {};
+    int off = 0;
+    for (int b = 0; b < nb; ++b) {
+        BlockDesc& d = hbd[b];
+        d.ring = rings[b];
+        d.out = outs ? outs[b] : nullptr;
+        d.head_out = head_outs ? head_outs[b] : nullptr;
+        for (int li = 0; li < 4; ++li) d.hidden[li] = cfg->hidden[b][li];
+        d.td2 = cfg->tdrop_s2[b];
+        d.td3 = cfg->tdrop_s3[b];
+        d.preds = have_head ? cfg->preds[b] : nullptr;
+        d.version = have_head ? cfg->version[b] : nullptr;
+        d.strip = cfg->strip[b];
+        d.n = ns[b];
+        d.offset = off;
+        off += ns[b];
+    }
+    // blocks with n == 0 must not capture records: move their offset past E.
+    for (int b = 0; b < nb; ++b)
+        if (hbd[b].n == 0) hbd[b].offset = E + 1;
+    // The staging buffer may still be the source of the previous call's
+    // copy; wait for that copy before overwriting it.
+    HIPCHK(hipEventSynchronize(w.bd_copied));
+    std::memcpy(w.bd_host, hbd, sizeof(hbd));
+    HIPCHK(hipMemcpyAsync(w.bd, w.bd_host, sizeof(hbd), hipMemcpyHostToDevice, st));
+    HIPCHK(hipEventRecord(w.bd_copied, st));
+
+    const int P = E * kPatch;
+    // Phase timing: events recorded on `st` between phases (optional).
+    hipEvent_t ev[SSLA_DRAIN_PHASES + 1] = {};
+    int n_ev = 0;
+    auto mark = [&]() -> int {
+        if (!phase_ms) return SSLA_OK;
+        if (!ev[n_ev]) HIPCHK(hipEventCreate(&ev[n_ev]));
+        HIPCHK(hipEventRecord(ev[n_ev], st));
+        ++n_ev;
+        return SSLA_OK;
+    };
+#define MARK() do { const int rc_ = mark(); if (rc_) return rc_; } while (0)
+    MARK();
+    const int bits2 = bits_for(nk2), bits3 = bits_for(nk3);
+    size_t tb = w.temp_bytes;
+
+    // ---- decode; tdrop_s2 from a stable sort of records by centre cell ----
+    hipLaunchKernelGGL(k_decode, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, w.X0,
+                       w.cell2, w.owner, w.ka, w.va);
+    HIPCHK(hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, E, 0,
+                                               bits2, st));
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.st2, 0);
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.en2, 0);
+    hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, nk2, w.st2, w.en2);
+    hipLaunchKernelGGL(k_tdrop, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, w.vb, nk2,
+                       G.C2, w.st2, w.bd, 2, G.window, w.pass2);
+    hipLaunchKernelGGL(k_tdrop_commit, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, G.C2,
+                       w.st2, w.en2, w.bd, 2);
+    // ---- s2 pair order: (record, delta) pairs sorted by patch cell ----------
+    hipLaunchKernelGGL(k_pairs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, 2,
+                       w.cell2, w.pass2, w.kb, w.vb);
+    HIPCHK(hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, 0,
+                                               bits2, st));
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.pst2, 0);
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.pen2, 0);
+    hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, nk2, w.pst2, w.pen2);
+    hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, w.va, nk2,
+                       w.pos2);
+    // ---- tdrop_s3 over pass2 records, by s3 centre cell ---------------------
+    hipLaunchKernelGGL(k_keys3, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, w.cell2,
+                       w.pass2, w.key3g, w.ka, w.va);
+    HIPCHK(hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, E, 0,
+                                               bits3, st));
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.st3, 0);
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.en3, 0);
+    hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, nk3, w.st3, w.en3);
+    hipLaunchKernelGGL(k_tdrop, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, w.vb, nk3,
+                       G.C3, w.st3, w.bd, 3, G.window, w.pass3);
+    hipLaunchKernelGGL(k_tdrop_commit, dim3(grid1(nk3, 256)), dim3(256), 0, st, nk3, G.C3,
+                       w.st3, w.en3, w.bd, 3);
+    // ---- s3 pair order ---------------------------------------------------------
+    hipLaunchKernelGGL(k_pairs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, 3,
+                       w.cell2, w.pass2, w.kb, w.vb);
+    HIPCHK(hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, 0,
+                                               bits3, st));
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.pst3, 0);
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.pen3, 0);
+    hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, nk3, w.pst3, w.pen3);
+    hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, w.va, nk3,
+                       w.pos3);
+    // ---- record lists: pass2 records, pass3 records (ring order) --------------
+    HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
+                                          w.pass2, w.list2, w.counts + 0, E, st));
+    // k_tdrop wrote pass3 = 0 for records that did not pass tdrop_s2.
+    HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
+                                          w.pass3, w.list3, w.counts + 1, E, st));
+    HIPCHK(hipGetLastError());
+
+    MARK();
+    const LayerWeightsS2S3* L = cfg->layers[0];
+    const unsigned tilesE = grid1(E, kTE);
+    // ---- L4: 24 -> 48, all records ----------------------------------------
+    hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(192), 0, st, E,
+                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, L[0].qvgIn, w.QVG);
+    MARK();
+    hipLaunchKernelGGL((k_scan<SSLA_C2>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
+                       w.bd, 0, w.QVG);
+    MARK();
+    hipLaunchKernelGGL((k_out<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(64), 0, st, E,
+                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, L[0].goW,
+                       L[0].input_proj, L[0].ln_gamma, L[0].ln_beta, w.X1);
+    MARK();
+    // ---- L5: 48 -> 48, state for all records, output for pass2 ---------------
+    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(192), 0, st, E,
+                       (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, L[1].qvgIn, w.QVG);
+    MARK();
+    hipLaunchKernelGGL((k_scan<SSLA_C2>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
+                       w.bd, 1, w.QVG);
+    MARK();
+    hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(64), 0, st, E,
+                       (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, L[1].goW,
+                       (const float*)nullptr, L[1].ln_gamma, L[1].ln_beta, w.X2);
+    MARK();
+    // ---- L6: 48 -> 96, pass2 records ------------------------------------------
+    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(320), 0, st, E,
+                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, L[2].qvgIn, w.QVG);
+    MARK();
+    hipLaunchKernelGGL((k_scan<SSLA_C3>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
+                       w.bd, 2, w.QVG);
+    MARK();
+    hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(128), 0, st, E,
+                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, L[2].goW,
+                       L[2].input_proj, L[2].ln_gamma, L[2].ln_beta, w.X3);
+    MARK();
+    // ---- L7: 96 -> 96, state for pass2, output for pass3 ----------------------
+    hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(320), 0, st, E,
+                       (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, L[3].qvgIn, w.QVG);
+    MARK();
+    hipLaunchKernelGGL((k_scan<SSLA_C3>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
+                       w.bd, 3, w.QVG);
+    MARK();
+    hipLaunchKernelGGL((k_out<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(128), 0, st, E,
+                       (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, L[3].goW,
+                       (const float*)nullptr, L[3].ln_gamma, L[3].ln_beta, w.X4);
+    MARK();
+    HIPCHK(hipGetLastError());
+    // ---- head ------------------------------------------------------------------
+    if (have_head) {
+        HeadPtrs hp{cfg->head_cls_conv_W, cfg->head_cls_conv_b, cfg->head_cls_pred_W,
+                    cfg->head_cls_pred_b, cfg->head_reg_conv_W, cfg->head_reg_conv_b,
+                    cfg->head_reg_pred_W, cfg->head_reg_pred_b, cfg->head_obj_pred_W,
+                    cfg->head_obj_pred_b};
+        hipLaunchKernelGGL(k_head, dim3(E), dim3(128), 0, st, (const int*)(w.counts + 1),
+                           w.list3, w.owner, w.X4, hp, w.H7);
+        hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.last3, -1);
+        hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.cnt3, 0);
+        hipLaunchKernelGGL(k_pred_last, dim3(grid1(E, 256)), dim3(256), 0, st,
+                           (const int*)(w.counts + 1), w.list3, w.owner, w.key3g, w.last3, w.cnt3);
+        hipLaunchKernelGGL(k_pred_write, dim3(grid1(E, 256)), dim3(256), 0, st,
+                           (const int*)(w.counts + 1), w.list3, w.owner, w.key3g, w.last3,
+                           w.cnt3, w.bd, G, w.H7);
+    }
+    MARK();
+    hipLaunchKernelGGL(k_emit, dim3(E), dim3(64), 0, st, E, w.bd, nb, w.cell2, w.owner,
+                       w.pass2, w.pass3, w.X4, w.H7, have_head ? 1 : 0);
+    HIPCHK(hipGetLastError());
+    MARK();
+#undef MARK
+    if (sync) HIPCHK(hipStreamSynchronize(st));
+    if (phase_ms) {
+        for (int k = 0; k + 1 < n_ev && k < SSLA_DRAIN_PHASES; ++k) {
+            float ms = 0.f;
+            HIPCHK(hipEventElapsedTime(&ms, ev[k], ev[k + 1]));
+            phase_ms[k] += ms;
+        }
+        for (int k = 0; k < n_ev; ++k) (void)hipEventDestroy(ev[k]);
+    }
+    return SSLA_OK;
+}
+
+}  // namespace ssla

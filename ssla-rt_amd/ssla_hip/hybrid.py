@@ -1,0 +1,297 @@
+"""Host-side driver of libssla_hip.so: device buffers, weight packing,
+configuration and the drain calls.
+
+Mirrors the reference's host helpers (orin/orin/hybrid_common.py:138-271,
+orin/orin/multi_block.py:128-340): random or weight-directory layers are
+packed into the device layouts of include/ssla_abi.h, a HybridS2S3Config is
+filled with device pointers, and the drain entry of the C ABI runs the
+rings.  All compute happens in the library; this module only moves bytes.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+from . import abi, lib
+from .events import GPU_LAYER_IO, RawLayer
+
+
+class DeviceBuffer:
+    """A device-visible allocation (HBM, or fine-grained host memory)."""
+
+    def __init__(self, nbytes: int, host: bool = False):
+        self.nbytes = int(nbytes)
+        self.host = host
+        p = ctypes.c_void_p()
+        L = lib.load()
+        rc = (L.ssla_hip_malloc_host if host else L.ssla_hip_malloc_device)(self.nbytes, ctypes.byref(p))
+        lib.check(rc, "malloc")
+        self.ptr = int(p.value)
+
+    @classmethod
+    def from_array(cls, arr: np.ndarray, host: bool = False) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        b = cls(arr.nbytes, host=host)
+        b.upload(arr)
+        return b
+
+    def upload(self, arr: np.ndarray, offset: int = 0) -> None:
+        arr = np.ascontiguousarray(arr)
+        if offset + arr.nbytes > self.nbytes:
+            raise ValueError("upload past the end of the buffer")
+        lib.check(lib.load().ssla_hip_memcpy(self.ptr + offset, arr.ctypes.data, arr.nbytes), "memcpy")
+
+    def download(self, dtype, count: int, offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        if offset + out.nbytes > self.nbytes:
+            raise ValueError("download past the end of the buffer")
+        lib.check(lib.load().ssla_hip_memcpy(out.ctypes.data, self.ptr + offset, out.nbytes), "memcpy")
+        return out
+
+    def zero(self) -> None:
+        lib.check(lib.load().ssla_hip_memset(self.ptr, 0, self.nbytes), "memset")
+
+    def free(self) -> None:
+        if self.ptr:
+            L = lib.load()
+            (L.ssla_hip_free_host if self.host else L.ssla_hip_free_device)(self.ptr)
+            self.ptr = 0
+
+
+def download_ptr(ptr: int, dtype, count: int) -> np.ndarray:
+    out = np.empty(count, dtype=dtype)
+    if count:
+        lib.check(lib.load().ssla_hip_memcpy(out.ctypes.data, ptr, out.nbytes), "memcpy")
+    return out
+
+
+def upload_ptr(ptr: int, arr: np.ndarray) -> None:
+    arr = np.ascontiguousarray(arr)
+    lib.check(lib.load().ssla_hip_memcpy(ptr, arr.ctypes.data, arr.nbytes), "memcpy")
+
+
+# ---- packing (orin/orin/weights_ssla.py:24-88) ----------------------------
+
+@dataclass
+class PackedLayer:
+    """Fused weights in the reference (oracle) layout."""
+    qvgIn: np.ndarray               # (9, 3*out, in)
+    goW: np.ndarray                 # (9, out, out)
+    input_proj: Optional[np.ndarray]  # (out, in) or None
+    ln_gamma: np.ndarray
+    ln_beta: np.ndarray
+
+
+def pack_raw_layer(raw: RawLayer) -> PackedLayer:
+    """qvgIn[p] = [qW; vW; gW] @ scatter_p, goW[p] = gather_p @ oW (fp32)."""
+    i = raw.W_in_cat.shape[0]
+    D = raw.qW.shape[0]
+    n_in = raw.W_in_cat.shape[1] // D
+    n_out = raw.W_out_cat.shape[0] // D
+    A = max(n_in, n_out)
+    qvg = np.empty((A, 3 * D, i), np.float32)
+    go = np.empty((A, D, D), np.float32)
+    for p in range(A):
+        pin = 0 if n_in == 1 else p
+        pout = 0 if n_out == 1 else p
+        scatter = np.ascontiguousarray(raw.W_in_cat[:, pin * D:(pin + 1) * D].T)
+        gather = np.ascontiguousarray(raw.W_out_cat[pout * D:(pout + 1) * D, :].T)
+        qvg[p] = np.concatenate([raw.qW @ scatter, raw.vW @ scatter, raw.gW @ scatter])
+        go[p] = gather @ raw.oW
+    return PackedLayer(qvg, go, raw.input_proj, raw.ln_gamma, raw.ln_beta)
+
+
+def device_layouts(p: PackedLayer):
+    """(qvgIn (9, in, 3*out), goW (9, out_in, out_out), input_proj (in, out))."""
+    qvg = np.ascontiguousarray(p.qvgIn.transpose(0, 2, 1))
+    go = np.ascontiguousarray(p.goW.transpose(0, 2, 1))
+    ip = None if p.input_proj is None else np.ascontiguousarray(p.input_proj.T)
+    return qvg, go, ip
+
+
+# ---- the drain ---------------------------------------------------------------
+
+class Drain:
+    """Owns one HybridS2S3Config and its device state; runs drain calls."""
+
+    def __init__(self):
+        self.cfg = abi.HybridS2S3Config()
+        self._owned: List[DeviceBuffer] = []
+        self._model = ctypes.c_void_p()
+        self._state_blocks: List[int] = []
+        self._pred_blocks: List[int] = []
+        self._rings: List[Optional[DeviceBuffer]] = []
+        self._outs: List[Optional[DeviceBuffer]] = []
+        self._heads: List[Optional[DeviceBuffer]] = []
+
+    # -- construction ---------------------------------------------------------
+    @classmethod
+    def from_weights_dir(cls, weights_dir: str, n_blocks: int = 1,
+                         with_preds: bool = True) -> "Drain":
+        d = cls()
+        L = lib.load()
+        lib.check(L.ssla_hip_model_load(weights_dir.encode(), ctypes.byref(d._model)), "model_load")
+        lib.check(L.ssla_hip_config_bind(d._model, n_blocks, ctypes.byref(d.cfg)), "config_bind")
+        for b in range(n_blocks):
+            lib.check(L.ssla_hip_state_alloc(ctypes.byref(d.cfg), b), "state_alloc")
+            d._state_blocks.append(b)
+            if with_preds and d.cfg.head_cls_conv_W:
+                lib.check(L.ssla_hip_preds_alloc(ctypes.byref(d.cfg), b), "preds_alloc")
+                d._pred_blocks.append(b)
+        return d
+
+    @classmethod
+    def from_packed(cls, layers: Sequence[PackedLayer], H2: int, W2: int, window: int,
+                    n_blocks: int = 1, h_init: Optional[Sequence[np.ndarray]] = None,
+                    strips: Optional[Sequence[tuple]] = None) -> "Drain":
+        """Random / array layers (hybrid_common.build_random_layers +
+        build_config).  strips: per block (x_lo, x_hi, y_lo, y_hi) owned s2
+        box; default the whole grid."""
+        d = cls()
+        c = d.cfg
+        c.H2, c.W2, c.H3, c.W3 = H2, W2, H2 >> 1, W2 >> 1
+        c.tdrop_window = window
+        c.head_out_dim = abi.HEAD_OUT
+        c.n_blocks = n_blocks
+        ptrs = []
+        for li, p in enumerate(layers):
+            qvg, go, ip = device_layouts(p)
+            bufs = [DeviceBuffer.from_array(a) if a is not None else None
+                    for a in (qvg, go, ip, p.ln_gamma, p.ln_beta)]
+            d._owned += [b for b in bufs if b is not None]
+            ptrs.append([b.ptr if b is not None else None for b in bufs])
+        for b in range(n_blocks):
+            x_lo, x_hi, y_lo, y_hi = strips[b] if strips else (0, W2, 0, H2)
+            s = c.strip[b]
+            s.owned_lo, s.owned_hi, s.owned_y_lo, s.owned_y_hi = x_lo, x_hi, y_lo, y_hi
+            s.s3_owned_lo, s.s3_owned_hi = x_lo >> 1, x_hi >> 1
+            s.s3_owned_y_lo, s.s3_owned_y_hi = y_lo >> 1, y_hi >> 1
+            for li in range(4):
+                lw = c.layers[b][li]
+                lw.qvgIn, lw.goW, lw.input_proj, lw.ln_gamma, lw.ln_beta = ptrs[li]
+            lib.check(lib.load().ssla_hip_state_alloc(ctypes.byref(c), b), "state_alloc")
+            d._state_blocks.append(b)
+            if h_init is not None:
+                for li in range(4):
+                    upload_ptr(c.hidden[b][li], h_init[li])
+        return d
+
+    # -- state access ---------------------------------------------------------
+    def cells(self, li: int) -> int:
+        c = self.cfg
+        return c.H2 * c.W2 if li < 2 else c.H3 * c.W3
+
+    def hidden(self, blk: int, li: int) -> np.ndarray:
+        out = GPU_LAYER_IO[li][1]
+        return download_ptr(self.cfg.hidden[blk][li], np.float32, self.cells(li) * out).reshape(-1, out)
+
+    def set_hidden(self, blk: int, li: int, arr: np.ndarray) -> None:
+        upload_ptr(self.cfg.hidden[blk][li], arr.astype(np.float32))
+
+    def counters(self, blk: int):
+        c = self.cfg
+        return (download_ptr(c.tdrop_s2[blk], np.uint8, c.H2 * c.W2),
+                download_ptr(c.tdrop_s3[blk], np.uint8, c.H3 * c.W3))
+
+    def set_counters(self, blk: int, td2: np.ndarray, td3: np.ndarray) -> None:
+        upload_ptr(self.cfg.tdrop_s2[blk], td2.astype(np.uint8))
+        upload_ptr(self.cfg.tdrop_s3[blk], td3.astype(np.uint8))
+
+    def preds(self, blk: int):
+        s = self.cfg.strip[blk]
+        n = (s.s3_owned_hi - s.s3_owned_lo) * (s.s3_owned_y_hi - s.s3_owned_y_lo)
+        if not self.cfg.preds[blk]:
+            return None, None
+        return (download_ptr(self.cfg.preds[blk], np.float32, n * 7).reshape(n, 7),
+                download_ptr(self.cfg.version[blk], np.uint32, n))
+
+    def reset(self, stream: int = 0, sync: bool = True) -> None:
+        L = lib.load()
+        for b in self._state_blocks:
+            if sync:
+                lib.check(L.ssla_hip_state_reset(ctypes.byref(self.cfg), b), "state_reset")
+            else:
+                lib.check(L.ssla_hip_state_reset_async(ctypes.byref(self.cfg), b, stream or None),
+                          "state_reset_async")
+
+    # -- rings ------------------------------------------------------------------
+    def load_rings(self, records: Sequence[np.ndarray], want_head: bool = False) -> None:
+        """Copy each block's records into HBM (resident before any timing)."""
+        for bufs in (self._rings, self._outs, self._heads):
+            for b in bufs:
+                if b is not None:
+                    b.free()
+        self._rings, self._outs, self._heads = [], [], []
+        self._ns = [int(r.size) for r in records]
+        for r in records:
+            r = np.ascontiguousarray(r, dtype=abi.INPUT_DTYPE)
+            n = max(1, r.size)
+            rb = DeviceBuffer(n * abi.INPUT_DTYPE.itemsize)
+            if r.size:
+                rb.upload(r)
+            self._rings.append(rb)
+            self._outs.append(DeviceBuffer(n * abi.OUTPUT_DTYPE.itemsize))
+            self._heads.append(DeviceBuffer(n * 7 * 4) if want_head else None)
+
+    def run(self, stream: int = 0, sync: bool = True, phase_ms: Optional[np.ndarray] = None) -> None:
+        """One drain call over the loaded rings.  phase_ms (float32 array of
+        len(abi.DRAIN_PHASES)) accumulates per-phase GPU time (needs sync)."""
+        nb = self.cfg.n_blocks
+        if len(self._rings) != nb:
+            raise ValueError(f"load_rings needs {nb} rings")
+        rings = (ctypes.c_void_p * nb)(*[b.ptr for b in self._rings])
+        ns = (ctypes.c_int * nb)(*self._ns)
+        outs = (ctypes.c_void_p * nb)(*[b.ptr for b in self._outs])
+        opts = abi.SslaHipDrainOpts()
+        opts.stream = stream or None
+        opts.sync = 1 if sync else 0
+        heads = None
+        if self._heads and self._heads[0] is not None:
+            heads = (ctypes.c_void_p * nb)(*[b.ptr for b in self._heads])
+            opts.head_outs = ctypes.cast(heads, ctypes.POINTER(ctypes.c_void_p))
+        if phase_ms is not None:
+            assert phase_ms.dtype == np.float32 and phase_ms.size >= len(abi.DRAIN_PHASES)
+            opts.phase_ms = phase_ms.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+        lib.check(lib.load().ssla_hip_drain_n_ex(ctypes.byref(self.cfg), rings, ns, outs,
+                                                 ctypes.byref(opts)), "drain_n_ex")
+
+    def results(self):
+        outs, heads = [], []
+        for b in range(self.cfg.n_blocks):
+            n = self._ns[b]
+            outs.append(self._outs[b].download(abi.OUTPUT_DTYPE, n))
+            h = self._heads[b]
+            heads.append(h.download(np.float32, n * 7).reshape(n, 7) if h is not None else None)
+        return outs, heads
+
+    def drain(self, records: Sequence[np.ndarray], want_head: bool = False):
+        self.load_rings(records, want_head=want_head)
+        self.run()
+        return self.results()
+
+    def close(self) -> None:
+        L = lib.load()
+        for bufs in (self._rings, self._outs, self._heads):
+            for b in bufs:
+                if b is not None:
+                    b.free()
+        for b in self._pred_blocks:
+            L.ssla_hip_preds_free(ctypes.byref(self.cfg), b)
+        for b in self._state_blocks:
+            L.ssla_hip_state_free(ctypes.byref(self.cfg), b)
+        self._pred_blocks, self._state_blocks = [], []
+        for b in self._owned:
+            b.free()
+        self._owned = []
+        if self._model:
+            L.ssla_hip_model_free(self._model)
+            self._model = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()

@@ -1,0 +1,44 @@
+"""The C ABI library loads without a GPU, exports every entry point that
+include/*.h declares, and its struct layouts match the reference contracts
+(HybridInputRec 128 B, HybridS2S3Config 4616 B with preds at 3968,
+HybridS2S3OutputSlot 392 B, GpuTimingSlot 40 B).  No compute call here."""
+import ctypes
+import re
+from pathlib import Path
+
+from ssla_hip import abi, lib
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared(header: str):
+    text = (ROOT / "include" / header).read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ssla_hip_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = lib.load()
+    names = declared("ssla_hip.h")
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(L, n), n
+    assert sorted(lib.EXPORTED) == names
+
+
+def test_layout_matches_mirror():
+    lib.check_layout()
+    lay = lib.layout()
+    assert lay["HybridInputRec"] == 128
+    assert lay["HybridS2S3Config"] == 4616 and lay["preds_offset"] == 3968
+    assert lay["HybridS2S3OutputSlot"] == 392 and lay["GpuTimingSlot"] == 40
+    assert abi.HybridS2S3Config.hidden.offset == 8 * 4 + 16 * 32 + 16 * 4 * 40
+
+
+def test_errors_do_not_cross_the_boundary():
+    L = lib.load()
+    assert L.ssla_hip_drain_n(None, None, None, None, None) < 0
+    assert b"null" in L.ssla_hip_last_error()
+    m = ctypes.c_void_p()
+    assert L.ssla_hip_model_load(b"/nonexistent/dir", ctypes.byref(m)) < 0
+    assert not m.value
