@@ -200,10 +200,12 @@ __global__ void k_tdrop_commit(uint32_t nk, int C, const int* __restrict__ start
 // the patch cell is outside the grid (or the record does not enter).
 __global__ void k_pair_pos(int n, const uint32_t* __restrict__ keys,
                            const uint32_t* __restrict__ vals, uint32_t nk,
-                           int* __restrict__ pos) {
+                           int* __restrict__ pos, int* __restrict__ pair_rec) {
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= n) return;
-    pos[vals[p]] = keys[p] < nk ? p : -1;
+    const bool in = keys[p] < nk;
+    pos[vals[p]] = in ? p : -1;
+    pair_rec[p] = in ? (int)(vals[p] / kPatch) : 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -217,7 +219,8 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
       const float* __restrict__ X, const int* __restrict__ pos,
       const float* __restrict__ W, float* __restrict__ QVG) {
     constexpr int NC = 3 * OUT;
-    __shared__ float xs[kTE][IN];
+    static_assert(IN % 4 == 0, "IN must be a multiple of 4");
+    __shared__ __align__(16) float xs[kTE][IN];
     __shared__ int rows[kTE];
     const int n = n_dev ? *n_dev : n_max;
     const int base = blockIdx.x * kTE;
@@ -243,10 +246,17 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
         float acc[kTE];
         #pragma unroll
         for (int r = 0; r < kTE; ++r) acc[r] = 0.f;
-        for (int i = 0; i < IN; ++i) {
-            const float wi = w[(size_t)i * NC];
+        for (int i = 0; i < IN; i += 4) {
+            const float w0 = w[(size_t)i * NC], w1 = w[(size_t)(i + 1) * NC];
+            const float w2 = w[(size_t)(i + 2) * NC], w3 = w[(size_t)(i + 3) * NC];
             #pragma unroll
-            for (int r = 0; r < kTE; ++r) acc[r] = fmaf(wi, xs[r][i], acc[r]);
+            for (int r = 0; r < kTE; ++r) {
+                const float4 xv = *reinterpret_cast<const float4*>(&xs[r][i]);
+                float a = fmaf(w0, xv.x, acc[r]);
+                a = fmaf(w1, xv.y, a);
+                a = fmaf(w2, xv.z, a);
+                acc[r] = fmaf(w3, xv.w, a);
+            }
         }
         #pragma unroll
         for (int r = 0; r < kTE; ++r) {
@@ -259,44 +269,117 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 }
 
 // ---------------------------------------------------------------------------
-// S: one workgroup per cell, one lane per channel; walks the cell's pairs in
-// ring order.  h = sigmoid(g) h + v; the q slot of the row becomes q*h.
+// S: the per-cell recurrence h = sigmoid(g) h + v over a cell's pairs in ring
+// order.  A cell's run is cut into chunks of kCH pairs so the work spreads
+// over many workgroups:
+//   A (k_scan_summary) per chunk: the chunk's map h -> Aj h + Bj, composed
+//                      from its (g, v) rows
+//   B (k_scan_carry)   per cell: walks its chunks in order, records each
+//                      chunk's start state, stores the final state
+//   C (k_scan_apply)   per chunk: replays the chunk from its start state and
+//                      replaces q by q*h in place for pairs whose record
+//                      needs this layer's output
+// One lane per channel in all three passes.
 // ---------------------------------------------------------------------------
+constexpr int kCH = 64;
+
+// chunk table of every key: ckey / cbeg / cend, count in *n_chunks
+__global__ void k_chunk_count(uint32_t nk, const int* __restrict__ start,
+                              const int* __restrict__ end, int* __restrict__ cnt) {
+    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= nk) return;
+    const int len = end[k] - start[k];
+    cnt[k] = len > 0 ? (len + kCH - 1) / kCH : 0;
+}
+
+__global__ void k_chunk_fill(uint32_t nk, const int* __restrict__ start,
+                             const int* __restrict__ end, const int* __restrict__ cnt,
+                             const int* __restrict__ coff, int* __restrict__ ckey,
+                             int* __restrict__ cbeg, int* __restrict__ cend,
+                             int* __restrict__ n_chunks) {
+    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= nk) return;
+    const int c0 = coff[k], nc = cnt[k], s = start[k], e = end[k];
+    for (int c = 0; c < nc; ++c) {
+        ckey[c0 + c] = (int)k;
+        cbeg[c0 + c] = s + c * kCH;
+        cend[c0 + c] = min(e, s + (c + 1) * kCH);
+    }
+    if (k == nk - 1) *n_chunks = c0 + nc;
+}
+
 template <int OUT>
 __global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
-k_scan(int C, const int* __restrict__ start, const int* __restrict__ end,
-       const BlockDesc* __restrict__ bd, int li, float* __restrict__ QVG) {
+k_scan_summary(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
+               const int* __restrict__ cend, const float* __restrict__ QVG,
+               float* __restrict__ Asum, float* __restrict__ Bsum) {
     constexpr int NC = 3 * OUT;
-    const int k = blockIdx.x;
+    const int j = blockIdx.x;
     const int c = threadIdx.x;
-    if (c >= OUT) return;
-    const int s = start[k], e = end[k];
-    if (e <= s) return;
-    const int b = k / C, cell = k % C;
-    float* hp = bd[b].hidden[li] + (size_t)cell * OUT + c;
-    float h = *hp;
-    float* row = QVG + (size_t)s * NC + c;
+    if (j >= *n_chunks || c >= OUT) return;
+    const int s = cbeg[j], e = cend[j];
+    const float* row = QVG + (size_t)s * NC + OUT + c;     // v at +0, g at +OUT
+    float A = 1.f, B = 0.f;
     int p = s;
     for (; p + 4 <= e; p += 4, row += 4 * NC) {
-        float q[4], v[4], gg[4];
+        float v[4], g[4];
         #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            q[j] = row[j * NC];
-            v[j] = row[j * NC + OUT];
-            gg[j] = row[j * NC + 2 * OUT];
-        }
+        for (int q = 0; q < 4; ++q) { v[q] = row[q * NC]; g[q] = row[q * NC + OUT]; }
         #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            h = fmaf(sigmoid_fast(gg[j]), h, v[j]);
-            row[j * NC] = q[j] * h;
+        for (int q = 0; q < 4; ++q) {
+            const float a = sigmoid_fast(g[q]);
+            A *= a;
+            B = fmaf(a, B, v[q]);
         }
     }
     for (; p < e; ++p, row += NC) {
-        const float q = row[0], v = row[OUT], gg = row[2 * OUT];
-        h = fmaf(sigmoid_fast(gg), h, v);
-        row[0] = q * h;
+        const float a = sigmoid_fast(row[OUT]);
+        A *= a;
+        B = fmaf(a, B, row[0]);
+    }
+    Asum[(size_t)j * OUT + c] = A;
+    Bsum[(size_t)j * OUT + c] = B;
+}
+
+template <int OUT>
+__global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
+k_scan_carry(int C, const int* __restrict__ start, const int* __restrict__ end,
+             const int* __restrict__ coff, const int* __restrict__ cnt,
+             const BlockDesc* __restrict__ bd, int li, const float* __restrict__ Asum,
+             const float* __restrict__ Bsum, float* __restrict__ Hs) {
+    const int k = blockIdx.x;
+    const int c = threadIdx.x;
+    if (c >= OUT || end[k] <= start[k]) return;
+    const int b = k / C, cell = k % C;
+    float* hp = bd[b].hidden[li] + (size_t)cell * OUT + c;
+    float h = *hp;
+    const int c0 = coff[k], nc = cnt[k];
+    for (int q = 0; q < nc; ++q) {
+        const size_t o = (size_t)(c0 + q) * OUT + c;
+        Hs[o] = h;
+        h = fmaf(Asum[o], h, Bsum[o]);
     }
     *hp = h;
+}
+
+template <int OUT>
+__global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
+k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
+             const int* __restrict__ cend, const float* __restrict__ Hs,
+             const int* __restrict__ pair_rec, const unsigned char* __restrict__ need,
+             float* __restrict__ QVG) {
+    constexpr int NC = 3 * OUT;
+    const int j = blockIdx.x;
+    const int c = threadIdx.x;
+    if (j >= *n_chunks || c >= OUT) return;
+    const int s = cbeg[j], e = cend[j];
+    float h = Hs[(size_t)j * OUT + c];
+    float* row = QVG + (size_t)s * NC + c;
+    for (int p = s; p < e; ++p, row += NC) {
+        const float v = row[OUT], g = row[2 * OUT];
+        h = fmaf(sigmoid_fast(g), h, v);
+        if (!need || need[pair_rec[p]]) row[0] *= h;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -311,10 +394,13 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
       const float* __restrict__ ip, const float* __restrict__ gamma,
       const float* __restrict__ beta, float* __restrict__ Y) {
     constexpr int NC = 3 * OUT;
-    __shared__ float vs[kTE][OUT > IN ? OUT : IN];
+    static_assert(IN % 4 == 0 && OUT % 4 == 0, "widths must be multiples of 4");
+    constexpr int VS = OUT > IN ? OUT : IN;
+    __shared__ __align__(16) float vs[kTE][VS];
     __shared__ float ys[kTE][OUT + 1];
     __shared__ double stat[kTE][2];
     __shared__ int rows[kTE];
+    __shared__ int prow[kPatch][kTE];
     const int n = n_dev ? *n_dev : n_max;
     const int base = blockIdx.x * kTE;
     if (base >= n) return;
@@ -323,44 +409,67 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
     if (threadIdx.x < kTE)
         rows[threadIdx.x] = threadIdx.x < cnt
             ? (list ? list[base + threadIdx.x] : base + threadIdx.x) : -1;
+    __syncthreads();
+    // pair rows of the tile's records, all deltas, staged once
+    for (int t = threadIdx.x; t < kTE * kPatch; t += blockDim.x) {
+        const int r = t / kPatch, d = t % kPatch;
+        const int g = rows[r];
+        prow[d][r] = g >= 0 ? pos[(size_t)g * kPatch + d] : -1;
+    }
     float acc[kTE];
     #pragma unroll
     for (int r = 0; r < kTE; ++r) acc[r] = 0.f;
+    constexpr int Q4 = OUT / 4;
     for (int d = 0; d < kPatch; ++d) {
         __syncthreads();
-        for (int t = threadIdx.x; t < kTE * OUT; t += blockDim.x) {
-            const int r = t / OUT, i = t % OUT;
-            const int g = rows[r];
-            float v = 0.f;
-            if (g >= 0) {
-                const int pr = pos[(size_t)g * kPatch + d];
-                if (pr >= 0) v = QVG[(size_t)pr * NC + i];
-            }
-            vs[r][i] = v;
+        // gather the q*h rows: independent float4 loads
+        for (int t = threadIdx.x; t < kTE * Q4; t += blockDim.x) {
+            const int r = t / Q4, q = t % Q4;
+            const int pr = prow[d][r];
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (pr >= 0) v = *reinterpret_cast<const float4*>(QVG + (size_t)pr * NC + 4 * q);
+            *reinterpret_cast<float4*>(&vs[r][4 * q]) = v;
         }
         __syncthreads();
         if (o < OUT) {
             const float* w = goW + (size_t)d * OUT * OUT + o;
-            for (int i = 0; i < OUT; ++i) {
-                const float wi = w[(size_t)i * OUT];
+            for (int i = 0; i < OUT; i += 4) {
+                const float w0 = w[(size_t)i * OUT], w1 = w[(size_t)(i + 1) * OUT];
+                const float w2 = w[(size_t)(i + 2) * OUT], w3 = w[(size_t)(i + 3) * OUT];
                 #pragma unroll
-                for (int r = 0; r < kTE; ++r) acc[r] = fmaf(wi, vs[r][i], acc[r]);
+                for (int r = 0; r < kTE; ++r) {
+                    const float4 v = *reinterpret_cast<const float4*>(&vs[r][i]);
+                    float a = fmaf(w0, v.x, acc[r]);
+                    a = fmaf(w1, v.y, a);
+                    a = fmaf(w2, v.z, a);
+                    acc[r] = fmaf(w3, v.w, a);
+                }
             }
         }
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < kTE * IN; t += blockDim.x) {
-        const int r = t / IN, i = t % IN;
+    constexpr int I4 = IN / 4;
+    for (int t = threadIdx.x; t < kTE * I4; t += blockDim.x) {
+        const int r = t / I4, q = t % I4;
         const int g = rows[r];
-        vs[r][i] = g >= 0 ? X[(size_t)g * IN + i] : 0.f;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (g >= 0) v = *reinterpret_cast<const float4*>(X + (size_t)g * IN + 4 * q);
+        *reinterpret_cast<float4*>(&vs[r][4 * q]) = v;
     }
     __syncthreads();
     if (o < OUT) {
         if (ip) {
-            for (int i = 0; i < IN; ++i) {
-                const float wi = ip[(size_t)i * OUT + o];
+            for (int i = 0; i < IN; i += 4) {
+                const float w0 = ip[(size_t)i * OUT + o], w1 = ip[(size_t)(i + 1) * OUT + o];
+                const float w2 = ip[(size_t)(i + 2) * OUT + o], w3 = ip[(size_t)(i + 3) * OUT + o];
                 #pragma unroll
-                for (int r = 0; r < kTE; ++r) acc[r] = fmaf(wi, vs[r][i], acc[r]);
+                for (int r = 0; r < kTE; ++r) {
+                    const float4 v = *reinterpret_cast<const float4*>(&vs[r][i]);
+                    float a = fmaf(w0, v.x, acc[r]);
+                    a = fmaf(w1, v.y, a);
+                    a = fmaf(w2, v.z, a);
+                    acc[r] = fmaf(w3, v.w, a);
+                }
             }
         } else {
             #pragma unroll
@@ -540,6 +649,11 @@ struct Workspace {
     float *X0, *X1, *X2, *X3, *X4, *QVG, *H7;
     int *cell2, *pos2, *pos3, *list2, *list3, *counts;
     int *st2, *en2, *st3, *en3, *pst2, *pen2, *pst3, *pen3, *last3, *cnt3;
+    int *prec2, *prec3;                        // record of each sorted pair
+    int *ccnt2, *coff2, *ccnt3, *coff3;        // chunks per key, offsets
+    int *ckey2, *cbeg2, *cend2, *ckey3, *cbeg3, *cend3;
+    float *Asum, *Bsum, *Hs;
+    int max_chunks = 0;
     unsigned char *owner, *pass2, *pass3;
     uint32_t *ka, *kb, *va, *vb, *key3g;
     BlockDesc* bd;
@@ -582,7 +696,10 @@ int ensure_workspace(int E, int nkeys) {
     HIPCHK(hipcub::DeviceSelect::Flagged(nullptr, t_sel, hipcub::CountingInputIterator<int>(0),
                                           (unsigned char*)nullptr, (int*)nullptr,
                                           (int*)nullptr, cap));
-    const size_t temp = std::max(t_sort, t_sel);
+    size_t t_scan = 0;
+    HIPCHK(hipcub::DeviceScan::ExclusiveSum(nullptr, t_scan, (int*)nullptr, (int*)nullptr, ck));
+    const size_t temp = std::max(std::max(t_sort, t_sel), t_scan);
+    const size_t mc = P / kCH + (size_t)ck + 1;    // chunk bound: full chunks + one tail per key
     struct Item { void** dst; size_t bytes; };
     Workspace& w = g_ws;
     std::vector<Item> items = {
@@ -598,7 +715,7 @@ int ensure_workspace(int E, int nkeys) {
         {(void**)&w.pos3, sizeof(int) * P},
         {(void**)&w.list2, sizeof(int) * (size_t)cap},
         {(void**)&w.list3, sizeof(int) * (size_t)cap},
-        {(void**)&w.counts, sizeof(int) * 4},
+        {(void**)&w.counts, sizeof(int) * 8},
         {(void**)&w.st2, sizeof(int) * (size_t)ck},
         {(void**)&w.en2, sizeof(int) * (size_t)ck},
         {(void**)&w.st3, sizeof(int) * (size_t)ck},
@@ -617,6 +734,21 @@ int ensure_workspace(int E, int nkeys) {
         {(void**)&w.va, sizeof(uint32_t) * P},
         {(void**)&w.vb, sizeof(uint32_t) * P},
         {(void**)&w.key3g, sizeof(uint32_t) * (size_t)cap},
+        {(void**)&w.prec2, sizeof(int) * P},
+        {(void**)&w.prec3, sizeof(int) * P},
+        {(void**)&w.ccnt2, sizeof(int) * (size_t)ck},
+        {(void**)&w.coff2, sizeof(int) * (size_t)ck},
+        {(void**)&w.ccnt3, sizeof(int) * (size_t)ck},
+        {(void**)&w.coff3, sizeof(int) * (size_t)ck},
+        {(void**)&w.ckey2, sizeof(int) * mc},
+        {(void**)&w.cbeg2, sizeof(int) * mc},
+        {(void**)&w.cend2, sizeof(int) * mc},
+        {(void**)&w.ckey3, sizeof(int) * mc},
+        {(void**)&w.cbeg3, sizeof(int) * mc},
+        {(void**)&w.cend3, sizeof(int) * mc},
+        {(void**)&w.Asum, sizeof(float) * mc * SSLA_C3},
+        {(void**)&w.Bsum, sizeof(float) * mc * SSLA_C3},
+        {(void**)&w.Hs, sizeof(float) * mc * SSLA_C3},
         {(void**)&w.bd, sizeof(BlockDesc) * SSLA_MAX_BLOCKS},
         {(void**)&w.temp, temp},
     };
@@ -639,6 +771,7 @@ int ensure_workspace(int E, int nkeys) {
     w.cap = cap;
     w.cap_keys = ck;
     w.temp_bytes = temp;
+    w.max_chunks = (int)mc;
     return SSLA_OK;
 }
 
@@ -784,7 +917,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.pen2, 0);
     hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, nk2, w.pst2, w.pen2);
     hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, w.va, nk2,
-                       w.pos2);
+                       w.pos2, w.prec2);
     // ---- tdrop_s3 over pass2 records, by s3 centre cell ---------------------
     hipLaunchKernelGGL(k_keys3, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, w.cell2,
                        w.pass2, w.key3g, w.ka, w.va);
@@ -806,7 +939,18 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.pen3, 0);
     hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, nk3, w.pst3, w.pen3);
     hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, w.va, nk3,
-                       w.pos3);
+                       w.pos3, w.prec3);
+    // ---- chunk tables of the per-cell pair runs ---------------------------------
+    hipLaunchKernelGGL(k_chunk_count, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, w.pst2,
+                       w.pen2, w.ccnt2);
+    HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt2, w.coff2, (int)nk2, st));
+    hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, w.pst2,
+                       w.pen2, w.ccnt2, w.coff2, w.ckey2, w.cbeg2, w.cend2, w.counts + 2);
+    hipLaunchKernelGGL(k_chunk_count, dim3(grid1(nk3, 256)), dim3(256), 0, st, nk3, w.pst3,
+                       w.pen3, w.ccnt3);
+    HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt3, w.coff3, (int)nk3, st));
+    hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(nk3, 256)), dim3(256), 0, st, nk3, w.pst3,
+                       w.pen3, w.ccnt3, w.coff3, w.ckey3, w.cbeg3, w.cend3, w.counts + 3);
     // ---- record lists: pass2 records, pass3 records (ring order) --------------
     HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
                                           w.pass2, w.list2, w.counts + 0, E, st));
@@ -822,8 +966,12 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(192), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, L[0].qvgIn, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_scan<SSLA_C2>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
-                       w.bd, 0, w.QVG);
+    hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
+                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
+    hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
+                       w.coff2, w.ccnt2, w.bd, 0, w.Asum, w.Bsum, w.Hs);
+    hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
+                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, (const unsigned char*)nullptr, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_out<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(64), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, L[0].goW,
@@ -833,8 +981,12 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(192), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, L[1].qvgIn, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_scan<SSLA_C2>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
-                       w.bd, 1, w.QVG);
+    hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
+                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
+    hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
+                       w.coff2, w.ccnt2, w.bd, 1, w.Asum, w.Bsum, w.Hs);
+    hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
+                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, w.pass2, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(64), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, L[1].goW,
@@ -844,8 +996,12 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(320), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, L[2].qvgIn, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_scan<SSLA_C3>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
-                       w.bd, 2, w.QVG);
+    hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
+                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
+    hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
+                       w.coff3, w.ccnt3, w.bd, 2, w.Asum, w.Bsum, w.Hs);
+    hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
+                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, (const unsigned char*)nullptr, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(128), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, L[2].goW,
@@ -855,8 +1011,12 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(320), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, L[3].qvgIn, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_scan<SSLA_C3>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
-                       w.bd, 3, w.QVG);
+    hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
+                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
+    hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
+                       w.coff3, w.ccnt3, w.bd, 3, w.Asum, w.Bsum, w.Hs);
+    hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
+                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, w.pass3, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_out<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(128), 0, st, E,
                        (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, L[3].goW,

@@ -22,8 +22,15 @@ from ssla_hip import abi, events
 
 pytestmark = pytest.mark.gpu
 
-FEAT_TOL = 2e-3
-HEAD_TOL = 2e-3
+FEAT_TOL = 1e-4
+HEAD_TOL = 5e-5
+# Hidden states grow to |h| ~ 70 over a run; they are compared relative to
+# their magnitude (the sequential fp32 oracle itself drifts ~1.4e-6 relative).
+HIDDEN_REL_TOL = 2e-5
+
+
+def hidden_close(a, b):
+    return np.abs(a - b).max() <= HIDDEN_REL_TOL * max(1.0, float(np.abs(b).max()))
 
 
 def say(*a):
@@ -78,7 +85,7 @@ def test_p1_single_domain(H):
         compare(out, p2, p3, feat, "p1")
         # hidden state and counters after the run
         for li in range(4):
-            assert np.abs(d.hidden(0, li) - st.H[li]).max() < FEAT_TOL
+            assert hidden_close(d.hidden(0, li), st.H[li]), li
         td2, td3 = d.counters(0)
         assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3)
 
@@ -247,4 +254,4 @@ def test_full_size_properties(H, stub_dir):
         say(f"full_size: split vs whole s3_feat max|d| = {dd:.3g}")
         assert dd <= FEAT_TOL
         for li in range(4):
-            assert np.abs(d.hidden(0, li) - h_a[li]).max() <= FEAT_TOL
+            assert hidden_close(d.hidden(0, li), h_a[li]), li
