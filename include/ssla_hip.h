@@ -124,8 +124,11 @@ void ssla_hip_preds_free(HybridS2S3Config* cfg, int blk);
  *   outs[b]    NULL or device pointer to ns[b] output slots: pass2/pass3 as
  *              1/0 for owned records and -1 for halo records; s3_feat holds
  *              the L7 output for pass-3 records and zeros otherwise
- *   batch_clks must be NULL (per-8-record clock pairs do not exist in the
- *              whole-ring scan; see ssla_hip_drain_n_ex / timing)
+ *   batch_clks NULL: the whole ring is drained at once (fastest).  Non-NULL:
+ *              records are taken in in-kernel batches of 8, one workgroup
+ *              per block, and batch_clks[b] (NULL or device memory, 2 u64
+ *              per batch) receives (t_pop, t_done) wall-clock ticks of each
+ *              batch (ssla_hip_wall_clock_khz gives the rate).
  * Records outside the s2 grid leave all state untouched and report
  * pass2 = pass3 = -2.  Synchronous.  Weights must be shared by all blocks. */
 int ssla_hip_drain_n(const HybridS2S3Config* cfg,
@@ -147,7 +150,8 @@ int ssla_hip_drain_n2(const HybridS2S3Config* cfg,
 typedef struct SslaHipDrainOpts {
     void*         stream;      /* hipStream_t; NULL = default stream */
     int           sync;        /* nonzero: wait for completion */
-    int           reserved;
+    int           batch;       /* 0: whole-ring drain; 1..32: in-kernel
+                                  batches of this many records */
     float* const* head_outs;   /* NULL or [n_blocks] device pointers to
                                   (ns[b], 7) raw head outputs, written for
                                   owned pass-3 records, zeros otherwise */
@@ -160,6 +164,54 @@ int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg,
                         const HybridInputRec* const* rings, const int* ns,
                         HybridS2S3OutputSlot* const* outs,
                         const SslaHipDrainOpts* opts);
+
+/* Ticks per millisecond of the constant-rate GPU clock used by batch_clks
+ * and GpuTimingSlot (s_memrealtime). */
+int ssla_hip_wall_clock_khz(int* out);
+
+/* Timing ring of block blk: `capacity` (power of two) GpuTimingSlot in HBM,
+ * timing_mask = capacity - 1, and kernel_start_clk / kernel_end_clk anchors
+ * in fine-grained host memory (hybrid_common.py:274-310).  All zeroed. */
+int  ssla_hip_timing_alloc(HybridS2S3Config* cfg, int blk, unsigned int capacity);
+void ssla_hip_timing_free(HybridS2S3Config* cfg, int blk);
+
+/* ---- persistent live drain --------------------------------------------
+ * Replaces k_ssla_s2s3_celled_persistent_multi
+ * (orin/kernels/ssla_s2_s3_head_celled.cuh:1547-1784) and its launch in
+ * orin/hybrid_runner_multi.py:514-523.  One workgroup per block polls
+ * rings[b] (capacity ring_mask + 1, a power of two, in fine-grained host
+ * memory): slot t is ready when its seq_done == t + 1.  Ready records are
+ * processed in ring order in batches of up to opts->max_batch; the head
+ * writes preds / version (last write per cell wins); GpuTimingSlot entries
+ * are written when cfg->timing[b] is set; *tails[b] and *events_done[b]
+ * advance (system-scope release) after each batch.  spin_ns is the idle
+ * sleep between polls.  The kernel returns when *stop_flag becomes
+ * nonzero, when a producer laps the ring (status 2), or after
+ * opts->idle_timeout_ms without a ready record (status 3).
+ * The kernel runs on its own non-blocking stream; do not call
+ * ssla_hip_device_synchronize while it runs. */
+typedef struct SslaHipLive SslaHipLive;
+
+typedef struct SslaHipLiveOpts {
+    int          max_batch;        /* 1..32; default 32 */
+    unsigned int idle_timeout_ms;  /* default 30000 */
+} SslaHipLiveOpts;
+
+int ssla_hip_persistent_start(const HybridS2S3Config* cfg,
+                              HybridInputRec* const* rings,
+                              unsigned long long ring_mask,
+                              unsigned long long* const* tails,
+                              int* stop_flag,
+                              unsigned long long* const* events_done,
+                              unsigned int spin_ns,
+                              const SslaHipLiveOpts* opts,
+                              SslaHipLive** out);
+
+/* Waits (up to timeout_ms, < 0 = forever) for the kernel to return after
+ * the caller set *stop_flag, then frees the session.  *status: 0 stopped
+ * by the flag, 2 ring overrun, 3 idle timeout.  Returns SSLA_ERR_STATE if
+ * the kernel is still running at the timeout (the session stays valid). */
+int ssla_hip_persistent_wait(SslaHipLive* h, int timeout_ms, int* status);
 
 #ifdef __cplusplus
 }

@@ -14,6 +14,7 @@
 #include <string>
 #include <vector>
 
+#include "drain_live.h"
 #include "drain_scan.h"
 #include "ssla_hip.h"
 #include "weights_dir.h"
@@ -263,8 +264,8 @@ int ssla_hip_memcpy(void* dst, const void* src, size_t nbytes) {
 int ssla_hip_memset(void* dst, int value, size_t nbytes) {
     if (!nbytes) return SSLA_OK;
     if (!dst) { set_error("null pointer"); return SSLA_ERR_ARG; }
-    API_HIP(hipMemset(dst, value, nbytes));
-    API_HIP(hipDeviceSynchronize());
+    API_HIP(hipMemsetAsync(dst, value, nbytes, nullptr));
+    API_HIP(hipStreamSynchronize(nullptr));
     return SSLA_OK;
 }
 
@@ -459,7 +460,7 @@ int ssla_hip_state_alloc(HybridS2S3Config* cfg, int blk) {
     void* base = nullptr;
     API_HIP(hipMalloc(&base, total));
     API_HIP(hipMemset(base, 0, total));
-    API_HIP(hipDeviceSynchronize());
+    API_HIP(hipStreamSynchronize(nullptr));
     char* p = static_cast<char*>(base);
     void* parts[6];
     for (int i = 0; i < 6; ++i) {
@@ -485,7 +486,7 @@ int ssla_hip_state_reset(const HybridS2S3Config* cfg, int blk) {
     if (!cfg->tdrop_s2[blk] || !cfg->tdrop_s3[blk]) { set_error("tdrop counters not allocated"); return SSLA_ERR_STATE; }
     API_HIP(hipMemset(cfg->tdrop_s2[blk], 0, c2));
     API_HIP(hipMemset(cfg->tdrop_s3[blk], 0, c3));
-    API_HIP(hipDeviceSynchronize());
+    API_HIP(hipStreamSynchronize(nullptr));
     return SSLA_OK;
 }
 
@@ -554,23 +555,93 @@ int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg, const HybridInputRec* const
     const bool sync = opts ? opts->sync != 0 : true;
     float* phase_ms = opts ? opts->phase_ms : nullptr;
     if (phase_ms && !sync) { set_error("phase_ms needs sync"); return SSLA_ERR_ARG; }
+    const int batch = opts ? opts->batch : 0;
+    if (batch != 0) {
+        if (phase_ms) { set_error("phase_ms is only measured by the whole-ring drain"); return SSLA_ERR_ARG; }
+        return batch_drain(cfg, rings, ns, outs, opts->head_outs, nullptr, batch, st, sync);
+    }
     return scan_drain(cfg, rings, ns, outs, opts ? opts->head_outs : nullptr, st, sync, phase_ms);
 }
 
 int ssla_hip_drain_n(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                      const int* ns, HybridS2S3OutputSlot* const* outs,
                      unsigned long long* const* batch_clks) {
+    if (!cfg || !rings || !ns) { set_error("null argument"); return SSLA_ERR_ARG; }
     if (batch_clks) {
-        for (int b = 0; cfg && b < cfg->n_blocks; ++b) {
-            if (batch_clks[b]) {
-                set_error("batch_clks are not produced by the whole-ring drain; pass NULL");
-                return SSLA_ERR_ARG;
-            }
-        }
+        // the reference's drain_n batching: 8 records per batch, clock pairs
+        return batch_drain(cfg, rings, ns, outs, nullptr, batch_clks, 8, nullptr, true);
     }
     SslaHipDrainOpts o{};
     o.sync = 1;
     return ssla_hip_drain_n_ex(cfg, rings, ns, outs, &o);
+}
+
+int ssla_hip_wall_clock_khz(int* out) {
+    if (!out) { set_error("null argument"); return SSLA_ERR_ARG; }
+    API_HIP(hipDeviceGetAttribute(out, hipDeviceAttributeWallClockRate, 0));
+    return SSLA_OK;
+}
+
+int ssla_hip_timing_alloc(HybridS2S3Config* cfg, int blk, unsigned int capacity) {
+    if (!cfg || blk < 0 || blk >= SSLA_MAX_BLOCKS) { set_error("bad block"); return SSLA_ERR_ARG; }
+    if (capacity == 0 || (capacity & (capacity - 1))) { set_error("capacity must be a power of two"); return SSLA_ERR_ARG; }
+    if (cfg->timing_mask && cfg->timing_mask != capacity - 1) {
+        set_error("all blocks share one timing capacity");
+        return SSLA_ERR_ARG;
+    }
+    void* t = nullptr;
+    API_HIP(hipMalloc(&t, sizeof(GpuTimingSlot) * (size_t)capacity));
+    API_HIP(hipMemset(t, 0, sizeof(GpuTimingSlot) * (size_t)capacity));
+    API_HIP(hipStreamSynchronize(nullptr));
+    void* clk = nullptr;
+    if (hipHostMalloc(&clk, 16, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess) {
+        (void)hipFree(t);
+        set_error("hipHostMalloc of clock anchors failed");
+        return SSLA_ERR_HIP;
+    }
+    std::memset(clk, 0, 16);
+    cfg->timing[blk] = static_cast<GpuTimingSlot*>(t);
+    cfg->timing_mask = capacity - 1;
+    cfg->kernel_start_clk[blk] = static_cast<unsigned long long*>(clk);
+    cfg->kernel_end_clk[blk] = static_cast<unsigned long long*>(clk) + 1;
+    std::lock_guard<std::mutex> lk(g_alloc_mu);
+    g_state_bases.insert(t);
+    g_pred_bases.insert(clk);
+    return SSLA_OK;
+}
+
+void ssla_hip_timing_free(HybridS2S3Config* cfg, int blk) {
+    if (!cfg || blk < 0 || blk >= SSLA_MAX_BLOCKS) return;
+    void* t = cfg->timing[blk];
+    void* clk = cfg->kernel_start_clk[blk];
+    std::lock_guard<std::mutex> lk(g_alloc_mu);
+    if (t && g_state_bases.erase(t)) {
+        (void)hipFree(t);
+        cfg->timing[blk] = nullptr;
+    }
+    if (clk && g_pred_bases.erase(clk)) {
+        (void)hipHostFree(clk);
+        cfg->kernel_start_clk[blk] = nullptr;
+        cfg->kernel_end_clk[blk] = nullptr;
+    }
+}
+
+int ssla_hip_persistent_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
+                              unsigned long long ring_mask, unsigned long long* const* tails,
+                              int* stop_flag, unsigned long long* const* events_done,
+                              unsigned int spin_ns, const SslaHipLiveOpts* opts, SslaHipLive** out) {
+    if (!cfg || !rings || !tails || !out) { set_error("null argument"); return SSLA_ERR_ARG; }
+    const int max_batch = (opts && opts->max_batch) ? opts->max_batch : kLiveBatchMax;
+    const unsigned idle = (opts && opts->idle_timeout_ms) ? opts->idle_timeout_ms : 30000u;
+    LiveSession* s = nullptr;
+    const int rc = live_start(cfg, rings, ring_mask, tails, stop_flag, events_done, spin_ns,
+                              max_batch, idle, &s);
+    *out = reinterpret_cast<SslaHipLive*>(s);
+    return rc;
+}
+
+int ssla_hip_persistent_wait(SslaHipLive* h, int timeout_ms, int* status) {
+    return live_wait(reinterpret_cast<LiveSession*>(h), timeout_ms, status);
 }
 
 int ssla_hip_drain_n2(const HybridS2S3Config* cfg, const HybridInputRec* ring0,

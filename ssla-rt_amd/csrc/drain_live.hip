@@ -1,0 +1,843 @@
+// drain_live.hip -- in-kernel batches of SSLA-S s2 + s3 + YOLOX head on
+// gfx950: the persistent live drain and the batch-mode drain.
+//
+// One 512-thread workgroup owns one stream (block): its hidden state, tdrop
+// counters, ring and outputs.  Records are taken in batches of up to 32 in
+// ring order, and each batch runs the same decomposition as the whole-ring
+// drain, inside the workgroup:
+//   tdrop   one wave, one lane per record: arrival rank among the batch's
+//           records at the same cell (ssla_ref.py:190-195)
+//   pairs   one wave builds the (record, delta) pairs in record order, the
+//           per-delta record lists, and per-cell successor links
+//   P       q, v, g rows, grouped by delta so each weight matrix streams
+//           through the CU once per batch (rows in a per-stream L2 scratch)
+//   S       one lane per (cell, channel) walks the cell's pairs in record
+//           order: h = sigmoid(g) h + v, q*h where the output is consumed
+//   O       one thread per (channel, record group): goW contraction over
+//           the record's pairs + residual, then fp64 LayerNorm per wave
+// The masks are the reference's (...celled.cuh:1027-1064): L4 all, L5 state
+// for all / output for pass2, L6 pass2, L7 state for pass2 / output for
+// pass3, head for owned pass3 records.
+//
+// The live kernel polls a ring in fine-grained host memory: one wave loads
+// 64 consecutive seq_done tags with system-scope acquire (one PCIe round
+// trip) and takes the ready prefix.  It stops on the host's stop flag, on a
+// ring overrun, or after an idle timeout on the constant-rate wall clock, so
+// every wave always reaches an exit.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <thread>
+#include <string>
+#include <vector>
+
+#include "drain_common.h"
+#include "drain_live.h"
+
+namespace ssla {
+
+struct LiveWeights {
+    LayerWeightsS2S3 L[4];
+    HeadPtrs head;
+    int have_head;
+};
+
+// Per-block view of the state, ring and outputs (device memory).
+struct LiveDesc {
+    const HybridInputRec* ring;
+    unsigned long long ring_mask;       // live: capacity - 1; batch mode: ~0
+    unsigned long long* tail;           // live: consumer position (host memory)
+    unsigned long long* events_done;    // live: mirror of tail for monitors
+    int n;                              // batch mode: records to drain
+    int pad0;
+    float* hidden[4];
+    unsigned char* td2;
+    unsigned char* td3;
+    float* scratch;                     // (LP + 1) rows of 3*96 floats; last row zero
+    HybridS2S3OutputSlot* out;          // batch mode
+    float* head_out;                    // batch mode
+    unsigned long long* batch_clk;      // batch mode
+    float* preds;
+    unsigned int* version;
+    GpuTimingSlot* timing;
+    unsigned int timing_mask;
+    unsigned int pad1;
+    unsigned long long* kstart;
+    unsigned long long* kend;
+    HybridStrip strip;
+};
+
+namespace {
+
+constexpr int LB = kLiveBatchMax;   // records per batch, at most
+constexpr int LT = 512;             // threads per workgroup
+constexpr int NW = LT / 64;         // waves per workgroup
+constexpr int LP = kPatch * LB;     // pairs per layer, at most
+constexpr int NCMAX = 3 * SSLA_C3;  // widest pair row
+constexpr int kWB = 24;             // weights held in registers per block (divides 24, 48, 96)
+
+struct Lds {
+    float X[LB][SSLA_C3];           // layer input (becomes the layer output)
+    float Y[LB][SSLA_C3];           // pre-LayerNorm sums / head cls hidden
+    float R[LB][SSLA_C3];           // head reg hidden
+    float H7[LB][8];
+    double stat[LB][2];
+    unsigned long long tpush[LB], temit[LB];
+    int ex[LB], ey[LB];             // coordinates at the current level
+    int c2[LB], c3[LB];             // s2 / s3 centre cell, -1 when absent
+    unsigned char vld[LB], own[LB], p2[LB], p3[LB];
+    int pidx[LB][kPatch];           // pair of (record, delta), or -1
+    int pe[LP], pc[LP], pnext[LP], lead[LP];
+    int dcnt[kPatch];
+    int dev[kPatch][LB];
+    int dpos[LB][kPatch];           // position of (record, delta) in dev[delta]
+    int npair, nlead, bsize, flag;
+    unsigned long long seq0, t_pop;
+};
+
+__device__ __forceinline__ double wave_sum(double v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_sumf(float v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Arrival-rank tdrop for one batch (wave 0; lane = record).  All lanes read
+// the counter in one load before the last record of each cell stores the
+// advanced value.
+__device__ void batch_tdrop(Lds& S, int B, unsigned char* td, const int* cell,
+                            const unsigned char* mask, unsigned char* pass, int window) {
+    if (threadIdx.x >= 64) return;
+    const int e = threadIdx.x;
+    if (e >= B) return;
+    const int c = cell[e];
+    const bool live = c >= 0 && (mask == nullptr || mask[e]);
+    if (!live) {
+        pass[e] = 0;
+        return;
+    }
+    int rank = 0;
+    bool last = true;
+    for (int j = 0; j < B; ++j) {
+        const bool lj = cell[j] == c && (mask == nullptr || mask[j]);
+        if (lj && j < e) ++rank;
+        if (lj && j > e) last = false;
+    }
+    const unsigned cnt = td[c];
+    const unsigned pre = (cnt + (unsigned)rank) & 255u;
+    pass[e] = (window <= 1 || pre % (unsigned)window == 0u) ? 1 : 0;
+    if (last) td[c] = (unsigned char)((cnt + (unsigned)rank + 1u) & 255u);
+}
+
+// One layer over the records of `set`, output for the records of `outm`
+// (nullptr = every record of the set).  Reads S.X, leaves the LayerNormed
+// output in S.X for output records.  Hl x Wl is the level's grid.
+template <int IN, int OUT>
+__device__ void batch_layer(Lds& S, int B, const unsigned char* set, const unsigned char* outm,
+                            const LayerWeightsS2S3& L, float* __restrict__ hidden,
+                            float* __restrict__ scratch, int Hl, int Wl) {
+    constexpr int NC = 3 * OUT;
+    const int tid = threadIdx.x;
+    // ---- pairs, per-delta lists (wave 0) ---------------------------------
+    if (tid < 64) {
+        const int e = tid;
+        const bool in = e < B && set[e];
+        unsigned bits = 0;
+        if (in) {
+            #pragma unroll
+            for (int d = 0; d < kPatch; ++d) {
+                const int ty = S.ey[e] + 1 - d / 3, tx = S.ex[e] + 1 - d % 3;
+                if (ty >= 0 && ty < Hl && tx >= 0 && tx < Wl) bits |= 1u << d;
+            }
+        }
+        const int cnt = __popc(bits);
+        int incl = cnt;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (e >= off) incl += v;
+        }
+        int k = incl - cnt;
+        if (e < LB) {
+            #pragma unroll
+            for (int d = 0; d < kPatch; ++d) {
+                int pi = -1;
+                if (bits & (1u << d)) {
+                    const int ty = S.ey[e] + 1 - d / 3, tx = S.ex[e] + 1 - d % 3;
+                    S.pe[k] = e;
+                    S.pc[k] = ty * Wl + tx;
+                    pi = k++;
+                }
+                S.pidx[e][d] = pi;
+            }
+        }
+        const unsigned long long lt = (1ull << e) - 1ull;
+        #pragma unroll
+        for (int d = 0; d < kPatch; ++d) {
+            const bool has = (bits >> d) & 1u;
+            const unsigned long long bal = __ballot(has);
+            const int at = __popcll(bal & lt);
+            if (has) S.dev[d][at] = e;
+            if (e < LB) S.dpos[e][d] = has ? at : -1;
+            if (e == 0) S.dcnt[d] = __popcll(bal);
+        }
+        const int total = __shfl(incl, 63, 64);
+        if (e == 0) {
+            S.npair = total;
+            S.nlead = 0;
+        }
+    }
+    __syncthreads();
+    // ---- successor links and one leader per cell -----------------------------
+    const int np = S.npair;
+    for (int p = tid; p < np; p += LT) {
+        const int c = S.pc[p];
+        int nx = -1;
+        for (int q = p + 1; q < np; ++q)
+            if (S.pc[q] == c) { nx = q; break; }
+        S.pnext[p] = nx;
+        bool lead = true;
+        for (int q = 0; q < p; ++q)
+            if (S.pc[q] == c) { lead = false; break; }
+        if (lead) S.lead[atomicAdd(&S.nlead, 1)] = p;
+    }
+    __syncthreads();
+    // ---- P: q, v, g rows, delta by delta --------------------------------------
+    {
+        constexpr int G = LT / NC;          // record groups sharing a column
+        const int c = tid % NC, g = tid / NC;
+        if (g < G) {
+            for (int d = 0; d < kPatch; ++d) {
+                const int n = S.dcnt[d];
+                if (n <= g * 8) continue;
+                const float* w = L.qvgIn + (size_t)d * IN * NC + c;
+                for (int r0 = g * 8; r0 < n; r0 += G * 8) {
+                    int ev[8];
+                    #pragma unroll
+                    for (int rr = 0; rr < 8; ++rr) ev[rr] = (r0 + rr < n) ? S.dev[d][r0 + rr] : 0;
+                    float acc[8];
+                    #pragma unroll
+                    for (int rr = 0; rr < 8; ++rr) acc[rr] = 0.f;
+                    // 24 weights of the column in flight per block of the input
+                    for (int i0 = 0; i0 < IN; i0 += kWB) {
+                        float wr[kWB];
+                        #pragma unroll
+                        for (int i = 0; i < kWB; ++i) wr[i] = w[(size_t)(i0 + i) * NC];
+                        #pragma unroll
+                        for (int i = 0; i < kWB; ++i) {
+                            #pragma unroll
+                            for (int rr = 0; rr < 8; ++rr) acc[rr] = fmaf(wr[i], S.X[ev[rr]][i0 + i], acc[rr]);
+                        }
+                    }
+                    #pragma unroll
+                    for (int rr = 0; rr < 8; ++rr)
+                        if (r0 + rr < n) scratch[(size_t)S.pidx[ev[rr]][d] * NC + c] = acc[rr];
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // ---- S: per-cell recurrence in record order -------------------------------
+    const int nl = S.nlead;
+    for (int t = tid; t < nl * OUT; t += LT) {
+        const int k = t / OUT, ch = t % OUT;
+        const int p0 = S.lead[k];
+        float* hp = hidden + (size_t)S.pc[p0] * OUT + ch;
+        float h = *hp;
+        for (int q = p0; q >= 0; q = S.pnext[q]) {
+            float* row = scratch + (size_t)q * NC;
+            h = fmaf(sigmoid_fast(row[2 * OUT + ch]), h, row[OUT + ch]);
+            if (outm == nullptr || outm[S.pe[q]]) row[ch] *= h;
+        }
+        *hp = h;
+    }
+    __syncthreads();
+    // ---- O: goW contraction + residual ------------------------------------------
+    // Per delta: the q*h rows of the records with a pair there are staged in
+    // LDS (S.R), the delta's goW column sits in registers, and each thread
+    // accumulates its channel for its records.
+    {
+        constexpr int GO = LT / OUT;
+        constexpr int KE = (LB + GO - 1) / GO;
+        const int o = tid % OUT, g = tid / OUT;
+        int ev[KE];
+        bool on[KE];
+        float acc[KE];
+        #pragma unroll
+        for (int k = 0; k < KE; ++k) {
+            const int e = g + k * GO;
+            on[k] = g < GO && e < B && set[e] && (outm == nullptr || outm[e]);
+            ev[k] = on[k] ? e : 0;
+            acc[k] = 0.f;
+        }
+        for (int d = 0; d < kPatch; ++d) {
+            const int n = S.dcnt[d];
+            if (n == 0) continue;
+            for (int t = tid; t < n * OUT; t += LT) {
+                const int k = t / OUT, i = t % OUT;
+                S.R[k][i] = scratch[(size_t)S.pidx[S.dev[d][k]][d] * NC + i];
+            }
+            __syncthreads();
+            if (g < GO) {
+                const float* w = L.goW + (size_t)d * OUT * OUT + o;
+                int pos[KE];
+                #pragma unroll
+                for (int k = 0; k < KE; ++k) pos[k] = on[k] ? S.dpos[ev[k]][d] : -1;
+                for (int i0 = 0; i0 < OUT; i0 += kWB) {
+                    float wr[kWB];
+                    #pragma unroll
+                    for (int i = 0; i < kWB; ++i) wr[i] = w[(size_t)(i0 + i) * OUT];
+                    #pragma unroll
+                    for (int k = 0; k < KE; ++k) {
+                        if (pos[k] < 0) continue;
+                        float a = acc[k];
+                        #pragma unroll
+                        for (int i = 0; i < kWB; ++i) a = fmaf(wr[i], S.R[pos[k]][i0 + i], a);
+                        acc[k] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        if (g < GO) {
+            if (L.input_proj) {
+                for (int i0 = 0; i0 < IN; i0 += kWB) {
+                    float wr[kWB];
+                    #pragma unroll
+                    for (int i = 0; i < kWB; ++i) wr[i] = L.input_proj[(size_t)(i0 + i) * OUT + o];
+                    #pragma unroll
+                    for (int i = 0; i < kWB; ++i) {
+                        #pragma unroll
+                        for (int k = 0; k < KE; ++k) acc[k] = fmaf(wr[i], S.X[ev[k]][i0 + i], acc[k]);
+                    }
+                }
+            } else {
+                #pragma unroll
+                for (int k = 0; k < KE; ++k) acc[k] += S.X[ev[k]][o];
+            }
+            #pragma unroll
+            for (int k = 0; k < KE; ++k)
+                if (on[k]) S.Y[ev[k]][o] = acc[k];
+        }
+    }
+    __syncthreads();
+    // ---- fp64 LayerNorm, one wave per record ----------------------------------------
+    {
+        const int wv = tid >> 6, lane = tid & 63;
+        for (int e = wv; e < B; e += NW) {
+            if (!(set[e] && (outm == nullptr || outm[e]))) continue;
+            const float a = lane < OUT ? S.Y[e][lane] : 0.f;
+            const float b = lane + 64 < OUT ? S.Y[e][lane + 64] : 0.f;
+            const double mean = wave_sum((double)a + (double)b) / (double)OUT;
+            const double da = lane < OUT ? (double)a - mean : 0.0;
+            const double db = lane + 64 < OUT ? (double)b - mean : 0.0;
+            const double var = wave_sum(da * da + db * db) / (double)OUT;
+            const double inv = 1.0 / sqrt(var + 1e-5);
+            if (lane < OUT)
+                S.X[e][lane] = (float)(da * inv * (double)L.ln_gamma[lane] + (double)L.ln_beta[lane]);
+            if (lane + 64 < OUT)
+                S.X[e][lane + 64] = (float)(db * inv * (double)L.ln_gamma[lane + 64] + (double)L.ln_beta[lane + 64]);
+        }
+    }
+    __syncthreads();
+}
+
+// Records [0, B) are in S (X rows, coordinates, ownership).  Runs both
+// stages, the tdrop gates and the head; leaves L7 outputs in S.X and head
+// rows in S.H7.
+__device__ void process_batch(Lds& S, int B, const LiveDesc& d, const LiveWeights& W,
+                              const Geometry& G) {
+    const int tid = threadIdx.x;
+    batch_tdrop(S, B, d.td2, S.c2, nullptr, S.p2, G.window);
+    __syncthreads();
+    batch_layer<SSLA_C1, SSLA_C2>(S, B, S.vld, nullptr, W.L[0], d.hidden[0], d.scratch, G.H2, G.W2);
+    batch_layer<SSLA_C2, SSLA_C2>(S, B, S.vld, S.p2, W.L[1], d.hidden[1], d.scratch, G.H2, G.W2);
+    if (tid < B) {                      // pool to s3
+        S.ex[tid] >>= 1;
+        S.ey[tid] >>= 1;
+        S.c3[tid] = S.vld[tid] ? S.ey[tid] * G.W3 + S.ex[tid] : -1;
+    }
+    __syncthreads();
+    batch_tdrop(S, B, d.td3, S.c3, S.p2, S.p3, G.window);
+    __syncthreads();
+    batch_layer<SSLA_C2, SSLA_C3>(S, B, S.p2, nullptr, W.L[2], d.hidden[2], d.scratch, G.H3, G.W3);
+    batch_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], d.hidden[3], d.scratch, G.H3, G.W3);
+    if (!W.have_head) return;
+    // ---- head hidden layers: y = SiLU(W x + b) for both branches ----------------
+    {
+        constexpr int C = SSLA_C3;
+        constexpr int GO = LT / C;
+        const int o = tid % C, g = tid / C;
+        if (g < GO) {
+            for (int e = g; e < B; e += GO) {
+                if (!(S.own[e] && S.p3[e])) continue;
+                float a = W.head.cls_conv_b[o], b = W.head.reg_conv_b[o];
+                for (int i0 = 0; i0 < C; i0 += kWB) {
+                    float wa[kWB], wb[kWB];
+                    #pragma unroll
+                    for (int i = 0; i < kWB; ++i) {
+                        wa[i] = W.head.cls_conv_W[(size_t)(i0 + i) * C + o];
+                        wb[i] = W.head.reg_conv_W[(size_t)(i0 + i) * C + o];
+                    }
+                    #pragma unroll
+                    for (int i = 0; i < kWB; ++i) {
+                        a = fmaf(wa[i], S.X[e][i0 + i], a);
+                        b = fmaf(wb[i], S.X[e][i0 + i], b);
+                    }
+                }
+                S.Y[e][o] = a * sigmoid_fast(a);
+                S.R[e][o] = b * sigmoid_fast(b);
+            }
+        }
+    }
+    __syncthreads();
+    // ---- head outputs [reg0..3, obj, cls0, cls1], one wave per record ------------
+    {
+        const int wv = tid >> 6, lane = tid & 63;
+        for (int e = wv; e < B; e += NW) {
+            if (!(S.own[e] && S.p3[e])) continue;
+            float part[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int i = lane; i < SSLA_C3; i += 64) {
+                const float yr = S.R[e][i], yc = S.Y[e][i];
+                #pragma unroll
+                for (int k = 0; k < 4; ++k) part[k] = fmaf(W.head.reg_pred_W[(size_t)i * 4 + k], yr, part[k]);
+                part[4] = fmaf(W.head.obj_pred_W[i], yr, part[4]);
+                part[5] = fmaf(W.head.cls_pred_W[(size_t)i * 2 + 0], yc, part[5]);
+                part[6] = fmaf(W.head.cls_pred_W[(size_t)i * 2 + 1], yc, part[6]);
+            }
+            #pragma unroll
+            for (int k = 0; k < 7; ++k) part[k] = wave_sumf(part[k]);
+            if (lane == 0) {
+                #pragma unroll
+                for (int k = 0; k < 4; ++k) S.H7[e][k] = part[k] + W.head.reg_pred_b[k];
+                S.H7[e][4] = part[4] + W.head.obj_pred_b[0];
+                S.H7[e][5] = part[5] + W.head.cls_pred_b[0];
+                S.H7[e][6] = part[6] + W.head.cls_pred_b[1];
+            }
+        }
+    }
+    __syncthreads();
+    // ---- prediction grid: last owned pass-3 record of each s3 cell writes --------
+    if (tid < B && S.own[tid] && S.p3[tid]) {
+        const int e = tid, c = S.c3[e];
+        int count = 0;
+        bool last = true;
+        for (int j = 0; j < B; ++j) {
+            const bool same = S.own[j] && S.p3[j] && S.c3[j] == c;
+            count += same ? 1 : 0;
+            if (same && j > e) last = false;
+        }
+        const HybridStrip& s = d.strip;
+        const int hx = S.ex[e] - s.s3_owned_lo, hy = S.ey[e] - s.s3_owned_y_lo;
+        const int w = s.s3_owned_hi - s.s3_owned_lo, h = s.s3_owned_y_hi - s.s3_owned_y_lo;
+        if (last && hx >= 0 && hx < w && hy >= 0 && hy < h) {
+            const int idx = hy * w + hx;
+            if (d.preds) {
+                #pragma unroll
+                for (int k = 0; k < 7; ++k) d.preds[(size_t)idx * 7 + k] = S.H7[e][k];
+            }
+            if (d.version) d.version[idx] += (unsigned)count;
+        }
+    }
+    __syncthreads();
+}
+
+// Loads B records starting at ring slot `first` (slots wrap with `mask`).
+__device__ void load_batch(Lds& S, int B, const HybridInputRec* ring, unsigned long long first,
+                           unsigned long long mask, const HybridStrip& s, const Geometry& G) {
+    const int tid = threadIdx.x;
+    for (int t = tid; t < B * SSLA_C1; t += LT) {
+        const int e = t / SSLA_C1, i = t % SSLA_C1;
+        S.X[e][i] = ring[(first + e) & mask].feat1[i];
+    }
+    if (tid < B) {
+        const HybridInputRec& r = ring[(first + tid) & mask];
+        const int x = r.x, y = r.y;
+        const bool v = x < G.W2 && y < G.H2;
+        S.vld[tid] = v ? 1 : 0;
+        S.ex[tid] = x;
+        S.ey[tid] = y;
+        S.c2[tid] = v ? y * G.W2 + x : -1;
+        S.own[tid] = (v && x >= s.owned_lo && x < s.owned_hi && y >= s.owned_y_lo && y < s.owned_y_hi) ? 1 : 0;
+        S.p2[tid] = 0;
+        S.p3[tid] = 0;
+        S.tpush[tid] = r.t_push_ns;
+        S.temit[tid] = r.t_emit_ns;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// batch-mode drain of pre-filled rings (one workgroup per block)
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(LT)
+k_batch_drain(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, int batch) {
+    __shared__ Lds S;
+    const LiveDesc& d = ld[blockIdx.x];
+    const int tid = threadIdx.x;
+    int bi = 0;
+    for (int base = 0; base < d.n; base += batch, ++bi) {
+        const int B = min(batch, d.n - base);
+        if (tid == 0) S.t_pop = (unsigned long long)wall_clock64();
+        load_batch(S, B, d.ring, (unsigned long long)base, ~0ull, d.strip, G);
+        __syncthreads();
+        process_batch(S, B, d, W, G);
+        // output slots and head rows
+        for (int t = tid; t < B * SSLA_C3; t += LT) {
+            const int e = t / SSLA_C3, i = t % SSLA_C3;
+            if (d.out) d.out[base + e].s3_feat[i] = (S.vld[e] && S.p3[e]) ? S.X[e][i] : 0.f;
+        }
+        if (tid < B) {
+            const int e = tid;
+            const bool v = S.vld[e], own = S.own[e];
+            if (d.out) {
+                d.out[base + e].pass2 = !v ? -2 : (own ? (int)S.p2[e] : -1);
+                d.out[base + e].pass3 = !v ? -2 : (own ? (int)S.p3[e] : -1);
+            }
+            if (d.head_out) {
+                const bool hv = W.have_head && own && S.p3[e];
+                #pragma unroll
+                for (int k = 0; k < 7; ++k) d.head_out[(size_t)(base + e) * 7 + k] = hv ? S.H7[e][k] : 0.f;
+            }
+        }
+        if (tid == 0 && d.batch_clk) {
+            d.batch_clk[(size_t)bi * 2 + 0] = S.t_pop;
+            d.batch_clk[(size_t)bi * 2 + 1] = (unsigned long long)wall_clock64();
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// persistent live drain
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(LT)
+k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* stop_flag,
+       unsigned int spin_ns, unsigned long long idle_ticks, int max_batch,
+       int* __restrict__ status) {
+    __shared__ Lds S;
+    const LiveDesc& d = ld[blockIdx.x];
+    const int tid = threadIdx.x;
+    const unsigned long long mask = d.ring_mask;
+    unsigned long long t = __hip_atomic_load(d.tail, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+    unsigned long long last_work = (unsigned long long)wall_clock64();
+    if (tid == 0 && d.kstart)
+        __hip_atomic_store(d.kstart, last_work, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    const int sleep_iters = (int)(spin_ns / 40u) + 1;
+    while (true) {
+        // every wave has read the previous round's flag / batch size
+        __syncthreads();
+        // ---- poll: wave 0 probes 64 consecutive tags ------------------------------
+        if (tid < 64) {
+            unsigned long long* tag = const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done);
+            const unsigned long long s = __hip_atomic_load(tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            const bool ready = s == t + (unsigned long long)tid + 1ull;
+            const unsigned long long bal = __ballot(ready);
+            const int lead = (int)__ffsll((long long)~bal) - 1;   // first not-ready lane, -1 if all
+            int n = lead < 0 ? 64 : lead;
+            if (n > max_batch) n = max_batch;
+            // a tag beyond this round's sequence means the producer lapped the ring
+            const bool lapped = (tid == 0) && s > t + 1ull;
+            if (tid == 0) {
+                const int stop = __hip_atomic_load(stop_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                const unsigned long long now = (unsigned long long)wall_clock64();
+                int f = 0;
+                if (stop) f = 1;
+                else if (lapped) f = 2;
+                else if (n == 0 && now - last_work > idle_ticks) f = 3;
+                S.flag = f;
+                S.bsize = n;
+            }
+        }
+        __syncthreads();
+        const int flag = S.flag, B = S.bsize;
+        if (flag) {
+            if (tid == 0) {
+                if (flag > 1) atomicMax(status, flag);
+                if (d.kend)
+                    __hip_atomic_store(d.kend, (unsigned long long)wall_clock64(), __ATOMIC_RELEASE,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            return;
+        }
+        if (B == 0) {
+            for (int i = 0; i < sleep_iters; ++i) __builtin_amdgcn_s_sleep(1);
+            continue;
+        }
+        // pairs with the producer's release store of the tags seen above:
+        // the records' fields are visible to the loads that follow
+        __atomic_thread_fence(__ATOMIC_ACQUIRE);
+        if (tid == 0) S.t_pop = (unsigned long long)wall_clock64();
+        load_batch(S, B, d.ring, t, mask, d.strip, G);
+        __syncthreads();
+        process_batch(S, B, d, W, G);
+        const unsigned long long t_done = (unsigned long long)wall_clock64();
+        if (tid < B && d.timing) {
+            const unsigned long long seq = t + (unsigned long long)tid;
+            GpuTimingSlot& ts = d.timing[seq & d.timing_mask];
+            ts.t_pop_clk = S.t_pop;
+            ts.t_done_clk = t_done;
+            ts.seq = (unsigned int)seq;
+            ts.owner = (S.own[tid] && S.p2[tid] && S.p3[tid]) ? 1u : 0u;
+            ts.t_push_ns = S.tpush[tid];
+            ts.t_emit_ns = S.temit[tid];
+        }
+        t += (unsigned long long)B;
+        last_work = t_done;
+        // predictions and timing of this batch become visible before the tail
+        __threadfence_system();
+        __syncthreads();
+        if (tid == 0) {
+            __hip_atomic_store(d.tail, t, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (d.events_done)
+                __hip_atomic_store(d.events_done, t, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+}
+
+#define LHIP(call)                                                            \
+    do {                                                                      \
+        hipError_t e_ = (call);                                               \
+        if (e_ != hipSuccess) {                                               \
+            set_error(std::string(#call) + ": " + hipGetErrorString(e_));    \
+            return SSLA_ERR_HIP;                                              \
+        }                                                                     \
+    } while (0)
+
+size_t scratch_floats() { return (size_t)(LP + 1) * NCMAX; }
+
+// batch-mode workspace: per-block scratch rows + the device block table
+std::mutex g_bmu;
+float* g_bscratch = nullptr;
+LiveDesc* g_bdesc = nullptr;
+LiveDesc* g_bdesc_host = nullptr;
+hipEvent_t g_bcopied = nullptr;
+
+}  // namespace
+
+static int live_weights(const HybridS2S3Config* cfg, LiveWeights* W, Geometry* G) {
+    const int nb = cfg->n_blocks;
+    if (nb < 1 || nb > SSLA_MAX_BLOCKS) {
+        set_error("n_blocks must be in [1, 16]");
+        return SSLA_ERR_ARG;
+    }
+    if (cfg->H2 <= 0 || cfg->W2 <= 0 || (cfg->H2 & 1) || (cfg->W2 & 1) ||
+        cfg->H3 != cfg->H2 / 2 || cfg->W3 != cfg->W2 / 2) {
+        set_error("grid must have even H2, W2 and H3 = H2/2, W3 = W2/2");
+        return SSLA_ERR_ARG;
+    }
+    for (int b = 0; b < nb; ++b)
+        for (int li = 0; li < 4; ++li) {
+            const LayerWeightsS2S3& L = cfg->layers[b][li];
+            const LayerWeightsS2S3& L0 = cfg->layers[0][li];
+            if (!L.qvgIn || !L.goW || !L.ln_gamma || !L.ln_beta || L.qvgIn != L0.qvgIn ||
+                L.goW != L0.goW || L.input_proj != L0.input_proj || L.ln_gamma != L0.ln_gamma ||
+                L.ln_beta != L0.ln_beta) {
+                set_error("all blocks must share one bound set of layer weights");
+                return SSLA_ERR_ARG;
+            }
+            if (!cfg->hidden[b][li] || !cfg->tdrop_s2[b] || !cfg->tdrop_s3[b]) {
+                set_error("block state not allocated");
+                return SSLA_ERR_ARG;
+            }
+        }
+    if (!cfg->layers[0][0].input_proj || !cfg->layers[0][2].input_proj ||
+        cfg->layers[0][1].input_proj || cfg->layers[0][3].input_proj) {
+        set_error("L4/L6 need input_proj and L5/L7 must not have one");
+        return SSLA_ERR_ARG;
+    }
+    for (int li = 0; li < 4; ++li) W->L[li] = cfg->layers[0][li];
+    W->head = HeadPtrs{cfg->head_cls_conv_W, cfg->head_cls_conv_b, cfg->head_cls_pred_W,
+                       cfg->head_cls_pred_b, cfg->head_reg_conv_W, cfg->head_reg_conv_b,
+                       cfg->head_reg_pred_W, cfg->head_reg_pred_b, cfg->head_obj_pred_W,
+                       cfg->head_obj_pred_b};
+    W->have_head = cfg->head_cls_conv_W != nullptr;
+    G->H2 = cfg->H2; G->W2 = cfg->W2; G->H3 = cfg->H3; G->W3 = cfg->W3;
+    G->C2 = G->H2 * G->W2; G->C3 = G->H3 * G->W3; G->nb = nb; G->window = cfg->tdrop_window;
+    return SSLA_OK;
+}
+
+static void live_desc_state(const HybridS2S3Config* cfg, int b, LiveDesc* d) {
+    for (int li = 0; li < 4; ++li) d->hidden[li] = cfg->hidden[b][li];
+    d->td2 = cfg->tdrop_s2[b];
+    d->td3 = cfg->tdrop_s3[b];
+    d->strip = cfg->strip[b];
+    const bool head = cfg->head_cls_conv_W != nullptr;
+    d->preds = head ? cfg->preds[b] : nullptr;
+    d->version = head ? cfg->version[b] : nullptr;
+}
+
+int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings, const int* ns,
+                HybridS2S3OutputSlot* const* outs, float* const* head_outs,
+                unsigned long long* const* batch_clks, int batch, hipStream_t st, bool sync) {
+    LiveWeights W;
+    Geometry G;
+    int rc = live_weights(cfg, &W, &G);
+    if (rc) return rc;
+    if (batch < 1 || batch > LB) {
+        set_error("batch must be in [1, 32]");
+        return SSLA_ERR_ARG;
+    }
+    const int nb = cfg->n_blocks;
+    for (int b = 0; b < nb; ++b)
+        if (ns[b] < 0 || (ns[b] > 0 && !rings[b])) {
+            set_error("bad ring / count for block " + std::to_string(b));
+            return SSLA_ERR_ARG;
+        }
+    std::lock_guard<std::mutex> lk(g_bmu);
+    if (!g_bscratch) {
+        const size_t bytes = sizeof(float) * scratch_floats() * SSLA_MAX_BLOCKS;
+        LHIP(hipMalloc(&g_bscratch, bytes));
+        LHIP(hipMemset(g_bscratch, 0, bytes));
+        LHIP(hipMalloc(&g_bdesc, sizeof(LiveDesc) * SSLA_MAX_BLOCKS));
+        LHIP(hipHostMalloc((void**)&g_bdesc_host, sizeof(LiveDesc) * SSLA_MAX_BLOCKS, hipHostMallocDefault));
+        LHIP(hipEventCreateWithFlags(&g_bcopied, hipEventDisableTiming));
+        LHIP(hipDeviceSynchronize());
+    }
+    LHIP(hipEventSynchronize(g_bcopied));
+    std::memset(g_bdesc_host, 0, sizeof(LiveDesc) * SSLA_MAX_BLOCKS);
+    for (int b = 0; b < nb; ++b) {
+        LiveDesc& d = g_bdesc_host[b];
+        live_desc_state(cfg, b, &d);
+        d.ring = rings[b];
+        d.ring_mask = ~0ull;
+        d.n = ns[b];
+        d.scratch = g_bscratch + scratch_floats() * b;
+        d.out = outs ? outs[b] : nullptr;
+        d.head_out = head_outs ? head_outs[b] : nullptr;
+        d.batch_clk = batch_clks ? batch_clks[b] : nullptr;
+    }
+    LHIP(hipMemcpyAsync(g_bdesc, g_bdesc_host, sizeof(LiveDesc) * nb, hipMemcpyHostToDevice, st));
+    LHIP(hipEventRecord(g_bcopied, st));
+    hipLaunchKernelGGL(k_batch_drain, dim3(nb), dim3(LT), 0, st, g_bdesc, W, G, batch);
+    LHIP(hipGetLastError());
+    if (sync) LHIP(hipStreamSynchronize(st));
+    return SSLA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// persistent session
+// ---------------------------------------------------------------------------
+struct LiveSession {
+    hipStream_t stream = nullptr;
+    LiveDesc* desc = nullptr;
+    float* scratch = nullptr;
+    int* status = nullptr;
+    int nb = 0;
+};
+
+int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
+               unsigned long long ring_mask, unsigned long long* const* tails, int* stop_flag,
+               unsigned long long* const* events_done, unsigned int spin_ns, int max_batch,
+               unsigned int idle_timeout_ms, LiveSession** out) {
+    *out = nullptr;
+    LiveWeights W;
+    Geometry G;
+    int rc = live_weights(cfg, &W, &G);
+    if (rc) return rc;
+    if ((ring_mask & (ring_mask + 1)) != 0) {
+        set_error("ring capacity must be a power of two (ring_mask = capacity - 1)");
+        return SSLA_ERR_ARG;
+    }
+    if (max_batch < 1 || max_batch > LB) {
+        set_error("max_batch must be in [1, 32]");
+        return SSLA_ERR_ARG;
+    }
+    if (!stop_flag) {
+        set_error("stop_flag is required");
+        return SSLA_ERR_ARG;
+    }
+    const int nb = cfg->n_blocks;
+    for (int b = 0; b < nb; ++b) {
+        if (!rings[b] || !tails[b]) {
+            set_error("every block needs a ring and a tail");
+            return SSLA_ERR_ARG;
+        }
+        if (cfg->timing[b] && (cfg->timing_mask & (cfg->timing_mask + 1)) != 0) {
+            set_error("timing_mask must be capacity - 1 of a power of two");
+            return SSLA_ERR_ARG;
+        }
+    }
+    int khz = 0;
+    LHIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, 0));
+    if (khz <= 0) khz = 100000;
+    LiveSession* s = new LiveSession();
+    s->nb = nb;
+    auto fail = [&](const char* what) {
+        set_error(std::string(what) + " failed while starting the live drain");
+        if (s->stream) (void)hipStreamDestroy(s->stream);
+        if (s->desc) (void)hipFree(s->desc);
+        if (s->scratch) (void)hipFree(s->scratch);
+        if (s->status) (void)hipFree(s->status);
+        delete s;
+        return SSLA_ERR_HIP;
+    };
+    if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess) return fail("stream");
+    const size_t sbytes = sizeof(float) * scratch_floats() * nb;
+    if (hipMalloc(&s->scratch, sbytes) != hipSuccess) return fail("scratch");
+    if (hipMalloc(&s->desc, sizeof(LiveDesc) * nb) != hipSuccess) return fail("desc");
+    if (hipMalloc(&s->status, sizeof(int)) != hipSuccess) return fail("status");
+    std::vector<LiveDesc> hd(nb);
+    std::memset(hd.data(), 0, sizeof(LiveDesc) * nb);
+    for (int b = 0; b < nb; ++b) {
+        LiveDesc& d = hd[b];
+        live_desc_state(cfg, b, &d);
+        d.ring = rings[b];
+        d.ring_mask = ring_mask;
+        d.tail = tails[b];
+        d.events_done = events_done ? events_done[b] : nullptr;
+        d.scratch = s->scratch + scratch_floats() * b;
+        d.timing = cfg->timing[b];
+        d.timing_mask = cfg->timing_mask;
+        d.kstart = cfg->kernel_start_clk[b];
+        d.kend = cfg->kernel_end_clk[b];
+    }
+    if (hipMemsetAsync(s->scratch, 0, sbytes, s->stream) != hipSuccess) return fail("memset");
+    if (hipMemsetAsync(s->status, 0, sizeof(int), s->stream) != hipSuccess) return fail("memset");
+    if (hipMemcpyAsync(s->desc, hd.data(), sizeof(LiveDesc) * nb, hipMemcpyHostToDevice, s->stream) != hipSuccess)
+        return fail("copy");
+    if (hipStreamSynchronize(s->stream) != hipSuccess) return fail("sync");
+    const unsigned long long idle = (unsigned long long)idle_timeout_ms * (unsigned long long)khz;
+    hipLaunchKernelGGL(k_live, dim3(nb), dim3(LT), 0, s->stream, s->desc, W, G, stop_flag, spin_ns,
+                       idle, max_batch, s->status);
+    if (hipGetLastError() != hipSuccess) return fail("launch");
+    *out = s;
+    return SSLA_OK;
+}
+
+int live_wait(LiveSession* s, int timeout_ms, int* status_out) {
+    if (!s) {
+        set_error("null session");
+        return SSLA_ERR_ARG;
+    }
+    const auto t0 = std::chrono::steady_clock::now();
+    while (true) {
+        const hipError_t q = hipStreamQuery(s->stream);
+        if (q == hipSuccess) break;
+        if (q != hipErrorNotReady) {
+            set_error(std::string("live drain failed: ") + hipGetErrorString(q));
+            return SSLA_ERR_HIP;
+        }
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        if (timeout_ms >= 0 && ms > timeout_ms) {
+            set_error("live drain still running (set *stop_flag first; the kernel also stops on its idle timeout)");
+            return SSLA_ERR_STATE;
+        }
+        std::this_thread::sleep_for(std::chrono::microseconds(200));
+    }
+    int st = 0;
+    LHIP(hipMemcpy(&st, s->status, sizeof(int), hipMemcpyDeviceToHost));
+    if (status_out) *status_out = st;
+    (void)hipStreamDestroy(s->stream);
+    (void)hipFree(s->desc);
+    (void)hipFree(s->scratch);
+    (void)hipFree(s->status);
+    delete s;
+    return SSLA_OK;
+}
+
+}  // namespace ssla

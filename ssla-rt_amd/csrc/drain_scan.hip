@@ -38,13 +38,13 @@
 #include <string>
 #include <vector>
 
+#include "drain_common.h"
 #include "drain_scan.h"
 
 namespace ssla {
 
 namespace {
 
-constexpr int kPatch = 9;
 constexpr int kTE = 32;              // records per projection / output tile
 
 struct BlockDesc {
@@ -60,17 +60,6 @@ struct BlockDesc {
     int                   n;
     int                   offset;
 };
-
-struct Geometry {
-    int H2, W2, H3, W3;
-    int C2, C3;          // cells per block at s2 / s3
-    int nb;              // blocks
-    int window;
-};
-
-__device__ __forceinline__ float sigmoid_fast(float x) {
-    return __fdividef(1.0f, 1.0f + __expf(-x));
-}
 
 __device__ __forceinline__ int find_block(const BlockDesc* bd, int nb, int g) {
     int b = 0;
@@ -508,12 +497,6 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 // (...celled.cuh:841-902).  One workgroup per record, one thread per hidden
 // channel.
 // ---------------------------------------------------------------------------
-struct HeadPtrs {
-    const float *cls_conv_W, *cls_conv_b, *cls_pred_W, *cls_pred_b;
-    const float *reg_conv_W, *reg_conv_b, *reg_pred_W, *reg_pred_b;
-    const float *obj_pred_W, *obj_pred_b;
-};
-
 __global__ void __launch_bounds__(128)
 k_head(const int* __restrict__ n_dev, const int* __restrict__ list,
        const unsigned char* __restrict__ owner, const float* __restrict__ X,

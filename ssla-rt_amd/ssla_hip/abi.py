@@ -101,10 +101,14 @@ class SslaHipDrainOpts(ctypes.Structure):
     _fields_ = [
         ("stream", ctypes.c_void_p),
         ("sync", ctypes.c_int),
-        ("reserved", ctypes.c_int),
+        ("batch", ctypes.c_int),
         ("head_outs", ctypes.POINTER(ctypes.c_void_p)),
         ("phase_ms", ctypes.POINTER(ctypes.c_float)),
     ]
+
+
+class SslaHipLiveOpts(ctypes.Structure):
+    _fields_ = [("max_batch", ctypes.c_int), ("idle_timeout_ms", ctypes.c_uint)]
 
 
 DRAIN_PHASES = ("order",

@@ -236,7 +236,8 @@ class Drain:
             self._outs.append(DeviceBuffer(n * abi.OUTPUT_DTYPE.itemsize))
             self._heads.append(DeviceBuffer(n * 7 * 4) if want_head else None)
 
-    def run(self, stream: int = 0, sync: bool = True, phase_ms: Optional[np.ndarray] = None) -> None:
+    def run(self, stream: int = 0, sync: bool = True, phase_ms: Optional[np.ndarray] = None,
+            batch: int = 0) -> None:
         """One drain call over the loaded rings.  phase_ms (float32 array of
         len(abi.DRAIN_PHASES)) accumulates per-phase GPU time (needs sync)."""
         nb = self.cfg.n_blocks
@@ -248,6 +249,7 @@ class Drain:
         opts = abi.SslaHipDrainOpts()
         opts.stream = stream or None
         opts.sync = 1 if sync else 0
+        opts.batch = batch
         heads = None
         if self._heads and self._heads[0] is not None:
             heads = (ctypes.c_void_p * nb)(*[b.ptr for b in self._heads])
@@ -267,13 +269,55 @@ class Drain:
             heads.append(h.download(np.float32, n * 7).reshape(n, 7) if h is not None else None)
         return outs, heads
 
-    def drain(self, records: Sequence[np.ndarray], want_head: bool = False):
+    def drain(self, records: Sequence[np.ndarray], want_head: bool = False, batch: int = 0):
+        """Drain pre-filled rings; batch 0 = whole-ring drain, 1..32 = in-kernel
+        batches of that many records."""
         self.load_rings(records, want_head=want_head)
-        self.run()
+        self.run(batch=batch)
         return self.results()
+
+    def drain_with_clocks(self, records: Sequence[np.ndarray]):
+        """ssla_hip_drain_n with batch_clks: in-kernel batches of 8 records and
+        a (t_pop, t_done) wall-clock pair per batch."""
+        self.load_rings(records)
+        nb = self.cfg.n_blocks
+        clk = [DeviceBuffer(max(1, (n + 7) // 8) * 16) for n in self._ns]
+        try:
+            rings = (ctypes.c_void_p * nb)(*[b.ptr for b in self._rings])
+            ns = (ctypes.c_int * nb)(*self._ns)
+            outs = (ctypes.c_void_p * nb)(*[b.ptr for b in self._outs])
+            clks = (ctypes.c_void_p * nb)(*[b.ptr for b in clk])
+            lib.check(lib.load().ssla_hip_drain_n(ctypes.byref(self.cfg), rings, ns, outs, clks),
+                      "drain_n")
+            outs_h, _ = self.results()
+            clocks = [c.download(np.uint64, 2 * ((n + 7) // 8)).reshape(-1, 2)
+                      for c, n in zip(clk, self._ns)]
+        finally:
+            for c in clk:
+                c.free()
+        return outs_h, clocks
+
+    # -- live (persistent) drain ---------------------------------------------------
+    def alloc_timing(self, capacity: int = 1 << 16) -> None:
+        L = lib.load()
+        for b in range(self.cfg.n_blocks):
+            lib.check(L.ssla_hip_timing_alloc(ctypes.byref(self.cfg), b, capacity), "timing_alloc")
+        self._timing = True
+
+    def timing(self, blk: int) -> np.ndarray:
+        n = self.cfg.timing_mask + 1
+        return download_ptr(self.cfg.timing[blk], abi.TIMING_DTYPE, n)
+
+    def kernel_clocks(self, blk: int):
+        v = np.ctypeslib.as_array((ctypes.c_ulonglong * 2).from_address(self.cfg.kernel_start_clk[blk]))
+        return int(v[0]), int(v[1])
 
     def close(self) -> None:
         L = lib.load()
+        if getattr(self, "_timing", False):
+            for b in range(self.cfg.n_blocks):
+                L.ssla_hip_timing_free(ctypes.byref(self.cfg), b)
+            self._timing = False
         for bufs in (self._rings, self._outs, self._heads):
             for b in bufs:
                 if b is not None:
@@ -295,3 +339,77 @@ class Drain:
 
     def __exit__(self, *exc):
         self.close()
+
+
+class HostRings:
+    """Per-block rings in fine-grained host memory with the producer-side
+    head counters and the consumer-side tail / events_done words, plus the
+    stop flag (orin/hybrid_runner_multi.py:446-462)."""
+
+    def __init__(self, n_blocks: int, capacity: int = 1 << 16):
+        if capacity & (capacity - 1):
+            raise ValueError("ring capacity must be a power of two")
+        self.n_blocks, self.capacity = n_blocks, capacity
+        self.bufs = [DeviceBuffer(capacity * abi.INPUT_DTYPE.itemsize, host=True) for _ in range(n_blocks)]
+        self.words = DeviceBuffer(8 * (3 * n_blocks + 1), host=True)
+        for b in self.bufs:
+            ctypes.memset(b.ptr, 0, b.nbytes)
+        ctypes.memset(self.words.ptr, 0, self.words.nbytes)
+        self.rings = [np.ctypeslib.as_array((ctypes.c_ubyte * b.nbytes).from_address(b.ptr))
+                      .view(abi.INPUT_DTYPE) for b in self.bufs]
+        w = np.ctypeslib.as_array((ctypes.c_ulonglong * (3 * n_blocks + 1)).from_address(self.words.ptr))
+        self.head, self.tail, self.done = w[:n_blocks], w[n_blocks:2 * n_blocks], w[2 * n_blocks:3 * n_blocks]
+        self.stop_ptr = self.words.ptr + 8 * 3 * n_blocks
+        self._stop = np.ctypeslib.as_array((ctypes.c_int * 1).from_address(self.stop_ptr))
+
+    def ptrs(self):
+        nb = self.n_blocks
+        base = self.words.ptr
+        return ((ctypes.c_void_p * nb)(*[b.ptr for b in self.bufs]),
+                (ctypes.c_void_p * nb)(*[base + 8 * (nb + b) for b in range(nb)]),
+                (ctypes.c_void_p * nb)(*[base + 8 * (2 * nb + b) for b in range(nb)]))
+
+    def push(self, blk: int, recs: np.ndarray) -> None:
+        """Single-producer publish: write each record, then its seq_done tag."""
+        ring = self.rings[blk]
+        h = int(self.head[blk])
+        for k in range(recs.size):
+            slot = (h + k) & (self.capacity - 1)
+            r = recs[k].copy()
+            r["seq_done"] = 0
+            ring[slot] = r
+            ring["seq_done"][slot] = h + k + 1
+        self.head[blk] = h + recs.size
+
+    def stop(self) -> None:
+        self._stop[0] = 1
+
+    def free(self) -> None:
+        for b in self.bufs:
+            b.free()
+        self.words.free()
+
+
+class LiveDrain:
+    """A running persistent drain over HostRings (ssla_hip_persistent_start)."""
+
+    def __init__(self, drain: Drain, rings: HostRings, spin_ns: int = 200, max_batch: int = 32,
+                 idle_timeout_ms: int = 30000):
+        self.rings = rings
+        self.h = ctypes.c_void_p()
+        bufs, tails, dones = rings.ptrs()
+        opts = abi.SslaHipLiveOpts(max_batch, idle_timeout_ms)
+        lib.check(lib.load().ssla_hip_persistent_start(
+            ctypes.byref(drain.cfg), bufs, rings.capacity - 1, tails, rings.stop_ptr, dones,
+            spin_ns, ctypes.byref(opts), ctypes.byref(self.h)), "persistent_start")
+
+    def wait(self, timeout_ms: int = 60000) -> int:
+        st = ctypes.c_int(-1)
+        lib.check(lib.load().ssla_hip_persistent_wait(self.h, timeout_ms, ctypes.byref(st)),
+                  "persistent_wait")
+        self.h = ctypes.c_void_p()
+        return st.value
+
+    def stop(self, timeout_ms: int = 60000) -> int:
+        self.rings.stop()
+        return self.wait(timeout_ms)

@@ -48,6 +48,14 @@ _SIGNATURES = {
     "ssla_hip_drain_n_ex": (_I, [ctypes.POINTER(abi.HybridS2S3Config), ctypes.POINTER(_VP),
                                  ctypes.POINTER(_I), ctypes.POINTER(_VP),
                                  ctypes.POINTER(abi.SslaHipDrainOpts)]),
+    "ssla_hip_wall_clock_khz": (_I, [ctypes.POINTER(_I)]),
+    "ssla_hip_timing_alloc": (_I, [ctypes.POINTER(abi.HybridS2S3Config), _I, ctypes.c_uint]),
+    "ssla_hip_timing_free": (None, [ctypes.POINTER(abi.HybridS2S3Config), _I]),
+    "ssla_hip_persistent_start": (_I, [ctypes.POINTER(abi.HybridS2S3Config), ctypes.POINTER(_VP),
+                                       ctypes.c_ulonglong, ctypes.POINTER(_VP), _VP,
+                                       ctypes.POINTER(_VP), ctypes.c_uint,
+                                       ctypes.POINTER(abi.SslaHipLiveOpts), ctypes.POINTER(_VP)]),
+    "ssla_hip_persistent_wait": (_I, [_VP, _I, ctypes.POINTER(_I)]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -1,0 +1,192 @@
+"""GPU parity of the in-kernel batch drain and the persistent live drain
+(libssla_hip.so C ABI) against the fp64 oracle.
+
+The batch drain takes records in batches of 1..32 inside one workgroup per
+block; the reference's drain_n contract (8-record batches with a clock pair
+per batch) is ssla_hip_drain_n with batch_clks.  The live drain polls rings
+in fine-grained host memory; here the test itself is the producer (records
+written, then their seq_done tags), so the check is deterministic: pass
+flags (through the timing slots' owner flag), counters, hidden state, and
+the prediction grid against the oracle.  Bars are those of
+test_drain_gpu.py.
+"""
+import ctypes
+import time
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from ssla_hip import abi, events
+
+pytestmark = pytest.mark.gpu
+
+FEAT_TOL = 1e-4
+HEAD_TOL = 5e-5
+HIDDEN_REL_TOL = 2e-5
+
+
+def say(*a):
+    print("[gpu-case]", *a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def H():
+    from ssla_hip import hybrid, lib
+    lib.load()
+    return hybrid
+
+
+def hidden_close(a, b):
+    return np.abs(a - b).max() <= HIDDEN_REL_TOL * max(1.0, float(np.abs(b).max()))
+
+
+def oracle_run(npz, rec, head=True):
+    st = O.S2S3(O.layers_from_npz(npz), 16, 20, 4, head=O.head_from_npz(npz) if head else None)
+    p2, p3, feat, h7 = st.run(rec.x, rec.y, rec.feat1, want_head=head)
+    return st, p2, p3, feat, h7
+
+
+def check_preds(preds, version, rec, p3, ref7):
+    m = p3 == 1
+    c3 = (rec.y.astype(int) >> 1) * 10 + (rec.x >> 1)
+    for cell in range(80):
+        k = np.nonzero(m & (c3 == cell))[0]
+        assert version[cell] == k.size, cell
+        if k.size:
+            assert np.abs(preds[cell] - ref7[k[-1]]).max() <= HEAD_TOL, cell
+
+
+@pytest.mark.parametrize("batch", [8, 17, 32])
+def test_batch_mode_matches_oracle(H, stub_dir, stub_npz, batch):
+    n = 6000
+    say("batch_mode", batch, n)
+    rec = events.blob_records(n, seed=11)
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        (out,), (h7,) = d.drain([events.to_records(rec)], want_head=True, batch=batch)
+        st, p2, p3, feat, ref7 = oracle_run(stub_npz, rec)
+        assert np.array_equal(out["pass2"], p2.astype(np.int32))
+        assert np.array_equal(out["pass3"], p3.astype(np.int32))
+        m = p3 == 1
+        df = np.abs(out["s3_feat"][m] - feat[m]).max()
+        dh = np.abs(h7[m] - ref7[m]).max()
+        say(f"batch {batch}: s3_feat max|d| {df:.3g}, head max|d| {dh:.3g}")
+        assert df <= FEAT_TOL and dh <= HEAD_TOL
+        for li in range(4):
+            assert hidden_close(d.hidden(0, li), st.H[li]), li
+        td2, td3 = d.counters(0)
+        assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3)
+        check_preds(*d.preds(0), rec, p3, ref7)
+
+
+def test_drain_n_with_batch_clocks(H, stub_dir, stub_npz):
+    n = 3001                       # partial last batch
+    say("drain_n batch_clks", n)
+    rec = events.blob_records(n, seed=12)
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        (out,), (clk,) = d.drain_with_clocks([events.to_records(rec)])
+        _, p2, p3, feat, _ = oracle_run(stub_npz, rec, head=False)
+        assert np.array_equal(out["pass2"], p2.astype(np.int32))
+        assert np.array_equal(out["pass3"], p3.astype(np.int32))
+        m = p3 == 1
+        assert np.abs(out["s3_feat"][m] - feat[m]).max() <= FEAT_TOL
+        assert clk.shape == ((n + 7) // 8, 2)
+        assert np.all(clk[:, 1] >= clk[:, 0]) and np.all(clk[:, 0] > 0)
+        assert np.all(np.diff(clk[:, 0].astype(np.int64)) >= 0)
+
+
+def _produce(rings, blk, recs, timeout_s=30.0, chunk=97):
+    """Publish records in chunks, never more than the ring holds ahead."""
+    t0 = time.time()
+    k = 0
+    while k < recs.size:
+        free = rings.capacity - int(rings.head[blk] - rings.tail[blk])
+        if free >= chunk or recs.size - k <= free:
+            m = min(chunk, recs.size - k, free)
+            rings.push(blk, recs[k:k + m])
+            k += m
+        elif time.time() - t0 > timeout_s:
+            raise TimeoutError("live drain stopped consuming")
+        else:
+            time.sleep(0.0002)
+
+
+def _wait_done(rings, blk, n, timeout_s=30.0):
+    t0 = time.time()
+    while int(rings.tail[blk]) < n:
+        if time.time() - t0 > timeout_s:
+            raise TimeoutError(f"block {blk}: tail {int(rings.tail[blk])} of {n}")
+        time.sleep(0.001)
+
+
+def test_live_single_stream(H, stub_dir, stub_npz):
+    n = 3000
+    say("live single stream", n)
+    rec = events.blob_records(n, seed=13)
+    recs = events.to_records(rec)
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        d.alloc_timing(4096)
+        rings = H.HostRings(1, capacity=1024)
+        live = H.LiveDrain(d, rings, idle_timeout_ms=15000)
+        try:
+            _produce(rings, 0, recs)
+            _wait_done(rings, 0, n)
+        finally:
+            status = live.stop()
+        assert status == 0
+        assert int(rings.done[0]) == n
+        st, p2, p3, feat, ref7 = oracle_run(stub_npz, rec)
+        ts = d.timing(0)[:n]
+        assert np.array_equal(ts["seq"], np.arange(n, dtype=np.uint32))
+        assert np.array_equal(ts["owner"], (p3 == 1).astype(np.uint32))
+        assert np.all(ts["t_done_clk"] >= ts["t_pop_clk"])
+        k0, k1 = d.kernel_clocks(0)
+        assert 0 < k0 <= int(ts["t_pop_clk"].min()) and k1 >= int(ts["t_done_clk"].max())
+        for li in range(4):
+            assert hidden_close(d.hidden(0, li), st.H[li]), li
+        td2, td3 = d.counters(0)
+        assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3)
+        check_preds(*d.preds(0), rec, p3, ref7)
+        from ssla_hip import lib
+        khz = ctypes.c_int()
+        lib.check(lib.load().ssla_hip_wall_clock_khz(ctypes.byref(khz)))
+        lat_us = (ts["t_done_clk"] - ts["t_pop_clk"]).astype(np.float64) / khz.value * 1e3
+        say(f"live: per-batch kernel time p50 {np.median(lat_us):.1f} us, max {lat_us.max():.1f} us")
+        rings.free()
+
+
+def test_live_four_streams(H, stub_dir, stub_npz):
+    n = 1500
+    say("live four streams", n)
+    recs = [events.blob_records(n, seed=20 + b) for b in range(4)]
+    with H.Drain.from_weights_dir(stub_dir, n_blocks=4) as d:
+        rings = H.HostRings(4, capacity=512)
+        live = H.LiveDrain(d, rings, idle_timeout_ms=15000)
+        try:
+            packed = [events.to_records(r) for r in recs]
+            for k in range(0, n, 100):
+                for b in range(4):
+                    _produce(rings, b, packed[b][k:k + 100])
+            for b in range(4):
+                _wait_done(rings, b, n)
+        finally:
+            status = live.stop()
+        assert status == 0
+        for b in range(4):
+            st, p2, p3, feat, ref7 = oracle_run(stub_npz, recs[b])
+            for li in range(4):
+                assert hidden_close(d.hidden(b, li), st.H[li]), (b, li)
+            td2, td3 = d.counters(b)
+            assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3)
+            check_preds(*d.preds(b), recs[b], p3, ref7)
+        rings.free()
+
+
+def test_live_idle_timeout_exits(H, stub_dir):
+    say("live idle timeout")
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        rings = H.HostRings(1, capacity=64)
+        live = H.LiveDrain(d, rings, idle_timeout_ms=300)
+        status = live.wait(timeout_ms=20000)
+        assert status == 3
+        rings.free()
