@@ -49,6 +49,13 @@ class OracleS2S3(ctypes.Structure):
 _lib = None
 
 
+class OracleS01(ctypes.Structure):
+    _fields_ = [("L", OracleLayer * 4), ("H", ctypes.POINTER(ctypes.c_float) * 4),
+                ("td0", ctypes.POINTER(ctypes.c_uint8)), ("td1", ctypes.POINTER(ctypes.c_uint8)),
+                ("last_t", ctypes.POINTER(ctypes.c_double)),
+                ("height", ctypes.c_int), ("width", ctypes.c_int), ("window", ctypes.c_int)]
+
+
 def build() -> None:
     subprocess.run(["make", "-s", "-C", str(HERE), "all"], check=True)
 
@@ -83,6 +90,13 @@ def load() -> ctypes.CDLL:
             f = getattr(L, nm)
             f.restype = None
             f.argtypes = [ctypes.POINTER(OracleHead), _FP, _FP]
+        L.oracle_preprocess.restype = None
+        L.oracle_preprocess.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_float, _FP]
+        L.oracle_s01_run.restype = ctypes.c_int
+        L.oracle_s01_run.argtypes = [ctypes.POINTER(OracleS01), ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         L.oracle_fuse_conv_bn.restype = None
         L.oracle_fuse_conv_bn.argtypes = [_FP, _FP, _FP, _FP, _FP, _FP, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_float, _FP, _FP]
@@ -211,17 +225,19 @@ def load_npz(weights_dir: str) -> Dict[str, np.ndarray]:
         return {k: np.array(z[k]) for k in z.files}
 
 
-def layers_from_npz(w) -> List[Layer]:
-    """Layers 4..7 of the sorted SSLA layer indices (ssla_kernels.cpp:178-198)."""
+def layers_from_npz(w, first: int = 4) -> List[Layer]:
+    """Four layers from position `first` of the sorted SSLA layer indices
+    (ssla_kernels.cpp:178-198): 4 gives L4..L7, 0 gives L0..L3."""
     idx = sorted(int(k.split("/")[1]) for k in w if k.startswith("layers/") and k.endswith("/W_in_cat"))
     out = []
     for li in range(4):
-        p = f"layers/{idx[4 + li]}"
+        p = f"layers/{idx[first + li]}"
         qvg, go = reshape(w[f"{p}/W_in_cat"], w[f"{p}/W_out_cat"], w[f"{p}/q_proj/weight"],
                           w[f"{p}/v_proj/weight"], w[f"{p}/g_proj/weight"], w[f"{p}/o_proj/weight"])
         ipk = f"{p}/input_proj/weight"
         out.append(Layer(qvg, go, _f32(w[ipk]) if ipk in w else None,
-                         _f32(w[f"{p}/norm/weight"]), _f32(w[f"{p}/norm/bias"])))
+                         _f32(w[f"{p}/norm/weight"]), _f32(w[f"{p}/norm/bias"]),
+                         3 if qvg.shape[0] == 9 else 1))
     return out
 
 
@@ -277,6 +293,56 @@ class S2S3:
         if rc < 0:
             raise ValueError("oracle_s2s3_run rejected its arguments")
         return p2, p3, feat, head7
+
+
+class S01:
+    """One producer shard over stages 0 + 1 (oracle_s01_run): layers L0..L3,
+    hidden state, tdrop counters and per-pixel last event times."""
+
+    def __init__(self, layers: Sequence[Layer], height: int, width: int, window: int):
+        self.layers = list(layers)
+        self.height, self.width, self.window = height, width, window
+        c0, c1 = height * width, (height // 2) * (width // 2)
+        dims = [L.goW.shape[1] for L in self.layers]
+        self.H = [np.zeros((c, d), np.float32) for c, d in zip((c0, c0, c1, c1), dims)]
+        self.td0 = np.zeros(c1, np.uint8)
+        self.td1 = np.zeros((height // 4) * (width // 4), np.uint8)
+        self.last_t = np.full(c0, -1.0, np.float64)
+
+    def run(self, events: np.ndarray, owner=None, precision: int = 64):
+        """events (n, 4) [t_us, x, y, p] -> (pass0, pass1, feat1 (n, 24), x2, y2)."""
+        ev = _f32(events).reshape(-1, 4)
+        n = ev.shape[0]
+        own = None if owner is None else np.ascontiguousarray(owner, np.uint8)
+        p0 = np.zeros(n, np.int8)
+        p1 = np.zeros(n, np.int8)
+        feat = np.zeros((n, C1), np.float32)
+        x2 = np.zeros(n, np.uint16)
+        y2 = np.zeros(n, np.uint16)
+        st = OracleS01()
+        for li in range(4):
+            st.L[li] = self.layers[li].c()
+            st.H[li] = _fp(self.H[li])
+        st.td0 = self.td0.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8))
+        st.td1 = self.td1.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8))
+        st.last_t = self.last_t.ctypes.data_as(ctypes.POINTER(ctypes.c_double))
+        st.height, st.width, st.window = self.height, self.width, self.window
+        rc = load().oracle_s01_run(ctypes.byref(st), ev.ctypes.data,
+                                   None if own is None else own.ctypes.data, n, precision,
+                                   p0.ctypes.data, p1.ctypes.data, feat.ctypes.data,
+                                   x2.ctypes.data, y2.ctypes.data)
+        if rc < 0:
+            raise ValueError("oracle_s01_run rejected its arguments")
+        return p0, p1, feat, x2, y2
+
+
+def preprocess(last_t: np.ndarray, height: int, width: int, t_us: float, x: int, y: int,
+               p: float) -> np.ndarray:
+    """oracle_preprocess on a (height*width,) float64 last-time array."""
+    assert last_t.dtype == np.float64 and last_t.flags.c_contiguous
+    out = np.zeros(2, np.float32)
+    load().oracle_preprocess(last_t.ctypes.data, height, width, t_us, x, y, p, _fp(out))
+    return out
 
 
 def decisions(x, y, H2: int, W2: int, window: int, td2=None, td3=None):

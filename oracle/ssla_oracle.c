@@ -311,6 +311,78 @@ int oracle_s2s3_run(OracleS2S3* st, const uint16_t* xs, const uint16_t* ys,
 }
 
 /* ------------------------------------------------------------------------ */
+/* One producer shard, stages 0 + 1                                          */
+/* ------------------------------------------------------------------------ */
+
+/* dt_norm = clamp((t - last) / 1e5, 0, 1), 1 for a pixel's first event;
+ * zeros outside the sensor (src/ssla_kernels.cpp:288-309). */
+void oracle_preprocess(double* last_t, int height, int width, float t_us, int x, int y,
+                       float p, float feat[2]) {
+    if (!in_grid(x, y, height, width)) {
+        feat[0] = feat[1] = 0.0f;
+        return;
+    }
+    const int pix = y * width + x;
+    const double prev = last_t[pix];
+    float dt = 1.0f;
+    if (prev >= 0.0) {
+        double v = ((double)t_us - prev) / 1e5;
+        if (v < 0.0) v = 0.0;
+        if (v > 1.0) v = 1.0;
+        dt = (float)v;
+    }
+    last_t[pix] = (double)t_us;
+    feat[0] = dt;
+    feat[1] = p;
+}
+
+int oracle_s01_run(OracleS01* st, const float* ev, const uint8_t* owner, int n,
+                   int precision, int8_t* pass0, int8_t* pass1, float* feat1,
+                   uint16_t* x2, uint16_t* y2) {
+    if (!st || !ev || n < 0 || (precision != 32 && precision != 64)) return -1;
+    if (st->height <= 0 || st->width <= 0 || (st->height & 3) || (st->width & 3)) return -1;
+    const layer_fn step = (precision == 64) ? oracle_layer_step_f64
+                                            : oracle_layer_step_f32;
+    const int H0 = st->height, W0 = st->width, H1 = H0 >> 1, W1 = W0 >> 1, W2 = W0 >> 2;
+    float in[2], b0[MAXD], b1[MAXD], b2[MAXD], b3[MAXD];
+    int n1 = 0;
+    for (int i = 0; i < n; ++i) {
+        const float* e = ev + (size_t)i * 4;
+        const int x = (int)e[1], y = (int)e[2];
+        int p0 = -2, p1 = -2;
+        if (feat1) memset(feat1 + (size_t)i * 24, 0, sizeof(float) * 24);
+        if (x2) x2[i] = 0;
+        if (y2) y2[i] = 0;
+        if (in_grid(x, y, H0, W0)) {
+            oracle_preprocess(st->last_t, H0, W0, e[0], x, y, e[3], in);
+            step(&st->L[0], in, st->H[0], x, y, H0, W0, b0);
+            step(&st->L[1], b0, st->H[1], x, y, H0, W0, b1);
+            if (owner && !owner[i]) {
+                p0 = p1 = -1;
+            } else {
+                const int sx = x >> 1, sy = y >> 1;
+                p0 = oracle_tdrop(st->td0, st->window, sy * W1 + sx);
+                p1 = 0;
+                if (p0) {
+                    step(&st->L[2], b1, st->H[2], sx, sy, H1, W1, b2);
+                    step(&st->L[3], b2, st->H[3], sx, sy, H1, W1, b3);
+                    p1 = oracle_tdrop(st->td1, st->window, (sy >> 1) * W2 + (sx >> 1));
+                    if (p1) {
+                        ++n1;
+                        if (feat1) memcpy(feat1 + (size_t)i * 24, b3, sizeof(float) * 24);
+                        if (x2) x2[i] = (uint16_t)(sx >> 1);
+                        if (y2) y2[i] = (uint16_t)(sy >> 1);
+                    }
+                }
+            }
+        }
+        if (pass0) pass0[i] = (int8_t)p0;
+        if (pass1) pass1[i] = (int8_t)p1;
+    }
+    return n1;
+}
+
+/* ------------------------------------------------------------------------ */
 /* BN fold (hybrid_common.py:327-349)                                       */
 /* ------------------------------------------------------------------------ */
 

@@ -20,6 +20,11 @@
  *   - oracle_head_raw          orin/kernels/ssla_s2_s3_head_celled.cuh:841-902
  *                              (raw [reg4, obj, cls2] of the 2-branch head)
  *   - oracle_fuse_conv_bn      orin/orin/hybrid_common.py:327-349
+ *   - oracle_s01_run           one producer shard: preprocess
+ *                              (src/ssla_kernels.cpp:288-309), stages 0 and 1
+ *                              of step_ref (orin/orin/ssla_ref.py:119-170),
+ *                              halo events stage 0 only
+ *                              (src/lib_stage01_to_gpu.cpp:210-330)
  *
  * Pinning (see tests/): tdrop + schedule by the published P1 pass counts;
  * reshape by the per-position module forward identity; layer_step by the
@@ -121,6 +126,36 @@ int oracle_s2s3_run(OracleS2S3* st, const uint16_t* xs, const uint16_t* ys,
 int oracle_s2s3_decisions(uint8_t* td2, uint8_t* td3, int H2, int W2,
                           int window, const uint16_t* xs, const uint16_t* ys,
                           int n, int8_t* pass2, int8_t* pass3);
+
+/* One producer shard over stages 0 + 1: layers L0..L3 (L0 with K = 1),
+ * hidden state H[li] (cells x OUT on the full or half grid), tdrop counters td0
+ * (height/2 * width/2) and td1 (height/4 * width/4), per-pixel last event time last_t (height * width,
+ * initialised to -1).                                                     */
+typedef struct {
+    OracleLayer L[4];
+    float*   H[4];
+    uint8_t* td0;
+    uint8_t* td1;
+    double*  last_t;
+    int height, width;
+    int window;
+} OracleS01;
+
+/* feat = [dt_norm, p] with dt_norm = clamp((t - last_t[pixel]) / 1e5, 0, 1)
+ * (1 for a pixel's first event); updates last_t; zeros outside the sensor. */
+void oracle_preprocess(double* last_t, int height, int width, float t_us,
+                       int x, int y, float p, float feat[2]);
+
+/* Events ev[i] = (t_us, x, y, p).  owner[i] = 0 marks a halo event (stage
+ * 0 for its state only, no tdrop); NULL = all owned.  Outputs (any NULL):
+ *   pass0[i], pass1[i]  1/0 (pass1 = 0 when pass0 = 0), -1 for halo
+ *                       events, -2 for events outside the sensor
+ *   feat1[i*24..]       L3 output when pass1, zeros otherwise
+ *   x2[i], y2[i]        s2 coordinates (x >> 2, y >> 2) when pass1
+ * Returns the number of pass1 events, or -1 on bad arguments.            */
+int oracle_s01_run(OracleS01* st, const float* ev, const uint8_t* owner, int n,
+                   int precision, int8_t* pass0, int8_t* pass1, float* feat1,
+                   uint16_t* x2, uint16_t* y2);
 
 /* Raw head output [reg0..3, obj, cls0, cls1] for one 96-float feature.   */
 void oracle_head_raw_f64(const OracleHead* h, const float* x, float out7[7]);

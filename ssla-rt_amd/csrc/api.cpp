@@ -16,6 +16,7 @@
 
 #include "drain_live.h"
 #include "drain_scan.h"
+#include "pack.h"
 #include "ssla_hip.h"
 #include "weights_dir.h"
 
@@ -42,37 +43,19 @@ namespace {
         }                                                                     \
     } while (0)
 
-constexpr int kChans[4] = {12, 24, 48, 96};   // SSLA-S stage widths
-
 // GPU layer li (0..3 = L4..L7): input / output widths.
 constexpr int kIn[4] = {24, 48, 48, 96};
 constexpr int kOut[4] = {48, 48, 96, 96};
 
-// ---- packing (ssla_kernels.cpp:73-153; weights_ssla.py:24-88) ------------
-//
-// qvgIn[p] = [qW; vW; gW] @ scatter_p and goW[p] = gather_p @ oW, with
-// scatter_p[d, c] = W_in_cat[c, p*D + d] and gather_p[i, j] =
-// W_out_cat[p*D + j, i]; products accumulate in fp32 over the inner index
-// in ascending order.  The device layouts are the transposes
-// (9, IN, 3*OUT) and (9, OUT_in, OUT_out).
+// ---- device layouts of the fused layer weights ---------------------------
+// qvgIn (A, 3*OUT, IN) -> (9, IN, 3*OUT); goW (A, D, D) -> (9, OUT_in, OUT_out);
+// input_proj (OUT, IN) -> (IN, OUT).
 struct PackedLayer {
     std::vector<float> qvg_dev;   // (9, IN, 3*OUT)
     std::vector<float> gow_dev;   // (9, OUT, OUT)
     std::vector<float> ip_dev;    // (IN, OUT) or empty
     std::vector<float> gamma, beta;
 };
-
-void mm_acc(const float* B, int bo, int bi, const float* A, int ai, float* C) {
-    for (int o = 0; o < bo; ++o) {
-        float* cr = C + (size_t)o * ai;
-        std::fill(cr, cr + ai, 0.0f);
-        for (int k = 0; k < bi; ++k) {
-            const float bv = B[(size_t)o * bi + k];
-            const float* ar = A + (size_t)k * ai;
-            for (int i = 0; i < ai; ++i) cr[i] += bv * ar[i];
-        }
-    }
-}
 
 const NpzTensor& need(const std::map<std::string, NpzTensor>& W, const std::string& k,
                       std::vector<int64_t> shape) {
@@ -93,59 +76,25 @@ const NpzTensor& need(const std::map<std::string, NpzTensor>& W, const std::stri
 
 PackedLayer pack_layer(const std::map<std::string, NpzTensor>& W, const std::string& pre,
                        int IN, int D) {
-    const auto win_t = W.find(pre + "/W_in_cat");
-    const auto wout_t = W.find(pre + "/W_out_cat");
-    if (win_t == W.end() || wout_t == W.end()) throw std::runtime_error("weights.npz: missing " + pre + "/W_*_cat");
-    const NpzTensor& Win = win_t->second;
-    const NpzTensor& Wout = wout_t->second;
-    if (Win.shape.size() != 2 || Win.shape[0] != IN || Wout.shape.size() != 2 || Wout.shape[1] != D)
-        throw std::runtime_error(pre + ": W_in_cat must be (in_dim, n*out_dim) and W_out_cat (n*out_dim, out_dim)");
-    const int win_cols = (int)Win.shape[1], wout_rows = (int)Wout.shape[0];
-    if (win_cols % D || wout_rows % D) throw std::runtime_error(pre + ": W_*_cat not a multiple of out_dim");
-    const int n_in = win_cols / D, n_out = wout_rows / D;
-    const int A = std::max(n_in, n_out);
-    if (A != 9) throw std::runtime_error(pre + ": expected 9 patch positions (K=3), found " + std::to_string(A));
-    if ((n_in != 1 && n_in != 9) || (n_out != 1 && n_out != 9)) throw std::runtime_error(pre + ": bad position count");
-    const NpzTensor& qW = need(W, pre + "/q_proj/weight", {D, D});
-    const NpzTensor& vW = need(W, pre + "/v_proj/weight", {D, D});
-    const NpzTensor& gW = need(W, pre + "/g_proj/weight", {D, D});
-    const NpzTensor& oW = need(W, pre + "/o_proj/weight", {D, D});
+    const FusedLayer F = fuse_layer(W, pre, IN, D);
+    if (F.A != 9) throw std::runtime_error(pre + ": expected 9 patch positions (K=3)");
     PackedLayer L;
-    L.gamma = need(W, pre + "/norm/weight", {D}).data;
-    L.beta = need(W, pre + "/norm/bias", {D}).data;
-    const auto ip = W.find(pre + "/input_proj/weight");
-    if (IN != D) {
-        if (ip == W.end()) throw std::runtime_error(pre + ": in_dim != out_dim but no input_proj");
-        const NpzTensor& P = need(W, pre + "/input_proj/weight", {D, IN});
+    L.gamma = F.gamma;
+    L.beta = F.beta;
+    if (!F.input_proj.empty()) {
         L.ip_dev.resize((size_t)IN * D);
         for (int o = 0; o < D; ++o)
-            for (int i = 0; i < IN; ++i) L.ip_dev[(size_t)i * D + o] = P.data[(size_t)o * IN + i];
-    } else if (ip != W.end()) {
-        throw std::runtime_error(pre + ": unexpected input_proj for in_dim == out_dim");
+            for (int i = 0; i < IN; ++i) L.ip_dev[(size_t)i * D + o] = F.input_proj[(size_t)o * IN + i];
     }
-    std::vector<float> scatter((size_t)D * IN), gather((size_t)D * D), blk((size_t)D * IN), go((size_t)D * D);
     L.qvg_dev.assign((size_t)9 * IN * 3 * D, 0.f);
     L.gow_dev.assign((size_t)9 * D * D, 0.f);
     for (int p = 0; p < 9; ++p) {
-        const int pin = n_in == 1 ? 0 : p, pout = n_out == 1 ? 0 : p;
-        for (int d = 0; d < D; ++d)
-            for (int c = 0; c < IN; ++c)
-                scatter[(size_t)d * IN + c] = Win.data[(size_t)c * win_cols + (size_t)pin * D + d];
-        for (int i = 0; i < D; ++i)
-            for (int j = 0; j < D; ++j)
-                gather[(size_t)i * D + j] = Wout.data[((size_t)pout * D + j) * D + i];
-        const NpzTensor* qvg[3] = {&qW, &vW, &gW};
-        for (int part = 0; part < 3; ++part) {
-            mm_acc(qvg[part]->data.data(), D, D, scatter.data(), IN, blk.data());
-            // blk (D, IN) -> device rows i, columns part*D + d
-            for (int d = 0; d < D; ++d)
-                for (int i = 0; i < IN; ++i)
-                    L.qvg_dev[((size_t)p * IN + i) * 3 * D + (size_t)part * D + d] = blk[(size_t)d * IN + i];
-        }
-        mm_acc(gather.data(), D, D, oW.data.data(), D, go.data());
+        for (int r = 0; r < 3 * D; ++r)
+            for (int i = 0; i < IN; ++i)
+                L.qvg_dev[((size_t)p * IN + i) * 3 * D + r] = F.qvgIn[((size_t)p * 3 * D + r) * IN + i];
         for (int o = 0; o < D; ++o)
             for (int i = 0; i < D; ++i)
-                L.gow_dev[((size_t)p * D + i) * D + o] = go[(size_t)o * D + i];
+                L.gow_dev[((size_t)p * D + i) * D + o] = F.goW[((size_t)p * D + o) * D + i];
     }
     return L;
 }
@@ -342,18 +291,9 @@ int ssla_hip_model_load(const char* dir, SslaHipModel** out) {
         info.W3 = info.W2 >> 1;
         // SSLA layer indices, sorted (ssla_kernels.cpp:178-198); the GPU
         // path takes the last four (stages 2 and 3).
-        std::vector<int> idx;
-        for (const auto& kv : W) {
-            const std::string& k = kv.first;
-            if (k.rfind("layers/", 0) != 0) continue;
-            const size_t sl = k.find('/', 7);
-            if (sl == std::string::npos || k.substr(sl + 1) != "W_in_cat") continue;
-            idx.push_back(std::stoi(k.substr(7, sl - 7)));
-        }
-        std::sort(idx.begin(), idx.end());
+        const std::vector<int> idx = ssla_layer_indices(W);
         if (idx.size() != 8)
             throw std::runtime_error("weights.npz: expected 8 SSLA layers, found " + std::to_string(idx.size()));
-        (void)kChans;
         for (int li = 0; li < 4; ++li)
             layers.push_back(pack_layer(W, "layers/" + std::to_string(idx[4 + li]), kIn[li], kOut[li]));
         info.has_head = W.count("head/cls_convs/0/0/weight") ? 1 : 0;

@@ -1,0 +1,592 @@
+// producer.cpp -- host CPU shards running SSLA-S stages 0 + 1 and feeding the
+// drain's rings: libstage01_to_gpu.so (s01g_*) and libstage01_capi.so (s0_*).
+//
+// Threads: one submitting thread (s01g_submit_batch, or the synthetic source)
+// routes each event to the x-strip shards that need it through per-shard
+// single-producer / single-consumer queues; every shard thread owns a private
+// Stage01 state.  The owner shard of an event runs the stages and, in the GPU
+// library, publishes surviving records to the attached rings.
+//
+// Build-time switch: STAGE01_TO_GPU selects the s01g_* library (tdrop checked
+// before the stages so dropped work runs state-only, and ring publishing);
+// without it the file builds the s0_* library (full stage 0 for every event,
+// tdrops after the stages, as the CPU-only reference path does).
+#include <pthread.h>
+#include <sched.h>
+#include <time.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <random>
+#include <thread>
+#include <vector>
+
+#include "ssla_abi.h"
+#include "stage01.h"
+
+namespace ssla {
+namespace {
+
+std::uint64_t mono_ns() {
+    timespec ts;
+    clock_gettime(CLOCK_MONOTONIC_RAW, &ts);
+    return (std::uint64_t)ts.tv_sec * 1000000000ull + (std::uint64_t)ts.tv_nsec;
+}
+
+void pin_self(int core) {
+    if (core < 0) return;
+    const unsigned n = std::thread::hardware_concurrency();
+    if (n && (unsigned)core >= n) return;
+    cpu_set_t cs;
+    CPU_ZERO(&cs);
+    CPU_SET(core, &cs);
+    pthread_setaffinity_np(pthread_self(), sizeof(cs), &cs);
+}
+
+inline void cpu_relax() { __builtin_ia32_pause(); }
+
+// Bounded single-producer / single-consumer queue (capacity 2^k).
+template <class T>
+class Queue {
+public:
+    explicit Queue(std::size_t cap) : mask_(cap - 1), buf_(cap) {}
+    bool try_push(const T& v) {
+        const std::size_t h = head_.load(std::memory_order_relaxed);
+        if (h - tail_.load(std::memory_order_acquire) > mask_) return false;
+        buf_[h & mask_] = v;
+        head_.store(h + 1, std::memory_order_release);
+        return true;
+    }
+    void push(const T& v) {
+        while (!try_push(v)) cpu_relax();
+    }
+    bool try_pop(T& out) {
+        const std::size_t t = tail_.load(std::memory_order_relaxed);
+        if (t == head_.load(std::memory_order_acquire)) return false;
+        out = buf_[t & mask_];
+        tail_.store(t + 1, std::memory_order_release);
+        return true;
+    }
+    std::size_t size() const {
+        return head_.load(std::memory_order_relaxed) - tail_.load(std::memory_order_relaxed);
+    }
+
+private:
+    const std::size_t mask_;
+    std::vector<T> buf_;
+    alignas(64) std::atomic<std::size_t> head_{0};
+    alignas(64) std::atomic<std::size_t> tail_{0};
+};
+
+struct Msg {
+    std::uint64_t t_arr_ns;    // entered the shard queue
+    std::uint64_t t_emit_ns;   // produced by the source
+    float t, x, y, p;
+    std::uint8_t owner, eof;
+};
+
+enum Seg { SEG_PRE, SEG_S0, SEG_TD0, SEG_S1, SEG_TD1, SEG_PUSH, NSEG };
+
+struct Shard {
+    int id = 0, core = -1;
+    std::unique_ptr<Stage01> st;
+    std::unique_ptr<Queue<Msg>> q;
+    std::vector<double> samples;
+    std::atomic<std::size_t> n_samples{0};
+    std::atomic<std::uint64_t> owner{0}, halo{0}, pass0{0}, pass1{0};
+    std::atomic<std::uint64_t> seg_ns[NSEG] = {}, seg_n[NSEG] = {};
+};
+
+struct RingOut {
+    HybridInputRec* buf = nullptr;
+    std::uint64_t* head = nullptr;
+    int x_lo = 0, x_hi = 0, y_lo = 0, y_hi = 0;
+    std::atomic<std::uint64_t> pushed{0};
+};
+
+constexpr int kMaxRings = SSLA_MAX_BLOCKS;
+
+}  // namespace
+
+struct Producer {
+    int N = 1, halo = 2, strip = 1, W = 0, H = 0;
+    std::vector<std::unique_ptr<Shard>> shards;
+    std::vector<std::thread> threads;
+    std::atomic<std::uint64_t> oob{0};
+    std::chrono::steady_clock::time_point t0;
+    // rings
+    std::atomic<bool> attached{false};
+    RingOut rings[kMaxRings];
+    int n_rings = 0, W2 = 0, H2 = 0;
+    std::uint64_t ring_mask = 0;
+    // synthetic source
+    std::atomic<bool> synth_on{false};
+    std::thread synth;
+    std::atomic<std::uint64_t> synth_n{0};
+
+    void route(float t, float x, float y, float p, std::uint64_t t_emit) {
+        const int ex = (int)x, ey = (int)y;
+        if (ex < 0 || ex >= W || ey < 0 || ey >= H) {
+            oob.fetch_add(1, std::memory_order_relaxed);
+            return;
+        }
+        const int home = ex / strip;
+        const int owner = std::min(home, N - 1);
+        const std::uint64_t now = mono_ns();
+        for (int k = std::max(0, home - 1); k <= std::min(N - 1, home + 1); ++k) {
+            if (ex < k * strip - halo || ex >= (k + 1) * strip + halo) continue;
+            Msg m{now, t_emit, t, x, y, p, (std::uint8_t)(k == owner), 0};
+            shards[k]->q->push(m);
+        }
+    }
+
+    void publish(int x2, int y2, float t, const float* feat1, std::uint64_t t_emit) {
+        if (x2 < 0 || x2 >= W2 || y2 < 0 || y2 >= H2) return;
+        for (int b = 0; b < n_rings; ++b) {
+            RingOut& r = rings[b];
+            if (x2 < r.x_lo || x2 >= r.x_hi || y2 < r.y_lo || y2 >= r.y_hi) continue;
+            const std::uint64_t slot = __atomic_fetch_add(r.head, 1ull, __ATOMIC_RELAXED);
+            HybridInputRec* d = r.buf + (slot & ring_mask);
+            d->t = t;
+            d->x = (unsigned short)x2;
+            d->y = (unsigned short)y2;
+            std::memcpy(d->feat1, feat1, sizeof(float) * SSLA_C1);
+            d->t_push_ns = mono_ns();
+            d->t_emit_ns = t_emit;
+            __atomic_store_n(&d->seq_done, slot + 1ull, __ATOMIC_RELEASE);
+            r.pushed.fetch_add(1, std::memory_order_relaxed);
+        }
+    }
+
+    void work(Shard* c, bool to_gpu) {
+        pin_self(c->core);
+        Stage01& st = *c->st;
+        const std::size_t cap = c->samples.size();
+        float f0[2], s0[12], s1[24];
+        auto seg = [&](int s, std::uint64_t a, std::uint64_t b) {
+            c->seg_ns[s].fetch_add(b - a, std::memory_order_relaxed);
+            c->seg_n[s].fetch_add(1, std::memory_order_relaxed);
+        };
+        while (true) {
+            Msg m;
+            if (!c->q->try_pop(m)) {
+                cpu_relax();
+                continue;
+            }
+            if (m.eof) break;
+            const int x = (int)m.x, y = (int)m.y;
+            const std::uint64_t a = mono_ns();
+            st.preprocess(m.t, x, y, m.p, f0);
+            const std::uint64_t b = mono_ns();
+            seg(SEG_PRE, a, b);
+            if (!m.owner) {
+                st.stage0(x, y, f0, s0, false);
+                seg(SEG_S0, b, mono_ns());
+                c->halo.fetch_add(1, std::memory_order_relaxed);
+                continue;
+            }
+            bool pass0 = false, pass1 = false;
+            if (to_gpu) {
+                // tdrop first: stage outputs nobody consumes run state-only
+                pass0 = st.tdrop_at(0, x >> 1, y >> 1);
+                const std::uint64_t t1 = mono_ns();
+                seg(SEG_TD0, b, t1);
+                st.stage0(x, y, f0, s0, pass0);
+                const std::uint64_t t2 = mono_ns();
+                seg(SEG_S0, t1, t2);
+                if (pass0) {
+                    pass1 = st.tdrop_at(1, x >> 2, y >> 2);
+                    const std::uint64_t t3 = mono_ns();
+                    seg(SEG_TD1, t2, t3);
+                    st.stage1(x >> 1, y >> 1, s0, s1, pass1);
+                    const std::uint64_t t4 = mono_ns();
+                    seg(SEG_S1, t3, t4);
+                    if (pass1 && attached.load(std::memory_order_acquire)) {
+                        publish(x >> 2, y >> 2, m.t, s1, m.t_emit_ns);
+                        seg(SEG_PUSH, t4, mono_ns());
+                    }
+                }
+            } else {
+                st.stage0(x, y, f0, s0, true);
+                const std::uint64_t t1 = mono_ns();
+                seg(SEG_S0, b, t1);
+                pass0 = st.tdrop_at(0, x >> 1, y >> 1);
+                const std::uint64_t t2 = mono_ns();
+                seg(SEG_TD0, t1, t2);
+                if (pass0) {
+                    st.stage1(x >> 1, y >> 1, s0, s1, true);
+                    const std::uint64_t t3 = mono_ns();
+                    seg(SEG_S1, t2, t3);
+                    pass1 = st.tdrop_at(1, x >> 2, y >> 2);
+                    seg(SEG_TD1, t3, mono_ns());
+                }
+            }
+            const std::size_t i = c->n_samples.fetch_add(1, std::memory_order_relaxed);
+            c->samples[i % cap] = (double)(mono_ns() - m.t_arr_ns);
+            c->owner.fetch_add(1, std::memory_order_relaxed);
+            if (pass0) c->pass0.fetch_add(1, std::memory_order_relaxed);
+            if (pass1) c->pass1.fetch_add(1, std::memory_order_relaxed);
+        }
+    }
+
+    void snapshot(double* out, int n_slots) const {
+        for (int i = 0; i < n_slots; ++i) out[i] = 0.0;
+        std::uint64_t own = 0, hal = 0, p0 = 0, p1 = 0, occ = 0;
+        std::vector<double> s;
+        std::uint64_t sn[NSEG] = {}, sc[NSEG] = {};
+        for (const auto& c : shards) {
+            own += c->owner.load();
+            hal += c->halo.load();
+            p0 += c->pass0.load();
+            p1 += c->pass1.load();
+            occ += c->q->size();
+            const std::size_t n = std::min(c->n_samples.load(), c->samples.size());
+            s.insert(s.end(), c->samples.begin(), c->samples.begin() + n);
+            for (int k = 0; k < NSEG; ++k) {
+                sn[k] += c->seg_ns[k].load();
+                sc[k] += c->seg_n[k].load();
+            }
+        }
+        out[0] = (double)own;
+        out[1] = (double)hal;
+        out[2] = (double)p0;
+        out[3] = (double)oob.load();
+        out[4] = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        out[5] = (double)occ;
+        if (!s.empty()) {
+            std::sort(s.begin(), s.end());
+            const double n = (double)s.size();
+            auto pct = [&](double q) {   // linear interpolation (include/lat_stats.h:33-40)
+                if (s.size() == 1) return s[0];
+                const double idx = q * (n - 1);
+                const std::size_t lo = (std::size_t)std::floor(idx);
+                const std::size_t hi = std::min(s.size() - 1, lo + 1);
+                return s[lo] * (1.0 - (idx - lo)) + s[hi] * (idx - lo);
+            };
+            double mean = 0.0;
+            for (double v : s) mean += v;
+            out[6] = pct(0.50) * 1e-3;
+            out[7] = pct(0.90) * 1e-3;
+            out[8] = pct(0.99) * 1e-3;
+            out[9] = pct(0.999) * 1e-3;
+            out[10] = s.back() * 1e-3;
+            out[11] = mean / n * 1e-3;
+            out[12] = n;
+        }
+        out[13] = (double)p1;
+        if (n_slots > 14) {
+            out[14] = (double)rings[0].pushed.load();
+            out[15] = (double)rings[1].pushed.load();
+        }
+        if (n_slots >= 28) {
+            for (int k = 0; k < NSEG; ++k) {
+                out[16 + k] = (double)sn[k];
+                out[22 + k] = (double)sc[k];
+            }
+        }
+    }
+
+    void reset_stats() {
+        for (auto& c : shards) {
+            c->owner = 0;
+            c->halo = 0;
+            c->pass0 = 0;
+            c->pass1 = 0;
+            c->n_samples = 0;
+            for (int k = 0; k < NSEG; ++k) {
+                c->seg_ns[k] = 0;
+                c->seg_n[k] = 0;
+            }
+        }
+        for (auto& r : rings) r.pushed = 0;
+        oob = 0;
+        t0 = std::chrono::steady_clock::now();
+    }
+
+    void stop_synth() {
+        if (synth_on.exchange(false) && synth.joinable()) synth.join();
+        if (synth.joinable()) synth.join();
+    }
+
+    void shutdown() {
+        stop_synth();
+        for (auto& c : shards) {
+            Msg m{};
+            m.eof = 1;
+            c->q->push(m);
+        }
+        for (auto& t : threads)
+            if (t.joinable()) t.join();
+    }
+};
+
+namespace {
+
+Producer* make_producer(const char* dir, int n_shards, int halo, int base_core, int sample_cap,
+                        unsigned shard_cap, bool to_gpu, const char* tag) {
+    if (!dir) return nullptr;
+    if (n_shards < 1) n_shards = 1;
+    if (sample_cap < 1024) sample_cap = 1024;
+    if (shard_cap < 4) shard_cap = 4;
+    unsigned p2 = 1;
+    while (p2 < shard_cap) p2 <<= 1;
+    auto P = std::make_unique<Producer>();
+    P->N = n_shards;
+    P->halo = halo;
+    try {
+        for (int k = 0; k < n_shards; ++k) {
+            auto c = std::make_unique<Shard>();
+            c->id = k;
+            c->core = base_core >= 0 ? base_core + k : -1;
+            c->st = std::make_unique<Stage01>(dir);
+            c->q = std::make_unique<Queue<Msg>>(p2);
+            c->samples.assign((std::size_t)sample_cap, 0.0);
+            P->shards.push_back(std::move(c));
+        }
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "[%s] load failed: %s\n", tag, e.what());
+        return nullptr;
+    }
+    P->W = P->shards[0]->st->W();
+    P->H = P->shards[0]->st->H();
+    P->strip = (P->W + n_shards - 1) / n_shards;
+    P->t0 = std::chrono::steady_clock::now();
+    Producer* raw = P.release();
+    for (int k = 0; k < n_shards; ++k)
+        raw->threads.emplace_back([raw, k, to_gpu]() { raw->work(raw->shards[k].get(), to_gpu); });
+    return raw;
+}
+
+int submit(Producer* P, const float* ev, int n) {
+    if (!P || !ev || n <= 0) return 0;
+    int accepted = 0;
+    for (int i = 0; i < n; ++i) {
+        const float* e = ev + 4 * (size_t)i;
+        const int ex = (int)e[1], ey = (int)e[2];
+        if (ex < 0 || ex >= P->W || ey < 0 || ey >= P->H) {
+            P->oob.fetch_add(1, std::memory_order_relaxed);
+            continue;
+        }
+        P->route(e[0], e[1], e[2], e[3], mono_ns());
+        ++accepted;
+    }
+    return accepted;
+}
+
+// Paced source: one event every 1 / rate, spin-waiting on the raw monotonic
+// clock; event time advances 1 / rate_mev microseconds per event.
+//   uniform (lib_stage01_to_gpu.cpp:624-706): xorshift64 (13, 7, 17) with
+//     seed 0x9E3779B97F4A7C15 when 0; x = r mod W, y = (r >> 16) mod H,
+//     p = bit 32 of r -- the same stream for the same seed;
+//   blobs: n_blobs Gaussian blobs moving at 0.5-2 px/ms and reflecting off
+//     the sensor edges, plus bg_frac uniform background, p = +-1.
+void synth_loop(Producer* P, double rate_mev, int core, std::uint64_t seed, int n_blobs,
+                double sigma, double bg_frac) {
+    pin_self(core);
+    const int W = P->W, H = P->H;
+    const double period_ns = rate_mev > 0 ? 1e3 / rate_mev : 0.0;
+    const float dt_us = rate_mev > 0 ? (float)(1.0 / rate_mev) : 1.0f;
+    std::uint64_t xs = seed ? seed : 0x9E3779B97F4A7C15ull;
+    auto next_u64 = [&xs]() {
+        xs ^= xs << 13;
+        xs ^= xs >> 7;
+        xs ^= xs << 17;
+        return xs;
+    };
+    std::mt19937_64 rng(xs);
+    std::uniform_real_distribution<double> U(0.0, 1.0);
+    std::normal_distribution<double> N01(0.0, 1.0);
+    struct Blob { double x0, y0, vx, vy; };
+    std::vector<Blob> blobs((std::size_t)std::max(0, n_blobs));
+    for (auto& b : blobs) {
+        b.x0 = U(rng) * (W - 1);
+        b.y0 = U(rng) * (H - 1);
+        const double sp = (0.5 + 1.5 * U(rng)) * 1e-3;     // px per microsecond
+        const double an = 2.0 * M_PI * U(rng);
+        b.vx = sp * std::cos(an);
+        b.vy = sp * std::sin(an);
+    }
+    auto reflect = [](double v, double hi) {
+        const double per = 2.0 * hi;
+        double m = std::fmod(v, per);
+        if (m < 0) m += per;
+        return m > hi ? per - m : m;
+    };
+    double next = (double)mono_ns();
+    float t_us = 0.f;
+    while (P->synth_on.load(std::memory_order_relaxed)) {
+        if (period_ns > 0) {
+            while ((double)mono_ns() < next) cpu_relax();
+            next += period_ns;
+        }
+        t_us += dt_us;
+        float x, y, p;
+        if (blobs.empty()) {
+            const std::uint64_t r = next_u64();
+            x = (float)(int)(r % (std::uint64_t)W);
+            y = (float)(int)((r >> 16) % (std::uint64_t)H);
+            p = (float)((r >> 32) & 1ull);
+        } else {
+            double fx, fy;
+            if (U(rng) < bg_frac) {
+                fx = std::floor(U(rng) * W);
+                fy = std::floor(U(rng) * H);
+            } else {
+                const Blob& b = blobs[(std::size_t)(U(rng) * blobs.size()) % blobs.size()];
+                fx = std::rint(reflect(b.x0 + b.vx * t_us, W - 1) + sigma * N01(rng));
+                fy = std::rint(reflect(b.y0 + b.vy * t_us, H - 1) + sigma * N01(rng));
+            }
+            x = (float)std::min<double>(W - 1, std::max(0.0, fx));
+            y = (float)std::min<double>(H - 1, std::max(0.0, fy));
+            p = U(rng) < 0.5 ? -1.f : 1.f;
+        }
+        P->route(t_us, x, y, p, mono_ns());
+        P->synth_n.fetch_add(1, std::memory_order_relaxed);
+    }
+}
+
+[[maybe_unused]] void start_synth(Producer* P, double rate, int core, std::uint64_t seed, int n_blobs, double sigma,
+                 double bg) {
+    if (!P || P->synth_on.load()) return;
+    if (P->synth.joinable()) P->synth.join();
+    P->synth_n = 0;
+    P->synth_on = true;
+    P->synth = std::thread(synth_loop, P, rate, core, seed, n_blobs, sigma, bg);
+}
+
+}  // namespace
+}  // namespace ssla
+
+using ssla::Producer;
+
+#ifdef STAGE01_TO_GPU
+#include "stage01_to_gpu.h"
+
+struct S01gHandle : Producer {};
+
+extern "C" {
+
+S01gHandle* s01g_init_full(const char* dir, int n_shards, int halo, int base_core, int sample_cap,
+                           unsigned int shard_ring_cap) {
+    return static_cast<S01gHandle*>(
+        ssla::make_producer(dir, n_shards, halo, base_core, sample_cap, shard_ring_cap, true, "s01g_init"));
+}
+
+S01gHandle* s01g_init(const char* dir, int n_shards, int halo, int base_core, int sample_cap) {
+    return s01g_init_full(dir, n_shards, halo, base_core, sample_cap, 1u << 16);
+}
+
+void s01g_attach_gpu_rings_multi(S01gHandle* h, int n, void* const* bufs, void* const* heads,
+                                 unsigned long long mask, int W2, int H2, const int* xlo,
+                                 const int* xhi, const int* ylo, const int* yhi) {
+    if (!h || n <= 0 || n > ssla::kMaxRings || !bufs || !heads || !xlo || !xhi || !ylo || !yhi) return;
+    h->attached.store(false, std::memory_order_release);
+    for (int b = 0; b < n; ++b) {
+        ssla::RingOut& r = h->rings[b];
+        r.buf = static_cast<HybridInputRec*>(bufs[b]);
+        r.head = static_cast<std::uint64_t*>(heads[b]);
+        r.x_lo = xlo[b];
+        r.x_hi = xhi[b];
+        r.y_lo = ylo[b];
+        r.y_hi = yhi[b];
+        r.pushed = 0;
+    }
+    h->n_rings = n;
+    h->ring_mask = mask;
+    h->W2 = W2;
+    h->H2 = H2;
+    h->attached.store(true, std::memory_order_release);
+}
+
+void s01g_attach_gpu_rings(S01gHandle* h, void* buf0, void* head0, void* buf1, void* head1,
+                           unsigned long long mask, int W2, int H2, int lo0, int hi0, int lo1,
+                           int hi1) {
+    void* bufs[2] = {buf0, buf1};
+    void* heads[2] = {head0, head1};
+    const int xlo[2] = {lo0, lo1}, xhi[2] = {hi0, hi1}, ylo[2] = {0, 0}, yhi[2] = {H2, H2};
+    s01g_attach_gpu_rings_multi(h, 2, bufs, heads, mask, W2, H2, xlo, xhi, ylo, yhi);
+}
+
+int s01g_submit_batch(S01gHandle* h, const float* ev, int n) { return ssla::submit(h, ev, n); }
+
+void s01g_snapshot_stats(S01gHandle* h, double* out) {
+    if (!out) return;
+    if (!h) {
+        for (int i = 0; i < 32; ++i) out[i] = 0.0;
+        return;
+    }
+    h->snapshot(out, 32);
+}
+
+void s01g_reset_stats(S01gHandle* h) {
+    if (h) h->reset_stats();
+}
+
+void s01g_shutdown(S01gHandle* h) {
+    if (!h) return;
+    h->shutdown();
+    delete h;
+}
+
+void s01g_start_synthetic(S01gHandle* h, double rate_mev, int pin_core, unsigned long long seed) {
+    ssla::start_synth(h, rate_mev, pin_core, seed, 0, 0.0, 1.0);
+}
+
+void s01g_start_synthetic_blobs(S01gHandle* h, double rate_mev, int pin_core,
+                                unsigned long long seed, int n_blobs, double sigma_px,
+                                double bg_frac) {
+    ssla::start_synth(h, rate_mev, pin_core, seed, n_blobs < 1 ? 1 : n_blobs, sigma_px, bg_frac);
+}
+
+void s01g_stop_synthetic(S01gHandle* h) {
+    if (h) h->stop_synth();
+}
+
+unsigned long long s01g_synthetic_n_pushed(S01gHandle* h) {
+    return h ? h->synth_n.load() : 0ull;
+}
+
+}  // extern "C"
+
+#else
+#include "stage01_capi.h"
+
+struct S0Handle : Producer {};
+
+extern "C" {
+
+S0Handle* s0_init(const char* dir, int n_shards, int halo, int base_core, int sample_cap) {
+    return static_cast<S0Handle*>(
+        ssla::make_producer(dir, n_shards, halo, base_core, sample_cap, 1u << 16, false, "s0_init"));
+}
+
+int s0_submit_batch(S0Handle* h, const float* ev, int n) { return ssla::submit(h, ev, n); }
+
+void s0_snapshot_stats(S0Handle* h, double* out) {
+    if (!out) return;
+    if (!h) {
+        for (int i = 0; i < 16; ++i) out[i] = 0.0;
+        return;
+    }
+    h->snapshot(out, 14);
+    out[14] = out[15] = 0.0;
+}
+
+void s0_reset_stats(S0Handle* h) {
+    if (h) h->reset_stats();
+}
+
+void s0_shutdown(S0Handle* h) {
+    if (!h) return;
+    h->shutdown();
+    delete h;
+}
+
+}  // extern "C"
+#endif

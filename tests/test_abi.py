@@ -1,4 +1,4 @@
-"""The C ABI library loads without a GPU, exports every entry point that
+"""The C ABI libraries load without a GPU, export every entry point that
 include/*.h declares, and its struct layouts match the reference contracts
 (HybridInputRec 128 B, HybridS2S3Config 4616 B with preds at 3968,
 HybridS2S3OutputSlot 392 B, GpuTimingSlot 40 B).  No compute call here."""
@@ -11,10 +11,24 @@ from ssla_hip import abi, lib
 ROOT = Path(__file__).resolve().parent.parent
 
 
-def declared(header: str):
+def declared(header: str, prefix: str = "ssla_hip_"):
     text = (ROOT / "include" / header).read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ssla_hip_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(" + prefix + r"\w+)\s*\(", text)))
+
+
+def test_producer_libraries_export_every_declared_symbol():
+    from ssla_hip import producer
+    g = producer.load_to_gpu()
+    names = declared("stage01_to_gpu.h", "s01g_")
+    assert len(names) == 12 and sorted(producer.EXPORTED_TO_GPU) == names
+    for n in names:
+        assert hasattr(g, n), n
+    c = producer.load_capi()
+    names = declared("stage01_capi.h", "s0_")
+    assert len(names) == 5 and sorted(producer.EXPORTED_CAPI) == names
+    for n in names:
+        assert hasattr(c, n), n
 
 
 def test_library_exports_every_declared_symbol():
