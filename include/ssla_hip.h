@@ -147,6 +147,14 @@ int ssla_hip_drain_n2(const HybridS2S3Config* cfg,
  * tdrop decisions), then for L4, L5, L6, L7 in turn: projection, per-cell
  * recurrence, gather + LayerNorm (1..12), 13 head, 14 output slots. */
 
+#define SSLA_BATCH_PHASES 32
+/* Slots of the in-kernel batch profile (batch-mode and live drains), summed
+ * over blocks: microseconds of 0 batch load, 1 tdrop s2, 2 s2 pairs,
+ * 3-6 L4 (projection, recurrence, contraction, LayerNorm), 7-10 L5,
+ * 11 pool + tdrop s3, 12 s3 pairs, 13-16 L6, 17-20 L7, 21 head hidden,
+ * 22 head outputs, 23 prediction grid, 24 outputs / publish; then counts:
+ * 25 batches, 26 records; 27-31 unused. */
+
 typedef struct SslaHipDrainOpts {
     void*         stream;      /* hipStream_t; NULL = default stream */
     int           sync;        /* nonzero: wait for completion */
@@ -158,6 +166,9 @@ typedef struct SslaHipDrainOpts {
     float*        phase_ms;    /* NULL or host float[SSLA_DRAIN_PHASES]:
                                   adds the GPU time of each phase, measured
                                   with HIP events on `stream` (needs sync) */
+    double*       batch_phase_us; /* NULL or host double[SSLA_BATCH_PHASES]:
+                                  batch mode only (needs sync); adds the
+                                  in-kernel wall-clock profile */
 } SslaHipDrainOpts;
 
 int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg,
@@ -195,6 +206,8 @@ typedef struct SslaHipLive SslaHipLive;
 typedef struct SslaHipLiveOpts {
     int          max_batch;        /* 1..32; default 32 */
     unsigned int idle_timeout_ms;  /* default 30000 */
+    double*      phase_us;         /* NULL or host double[SSLA_BATCH_PHASES]:
+                                      filled (added to) by persistent_wait */
 } SslaHipLiveOpts;
 
 int ssla_hip_persistent_start(const HybridS2S3Config* cfg,

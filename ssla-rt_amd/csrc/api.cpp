@@ -496,10 +496,12 @@ int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg, const HybridInputRec* const
     float* phase_ms = opts ? opts->phase_ms : nullptr;
     if (phase_ms && !sync) { set_error("phase_ms needs sync"); return SSLA_ERR_ARG; }
     const int batch = opts ? opts->batch : 0;
+    double* bph = opts ? opts->batch_phase_us : nullptr;
     if (batch != 0) {
         if (phase_ms) { set_error("phase_ms is only measured by the whole-ring drain"); return SSLA_ERR_ARG; }
-        return batch_drain(cfg, rings, ns, outs, opts->head_outs, nullptr, batch, st, sync);
+        return batch_drain(cfg, rings, ns, outs, opts->head_outs, nullptr, batch, st, sync, bph);
     }
+    if (bph) { set_error("batch_phase_us is only measured by the batch-mode drain"); return SSLA_ERR_ARG; }
     return scan_drain(cfg, rings, ns, outs, opts ? opts->head_outs : nullptr, st, sync, phase_ms);
 }
 
@@ -509,7 +511,7 @@ int ssla_hip_drain_n(const HybridS2S3Config* cfg, const HybridInputRec* const* r
     if (!cfg || !rings || !ns) { set_error("null argument"); return SSLA_ERR_ARG; }
     if (batch_clks) {
         // the reference's drain_n batching: 8 records per batch, clock pairs
-        return batch_drain(cfg, rings, ns, outs, nullptr, batch_clks, 8, nullptr, true);
+        return batch_drain(cfg, rings, ns, outs, nullptr, batch_clks, 8, nullptr, true, nullptr);
     }
     SslaHipDrainOpts o{};
     o.sync = 1;
@@ -575,7 +577,7 @@ int ssla_hip_persistent_start(const HybridS2S3Config* cfg, HybridInputRec* const
     const unsigned idle = (opts && opts->idle_timeout_ms) ? opts->idle_timeout_ms : 30000u;
     LiveSession* s = nullptr;
     const int rc = live_start(cfg, rings, ring_mask, tails, stop_flag, events_done, spin_ns,
-                              max_batch, idle, &s);
+                              max_batch, idle, opts ? opts->phase_us : nullptr, &s);
     *out = reinterpret_cast<SslaHipLive*>(s);
     return rc;
 }

@@ -16,17 +16,19 @@ void set_error(const std::string& msg);
 
 // Drains pre-filled rings in batches of `batch` records (ring order), one
 // workgroup per block; batch_clks[b] (optional) receives a (t_pop, t_done)
-// wall-clock pair per batch.
+// wall-clock pair per batch; phase_us (optional, needs sync) accumulates the
+// in-kernel phase profile (SSLA_BATCH_PHASES slots).
 int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings, const int* ns,
                 HybridS2S3OutputSlot* const* outs, float* const* head_outs,
-                unsigned long long* const* batch_clks, int batch, hipStream_t st, bool sync);
+                unsigned long long* const* batch_clks, int batch, hipStream_t st, bool sync,
+                double* phase_us);
 
 struct LiveSession;
 
 int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
                unsigned long long ring_mask, unsigned long long* const* tails, int* stop_flag,
                unsigned long long* const* events_done, unsigned int spin_ns, int max_batch,
-               unsigned int idle_timeout_ms, LiveSession** out);
+               unsigned int idle_timeout_ms, double* phase_us, LiveSession** out);
 
 // Waits until the kernel has exited (after the caller set *stop_flag) and
 // frees the session; *status_out: 0 stopped by flag, 2 ring overrun,

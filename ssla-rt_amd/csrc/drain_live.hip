@@ -3,27 +3,36 @@
 //
 // One 512-thread workgroup owns one stream (block): its hidden state, tdrop
 // counters, ring and outputs.  Records are taken in batches of up to 32 in
-// ring order, and each batch runs the same decomposition as the whole-ring
-// drain, inside the workgroup:
+// ring order; each batch runs the reference's per-event schedule as a few
+// workgroup-wide phases per layer:
 //   tdrop   one wave, one lane per record: arrival rank among the batch's
 //           records at the same cell (ssla_ref.py:190-195)
-//   pairs   one wave builds the (record, delta) pairs in record order, the
-//           per-delta record lists, and per-cell successor links
-//   P       q, v, g rows, grouped by delta so each weight matrix streams
-//           through the CU once per batch (rows in a per-stream L2 scratch)
+//   pairs   one wave builds the (record, delta) pairs in record order and the
+//           per-delta record lists; one thread per pair finds the next pair
+//           at its cell among the later records' patches
+//   P       q, v, g: one thread per weight column (delta, channel) reads
+//           the column in chunks of up to 48 weights held in registers and
+//           applies each chunk to eight records at a time; v and g for every
+//           pair, q only for the pairs of the layer's output records
 //   S       one lane per (cell, channel) walks the cell's pairs in record
-//           order: h = sigmoid(g) h + v, q*h where the output is consumed
-//   O       one thread per (channel, record group): goW contraction over
-//           the record's pairs + residual, then fp64 LayerNorm per wave
+//           order, loading eight pairs' g, v (and q) before the eight
+//           dependent steps h = sigmoid(g) h + v; q*h where it is consumed
+//   O       one thread per goW column (delta, channel) and residual column
+//           over chunks of eight output records whose q*h rows
+//           are staged in LDS; per-delta partial sums are reduced in delta
+//           order, then fp64 LayerNorm, one wave per record
 // The masks are the reference's (...celled.cuh:1027-1064): L4 all, L5 state
 // for all / output for pass2, L6 pass2, L7 state for pass2 / output for
-// pass3, head for owned pass3 records.
+// pass3, head for owned pass3 records.  L4/L5 share one pair set, L6/L7
+// another.
 //
 // The live kernel polls a ring in fine-grained host memory: one wave loads
-// 64 consecutive seq_done tags with system-scope acquire (one PCIe round
-// trip) and takes the ready prefix.  It stops on the host's stop flag, on a
-// ring overrun, or after an idle timeout on the constant-rate wall clock, so
-// every wave always reaches an exit.
+// 64 consecutive seq_done tags and takes the ready prefix.  It stops on the
+// host's stop flag, on a ring overrun, or after an idle timeout on the
+// constant-rate wall clock, so every wave always reaches an exit.
+//
+// With a profile buffer attached, thread 0 adds the wall-clock time of each
+// phase (after its closing barrier) to one of SSLA_BATCH_PHASES slots.
 #include <hip/hip_runtime.h>
 
 #include <chrono>
@@ -56,7 +65,7 @@ struct LiveDesc {
     float* hidden[4];
     unsigned char* td2;
     unsigned char* td3;
-    float* scratch;                     // (LP + 1) rows of 3*96 floats; last row zero
+    float* scratch;                     // LP rows of 3*96 floats
     HybridS2S3OutputSlot* out;          // batch mode
     float* head_out;                    // batch mode
     unsigned long long* batch_clk;      // batch mode
@@ -67,6 +76,7 @@ struct LiveDesc {
     unsigned int pad1;
     unsigned long long* kstart;
     unsigned long long* kend;
+    unsigned long long* prof;           // SSLA_BATCH_PHASES sums, or null
     HybridStrip strip;
 };
 
@@ -77,26 +87,53 @@ constexpr int LT = 512;             // threads per workgroup
 constexpr int NW = LT / 64;         // waves per workgroup
 constexpr int LP = kPatch * LB;     // pairs per layer, at most
 constexpr int NCMAX = 3 * SSLA_C3;  // widest pair row
-constexpr int kWB = 24;             // weights held in registers per block (divides 24, 48, 96)
+constexpr int OCH = 8;              // output records per contraction chunk
+constexpr int NPROF = SSLA_BATCH_PHASES;
 
-struct Lds {
-    float X[LB][SSLA_C3];           // layer input (becomes the layer output)
-    float Y[LB][SSLA_C3];           // pre-LayerNorm sums / head cls hidden
-    float R[LB][SSLA_C3];           // head reg hidden
-    float H7[LB][8];
-    double stat[LB][2];
-    unsigned long long tpush[LB], temit[LB];
-    int ex[LB], ey[LB];             // coordinates at the current level
-    int c2[LB], c3[LB];             // s2 / s3 centre cell, -1 when absent
-    unsigned char vld[LB], own[LB], p2[LB], p3[LB];
-    int pidx[LB][kPatch];           // pair of (record, delta), or -1
-    int pe[LP], pc[LP], pnext[LP], lead[LP];
-    int dcnt[kPatch];
-    int dev[kPatch][LB];
-    int dpos[LB][kPatch];           // position of (record, delta) in dev[delta]
-    int npair, nlead, bsize, flag;
-    unsigned long long seq0, t_pop;
+// profile slots (order of SSLA_BATCH_PHASES)
+enum {
+    PF_LOAD = 0, PF_TD2, PF_PAIRS2, PF_L4, PF_L5 = PF_L4 + 4, PF_TD3 = PF_L5 + 4, PF_PAIRS3,
+    PF_L6, PF_L7 = PF_L6 + 4, PF_HEADH = PF_L7 + 4, PF_HEADO, PF_PREDS, PF_PUBLISH,
+    PF_BATCHES, PF_RECORDS
 };
+static_assert(PF_RECORDS < NPROF, "profile slots");
+
+struct alignas(16) Lds {
+    float X[LB][SSLA_C3];                // layer input (becomes the layer output)
+    float Y[LB][SSLA_C3];                // pre-LayerNorm sums / head cls hidden
+    float R[LB][SSLA_C3];                // head reg hidden
+    float QH[OCH][kPatch][SSLA_C3];      // q*h rows of one output chunk
+    float PB[kPatch + 1][OCH][SSLA_C3];  // per-delta partial sums (+ residual)
+    float H7[LB][8];
+    unsigned long long tpush[LB], temit[LB];
+    int ex[LB], ey[LB];                  // coordinates at the current level
+    int c2[LB], c3[LB];                  // s2 / s3 centre cell, -1 when absent
+    unsigned char vld[LB], own[LB], p2[LB], p3[LB];
+    int pidx[LB][kPatch];                // pair of (record, delta), or -1
+    int pe[LP], pc[LP], pnext[LP], lead[LP];
+    unsigned pk[LB];                     // x | y << 16 of records in the pair set, else ~0
+    int dcnt[kPatch], dcnto[kPatch];
+    int dev[kPatch][LB];                 // records with a pair at delta
+    int devo[kPatch][LB];                // ... that are output records of the layer
+    int ol[LB];                          // output records of the current layer
+    int npair, nlead, nout, bsize, flag, prof_on;
+    unsigned long long t_pop, tprev;
+    unsigned long long prof[NPROF];
+};
+
+// The workgroup's working set.  A namespace-scope LDS variable (rather than
+// a parameter) keeps its address space and 16-byte alignment visible inside
+// the per-batch function that both kernels call, so row reads compile to
+// ds_read_b128.
+__shared__ Lds g_lds;
+
+__device__ __forceinline__ void mark(Lds& S, int slot) {
+    if (S.prof_on && threadIdx.x == 0) {
+        const unsigned long long t = (unsigned long long)wall_clock64();
+        S.prof[slot] += t - S.tprev;
+        S.tprev = t;
+    }
+}
 
 __device__ __forceinline__ double wave_sum(double v) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -108,10 +145,57 @@ __device__ __forceinline__ float wave_sumf(float v) {
     return v;
 }
 
+// Global-memory accesses through address-space-1 pointers: the state,
+// scratch and weight pointers reach the per-batch code as generic pointers
+// loaded from the block table, which would otherwise compile to flat
+// instructions that also wait on the LDS counter.
+#define SSLA_GLOBAL __attribute__((address_space(1)))
+__device__ __forceinline__ float gload(const float* p) {
+    return *(const SSLA_GLOBAL float*)p;
+}
+__device__ __forceinline__ void gstore(float* p, float v) {
+    *(SSLA_GLOBAL float*)p = v;
+}
+
+// A float4 of an LDS row: x is 16-byte aligned and `at` a multiple of 4.
+__device__ __forceinline__ float4 lds4(const float* x, int at) {
+    return reinterpret_cast<const float4*>(__builtin_assume_aligned(x, 16))[at >> 2];
+}
+
+__device__ __forceinline__ float dot4(const float* w, float4 x, float a) {
+    a = fmaf(w[0], x.x, a);
+    a = fmaf(w[1], x.y, a);
+    a = fmaf(w[2], x.z, a);
+    return fmaf(w[3], x.w, a);
+}
+
+// acc[r] += sum_{i<K} w[i * ws] * x[off[r] + i] for eight rows of an LDS
+// array x: the weight column is read in chunks of 24 or 32 values, each
+// chunk's loads issued together and reused by the eight rows.
+template <int K>
+__device__ __forceinline__ void coldot8(const float* __restrict__ w, int ws, const float* x,
+                                        const int* off, float* acc) {
+    constexpr int KC = (K % 32 == 0) ? 32 : 24;
+    static_assert(K % KC == 0 && KC % 4 == 0, "column chunking");
+    #pragma nounroll
+    for (int k0 = 0; k0 < K; k0 += KC) {
+        float wr[KC];
+        #pragma unroll
+        for (int i = 0; i < KC; ++i) wr[i] = gload(w + (size_t)(k0 + i) * ws);
+        #pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            float a = acc[r];
+            #pragma unroll
+            for (int i = 0; i < KC; i += 4) a = dot4(wr + i, lds4(x, off[r] + k0 + i), a);
+            acc[r] = a;
+        }
+    }
+}
+
 // Arrival-rank tdrop for one batch (wave 0; lane = record).  All lanes read
 // the counter in one load before the last record of each cell stores the
 // advanced value.
-__device__ void batch_tdrop(Lds& S, int B, unsigned char* td, const int* cell,
+__device__ __forceinline__ void batch_tdrop(Lds& S, int B, unsigned char* td, const int* cell,
                             const unsigned char* mask, unsigned char* pass, int window) {
     if (threadIdx.x >= 64) return;
     const int e = threadIdx.x;
@@ -135,16 +219,11 @@ __device__ void batch_tdrop(Lds& S, int B, unsigned char* td, const int* cell,
     if (last) td[c] = (unsigned char)((cnt + (unsigned)rank + 1u) & 255u);
 }
 
-// One layer over the records of `set`, output for the records of `outm`
-// (nullptr = every record of the set).  Reads S.X, leaves the LayerNormed
-// output in S.X for output records.  Hl x Wl is the level's grid.
-template <int IN, int OUT>
-__device__ void batch_layer(Lds& S, int B, const unsigned char* set, const unsigned char* outm,
-                            const LayerWeightsS2S3& L, float* __restrict__ hidden,
-                            float* __restrict__ scratch, int Hl, int Wl) {
-    constexpr int NC = 3 * OUT;
+// (record, delta) pairs of the records in `set` on an Hl x Wl grid, in
+// record order; per-delta record lists; successor links and one leader per
+// cell.  Ends with a barrier.
+__device__ __forceinline__ void build_pairs(Lds& S, int B, const unsigned char* set, int Hl, int Wl) {
     const int tid = threadIdx.x;
-    // ---- pairs, per-delta lists (wave 0) ---------------------------------
     if (tid < 64) {
         const int e = tid;
         const bool in = e < B && set[e];
@@ -181,228 +260,263 @@ __device__ void batch_layer(Lds& S, int B, const unsigned char* set, const unsig
         for (int d = 0; d < kPatch; ++d) {
             const bool has = (bits >> d) & 1u;
             const unsigned long long bal = __ballot(has);
-            const int at = __popcll(bal & lt);
-            if (has) S.dev[d][at] = e;
-            if (e < LB) S.dpos[e][d] = has ? at : -1;
+            if (has) S.dev[d][__popcll(bal & lt)] = e;
             if (e == 0) S.dcnt[d] = __popcll(bal);
         }
         const int total = __shfl(incl, 63, 64);
+        if (e < LB) S.pk[e] = in ? ((unsigned)S.ex[e] | ((unsigned)S.ey[e] << 16)) : 0xffffffffu;
         if (e == 0) {
             S.npair = total;
             S.nlead = 0;
         }
     }
     __syncthreads();
-    // ---- successor links and one leader per cell -----------------------------
+    // Links: the pair after p at p's cell belongs to the first later record
+    // of the set whose 3x3 patch holds the cell; p leads its cell when no
+    // earlier record's patch does.  O(B) per pair.
     const int np = S.npair;
     for (int p = tid; p < np; p += LT) {
-        const int c = S.pc[p];
+        const int e = S.pe[p], c = S.pc[p];
+        const int ty = c / Wl, tx = c - ty * Wl;
         int nx = -1;
-        for (int q = p + 1; q < np; ++q)
-            if (S.pc[q] == c) { nx = q; break; }
-        S.pnext[p] = nx;
         bool lead = true;
-        for (int q = 0; q < p; ++q)
-            if (S.pc[q] == c) { lead = false; break; }
+        for (int j = 0; j < B; ++j) {
+            const unsigned k = S.pk[j];
+            const int dx = tx - (int)(k & 0xffffu), dy = ty - (int)(k >> 16);
+            if (k == 0xffffffffu || dx < -1 || dx > 1 || dy < -1 || dy > 1) continue;
+            if (j < e) lead = false;
+            else if (j > e && nx < 0) nx = S.pidx[j][(1 - dy) * 3 + (1 - dx)];
+        }
+        S.pnext[p] = nx;
         if (lead) S.lead[atomicAdd(&S.nlead, 1)] = p;
-    }
-    __syncthreads();
-    // ---- P: q, v, g rows, delta by delta --------------------------------------
-    {
-        constexpr int G = LT / NC;          // record groups sharing a column
-        const int c = tid % NC, g = tid / NC;
-        if (g < G) {
-            for (int d = 0; d < kPatch; ++d) {
-                const int n = S.dcnt[d];
-                if (n <= g * 8) continue;
-                const float* w = L.qvgIn + (size_t)d * IN * NC + c;
-                for (int r0 = g * 8; r0 < n; r0 += G * 8) {
-                    int ev[8];
-                    #pragma unroll
-                    for (int rr = 0; rr < 8; ++rr) ev[rr] = (r0 + rr < n) ? S.dev[d][r0 + rr] : 0;
-                    float acc[8];
-                    #pragma unroll
-                    for (int rr = 0; rr < 8; ++rr) acc[rr] = 0.f;
-                    // 24 weights of the column in flight per block of the input
-                    for (int i0 = 0; i0 < IN; i0 += kWB) {
-                        float wr[kWB];
-                        #pragma unroll
-                        for (int i = 0; i < kWB; ++i) wr[i] = w[(size_t)(i0 + i) * NC];
-                        #pragma unroll
-                        for (int i = 0; i < kWB; ++i) {
-                            #pragma unroll
-                            for (int rr = 0; rr < 8; ++rr) acc[rr] = fmaf(wr[i], S.X[ev[rr]][i0 + i], acc[rr]);
-                        }
-                    }
-                    #pragma unroll
-                    for (int rr = 0; rr < 8; ++rr)
-                        if (r0 + rr < n) scratch[(size_t)S.pidx[ev[rr]][d] * NC + c] = acc[rr];
-                }
-            }
-        }
-    }
-    __syncthreads();
-    // ---- S: per-cell recurrence in record order -------------------------------
-    const int nl = S.nlead;
-    for (int t = tid; t < nl * OUT; t += LT) {
-        const int k = t / OUT, ch = t % OUT;
-        const int p0 = S.lead[k];
-        float* hp = hidden + (size_t)S.pc[p0] * OUT + ch;
-        float h = *hp;
-        for (int q = p0; q >= 0; q = S.pnext[q]) {
-            float* row = scratch + (size_t)q * NC;
-            h = fmaf(sigmoid_fast(row[2 * OUT + ch]), h, row[OUT + ch]);
-            if (outm == nullptr || outm[S.pe[q]]) row[ch] *= h;
-        }
-        *hp = h;
-    }
-    __syncthreads();
-    // ---- O: goW contraction + residual ------------------------------------------
-    // Per delta: the q*h rows of the records with a pair there are staged in
-    // LDS (S.R), the delta's goW column sits in registers, and each thread
-    // accumulates its channel for its records.
-    {
-        constexpr int GO = LT / OUT;
-        constexpr int KE = (LB + GO - 1) / GO;
-        const int o = tid % OUT, g = tid / OUT;
-        int ev[KE];
-        bool on[KE];
-        float acc[KE];
-        #pragma unroll
-        for (int k = 0; k < KE; ++k) {
-            const int e = g + k * GO;
-            on[k] = g < GO && e < B && set[e] && (outm == nullptr || outm[e]);
-            ev[k] = on[k] ? e : 0;
-            acc[k] = 0.f;
-        }
-        for (int d = 0; d < kPatch; ++d) {
-            const int n = S.dcnt[d];
-            if (n == 0) continue;
-            for (int t = tid; t < n * OUT; t += LT) {
-                const int k = t / OUT, i = t % OUT;
-                S.R[k][i] = scratch[(size_t)S.pidx[S.dev[d][k]][d] * NC + i];
-            }
-            __syncthreads();
-            if (g < GO) {
-                const float* w = L.goW + (size_t)d * OUT * OUT + o;
-                int pos[KE];
-                #pragma unroll
-                for (int k = 0; k < KE; ++k) pos[k] = on[k] ? S.dpos[ev[k]][d] : -1;
-                for (int i0 = 0; i0 < OUT; i0 += kWB) {
-                    float wr[kWB];
-                    #pragma unroll
-                    for (int i = 0; i < kWB; ++i) wr[i] = w[(size_t)(i0 + i) * OUT];
-                    #pragma unroll
-                    for (int k = 0; k < KE; ++k) {
-                        if (pos[k] < 0) continue;
-                        float a = acc[k];
-                        #pragma unroll
-                        for (int i = 0; i < kWB; ++i) a = fmaf(wr[i], S.R[pos[k]][i0 + i], a);
-                        acc[k] = a;
-                    }
-                }
-            }
-            __syncthreads();
-        }
-        if (g < GO) {
-            if (L.input_proj) {
-                for (int i0 = 0; i0 < IN; i0 += kWB) {
-                    float wr[kWB];
-                    #pragma unroll
-                    for (int i = 0; i < kWB; ++i) wr[i] = L.input_proj[(size_t)(i0 + i) * OUT + o];
-                    #pragma unroll
-                    for (int i = 0; i < kWB; ++i) {
-                        #pragma unroll
-                        for (int k = 0; k < KE; ++k) acc[k] = fmaf(wr[i], S.X[ev[k]][i0 + i], acc[k]);
-                    }
-                }
-            } else {
-                #pragma unroll
-                for (int k = 0; k < KE; ++k) acc[k] += S.X[ev[k]][o];
-            }
-            #pragma unroll
-            for (int k = 0; k < KE; ++k)
-                if (on[k]) S.Y[ev[k]][o] = acc[k];
-        }
-    }
-    __syncthreads();
-    // ---- fp64 LayerNorm, one wave per record ----------------------------------------
-    {
-        const int wv = tid >> 6, lane = tid & 63;
-        for (int e = wv; e < B; e += NW) {
-            if (!(set[e] && (outm == nullptr || outm[e]))) continue;
-            const float a = lane < OUT ? S.Y[e][lane] : 0.f;
-            const float b = lane + 64 < OUT ? S.Y[e][lane + 64] : 0.f;
-            const double mean = wave_sum((double)a + (double)b) / (double)OUT;
-            const double da = lane < OUT ? (double)a - mean : 0.0;
-            const double db = lane + 64 < OUT ? (double)b - mean : 0.0;
-            const double var = wave_sum(da * da + db * db) / (double)OUT;
-            const double inv = 1.0 / sqrt(var + 1e-5);
-            if (lane < OUT)
-                S.X[e][lane] = (float)(da * inv * (double)L.ln_gamma[lane] + (double)L.ln_beta[lane]);
-            if (lane + 64 < OUT)
-                S.X[e][lane + 64] = (float)(db * inv * (double)L.ln_gamma[lane + 64] + (double)L.ln_beta[lane + 64]);
-        }
     }
     __syncthreads();
 }
 
-// Records [0, B) are in S (X rows, coordinates, ownership).  Runs both
-// stages, the tdrop gates and the head; leaves L7 outputs in S.X and head
-// rows in S.H7.
-__device__ void process_batch(Lds& S, int B, const LiveDesc& d, const LiveWeights& W,
-                              const Geometry& G) {
+// P: scratch[pair][0, 3*OUT) = [q | v | g] of the pair's (record, delta).
+// v and g columns run over every pair at delta; q columns only over the
+// pairs of output records (S.devo), the only ones whose q is consumed.
+template <int IN, int OUT>
+__device__ __forceinline__ void phase_proj(Lds& S, const float* __restrict__ qvgIn,
+                                           float* __restrict__ scratch) {
+    constexpr int NC = 3 * OUT;
+    for (int u = threadIdx.x; u < kPatch * NC; u += LT) {
+        const int d = u / NC, c = u - d * NC;
+        const bool qcol = c < OUT;
+        const int n = qcol ? S.dcnto[d] : S.dcnt[d];
+        if (n == 0) continue;
+        const int* list = qcol ? S.devo[d] : S.dev[d];
+        const float* w = qvgIn + (size_t)d * IN * NC + c;
+        for (int k0 = 0; k0 < n; k0 += 8) {
+            int off[8];
+            float acc[8];
+            #pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                off[r] = list[min(k0 + r, n - 1)] * SSLA_C3;
+                acc[r] = 0.f;
+            }
+            coldot8<IN>(w, NC, &S.X[0][0], off, acc);
+            #pragma unroll
+            for (int r = 0; r < 8; ++r)
+                if (k0 + r < n) gstore(scratch + (size_t)S.pidx[list[k0 + r]][d] * NC + c, acc[r]);
+        }
+    }
+}
+
+// S: the per-cell recurrence in record order; q*h replaces q for pairs of
+// output records (outm == nullptr: every record of the set).
+template <int OUT>
+__device__ __forceinline__ void phase_recur(Lds& S, float* __restrict__ hidden,
+                                            float* __restrict__ scratch, const unsigned char* outm) {
+    constexpr int NC = 3 * OUT;
+    constexpr int CH = 8;
+    const int nl = S.nlead;
+    for (int t = threadIdx.x; t < nl * OUT; t += LT) {
+        const int k = t / OUT, ch = t - k * OUT;
+        int q = S.lead[k];
+        float* hp = hidden + (size_t)S.pc[q] * OUT + ch;
+        float h = gload(hp);
+        while (q >= 0) {
+            int qs[CH];
+            #pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                qs[j] = q;
+                if (q >= 0) q = S.pnext[q];
+            }
+            float gv[CH], vv[CH], qv[CH];
+            bool ov[CH];
+            #pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const int p = qs[j] < 0 ? 0 : qs[j];      // pair 0 exists: loads stay in bounds
+                const float* row = scratch + (size_t)p * NC;
+                ov[j] = qs[j] >= 0 && (outm == nullptr || outm[S.pe[p]]);
+                gv[j] = gload(row + 2 * OUT + ch);
+                vv[j] = gload(row + OUT + ch);
+                qv[j] = gload(row + ch);
+            }
+            #pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                if (qs[j] >= 0) {
+                    h = fmaf(sigmoid_fast(gv[j]), h, vv[j]);
+                    if (ov[j]) gstore(scratch + (size_t)qs[j] * NC + ch, qv[j] * h);
+                }
+            }
+        }
+        gstore(hp, h);
+    }
+}
+
+// O: Y[e] = sum_delta goW[delta]^T qh(e, delta) + residual for the output
+// records S.ol[0, S.nout), in chunks of eight records: one thread per goW
+// column (delta, channel) and, with input_proj, per residual column; the
+// per-delta partial sums are added in delta order.
+template <int IN, int OUT>
+__device__ __forceinline__ void phase_out(Lds& S, const LayerWeightsS2S3& L,
+                                          const float* __restrict__ scratch) {
+    constexpr int NC = 3 * OUT;
     const int tid = threadIdx.x;
-    batch_tdrop(S, B, d.td2, S.c2, nullptr, S.p2, G.window);
-    __syncthreads();
-    batch_layer<SSLA_C1, SSLA_C2>(S, B, S.vld, nullptr, W.L[0], d.hidden[0], d.scratch, G.H2, G.W2);
-    batch_layer<SSLA_C2, SSLA_C2>(S, B, S.vld, S.p2, W.L[1], d.hidden[1], d.scratch, G.H2, G.W2);
-    if (tid < B) {                      // pool to s3
-        S.ex[tid] >>= 1;
-        S.ey[tid] >>= 1;
-        S.c3[tid] = S.vld[tid] ? S.ey[tid] * G.W3 + S.ex[tid] : -1;
+    const bool ip = L.input_proj != nullptr;
+    const int nu = kPatch * OUT + (ip ? OUT : 0);
+    const int no = S.nout;
+    for (int c0 = 0; c0 < no; c0 += OCH) {
+        const int m = min(OCH, no - c0);
+        for (int t = tid; t < m * kPatch * OUT; t += LT) {
+            const int r = t / (kPatch * OUT), rem = t - r * (kPatch * OUT);
+            const int dd = rem / OUT, i = rem - dd * OUT;
+            const int p = S.pidx[S.ol[c0 + r]][dd];
+            S.QH[r][dd][i] = p >= 0 ? gload(scratch + (size_t)p * NC + i) : 0.f;
+        }
+        __syncthreads();
+        for (int u = tid; u < nu; u += LT) {
+            const int d = u / OUT, j = u - d * OUT;
+            const bool live = d == kPatch || S.dcnto[d] > 0;
+            float acc[8];
+            #pragma unroll
+            for (int r = 0; r < 8; ++r) acc[r] = 0.f;
+            if (live) {
+                int off[8];
+                if (d < kPatch) {
+                    #pragma unroll
+                    for (int r = 0; r < 8; ++r) off[r] = (min(r, m - 1) * kPatch + d) * SSLA_C3;
+                    coldot8<OUT>(L.goW + (size_t)d * OUT * OUT + j, OUT, &S.QH[0][0][0], off, acc);
+                } else {
+                    #pragma unroll
+                    for (int r = 0; r < 8; ++r) off[r] = S.ol[c0 + min(r, m - 1)] * SSLA_C3;
+                    coldot8<IN>(L.input_proj + j, OUT, &S.X[0][0], off, acc);
+                }
+            }
+            #pragma unroll
+            for (int r = 0; r < 8; ++r)
+                if (r < m) S.PB[d][r][j] = acc[r];
+        }
+        __syncthreads();
+        for (int t = tid; t < m * OUT; t += LT) {
+            const int r = t / OUT, jj = t - r * OUT;
+            const int e = S.ol[c0 + r];
+            float a = 0.f;
+            #pragma unroll
+            for (int dd = 0; dd < kPatch; ++dd) a += S.PB[dd][r][jj];
+            S.Y[e][jj] = a + (ip ? S.PB[kPatch][r][jj] : S.X[e][jj]);
+        }
+        __syncthreads();
+    }
+}
+
+// One layer over the pairs built for `set`; output (LayerNormed, in S.X) for
+// the records of set and outm (outm == nullptr: all of set).
+template <int IN, int OUT>
+__device__ __forceinline__ void batch_layer(Lds& S, int B, const unsigned char* set, const unsigned char* outm,
+                            const LayerWeightsS2S3& L, float* __restrict__ hidden,
+                            float* __restrict__ scratch, int slot) {
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const bool o = tid < B && set[tid] && (outm == nullptr || outm[tid]);
+        const unsigned long long lt = (1ull << tid) - 1ull;
+        const unsigned long long bal = __ballot(o);
+        if (o) S.ol[__popcll(bal & lt)] = tid;
+        if (tid == 0) S.nout = __popcll(bal);
+        #pragma unroll
+        for (int d = 0; d < kPatch; ++d) {
+            const bool has = o && S.pidx[tid][d] >= 0;
+            const unsigned long long bd = __ballot(has);
+            if (has) S.devo[d][__popcll(bd & lt)] = tid;
+            if (tid == 0) S.dcnto[d] = __popcll(bd);
+        }
     }
     __syncthreads();
-    batch_tdrop(S, B, d.td3, S.c3, S.p2, S.p3, G.window);
+    phase_proj<IN, OUT>(S, L.qvgIn, scratch);
     __syncthreads();
-    batch_layer<SSLA_C2, SSLA_C3>(S, B, S.p2, nullptr, W.L[2], d.hidden[2], d.scratch, G.H3, G.W3);
-    batch_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], d.hidden[3], d.scratch, G.H3, G.W3);
-    if (!W.have_head) return;
-    // ---- head hidden layers: y = SiLU(W x + b) for both branches ----------------
-    {
-        constexpr int C = SSLA_C3;
-        constexpr int GO = LT / C;
-        const int o = tid % C, g = tid / C;
-        if (g < GO) {
-            for (int e = g; e < B; e += GO) {
-                if (!(S.own[e] && S.p3[e])) continue;
-                float a = W.head.cls_conv_b[o], b = W.head.reg_conv_b[o];
-                for (int i0 = 0; i0 < C; i0 += kWB) {
-                    float wa[kWB], wb[kWB];
-                    #pragma unroll
-                    for (int i = 0; i < kWB; ++i) {
-                        wa[i] = W.head.cls_conv_W[(size_t)(i0 + i) * C + o];
-                        wb[i] = W.head.reg_conv_W[(size_t)(i0 + i) * C + o];
-                    }
-                    #pragma unroll
-                    for (int i = 0; i < kWB; ++i) {
-                        a = fmaf(wa[i], S.X[e][i0 + i], a);
-                        b = fmaf(wb[i], S.X[e][i0 + i], b);
-                    }
-                }
-                S.Y[e][o] = a * sigmoid_fast(a);
-                S.R[e][o] = b * sigmoid_fast(b);
+    mark(S, slot + 0);
+    phase_recur<OUT>(S, hidden, scratch, outm);
+    __syncthreads();
+    mark(S, slot + 1);
+    phase_out<IN, OUT>(S, L, scratch);
+    mark(S, slot + 2);
+    // fp64 LayerNorm, one wave per output record
+    const int wv = tid >> 6, lane = tid & 63, no = S.nout;
+    for (int r = wv; r < no; r += NW) {
+        const int e = S.ol[r];
+        const float a = lane < OUT ? S.Y[e][lane] : 0.f;
+        const float b = lane + 64 < OUT ? S.Y[e][lane + 64] : 0.f;
+        const double mean = wave_sum((double)a + (double)b) / (double)OUT;
+        const double da = lane < OUT ? (double)a - mean : 0.0;
+        const double db = lane + 64 < OUT ? (double)b - mean : 0.0;
+        const double var = wave_sum(da * da + db * db) / (double)OUT;
+        const double inv = 1.0 / sqrt(var + 1e-5);
+        if (lane < OUT)
+            S.X[e][lane] = (float)(da * inv * (double)L.ln_gamma[lane] + (double)L.ln_beta[lane]);
+        if (lane + 64 < OUT)
+            S.X[e][lane + 64] = (float)(db * inv * (double)L.ln_gamma[lane + 64] + (double)L.ln_beta[lane + 64]);
+    }
+    __syncthreads();
+    mark(S, slot + 3);
+}
+
+// Head of the owned pass-3 records: hidden layers y = SiLU(W x + b) of both
+// branches (one thread per weight column), then the seven outputs
+// [reg0..3, obj, cls0, cls1] (one wave per record) and the prediction grid.
+__device__ __forceinline__ void batch_head(Lds& S, int B, const LiveDesc& d, const LiveWeights& W) {
+    constexpr int C = SSLA_C3;
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const bool o = tid < B && S.own[tid] && S.p3[tid];
+        const unsigned long long bal = __ballot(o);
+        if (o) S.ol[__popcll(bal & ((1ull << tid) - 1ull))] = tid;
+        if (tid == 0) S.nout = __popcll(bal);
+    }
+    __syncthreads();
+    const int nh = S.nout;
+    if (tid < 2 * C) {
+        const int br = tid / C, o = tid - br * C;
+        const float* Wc = (br == 0 ? W.head.cls_conv_W : W.head.reg_conv_W) + o;
+        const float bias = (br == 0 ? W.head.cls_conv_b : W.head.reg_conv_b)[o];
+        for (int r0 = 0; r0 < nh; r0 += 8) {
+            int off[8];
+            float acc[8];
+            #pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                off[r] = S.ol[min(r0 + r, nh - 1)] * SSLA_C3;
+                acc[r] = bias;
+            }
+            coldot8<C>(Wc, C, &S.X[0][0], off, acc);
+            #pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                if (r0 + r >= nh) break;
+                const int e = S.ol[r0 + r];
+                const float y = acc[r] * sigmoid_fast(acc[r]);
+                if (br == 0) S.Y[e][o] = y;
+                else S.R[e][o] = y;
             }
         }
     }
     __syncthreads();
-    // ---- head outputs [reg0..3, obj, cls0, cls1], one wave per record ------------
+    mark(S, PF_HEADH);
     {
         const int wv = tid >> 6, lane = tid & 63;
-        for (int e = wv; e < B; e += NW) {
-            if (!(S.own[e] && S.p3[e])) continue;
+        for (int r = wv; r < nh; r += NW) {
+            const int e = S.ol[r];
             float part[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            for (int i = lane; i < SSLA_C3; i += 64) {
+            for (int i = lane; i < C; i += 64) {
                 const float yr = S.R[e][i], yc = S.Y[e][i];
                 #pragma unroll
                 for (int k = 0; k < 4; ++k) part[k] = fmaf(W.head.reg_pred_W[(size_t)i * 4 + k], yr, part[k]);
@@ -422,7 +536,8 @@ __device__ void process_batch(Lds& S, int B, const LiveDesc& d, const LiveWeight
         }
     }
     __syncthreads();
-    // ---- prediction grid: last owned pass-3 record of each s3 cell writes --------
+    mark(S, PF_HEADO);
+    // prediction grid: the last owned pass-3 record of each s3 cell writes
     if (tid < B && S.own[tid] && S.p3[tid]) {
         const int e = tid, c = S.c3[e];
         int count = 0;
@@ -445,10 +560,53 @@ __device__ void process_batch(Lds& S, int B, const LiveDesc& d, const LiveWeight
         }
     }
     __syncthreads();
+    mark(S, PF_PREDS);
+}
+
+// Records [0, B) are in S (X rows, coordinates, ownership).  Runs both
+// stages, the tdrop gates and the head; leaves L7 outputs in S.X and head
+// rows in S.H7.
+__device__ __noinline__ void process_batch(int B, const LiveDesc& d, const LiveWeights& W,
+                                          const Geometry& G) {
+    Lds& S = g_lds;
+    const int tid = threadIdx.x;
+    batch_tdrop(S, B, d.td2, S.c2, nullptr, S.p2, G.window);
+    __syncthreads();
+    mark(S, PF_TD2);
+    build_pairs(S, B, S.vld, G.H2, G.W2);
+    mark(S, PF_PAIRS2);
+    batch_layer<SSLA_C1, SSLA_C2>(S, B, S.vld, nullptr, W.L[0], d.hidden[0], d.scratch, PF_L4);
+    batch_layer<SSLA_C2, SSLA_C2>(S, B, S.vld, S.p2, W.L[1], d.hidden[1], d.scratch, PF_L5);
+    if (tid < B) {                      // pool to s3
+        S.ex[tid] >>= 1;
+        S.ey[tid] >>= 1;
+        S.c3[tid] = S.vld[tid] ? S.ey[tid] * G.W3 + S.ex[tid] : -1;
+    }
+    __syncthreads();
+    batch_tdrop(S, B, d.td3, S.c3, S.p2, S.p3, G.window);
+    __syncthreads();
+    mark(S, PF_TD3);
+    build_pairs(S, B, S.p2, G.H3, G.W3);
+    mark(S, PF_PAIRS3);
+    batch_layer<SSLA_C2, SSLA_C3>(S, B, S.p2, nullptr, W.L[2], d.hidden[2], d.scratch, PF_L6);
+    batch_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], d.hidden[3], d.scratch, PF_L7);
+    if (W.have_head) batch_head(S, B, d, W);
+}
+
+__device__ __forceinline__ void prof_begin(Lds& S, const LiveDesc& d) {
+    if (threadIdx.x == 0) {
+        S.prof_on = d.prof != nullptr;
+        for (int k = 0; k < NPROF; ++k) S.prof[k] = 0;
+    }
+}
+
+__device__ __forceinline__ void prof_end(Lds& S, const LiveDesc& d) {
+    if (threadIdx.x == 0 && d.prof)
+        for (int k = 0; k < NPROF; ++k) d.prof[k] = S.prof[k];
 }
 
 // Loads B records starting at ring slot `first` (slots wrap with `mask`).
-__device__ void load_batch(Lds& S, int B, const HybridInputRec* ring, unsigned long long first,
+__device__ __forceinline__ void load_batch(Lds& S, int B, const HybridInputRec* ring, unsigned long long first,
                            unsigned long long mask, const HybridStrip& s, const Geometry& G) {
     const int tid = threadIdx.x;
     for (int t = tid; t < B * SSLA_C1; t += LT) {
@@ -471,21 +629,27 @@ __device__ void load_batch(Lds& S, int B, const HybridInputRec* ring, unsigned l
     }
 }
 
+
 // ---------------------------------------------------------------------------
 // batch-mode drain of pre-filled rings (one workgroup per block)
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(LT)
 k_batch_drain(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, int batch) {
-    __shared__ Lds S;
+    Lds& S = g_lds;
     const LiveDesc& d = ld[blockIdx.x];
     const int tid = threadIdx.x;
+    prof_begin(S, d);
     int bi = 0;
     for (int base = 0; base < d.n; base += batch, ++bi) {
         const int B = min(batch, d.n - base);
-        if (tid == 0) S.t_pop = (unsigned long long)wall_clock64();
+        if (tid == 0) {
+            S.t_pop = (unsigned long long)wall_clock64();
+            S.tprev = S.t_pop;
+        }
         load_batch(S, B, d.ring, (unsigned long long)base, ~0ull, d.strip, G);
         __syncthreads();
-        process_batch(S, B, d, W, G);
+        mark(S, PF_LOAD);
+        process_batch(B, d, W, G);
         // output slots and head rows
         for (int t = tid; t < B * SSLA_C3; t += LT) {
             const int e = t / SSLA_C3, i = t % SSLA_C3;
@@ -509,7 +673,13 @@ k_batch_drain(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, int ba
             d.batch_clk[(size_t)bi * 2 + 1] = (unsigned long long)wall_clock64();
         }
         __syncthreads();
+        mark(S, PF_PUBLISH);
+        if (tid == 0) {
+            S.prof[PF_BATCHES] += 1;
+            S.prof[PF_RECORDS] += (unsigned long long)B;
+        }
     }
+    prof_end(S, d);
 }
 
 // ---------------------------------------------------------------------------
@@ -519,9 +689,10 @@ __global__ void __launch_bounds__(LT)
 k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* stop_flag,
        unsigned int spin_ns, unsigned long long idle_ticks, int max_batch,
        int* __restrict__ status) {
-    __shared__ Lds S;
+    Lds& S = g_lds;
     const LiveDesc& d = ld[blockIdx.x];
     const int tid = threadIdx.x;
+    prof_begin(S, d);
     const unsigned long long mask = d.ring_mask;
     unsigned long long t = __hip_atomic_load(d.tail, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
     unsigned long long last_work = (unsigned long long)wall_clock64();
@@ -562,6 +733,7 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
                     __hip_atomic_store(d.kend, (unsigned long long)wall_clock64(), __ATOMIC_RELEASE,
                                        __HIP_MEMORY_SCOPE_SYSTEM);
             }
+            prof_end(S, d);
             return;
         }
         if (B == 0) {
@@ -571,10 +743,14 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
         // pairs with the producer's release store of the tags seen above:
         // the records' fields are visible to the loads that follow
         __atomic_thread_fence(__ATOMIC_ACQUIRE);
-        if (tid == 0) S.t_pop = (unsigned long long)wall_clock64();
+        if (tid == 0) {
+            S.t_pop = (unsigned long long)wall_clock64();
+            S.tprev = S.t_pop;
+        }
         load_batch(S, B, d.ring, t, mask, d.strip, G);
         __syncthreads();
-        process_batch(S, B, d, W, G);
+        mark(S, PF_LOAD);
+        process_batch(B, d, W, G);
         const unsigned long long t_done = (unsigned long long)wall_clock64();
         if (tid < B && d.timing) {
             const unsigned long long seq = t + (unsigned long long)tid;
@@ -596,6 +772,11 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
             if (d.events_done)
                 __hip_atomic_store(d.events_done, t, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         }
+        mark(S, PF_PUBLISH);
+        if (tid == 0) {
+            S.prof[PF_BATCHES] += 1;
+            S.prof[PF_RECORDS] += (unsigned long long)B;
+        }
     }
 }
 
@@ -608,7 +789,7 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
         }                                                                     \
     } while (0)
 
-size_t scratch_floats() { return (size_t)(LP + 1) * NCMAX; }
+size_t scratch_floats() { return (size_t)LP * NCMAX; }
 
 // batch-mode workspace: per-block scratch rows + the device block table
 std::mutex g_bmu;
@@ -616,6 +797,8 @@ float* g_bscratch = nullptr;
 LiveDesc* g_bdesc = nullptr;
 LiveDesc* g_bdesc_host = nullptr;
 hipEvent_t g_bcopied = nullptr;
+unsigned long long* g_bprof = nullptr;
+unsigned long long* g_bprof_host = nullptr;
 
 }  // namespace
 
@@ -671,9 +854,23 @@ static void live_desc_state(const HybridS2S3Config* cfg, int b, LiveDesc* d) {
     d->version = head ? cfg->version[b] : nullptr;
 }
 
+// Adds the per-block profile sums in `dev` (NPROF x nb, wall-clock ticks and
+// counts) to phase_us: times in microseconds, the last two slots as counts.
+static void add_profile(const unsigned long long* host, int nb, double* phase_us) {
+    int khz = 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, 0) != hipSuccess || khz <= 0)
+        khz = 100000;
+    for (int b = 0; b < nb; ++b)
+        for (int k = 0; k < NPROF; ++k) {
+            const double v = (double)host[(size_t)b * NPROF + k];
+            phase_us[k] += (k == PF_BATCHES || k == PF_RECORDS) ? v : v * 1000.0 / (double)khz;
+        }
+}
+
 int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings, const int* ns,
                 HybridS2S3OutputSlot* const* outs, float* const* head_outs,
-                unsigned long long* const* batch_clks, int batch, hipStream_t st, bool sync) {
+                unsigned long long* const* batch_clks, int batch, hipStream_t st, bool sync,
+                double* phase_us) {
     LiveWeights W;
     Geometry G;
     int rc = live_weights(cfg, &W, &G);
@@ -688,11 +885,18 @@ int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
             set_error("bad ring / count for block " + std::to_string(b));
             return SSLA_ERR_ARG;
         }
+    if (phase_us && !sync) {
+        set_error("batch_phase_us needs sync");
+        return SSLA_ERR_ARG;
+    }
     std::lock_guard<std::mutex> lk(g_bmu);
     if (!g_bscratch) {
         const size_t bytes = sizeof(float) * scratch_floats() * SSLA_MAX_BLOCKS;
         LHIP(hipMalloc(&g_bscratch, bytes));
         LHIP(hipMemset(g_bscratch, 0, bytes));
+        LHIP(hipMalloc(&g_bprof, sizeof(unsigned long long) * NPROF * SSLA_MAX_BLOCKS));
+        LHIP(hipHostMalloc((void**)&g_bprof_host, sizeof(unsigned long long) * NPROF * SSLA_MAX_BLOCKS,
+                           hipHostMallocDefault));
         LHIP(hipMalloc(&g_bdesc, sizeof(LiveDesc) * SSLA_MAX_BLOCKS));
         LHIP(hipHostMalloc((void**)&g_bdesc_host, sizeof(LiveDesc) * SSLA_MAX_BLOCKS, hipHostMallocDefault));
         LHIP(hipEventCreateWithFlags(&g_bcopied, hipEventDisableTiming));
@@ -710,12 +914,18 @@ int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
         d.out = outs ? outs[b] : nullptr;
         d.head_out = head_outs ? head_outs[b] : nullptr;
         d.batch_clk = batch_clks ? batch_clks[b] : nullptr;
+        d.prof = phase_us ? g_bprof + (size_t)NPROF * b : nullptr;
     }
     LHIP(hipMemcpyAsync(g_bdesc, g_bdesc_host, sizeof(LiveDesc) * nb, hipMemcpyHostToDevice, st));
     LHIP(hipEventRecord(g_bcopied, st));
     hipLaunchKernelGGL(k_batch_drain, dim3(nb), dim3(LT), 0, st, g_bdesc, W, G, batch);
     LHIP(hipGetLastError());
     if (sync) LHIP(hipStreamSynchronize(st));
+    if (phase_us) {
+        LHIP(hipMemcpy(g_bprof_host, g_bprof, sizeof(unsigned long long) * NPROF * nb,
+                       hipMemcpyDeviceToHost));
+        add_profile(g_bprof_host, nb, phase_us);
+    }
     return SSLA_OK;
 }
 
@@ -727,13 +937,15 @@ struct LiveSession {
     LiveDesc* desc = nullptr;
     float* scratch = nullptr;
     int* status = nullptr;
+    unsigned long long* prof = nullptr;
+    double* phase_us = nullptr;
     int nb = 0;
 };
 
 int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
                unsigned long long ring_mask, unsigned long long* const* tails, int* stop_flag,
                unsigned long long* const* events_done, unsigned int spin_ns, int max_batch,
-               unsigned int idle_timeout_ms, LiveSession** out) {
+               unsigned int idle_timeout_ms, double* phase_us, LiveSession** out) {
     *out = nullptr;
     LiveWeights W;
     Geometry G;
@@ -773,6 +985,7 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
         if (s->desc) (void)hipFree(s->desc);
         if (s->scratch) (void)hipFree(s->scratch);
         if (s->status) (void)hipFree(s->status);
+        if (s->prof) (void)hipFree(s->prof);
         delete s;
         return SSLA_ERR_HIP;
     };
@@ -781,6 +994,10 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
     if (hipMalloc(&s->scratch, sbytes) != hipSuccess) return fail("scratch");
     if (hipMalloc(&s->desc, sizeof(LiveDesc) * nb) != hipSuccess) return fail("desc");
     if (hipMalloc(&s->status, sizeof(int)) != hipSuccess) return fail("status");
+    if (phase_us) {
+        if (hipMalloc(&s->prof, sizeof(unsigned long long) * NPROF * nb) != hipSuccess) return fail("profile");
+        s->phase_us = phase_us;
+    }
     std::vector<LiveDesc> hd(nb);
     std::memset(hd.data(), 0, sizeof(LiveDesc) * nb);
     for (int b = 0; b < nb; ++b) {
@@ -795,6 +1012,7 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
         d.timing_mask = cfg->timing_mask;
         d.kstart = cfg->kernel_start_clk[b];
         d.kend = cfg->kernel_end_clk[b];
+        d.prof = s->prof ? s->prof + (size_t)NPROF * b : nullptr;
     }
     if (hipMemsetAsync(s->scratch, 0, sbytes, s->stream) != hipSuccess) return fail("memset");
     if (hipMemsetAsync(s->status, 0, sizeof(int), s->stream) != hipSuccess) return fail("memset");
@@ -832,6 +1050,12 @@ int live_wait(LiveSession* s, int timeout_ms, int* status_out) {
     int st = 0;
     LHIP(hipMemcpy(&st, s->status, sizeof(int), hipMemcpyDeviceToHost));
     if (status_out) *status_out = st;
+    if (s->prof) {
+        std::vector<unsigned long long> h((size_t)NPROF * s->nb);
+        LHIP(hipMemcpy(h.data(), s->prof, sizeof(unsigned long long) * h.size(), hipMemcpyDeviceToHost));
+        add_profile(h.data(), s->nb, s->phase_us);
+        (void)hipFree(s->prof);
+    }
     (void)hipStreamDestroy(s->stream);
     (void)hipFree(s->desc);
     (void)hipFree(s->scratch);

@@ -104,17 +104,28 @@ class SslaHipDrainOpts(ctypes.Structure):
         ("batch", ctypes.c_int),
         ("head_outs", ctypes.POINTER(ctypes.c_void_p)),
         ("phase_ms", ctypes.POINTER(ctypes.c_float)),
+        ("batch_phase_us", ctypes.POINTER(ctypes.c_double)),
     ]
 
 
 class SslaHipLiveOpts(ctypes.Structure):
-    _fields_ = [("max_batch", ctypes.c_int), ("idle_timeout_ms", ctypes.c_uint)]
+    _fields_ = [("max_batch", ctypes.c_int), ("idle_timeout_ms", ctypes.c_uint),
+                ("phase_us", ctypes.POINTER(ctypes.c_double))]
 
 
 DRAIN_PHASES = ("order",
                 "L4.proj", "L4.scan", "L4.out", "L5.proj", "L5.scan", "L5.out",
                 "L6.proj", "L6.scan", "L6.out", "L7.proj", "L7.scan", "L7.out",
                 "head", "emit")
+
+# in-kernel profile of the batch-mode and live drains (SSLA_BATCH_PHASES);
+# times in microseconds except the two trailing counts
+BATCH_PHASES = ("load", "tdrop2", "pairs2",
+                "L4.proj", "L4.scan", "L4.out", "L4.ln", "L5.proj", "L5.scan", "L5.out", "L5.ln",
+                "tdrop3", "pairs3",
+                "L6.proj", "L6.scan", "L6.out", "L6.ln", "L7.proj", "L7.scan", "L7.out", "L7.ln",
+                "head.hidden", "head.out", "preds", "publish", "batches", "records")
+N_BATCH_PHASES = 32
 
 
 assert ctypes.sizeof(HybridS2S3Config) == 4616

@@ -237,7 +237,7 @@ class Drain:
             self._heads.append(DeviceBuffer(n * 7 * 4) if want_head else None)
 
     def run(self, stream: int = 0, sync: bool = True, phase_ms: Optional[np.ndarray] = None,
-            batch: int = 0) -> None:
+            batch: int = 0, batch_phase_us: Optional[np.ndarray] = None) -> None:
         """One drain call over the loaded rings.  phase_ms (float32 array of
         len(abi.DRAIN_PHASES)) accumulates per-phase GPU time (needs sync)."""
         nb = self.cfg.n_blocks
@@ -257,6 +257,9 @@ class Drain:
         if phase_ms is not None:
             assert phase_ms.dtype == np.float32 and phase_ms.size >= len(abi.DRAIN_PHASES)
             opts.phase_ms = phase_ms.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+        if batch_phase_us is not None:
+            assert batch_phase_us.dtype == np.float64 and batch_phase_us.size >= abi.N_BATCH_PHASES
+            opts.batch_phase_us = batch_phase_us.ctypes.data_as(ctypes.POINTER(ctypes.c_double))
         lib.check(lib.load().ssla_hip_drain_n_ex(ctypes.byref(self.cfg), rings, ns, outs,
                                                  ctypes.byref(opts)), "drain_n_ex")
 
@@ -369,6 +372,10 @@ class HostRings:
                 (ctypes.c_void_p * nb)(*[base + 8 * (nb + b) for b in range(nb)]),
                 (ctypes.c_void_p * nb)(*[base + 8 * (2 * nb + b) for b in range(nb)]))
 
+    def head_ptrs(self):
+        """Addresses of the producer-side head words (one per block)."""
+        return [self.words.ptr + 8 * b for b in range(self.n_blocks)]
+
     def push(self, blk: int, recs: np.ndarray) -> None:
         """Single-producer publish: write each record, then its seq_done tag."""
         ring = self.rings[blk]
@@ -394,11 +401,15 @@ class LiveDrain:
     """A running persistent drain over HostRings (ssla_hip_persistent_start)."""
 
     def __init__(self, drain: Drain, rings: HostRings, spin_ns: int = 200, max_batch: int = 32,
-                 idle_timeout_ms: int = 30000):
+                 idle_timeout_ms: int = 30000, profile: bool = False):
         self.rings = rings
         self.h = ctypes.c_void_p()
         bufs, tails, dones = rings.ptrs()
+        # in-kernel phase profile, filled by wait() (abi.BATCH_PHASES order)
+        self.phase_us = np.zeros(abi.N_BATCH_PHASES, np.float64) if profile else None
         opts = abi.SslaHipLiveOpts(max_batch, idle_timeout_ms)
+        if profile:
+            opts.phase_us = self.phase_us.ctypes.data_as(ctypes.POINTER(ctypes.c_double))
         lib.check(lib.load().ssla_hip_persistent_start(
             ctypes.byref(drain.cfg), bufs, rings.capacity - 1, tails, rings.stop_ptr, dones,
             spin_ns, ctypes.byref(opts), ctypes.byref(self.h)), "persistent_start")

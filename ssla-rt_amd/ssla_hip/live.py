@@ -1,0 +1,177 @@
+"""The live hybrid pipeline: host producer shards -> fine-grained rings ->
+persistent drain kernel, with emit -> prediction latency.
+
+Mirrors the reference's live runner (orin/hybrid_runner_multi.py:430-760):
+the producer (libstage01_to_gpu.so) runs stages 0 + 1 on CPU shards fed by
+its paced synthetic source and publishes records to one ring per block; the
+persistent kernel drains them and writes a GpuTimingSlot per record.  GPU
+clock stamps are put on the host clock with a two-point calibration: the
+kernel's start and exit stamps, each observed by a host thread spinning on
+the fine-grained word the kernel writes (hybrid_runner_multi.py:525-534,
+688-760).  Latency statistics cover output-producing records (owner, pass2
+and pass3), as the reference reports them.
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+from typing import Dict, Optional
+
+import numpy as np
+
+from . import abi
+from .hybrid import Drain, HostRings, LiveDrain
+from .producer import S01gAPI
+
+
+def _now_ns() -> int:
+    return time.clock_gettime_ns(time.CLOCK_MONOTONIC_RAW)
+
+
+def _spin_nonzero(read, timeout_s: float) -> int:
+    t_end = time.monotonic() + timeout_s
+    while True:
+        v = read()
+        if v:
+            return v
+        if time.monotonic() > t_end:
+            return 0
+
+
+def pct(a: np.ndarray, q: float) -> float:
+    """Linear-interpolation percentile (include/lat_stats.h:33-40)."""
+    return float(np.percentile(a, q * 100.0)) if a.size else float("nan")
+
+
+@dataclass
+class LiveResult:
+    status: int                       # kernel exit: 0 stop flag, 2 overrun, 3 idle
+    duration_s: float
+    synth_events: int
+    ring_records: int                 # records the producer published
+    drained: int                      # records the kernel consumed
+    output_records: int               # owner & pass2 & pass3 records timed
+    lat_us: Dict[str, float] = field(default_factory=dict)
+    producer_stats: list = field(default_factory=list)
+    phase_us: Optional[np.ndarray] = None
+    batch_sizes: Dict[str, float] = field(default_factory=dict)
+
+    @property
+    def drain_rate_kev_s(self) -> float:
+        return self.drained / self.duration_s / 1e3
+
+    @property
+    def output_rate_kev_s(self) -> float:
+        return self.output_records / self.duration_s / 1e3
+
+
+def pick_cores(n_shards: int):
+    """(synth_core, base_core) inside this process's CPU set: the source on
+    the first allowed core, shards on the next n_shards consecutive ones;
+    -1 (unpinned) where the set has no such run."""
+    import os
+    allowed = sorted(os.sched_getaffinity(0))
+    if len(allowed) < n_shards + 1:
+        return -1, -1
+    first = allowed[0]
+    for i in range(1, len(allowed) - n_shards + 1):
+        run = allowed[i:i + n_shards]
+        if run[-1] - run[0] == n_shards - 1:
+            return first, run[0]
+    return first, -1
+
+
+def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n_shards: int = 6,
+             halo: int = 2, base_core: Optional[int] = None, synth_core: Optional[int] = None,
+             seed: int = 1,
+             n_blobs: int = 8, sigma_px: float = 3.0, bg_frac: float = 0.1,
+             ring_capacity: int = 1 << 16, timing_capacity: int = 1 << 22, max_batch: int = 32,
+             spin_ns: int = 200, profile: bool = True, drain_timeout_s: float = 30.0) -> LiveResult:
+    """One live run on one GPU (one block owning the whole grid)."""
+    if base_core is None or synth_core is None:
+        sc, bc = pick_cores(n_shards)
+        synth_core = sc if synth_core is None else synth_core
+        base_core = bc if base_core is None else base_core
+    drain = Drain.from_weights_dir(weights_dir, n_blocks=1)
+    rings = HostRings(1, ring_capacity)
+    prod = S01gAPI()
+    live = None
+    try:
+        drain.alloc_timing(timing_capacity)
+        c = drain.cfg
+        prod.init(weights_dir, n_shards, halo, base_core, 1 << 16, 1 << 16)
+        prod.attach_multi([rings.bufs[0].ptr], rings.head_ptrs(), ring_capacity - 1, c.W2, c.H2,
+                          [0], [c.W2], [0], [c.H2])
+        live = LiveDrain(drain, rings, spin_ns=spin_ns, max_batch=max_batch,
+                         idle_timeout_ms=int((duration_s + drain_timeout_s + 30) * 1000),
+                         profile=profile)
+        clk = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_ulonglong * 2).from_address(c.kernel_start_clk[0]))
+        k0 = _spin_nonzero(lambda: int(clk[0]), 30.0)
+        t0_cpu = _now_ns()
+        if not k0:
+            raise RuntimeError("the live kernel did not start")
+        prod.reset()
+        t_start = time.monotonic()
+        prod.start_synthetic_blobs(rate_mev, synth_core, seed, n_blobs, sigma_px, bg_frac)
+        time.sleep(duration_s)
+        prod.stop_synthetic()
+        t_stop = time.monotonic()
+        n_synth = prod.synthetic_n_pushed()
+        # let the shards finish what was routed, then the kernel catch up
+        t_end = time.monotonic() + drain_timeout_s
+        while True:
+            st = prod.stats()
+            if st[0] >= n_synth and st[5] == 0:
+                break
+            if time.monotonic() > t_end:
+                break
+            time.sleep(0.001)
+        head = int(rings.head[0])
+        while int(rings.done[0]) < head and time.monotonic() < t_end:
+            time.sleep(0.0005)
+        drained = int(rings.done[0])
+        rings.stop()
+        k1 = _spin_nonzero(lambda: int(clk[1]), 30.0)
+        t1_cpu = _now_ns()
+        status = live.wait()
+        phase = live.phase_us
+        live = None
+        prod_stats = prod.stats()
+        ns_per_tick = (t1_cpu - t0_cpu) / max(1, (k1 - k0)) if k1 else 1e6 / 1e5
+        tv = drain.timing(0)
+        n_keep = min(drained, tv.size)
+        tv = tv[(np.arange(drained - n_keep, drained) & (tv.size - 1))] if n_keep else tv[:0]
+        ok = (tv["t_done_clk"] != 0) & (tv["t_emit_ns"] != 0) & (tv["t_push_ns"] != 0)
+        own = ok & (tv["owner"] == 1)
+        t_done = t0_cpu + (tv["t_done_clk"].astype(np.float64) - k0) * ns_per_tick
+        e2d = (t_done - tv["t_emit_ns"].astype(np.float64)) / 1e3
+        e2p = (tv["t_push_ns"].astype(np.float64) - tv["t_emit_ns"].astype(np.float64)) / 1e3
+        p2d = (t_done - tv["t_push_ns"].astype(np.float64)) / 1e3
+        kern = (tv["t_done_clk"].astype(np.float64) - tv["t_pop_clk"].astype(np.float64)) * ns_per_tick / 1e3
+        lat = {}
+        for name, arr in (("emit_to_done", e2d), ("emit_to_push", e2p), ("push_to_done", p2d),
+                          ("kernel", kern)):
+            a = arr[own]
+            lat[name + "_p50"] = pct(a, 0.50)
+            lat[name + "_p99"] = pct(a, 0.99)
+            lat[name + "_max"] = float(a.max()) if a.size else float("nan")
+        a = e2d[ok]
+        lat["all_emit_to_done_p50"] = pct(a, 0.50)
+        lat["all_emit_to_done_p99"] = pct(a, 0.99)
+        lat["ns_per_tick"] = ns_per_tick
+        bs = {}
+        if phase is not None and phase[26] > 0:
+            bs = {"batches": float(phase[25]), "mean": float(phase[26] / max(1.0, phase[25]))}
+        return LiveResult(status=status, duration_s=t_stop - t_start, synth_events=n_synth,
+                          ring_records=head, drained=drained, output_records=int(own.sum()),
+                          lat_us=lat, producer_stats=prod_stats, phase_us=phase, batch_sizes=bs)
+    finally:
+        if live is not None:
+            rings.stop()
+            try:
+                live.wait(60000)
+            except Exception:
+                pass
+        prod.shutdown()
+        drain.close()
+        rings.free()

@@ -57,7 +57,7 @@ def check_preds(preds, version, rec, p3, ref7):
             assert np.abs(preds[cell] - ref7[k[-1]]).max() <= HEAD_TOL, cell
 
 
-@pytest.mark.parametrize("batch", [8, 17, 32])
+@pytest.mark.parametrize("batch", [1, 8, 17, 32])
 def test_batch_mode_matches_oracle(H, stub_dir, stub_npz, batch):
     n = 6000
     say("batch_mode", batch, n)
@@ -190,3 +190,62 @@ def test_live_idle_timeout_exits(H, stub_dir):
         status = live.wait(timeout_ms=20000)
         assert status == 3
         rings.free()
+
+
+def test_live_fed_by_producer_matches_oracle(H, stub_dir, stub_npz):
+    """Raw events -> host producer (one shard) -> fine-grained ring ->
+    persistent kernel; the ring's records then drive the oracle, whose state,
+    flags and predictions the kernel must match."""
+    from ssla_hip import producer as P
+    n_ev = 40000
+    say("live fed by producer", n_ev)
+    rng = np.random.default_rng(5)
+    ev = P.events_array(np.arange(n_ev), rng.integers(0, 80, n_ev), rng.integers(0, 64, n_ev),
+                        np.where(rng.random(n_ev) < 0.5, -1.0, 1.0))
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        d.alloc_timing(1 << 14)
+        rings = H.HostRings(1, capacity=1 << 14)
+        api = P.S01gAPI()
+        api.init(stub_dir, 1, 2, -1, 4096)
+        live = None
+        try:
+            api.attach_multi([rings.bufs[0].ptr], rings.head_ptrs(), rings.capacity - 1, 20, 16,
+                             [0], [20], [0], [16])
+            live = H.LiveDrain(d, rings, idle_timeout_ms=20000)
+            assert api.submit(ev) == n_ev
+            st_p = api.wait_processed(n_ev, 0)
+            n = int(rings.head[0])
+            assert n == st_p[14] and 0 < n < rings.capacity
+            _wait_done(rings, 0, n)
+        finally:
+            status = live.stop() if live is not None else -1
+            api.shutdown()
+        assert status == 0
+        recs = rings.rings[0][:n].copy()
+        assert np.array_equal(recs["seq_done"], np.arange(1, n + 1, dtype=np.uint64))
+        rec = events.Records(recs["t"], recs["x"], recs["y"], recs["feat1"])
+        st, p2, p3, feat, ref7 = oracle_run(stub_npz, rec)
+        ts = d.timing(0)[:n]
+        assert np.array_equal(ts["owner"], (p3 == 1).astype(np.uint32))
+        assert np.all(ts["t_push_ns"] >= ts["t_emit_ns"]) and np.all(ts["t_emit_ns"] > 0)
+        for li in range(4):
+            assert hidden_close(d.hidden(0, li), st.H[li]), li
+        td2, td3 = d.counters(0)
+        assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3)
+        check_preds(*d.preds(0), rec, p3, ref7)
+        rings.free()
+
+
+def test_run_live_short(stub_dir):
+    """The live pipeline end to end at a low rate: nothing lost, latencies
+    measured for output-producing records."""
+    from ssla_hip import live as LV
+    say("run_live 0.2 Mev/s 1 s")
+    r = LV.run_live(stub_dir, rate_mev=0.2, duration_s=1.0, n_shards=2, halo=2,
+                    timing_capacity=1 << 16)
+    say(f"run_live: status {r.status} ring {r.ring_records} drained {r.drained} "
+        f"out {r.output_records} lat {r.lat_us}")
+    assert r.status == 0
+    assert r.drained == r.ring_records > 0 and r.output_records > 0
+    assert 0 < r.lat_us["emit_to_push_p50"] <= r.lat_us["emit_to_done_p50"]
+    assert r.lat_us["kernel_p50"] > 0
