@@ -10,17 +10,16 @@
 //   pairs   one wave builds the (record, delta) pairs in record order and the
 //           per-delta record lists; one thread per pair finds the next pair
 //           at its cell among the later records' patches
-//   P       q, v, g: one thread per weight column (delta, channel) reads
-//           the column in chunks of up to 48 weights held in registers and
-//           applies each chunk to eight records at a time; v and g for every
+//   P       q, v, g as 16 x 16 MFMA tiles: per delta, the records with a
+//           pair there times the delta's weight columns; v and g for every
 //           pair, q only for the pairs of the layer's output records
 //   S       one lane per (cell, channel) walks the cell's pairs in record
 //           order, loading eight pairs' g, v (and q) before the eight
 //           dependent steps h = sigmoid(g) h + v; q*h where it is consumed
-//   O       one thread per goW column (delta, channel) and residual column
-//           over chunks of eight output records whose q*h rows
-//           are staged in LDS; per-delta partial sums are reduced in delta
-//           order, then fp64 LayerNorm, one wave per record
+//   O       16 output records at a time: their nine q*h rows (and input,
+//           for the residual projection) staged in LDS as one row each and
+//           contracted with [goW; input_proj] by MFMA, K split four ways
+//           and added in order; then fp64 LayerNorm, one wave per record
 // The masks are the reference's (...celled.cuh:1027-1064): L4 all, L5 state
 // for all / output for pass2, L6 pass2, L7 state for pass2 / output for
 // pass3, head for owned pass3 records.  L4/L5 share one pair set, L6/L7
@@ -50,6 +49,8 @@ namespace ssla {
 
 struct LiveWeights {
     LayerWeightsS2S3 L[4];
+    const float* pp[4];     // projection weights in MFMA B-fragment order
+    const float* po[4];     // contraction weights ([goW; input_proj]) likewise
     HeadPtrs head;
     int have_head;
 };
@@ -87,7 +88,10 @@ constexpr int LT = 512;             // threads per workgroup
 constexpr int NW = LT / 64;         // waves per workgroup
 constexpr int LP = kPatch * LB;     // pairs per layer, at most
 constexpr int NCMAX = 3 * SSLA_C3;  // widest pair row
-constexpr int OCH = 8;              // output records per contraction chunk
+constexpr int XS = 100;             // LDS row stride of record features (4 mod 32 banks)
+constexpr int MT = 16;              // MFMA tile rows / columns (v_mfma_f32_16x16x4_f32)
+constexpr int QS = kPatch * SSLA_C3 + SSLA_C3 / 2 + 4;   // contraction row: 9*OUT q*h + IN residual
+constexpr int KSPL = 8;             // split of the contraction's K among waves
 constexpr int NPROF = SSLA_BATCH_PHASES;
 
 // profile slots (order of SSLA_BATCH_PHASES)
@@ -99,11 +103,13 @@ enum {
 static_assert(PF_RECORDS < NPROF, "profile slots");
 
 struct alignas(16) Lds {
-    float X[LB][SSLA_C3];                // layer input (becomes the layer output)
-    float Y[LB][SSLA_C3];                // pre-LayerNorm sums / head cls hidden
-    float R[LB][SSLA_C3];                // head reg hidden
-    float QH[OCH][kPatch][SSLA_C3];      // q*h rows of one output chunk
-    float PB[kPatch + 1][OCH][SSLA_C3];  // per-delta partial sums (+ residual)
+    float X[LB][XS];                     // layer input (becomes the layer output)
+    float Y[LB][XS];                     // pre-LayerNorm sums / head cls hidden
+    union {
+        float QH[MT][QS];                // contraction rows of one 16-record chunk
+        float R[LB][XS];                 // head reg hidden (after the last layer)
+    };
+    float PK[KSPL][MT][SSLA_C3];         // split-K partial sums
     float H7[LB][8];
     unsigned long long tpush[LB], temit[LB];
     int ex[LB], ey[LB];                  // coordinates at the current level
@@ -156,6 +162,8 @@ __device__ __forceinline__ float gload(const float* p) {
 __device__ __forceinline__ void gstore(float* p, float v) {
     *(SSLA_GLOBAL float*)p = v;
 }
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // A float4 of an LDS row: x is 16-byte aligned and `at` a multiple of 4.
 __device__ __forceinline__ float4 lds4(const float* x, int at) {
@@ -293,34 +301,95 @@ __device__ __forceinline__ void build_pairs(Lds& S, int B, const unsigned char* 
     __syncthreads();
 }
 
-// P: scratch[pair][0, 3*OUT) = [q | v | g] of the pair's (record, delta).
-// v and g columns run over every pair at delta; q columns only over the
-// pairs of output records (S.devo), the only ones whose q is consumed.
+// P: scratch[pair][0, 3*OUT) = [q | v | g] of the pair's (record, delta),
+// as 16 x 16 MFMA tiles (v_mfma_f32_16x16x4_f32): per delta, the records
+// with a pair there (rows) times the delta's weight columns.  v and g
+// columns take every pair at delta; q columns only the pairs of output
+// records (S.devo), the only ones whose q is consumed.  Each wave owns
+// whole (delta, column tile) items and keeps the tile's IN x 16 weights in
+// registers across its row tiles, and loads its next item's weights while
+// the current item runs.
+//   A operand: lane (i, k) = (lane % 16, lane / 16) holds row i, k
+//   B operand: lane holds column i, k;  D: lane holds rows 4k..4k+3, column i
 template <int IN, int OUT>
-__device__ __forceinline__ void phase_proj(Lds& S, const float* __restrict__ qvgIn,
-                                           float* __restrict__ scratch) {
-    constexpr int NC = 3 * OUT;
-    for (int u = threadIdx.x; u < kPatch * NC; u += LT) {
-        const int d = u / NC, c = u - d * NC;
-        const bool qcol = c < OUT;
-        const int n = qcol ? S.dcnto[d] : S.dcnt[d];
-        if (n == 0) continue;
-        const int* list = qcol ? S.devo[d] : S.dev[d];
-        const float* w = qvgIn + (size_t)d * IN * NC + c;
-        for (int k0 = 0; k0 < n; k0 += 8) {
-            int off[8];
-            float acc[8];
+struct ProjTile {
+    static constexpr int NC = 3 * OUT, T = NC / MT, TQ = OUT / MT, KS = IN / 4;
+    static constexpr int KS4 = (KS + 3) / 4;      // float4 groups of k-steps
+    static constexpr int N = kPatch * T;          // (delta, column tile) items
+    static constexpr size_t PACKED = (size_t)N * KS4 * 256;   // floats
+    // B operand of item `it`: the tile's IN x 16 weights in fragment order,
+    // lane (i, k) holding column i, rows k, k+4, ... -- one float4 per four
+    // k-steps, 1 KB contiguous per wave.
+    static __device__ __forceinline__ void load(const float* __restrict__ pp, int it, int lane,
+                                                float* b) {
+        const SSLA_GLOBAL f32x4* src = (const SSLA_GLOBAL f32x4*)pp + (size_t)it * KS4 * 64 + lane;
+        #pragma unroll
+        for (int g = 0; g < KS4; ++g) {
+            const f32x4 v = src[g * 64];
             #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                off[r] = list[min(k0 + r, n - 1)] * SSLA_C3;
-                acc[r] = 0.f;
-            }
-            coldot8<IN>(w, NC, &S.X[0][0], off, acc);
-            #pragma unroll
-            for (int r = 0; r < 8; ++r)
-                if (k0 + r < n) gstore(scratch + (size_t)S.pidx[list[k0 + r]][d] * NC + c, acc[r]);
+            for (int j = 0; j < 4; ++j) b[4 * g + j] = v[j];
         }
     }
+    static __device__ __forceinline__ void run(Lds& S, int it, int li, int lk, const float* b,
+                                               float* __restrict__ scratch) {
+        const int d = it / T, t = it - d * T;
+        const bool qt = t < TQ;
+        const int n = qt ? S.dcnto[d] : S.dcnt[d];
+        const int* list = qt ? S.devo[d] : S.dev[d];
+        const int col = t * MT + li;
+        const float* X = &S.X[0][0];
+        for (int m0 = 0; m0 < n; m0 += MT) {
+            const int xr = list[min(m0 + li, n - 1)] * XS + lk;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            #pragma unroll
+            for (int s = 0; s < KS; ++s)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(X[xr + s * 4], b[s], acc, 0, 0, 0);
+            #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int rr = m0 + 4 * lk + r;
+                if (rr < n) gstore(scratch + (size_t)S.pidx[list[rr]][d] * NC + col, acc[r]);
+            }
+        }
+    }
+};
+
+template <int IN, int OUT>
+__device__ __forceinline__ void phase_proj(Lds& S, const float* __restrict__ pp,
+                                           float* __restrict__ scratch) {
+    using P = ProjTile<IN, OUT>;
+    static_assert(OUT % MT == 0 && IN % 4 == 0, "tile shapes");
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int li = lane & 15, lk = lane >> 4;
+    // two items in flight per wave: the next item's weights load while the
+    // current item's tiles run
+    float b0[P::KS4 * 4], b1[P::KS4 * 4];
+    int it = wv;
+    if (it < P::N) P::load(pp, it, lane, b0);
+    while (it < P::N) {
+        const int i1 = it + NW, i2 = i1 + NW;
+        if (i1 < P::N) P::load(pp, i1, lane, b1);
+        P::run(S, it, li, lk, b0, scratch);
+        if (i1 >= P::N) break;
+        if (i2 < P::N) P::load(pp, i2, lane, b0);
+        P::run(S, i1, li, lk, b1, scratch);
+        it = i2;
+    }
+}
+
+// Packs qvgIn (9, IN, 3*OUT) into the projection's fragment order: element
+// (item, group g, lane, j) = W[delta][(4g + j) * 4 + lane / 16][t * 16 + lane % 16]
+// (zero past IN).
+template <int IN, int OUT>
+__global__ void k_pack_proj(const float* __restrict__ qvgIn, float* __restrict__ pp) {
+    using P = ProjTile<IN, OUT>;
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= P::PACKED) return;
+    const int j = (int)(q & 3), lane = (int)((q >> 2) & 63);
+    const size_t r = q >> 8;
+    const int g = (int)(r % P::KS4), it = (int)(r / P::KS4);
+    const int d = it / P::T, t = it - d * P::T;
+    const int k = (4 * g + j) * 4 + lane / 16, c = t * MT + lane % 16;
+    pp[q] = k < IN ? qvgIn[((size_t)d * IN + k) * P::NC + c] : 0.f;
 }
 
 // S: the per-cell recurrence in record order; q*h replaces q for pairs of
@@ -366,48 +435,86 @@ __device__ __forceinline__ void phase_recur(Lds& S, float* __restrict__ hidden,
     }
 }
 
-// O: Y[e] = sum_delta goW[delta]^T qh(e, delta) + residual for the output
-// records S.ol[0, S.nout), in chunks of eight records: one thread per goW
-// column (delta, channel) and, with input_proj, per residual column; the
-// per-delta partial sums are added in delta order.
+// One (column tile, K part) item of the contraction below: B operand loads
+// (the part's weights, one register per 4-row step) and the MFMA chain over
+// the staged rows, leaving the partial tile in S.PK[part].
 template <int IN, int OUT>
-__device__ __forceinline__ void phase_out(Lds& S, const LayerWeightsS2S3& L,
-                                          const float* __restrict__ scratch) {
-    constexpr int NC = 3 * OUT;
-    const int tid = threadIdx.x;
-    const bool ip = L.input_proj != nullptr;
-    const int nu = kPatch * OUT + (ip ? OUT : 0);
-    const int no = S.nout;
-    for (int c0 = 0; c0 < no; c0 += OCH) {
-        const int m = min(OCH, no - c0);
-        for (int t = tid; t < m * kPatch * OUT; t += LT) {
-            const int r = t / (kPatch * OUT), rem = t - r * (kPatch * OUT);
-            const int dd = rem / OUT, i = rem - dd * OUT;
-            const int p = S.pidx[S.ol[c0 + r]][dd];
-            S.QH[r][dd][i] = p >= 0 ? gload(scratch + (size_t)p * NC + i) : 0.f;
-        }
-        __syncthreads();
-        for (int u = tid; u < nu; u += LT) {
-            const int d = u / OUT, j = u - d * OUT;
-            const bool live = d == kPatch || S.dcnto[d] > 0;
-            float acc[8];
+struct OutTile {
+    static constexpr bool IP = IN != OUT;          // L4 / L6 project the residual
+    static constexpr int KQ = kPatch * OUT, KT = KQ + (IP ? IN : 0);
+    static constexpr int NT = OUT / MT, STEPS = KT / 4, SPER = (STEPS + KSPL - 1) / KSPL;
+    static constexpr int N = NT * KSPL;            // (column tile, K part) items
+    static constexpr int SP4 = (SPER + 3) / 4;
+    static constexpr size_t PACKED = (size_t)N * SP4 * 256;   // floats
+    static __device__ __forceinline__ void load(const float* __restrict__ po, int it, int lane,
+                                                float* b) {
+        const SSLA_GLOBAL f32x4* src = (const SSLA_GLOBAL f32x4*)po + (size_t)it * SP4 * 64 + lane;
+        #pragma unroll
+        for (int g = 0; g < SP4; ++g) {
+            const f32x4 v = src[g * 64];
             #pragma unroll
-            for (int r = 0; r < 8; ++r) acc[r] = 0.f;
-            if (live) {
-                int off[8];
-                if (d < kPatch) {
-                    #pragma unroll
-                    for (int r = 0; r < 8; ++r) off[r] = (min(r, m - 1) * kPatch + d) * SSLA_C3;
-                    coldot8<OUT>(L.goW + (size_t)d * OUT * OUT + j, OUT, &S.QH[0][0][0], off, acc);
+            for (int j = 0; j < 4; ++j) b[4 * g + j] = v[j];
+        }
+    }
+    static __device__ __forceinline__ void run(Lds& S, int it, int li, int lk, const float* b) {
+        const int nt = it / KSPL, ks = it - nt * KSPL;
+        const int col = nt * MT + li;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        #pragma unroll
+        for (int j = 0; j < SPER; ++j) {
+            const int s = min(ks * SPER + j, STEPS - 1);  // past the end b is 0
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(S.QH[li][s * 4 + lk], b[j], acc, 0, 0, 0);
+        }
+        #pragma unroll
+        for (int r = 0; r < 4; ++r) S.PK[ks][4 * lk + r][col] = acc[r];
+    }
+};
+
+// O: Y[e] = sum_delta goW[delta]^T qh(e, delta) + residual for the output
+// records S.ol[0, S.nout), 16 records at a time, as one MFMA contraction
+// over K = 9*OUT (+ IN): each record's row holds its nine q*h rows (zeros
+// where the patch cell is out of bounds) and, with input_proj, its input;
+// B is goW (9*OUT x OUT, delta-major) followed by input_proj.  Waves own
+// (column tile, K part) items with the part's weights in registers; the
+// parts are added in order.
+template <int IN, int OUT>
+__device__ __forceinline__ void phase_out(Lds& S, const float* __restrict__ po,
+                                          const float* __restrict__ scratch) {
+    using O = OutTile<IN, OUT>;
+    constexpr int NC = 3 * OUT;
+    static_assert(O::KT <= QS, "contraction row");
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int li = lane & 15, lk = lane >> 4;
+    const int no = S.nout;
+    for (int c0 = 0; c0 < no; c0 += MT) {
+        const int m = min(MT, no - c0);
+        for (int t = tid; t < MT * O::KT; t += LT) {
+            const int r = t / O::KT, k = t - r * O::KT;
+            float v = 0.f;
+            if (r < m) {
+                const int e = S.ol[c0 + r];
+                if (k < O::KQ) {
+                    const int d = k / OUT, i = k - d * OUT;
+                    const int p = S.pidx[e][d];
+                    if (p >= 0) v = gload(scratch + (size_t)p * NC + i);
                 } else {
-                    #pragma unroll
-                    for (int r = 0; r < 8; ++r) off[r] = S.ol[c0 + min(r, m - 1)] * SSLA_C3;
-                    coldot8<IN>(L.input_proj + j, OUT, &S.X[0][0], off, acc);
+                    v = S.X[e][k - O::KQ];
                 }
             }
-            #pragma unroll
-            for (int r = 0; r < 8; ++r)
-                if (r < m) S.PB[d][r][j] = acc[r];
+            S.QH[r][k] = v;
+        }
+        __syncthreads();
+        float b0[O::SP4 * 4], b1[O::SP4 * 4];
+        int it = wv;
+        if (it < O::N) O::load(po, it, lane, b0);
+        while (it < O::N) {
+            const int i1 = it + NW, i2 = i1 + NW;
+            if (i1 < O::N) O::load(po, i1, lane, b1);
+            O::run(S, it, li, lk, b0);
+            if (i1 >= O::N) break;
+            if (i2 < O::N) O::load(po, i2, lane, b0);
+            O::run(S, i1, li, lk, b1);
+            it = i2;
         }
         __syncthreads();
         for (int t = tid; t < m * OUT; t += LT) {
@@ -415,19 +522,41 @@ __device__ __forceinline__ void phase_out(Lds& S, const LayerWeightsS2S3& L,
             const int e = S.ol[c0 + r];
             float a = 0.f;
             #pragma unroll
-            for (int dd = 0; dd < kPatch; ++dd) a += S.PB[dd][r][jj];
-            S.Y[e][jj] = a + (ip ? S.PB[kPatch][r][jj] : S.X[e][jj]);
+            for (int ks = 0; ks < KSPL; ++ks) a += S.PK[ks][r][jj];
+            S.Y[e][jj] = O::IP ? a : a + S.X[e][jj];
         }
         __syncthreads();
     }
+}
+
+// Packs [goW (9*OUT, OUT); input_proj (IN, OUT)] into the contraction's
+// fragment order: element (item (nt, ks), group g, lane, j) = B[k][nt*16 +
+// lane % 16] with k = (ks*SPER + 4g + j) * 4 + lane / 16 (zero past the part
+// or past K).
+template <int IN, int OUT>
+__global__ void k_pack_out(const float* __restrict__ goW, const float* __restrict__ ip,
+                           float* __restrict__ po) {
+    using O = OutTile<IN, OUT>;
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= O::PACKED) return;
+    const int j = (int)(q & 3), lane = (int)((q >> 2) & 63);
+    const size_t r = q >> 8;
+    const int g = (int)(r % O::SP4), it = (int)(r / O::SP4);
+    const int nt = it / KSPL, ks = it - nt * KSPL;
+    const int step = 4 * g + j, s = ks * O::SPER + step;
+    const int k = s * 4 + lane / 16, c = nt * MT + lane % 16;
+    float v = 0.f;
+    if (step < O::SPER && s < O::STEPS)
+        v = k < O::KQ ? goW[(size_t)k * OUT + c] : ip[(size_t)(k - O::KQ) * OUT + c];
+    po[q] = v;
 }
 
 // One layer over the pairs built for `set`; output (LayerNormed, in S.X) for
 // the records of set and outm (outm == nullptr: all of set).
 template <int IN, int OUT>
 __device__ __forceinline__ void batch_layer(Lds& S, int B, const unsigned char* set, const unsigned char* outm,
-                            const LayerWeightsS2S3& L, float* __restrict__ hidden,
-                            float* __restrict__ scratch, int slot) {
+                            const LayerWeightsS2S3& L, const float* pp, const float* po,
+                            float* __restrict__ hidden, float* __restrict__ scratch, int slot) {
     const int tid = threadIdx.x;
     if (tid < 64) {
         const bool o = tid < B && set[tid] && (outm == nullptr || outm[tid]);
@@ -444,13 +573,13 @@ __device__ __forceinline__ void batch_layer(Lds& S, int B, const unsigned char* 
         }
     }
     __syncthreads();
-    phase_proj<IN, OUT>(S, L.qvgIn, scratch);
+    phase_proj<IN, OUT>(S, pp, scratch);
     __syncthreads();
     mark(S, slot + 0);
     phase_recur<OUT>(S, hidden, scratch, outm);
     __syncthreads();
     mark(S, slot + 1);
-    phase_out<IN, OUT>(S, L, scratch);
+    phase_out<IN, OUT>(S, po, scratch);
     mark(S, slot + 2);
     // fp64 LayerNorm, one wave per output record
     const int wv = tid >> 6, lane = tid & 63, no = S.nout;
@@ -495,7 +624,7 @@ __device__ __forceinline__ void batch_head(Lds& S, int B, const LiveDesc& d, con
             float acc[8];
             #pragma unroll
             for (int r = 0; r < 8; ++r) {
-                off[r] = S.ol[min(r0 + r, nh - 1)] * SSLA_C3;
+                off[r] = S.ol[min(r0 + r, nh - 1)] * XS;
                 acc[r] = bias;
             }
             coldot8<C>(Wc, C, &S.X[0][0], off, acc);
@@ -575,8 +704,8 @@ __device__ __noinline__ void process_batch(int B, const LiveDesc& d, const LiveW
     mark(S, PF_TD2);
     build_pairs(S, B, S.vld, G.H2, G.W2);
     mark(S, PF_PAIRS2);
-    batch_layer<SSLA_C1, SSLA_C2>(S, B, S.vld, nullptr, W.L[0], d.hidden[0], d.scratch, PF_L4);
-    batch_layer<SSLA_C2, SSLA_C2>(S, B, S.vld, S.p2, W.L[1], d.hidden[1], d.scratch, PF_L5);
+    batch_layer<SSLA_C1, SSLA_C2>(S, B, S.vld, nullptr, W.L[0], W.pp[0], W.po[0], d.hidden[0], d.scratch, PF_L4);
+    batch_layer<SSLA_C2, SSLA_C2>(S, B, S.vld, S.p2, W.L[1], W.pp[1], W.po[1], d.hidden[1], d.scratch, PF_L5);
     if (tid < B) {                      // pool to s3
         S.ex[tid] >>= 1;
         S.ey[tid] >>= 1;
@@ -588,8 +717,8 @@ __device__ __noinline__ void process_batch(int B, const LiveDesc& d, const LiveW
     mark(S, PF_TD3);
     build_pairs(S, B, S.p2, G.H3, G.W3);
     mark(S, PF_PAIRS3);
-    batch_layer<SSLA_C2, SSLA_C3>(S, B, S.p2, nullptr, W.L[2], d.hidden[2], d.scratch, PF_L6);
-    batch_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], d.hidden[3], d.scratch, PF_L7);
+    batch_layer<SSLA_C2, SSLA_C3>(S, B, S.p2, nullptr, W.L[2], W.pp[2], W.po[2], d.hidden[2], d.scratch, PF_L6);
+    batch_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], W.pp[3], W.po[3], d.hidden[3], d.scratch, PF_L7);
     if (W.have_head) batch_head(S, B, d, W);
 }
 
@@ -798,6 +927,7 @@ LiveDesc* g_bdesc = nullptr;
 LiveDesc* g_bdesc_host = nullptr;
 hipEvent_t g_bcopied = nullptr;
 unsigned long long* g_bprof = nullptr;
+float* g_bpack = nullptr;
 unsigned long long* g_bprof_host = nullptr;
 
 }  // namespace
@@ -841,6 +971,41 @@ static int live_weights(const HybridS2S3Config* cfg, LiveWeights* W, Geometry* G
     W->have_head = cfg->head_cls_conv_W != nullptr;
     G->H2 = cfg->H2; G->W2 = cfg->W2; G->H3 = cfg->H3; G->W3 = cfg->W3;
     G->C2 = G->H2 * G->W2; G->C3 = G->H3 * G->W3; G->nb = nb; G->window = cfg->tdrop_window;
+    return SSLA_OK;
+}
+
+// Device floats of the fragment-order weight copies of the four layers.
+static size_t packed_floats() {
+    return ProjTile<SSLA_C1, SSLA_C2>::PACKED + ProjTile<SSLA_C2, SSLA_C2>::PACKED +
+           ProjTile<SSLA_C2, SSLA_C3>::PACKED + ProjTile<SSLA_C3, SSLA_C3>::PACKED +
+           OutTile<SSLA_C1, SSLA_C2>::PACKED + OutTile<SSLA_C2, SSLA_C2>::PACKED +
+           OutTile<SSLA_C2, SSLA_C3>::PACKED + OutTile<SSLA_C3, SSLA_C3>::PACKED;
+}
+
+template <int IN, int OUT>
+static float* pack_layer_weights(const LayerWeightsS2S3& L, float* dst, const float** pp,
+                                 const float** po, hipStream_t st) {
+    constexpr int TB = 256;
+    const size_t np = ProjTile<IN, OUT>::PACKED, no = OutTile<IN, OUT>::PACKED;
+    hipLaunchKernelGGL((k_pack_proj<IN, OUT>), dim3((unsigned)((np + TB - 1) / TB)), dim3(TB), 0, st,
+                       L.qvgIn, dst);
+    *pp = dst;
+    dst += np;
+    hipLaunchKernelGGL((k_pack_out<IN, OUT>), dim3((unsigned)((no + TB - 1) / TB)), dim3(TB), 0, st,
+                       L.goW, L.input_proj, dst);
+    *po = dst;
+    return dst + no;
+}
+
+// Fills W->pp / W->po from the bound weights into `buf` (packed_floats()
+// floats) on stream st.
+static int pack_weights(LiveWeights* W, float* buf, hipStream_t st) {
+    float* p = buf;
+    p = pack_layer_weights<SSLA_C1, SSLA_C2>(W->L[0], p, &W->pp[0], &W->po[0], st);
+    p = pack_layer_weights<SSLA_C2, SSLA_C2>(W->L[1], p, &W->pp[1], &W->po[1], st);
+    p = pack_layer_weights<SSLA_C2, SSLA_C3>(W->L[2], p, &W->pp[2], &W->po[2], st);
+    p = pack_layer_weights<SSLA_C3, SSLA_C3>(W->L[3], p, &W->pp[3], &W->po[3], st);
+    LHIP(hipGetLastError());
     return SSLA_OK;
 }
 
@@ -895,6 +1060,7 @@ int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
         LHIP(hipMalloc(&g_bscratch, bytes));
         LHIP(hipMemset(g_bscratch, 0, bytes));
         LHIP(hipMalloc(&g_bprof, sizeof(unsigned long long) * NPROF * SSLA_MAX_BLOCKS));
+        LHIP(hipMalloc(&g_bpack, sizeof(float) * packed_floats()));
         LHIP(hipHostMalloc((void**)&g_bprof_host, sizeof(unsigned long long) * NPROF * SSLA_MAX_BLOCKS,
                            hipHostMallocDefault));
         LHIP(hipMalloc(&g_bdesc, sizeof(LiveDesc) * SSLA_MAX_BLOCKS));
@@ -918,6 +1084,8 @@ int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     }
     LHIP(hipMemcpyAsync(g_bdesc, g_bdesc_host, sizeof(LiveDesc) * nb, hipMemcpyHostToDevice, st));
     LHIP(hipEventRecord(g_bcopied, st));
+    rc = pack_weights(&W, g_bpack, st);
+    if (rc) return rc;
     hipLaunchKernelGGL(k_batch_drain, dim3(nb), dim3(LT), 0, st, g_bdesc, W, G, batch);
     LHIP(hipGetLastError());
     if (sync) LHIP(hipStreamSynchronize(st));
@@ -939,6 +1107,7 @@ struct LiveSession {
     int* status = nullptr;
     unsigned long long* prof = nullptr;
     double* phase_us = nullptr;
+    float* pack = nullptr;
     int nb = 0;
 };
 
@@ -986,6 +1155,7 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
         if (s->scratch) (void)hipFree(s->scratch);
         if (s->status) (void)hipFree(s->status);
         if (s->prof) (void)hipFree(s->prof);
+        if (s->pack) (void)hipFree(s->pack);
         delete s;
         return SSLA_ERR_HIP;
     };
@@ -994,6 +1164,8 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
     if (hipMalloc(&s->scratch, sbytes) != hipSuccess) return fail("scratch");
     if (hipMalloc(&s->desc, sizeof(LiveDesc) * nb) != hipSuccess) return fail("desc");
     if (hipMalloc(&s->status, sizeof(int)) != hipSuccess) return fail("status");
+    if (hipMalloc(&s->pack, sizeof(float) * packed_floats()) != hipSuccess) return fail("weights");
+    if (pack_weights(&W, s->pack, s->stream) != SSLA_OK) return fail("weight packing");
     if (phase_us) {
         if (hipMalloc(&s->prof, sizeof(unsigned long long) * NPROF * nb) != hipSuccess) return fail("profile");
         s->phase_us = phase_us;
@@ -1056,6 +1228,7 @@ int live_wait(LiveSession* s, int timeout_ms, int* status_out) {
         add_profile(h.data(), s->nb, s->phase_us);
         (void)hipFree(s->prof);
     }
+    (void)hipFree(s->pack);
     (void)hipStreamDestroy(s->stream);
     (void)hipFree(s->desc);
     (void)hipFree(s->scratch);

@@ -11,67 +11,66 @@ namespace {
 
 inline float sigmoid(float x) { return 1.0f / (1.0f + std::exp(-x)); }
 
-// One SSLA layer for one event at (x, y) on an (Hl, Wl) grid.  Patch cells are
-// visited in the reference's order: the fixed delta 8..0 table for interior
-// events, the dy/dx walk on the border (ssla_kernels.cpp:343-369).
+// One SSLA layer for one event at (x, y) on an (Hl, Wl) grid.  Patch cells
+// are visited in the reference's order: the fixed delta 8..0 table for
+// interior events, the dy/dx walk on the border (ssla_kernels.cpp:343-369).
+// Weights are input-major (T.qvg (A, IN, 3*OUT), T.go (A, OUT, OUT) with
+// T.go[p][i][o], T.ip (IN, OUT)) so every inner loop runs over contiguous
+// output channels and vectorises.
 template <int IN, int OUT>
-void layer(const FusedLayer& L, float* H, int x, int y, int Hl, int Wl, const float* in,
-           float* out, bool full) {
-    float acc[OUT] = {};
-    float res[OUT];
+void layer(const TLayer& T, float* H, int x, int y, int Hl, int Wl, const float* in, float* out,
+           bool full) {
+    constexpr int NC = 3 * OUT;
+    alignas(32) float acc[OUT] = {};
+    alignas(32) float res[OUT];
     if (full) {
-        if (!L.input_proj.empty()) {
-            for (int o = 0; o < OUT; ++o) {
-                const float* w = L.input_proj.data() + (size_t)o * IN;
-                float s = 0.f;
-                for (int i = 0; i < IN; ++i) s += w[i] * in[i];
-                res[o] = s;
+        if (!T.ip.empty()) {
+            for (int o = 0; o < OUT; ++o) res[o] = 0.f;
+            for (int i = 0; i < IN; ++i) {
+                const float xi = in[i];
+                const float* w = T.ip.data() + (size_t)i * OUT;
+                for (int o = 0; o < OUT; ++o) res[o] += xi * w[o];
             }
         } else {
             for (int o = 0; o < OUT; ++o) res[o] = in[o];
         }
     }
     auto patch = [&](int cell, int p) {
-        const float* Wp = L.qvgIn.data() + (size_t)p * 3 * OUT * IN;
-        float q[OUT], v[OUT], g[OUT];
-        for (int o = 0; o < OUT; ++o) {
-            const float* wv = Wp + (size_t)(OUT + o) * IN;
-            const float* wg = Wp + (size_t)(2 * OUT + o) * IN;
-            float sv = 0.f, sg = 0.f;
-            for (int i = 0; i < IN; ++i) {
-                sv += wv[i] * in[i];
-                sg += wg[i] * in[i];
-            }
-            v[o] = sv;
-            g[o] = sg;
-        }
+        const float* Wp = T.qvg.data() + (size_t)p * IN * NC;
         float* h = H + (size_t)cell * OUT;
+        alignas(32) float r[NC];
         if (!full) {
-            for (int c = 0; c < OUT; ++c) h[c] = sigmoid(g[c]) * h[c] + v[c];
+            // state only: the v and g columns
+            for (int c = OUT; c < NC; ++c) r[c] = 0.f;
+            for (int i = 0; i < IN; ++i) {
+                const float xi = in[i];
+                const float* w = Wp + (size_t)i * NC;
+                for (int c = OUT; c < NC; ++c) r[c] += xi * w[c];
+            }
+            for (int c = 0; c < OUT; ++c) h[c] = sigmoid(r[2 * OUT + c]) * h[c] + r[OUT + c];
             return;
         }
-        for (int o = 0; o < OUT; ++o) {
-            const float* wq = Wp + (size_t)o * IN;
-            float s = 0.f;
-            for (int i = 0; i < IN; ++i) s += wq[i] * in[i];
-            q[o] = s;
+        for (int c = 0; c < NC; ++c) r[c] = 0.f;
+        for (int i = 0; i < IN; ++i) {
+            const float xi = in[i];
+            const float* w = Wp + (size_t)i * NC;
+            for (int c = 0; c < NC; ++c) r[c] += xi * w[c];
         }
-        float qh[OUT];
+        alignas(32) float qh[OUT];
         for (int c = 0; c < OUT; ++c) {
-            const float hc = sigmoid(g[c]) * h[c] + v[c];
+            const float hc = sigmoid(r[2 * OUT + c]) * h[c] + r[OUT + c];
             h[c] = hc;
-            qh[c] = q[c] * hc;
+            qh[c] = r[c] * hc;
         }
-        const float* G = L.goW.data() + (size_t)p * OUT * OUT;
-        for (int o = 0; o < OUT; ++o) {
-            const float* w = G + (size_t)o * OUT;
-            float s = 0.f;
-            for (int i = 0; i < OUT; ++i) s += w[i] * qh[i];
-            acc[o] += s;
+        const float* G = T.go.data() + (size_t)p * OUT * OUT;
+        for (int i = 0; i < OUT; ++i) {
+            const float qi = qh[i];
+            const float* w = G + (size_t)i * OUT;
+            for (int o = 0; o < OUT; ++o) acc[o] += qi * w[o];
         }
     };
     const int base = y * Wl + x;
-    if (L.A == 1) {
+    if (T.A == 1) {
         patch(base, 0);
     } else if (x > 0 && x + 1 < Wl && y > 0 && y + 1 < Hl) {
         const int offs[9] = {-Wl - 1, -Wl, -Wl + 1, -1, 0, 1, Wl - 1, Wl, Wl + 1};
@@ -102,7 +101,32 @@ void layer(const FusedLayer& L, float* H, int x, int y, int Hl, int Wl, const fl
     var /= OUT;
     const double inv = 1.0 / std::sqrt(var + 1e-5);
     for (int o = 0; o < OUT; ++o)
-        out[o] = (float)(((double)acc[o] - mean) * inv * (double)L.gamma[o] + (double)L.beta[o]);
+        out[o] = (float)(((double)acc[o] - mean) * inv * (double)T.gamma[o] + (double)T.beta[o]);
+}
+
+// Input-major copies of a fused layer (see layer()).
+TLayer transpose_layer(const FusedLayer& L) {
+    TLayer T;
+    const int A = L.A, IN = L.in_dim, D = L.out_dim, NC = 3 * D;
+    T.A = A;
+    T.qvg.resize((size_t)A * IN * NC);
+    T.go.resize((size_t)A * D * D);
+    for (int p = 0; p < A; ++p) {
+        for (int r = 0; r < NC; ++r)
+            for (int i = 0; i < IN; ++i)
+                T.qvg[((size_t)p * IN + i) * NC + r] = L.qvgIn[((size_t)p * NC + r) * IN + i];
+        for (int o = 0; o < D; ++o)
+            for (int i = 0; i < D; ++i)
+                T.go[((size_t)p * D + i) * D + o] = L.goW[((size_t)p * D + o) * D + i];
+    }
+    if (!L.input_proj.empty()) {
+        T.ip.resize((size_t)IN * D);
+        for (int o = 0; o < D; ++o)
+            for (int i = 0; i < IN; ++i) T.ip[(size_t)i * D + o] = L.input_proj[(size_t)o * IN + i];
+    }
+    T.gamma = L.gamma;
+    T.beta = L.beta;
+    return T;
 }
 
 }  // namespace
@@ -121,9 +145,10 @@ Stage01::Stage01(const std::string& dir) {
     if (idx.size() != 8) throw std::runtime_error("weights.npz: expected 8 SSLA layers");
     const int io[4][2] = {{2, 12}, {12, 12}, {12, 24}, {24, 24}};
     for (int l = 0; l < 4; ++l) {
-        L_[l] = fuse_layer(Wt, "layers/" + std::to_string(idx[l]), io[l][0], io[l][1]);
-        if ((l == 0) != (L_[l].A == 1))
+        const FusedLayer F = fuse_layer(Wt, "layers/" + std::to_string(idx[l]), io[l][0], io[l][1]);
+        if ((l == 0) != (F.A == 1))
             throw std::runtime_error("weights.npz: layer 0 must have K = 1 and layers 1-3 K = 3");
+        L_[l] = transpose_layer(F);
     }
     reset();
 }

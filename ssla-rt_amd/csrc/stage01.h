@@ -13,6 +13,13 @@
 
 namespace ssla {
 
+// One layer with input-major weights: qvg (A, IN, 3*OUT), go (A, OUT, OUT)
+// indexed [p][i][o], ip (IN, OUT) or empty.
+struct TLayer {
+    int A = 0;
+    std::vector<float> qvg, go, ip, gamma, beta;
+};
+
 class Stage01 {
 public:
     // Loads meta.json + weights.npz; throws std::runtime_error on errors.
@@ -38,7 +45,7 @@ public:
 
 private:
     int H_ = 0, W_ = 0, window_ = 4;
-    FusedLayer L_[4];
+    TLayer L_[4];
     std::vector<float> hidden_[4];
     std::vector<std::uint8_t> td_[2];
     std::vector<double> last_t_;
