@@ -13,8 +13,15 @@ step is the count of the first warmup step (re-checked after timing).
 value = output-producing records (owner & pass2 & pass3) per second, in
 kev/s, over exactly --steps timed steps.  Alongside: ring-record kev/s (the
 unit of the reference's 247 kev/s Orin figure), the roofline of the
-dominant phase from HIP events on the drain's stream, and the CPU baseline
+dominant kernel from HIP events on the drain's stream, and the CPU baseline
 (the oracle's fp32 path, single thread) on a bounded sample.
+
+The metric's latency half comes from the live pipeline, run after the timed
+region: the host producer (6 shards, halo 2) fed by its paced synthetic
+source at 2.0 Mev/s with the same blob distribution, fine-grained rings, the
+persistent drain kernel, for 8 s; emit -> prediction p50 / p99 / max of the
+output-producing records, GPU clocks put on the host clock by the kernel's
+start / exit stamps.
 """
 import argparse
 import json
@@ -46,10 +53,12 @@ def inbounds(x, y, H, W):
     return n
 
 
-def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20):
-    """Minimal MACs of each phase (the reference's skipping semantics:
-    L5 output and L6/L7 only for pass2, L7 output and head for pass3) and
-    the bytes each phase moves through its interface."""
+def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20, chunk=64):
+    """Algorithmic work of each launch of the whole-ring drain: the minimal
+    MACs of the reference's skipping semantics (L5 output and L6/L7 only for
+    pass2, L7 output and head for pass3) and the bytes each launch must move
+    through HBM at its interface (rows in, rows out; weights excluded, they
+    stay in cache).  Returns ({phase: flops}, {phase: bytes}, total MACs)."""
     x = x.astype(np.int64)
     y = y.astype(np.int64)
     n2 = inbounds(x, y, H2, W2)
@@ -57,24 +66,45 @@ def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20):
     n3 = inbounds(x >> 1, y >> 1, H2 >> 1, W2 >> 1)
     S2, S2p, S3p, S3pp = n2.sum(), n2[m2].sum(), n3[m2].sum(), n3[m3].sum()
     N, N2, N3 = x.size, int(m2.sum()), int(m3.sum())
+    F = 4.0
     mac = {
         "L4.proj": S2 * C1 * 3 * C2,
         "L4.out": S2 * C2 * C2 + N * C1 * C2,
-        "L5.proj": S2 * C2 * 2 * C2 + S2p * C2 * C2,
+        "L5.proj_vg": S2 * C2 * 2 * C2,
+        "L5.proj_q": S2p * C2 * C2,
         "L5.out": S2p * C2 * C2,
         "L6.proj": S3p * C2 * 3 * C3,
         "L6.out": S3p * C3 * C3 + N2 * C2 * C3,
-        "L7.proj": S3p * C3 * 2 * C3 + S3pp * C3 * C3,
+        "L7.proj_vg": S3p * C3 * 2 * C3,
+        "L7.proj_q": S3pp * C3 * C3,
         "L7.out": S3pp * C3 * C3,
         "head": int((m3 & (owner == 1)).sum()) * (2 * C3 * C3 + 7 * C3),
     }
     flops = {k: 2.0 * v for k, v in mac.items()}
-    pairs = {"L4": S2, "L5": S2, "L6": S3p, "L7": S3p}
-    outd = {"L4": C2, "L5": C2, "L6": C3, "L7": C3}
-    byts = {}
-    for L in ("L4", "L5", "L6", "L7"):
-        byts[f"{L}.scan"] = 4.0 * pairs[L] * 4 * outd[L]          # read q,v,g; write q*h
-        flops[f"{L}.scan"] = 4.0 * pairs[L] * outd[L]               # fma + mul (+ sigmoid)
+    byts = {
+        "L4.proj": F * (N * C1 + S2 * 3 * C2),
+        "L4.out": F * (S2 * C2 + N * C1 + N * C2),
+        "L5.proj_vg": F * (N * C2 + S2 * 2 * C2),
+        "L5.proj_q": F * (N2 * C2 + S2p * C2),
+        "L5.out": F * (S2p * C2 + 2 * N2 * C2),
+        "L6.proj": F * (N2 * C2 + S3p * 3 * C3),
+        "L6.out": F * (S3p * C3 + N2 * C2 + N2 * C3),
+        "L7.proj_vg": F * (N2 * C3 + S3p * 2 * C3),
+        "L7.proj_q": F * (N3 * C3 + S3pp * C3),
+        "L7.out": F * (S3pp * C3 + 2 * N3 * C3),
+    }
+    # scan passes: summary reads v, g; carry touches each chunk's map and
+    # start state; apply reads v, g (and q where consumed) and writes q*h there
+    for L, pairs, need, out in (("L4", S2, S2, C2), ("L5", S2, S2p, C2),
+                                ("L6", S3p, S3p, C3), ("L7", S3p, S3pp, C3)):
+        chunks = pairs / chunk
+        byts[f"{L}.sum"] = F * (pairs * 2 * out + chunks * 2 * out)
+        byts[f"{L}.carry"] = F * chunks * 3 * out
+        byts[f"{L}.apply"] = F * (pairs * 2 * out + 2 * need * out + chunks * out)
+        flops[f"{L}.sum"] = 4.0 * pairs * out
+        flops[f"{L}.carry"] = 2.0 * chunks * out
+        flops[f"{L}.apply"] = 4.0 * pairs * out
+    byts["emit"] = float(N * 392)
     total_mac = sum(mac.values())
     return flops, byts, total_mac
 
@@ -108,6 +138,63 @@ def cpu_baseline(stub_dir, rec, budget_s=15.0):
             "ring_record_kev_s": round(n / dt / 1e3, 3)}
 
 
+# kernel of each timed launch of the whole-ring drain (ssla-rt_amd/csrc/drain_scan.hip)
+PHASE_KERNEL = {"order": "ordering kernels", "head": "k_head + k_pred_*", "emit": "k_emit"}
+for _L, (_i, _o) in zip(("L4", "L5", "L6", "L7"), ((C1, C2), (C2, C2), (C2, C3), (C3, C3))):
+    for _ph in ("proj", "proj_vg", "proj_q"):
+        PHASE_KERNEL[f"{_L}.{_ph}"] = f"k_qvg<{_i}, {_o}>"
+    PHASE_KERNEL[f"{_L}.sum"] = f"k_scan_summary<{_o}>"
+    PHASE_KERNEL[f"{_L}.carry"] = f"k_scan_carry<{_o}>"
+    PHASE_KERNEL[f"{_L}.apply"] = f"k_scan_apply<{_o}>"
+    PHASE_KERNEL[f"{_L}.out"] = f"k_out<{_i}, {_o}>"
+RIDGE = PEAK_FP32_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)     # FLOP/B
+
+
+def hbm_traffic(phase: str):
+    """HBM bytes of the launch `phase` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE x fetch scale + WRITE_SIZE x write scale, scales
+    from a plain copy of known size), or None when absent."""
+    f = ROOT / "profiles" / "drain_80x64_200k_hbm_traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text())["launches"][phase]["hbm_bytes"]
+    except (KeyError, ValueError):
+        return None
+
+
+def _per_batch(phase_us):
+    """In-kernel wall-clock profile of the live kernel, per batch (µs)."""
+    from ssla_hip import abi
+    if phase_us is None or phase_us[25] <= 0:
+        return None
+    nb = float(phase_us[25])
+    return {k: round(float(phase_us[i]) / nb, 2) for i, k in enumerate(abi.BATCH_PHASES[:25])}
+
+
+def live_latency(stub_dir, rate_mev=2.0, duration_s=8.0):
+    from ssla_hip import live
+    r = live.run_live(stub_dir, rate_mev=rate_mev, duration_s=duration_s, n_shards=6, halo=2)
+    lat = r.lat_us
+    return {
+        "p50": round(lat["emit_to_done_p50"], 2), "p99": round(lat["emit_to_done_p99"], 2),
+        "max": round(lat["emit_to_done_max"], 2),
+        "push_to_done_p50": round(lat["push_to_done_p50"], 2),
+        "push_to_done_p99": round(lat["push_to_done_p99"], 2),
+        "emit_to_push_p50": round(lat["emit_to_push_p50"], 2),
+        "emit_to_push_p99": round(lat["emit_to_push_p99"], 2),
+        "kernel_batch_p50": round(lat["kernel_p50"], 2),
+        "mean_batch": round(r.batch_sizes.get("mean", 0.0), 2),
+        "sustained_drain_kev_s": round(r.drain_rate_kev_s, 2),
+        "output_kev_s": round(r.output_rate_kev_s, 3),
+        "records": r.ring_records, "drained": r.drained, "kernel_status": r.status,
+        "kernel_phase_us_per_batch": _per_batch(r.phase_us),
+        "config": f"live: paced blob source {rate_mev} Mev/s -> 6 host shards (halo 2) -> "
+                  f"fine-grained ring -> persistent kernel, {r.duration_s:.1f} s; "
+                  f"{r.synth_events} events emitted",
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -116,6 +203,8 @@ def main() -> int:
     ap.add_argument("--n", type=int, default=200_000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-live", action="store_true", help="skip the live latency run")
+    ap.add_argument("--live-seconds", type=float, default=8.0)
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (one drain instance set per "
@@ -156,16 +245,24 @@ def main() -> int:
     ring_rate = a.n * a.steps / dt / 1e3
     per = {k: float(v) / a.steps for k, v in zip(abi.DRAIN_PHASES, phase)}
     flops, byts, total_mac = algorithmic_work(rec.x, rec.y, out["pass2"], out["pass3"], owner)
-    dom = max(per, key=per.get)
-    if dom in byts:
-        ach = byts[dom] / (per[dom] * 1e-3) / 1e9
-        roof = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS,
-                "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 5), "traffic": None}
+    # dominant single-kernel launch (the ordering phase is several kernels)
+    single = {k: v for k, v in per.items() if k not in ("order", "head")}
+    dom = max(single, key=single.get)
+    kname = PHASE_KERNEL.get(dom, dom)
+    traffic = hbm_traffic(dom)
+    fl, by = flops.get(dom, 0.0), byts.get(dom, 0.0)
+    if by > 0 and fl / by < RIDGE:
+        ach = by / (per[dom] * 1e-3) / 1e9
+        roof = {"kernel": f"{kname} ({dom})", "bound": "hbm", "achieved": round(ach, 2),
+                "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 5),
+                "traffic": traffic, "avg_launch_ms": round(per[dom], 5),
+                "algorithmic_bytes_per_launch": int(by), "algorithmic_flops_per_launch": int(fl)}
     else:
-        ach = flops.get(dom, 0.0) / (per[dom] * 1e-3) / 1e12
-        roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 4),
+        ach = fl / (per[dom] * 1e-3) / 1e12
+        roof = {"kernel": f"{kname} ({dom})", "bound": "mfma", "achieved": round(ach, 4),
                 "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_TFLOPS, 5),
-                "traffic": None}
+                "traffic": traffic, "avg_launch_ms": round(per[dom], 5),
+                "algorithmic_bytes_per_launch": int(by), "algorithmic_flops_per_launch": int(fl)}
     whole = 2.0 * total_mac / (ms_step * 1e-3) / 1e12
     res = {
         "metric": METRIC, "value": round(value, 3), "unit": "kev/s", "n_gpus": 1,
@@ -176,13 +273,14 @@ def main() -> int:
                                "Gaussian blobs + 10% background, stub weights seed 1, tdrop 4",
                    "records": a.n, "instances": 1, "output_producing_per_step": n_out},
         "ring_record_kev_s": round(ring_rate, 2),
-        "latency_us": {"p50": None, "p99": None,
-                       "note": "emit->prediction needs the live pipeline; not measured by the offline drain"},
+        "latency_us": None,
         "whole_drain_tflops": round(whole, 4),
         "phase_ms": {k: round(v, 5) for k, v in per.items()},
         "roofline": roof,
     }
     d.close()
+    if not a.no_live:
+        res["latency_us"] = live_latency(tmp.name, 2.0, a.live_seconds)
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(tmp.name, rec, a.cpu_seconds)
     tmp.cleanup()

@@ -142,10 +142,15 @@ int ssla_hip_drain_n2(const HybridS2S3Config* cfg,
                       int n0, int n1,
                       HybridS2S3OutputSlot* out0, HybridS2S3OutputSlot* out1);
 
-#define SSLA_DRAIN_PHASES 15
-/* Phase order of SslaHipDrainOpts.phase_ms: 0 ordering (decode, sorts,
- * tdrop decisions), then for L4, L5, L6, L7 in turn: projection, per-cell
- * recurrence, gather + LayerNorm (1..12), 13 head, 14 output slots. */
+#define SSLA_DRAIN_PHASES 25
+/* Phase order of SslaHipDrainOpts.phase_ms (one kernel launch each, except
+ * 0, 23): 0 ordering (decode, sorts, tdrop decisions, chunk tables);
+ * L4: 1 projection, 2 scan summary, 3 scan carry, 4 scan apply,
+ * 5 contraction + LayerNorm; L5: 6 projection of v, g, 7 projection of q
+ * (pass-2 records), 8-10 scan, 11 contraction; L6: 12 projection, 13-15
+ * scan, 16 contraction; L7: 17 projection of v, g, 18 projection of q
+ * (pass-3 records), 19-21 scan, 22 contraction; 23 head and prediction
+ * grid, 24 output slots. */
 
 #define SSLA_BATCH_PHASES 32
 /* Slots of the in-kernel batch profile (batch-mode and live drains), summed

@@ -44,13 +44,13 @@
 
 #include "drain_common.h"
 #include "drain_live.h"
+#include "mfma_pack.h"
 
 namespace ssla {
 
 struct LiveWeights {
     LayerWeightsS2S3 L[4];
-    const float* pp[4];     // projection weights in MFMA B-fragment order
-    const float* po[4];     // contraction weights ([goW; input_proj]) likewise
+    PackedWeights pk;       // MFMA fragment-order copies of the layer weights
     HeadPtrs head;
     int have_head;
 };
@@ -89,9 +89,9 @@ constexpr int NW = LT / 64;         // waves per workgroup
 constexpr int LP = kPatch * LB;     // pairs per layer, at most
 constexpr int NCMAX = 3 * SSLA_C3;  // widest pair row
 constexpr int XS = 100;             // LDS row stride of record features (4 mod 32 banks)
-constexpr int MT = 16;              // MFMA tile rows / columns (v_mfma_f32_16x16x4_f32)
+constexpr int MT = kMT;             // MFMA tile rows / columns (v_mfma_f32_16x16x4_f32)
 constexpr int QS = kPatch * SSLA_C3 + SSLA_C3 / 2 + 4;   // contraction row: 9*OUT q*h + IN residual
-constexpr int KSPL = 8;             // split of the contraction's K among waves
+constexpr int KSPL = kKSplit;       // split of the contraction's K among waves
 constexpr int NPROF = SSLA_BATCH_PHASES;
 
 // profile slots (order of SSLA_BATCH_PHASES)
@@ -150,20 +150,6 @@ __device__ __forceinline__ float wave_sumf(float v) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
     return v;
 }
-
-// Global-memory accesses through address-space-1 pointers: the state,
-// scratch and weight pointers reach the per-batch code as generic pointers
-// loaded from the block table, which would otherwise compile to flat
-// instructions that also wait on the LDS counter.
-#define SSLA_GLOBAL __attribute__((address_space(1)))
-__device__ __forceinline__ float gload(const float* p) {
-    return *(const SSLA_GLOBAL float*)p;
-}
-__device__ __forceinline__ void gstore(float* p, float v) {
-    *(SSLA_GLOBAL float*)p = v;
-}
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // A float4 of an LDS row: x is 16-byte aligned and `at` a multiple of 4.
 __device__ __forceinline__ float4 lds4(const float* x, int at) {
@@ -312,24 +298,11 @@ __device__ __forceinline__ void build_pairs(Lds& S, int B, const unsigned char* 
 //   A operand: lane (i, k) = (lane % 16, lane / 16) holds row i, k
 //   B operand: lane holds column i, k;  D: lane holds rows 4k..4k+3, column i
 template <int IN, int OUT>
-struct ProjTile {
-    static constexpr int NC = 3 * OUT, T = NC / MT, TQ = OUT / MT, KS = IN / 4;
-    static constexpr int KS4 = (KS + 3) / 4;      // float4 groups of k-steps
-    static constexpr int N = kPatch * T;          // (delta, column tile) items
-    static constexpr size_t PACKED = (size_t)N * KS4 * 256;   // floats
-    // B operand of item `it`: the tile's IN x 16 weights in fragment order,
-    // lane (i, k) holding column i, rows k, k+4, ... -- one float4 per four
-    // k-steps, 1 KB contiguous per wave.
-    static __device__ __forceinline__ void load(const float* __restrict__ pp, int it, int lane,
-                                                float* b) {
-        const SSLA_GLOBAL f32x4* src = (const SSLA_GLOBAL f32x4*)pp + (size_t)it * KS4 * 64 + lane;
-        #pragma unroll
-        for (int g = 0; g < KS4; ++g) {
-            const f32x4 v = src[g * 64];
-            #pragma unroll
-            for (int j = 0; j < 4; ++j) b[4 * g + j] = v[j];
-        }
-    }
+struct ProjTile : ProjPack<IN, OUT> {
+    using ProjPack<IN, OUT>::T;
+    using ProjPack<IN, OUT>::TQ;
+    using ProjPack<IN, OUT>::KS;
+    using ProjPack<IN, OUT>::NC;
     static __device__ __forceinline__ void run(Lds& S, int it, int li, int lk, const float* b,
                                                float* __restrict__ scratch) {
         const int d = it / T, t = it - d * T;
@@ -374,22 +347,6 @@ __device__ __forceinline__ void phase_proj(Lds& S, const float* __restrict__ pp,
         P::run(S, i1, li, lk, b1, scratch);
         it = i2;
     }
-}
-
-// Packs qvgIn (9, IN, 3*OUT) into the projection's fragment order: element
-// (item, group g, lane, j) = W[delta][(4g + j) * 4 + lane / 16][t * 16 + lane % 16]
-// (zero past IN).
-template <int IN, int OUT>
-__global__ void k_pack_proj(const float* __restrict__ qvgIn, float* __restrict__ pp) {
-    using P = ProjTile<IN, OUT>;
-    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= P::PACKED) return;
-    const int j = (int)(q & 3), lane = (int)((q >> 2) & 63);
-    const size_t r = q >> 8;
-    const int g = (int)(r % P::KS4), it = (int)(r / P::KS4);
-    const int d = it / P::T, t = it - d * P::T;
-    const int k = (4 * g + j) * 4 + lane / 16, c = t * MT + lane % 16;
-    pp[q] = k < IN ? qvgIn[((size_t)d * IN + k) * P::NC + c] : 0.f;
 }
 
 // S: the per-cell recurrence in record order; q*h replaces q for pairs of
@@ -439,23 +396,9 @@ __device__ __forceinline__ void phase_recur(Lds& S, float* __restrict__ hidden,
 // (the part's weights, one register per 4-row step) and the MFMA chain over
 // the staged rows, leaving the partial tile in S.PK[part].
 template <int IN, int OUT>
-struct OutTile {
-    static constexpr bool IP = IN != OUT;          // L4 / L6 project the residual
-    static constexpr int KQ = kPatch * OUT, KT = KQ + (IP ? IN : 0);
-    static constexpr int NT = OUT / MT, STEPS = KT / 4, SPER = (STEPS + KSPL - 1) / KSPL;
-    static constexpr int N = NT * KSPL;            // (column tile, K part) items
-    static constexpr int SP4 = (SPER + 3) / 4;
-    static constexpr size_t PACKED = (size_t)N * SP4 * 256;   // floats
-    static __device__ __forceinline__ void load(const float* __restrict__ po, int it, int lane,
-                                                float* b) {
-        const SSLA_GLOBAL f32x4* src = (const SSLA_GLOBAL f32x4*)po + (size_t)it * SP4 * 64 + lane;
-        #pragma unroll
-        for (int g = 0; g < SP4; ++g) {
-            const f32x4 v = src[g * 64];
-            #pragma unroll
-            for (int j = 0; j < 4; ++j) b[4 * g + j] = v[j];
-        }
-    }
+struct OutTile : OutPack<IN, OUT> {
+    using OutPack<IN, OUT>::SPER;
+    using OutPack<IN, OUT>::STEPS;
     static __device__ __forceinline__ void run(Lds& S, int it, int li, int lk, const float* b) {
         const int nt = it / KSPL, ks = it - nt * KSPL;
         const int col = nt * MT + li;
@@ -527,28 +470,6 @@ __device__ __forceinline__ void phase_out(Lds& S, const float* __restrict__ po,
         }
         __syncthreads();
     }
-}
-
-// Packs [goW (9*OUT, OUT); input_proj (IN, OUT)] into the contraction's
-// fragment order: element (item (nt, ks), group g, lane, j) = B[k][nt*16 +
-// lane % 16] with k = (ks*SPER + 4g + j) * 4 + lane / 16 (zero past the part
-// or past K).
-template <int IN, int OUT>
-__global__ void k_pack_out(const float* __restrict__ goW, const float* __restrict__ ip,
-                           float* __restrict__ po) {
-    using O = OutTile<IN, OUT>;
-    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= O::PACKED) return;
-    const int j = (int)(q & 3), lane = (int)((q >> 2) & 63);
-    const size_t r = q >> 8;
-    const int g = (int)(r % O::SP4), it = (int)(r / O::SP4);
-    const int nt = it / KSPL, ks = it - nt * KSPL;
-    const int step = 4 * g + j, s = ks * O::SPER + step;
-    const int k = s * 4 + lane / 16, c = nt * MT + lane % 16;
-    float v = 0.f;
-    if (step < O::SPER && s < O::STEPS)
-        v = k < O::KQ ? goW[(size_t)k * OUT + c] : ip[(size_t)(k - O::KQ) * OUT + c];
-    po[q] = v;
 }
 
 // One layer over the pairs built for `set`; output (LayerNormed, in S.X) for
@@ -704,8 +625,8 @@ __device__ __noinline__ void process_batch(int B, const LiveDesc& d, const LiveW
     mark(S, PF_TD2);
     build_pairs(S, B, S.vld, G.H2, G.W2);
     mark(S, PF_PAIRS2);
-    batch_layer<SSLA_C1, SSLA_C2>(S, B, S.vld, nullptr, W.L[0], W.pp[0], W.po[0], d.hidden[0], d.scratch, PF_L4);
-    batch_layer<SSLA_C2, SSLA_C2>(S, B, S.vld, S.p2, W.L[1], W.pp[1], W.po[1], d.hidden[1], d.scratch, PF_L5);
+    batch_layer<SSLA_C1, SSLA_C2>(S, B, S.vld, nullptr, W.L[0], W.pk.pp[0], W.pk.po[0], d.hidden[0], d.scratch, PF_L4);
+    batch_layer<SSLA_C2, SSLA_C2>(S, B, S.vld, S.p2, W.L[1], W.pk.pp[1], W.pk.po[1], d.hidden[1], d.scratch, PF_L5);
     if (tid < B) {                      // pool to s3
         S.ex[tid] >>= 1;
         S.ey[tid] >>= 1;
@@ -717,8 +638,8 @@ __device__ __noinline__ void process_batch(int B, const LiveDesc& d, const LiveW
     mark(S, PF_TD3);
     build_pairs(S, B, S.p2, G.H3, G.W3);
     mark(S, PF_PAIRS3);
-    batch_layer<SSLA_C2, SSLA_C3>(S, B, S.p2, nullptr, W.L[2], W.pp[2], W.po[2], d.hidden[2], d.scratch, PF_L6);
-    batch_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], W.pp[3], W.po[3], d.hidden[3], d.scratch, PF_L7);
+    batch_layer<SSLA_C2, SSLA_C3>(S, B, S.p2, nullptr, W.L[2], W.pk.pp[2], W.pk.po[2], d.hidden[2], d.scratch, PF_L6);
+    batch_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], W.pk.pp[3], W.pk.po[3], d.hidden[3], d.scratch, PF_L7);
     if (W.have_head) batch_head(S, B, d, W);
 }
 
@@ -974,41 +895,6 @@ static int live_weights(const HybridS2S3Config* cfg, LiveWeights* W, Geometry* G
     return SSLA_OK;
 }
 
-// Device floats of the fragment-order weight copies of the four layers.
-static size_t packed_floats() {
-    return ProjTile<SSLA_C1, SSLA_C2>::PACKED + ProjTile<SSLA_C2, SSLA_C2>::PACKED +
-           ProjTile<SSLA_C2, SSLA_C3>::PACKED + ProjTile<SSLA_C3, SSLA_C3>::PACKED +
-           OutTile<SSLA_C1, SSLA_C2>::PACKED + OutTile<SSLA_C2, SSLA_C2>::PACKED +
-           OutTile<SSLA_C2, SSLA_C3>::PACKED + OutTile<SSLA_C3, SSLA_C3>::PACKED;
-}
-
-template <int IN, int OUT>
-static float* pack_layer_weights(const LayerWeightsS2S3& L, float* dst, const float** pp,
-                                 const float** po, hipStream_t st) {
-    constexpr int TB = 256;
-    const size_t np = ProjTile<IN, OUT>::PACKED, no = OutTile<IN, OUT>::PACKED;
-    hipLaunchKernelGGL((k_pack_proj<IN, OUT>), dim3((unsigned)((np + TB - 1) / TB)), dim3(TB), 0, st,
-                       L.qvgIn, dst);
-    *pp = dst;
-    dst += np;
-    hipLaunchKernelGGL((k_pack_out<IN, OUT>), dim3((unsigned)((no + TB - 1) / TB)), dim3(TB), 0, st,
-                       L.goW, L.input_proj, dst);
-    *po = dst;
-    return dst + no;
-}
-
-// Fills W->pp / W->po from the bound weights into `buf` (packed_floats()
-// floats) on stream st.
-static int pack_weights(LiveWeights* W, float* buf, hipStream_t st) {
-    float* p = buf;
-    p = pack_layer_weights<SSLA_C1, SSLA_C2>(W->L[0], p, &W->pp[0], &W->po[0], st);
-    p = pack_layer_weights<SSLA_C2, SSLA_C2>(W->L[1], p, &W->pp[1], &W->po[1], st);
-    p = pack_layer_weights<SSLA_C2, SSLA_C3>(W->L[2], p, &W->pp[2], &W->po[2], st);
-    p = pack_layer_weights<SSLA_C3, SSLA_C3>(W->L[3], p, &W->pp[3], &W->po[3], st);
-    LHIP(hipGetLastError());
-    return SSLA_OK;
-}
-
 static void live_desc_state(const HybridS2S3Config* cfg, int b, LiveDesc* d) {
     for (int li = 0; li < 4; ++li) d->hidden[li] = cfg->hidden[b][li];
     d->td2 = cfg->tdrop_s2[b];
@@ -1060,7 +946,7 @@ int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
         LHIP(hipMalloc(&g_bscratch, bytes));
         LHIP(hipMemset(g_bscratch, 0, bytes));
         LHIP(hipMalloc(&g_bprof, sizeof(unsigned long long) * NPROF * SSLA_MAX_BLOCKS));
-        LHIP(hipMalloc(&g_bpack, sizeof(float) * packed_floats()));
+        LHIP(hipMalloc(&g_bpack, sizeof(float) * packed_weight_floats()));
         LHIP(hipHostMalloc((void**)&g_bprof_host, sizeof(unsigned long long) * NPROF * SSLA_MAX_BLOCKS,
                            hipHostMallocDefault));
         LHIP(hipMalloc(&g_bdesc, sizeof(LiveDesc) * SSLA_MAX_BLOCKS));
@@ -1084,8 +970,7 @@ int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     }
     LHIP(hipMemcpyAsync(g_bdesc, g_bdesc_host, sizeof(LiveDesc) * nb, hipMemcpyHostToDevice, st));
     LHIP(hipEventRecord(g_bcopied, st));
-    rc = pack_weights(&W, g_bpack, st);
-    if (rc) return rc;
+    LHIP(pack_weights(W.L, g_bpack, &W.pk, st));
     hipLaunchKernelGGL(k_batch_drain, dim3(nb), dim3(LT), 0, st, g_bdesc, W, G, batch);
     LHIP(hipGetLastError());
     if (sync) LHIP(hipStreamSynchronize(st));
@@ -1164,8 +1049,8 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
     if (hipMalloc(&s->scratch, sbytes) != hipSuccess) return fail("scratch");
     if (hipMalloc(&s->desc, sizeof(LiveDesc) * nb) != hipSuccess) return fail("desc");
     if (hipMalloc(&s->status, sizeof(int)) != hipSuccess) return fail("status");
-    if (hipMalloc(&s->pack, sizeof(float) * packed_floats()) != hipSuccess) return fail("weights");
-    if (pack_weights(&W, s->pack, s->stream) != SSLA_OK) return fail("weight packing");
+    if (hipMalloc(&s->pack, sizeof(float) * packed_weight_floats()) != hipSuccess) return fail("weights");
+    if (pack_weights(W.L, s->pack, &W.pk, s->stream) != hipSuccess) return fail("weight packing");
     if (phase_us) {
         if (hipMalloc(&s->prof, sizeof(unsigned long long) * NPROF * nb) != hipSuccess) return fail("profile");
         s->phase_us = phase_us;

@@ -15,12 +15,13 @@
 // Only the h_c recurrence is ordered, and only among events touching the
 // same cell.  Per layer the drain therefore runs three phases over all
 // records of all rings:
-//   P  (k_qvg)   q, v, g for every (record, delta) pair, written in
-//                per-cell ring order (pair rows sorted by target cell)
-//   S  (k_scan)  one workgroup per cell walks its pairs in ring order and
-//                turns (q, v, g) rows into q*h rows in place
-//   O  (k_out)   per record: gather the <= 9 q*h rows, goW contraction,
-//                residual, fp64 LayerNorm
+//   P  (k_qvg)   q, v, g for every (record, delta) pair as MFMA tiles,
+//                written in per-cell ring order (pair rows sorted by
+//                target cell); q only where the layer's output is used
+//   S  (k_scan)  chunked per-cell scan: turns (q, v, g) rows into q*h rows
+//                in place, in ring order
+//   O  (k_out)   per record: the <= 9 q*h rows contracted with goW by
+//                MFMA, residual, fp64 LayerNorm
 // The temporal-dropout decisions (ssla_ref.py:190-195) depend only on the
 // per-cell arrival rank of a record, so they come from a stable sort of
 // records by cell: pass = ((counter + rank) mod 256) % window == 0.
@@ -40,12 +41,12 @@
 
 #include "drain_common.h"
 #include "drain_scan.h"
+#include "mfma_pack.h"
 
 namespace ssla {
 
 namespace {
 
-constexpr int kTE = 32;              // records per projection / output tile
 
 struct BlockDesc {
     const HybridInputRec* ring;
@@ -198,62 +199,80 @@ __global__ void k_pair_pos(int n, const uint32_t* __restrict__ keys,
 }
 
 // ---------------------------------------------------------------------------
-// P: q, v, g rows.  One workgroup = kTE records x all 9 deltas; one thread
-// per output column of [q | v | g].  Weight rows (9, IN, 3*OUT) stream from
-// L2 once per tile and feed kTE FMAs each; x comes from LDS as broadcasts.
+// P: q, v, g rows as 16 x 16 MFMA tiles (v_mfma_f32_16x16x4_f32, operand
+// layout in mfma_pack.h).  One workgroup = 64 records (rows, staged in LDS)
+// x all 9 deltas x the column tiles [tlo, thi) of [q | v | g]; each wave
+// owns (delta, column tile) items, loads an item's weights (fragment order,
+// one float4 per four k-steps) while the previous item's four row tiles run,
+// and writes each row to the pair's sorted position.  (Staging whole rows in
+// LDS for 16-byte stores measured slower: the extra barriers cost more than
+// the partial-line writes.)
 // ---------------------------------------------------------------------------
+constexpr int kTM = 64;     // records per projection / contraction workgroup
+
 template <int IN, int OUT>
-__global__ void __launch_bounds__(((3 * OUT + 63) / 64) * 64)
+__global__ void __launch_bounds__(256)
 k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
-      const float* __restrict__ X, const int* __restrict__ pos,
-      const float* __restrict__ W, float* __restrict__ QVG) {
-    constexpr int NC = 3 * OUT;
-    static_assert(IN % 4 == 0, "IN must be a multiple of 4");
-    __shared__ __align__(16) float xs[kTE][IN];
-    __shared__ int rows[kTE];
+      const float* __restrict__ X, const int* __restrict__ pos, const float* __restrict__ pp,
+      float* __restrict__ QVG, int tlo, int thi) {
+    using P = ProjPack<IN, OUT>;
+    constexpr int NC = P::NC, XST = IN + 4;
+    __shared__ __align__(16) float xs[kTM * XST];
+    __shared__ int prow[kPatch][kTM];
     const int n = n_dev ? *n_dev : n_max;
-    const int base = blockIdx.x * kTE;
+    const int base = blockIdx.x * kTM;
     if (base >= n) return;
-    const int cnt = min(kTE, n - base);
-    for (int t = threadIdx.x; t < kTE * IN; t += blockDim.x) {
-        const int r = t / IN, i = t % IN;
-        float v = 0.f;
+    const int cnt = min(kTM, n - base);
+    const int tid = threadIdx.x;
+    constexpr int I4 = IN / 4;
+    for (int t = tid; t < kTM * I4; t += 256) {
+        const int r = t / I4, q = t - r * I4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (r < cnt) {
             const int g = list ? list[base + r] : base + r;
-            v = X[(size_t)g * IN + i];
+            v = reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q];
         }
-        xs[r][i] = v;
+        *reinterpret_cast<float4*>(&xs[r * XST + 4 * q]) = v;
     }
-    if (threadIdx.x < kTE)
-        rows[threadIdx.x] = threadIdx.x < cnt
-            ? (list ? list[base + threadIdx.x] : base + threadIdx.x) : -1;
+    for (int t = tid; t < kTM * kPatch; t += 256) {
+        const int r = t / kPatch, d = t - r * kPatch;
+        int pr = -1;
+        if (r < cnt) {
+            const int g = list ? list[base + r] : base + r;
+            pr = pos[(size_t)g * kPatch + d];
+        }
+        prow[d][r] = pr;
+    }
     __syncthreads();
-    const int c = threadIdx.x;
-    if (c >= NC) return;
-    for (int d = 0; d < kPatch; ++d) {
-        const float* w = W + (size_t)d * IN * NC + c;
-        float acc[kTE];
-        #pragma unroll
-        for (int r = 0; r < kTE; ++r) acc[r] = 0.f;
-        for (int i = 0; i < IN; i += 4) {
-            const float w0 = w[(size_t)i * NC], w1 = w[(size_t)(i + 1) * NC];
-            const float w2 = w[(size_t)(i + 2) * NC], w3 = w[(size_t)(i + 3) * NC];
+    const int lane = tid & 63, wv = tid >> 6, li = lane & 15, lk = lane >> 4;
+    const int nti = thi - tlo, N = kPatch * nti, mtiles = (cnt + kMT - 1) / kMT;
+    auto item = [&](int it) { const int d = it / nti; return d * P::T + tlo + (it - d * nti); };
+    auto run = [&](int it, const float* b) {
+        const int d = it / nti, t = tlo + (it - d * nti), col = t * kMT + li;
+        for (int m = 0; m < mtiles; ++m) {
+            const float* a = &xs[(m * kMT + li) * XST + lk];
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
             #pragma unroll
-            for (int r = 0; r < kTE; ++r) {
-                const float4 xv = *reinterpret_cast<const float4*>(&xs[r][i]);
-                float a = fmaf(w0, xv.x, acc[r]);
-                a = fmaf(w1, xv.y, a);
-                a = fmaf(w2, xv.z, a);
-                acc[r] = fmaf(w3, xv.w, a);
+            for (int s = 0; s < P::KS; ++s)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s], b[s], acc, 0, 0, 0);
+            #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int pr = prow[d][m * kMT + 4 * lk + r];
+                if (pr >= 0) gstore(QVG + (size_t)pr * NC + col, acc[r]);
             }
         }
-        #pragma unroll
-        for (int r = 0; r < kTE; ++r) {
-            const int g = rows[r];
-            if (g < 0) continue;
-            const int pr = pos[(size_t)g * kPatch + d];
-            if (pr >= 0) QVG[(size_t)pr * NC + c] = acc[r];
-        }
+    };
+    float b0[P::KS4 * 4], b1[P::KS4 * 4];
+    int it = wv;
+    if (it < N) P::load(pp, item(it), lane, b0);
+    while (it < N) {
+        const int i1 = it + 4, i2 = i1 + 4;
+        if (i1 < N) P::load(pp, item(i1), lane, b1);
+        run(it, b0);
+        if (i1 >= N) break;
+        if (i2 < N) P::load(pp, item(i2), lane, b0);
+        run(i1, b1);
+        it = i2;
     }
 }
 
@@ -309,22 +328,23 @@ k_scan_summary(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
     const int s = cbeg[j], e = cend[j];
     const float* row = QVG + (size_t)s * NC + OUT + c;     // v at +0, g at +OUT
     float A = 1.f, B = 0.f;
-    int p = s;
-    for (; p + 4 <= e; p += 4, row += 4 * NC) {
-        float v[4], g[4];
+    constexpr int U = 16;        // pairs whose v, g are in flight together
+    for (int p0 = s; p0 < e; p0 += U, row += U * NC) {
+        float v[U], g[U];
         #pragma unroll
-        for (int q = 0; q < 4; ++q) { v[q] = row[q * NC]; g[q] = row[q * NC + OUT]; }
-        #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float a = sigmoid_fast(g[q]);
-            A *= a;
-            B = fmaf(a, B, v[q]);
+        for (int q = 0; q < U; ++q) {
+            const int k = p0 + q < e ? q : 0;
+            v[q] = gload(row + (size_t)k * NC);
+            g[q] = gload(row + (size_t)k * NC + OUT);
         }
-    }
-    for (; p < e; ++p, row += NC) {
-        const float a = sigmoid_fast(row[OUT]);
-        A *= a;
-        B = fmaf(a, B, row[0]);
+        #pragma unroll
+        for (int q = 0; q < U; ++q) {
+            if (p0 + q < e) {
+                const float a = sigmoid_fast(g[q]);
+                A *= a;
+                B = fmaf(a, B, v[q]);
+            }
+        }
     }
     Asum[(size_t)j * OUT + c] = A;
     Bsum[(size_t)j * OUT + c] = B;
@@ -343,10 +363,22 @@ k_scan_carry(int C, const int* __restrict__ start, const int* __restrict__ end,
     float* hp = bd[b].hidden[li] + (size_t)cell * OUT + c;
     float h = *hp;
     const int c0 = coff[k], nc = cnt[k];
-    for (int q = 0; q < nc; ++q) {
-        const size_t o = (size_t)(c0 + q) * OUT + c;
-        Hs[o] = h;
-        h = fmaf(Asum[o], h, Bsum[o]);
+    constexpr int U = 16;        // chunks whose maps are in flight together
+    for (int q0 = 0; q0 < nc; q0 += U) {
+        float a[U], b[U];
+        #pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const size_t o = (size_t)(c0 + (q0 + q < nc ? q0 + q : q0)) * OUT + c;
+            a[q] = gload(Asum + o);
+            b[q] = gload(Bsum + o);
+        }
+        #pragma unroll
+        for (int q = 0; q < U; ++q) {
+            if (q0 + q < nc) {
+                gstore(Hs + (size_t)(c0 + q0 + q) * OUT + c, h);
+                h = fmaf(a[q], h, b[q]);
+            }
+        }
     }
     *hp = h;
 }
@@ -364,112 +396,146 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
     const int s = cbeg[j], e = cend[j];
     float h = Hs[(size_t)j * OUT + c];
     float* row = QVG + (size_t)s * NC + c;
-    for (int p = s; p < e; ++p, row += NC) {
-        const float v = row[OUT], g = row[2 * OUT];
-        h = fmaf(sigmoid_fast(g), h, v);
-        if (!need || need[pair_rec[p]]) row[0] *= h;
+    constexpr int U = 8;         // pairs whose q, v, g are in flight together
+    for (int p0 = s; p0 < e; p0 += U, row += U * NC) {
+        float q[U], v[U], g[U];
+        bool use[U];
+        #pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = p0 + u < e ? u : 0;
+            use[u] = p0 + u < e && (!need || need[pair_rec[p0 + k]]);
+            q[u] = use[u] ? gload(row + (size_t)k * NC) : 0.f;
+            v[u] = gload(row + (size_t)k * NC + OUT);
+            g[u] = gload(row + (size_t)k * NC + 2 * OUT);
+        }
+        #pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (p0 + u < e) {
+                h = fmaf(sigmoid_fast(g[u]), h, v[u]);
+                if (use[u]) gstore(row + (size_t)u * NC, q[u] * h);
+            }
+        }
     }
 }
 
 // ---------------------------------------------------------------------------
 // O: per record y = sum_delta goW[delta]^T qh + residual, fp64 LayerNorm.
-// One workgroup = kTE records; one thread per output channel.
+// One workgroup = 64 records.  The contraction over K = 9*OUT (+ IN) runs in
+// parts at delta boundaries: each part's rows (the records' q*h rows at that
+// delta, zeros where out of bounds; or their inputs for input_proj) are
+// staged in LDS and each wave accumulates its 16-column tiles for all four
+// row tiles by MFMA, with the next part's weights loading meanwhile.
 // ---------------------------------------------------------------------------
 template <int IN, int OUT>
-__global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
+__global__ void __launch_bounds__(256)
 k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
       const float* __restrict__ X, const int* __restrict__ pos,
-      const float* __restrict__ QVG, const float* __restrict__ goW,
-      const float* __restrict__ ip, const float* __restrict__ gamma,
-      const float* __restrict__ beta, float* __restrict__ Y) {
-    constexpr int NC = 3 * OUT;
-    static_assert(IN % 4 == 0 && OUT % 4 == 0, "widths must be multiples of 4");
-    constexpr int VS = OUT > IN ? OUT : IN;
-    __shared__ __align__(16) float vs[kTE][VS];
-    __shared__ float ys[kTE][OUT + 1];
-    __shared__ double stat[kTE][2];
-    __shared__ int rows[kTE];
-    __shared__ int prow[kPatch][kTE];
+      const float* __restrict__ QVG, const float* __restrict__ po,
+      const float* __restrict__ gamma, const float* __restrict__ beta, float* __restrict__ Y) {
+    using O = OutPackD<IN, OUT>;
+    constexpr int NC = 3 * OUT, QST = OUT + 4, TPW = (O::NT + 3) / 4;
+    constexpr int O4 = OUT / 4, I4 = IN / 4;
+    __shared__ __align__(16) float qs[kTM * QST];
+    __shared__ float ys[kTM][OUT + 1];
+    __shared__ double stat[kTM][2];
+    __shared__ int rows[kTM];
+    __shared__ int prow[kPatch][kTM];
     const int n = n_dev ? *n_dev : n_max;
-    const int base = blockIdx.x * kTE;
+    const int base = blockIdx.x * kTM;
     if (base >= n) return;
-    const int cnt = min(kTE, n - base);
-    const int o = threadIdx.x;
-    if (threadIdx.x < kTE)
-        rows[threadIdx.x] = threadIdx.x < cnt
-            ? (list ? list[base + threadIdx.x] : base + threadIdx.x) : -1;
+    const int cnt = min(kTM, n - base);
+    const int tid = threadIdx.x;
+    if (tid < kTM) rows[tid] = tid < cnt ? (list ? list[base + tid] : base + tid) : -1;
     __syncthreads();
-    // pair rows of the tile's records, all deltas, staged once
-    for (int t = threadIdx.x; t < kTE * kPatch; t += blockDim.x) {
-        const int r = t / kPatch, d = t % kPatch;
+    for (int t = tid; t < kTM * kPatch; t += 256) {
+        const int r = t / kPatch, d = t - r * kPatch;
         const int g = rows[r];
         prow[d][r] = g >= 0 ? pos[(size_t)g * kPatch + d] : -1;
     }
-    float acc[kTE];
+    const int lane = tid & 63, wv = tid >> 6, li = lane & 15, lk = lane >> 4;
+    const int mtiles = (cnt + kMT - 1) / kMT;
+    f32x4 acc[TPW][4];
     #pragma unroll
-    for (int r = 0; r < kTE; ++r) acc[r] = 0.f;
-    constexpr int Q4 = OUT / 4;
-    for (int d = 0; d < kPatch; ++d) {
-        __syncthreads();
-        // gather the q*h rows: independent float4 loads
-        for (int t = threadIdx.x; t < kTE * Q4; t += blockDim.x) {
-            const int r = t / Q4, q = t % Q4;
-            const int pr = prow[d][r];
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (pr >= 0) v = *reinterpret_cast<const float4*>(QVG + (size_t)pr * NC + 4 * q);
-            *reinterpret_cast<float4*>(&vs[r][4 * q]) = v;
-        }
-        __syncthreads();
-        if (o < OUT) {
-            const float* w = goW + (size_t)d * OUT * OUT + o;
-            for (int i = 0; i < OUT; i += 4) {
-                const float w0 = w[(size_t)i * OUT], w1 = w[(size_t)(i + 1) * OUT];
-                const float w2 = w[(size_t)(i + 2) * OUT], w3 = w[(size_t)(i + 3) * OUT];
-                #pragma unroll
-                for (int r = 0; r < kTE; ++r) {
-                    const float4 v = *reinterpret_cast<const float4*>(&vs[r][i]);
-                    float a = fmaf(w0, v.x, acc[r]);
-                    a = fmaf(w1, v.y, a);
-                    a = fmaf(w2, v.z, a);
-                    acc[r] = fmaf(w3, v.w, a);
-                }
-            }
-        }
-    }
-    __syncthreads();
-    constexpr int I4 = IN / 4;
-    for (int t = threadIdx.x; t < kTE * I4; t += blockDim.x) {
-        const int r = t / I4, q = t % I4;
-        const int g = rows[r];
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (g >= 0) v = *reinterpret_cast<const float4*>(X + (size_t)g * IN + 4 * q);
-        *reinterpret_cast<float4*>(&vs[r][4 * q]) = v;
-    }
-    __syncthreads();
-    if (o < OUT) {
-        if (ip) {
-            for (int i = 0; i < IN; i += 4) {
-                const float w0 = ip[(size_t)i * OUT + o], w1 = ip[(size_t)(i + 1) * OUT + o];
-                const float w2 = ip[(size_t)(i + 2) * OUT + o], w3 = ip[(size_t)(i + 3) * OUT + o];
-                #pragma unroll
-                for (int r = 0; r < kTE; ++r) {
-                    const float4 v = *reinterpret_cast<const float4*>(&vs[r][i]);
-                    float a = fmaf(w0, v.x, acc[r]);
-                    a = fmaf(w1, v.y, a);
-                    a = fmaf(w2, v.z, a);
-                    acc[r] = fmaf(w3, v.w, a);
-                }
+    for (int u = 0; u < TPW; ++u)
+        #pragma unroll
+        for (int m = 0; m < 4; ++m) acc[u][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto stage = [&](int part) {
+        if (part < kPatch) {
+            for (int t = tid; t < kTM * O4; t += 256) {
+                const int r = t / O4, q = t - r * O4;
+                const int pr = prow[part][r];
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (pr >= 0) v = reinterpret_cast<const float4*>(QVG + (size_t)pr * NC)[q];
+                *reinterpret_cast<float4*>(&qs[r * QST + 4 * q]) = v;
             }
         } else {
-            #pragma unroll
-            for (int r = 0; r < kTE; ++r) acc[r] += vs[r][o];
+            for (int t = tid; t < kTM * O4; t += 256) {
+                const int r = t / O4, q = t - r * O4;
+                const int g = rows[r];
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (g >= 0 && q < I4) v = reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q];
+                *reinterpret_cast<float4*>(&qs[r * QST + 4 * q]) = v;
+            }
         }
+    };
+    auto loadb = [&](int part, float (&b)[TPW][O::SD]) {
         #pragma unroll
-        for (int r = 0; r < kTE; ++r) ys[r][o] = acc[r];
+        for (int u = 0; u < TPW; ++u)
+            if (wv + 4 * u < O::NT) O::load(po, wv + 4 * u, part, lane, b[u]);
+    };
+    auto compute = [&](const float (&b)[TPW][O::SD]) {
+        #pragma unroll
+        for (int u = 0; u < TPW; ++u) {
+            if (wv + 4 * u >= O::NT) continue;
+            #pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                if (m >= mtiles) continue;
+                const float* a = &qs[(m * kMT + li) * QST + lk];
+                f32x4 c = acc[u][m];
+                #pragma unroll
+                for (int s = 0; s < O::SD; ++s)
+                    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s], b[u][s], c, 0, 0, 0);
+                acc[u][m] = c;
+            }
+        }
+    };
+    float b0[TPW][O::SD], b1[TPW][O::SD];
+    loadb(0, b0);
+    #pragma unroll 1
+    for (int part = 0; part < O::PARTS; part += 2) {
+        __syncthreads();                  // previous part's rows fully read
+        stage(part);
+        __syncthreads();
+        if (part + 1 < O::PARTS) loadb(part + 1, b1);
+        compute(b0);
+        if (part + 1 >= O::PARTS) break;
+        __syncthreads();
+        stage(part + 1);
+        __syncthreads();
+        if (part + 2 < O::PARTS) loadb(part + 2, b0);
+        compute(b1);
+    }
+    #pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+        const int nt = wv + 4 * u;
+        if (nt >= O::NT) continue;
+        #pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            if (m >= mtiles) continue;
+            #pragma unroll
+            for (int r = 0; r < 4; ++r) ys[m * kMT + 4 * lk + r][nt * kMT + li] = acc[u][m][r];
+        }
     }
     __syncthreads();
-    if (threadIdx.x < kTE) {
-        const int r = threadIdx.x;
+    if (!O::IP) {
+        for (int t = tid; t < cnt * OUT; t += 256) {
+            const int r = t / OUT, o = t - r * OUT;
+            ys[r][o] += X[(size_t)rows[r] * OUT + o];
+        }
+        __syncthreads();
+    }
+    if (tid < cnt) {
+        const int r = tid;
         double s = 0.0;
         for (int i = 0; i < OUT; ++i) s += (double)ys[r][i];
         const double mean = s / (double)OUT;
@@ -483,12 +549,10 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
         stat[r][1] = 1.0 / sqrt(var + 1e-5);
     }
     __syncthreads();
-    if (o < OUT) {
-        const double gm = (double)gamma[o], bt = (double)beta[o];
-        for (int r = 0; r < cnt; ++r) {
-            const double v = ((double)ys[r][o] - stat[r][0]) * stat[r][1];
-            Y[(size_t)rows[r] * OUT + o] = (float)(v * gm + bt);
-        }
+    for (int t = tid; t < cnt * OUT; t += 256) {
+        const int r = t / OUT, o = t - r * OUT;
+        const double v = ((double)ys[r][o] - stat[r][0]) * stat[r][1];
+        Y[(size_t)rows[r] * OUT + o] = (float)(v * (double)gamma[o] + (double)beta[o]);
     }
 }
 
@@ -644,6 +708,7 @@ struct Workspace {
     hipEvent_t bd_copied = nullptr;    // the last staging copy has been read
     void* temp;
     size_t temp_bytes;
+    float* packed = nullptr;           // fragment-order weight copies (packed_weight_floats_d)
 };
 
 std::mutex g_ws_mu;
@@ -748,6 +813,7 @@ int ensure_workspace(int E, int nkeys) {
         HIPCHK(hipHostMalloc((void**)&w.bd_host, sizeof(BlockDesc) * SSLA_MAX_BLOCKS,
                              hipHostMallocDefault));
         HIPCHK(hipEventCreateWithFlags(&w.bd_copied, hipEventDisableTiming));
+        HIPCHK(hipMalloc(&w.packed, sizeof(float) * packed_weight_floats_d()));
     }
     w.base = base;
     w.bytes = total;
@@ -875,6 +941,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
         return SSLA_OK;
     };
 #define MARK() do { const int rc_ = mark(); if (rc_) return rc_; } while (0)
+    // fragment-order copies of the layer weights for the MFMA kernels
+    PackedWeights pk;
+    HIPCHK(pack_weights_d(cfg->layers[0], w.packed, &pk, st));
     MARK();
     const int bits2 = bits_for(nk2), bits3 = bits_for(nk3);
     size_t tb = w.temp_bytes;
@@ -944,66 +1013,86 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
 
     MARK();
     const LayerWeightsS2S3* L = cfg->layers[0];
-    const unsigned tilesE = grid1(E, kTE);
+    const unsigned tilesE = grid1(E, kTM);
+    constexpr int T2 = ProjPack<SSLA_C2, SSLA_C2>::T, Q2 = ProjPack<SSLA_C2, SSLA_C2>::TQ;
+    constexpr int T3 = ProjPack<SSLA_C3, SSLA_C3>::T, Q3 = ProjPack<SSLA_C3, SSLA_C3>::TQ;
     // ---- L4: 24 -> 48, all records ----------------------------------------
-    hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(192), 0, st, E,
-                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, L[0].qvgIn, w.QVG);
+    hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
+                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, pk.pp[0], w.QVG,
+                       0, ProjPack<SSLA_C1, SSLA_C2>::T);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
+    MARK();
     hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
                        w.coff2, w.ccnt2, w.bd, 0, w.Asum, w.Bsum, w.Hs);
+    MARK();
     hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, (const unsigned char*)nullptr, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_out<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(64), 0, st, E,
-                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, L[0].goW,
-                       L[0].input_proj, L[0].ln_gamma, L[0].ln_beta, w.X1);
+    hipLaunchKernelGGL((k_out<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
+                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, pk.po[0],
+                       L[0].ln_gamma, L[0].ln_beta, w.X1);
     MARK();
     // ---- L5: 48 -> 48, state for all records, output for pass2 ---------------
-    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(192), 0, st, E,
-                       (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, L[1].qvgIn, w.QVG);
+    // v, g for every record; q only for pass2 records (the consumed ones)
+    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
+                       (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, pk.pp[1], w.QVG,
+                       Q2, T2);
+    MARK();
+    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
+                       (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, pk.pp[1], w.QVG, 0, Q2);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
+    MARK();
     hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
                        w.coff2, w.ccnt2, w.bd, 1, w.Asum, w.Bsum, w.Hs);
+    MARK();
     hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, w.pass2, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(64), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, L[1].goW,
-                       (const float*)nullptr, L[1].ln_gamma, L[1].ln_beta, w.X2);
+    hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
+                       (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, pk.po[1],
+                       L[1].ln_gamma, L[1].ln_beta, w.X2);
     MARK();
     // ---- L6: 48 -> 96, pass2 records ------------------------------------------
-    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(320), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, L[2].qvgIn, w.QVG);
+    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
+                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, pk.pp[2], w.QVG,
+                       0, ProjPack<SSLA_C2, SSLA_C3>::T);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
+    MARK();
     hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
                        w.coff3, w.ccnt3, w.bd, 2, w.Asum, w.Bsum, w.Hs);
+    MARK();
     hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, (const unsigned char*)nullptr, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(128), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, L[2].goW,
-                       L[2].input_proj, L[2].ln_gamma, L[2].ln_beta, w.X3);
+    hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
+                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, pk.po[2],
+                       L[2].ln_gamma, L[2].ln_beta, w.X3);
     MARK();
     // ---- L7: 96 -> 96, state for pass2, output for pass3 ----------------------
-    hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(320), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, L[3].qvgIn, w.QVG);
+    hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
+                       (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, pk.pp[3], w.QVG, Q3, T3);
+    MARK();
+    hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
+                       (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, pk.pp[3], w.QVG, 0, Q3);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
+    MARK();
     hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
                        w.coff3, w.ccnt3, w.bd, 3, w.Asum, w.Bsum, w.Hs);
+    MARK();
     hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, w.pass3, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_out<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(128), 0, st, E,
-                       (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, L[3].goW,
-                       (const float*)nullptr, L[3].ln_gamma, L[3].ln_beta, w.X4);
+    hipLaunchKernelGGL((k_out<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
+                       (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, pk.po[3],
+                       L[3].ln_gamma, L[3].ln_beta, w.X4);
     MARK();
     HIPCHK(hipGetLastError());
     // ---- head ------------------------------------------------------------------
