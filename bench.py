@@ -109,7 +109,7 @@ def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20, chunk=64):
     return flops, byts, total_mac
 
 
-def cpu_baseline(stub_dir, rec, budget_s=15.0):
+def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20):
     """The oracle's fp32 path (the generic C++ reference path restated),
     one thread pinned to one core, on the first records of the workload."""
     from oracle import oracle as O
@@ -120,13 +120,13 @@ def cpu_baseline(stub_dir, rec, budget_s=15.0):
         os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
     except (AttributeError, OSError):
         pass
-    st = O.S2S3(layers, 16, 20, 4, head=head)
+    st = O.S2S3(layers, H2, W2, 4, head=head)
     k = 4000
     t0 = time.perf_counter()
     st.run(rec.x[:k], rec.y[:k], rec.feat1[:k], precision=32, want_feat=False, want_head=True)
     rate = k / (time.perf_counter() - t0)
     n = int(min(rec.x.size, max(k, rate * budget_s)))
-    st = O.S2S3(layers, 16, 20, 4, head=head)
+    st = O.S2S3(layers, H2, W2, 4, head=head)
     t0 = time.perf_counter()
     p2, p3, _, _ = st.run(rec.x[:n], rec.y[:n], rec.feat1[:n], precision=32,
                           want_feat=False, want_head=True)
@@ -195,12 +195,64 @@ def live_latency(stub_dir, rate_mev=2.0, duration_s=8.0):
     }
 
 
+def _roofline(per, flops, byts):
+    # dominant single-kernel launch (the ordering phase is several kernels)
+    single = {k: v for k, v in per.items() if k not in ("order", "head")}
+    dom = max(single, key=single.get)
+    kname = PHASE_KERNEL.get(dom, dom)
+    traffic = hbm_traffic(dom)
+    fl, by = flops.get(dom, 0.0), byts.get(dom, 0.0)
+    base = {"kernel": f"{kname} ({dom})", "traffic": traffic, "avg_launch_ms": round(per[dom], 5),
+            "algorithmic_bytes_per_launch": int(by), "algorithmic_flops_per_launch": int(fl)}
+    if by > 0 and fl / by < RIDGE:
+        ach = by / (per[dom] * 1e-3) / 1e9
+        return dict(base, bound="hbm", achieved=round(ach, 2), peak=PEAK_HBM_GBS, unit="GB/s",
+                    frac=round(ach / PEAK_HBM_GBS, 5))
+    ach = fl / (per[dom] * 1e-3) / 1e12
+    return dict(base, bound="mfma", achieved=round(ach, 4), peak=PEAK_FP32_TFLOPS, unit="TFLOP/s",
+                frac=round(ach / PEAK_FP32_TFLOPS, 5))
+
+
+WORKLOADS = {
+    "80x64": dict(height=64, width=80, streams=1, n=200_000, steps=20, warmup=3),
+    "640x480": dict(height=480, width=640, streams=1, n=1_250_000, steps=5, warmup=1),
+    "16streams": dict(height=64, width=80, streams=16, n=200_000, steps=5, warmup=1),
+}
+
+
+def replay_latency(stub_dir, recs, offline_p3, rate_per_stream=125_000.0):
+    """Live multi-stream run: each stream's ring records replayed at the
+    2 Mev/s stream's record rate into its own ring of one persistent kernel;
+    push -> prediction latency per stream and drop drift against the same
+    records' offline decisions."""
+    from ssla_hip import events, live
+    r = live.run_replay(stub_dir, [events.to_records(x) for x in recs], rate_per_stream,
+                        timing_capacity=1 << 18, expect_p3=offline_p3)
+    st = r.streams
+    p50 = [s["push_to_done_p50"] for s in st]
+    p99 = [s["push_to_done_p99"] for s in st]
+    return {
+        "p50": round(float(np.median(p50)), 2), "p99": round(float(max(p99)), 2),
+        "per_stream_p50": [round(v, 2) for v in p50], "per_stream_p99": [round(v, 2) for v in p99],
+        "drop_drift_per_stream": [s["drop_drift"] for s in st],
+        "aggregate_drain_kev_s": round(r.drained / r.duration_s / 1e3, 2),
+        "kernel_status": r.status, "kernel_phase_us_per_batch": _per_batch(r.phase_us),
+        "config": f"live: {len(recs)} rings replayed at {rate_per_stream:.0f} records/s each "
+                  "(post-stage-1 records, published at emit) -> one persistent kernel, one "
+                  "workgroup per stream; latency push -> prediction",
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--n", type=int, default=200_000)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--n", type=int, default=None, help="ring records per stream")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="80x64",
+                    help="80x64: the offline-drain configuration (+ live latency); 640x480: "
+                         "one second of the 20 Mev/s full-resolution stream; 16streams: 16 "
+                         "independent 80x64 instances in one call")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-live", action="store_true", help="skip the live latency run")
@@ -210,79 +262,90 @@ def main() -> int:
         print("bench.py: this build measures one GPU only (one drain instance set per "
               "device, no collectives); run with --gpus 1", file=sys.stderr)
         return 2
+    wl = WORKLOADS[a.workload]
+    n = a.n or wl["n"]
+    steps = a.steps if a.steps is not None else wl["steps"]
+    warmup = a.warmup if a.warmup is not None else wl["warmup"]
+    H0, W0, S = wl["height"], wl["width"], wl["streams"]
+    H2, W2 = H0 // 4, W0 // 4
 
     from ssla_hip import abi, events, hybrid, lib, stub
     lib.load()
     lib.check_layout()
     tmp = tempfile.TemporaryDirectory()
-    stub.write_stub(tmp.name, height=64, width=80, seed=1, tdrop=4)
-    rec = events.blob_records(a.n, seed=1)
-    ring = events.to_records(rec)
+    stub.write_stub(tmp.name, height=H0, width=W0, seed=1, tdrop=4)
+    if a.workload == "640x480":
+        recs = [events.edge_blob_records(n, seed=1)]
+        desc = (f"offline drain of {n} ring records at 640x480 (s2 160x120): 64 moving edge "
+                "blobs + 5% hot pixels (1% of pixels), one second of the 20 Mev/s stream")
+    else:
+        recs = [events.blob_records(n, seed=1 + s, height=H0, width=W0) for s in range(S)]
+        desc = (f"offline drain of {n} ring records at 80x64 (s2 20x16): 8 moving "
+                "Gaussian blobs + 10% background")
+        if S > 1:
+            desc = f"{S} independent instances (stream seeds 1..{S}), each an " + desc
+    desc += ", stub weights seed 1, tdrop 4"
 
-    d = hybrid.Drain.from_weights_dir(tmp.name)
-    d.load_rings([ring], want_head=True)
+    d = hybrid.Drain.from_weights_dir(tmp.name, n_blocks=S)
+    d.load_rings([events.to_records(r) for r in recs], want_head=True)
     nph = len(abi.DRAIN_PHASES)
-    for _ in range(a.warmup):
+    for _ in range(warmup):
         d.reset(sync=False)
         d.run(sync=True)
-    (out,), _ = d.results()
-    owner = np.ones(a.n, np.int32)
-    n_out = int(((out["pass3"] == 1) & (owner == 1)).sum())
+    outs, _ = d.results()
+    n_out = sum(int((o["pass3"] == 1).sum()) for o in outs)
 
     phase = np.zeros(nph, np.float32)
     lib.check(lib.load().ssla_hip_device_synchronize())
     t0 = time.perf_counter()
-    for _ in range(a.steps):
+    for _ in range(steps):
         d.reset(sync=False)
         d.run(sync=True, phase_ms=phase)
     lib.check(lib.load().ssla_hip_device_synchronize())
     dt = time.perf_counter() - t0
-    (out2,), _ = d.results()
-    assert int((out2["pass3"] == 1).sum()) == n_out, "steps did not repeat identical work"
+    outs2, _ = d.results()
+    assert sum(int((o["pass3"] == 1).sum()) for o in outs2) == n_out, \
+        "steps did not repeat identical work"
 
-    ms_step = dt * 1e3 / a.steps
-    value = n_out * a.steps / dt / 1e3
-    ring_rate = a.n * a.steps / dt / 1e3
-    per = {k: float(v) / a.steps for k, v in zip(abi.DRAIN_PHASES, phase)}
-    flops, byts, total_mac = algorithmic_work(rec.x, rec.y, out["pass2"], out["pass3"], owner)
-    # dominant single-kernel launch (the ordering phase is several kernels)
-    single = {k: v for k, v in per.items() if k not in ("order", "head")}
-    dom = max(single, key=single.get)
-    kname = PHASE_KERNEL.get(dom, dom)
-    traffic = hbm_traffic(dom)
-    fl, by = flops.get(dom, 0.0), byts.get(dom, 0.0)
-    if by > 0 and fl / by < RIDGE:
-        ach = by / (per[dom] * 1e-3) / 1e9
-        roof = {"kernel": f"{kname} ({dom})", "bound": "hbm", "achieved": round(ach, 2),
-                "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 5),
-                "traffic": traffic, "avg_launch_ms": round(per[dom], 5),
-                "algorithmic_bytes_per_launch": int(by), "algorithmic_flops_per_launch": int(fl)}
-    else:
-        ach = fl / (per[dom] * 1e-3) / 1e12
-        roof = {"kernel": f"{kname} ({dom})", "bound": "mfma", "achieved": round(ach, 4),
-                "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_TFLOPS, 5),
-                "traffic": traffic, "avg_launch_ms": round(per[dom], 5),
-                "algorithmic_bytes_per_launch": int(by), "algorithmic_flops_per_launch": int(fl)}
+    ms_step = dt * 1e3 / steps
+    value = n_out * steps / dt / 1e3
+    ring_rate = n * S * steps / dt / 1e3
+    per = {k: float(v) / steps for k, v in zip(abi.DRAIN_PHASES, phase)}
+    flops, byts, total_mac = {}, {}, 0
+    for r, o in zip(recs, outs):
+        f_, b_, m_ = algorithmic_work(r.x, r.y, o["pass2"], o["pass3"], np.ones(n, np.int32),
+                                      H2, W2)
+        for k, v in f_.items():
+            flops[k] = flops.get(k, 0.0) + v
+        for k, v in b_.items():
+            byts[k] = byts.get(k, 0.0) + v
+        total_mac += m_
+    roof = _roofline(per, flops, byts)
+    if a.workload != "80x64":
+        roof["traffic"] = None           # the committed PMC summary is of the 80x64 workload
     whole = 2.0 * total_mac / (ms_step * 1e-3) / 1e12
+    hbm = sum(byts.values()) / (ms_step * 1e-3) / 1e9
     res = {
         "metric": METRIC, "value": round(value, 3), "unit": "kev/s", "n_gpus": 1,
-        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 4),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": f"offline drain of {a.n} ring records at 80x64 (s2 20x16): 8 moving "
-                               "Gaussian blobs + 10% background, stub weights seed 1, tdrop 4",
-                   "records": a.n, "instances": 1, "output_producing_per_step": n_out},
+        "config": {"workload": desc, "records": n * S, "instances": S,
+                   "output_producing_per_step": n_out},
         "ring_record_kev_s": round(ring_rate, 2),
         "latency_us": None,
         "whole_drain_tflops": round(whole, 4),
+        "whole_drain_algorithmic_hbm_gbs": round(hbm, 1),
         "phase_ms": {k: round(v, 5) for k, v in per.items()},
         "roofline": roof,
     }
     d.close()
-    if not a.no_live:
+    if a.workload == "80x64" and not a.no_live:
         res["latency_us"] = live_latency(tmp.name, 2.0, a.live_seconds)
+    if a.workload == "16streams" and not a.no_live:
+        res["latency_us"] = replay_latency(tmp.name, recs, [o["pass3"] for o in outs])
     if not a.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(tmp.name, rec, a.cpu_seconds)
+        res["cpu_baseline"] = cpu_baseline(tmp.name, recs[0], a.cpu_seconds, H2, W2)
     tmp.cleanup()
     print(json.dumps(res))
     return 0

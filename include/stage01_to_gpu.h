@@ -76,6 +76,20 @@ void s01g_start_synthetic_blobs(S01gHandle* h, double rate_mev, int pin_core,
                                 unsigned long long seed, int n_blobs,
                                 double sigma_px, double bg_frac);
 
+/* No counterpart in the reference: replays pre-built ring records (post
+ * stage 1, one array per ring, owned by the caller until stop) into n rings
+ * at a paced aggregate rate, round-robin across rings, with the same publish
+ * protocol and t_emit_ns = t_push_ns = publish time -- the source of the
+ * multi-stream live benchmark.  NULL on bad arguments. */
+typedef struct S01gReplay S01gReplay;
+S01gReplay* s01g_replay_start(int n_rings, void* const* ring_bufs,
+                              void* const* ring_heads, unsigned long long ring_mask,
+                              const void* const* records, const int* counts,
+                              double rate_rec_s, int pin_core);
+int  s01g_replay_done(S01gReplay* r);                 /* 1 when all are published */
+unsigned long long s01g_replay_published(S01gReplay* r);
+void s01g_replay_stop(S01gReplay* r);                 /* joins and frees */
+
 #ifdef __cplusplus
 }
 #endif

@@ -554,6 +554,90 @@ unsigned long long s01g_synthetic_n_pushed(S01gHandle* h) {
 
 }  // extern "C"
 
+// ---------------------------------------------------------------------------
+// Replay of ring records into several rings (multi-stream live benchmark)
+// ---------------------------------------------------------------------------
+struct S01gReplay {
+    std::vector<HybridInputRec*> bufs;
+    std::vector<std::uint64_t*> heads;
+    std::vector<const HybridInputRec*> recs;
+    std::vector<int> counts;
+    std::uint64_t mask = 0;
+    double period_ns = 0.0;
+    int core = -1;
+    std::atomic<bool> stop{false}, done{false};
+    std::atomic<std::uint64_t> published{0};
+    std::thread th;
+
+    void run() {
+        ssla::pin_self(core);
+        int most = 0;
+        for (int c : counts) most = std::max(most, c);
+        double next = (double)ssla::mono_ns();
+        for (int k = 0; k < most && !stop.load(std::memory_order_relaxed); ++k) {
+            for (size_t b = 0; b < bufs.size(); ++b) {
+                if (k >= counts[b]) continue;
+                if (period_ns > 0) {
+                    while ((double)ssla::mono_ns() < next) ssla::cpu_relax();
+                    next += period_ns;
+                }
+                const std::uint64_t slot = __atomic_fetch_add(heads[b], 1ull, __ATOMIC_RELAXED);
+                HybridInputRec* d = bufs[b] + (slot & mask);
+                const HybridInputRec& r = recs[b][k];
+                d->t = r.t;
+                d->x = r.x;
+                d->y = r.y;
+                std::memcpy(d->feat1, r.feat1, sizeof(float) * SSLA_C1);
+                const std::uint64_t now = ssla::mono_ns();
+                d->t_push_ns = now;
+                d->t_emit_ns = now;
+                __atomic_store_n(&d->seq_done, slot + 1ull, __ATOMIC_RELEASE);
+                published.fetch_add(1, std::memory_order_relaxed);
+            }
+        }
+        done.store(true, std::memory_order_release);
+    }
+};
+
+extern "C" {
+
+S01gReplay* s01g_replay_start(int n_rings, void* const* ring_bufs, void* const* ring_heads,
+                              unsigned long long ring_mask, const void* const* records,
+                              const int* counts, double rate_rec_s, int pin_core) {
+    if (n_rings <= 0 || n_rings > 64 || !ring_bufs || !ring_heads || !records || !counts)
+        return nullptr;
+    if ((ring_mask & (ring_mask + 1)) != 0) return nullptr;
+    auto* r = new S01gReplay();
+    for (int b = 0; b < n_rings; ++b) {
+        if (!ring_bufs[b] || !ring_heads[b] || counts[b] < 0 || (counts[b] > 0 && !records[b])) {
+            delete r;
+            return nullptr;
+        }
+        r->bufs.push_back(static_cast<HybridInputRec*>(ring_bufs[b]));
+        r->heads.push_back(static_cast<std::uint64_t*>(ring_heads[b]));
+        r->recs.push_back(static_cast<const HybridInputRec*>(records[b]));
+        r->counts.push_back(counts[b]);
+    }
+    r->mask = ring_mask;
+    r->period_ns = rate_rec_s > 0 ? 1e9 / rate_rec_s : 0.0;
+    r->core = pin_core;
+    r->th = std::thread([r]() { r->run(); });
+    return r;
+}
+
+int s01g_replay_done(S01gReplay* r) { return r && r->done.load(std::memory_order_acquire) ? 1 : 0; }
+
+unsigned long long s01g_replay_published(S01gReplay* r) { return r ? r->published.load() : 0ull; }
+
+void s01g_replay_stop(S01gReplay* r) {
+    if (!r) return;
+    r->stop.store(true);
+    if (r->th.joinable()) r->th.join();
+    delete r;
+}
+
+}  // extern "C"
+
 #else
 #include "stage01_capi.h"
 

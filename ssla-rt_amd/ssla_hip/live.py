@@ -175,3 +175,95 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
         prod.shutdown()
         drain.close()
         rings.free()
+
+
+@dataclass
+class ReplayResult:
+    status: int
+    duration_s: float
+    streams: list                      # per stream: dict of counts and latencies (us)
+    phase_us: Optional[np.ndarray] = None
+
+    @property
+    def drained(self) -> int:
+        return sum(s["drained"] for s in self.streams)
+
+
+def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity: int = 1 << 16,
+               timing_capacity: int = 1 << 18, max_batch: int = 32, spin_ns: int = 200,
+               pin_core: Optional[int] = None, profile: bool = True, expect_p3=None,
+               drain_timeout_s: float = 60.0) -> ReplayResult:
+    """Several streams live on one GPU: pre-built ring records (one array per
+    stream) replayed into one ring each at rate_per_stream records/s, one
+    persistent workgroup per stream.  Latency is push -> prediction (the
+    records are published at their emit time).  expect_p3 (optional, one
+    pass-3 flag array per stream) gives each stream's drop drift: records
+    whose timing-slot owner flag differs from it."""
+    from .producer import Replay
+    nb = len(streams)
+    if pin_core is None:
+        pin_core, _ = pick_cores(1)
+    drain = Drain.from_weights_dir(weights_dir, n_blocks=nb)
+    rings = HostRings(nb, ring_capacity)
+    live = rp = None
+    try:
+        drain.alloc_timing(timing_capacity)
+        c = drain.cfg
+        live = LiveDrain(drain, rings, spin_ns=spin_ns, max_batch=max_batch,
+                         idle_timeout_ms=int((drain_timeout_s + 60) * 1000), profile=profile)
+        clk = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_ulonglong * 2).from_address(c.kernel_start_clk[0]))
+        k0 = _spin_nonzero(lambda: int(clk[0]), 30.0)
+        t0_cpu = _now_ns()
+        if not k0:
+            raise RuntimeError("the live kernel did not start")
+        t_start = time.monotonic()
+        rp = Replay([b.ptr for b in rings.bufs], rings.head_ptrs(), ring_capacity - 1, streams,
+                    rate_per_stream * nb, pin_core)
+        t_end = time.monotonic() + sum(s.size for s in streams) / max(1.0, rate_per_stream * nb) \
+            + drain_timeout_s
+        while not rp.done() and time.monotonic() < t_end:
+            time.sleep(0.001)
+        duration = time.monotonic() - t_start
+        counts = [int(s.size) for s in streams]
+        while any(int(rings.done[b]) < counts[b] for b in range(nb)) and time.monotonic() < t_end:
+            time.sleep(0.0005)
+        drained = [int(rings.done[b]) for b in range(nb)]
+        rp.stop()
+        rp = None
+        rings.stop()
+        k1 = _spin_nonzero(lambda: int(clk[1]), 30.0)
+        t1_cpu = _now_ns()
+        status = live.wait()
+        phase = live.phase_us
+        live = None
+        ns_per_tick = (t1_cpu - t0_cpu) / max(1, (k1 - k0)) if k1 else 10.0
+        out = []
+        for b in range(nb):
+            n = min(drained[b], timing_capacity)
+            tv = drain.timing(b)[:n]
+            own = tv["owner"] == 1
+            t_done = t0_cpu + (tv["t_done_clk"].astype(np.float64) - k0) * ns_per_tick
+            lat = (t_done - tv["t_push_ns"].astype(np.float64)) / 1e3
+            kern = (tv["t_done_clk"].astype(np.float64) - tv["t_pop_clk"].astype(np.float64)) \
+                * ns_per_tick / 1e3
+            a = lat[own]
+            s = {"records": counts[b], "drained": drained[b], "output_records": int(own.sum()),
+                 "push_to_done_p50": pct(a, 0.50), "push_to_done_p99": pct(a, 0.99),
+                 "push_to_done_max": float(a.max()) if a.size else float("nan"),
+                 "kernel_p50": pct(kern[own], 0.50)}
+            if expect_p3 is not None:
+                e = np.asarray(expect_p3[b])[:n] == 1
+                s["drop_drift"] = int((own != e).sum())
+            out.append(s)
+        return ReplayResult(status=status, duration_s=duration, streams=out, phase_us=phase)
+    finally:
+        if rp is not None:
+            rp.stop()
+        if live is not None:
+            rings.stop()
+            try:
+                live.wait(60000)
+            except Exception:
+                pass
+        drain.close()
+        rings.free()

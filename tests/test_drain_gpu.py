@@ -255,3 +255,50 @@ def test_full_size_properties(H, stub_dir):
         assert dd <= FEAT_TOL
         for li in range(4):
             assert hidden_close(d.hidden(0, li), h_a[li]), li
+
+
+@pytest.fixture(scope="module")
+def stub_640(tmp_path_factory):
+    from ssla_hip import stub
+    d = tmp_path_factory.mktemp("stub_640x480")
+    stub.write_stub(str(d), height=480, width=640, seed=1, tdrop=4)
+    return str(d)
+
+
+def test_640x480_matches_oracle(H, stub_640):
+    """Full-resolution grid (s2 160 x 120, s3 80 x 60): edge blobs plus hot
+    pixels, whole-ring drain and in-kernel batches against the oracle."""
+    n = 20_000
+    say("640x480", n)
+    npz = O.load_npz(stub_640)
+    layers, head = O.layers_from_npz(npz), O.head_from_npz(npz)
+    rec = events.edge_blob_records(n, seed=2)
+    st = O.S2S3(layers, 120, 160, 4, head=head)
+    p2, p3, feat, ref7 = st.run(rec.x, rec.y, rec.feat1, want_head=True)
+    with H.Drain.from_weights_dir(stub_640) as d:
+        (out,), (h7,) = d.drain([events.to_records(rec)], want_head=True)
+        compare(out, p2, p3, feat, "640x480 whole ring")
+        m = p3 == 1
+        assert np.abs(h7[m] - ref7[m]).max() <= HEAD_TOL
+        for li in range(4):
+            assert hidden_close(d.hidden(0, li), st.H[li]), li
+        d.reset()
+        (out,), (h7,) = d.drain([events.to_records(rec)], want_head=True, batch=32)
+        compare(out, p2, p3, feat, "640x480 batches of 32")
+        assert np.abs(h7[m] - ref7[m]).max() <= HEAD_TOL
+
+
+def test_640x480_full_size_properties(H, stub_640):
+    """One second of the 20 Mev/s full-resolution stream (1.25M records):
+    exact flags and counters against the decision schedule."""
+    n = 1_250_000
+    say("640x480 full size", n)
+    rec = events.edge_blob_records(n, seed=1)
+    d2, d3, td2, td3 = O.decisions(rec.x, rec.y, 120, 160, 4)
+    with H.Drain.from_weights_dir(stub_640) as d:
+        (a,), _ = d.drain([events.to_records(rec)])
+        assert np.array_equal(a["pass2"], d2.astype(np.int32))
+        assert np.array_equal(a["pass3"], d3.astype(np.int32))
+        c2, c3 = d.counters(0)
+        assert np.array_equal(c2, td2) and np.array_equal(c3, td3)
+        say(f"640x480 full size: {int((d3 == 1).sum())} pass3 records")

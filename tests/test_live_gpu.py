@@ -249,3 +249,21 @@ def test_run_live_short(stub_dir):
     assert r.drained == r.ring_records > 0 and r.output_records > 0
     assert 0 < r.lat_us["emit_to_push_p50"] <= r.lat_us["emit_to_done_p50"]
     assert r.lat_us["kernel_p50"] > 0
+
+
+def test_replay_four_streams_live(stub_dir, stub_npz):
+    """Four streams replayed into four rings of one persistent kernel: every
+    record drained, drop drift 0 per stream against the oracle's schedule."""
+    from ssla_hip import live as LV
+    n = 3000
+    say("replay four streams", n)
+    recs = [events.blob_records(n, seed=40 + s) for s in range(4)]
+    expect = [O.decisions(r.x, r.y, 16, 20, 4)[1] for r in recs]
+    res = LV.run_replay(stub_dir, [events.to_records(r) for r in recs], 50_000.0,
+                        ring_capacity=1 << 12, timing_capacity=1 << 12, expect_p3=expect)
+    say("replay:", res.status, [(s["drained"], s["drop_drift"], round(s["push_to_done_p50"], 1))
+                                for s in res.streams])
+    assert res.status == 0
+    for s in res.streams:
+        assert s["drained"] == n and s["drop_drift"] == 0
+        assert s["output_records"] > 0 and 0 < s["push_to_done_p50"] < 1e5

@@ -399,3 +399,33 @@ def test_capi_counts_match_oracle(stub_dir, stub_npz):
     assert st[0] == len(ev) and st[1] == len(halo_to)
     assert st[2] == (p0 == 1).sum() and st[13] == (p1 == 1).sum()
     assert st[14] == st[15] == 0
+
+
+def test_replay_publishes_every_ring_in_order():
+    """s01g_replay_*: each ring receives its records in order with the
+    publish protocol; rings of different lengths; unpaced and paced."""
+    from ssla_hip import events
+    rng = np.random.default_rng(9)
+    recs = []
+    for n in (700, 0, 1234):
+        r = events.Records(np.arange(n, dtype=np.float32), rng.integers(0, 20, n).astype(np.uint16),
+                           rng.integers(0, 16, n).astype(np.uint16),
+                           rng.normal(0, 0.5, (n, 24)).astype(np.float32))
+        recs.append(events.to_records(r))
+    for rate in (0.0, 2e6):
+        rings = _Rings(3, cap=1 << 11)
+        rp = P.Replay(rings.buf_ptrs(), rings.head_ptrs(), rings.cap - 1, recs, rate)
+        t_end = time.monotonic() + 30
+        while not rp.done() and time.monotonic() < t_end:
+            time.sleep(0.001)
+        assert rp.done() and rp.published() == 700 + 1234
+        rp.stop()
+        for k, src in enumerate(recs):
+            got = rings.records(k)
+            assert got.size == src.size
+            for f in ("t", "x", "y", "feat1"):
+                assert np.array_equal(got[f], src[f]), (k, f)
+            assert np.array_equal(got["t_push_ns"], got["t_emit_ns"])
+            assert (got["t_push_ns"] > 0).all() and (np.diff(got["t_push_ns"].astype(np.int64)) >= 0).all()
+    with pytest.raises(RuntimeError):
+        P.Replay([0], [0], 1023, [recs[0]], 0.0)
