@@ -231,6 +231,104 @@ int ssla_hip_persistent_start(const HybridS2S3Config* cfg,
  * the kernel is still running at the timeout (the session stays valid). */
 int ssla_hip_persistent_wait(SslaHipLive* h, int timeout_ms, int* status);
 
+/* ---- prediction grid: host-side consumer ------------------------------
+ * Host code only: these calls make no HIP call and need no GPU.
+ *
+ * Each owned s3 cell of block b holds SSLA_HEAD_OUT raw head floats
+ * [tx, ty, log_w, log_h, obj, cls0, cls1] in cfg->preds[b] and a version
+ * word in cfg->version[b] that counts the pass-3 records the head has
+ * written to the cell (0 = never written; the reference adds 1 per write,
+ * orin/kernels/ssla_s2_s3_head_celled.cuh:900,1498,1750).  While the device
+ * writes a cell it holds SSLA_PRED_BUSY in the word, and the values are
+ * stored between two system-scope fences, so a reader that sees the same
+ * word (busy bit clear) before and after copying a cell has a whole cell.
+ * Counts wrap at 2^31. */
+#define SSLA_PRED_BUSY 0x80000000u
+
+/* Copies n_cells cells (cols floats + version each) torn-free: a cell is
+ * retried up to max_tries times (>= 1).  Returns the number of cells that
+ * stayed busy or kept changing (their version_out has SSLA_PRED_BUSY set
+ * and preds_out holds the last copy), or a negative SSLA_ERR_*.  Replaces
+ * the direct reads of the pinned views (orin/hybrid_runner_multi.py:648-656,
+ * orin/orin/multi_block.py:229-253). */
+int ssla_hip_preds_snapshot(const float* preds, const unsigned* version, int n_cells, int cols,
+                            float* preds_out, unsigned* version_out, int max_tries);
+
+/* decode_yolox_cell's transform (vendor/openeva/heads/async_yolox.h:189-196)
+ * on n_cells raw rows of cols (>= 5) floats: cell i sits at grid
+ * (gx0 + i % grid_w, gy0 + i / grid_w) and becomes
+ * [(tx+gx)*stride_w, (ty+gy)*stride_h, exp(log_w)*stride_w,
+ *  exp(log_h)*stride_h, obj, cls...] (logits stay raw). */
+int ssla_hip_decode_cells(const float* raw, int n_cells, int cols, int grid_w, int gx0, int gy0,
+                          int stride_w, int stride_h, float* out);
+
+/* The whole s3 grid as the CPU pipeline's DetectionOutput holds it
+ * (src/ssla_kernels.cpp:934-966): out is (H3*W3, SSLA_HEAD_OUT), row
+ * gy*W3 + gx, decoded as ssla_hip_decode_cells.  Cells of every block's
+ * owned box with version > 0 come from a torn-free read of cfg->preds[b];
+ * every other cell holds zero_row (the head's raw output for an all-zero
+ * feature, ssla_hip_model_head_row), as the CPU pipeline prepopulates them
+ * (src/ssla_kernels.cpp:966-987).  Returns the number of torn cells (left at
+ * zero_row) or a negative SSLA_ERR_*. */
+int ssla_hip_grid_decode(const HybridS2S3Config* cfg, const float* zero_row, int stride_w,
+                         int stride_h, int max_tries, float* out);
+
+/* The live demo's box collection for one block
+ * (orin/hybrid_runner_multi.py:163-207), in fp32: over the s3w*s3h raw rows
+ * (row-major over the block's owned s3 box at (s3x_lo, s3y_lo)),
+ * obj = sigmoid(raw[4]); cells with obj >= obj_thresh give the box
+ *   cx = s3x*8 + 4 + tx*8, cy = s3y*8 + 4 + ty*8,
+ *   w = clip(exp(log_w)*8, 2, W_full), h = clip(exp(log_h)*8, 2, H_full),
+ *   [(cx - w/2)*scale, (cy - h/2)*scale, w*scale, h*scale]
+ * and score obj, in cell order.  *max_seen is raised to the largest obj
+ * seen (the caller initialises it).  Returns the number of cells kept
+ * (boxes past max_boxes are counted, not written). */
+int ssla_hip_collect_boxes(const float* raw, int s3w, int s3h, int s3x_lo, int s3y_lo, float scale,
+                           float obj_thresh, int W_full, int H_full, float* boxes_xywh,
+                           float* scores, int max_boxes, float* max_seen);
+
+/* Host-side YOLOX head on one 96-channel s3 feature: out[0..6] = raw
+ * [reg4, obj, cls2] with BatchNorm folded as the device head has it.  With
+ * an all-zero feature this is the row the CPU pipeline prepopulates
+ * (src/ssla_kernels.cpp:966-987).  SSLA_ERR_STATE if the model has no head. */
+int ssla_hip_model_head_row(const SslaHipModel* m, const float* feat, float* out);
+/* The same from a weight directory's head (needs no GPU). */
+int ssla_hip_head_row(const char* weights_dir, const float* feat, float* out);
+
+/* ---- OEVA head-grid dumps (include/oracle.h:10-18) --------------------
+ * Little-endian file: uint32 magic 0x4F455641 ("OEVA"), uint32 version 1,
+ * uint32 num_anchors, uint32 cols, uint32 num_checkpoints, then per
+ * checkpoint uint64 event_idx and float[num_anchors * cols]. */
+#define SSLA_OEVA_MAGIC   0x4F455641u
+#define SSLA_OEVA_VERSION 1u
+
+/* Writes n_cp checkpoints (preds: n_cp * num_anchors * cols floats) in one
+ * go; OracleRecorder::save (include/oracle.h:57-77). */
+int ssla_hip_oeva_write(const char* path, unsigned num_anchors, unsigned cols, unsigned n_cp,
+                        const unsigned long long* event_idx, const float* preds);
+/* out3 = {num_anchors, cols, num_checkpoints}.  SSLA_ERR_IO when the file
+ * cannot be opened, SSLA_ERR_FORMAT on a short header or a bad
+ * magic/version (include/oracle.h:103-116). */
+int ssla_hip_oeva_header(const char* path, unsigned* out3);
+/* Reads every checkpoint (cap_cp >= num_checkpoints); a truncated body
+ * leaves the checkpoints past the short read zero-filled, as
+ * include/oracle.h:117-121 does. */
+int ssla_hip_oeva_read(const char* path, unsigned long long* event_idx, float* preds,
+                       unsigned cap_cp);
+
+typedef struct SslaHipOevaDiff {
+    int    ok;                /* shapes, checkpoint counts and indices agree */
+    size_t n_cp;
+    double max_abs_delta;
+    size_t n_mismatched_cp;   /* checkpoints with any |delta| > tol_abs */
+} SslaHipOevaDiff;
+
+/* deploy::diff_dumps (include/oracle.h:90-150): ok = 0 on a shape or count
+ * mismatch (nothing compared) or at the first checkpoint whose event_idx
+ * differs (comparison stops there); NaN deltas are passed over. */
+int ssla_hip_oeva_diff(const char* path_a, const char* path_b, double tol_abs,
+                       SslaHipOevaDiff* out);
+
 #ifdef __cplusplus
 }
 #endif

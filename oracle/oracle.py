@@ -378,4 +378,13 @@ def load_ref() -> Optional[ctypes.CDLL]:
     L.ref_lru_step.argtypes = [_FP, _FP, _FP, _FP, _FP, ctypes.c_int]
     L.ref_mm.restype = ctypes.c_int
     L.ref_mm.argtypes = [_FP, ctypes.c_int, ctypes.c_int, _FP, ctypes.c_int, _FP]
+    if hasattr(L, "ref_oeva_record"):
+        L.ref_oeva_record.restype = ctypes.c_int
+        L.ref_oeva_record.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_ulonglong, ctypes.c_int,
+                                      ctypes.POINTER(ctypes.c_ulonglong), _FP,
+                                      ctypes.POINTER(ctypes.c_int)]
+        L.ref_oeva_diff.restype = ctypes.c_int
+        L.ref_oeva_diff.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_double,
+                                    ctypes.POINTER(ctypes.c_double)]
     return L

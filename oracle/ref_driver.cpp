@@ -13,6 +13,8 @@
 //   ref_layernorm   openeva::prim::layernorm_ct  vendor/openeva/prim/layernorm.h:40-60
 //   ref_lru_step    openeva::prim::lru_step      vendor/openeva/prim/rnn.h:79-90
 //   ref_mm          openeva::prim::mm            vendor/openeva/prim/matmul.h:22-38
+//   ref_oeva_record deploy::OracleRecorder       include/oracle.h:35-89
+//   ref_oeva_diff   deploy::diff_dumps           include/oracle.h:90-150
 #include <cstring>
 #include <exception>
 #include <string>
@@ -25,6 +27,7 @@
 #include "openeva/prim/matmul.h"
 #include "openeva/prim/rnn.h"
 #include "src/weights_loader.h"
+#include "include/oracle.h"
 
 extern "C" {
 
@@ -106,6 +109,43 @@ int ref_mm(const float* B, int bo, int bi, const float* A, int ai, float* C) {
         std::vector<float> va(A, A + static_cast<std::size_t>(bi) * ai);
         const auto vc = openeva::prim::mm(vb, bo, bi, va, bi, ai);
         std::memcpy(C, vc.data(), sizeof(float) * vc.size());
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// Feeds n (event_idx, predictions) pairs to an OracleRecorder(num_anchors,
+// cols, every, path) as DetectionOutputs of num_anchors*cols floats
+// (preds + i*per) -- or of `sizes[i]` floats when sizes is non-NULL -- then
+// saves.  Returns the number of checkpoints kept, or -1.
+int ref_oeva_record(const char* path, int num_anchors, int cols, unsigned long long every, int n,
+                    const unsigned long long* event_idx, const float* preds, const int* sizes) {
+    try {
+        deploy::OracleRecorder rec(num_anchors, cols, every, path);
+        const std::size_t per = static_cast<std::size_t>(num_anchors) * cols;
+        for (int i = 0; i < n; ++i) {
+            openeva::DetectionOutput det;
+            const std::size_t sz = sizes ? static_cast<std::size_t>(sizes[i]) : per;
+            det.predictions.shape = {sz};
+            det.predictions.data.assign(preds + i * per, preds + i * per + sz);
+            rec.record(event_idx[i], openeva::ModelOutput{det});
+        }
+        rec.save();
+        return static_cast<int>(rec.num_checkpoints());
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// out = {ok, n_cp, max_abs_delta, n_mismatched_cp}; returns 0 or -1 (throw).
+int ref_oeva_diff(const char* a, const char* b, double tol_abs, double* out) {
+    try {
+        const deploy::DiffReport r = deploy::diff_dumps(a, b, tol_abs);
+        out[0] = r.ok ? 1.0 : 0.0;
+        out[1] = static_cast<double>(r.n_cp);
+        out[2] = r.max_abs_delta;
+        out[3] = static_cast<double>(r.n_mismatched_cp);
         return 0;
     } catch (const std::exception&) {
         return -1;

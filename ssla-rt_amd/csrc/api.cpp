@@ -148,6 +148,33 @@ PackedHead pack_head(const std::map<std::string, NpzTensor>& W, int n_cls) {
     return h;
 }
 
+// Raw head row [reg4, obj, cls2] of one 96-channel feature in fp32, the
+// device head's arithmetic (1x1 convs with BN folded, SiLU, three preds).
+void head_row_host(const PackedHead& h, const float* x, float* out) {
+    const int C = 96;
+    float cf[C], rf[C];
+    for (int o = 0; o < C; ++o) {
+        float a = h.cls_conv_b[o], r = h.reg_conv_b[o];
+        for (int i = 0; i < C; ++i) {
+            a += x[i] * h.cls_conv_W[(size_t)i * C + o];
+            r += x[i] * h.reg_conv_W[(size_t)i * C + o];
+        }
+        cf[o] = a / (1.0f + std::exp(-a));
+        rf[o] = r / (1.0f + std::exp(-r));
+    }
+    auto pred = [&](const float* f, const std::vector<float>& Wt, const std::vector<float>& b,
+                    int rows, float* dst) {
+        for (int k = 0; k < rows; ++k) {
+            float a = b[k];
+            for (int i = 0; i < C; ++i) a += f[i] * Wt[(size_t)i * rows + k];
+            dst[k] = a;
+        }
+    };
+    pred(rf, h.reg_pred_W, h.reg_pred_b, 4, out);
+    pred(rf, h.obj_pred_W, h.obj_pred_b, 1, out + 4);
+    pred(cf, h.cls_pred_W, h.cls_pred_b, 2, out + 5);
+}
+
 }  // namespace
 }  // namespace ssla
 
@@ -158,6 +185,7 @@ struct SslaHipModel {
     LayerWeightsS2S3 layers[4] = {};
     const float* head[10] = {};   // cls_conv W,b, cls_pred W,b, reg_conv W,b, reg_pred W,b, obj W,b
     SslaHipModelInfo info = {};
+    PackedHead host_head;         // host copy for ssla_hip_model_head_row
 };
 
 extern "C" {
@@ -349,7 +377,37 @@ int ssla_hip_model_load(const char* dir, SslaHipModel** out) {
         m->layers[li].ln_beta = ptrs[li * 5 + 4];
     }
     for (int k = 0; k < 10; ++k) m->head[k] = ptrs[20 + k];
+    m->host_head = std::move(head);
     *out = m;
+    return SSLA_OK;
+}
+
+int ssla_hip_model_head_row(const SslaHipModel* m, const float* feat, float* out) {
+    if (!m || !feat || !out) { set_error("model_head_row: null argument"); return SSLA_ERR_ARG; }
+    if (!m->info.has_head) { set_error("model_head_row: the model has no head"); return SSLA_ERR_STATE; }
+    head_row_host(m->host_head, feat, out);
+    return SSLA_OK;
+}
+
+int ssla_hip_head_row(const char* weights_dir, const float* feat, float* out) {
+    if (!weights_dir || !feat || !out) { set_error("head_row: null argument"); return SSLA_ERR_ARG; }
+    std::map<std::string, NpzTensor> W;
+    try {
+        W = read_npz(weights_dir);
+    } catch (const std::exception& e) {
+        set_error(e.what());
+        return SSLA_ERR_IO;
+    }
+    if (!W.count("head/cls_convs/0/0/weight")) {
+        set_error("head_row: weights.npz has no head");
+        return SSLA_ERR_STATE;
+    }
+    try {
+        head_row_host(pack_head(W, 2), feat, out);
+    } catch (const std::exception& e) {
+        set_error(e.what());
+        return SSLA_ERR_FORMAT;
+    }
     return SSLA_OK;
 }
 

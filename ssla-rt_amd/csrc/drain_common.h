@@ -30,4 +30,31 @@ __device__ __forceinline__ float sigmoid_fast(float x) {
     return __fdividef(1.0f, 1.0f + __expf(-x));
 }
 
+// Bit 31 of a prediction cell's version marks a write in progress.
+constexpr unsigned kPredBusy = 0x80000000u;
+
+// Publishes one prediction-grid cell (fine-grained host memory) for
+// concurrent host readers: the version's busy bit is set, the seven values
+// are stored between two system-scope fences, and the version ends at
+// old + count with the bit clear -- so a reader that sees the same version
+// before and after copying a cell, without the bit, has a whole cell.
+__device__ __forceinline__ void publish_pred(float* preds7, unsigned* version, const float* v7,
+                                             unsigned count) {
+    unsigned old = 0;
+    if (version) {
+        old = __hip_atomic_load(version, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) & ~kPredBusy;
+        __hip_atomic_store(version, old | kPredBusy, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __threadfence_system();
+    }
+    if (preds7) {
+        #pragma unroll
+        for (int q = 0; q < 7; ++q) preds7[q] = v7[q];
+    }
+    if (version) {
+        __threadfence_system();
+        __hip_atomic_store(version, (old + count) & ~kPredBusy, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
 }  // namespace ssla

@@ -602,11 +602,8 @@ __device__ __forceinline__ void batch_head(Lds& S, int B, const LiveDesc& d, con
         const int w = s.s3_owned_hi - s.s3_owned_lo, h = s.s3_owned_y_hi - s.s3_owned_y_lo;
         if (last && hx >= 0 && hx < w && hy >= 0 && hy < h) {
             const int idx = hy * w + hx;
-            if (d.preds) {
-                #pragma unroll
-                for (int k = 0; k < 7; ++k) d.preds[(size_t)idx * 7 + k] = S.H7[e][k];
-            }
-            if (d.version) d.version[idx] += (unsigned)count;
+            publish_pred(d.preds ? d.preds + (size_t)idx * 7 : nullptr,
+                         d.version ? d.version + idx : nullptr, S.H7[e], (unsigned)count);
         }
     }
     __syncthreads();

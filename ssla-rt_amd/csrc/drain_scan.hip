@@ -646,12 +646,11 @@ __global__ void k_pred_write(const int* __restrict__ n_dev, const int* __restric
     const int w = s.s3_owned_hi - s.s3_owned_lo, h = s.s3_owned_y_hi - s.s3_owned_y_lo;
     if (hx < 0 || hx >= w || hy < 0 || hy >= h) return;
     const int idx = hy * w + hx;
-    if (bd[b].preds) {
-        float* dst = bd[b].preds + (size_t)idx * 7;
-        #pragma unroll
-        for (int q = 0; q < 7; ++q) dst[q] = H7[(size_t)g * 7 + q];
-    }
-    if (bd[b].version) bd[b].version[idx] += (unsigned)count[k];
+    float v7[7];
+    #pragma unroll
+    for (int q = 0; q < 7; ++q) v7[q] = H7[(size_t)g * 7 + q];
+    publish_pred(bd[b].preds ? bd[b].preds + (size_t)idx * 7 : nullptr,
+                 bd[b].version ? bd[b].version + idx : nullptr, v7, (unsigned)count[k]);
 }
 
 // Output slots (...celled.cuh:1233-1247 conventions) and raw head rows.

@@ -113,6 +113,16 @@ class SslaHipLiveOpts(ctypes.Structure):
                 ("phase_us", ctypes.POINTER(ctypes.c_double))]
 
 
+class SslaHipOevaDiff(ctypes.Structure):
+    _fields_ = [("ok", ctypes.c_int), ("n_cp", ctypes.c_size_t),
+                ("max_abs_delta", ctypes.c_double), ("n_mismatched_cp", ctypes.c_size_t)]
+
+
+PRED_BUSY = 0x80000000
+OEVA_MAGIC = 0x4F455641
+OEVA_VERSION = 1
+
+
 DRAIN_PHASES = ("order",
                 "L4.proj", "L4.sum", "L4.carry", "L4.apply", "L4.out",
                 "L5.proj_vg", "L5.proj_q", "L5.sum", "L5.carry", "L5.apply", "L5.out",

@@ -15,7 +15,7 @@ from typing import List, Optional, Sequence
 
 import numpy as np
 
-from . import abi, lib
+from . import abi, grid, lib
 from .events import GPU_LAYER_IO, RawLayer
 
 
@@ -200,13 +200,38 @@ class Drain:
         upload_ptr(self.cfg.tdrop_s2[blk], td2.astype(np.uint8))
         upload_ptr(self.cfg.tdrop_s3[blk], td3.astype(np.uint8))
 
-    def preds(self, blk: int):
+    def preds(self, blk: int, max_tries: int = 64):
+        """Torn-free copy of block blk's prediction cells: (preds (n, 7),
+        version (n,)).  Raises if a cell stays busy for max_tries reads."""
         s = self.cfg.strip[blk]
         n = (s.s3_owned_hi - s.s3_owned_lo) * (s.s3_owned_y_hi - s.s3_owned_y_lo)
         if not self.cfg.preds[blk]:
             return None, None
-        return (download_ptr(self.cfg.preds[blk], np.float32, n * 7).reshape(n, 7),
-                download_ptr(self.cfg.version[blk], np.uint32, n))
+        p, v, torn = grid.snapshot_ptr(self.cfg.preds[blk], self.cfg.version[blk], n,
+                                       abi.HEAD_OUT, max_tries)
+        if torn:
+            raise lib.SslaHipError(f"preds: {torn} cells of block {blk} kept changing")
+        return p, v
+
+    def zero_row(self) -> np.ndarray:
+        """The head's raw output for an all-zero feature (the value of a cell
+        no record has reached yet in the CPU pipeline)."""
+        if not self._model:
+            raise lib.SslaHipError("zero_row: no model loaded (random layers have no head)")
+        x = np.zeros(96, np.float32)
+        out = np.zeros(abi.HEAD_OUT, np.float32)
+        fp = ctypes.POINTER(ctypes.c_float)
+        lib.check(lib.load().ssla_hip_model_head_row(self._model, x.ctypes.data_as(fp),
+                                                     out.ctypes.data_as(fp)), "model_head_row")
+        return out
+
+    def head_grid(self, stride: int = 8, max_tries: int = 64) -> np.ndarray:
+        """Decoded (H3*W3, 7) grid, row gy*W3 + gx, as the CPU pipeline's
+        detection output holds it."""
+        out, torn = grid.grid_decode(self.cfg, self.zero_row(), stride, stride, max_tries)
+        if torn:
+            raise lib.SslaHipError(f"head_grid: {torn} cells kept changing")
+        return out
 
     def reset(self, stream: int = 0, sync: bool = True) -> None:
         L = lib.load()
@@ -278,6 +303,25 @@ class Drain:
         self.load_rings(records, want_head=want_head)
         self.run(batch=batch)
         return self.results()
+
+    def drain_recorded(self, records: Sequence[np.ndarray], recorder: "grid.OracleRecorder",
+                       stride: int = 8, batch: int = 0) -> None:
+        """Drain the rings with the head grid recorded after ring position i
+        for every i the recorder wants (i % every == 0), as the reference's
+        equivalence harness records after each step (include/oracle.h:42-53,
+        src/legacy/schemes/s1_reference.cpp:170-180).  Every ring is cut at
+        the same positions; records past the last checkpoint are drained too."""
+        n = max((len(r) for r in records), default=0)
+        cuts = [i + 1 for i in range(n) if recorder.wants(i)]
+        if not cuts or cuts[-1] != n:
+            cuts.append(n)
+        lo = 0
+        for hi in cuts:
+            if hi > lo:
+                self.drain([r[lo:hi] for r in records], batch=batch)
+            if hi >= 1 and recorder.wants(hi - 1):
+                recorder.record(hi - 1, self.head_grid(stride))
+            lo = hi
 
     def drain_with_clocks(self, records: Sequence[np.ndarray]):
         """ssla_hip_drain_n with batch_clks: in-kernel batches of 8 records and

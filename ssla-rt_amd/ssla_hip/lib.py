@@ -19,6 +19,7 @@ SSLA_OK = 0
 
 # name -> (restype, argtypes); exactly the entry points of include/ssla_hip.h
 _VP, _I, _LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
+_FP, _UP = ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_uint)
 _SIGNATURES = {
     "ssla_hip_last_error": (ctypes.c_char_p, []),
     "ssla_hip_abi_layout": (_I, [ctypes.POINTER(_LL), _I]),
@@ -56,6 +57,20 @@ _SIGNATURES = {
                                        ctypes.POINTER(_VP), ctypes.c_uint,
                                        ctypes.POINTER(abi.SslaHipLiveOpts), ctypes.POINTER(_VP)]),
     "ssla_hip_persistent_wait": (_I, [_VP, _I, ctypes.POINTER(_I)]),
+    "ssla_hip_preds_snapshot": (_I, [_FP, _UP, _I, _I, _FP, _UP, _I]),
+    "ssla_hip_decode_cells": (_I, [_FP, _I, _I, _I, _I, _I, _I, _I, _FP]),
+    "ssla_hip_grid_decode": (_I, [ctypes.POINTER(abi.HybridS2S3Config), _FP, _I, _I, _I, _FP]),
+    "ssla_hip_collect_boxes": (_I, [_FP, _I, _I, _I, _I, ctypes.c_float, ctypes.c_float, _I, _I,
+                                    _FP, _FP, _I, _FP]),
+    "ssla_hip_model_head_row": (_I, [_VP, _FP, _FP]),
+    "ssla_hip_head_row": (_I, [ctypes.c_char_p, _FP, _FP]),
+    "ssla_hip_oeva_write": (_I, [ctypes.c_char_p, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint,
+                                 ctypes.POINTER(ctypes.c_ulonglong), _FP]),
+    "ssla_hip_oeva_header": (_I, [ctypes.c_char_p, _UP]),
+    "ssla_hip_oeva_read": (_I, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_ulonglong), _FP,
+                                ctypes.c_uint]),
+    "ssla_hip_oeva_diff": (_I, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_double,
+                                ctypes.POINTER(abi.SslaHipOevaDiff)]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -148,6 +148,41 @@ def test_stub_weights_blob_stream_with_head(H, stub_dir, stub_npz):
                 assert np.all(preds[cell] == 0)
 
 
+def test_head_grid_dump_matches_oracle(H, stub_dir, stub_npz, tmp_path):
+    """OEVA equivalence dump (include/oracle.h) of the decoded head grid,
+    recorded every 1000 ring records from the GPU drain, against the same
+    dump built from the oracle's per-record head outputs (last pass-3 write
+    per s3 cell over a grid prepopulated with the zero-feature row)."""
+    from ssla_hip import grid
+    n, every, W3 = 6000, 1000, 10
+    say("head grid dump", n, every)
+    rec = events.blob_records(n, seed=2)
+    head = O.head_from_npz(stub_npz)
+    gpu_path, ora_path = tmp_path / "gpu.oeva", tmp_path / "oracle.oeva"
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        zero = d.zero_row()
+        r = grid.OracleRecorder(80, 7, every, str(gpu_path))
+        d.drain_recorded([events.to_records(rec)], r)
+        r.save()
+    zero_ref = O.head_raw(head, np.zeros(96, np.float32))
+    assert np.abs(zero - zero_ref).max() <= HEAD_TOL
+    st = O.S2S3(O.layers_from_npz(stub_npz), 16, 20, 4, head=head)
+    p2, p3, feat, ref7 = st.run(rec.x, rec.y, rec.feat1, want_head=True)
+    c3 = (rec.y.astype(int) >> 1) * W3 + (rec.x >> 1)
+    raw = np.tile(zero_ref, (80, 1)).astype(np.float32)
+    idx, cps = [], []
+    for i in range(n):
+        if p3[i] == 1:
+            raw[c3[i]] = ref7[i]
+        if i % every == 0:
+            idx.append(i)
+            cps.append(grid.decode_cells(raw, grid_w=W3))
+    grid.write_dump(ora_path, 80, 7, idx, cps)
+    rep = grid.diff_dumps(ora_path, gpu_path, tol_abs=1e-3)
+    say(f"head grid dump: {rep}")
+    assert rep.ok and rep.n_cp == 6 and rep.n_mismatched_cp == 0
+
+
 def test_sixteen_streams(H, stub_dir, stub_npz):
     n = 4000
     say("sixteen_streams", n)

@@ -155,6 +155,36 @@ def test_live_single_stream(H, stub_dir, stub_npz):
         rings.free()
 
 
+def test_live_preds_read_while_running(H, stub_dir, stub_npz):
+    """The host reads the prediction grid between pushes while the live
+    kernel writes it: every snapshot is whole (no cell stays busy), versions
+    never go back, and the last snapshot matches the oracle."""
+    n = 3000
+    say("live preds read while running", n)
+    rec = events.blob_records(n, seed=17)
+    recs = events.to_records(rec)
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        rings = H.HostRings(1, capacity=1024)
+        live = H.LiveDrain(d, rings, idle_timeout_ms=15000)
+        snaps = 0
+        try:
+            prev = np.zeros(80, np.uint32)
+            for lo in range(0, n, 150):
+                _produce(rings, 0, recs[lo:lo + 150])
+                preds, version = d.preds(0)      # raises if a cell stays busy
+                assert np.all(version >= prev)
+                assert np.all(np.isfinite(preds[version > 0]))
+                prev = version
+                snaps += 1
+            _wait_done(rings, 0, n)
+        finally:
+            status = live.stop()
+        assert status == 0 and snaps == 20
+        st, p2, p3, feat, ref7 = oracle_run(stub_npz, rec)
+        check_preds(*d.preds(0), rec, p3, ref7)
+        rings.free()
+
+
 def test_live_four_streams(H, stub_dir, stub_npz):
     n = 1500
     say("live four streams", n)
