@@ -19,7 +19,8 @@ dominant kernel from HIP events on the drain's stream, and the CPU baseline
 The metric's latency half comes from the live pipeline, run after the timed
 region: the host producer (6 shards, halo 2) fed by its paced synthetic
 source at 2.0 Mev/s with the same blob distribution, fine-grained rings, the
-persistent drain kernel, for 8 s; emit -> prediction p50 / p99 / max of the
+persistent drain kernel over 8 GPU blocks (the reference's default 2 x 4
+strip topology with a 2-cell halo), for 8 s; emit -> prediction p50 / p99 / max of the
 output-producing records, GPU clocks put on the host clock by the kernel's
 start / exit stamps.
 """
@@ -172,9 +173,10 @@ def _per_batch(phase_us):
     return {k: round(float(phase_us[i]) / nb, 2) for i, k in enumerate(abi.BATCH_PHASES[:25])}
 
 
-def live_latency(stub_dir, rate_mev=2.0, duration_s=8.0):
+def live_latency(stub_dir, rate_mev=2.0, duration_s=8.0, gpu_blocks=8):
     from ssla_hip import live
-    r = live.run_live(stub_dir, rate_mev=rate_mev, duration_s=duration_s, n_shards=6, halo=2)
+    r = live.run_live(stub_dir, rate_mev=rate_mev, duration_s=duration_s, n_shards=6, halo=2,
+                      gpu_blocks=gpu_blocks)
     lat = r.lat_us
     return {
         "p50": round(lat["emit_to_done_p50"], 2), "p99": round(lat["emit_to_done_p99"], 2),
@@ -190,7 +192,8 @@ def live_latency(stub_dir, rate_mev=2.0, duration_s=8.0):
         "records": r.ring_records, "drained": r.drained, "kernel_status": r.status,
         "kernel_phase_us_per_batch": _per_batch(r.phase_us),
         "config": f"live: paced blob source {rate_mev} Mev/s -> 6 host shards (halo 2) -> "
-                  f"fine-grained ring -> persistent kernel, {r.duration_s:.1f} s; "
+                  f"{r.gpu_blocks} GPU blocks (owned s2 strips, halo 2), one fine-grained ring "
+                  f"and persistent workgroup each, {r.duration_s:.1f} s; "
                   f"{r.synth_events} events emitted",
     }
 
@@ -257,6 +260,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-live", action="store_true", help="skip the live latency run")
     ap.add_argument("--live-seconds", type=float, default=8.0)
+    ap.add_argument("--live-blocks", type=int, default=8, choices=[1, 2, 4, 8],
+                    help="GPU blocks (owned strips) of the live run")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (one drain instance set per "
@@ -341,7 +346,7 @@ def main() -> int:
     }
     d.close()
     if a.workload == "80x64" and not a.no_live:
-        res["latency_us"] = live_latency(tmp.name, 2.0, a.live_seconds)
+        res["latency_us"] = live_latency(tmp.name, 2.0, a.live_seconds, a.live_blocks)
     if a.workload == "16streams" and not a.no_live:
         res["latency_us"] = replay_latency(tmp.name, recs, [o["pass3"] for o in outs])
     if not a.no_cpu_baseline:

@@ -130,11 +130,22 @@ class Drain:
     # -- construction ---------------------------------------------------------
     @classmethod
     def from_weights_dir(cls, weights_dir: str, n_blocks: int = 1,
-                         with_preds: bool = True) -> "Drain":
+                         with_preds: bool = True,
+                         strips: Optional[Sequence[tuple]] = None) -> "Drain":
+        """strips: per block (x_lo, x_hi, y_lo, y_hi) owned s2 box (e.g.
+        topology.grid_topology(...)[b].owned); default the whole grid."""
         d = cls()
         L = lib.load()
         lib.check(L.ssla_hip_model_load(weights_dir.encode(), ctypes.byref(d._model)), "model_load")
         lib.check(L.ssla_hip_config_bind(d._model, n_blocks, ctypes.byref(d.cfg)), "config_bind")
+        if strips is not None:
+            if len(strips) != n_blocks:
+                raise ValueError("from_weights_dir: one strip per block")
+            for b, (x_lo, x_hi, y_lo, y_hi) in enumerate(strips):
+                s = d.cfg.strip[b]
+                s.owned_lo, s.owned_hi, s.owned_y_lo, s.owned_y_hi = x_lo, x_hi, y_lo, y_hi
+                s.s3_owned_lo, s.s3_owned_hi = x_lo >> 1, x_hi >> 1
+                s.s3_owned_y_lo, s.s3_owned_y_hi = y_lo >> 1, y_hi >> 1
         for b in range(n_blocks):
             lib.check(L.ssla_hip_state_alloc(ctypes.byref(d.cfg), b), "state_alloc")
             d._state_blocks.append(b)

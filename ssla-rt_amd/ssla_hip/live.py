@@ -19,9 +19,21 @@ from typing import Dict, Optional
 
 import numpy as np
 
-from . import abi
+from . import abi, lib
 from .hybrid import Drain, HostRings, LiveDrain
 from .producer import S01gAPI
+from .topology import grid_topology
+
+
+def model_info(weights_dir: str) -> "abi.SslaHipModelInfo":
+    """Grid sizes of a weight directory (meta.json), without a GPU."""
+    meta = (abi.ctypes.c_int * 4)()
+    lib.check(lib.load().ssla_hip_meta_read(weights_dir.encode(), meta), "meta_read")
+    i = abi.SslaHipModelInfo()
+    i.height, i.width, i.num_classes, i.tdrop_window = meta
+    i.H2, i.W2 = i.height >> 2, i.width >> 2
+    i.H3, i.W3 = i.H2 >> 1, i.W2 >> 1
+    return i
 
 
 def _now_ns() -> int:
@@ -55,6 +67,7 @@ class LiveResult:
     producer_stats: list = field(default_factory=list)
     phase_us: Optional[np.ndarray] = None
     batch_sizes: Dict[str, float] = field(default_factory=dict)
+    gpu_blocks: int = 1
 
     @property
     def drain_rate_kev_s(self) -> float:
@@ -83,32 +96,43 @@ def pick_cores(n_shards: int):
 
 def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n_shards: int = 6,
              halo: int = 2, base_core: Optional[int] = None, synth_core: Optional[int] = None,
-             seed: int = 1,
+             seed: int = 1, gpu_blocks: int = 8,
              n_blobs: int = 8, sigma_px: float = 3.0, bg_frac: float = 0.1,
              ring_capacity: int = 1 << 16, timing_capacity: int = 1 << 22, max_batch: int = 32,
              spin_ns: int = 200, profile: bool = True, drain_timeout_s: float = 30.0) -> LiveResult:
-    """One live run on one GPU (one block owning the whole grid)."""
+    """One live run on one GPU.  gpu_blocks (1, 2, 4, 8; the reference's
+    default is 8) splits the s2 grid into owned strips with a 2-cell halo
+    (topology.grid_topology); each strip has its own ring, hidden state and
+    prediction grid and is drained by its own workgroup.  Halo records are
+    published to every strip whose processed window holds them; latency
+    covers the records that produce a prediction (owner, pass2, pass3)."""
     if base_core is None or synth_core is None:
         sc, bc = pick_cores(n_shards)
         synth_core = sc if synth_core is None else synth_core
         base_core = bc if base_core is None else base_core
-    drain = Drain.from_weights_dir(weights_dir, n_blocks=1)
-    rings = HostRings(1, ring_capacity)
+    info = model_info(weights_dir)
+    topo = grid_topology(gpu_blocks, info.W2, info.H2)
+    nb = len(topo)
+    drain = Drain.from_weights_dir(weights_dir, n_blocks=nb, strips=[t.owned for t in topo])
+    rings = HostRings(nb, ring_capacity)
     prod = S01gAPI()
     live = None
     try:
         drain.alloc_timing(timing_capacity)
         c = drain.cfg
         prod.init(weights_dir, n_shards, halo, base_core, 1 << 16, 1 << 16)
-        prod.attach_multi([rings.bufs[0].ptr], rings.head_ptrs(), ring_capacity - 1, c.W2, c.H2,
-                          [0], [c.W2], [0], [c.H2])
+        prod.attach_multi([rings.bufs[b].ptr for b in range(nb)], rings.head_ptrs(),
+                          ring_capacity - 1, c.W2, c.H2,
+                          [t.proc_x_lo for t in topo], [t.proc_x_hi for t in topo],
+                          [t.proc_y_lo for t in topo], [t.proc_y_hi for t in topo])
         live = LiveDrain(drain, rings, spin_ns=spin_ns, max_batch=max_batch,
                          idle_timeout_ms=int((duration_s + drain_timeout_s + 30) * 1000),
                          profile=profile)
-        clk = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_ulonglong * 2).from_address(c.kernel_start_clk[0]))
-        k0 = _spin_nonzero(lambda: int(clk[0]), 30.0)
+        clks = [np.ctypeslib.as_array((np.ctypeslib.ctypes.c_ulonglong * 2).from_address(
+            c.kernel_start_clk[b])) for b in range(nb)]
+        k0 = [_spin_nonzero(lambda a=a: int(a[0]), 30.0) for a in clks]
         t0_cpu = _now_ns()
-        if not k0:
+        if not all(k0):
             raise RuntimeError("the live kernel did not start")
         prod.reset()
         t_start = time.monotonic()
@@ -126,45 +150,53 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
             if time.monotonic() > t_end:
                 break
             time.sleep(0.001)
-        head = int(rings.head[0])
-        while int(rings.done[0]) < head and time.monotonic() < t_end:
+        heads = [int(rings.head[b]) for b in range(nb)]
+        while any(int(rings.done[b]) < heads[b] for b in range(nb)) and time.monotonic() < t_end:
             time.sleep(0.0005)
-        drained = int(rings.done[0])
+        drained = [int(rings.done[b]) for b in range(nb)]
         rings.stop()
-        k1 = _spin_nonzero(lambda: int(clk[1]), 30.0)
+        k1 = [_spin_nonzero(lambda a=a: int(a[1]), 30.0) for a in clks]
         t1_cpu = _now_ns()
         status = live.wait()
         phase = live.phase_us
         live = None
         prod_stats = prod.stats()
-        ns_per_tick = (t1_cpu - t0_cpu) / max(1, (k1 - k0)) if k1 else 1e6 / 1e5
-        tv = drain.timing(0)
-        n_keep = min(drained, tv.size)
-        tv = tv[(np.arange(drained - n_keep, drained) & (tv.size - 1))] if n_keep else tv[:0]
-        ok = (tv["t_done_clk"] != 0) & (tv["t_emit_ns"] != 0) & (tv["t_push_ns"] != 0)
-        own = ok & (tv["owner"] == 1)
-        t_done = t0_cpu + (tv["t_done_clk"].astype(np.float64) - k0) * ns_per_tick
-        e2d = (t_done - tv["t_emit_ns"].astype(np.float64)) / 1e3
-        e2p = (tv["t_push_ns"].astype(np.float64) - tv["t_emit_ns"].astype(np.float64)) / 1e3
-        p2d = (t_done - tv["t_push_ns"].astype(np.float64)) / 1e3
-        kern = (tv["t_done_clk"].astype(np.float64) - tv["t_pop_clk"].astype(np.float64)) * ns_per_tick / 1e3
+        cols = {k: [] for k in ("e2d", "e2p", "p2d", "kern", "own", "ok")}
+        for b in range(nb):
+            # per-block two-point calibration of the GPU clock
+            ns_per_tick = (t1_cpu - t0_cpu) / max(1, (k1[b] - k0[b])) if k1[b] else 1e6 / 1e5
+            tv = drain.timing(b)
+            n_keep = min(drained[b], tv.size)
+            tv = tv[(np.arange(drained[b] - n_keep, drained[b]) & (tv.size - 1))] if n_keep else tv[:0]
+            ok = (tv["t_done_clk"] != 0) & (tv["t_emit_ns"] != 0) & (tv["t_push_ns"] != 0)
+            t_done = t0_cpu + (tv["t_done_clk"].astype(np.float64) - k0[b]) * ns_per_tick
+            cols["e2d"].append((t_done - tv["t_emit_ns"].astype(np.float64)) / 1e3)
+            cols["e2p"].append((tv["t_push_ns"].astype(np.float64)
+                                - tv["t_emit_ns"].astype(np.float64)) / 1e3)
+            cols["p2d"].append((t_done - tv["t_push_ns"].astype(np.float64)) / 1e3)
+            cols["kern"].append((tv["t_done_clk"].astype(np.float64)
+                                 - tv["t_pop_clk"].astype(np.float64)) * ns_per_tick / 1e3)
+            cols["own"].append(ok & (tv["owner"] == 1))
+            cols["ok"].append(ok)
+        cat = {k: np.concatenate(v) if v else np.zeros(0) for k, v in cols.items()}
+        own, ok = cat["own"].astype(bool), cat["ok"].astype(bool)
         lat = {}
-        for name, arr in (("emit_to_done", e2d), ("emit_to_push", e2p), ("push_to_done", p2d),
-                          ("kernel", kern)):
-            a = arr[own]
+        for name, key in (("emit_to_done", "e2d"), ("emit_to_push", "e2p"),
+                          ("push_to_done", "p2d"), ("kernel", "kern")):
+            a = cat[key][own]
             lat[name + "_p50"] = pct(a, 0.50)
             lat[name + "_p99"] = pct(a, 0.99)
             lat[name + "_max"] = float(a.max()) if a.size else float("nan")
-        a = e2d[ok]
+        a = cat["e2d"][ok]
         lat["all_emit_to_done_p50"] = pct(a, 0.50)
         lat["all_emit_to_done_p99"] = pct(a, 0.99)
-        lat["ns_per_tick"] = ns_per_tick
         bs = {}
         if phase is not None and phase[26] > 0:
             bs = {"batches": float(phase[25]), "mean": float(phase[26] / max(1.0, phase[25]))}
         return LiveResult(status=status, duration_s=t_stop - t_start, synth_events=n_synth,
-                          ring_records=head, drained=drained, output_records=int(own.sum()),
-                          lat_us=lat, producer_stats=prod_stats, phase_us=phase, batch_sizes=bs)
+                          ring_records=sum(heads), drained=sum(drained),
+                          output_records=int(own.sum()), lat_us=lat, producer_stats=prod_stats,
+                          phase_us=phase, batch_sizes=bs, gpu_blocks=nb)
     finally:
         if live is not None:
             rings.stop()

@@ -183,6 +183,25 @@ def test_head_grid_dump_matches_oracle(H, stub_dir, stub_npz, tmp_path):
     assert rep.ok and rep.n_cp == 6 and rep.n_mismatched_cp == 0
 
 
+def test_trained_checkpoint_weights(H, trained_dir):
+    """A weight directory converted from a trained-style checkpoint (conv
+    biases, BatchNorm statistics away from (0, 1), tdrop window 6)."""
+    n = 8000
+    say("trained checkpoint", n)
+    npz = O.load_npz(trained_dir)
+    rec = events.blob_records(n, seed=4)
+    with H.Drain.from_weights_dir(trained_dir) as d:
+        assert d.cfg.tdrop_window == 6
+        (out,), (h7,) = d.drain([events.to_records(rec)], want_head=True)
+    st = O.S2S3(O.layers_from_npz(npz), 16, 20, 6, head=O.head_from_npz(npz))
+    p2, p3, feat, ref7 = st.run(rec.x, rec.y, rec.feat1, want_head=True)
+    compare(out, p2, p3, feat, "trained")
+    m = p3 == 1
+    dh = np.abs(h7[m] - ref7[m]).max()
+    say(f"trained head max|d| = {dh:.3g}")
+    assert dh <= HEAD_TOL
+
+
 def test_sixteen_streams(H, stub_dir, stub_npz):
     n = 4000
     say("sixteen_streams", n)

@@ -266,6 +266,76 @@ def test_live_fed_by_producer_matches_oracle(H, stub_dir, stub_npz):
         rings.free()
 
 
+def test_live_eight_blocks_fed_by_producer(H, stub_dir, stub_npz):
+    """The reference's default live topology: 8 owned strips (2 x 4) with a
+    2-cell halo, one ring and workgroup each, fed by two producer shards.
+    Each ring's records (in ring order) drive an oracle with that block's
+    ownership mask; state, flags and predictions must match per block."""
+    from ssla_hip import producer as P
+    from ssla_hip.topology import grid_topology
+    n_ev = 40000
+    say("live eight blocks fed by producer", n_ev)
+    rng = np.random.default_rng(6)
+    ev = P.events_array(np.arange(n_ev), rng.integers(0, 80, n_ev), rng.integers(0, 64, n_ev),
+                        np.where(rng.random(n_ev) < 0.5, -1.0, 1.0))
+    topo = grid_topology(8, 20, 16)
+    with H.Drain.from_weights_dir(stub_dir, n_blocks=8, strips=[t.owned for t in topo]) as d:
+        d.alloc_timing(1 << 14)
+        rings = H.HostRings(8, capacity=1 << 14)
+        api = P.S01gAPI()
+        api.init(stub_dir, 2, 2, -1, 4096)
+        live = None
+        try:
+            api.attach_multi([rings.bufs[b].ptr for b in range(8)], rings.head_ptrs(),
+                             rings.capacity - 1, 20, 16,
+                             [t.proc_x_lo for t in topo], [t.proc_x_hi for t in topo],
+                             [t.proc_y_lo for t in topo], [t.proc_y_hi for t in topo])
+            live = H.LiveDrain(d, rings, idle_timeout_ms=20000)
+            assert api.submit(ev) == n_ev
+            api.wait_processed(n_ev, 0)
+            ns = [int(rings.head[b]) for b in range(8)]
+            assert all(0 < n < rings.capacity for n in ns)
+            for b in range(8):
+                _wait_done(rings, b, ns[b])
+        finally:
+            status = live.stop() if live is not None else -1
+            api.shutdown()
+        assert status == 0
+        head = O.head_from_npz(stub_npz)
+        layers = O.layers_from_npz(stub_npz)
+        for b, t in enumerate(topo):
+            recs = rings.rings[b][:ns[b]].copy()
+            assert np.array_equal(recs["seq_done"], np.arange(1, ns[b] + 1, dtype=np.uint64))
+            x, y = recs["x"].astype(int), recs["y"].astype(int)
+            assert np.all((x >= t.proc_x_lo) & (x < t.proc_x_hi) & (y >= t.proc_y_lo)
+                          & (y < t.proc_y_hi))
+            own = (x >= t.owned_x_lo) & (x < t.owned_x_hi) & (y >= t.owned_y_lo) & (y < t.owned_y_hi)
+            st = O.S2S3(layers, 16, 20, 4, head=head)
+            p2, p3, feat, ref7 = st.run(recs["x"], recs["y"], recs["feat1"], owner=own,
+                                        want_head=True)
+            ts = d.timing(b)[:ns[b]]
+            assert np.array_equal(ts["owner"], (own & (p3 == 1)).astype(np.uint32)), b
+            for li in range(4):
+                assert hidden_close(d.hidden(b, li), st.H[li]), (b, li)
+            td2, td3 = d.counters(b)
+            assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3), b
+            # predictions: owned pass-3 records whose s3 cell is in the block's s3 box
+            x3l, x3h, y3l, y3h = (t.owned_x_lo >> 1, t.owned_x_hi >> 1, t.owned_y_lo >> 1,
+                                  t.owned_y_hi >> 1)
+            w3 = x3h - x3l
+            preds, version = d.preds(b)
+            hit = own & (p3 == 1) & ((x >> 1) >= x3l) & ((x >> 1) < x3h) \
+                & ((y >> 1) >= y3l) & ((y >> 1) < y3h)
+            cell = ((y >> 1) - y3l) * w3 + ((x >> 1) - x3l)
+            for c in range(version.size):
+                k = np.nonzero(hit & (cell == c))[0]
+                assert version[c] == k.size, (b, c)
+                if k.size:
+                    assert np.abs(preds[c] - ref7[k[-1]]).max() <= HEAD_TOL, (b, c)
+        say("eight blocks: records per ring", ns)
+        rings.free()
+
+
 def test_run_live_short(stub_dir):
     """The live pipeline end to end at a low rate: nothing lost, latencies
     measured for output-producing records."""
