@@ -246,7 +246,7 @@ int ssla_hip_persistent_wait(SslaHipLive* h, int timeout_ms, int* status);
 #define SSLA_PRED_BUSY 0x80000000u
 
 /* Copies n_cells cells (cols floats + version each) torn-free: a cell is
- * retried up to max_tries times (>= 1).  Returns the number of cells that
+ * read up to max_tries times (>= 1), about 1 us apart.  Returns the number of cells that
  * stayed busy or kept changing (their version_out has SSLA_PRED_BUSY set
  * and preds_out holds the last copy), or a negative SSLA_ERR_*.  Replaces
  * the direct reads of the pinned views (orin/hybrid_runner_multi.py:648-656,

@@ -12,6 +12,7 @@
 //   * the OEVA head-grid dump format and its diff (include/oracle.h:10-18,
 //     57-77, 90-150).
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -33,6 +34,14 @@ constexpr unsigned kBusy = SSLA_PRED_BUSY;
 
 inline unsigned load_acquire(const unsigned* p) {
     return __atomic_load_n(p, __ATOMIC_ACQUIRE);
+}
+
+// About a microsecond between two reads of a busy cell: the device's
+// publish of one cell (two system fences over PCIe) takes microseconds, so
+// back-to-back retries would all land inside one write.
+inline void backoff() {
+    const auto t0 = std::chrono::steady_clock::now();
+    while (std::chrono::steady_clock::now() - t0 < std::chrono::microseconds(1)) __builtin_ia32_pause();
 }
 
 // One cell of `cols` floats read between two acquire loads of its version.
@@ -119,7 +128,10 @@ int ssla_hip_preds_snapshot(const float* preds, const unsigned* version, int n_c
         const float* src = preds + size_t(c) * cols;
         float* dst = preds_out + size_t(c) * cols;
         bool ok = false;
-        for (int t = 0; t < max_tries && !ok; ++t) ok = read_cell(src, version + c, cols, dst, version_out + c);
+        for (int t = 0; t < max_tries && !ok; ++t) {
+            if (t) backoff();
+            ok = read_cell(src, version + c, cols, dst, version_out + c);
+        }
         if (!ok) {
             version_out[c] |= kBusy;
             ++torn;
@@ -172,8 +184,10 @@ int ssla_hip_grid_decode(const HybridS2S3Config* cfg, const float* zero_row, int
         for (int i = 0; i < w * h; ++i) {
             unsigned ver = 0;
             bool ok = false;
-            for (int t = 0; t < (max_tries < 1 ? 1 : max_tries) && !ok; ++t)
+            for (int t = 0; t < (max_tries < 1 ? 1 : max_tries) && !ok; ++t) {
+                if (t) backoff();
                 ok = read_cell(p + size_t(i) * cols, v + i, cols, cell.data(), &ver);
+            }
             if (!ok) ++torn;
             if (!ok || ver == 0) continue;
             const int gx = s.s3_owned_lo + i % w, gy = s.s3_owned_y_lo + i / w;

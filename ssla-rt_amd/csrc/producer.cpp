@@ -164,74 +164,128 @@ struct Producer {
         }
     }
 
+    // Shard loop: takes what its queue holds (up to kBatch messages, never
+    // waiting for more), decides tdrop for each message in order, then runs
+    // the stages layer by layer over the batch (Stage01::stage*_batch; each
+    // layer's state still sees the events in queue order) and publishes the
+    // pass-1 records in order.  A message's segment times are its batch's
+    // times divided over the batch.
+    static constexpr int kBatch = 16;
+
     void work(Shard* c, bool to_gpu) {
         pin_self(c->core);
         Stage01& st = *c->st;
         const std::size_t cap = c->samples.size();
-        float f0[2], s0[12], s1[24];
-        auto seg = [&](int s, std::uint64_t a, std::uint64_t b) {
+        Msg m[kBatch];
+        int x[kBatch], y[kBatch], x1[kBatch], y1[kBatch], k1[kBatch];
+        std::uint8_t full0[kBatch], full1[kBatch], pass0[kBatch], pass1[kBatch];
+        alignas(32) float f0[kBatch * 2], s0[kBatch * 12], in1[kBatch * 12], s1[kBatch * 24];
+        auto seg = [&](int s, std::uint64_t a, std::uint64_t b, int n) {
             c->seg_ns[s].fetch_add(b - a, std::memory_order_relaxed);
-            c->seg_n[s].fetch_add(1, std::memory_order_relaxed);
+            c->seg_n[s].fetch_add((std::uint64_t)n, std::memory_order_relaxed);
         };
-        while (true) {
-            Msg m;
-            if (!c->q->try_pop(m)) {
-                cpu_relax();
+        bool eof = false;
+        while (!eof) {
+            int n = 0;
+            while (n < kBatch && c->q->try_pop(m[n])) {
+                if (m[n].eof) {
+                    eof = true;
+                    break;
+                }
+                ++n;
+            }
+            if (n == 0) {
+                if (!eof) cpu_relax();
                 continue;
             }
-            if (m.eof) break;
-            const int x = (int)m.x, y = (int)m.y;
             const std::uint64_t a = mono_ns();
-            st.preprocess(m.t, x, y, m.p, f0);
-            const std::uint64_t b = mono_ns();
-            seg(SEG_PRE, a, b);
-            if (!m.owner) {
-                st.stage0(x, y, f0, s0, false);
-                seg(SEG_S0, b, mono_ns());
-                c->halo.fetch_add(1, std::memory_order_relaxed);
-                continue;
+            for (int i = 0; i < n; ++i) {
+                x[i] = (int)m[i].x;
+                y[i] = (int)m[i].y;
+                st.preprocess(m[i].t, x[i], y[i], m[i].p, f0 + 2 * i);
             }
-            bool pass0 = false, pass1 = false;
+            const std::uint64_t b = mono_ns();
+            seg(SEG_PRE, a, b, n);
+            int n1 = 0, n_own = 0;
             if (to_gpu) {
                 // tdrop first: stage outputs nobody consumes run state-only
-                pass0 = st.tdrop_at(0, x >> 1, y >> 1);
+                for (int i = 0; i < n; ++i) {
+                    pass0[i] = pass1[i] = 0;
+                    if (m[i].owner) {
+                        ++n_own;
+                        pass0[i] = st.tdrop_at(0, x[i] >> 1, y[i] >> 1);
+                        if (pass0[i]) {
+                            pass1[i] = st.tdrop_at(1, x[i] >> 2, y[i] >> 2);
+                            k1[n1] = i;
+                            x1[n1] = x[i] >> 1;
+                            y1[n1] = y[i] >> 1;
+                            full1[n1] = pass1[i];
+                            ++n1;
+                        }
+                    }
+                    full0[i] = pass0[i];
+                }
                 const std::uint64_t t1 = mono_ns();
-                seg(SEG_TD0, b, t1);
-                st.stage0(x, y, f0, s0, pass0);
+                seg(SEG_TD0, b, t1, n);
+                st.stage0_batch(n, x, y, f0, full0, s0);
                 const std::uint64_t t2 = mono_ns();
-                seg(SEG_S0, t1, t2);
-                if (pass0) {
-                    pass1 = st.tdrop_at(1, x >> 2, y >> 2);
+                seg(SEG_S0, t1, t2, n);
+                if (n1) {
+                    for (int j = 0; j < n1; ++j) std::memcpy(in1 + 12 * j, s0 + 12 * k1[j], sizeof(float) * 12);
+                    st.stage1_batch(n1, x1, y1, in1, full1, s1);
                     const std::uint64_t t3 = mono_ns();
-                    seg(SEG_TD1, t2, t3);
-                    st.stage1(x >> 1, y >> 1, s0, s1, pass1);
-                    const std::uint64_t t4 = mono_ns();
-                    seg(SEG_S1, t3, t4);
-                    if (pass1 && attached.load(std::memory_order_acquire)) {
-                        publish(x >> 2, y >> 2, m.t, s1, m.t_emit_ns);
-                        seg(SEG_PUSH, t4, mono_ns());
+                    seg(SEG_S1, t2, t3, n1);
+                    if (attached.load(std::memory_order_acquire)) {
+                        int np = 0;
+                        for (int j = 0; j < n1; ++j) {
+                            if (!full1[j]) continue;
+                            publish(x1[j] >> 1, y1[j] >> 1, m[k1[j]].t, s1 + 24 * j, m[k1[j]].t_emit_ns);
+                            ++np;
+                        }
+                        if (np) seg(SEG_PUSH, t3, mono_ns(), np);
                     }
                 }
             } else {
-                st.stage0(x, y, f0, s0, true);
+                for (int i = 0; i < n; ++i) {
+                    full0[i] = m[i].owner;
+                    n_own += m[i].owner;
+                }
+                st.stage0_batch(n, x, y, f0, full0, s0);
                 const std::uint64_t t1 = mono_ns();
-                seg(SEG_S0, b, t1);
-                pass0 = st.tdrop_at(0, x >> 1, y >> 1);
+                seg(SEG_S0, b, t1, n);
+                for (int i = 0; i < n; ++i) {
+                    pass0[i] = pass1[i] = 0;
+                    if (!m[i].owner) continue;
+                    pass0[i] = st.tdrop_at(0, x[i] >> 1, y[i] >> 1);
+                    if (pass0[i]) {
+                        k1[n1] = i;
+                        x1[n1] = x[i] >> 1;
+                        y1[n1] = y[i] >> 1;
+                        full1[n1] = 1;
+                        std::memcpy(in1 + 12 * n1, s0 + 12 * i, sizeof(float) * 12);
+                        ++n1;
+                    }
+                }
                 const std::uint64_t t2 = mono_ns();
-                seg(SEG_TD0, t1, t2);
-                if (pass0) {
-                    st.stage1(x >> 1, y >> 1, s0, s1, true);
+                seg(SEG_TD0, t1, t2, n);
+                if (n1) {
+                    st.stage1_batch(n1, x1, y1, in1, full1, s1);
                     const std::uint64_t t3 = mono_ns();
-                    seg(SEG_S1, t2, t3);
-                    pass1 = st.tdrop_at(1, x >> 2, y >> 2);
-                    seg(SEG_TD1, t3, mono_ns());
+                    seg(SEG_S1, t2, t3, n1);
+                    for (int j = 0; j < n1; ++j) pass1[k1[j]] = st.tdrop_at(1, x1[j] >> 1, y1[j] >> 1);
+                    seg(SEG_TD1, t3, mono_ns(), n1);
                 }
             }
-            const std::size_t i = c->n_samples.fetch_add(1, std::memory_order_relaxed);
-            c->samples[i % cap] = (double)(mono_ns() - m.t_arr_ns);
-            c->owner.fetch_add(1, std::memory_order_relaxed);
-            if (pass0) c->pass0.fetch_add(1, std::memory_order_relaxed);
-            if (pass1) c->pass1.fetch_add(1, std::memory_order_relaxed);
+            const std::uint64_t done = mono_ns();
+            for (int i = 0; i < n; ++i) {
+                if (!m[i].owner) continue;
+                const std::size_t k = c->n_samples.fetch_add(1, std::memory_order_relaxed);
+                c->samples[k % cap] = (double)(done - m[i].t_arr_ns);
+                if (pass0[i]) c->pass0.fetch_add(1, std::memory_order_relaxed);
+                if (pass1[i]) c->pass1.fetch_add(1, std::memory_order_relaxed);
+            }
+            c->owner.fetch_add((std::uint64_t)n_own, std::memory_order_relaxed);
+            c->halo.fetch_add((std::uint64_t)(n - n_own), std::memory_order_relaxed);
         }
     }
 

@@ -211,9 +211,10 @@ class Drain:
         upload_ptr(self.cfg.tdrop_s2[blk], td2.astype(np.uint8))
         upload_ptr(self.cfg.tdrop_s3[blk], td3.astype(np.uint8))
 
-    def preds(self, blk: int, max_tries: int = 64):
+    def preds(self, blk: int, max_tries: int = 2000):
         """Torn-free copy of block blk's prediction cells: (preds (n, 7),
-        version (n,)).  Raises if a cell stays busy for max_tries reads."""
+        version (n,)).  Raises if a cell stays busy for max_tries reads
+        (about 1 us apart)."""
         s = self.cfg.strip[blk]
         n = (s.s3_owned_hi - s.s3_owned_lo) * (s.s3_owned_y_hi - s.s3_owned_y_lo)
         if not self.cfg.preds[blk]:
@@ -236,7 +237,7 @@ class Drain:
                                                      out.ctypes.data_as(fp)), "model_head_row")
         return out
 
-    def head_grid(self, stride: int = 8, max_tries: int = 64) -> np.ndarray:
+    def head_grid(self, stride: int = 8, max_tries: int = 2000) -> np.ndarray:
         """Decoded (H3*W3, 7) grid, row gy*W3 + gx, as the CPU pipeline's
         detection output holds it."""
         out, torn = grid.grid_decode(self.cfg, self.zero_row(), stride, stride, max_tries)
