@@ -52,13 +52,23 @@ void s01g_attach_gpu_rings_multi(S01gHandle* h, int n_blocks,
 /* lib_stage01_to_gpu.cpp:504-538: events [t_us, x, y, p] x n; returns the
  * number accepted (events outside the sensor are counted as oob) */
 int  s01g_submit_batch(S01gHandle* h, const float* events_packed, int n);
+/* No counterpart in the reference (its rings overwrite unread slots and the
+ * drain reports the overrun): optional back-pressure.  tails[b] (n entries,
+ * n <= the attached ring count; NULL or n = 0 turns it off) is ring b's
+ * consumer tail, e.g. the drain's tails in fine-grained memory.  A
+ * publisher that claims slot s waits until s - tail <= mask, at most
+ * timeout_ns, then writes anyway.  Call after attaching the rings (an
+ * attach turns it off). */
+void s01g_set_ring_tails(S01gHandle* h, int n, const unsigned long long* const* tails,
+                         unsigned long long timeout_ns);
 /* lib_stage01_to_gpu.cpp:540-611: 32 slots
  *   0 owner events, 1 halo events, 2 pass stage 0, 3 oob, 4 seconds since
  *   init/reset, 5 shard-ring occupancy, 6..11 owner latency p50 p90 p99
  *   p99.9 max mean (us, arrival -> shard done), 12 latency samples,
  *   13 pass stage 1, 14/15 records pushed to ring 0/1, 16..21 segment time
  *   sums (ns: preprocess, s0, tdrop0, s1, tdrop1, push), 22..27 segment
- *   counts, 28..31 reserved */
+ *   counts, 28 back-pressure waits, 29 their total ns, 30 waits that
+ *   timed out (the slot was overwritten), 31 reserved */
 void s01g_snapshot_stats(S01gHandle* h, double* out);
 void s01g_reset_stats(S01gHandle* h);
 void s01g_shutdown(S01gHandle* h);

@@ -106,6 +106,7 @@ struct Shard {
 struct RingOut {
     HybridInputRec* buf = nullptr;
     std::uint64_t* head = nullptr;
+    const std::uint64_t* tail = nullptr;   // consumer's tail (back-pressure), or null
     int x_lo = 0, x_hi = 0, y_lo = 0, y_hi = 0;
     std::atomic<std::uint64_t> pushed{0};
 };
@@ -125,6 +126,9 @@ struct Producer {
     RingOut rings[kMaxRings];
     int n_rings = 0, W2 = 0, H2 = 0;
     std::uint64_t ring_mask = 0;
+    // back-pressure: a claimed slot waits for the consumer's tail to free it
+    std::uint64_t bp_timeout_ns = 0;
+    std::atomic<std::uint64_t> bp_waits{0}, bp_wait_ns{0}, bp_overruns{0};
     // synthetic source
     std::atomic<bool> synth_on{false};
     std::thread synth;
@@ -152,6 +156,23 @@ struct Producer {
             RingOut& r = rings[b];
             if (x2 < r.x_lo || x2 >= r.x_hi || y2 < r.y_lo || y2 >= r.y_hi) continue;
             const std::uint64_t slot = __atomic_fetch_add(r.head, 1ull, __ATOMIC_RELAXED);
+            if (r.tail && slot - __atomic_load_n(r.tail, __ATOMIC_ACQUIRE) > ring_mask) {
+                // the slot still holds a record the consumer has not taken:
+                // wait for it, up to bp_timeout_ns, then overwrite (the
+                // consumer reports the overrun)
+                const std::uint64_t w0 = mono_ns();
+                std::uint64_t now = w0;
+                while (slot - __atomic_load_n(r.tail, __ATOMIC_ACQUIRE) > ring_mask) {
+                    cpu_relax();
+                    now = mono_ns();
+                    if (now - w0 > bp_timeout_ns) {
+                        bp_overruns.fetch_add(1, std::memory_order_relaxed);
+                        break;
+                    }
+                }
+                bp_waits.fetch_add(1, std::memory_order_relaxed);
+                bp_wait_ns.fetch_add(now - w0, std::memory_order_relaxed);
+            }
             HybridInputRec* d = r.buf + (slot & ring_mask);
             d->t = t;
             d->x = (unsigned short)x2;
@@ -344,6 +365,11 @@ struct Producer {
                 out[22 + k] = (double)sc[k];
             }
         }
+        if (n_slots >= 31) {
+            out[28] = (double)bp_waits.load();
+            out[29] = (double)bp_wait_ns.load();
+            out[30] = (double)bp_overruns.load();
+        }
     }
 
     void reset_stats() {
@@ -359,6 +385,9 @@ struct Producer {
             }
         }
         for (auto& r : rings) r.pushed = 0;
+        bp_waits = 0;
+        bp_wait_ns = 0;
+        bp_overruns = 0;
         oob = 0;
         t0 = std::chrono::steady_clock::now();
     }
@@ -550,6 +579,7 @@ void s01g_attach_gpu_rings_multi(S01gHandle* h, int n, void* const* bufs, void* 
         r.y_lo = ylo[b];
         r.y_hi = yhi[b];
         r.pushed = 0;
+        r.tail = nullptr;
     }
     h->n_rings = n;
     h->ring_mask = mask;
@@ -565,6 +595,14 @@ void s01g_attach_gpu_rings(S01gHandle* h, void* buf0, void* head0, void* buf1, v
     void* heads[2] = {head0, head1};
     const int xlo[2] = {lo0, lo1}, xhi[2] = {hi0, hi1}, ylo[2] = {0, 0}, yhi[2] = {H2, H2};
     s01g_attach_gpu_rings_multi(h, 2, bufs, heads, mask, W2, H2, xlo, xhi, ylo, yhi);
+}
+
+void s01g_set_ring_tails(S01gHandle* h, int n, const unsigned long long* const* tails,
+                         unsigned long long timeout_ns) {
+    if (!h || n < 0 || n > h->n_rings) return;
+    h->bp_timeout_ns = timeout_ns;
+    for (int b = 0; b < h->n_rings; ++b)
+        h->rings[b].tail = (tails && b < n) ? reinterpret_cast<const std::uint64_t*>(tails[b]) : nullptr;
 }
 
 int s01g_submit_batch(S01gHandle* h, const float* ev, int n) { return ssla::submit(h, ev, n); }

@@ -432,6 +432,10 @@ class HostRings:
         """Addresses of the producer-side head words (one per block)."""
         return [self.words.ptr + 8 * b for b in range(self.n_blocks)]
 
+    def tail_ptrs(self):
+        """Addresses of the consumer-side tail words (for back-pressure)."""
+        return [self.words.ptr + 8 * (self.n_blocks + b) for b in range(self.n_blocks)]
+
     def push(self, blk: int, recs: np.ndarray) -> None:
         """Single-producer publish: write each record, then its seq_done tag."""
         ring = self.rings[blk]

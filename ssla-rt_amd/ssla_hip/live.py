@@ -99,8 +99,10 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
              seed: int = 1, gpu_blocks: int = 8,
              n_blobs: int = 8, sigma_px: float = 3.0, bg_frac: float = 0.1,
              ring_capacity: int = 1 << 16, timing_capacity: int = 1 << 22, max_batch: int = 32,
-             spin_ns: int = 200, profile: bool = True, drain_timeout_s: float = 30.0) -> LiveResult:
-    """One live run on one GPU.  gpu_blocks (1, 2, 4, 8; the reference's
+             spin_ns: int = 200, profile: bool = True, drain_timeout_s: float = 30.0,
+             back_pressure: bool = False) -> LiveResult:
+    """One live run on one GPU.  back_pressure makes the producer wait for
+    each ring's tail instead of overwriting unread slots.  gpu_blocks (1, 2, 4, 8; the reference's
     default is 8) splits the s2 grid into owned strips with a 2-cell halo
     (topology.grid_topology); each strip has its own ring, hidden state and
     prediction grid and is drained by its own workgroup.  Halo records are
@@ -125,6 +127,8 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
                           ring_capacity - 1, c.W2, c.H2,
                           [t.proc_x_lo for t in topo], [t.proc_x_hi for t in topo],
                           [t.proc_y_lo for t in topo], [t.proc_y_hi for t in topo])
+        if back_pressure:
+            prod.set_ring_tails(rings.tail_ptrs(), timeout_ms=1000.0 * drain_timeout_s)
         live = LiveDrain(drain, rings, spin_ns=spin_ns, max_batch=max_batch,
                          idle_timeout_ms=int((duration_s + drain_timeout_s + 30) * 1000),
                          profile=profile)

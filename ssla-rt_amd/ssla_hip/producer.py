@@ -37,6 +37,7 @@ _TO_GPU_SIGNATURES = {
     "s01g_init_full": (_vp, [ctypes.c_char_p, _i, _i, _i, _i, ctypes.c_uint]),
     "s01g_attach_gpu_rings": (None, [_vp, _vp, _vp, _vp, _vp, _u64, _i, _i, _i, _i, _i, _i]),
     "s01g_attach_gpu_rings_multi": (None, [_vp, _i, _vpp, _vpp, _u64, _i, _i, _ip, _ip, _ip, _ip]),
+    "s01g_set_ring_tails": (None, [_vp, _i, _vpp, _u64]),
     "s01g_submit_batch": (_i, [_vp, _fptr, _i]),
     "s01g_snapshot_stats": (None, [_vp, _dptr]),
     "s01g_reset_stats": (None, [_vp]),
@@ -147,6 +148,16 @@ class S01gAPI:
                 for a in (proc_x_los, proc_x_his, proc_y_los, proc_y_his)]
         self._attach_keepalive = (bufs, heads, arrs)
         self.lib.s01g_attach_gpu_rings_multi(self.handle, n, bufs, heads, ring_mask, W2, H2, *arrs)
+
+    def set_ring_tails(self, tail_ptrs: Sequence[int], timeout_ms: float = 1000.0) -> None:
+        """Back-pressure: publishers wait (up to timeout_ms) for each ring's
+        consumer tail (addresses of u64 words) to free a claimed slot.  An
+        empty sequence turns it off."""
+        n = len(tail_ptrs)
+        arr = (ctypes.c_void_p * max(1, n))(*[int(p) for p in tail_ptrs])
+        self._tails_keepalive = arr
+        self.lib.s01g_set_ring_tails(self.handle, n, arr if n else None,
+                                     int(timeout_ms * 1e6))
 
     def submit(self, events: np.ndarray) -> int:
         ev = np.ascontiguousarray(events, np.float32)

@@ -429,3 +429,72 @@ def test_replay_publishes_every_ring_in_order():
             assert (got["t_push_ns"] > 0).all() and (np.diff(got["t_push_ns"].astype(np.int64)) >= 0).all()
     with pytest.raises(RuntimeError):
         P.Replay([0], [0], 1023, [recs[0]], 0.0)
+
+
+def test_back_pressure_never_overwrites_unread_slots(stub_dir, stub_npz):
+    """A 64-slot ring drained slowly by a consumer thread: with the tails
+    set, publishers wait for their slot, so every record arrives once, in
+    slot order, and none is overwritten."""
+    import threading
+    import time
+    ev = _events(6000, seed=31)
+    cap = 64
+    buf = np.zeros(cap, abi.INPUT_DTYPE)
+    words = np.zeros(2, np.uint64)            # head, tail
+    got = []
+    stop = threading.Event()
+
+    def consumer():
+        t = 0
+        while not stop.is_set() or int(words[0]) > t:
+            if int(buf[t & (cap - 1)]["seq_done"]) == t + 1:
+                got.append(buf[t & (cap - 1)].copy())
+                t += 1
+                words[1] = t
+                if t % 16 == 0:
+                    time.sleep(0.0005)
+            else:
+                time.sleep(0)
+
+    api = P.S01gAPI()
+    api.init(stub_dir, 2, 2, -1, 1 << 14, 1 << 12)
+    th = threading.Thread(target=consumer)
+    th.start()
+    try:
+        api.attach_multi([buf.ctypes.data], [words.ctypes.data], cap - 1, W0 // 4, H0 // 4,
+                         [0], [W0 // 4], [0], [H0 // 4])
+        api.set_ring_tails([words.ctypes.data + 8], timeout_ms=5000)
+        api.submit(ev)
+        owner, halo_to = P.routing(ev[:, 1], W0, 2, 2)
+        st = api.wait_processed(len(ev), len(halo_to))
+    finally:
+        api.shutdown()
+        stop.set()
+        th.join(30)
+    n = int(words[0])
+    assert len(got) == n == st[14] and st[28] > 0 and st[30] == 0
+    recs = np.array(got)
+    p0, p1, feat = _oracle_sharded(stub_npz, ev, 2, 2, 4)
+    _check_records(recs, ev, p1, feat)
+
+
+def test_back_pressure_times_out_and_overwrites(stub_dir):
+    """A consumer that never advances: publishers give up after the
+    timeout, count it, and overwrite (the drain would report the overrun)."""
+    ev = _events(3000, seed=32)
+    cap = 16
+    buf = np.zeros(cap, abi.INPUT_DTYPE)
+    words = np.zeros(2, np.uint64)
+    api = P.S01gAPI()
+    api.init(stub_dir, 1, 2, -1, 1 << 14, 1 << 12)
+    try:
+        api.attach_multi([buf.ctypes.data], [words.ctypes.data], cap - 1, W0 // 4, H0 // 4,
+                         [0], [W0 // 4], [0], [H0 // 4])
+        api.set_ring_tails([words.ctypes.data + 8], timeout_ms=0.05)
+        api.submit(ev)
+        st = api.wait_processed(len(ev), 0)
+    finally:
+        api.shutdown()
+    n = int(words[0])
+    assert n == st[14] > cap
+    assert st[30] == n - cap and st[28] == n - cap
