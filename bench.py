@@ -25,6 +25,7 @@ output-producing records, GPU clocks put on the host clock by the kernel's
 start / exit stamps.
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -328,6 +329,15 @@ def main() -> int:
     roof = _roofline(per, flops, byts)
     if a.workload != "80x64":
         roof["traffic"] = None           # the committed PMC summary is of the 80x64 workload
+    if roof.get("unit") == "GB/s":
+        # what this device reaches on write-dominated traffic (the published
+        # 8 TB/s counts read and write capacity together)
+        ceil = (ctypes.c_double * 3)()
+        lib.check(lib.load().ssla_hip_hbm_ceiling(ceil, 3), "hbm_ceiling")
+        roof["measured_ceiling_gbs"] = {"write_stream": round(ceil[0], 1),
+                                        "copy_read_write": round(ceil[1], 1),
+                                        "rows_576B_permuted": round(ceil[2], 1)}
+        roof["frac_of_write_ceiling"] = round(roof["achieved"] / ceil[0], 4)
     whole = 2.0 * total_mac / (ms_step * 1e-3) / 1e12
     hbm = sum(byts.values()) / (ms_step * 1e-3) / 1e9
     res = {

@@ -329,6 +329,14 @@ typedef struct SslaHipOevaDiff {
 int ssla_hip_oeva_diff(const char* path_a, const char* path_b, double tol_abs,
                        SslaHipOevaDiff* out);
 
+/* ---- measured HBM ceilings (no counterpart in the reference) ----------
+ * Times three traffic patterns on the current device and writes GB/s into
+ * gbs[0..2]: streaming 16-byte writes over 1 GiB; a streaming copy (read and
+ * write bytes counted); 576-byte rows written as MFMA-tile column segments at
+ * a random permutation of 1.8 M row positions.  Allocates and frees 2 GiB.
+ * Used by bench.py to state what a write-dominated kernel can reach. */
+int ssla_hip_hbm_ceiling(double* gbs, int n);
+
 #ifdef __cplusplus
 }
 #endif

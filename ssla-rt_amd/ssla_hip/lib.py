@@ -71,6 +71,7 @@ _SIGNATURES = {
                                 ctypes.c_uint]),
     "ssla_hip_oeva_diff": (_I, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_double,
                                 ctypes.POINTER(abi.SslaHipOevaDiff)]),
+    "ssla_hip_hbm_ceiling": (_I, [ctypes.POINTER(ctypes.c_double), _I]),
 }
 
 EXPORTED = tuple(_SIGNATURES)
