@@ -300,20 +300,30 @@ __global__ void k_chunk_count(uint32_t nk, const int* __restrict__ start,
     cnt[k] = len > 0 ? (len + kCH - 1) / kCH : 0;
 }
 
-__global__ void k_chunk_fill(uint32_t nk, const int* __restrict__ start,
+// One thread per chunk slot j < max_chunks: its key is the last k with
+// coff[k] <= j among keys that have chunks (binary search over the
+// exclusive scan of the chunk counts).
+__global__ void k_chunk_fill(uint32_t nk, int max_chunks, const int* __restrict__ start,
                              const int* __restrict__ end, const int* __restrict__ cnt,
                              const int* __restrict__ coff, int* __restrict__ ckey,
                              int* __restrict__ cbeg, int* __restrict__ cend,
                              int* __restrict__ n_chunks) {
-    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-    if (k >= nk) return;
-    const int c0 = coff[k], nc = cnt[k], s = start[k], e = end[k];
-    for (int c = 0; c < nc; ++c) {
-        ckey[c0 + c] = (int)k;
-        cbeg[c0 + c] = s + c * kCH;
-        cend[c0 + c] = min(e, s + (c + 1) * kCH);
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    const int total = coff[nk - 1] + cnt[nk - 1];
+    if (j == 0) *n_chunks = total;
+    if (j >= total || j >= max_chunks) return;
+    int lo = 0, hi = (int)nk - 1;          // largest k with coff[k] <= j
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (coff[mid] <= j) lo = mid; else hi = mid - 1;
     }
-    if (k == nk - 1) *n_chunks = c0 + nc;
+    // (a key without chunks shares its coff with the next key, so the
+    // largest such k always has chunks; the step below only guards that)
+    while (lo + 1 < (int)nk && cnt[lo] == 0) ++lo;
+    const int c = j - coff[lo], s = start[lo], e = end[lo];
+    ckey[j] = lo;
+    cbeg[j] = s + c * kCH;
+    cend[j] = min(e, s + (c + 1) * kCH);
 }
 
 template <int OUT>
@@ -995,12 +1005,14 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL(k_chunk_count, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, w.pst2,
                        w.pen2, w.ccnt2);
     HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt2, w.coff2, (int)nk2, st));
-    hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, w.pst2,
+    hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(w.max_chunks, 256)), dim3(256), 0, st, nk2,
+                       w.max_chunks, w.pst2,
                        w.pen2, w.ccnt2, w.coff2, w.ckey2, w.cbeg2, w.cend2, w.counts + 2);
     hipLaunchKernelGGL(k_chunk_count, dim3(grid1(nk3, 256)), dim3(256), 0, st, nk3, w.pst3,
                        w.pen3, w.ccnt3);
     HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt3, w.coff3, (int)nk3, st));
-    hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(nk3, 256)), dim3(256), 0, st, nk3, w.pst3,
+    hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(w.max_chunks, 256)), dim3(256), 0, st, nk3,
+                       w.max_chunks, w.pst3,
                        w.pen3, w.ccnt3, w.coff3, w.ckey3, w.cbeg3, w.cend3, w.counts + 3);
     // ---- record lists: pass2 records, pass3 records (ring order) --------------
     HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
