@@ -567,59 +567,90 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 }
 
 // ---------------------------------------------------------------------------
-// head: raw [reg0..3, obj, cls0, cls1] for owned pass-3 records
-// (...celled.cuh:841-902).  One workgroup per record, one thread per hidden
-// channel.
+// head: raw [reg0..3, obj, cls0, cls1] for pass-3 records
+// (...celled.cuh:841-902).  One workgroup = 64 records (list order): their
+// 96-channel features staged in LDS; the two 1x1 convolutions (cls, reg; BN
+// folded) as one 64 x 192 x 96 product of 16 x 16 MFMA tiles whose B
+// operands are read straight from the row-major (IN, OUT) weights (lane l
+// takes row 4s + l/16, column l%16 of step s); SiLU into LDS; then the
+// seven prediction dot products, four threads per record.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(128)
+__global__ void __launch_bounds__(256)
 k_head(const int* __restrict__ n_dev, const int* __restrict__ list,
-       const unsigned char* __restrict__ owner, const float* __restrict__ X,
-       HeadPtrs hp, float* __restrict__ H7) {
-    constexpr int C = SSLA_C3;
-    __shared__ float x[C], yc[C], yr[C];
-    const int j = blockIdx.x;
-    if (j >= *n_dev) return;
-    const int g = list[j];
-    if (!owner[g]) return;
-    const int t = threadIdx.x;
-    if (t < C) x[t] = X[(size_t)g * C + t];
+       const float* __restrict__ X, HeadPtrs hp, float* __restrict__ H7) {
+    constexpr int C = SSLA_C3, XST = C + 4, HST = 2 * C + 4, CT = 2 * C / kMT;
+    __shared__ __align__(16) float xs[kTM * XST];
+    __shared__ float hs[kTM * HST];           // [yc | yr] per record
+    __shared__ int rows[kTM];
+    const int n = *n_dev;
+    const int base = blockIdx.x * kTM;
+    if (base >= n) return;
+    const int cnt = min(kTM, n - base);
+    const int tid = threadIdx.x;
+    if (tid < kTM) rows[tid] = tid < cnt ? list[base + tid] : -1;
     __syncthreads();
-    if (t < C) {
-        float a = hp.cls_conv_b[t], b = hp.reg_conv_b[t];
-        for (int i = 0; i < C; ++i) {
-            a = fmaf(hp.cls_conv_W[(size_t)i * C + t], x[i], a);
-            b = fmaf(hp.reg_conv_W[(size_t)i * C + t], x[i], b);
-        }
-        yc[t] = a * sigmoid_fast(a);
-        yr[t] = b * sigmoid_fast(b);
+    constexpr int C4 = C / 4;
+    for (int t = tid; t < kTM * C4; t += 256) {
+        const int r = t / C4, q = t - r * C4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (rows[r] >= 0) v = reinterpret_cast<const float4*>(X)[(size_t)rows[r] * C4 + q];
+        *reinterpret_cast<float4*>(&xs[r * XST + 4 * q]) = v;
     }
     __syncthreads();
-    // outputs 0..3 reg, 4 obj, 5..6 cls: one wave, lane-strided partial sums
-    if (t < 64) {
-        float part[7];
+    const int lane = tid & 63, wv = tid >> 6, li = lane & 15, lk = lane >> 4;
+    const int mtiles = (cnt + kMT - 1) / kMT;
+    // column tiles 0..5: cls conv, 6..11: reg conv; wave wv takes tiles wv, wv+4, wv+8
+    for (int ct = wv; ct < CT; ct += 4) {
+        const bool reg = ct >= CT / 2;
+        const float* W = reg ? hp.reg_conv_W : hp.cls_conv_W;
+        const float* bias = reg ? hp.reg_conv_b : hp.cls_conv_b;
+        const int col = (reg ? ct - CT / 2 : ct) * kMT + li;
+        float b[C / 4];
         #pragma unroll
-        for (int k = 0; k < 7; ++k) part[k] = 0.f;
-        for (int i = t; i < C; i += 64) {
+        for (int s = 0; s < C / 4; ++s) b[s] = gload(W + (size_t)(4 * s + lk) * C + col);
+        const float bc = bias[col];
+        for (int m = 0; m < mtiles; ++m) {
+            const float* a = &xs[(m * kMT + li) * XST + lk];
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
             #pragma unroll
-            for (int k = 0; k < 4; ++k) part[k] = fmaf(hp.reg_pred_W[(size_t)i * 4 + k], yr[i], part[k]);
-            part[4] = fmaf(hp.obj_pred_W[i], yr[i], part[4]);
+            for (int s = 0; s < C / 4; ++s)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s], b[s], acc, 0, 0, 0);
             #pragma unroll
-            for (int k = 0; k < 2; ++k) part[5 + k] = fmaf(hp.cls_pred_W[(size_t)i * 2 + k], yc[i], part[5 + k]);
+            for (int r = 0; r < 4; ++r) {
+                const float y = acc[r] + bc;
+                hs[(m * kMT + 4 * lk + r) * HST + ct * kMT + li] = y * sigmoid_fast(y);
+            }
         }
+    }
+    __syncthreads();
+    // predictions: record r = tid / 4, channels part, part + 4, ... (24 each)
+    const int r = tid >> 2, part = tid & 3;
+    float o[7];
+    #pragma unroll
+    for (int k = 0; k < 7; ++k) o[k] = 0.f;
+    if (r < cnt) {
+        const float* yc = &hs[r * HST];
+        const float* yr = yc + C;
+        for (int i = part; i < C; i += 4) {
+            #pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = fmaf(hp.reg_pred_W[(size_t)i * 4 + k], yr[i], o[k]);
+            o[4] = fmaf(hp.obj_pred_W[i], yr[i], o[4]);
+            #pragma unroll
+            for (int k = 0; k < 2; ++k) o[5 + k] = fmaf(hp.cls_pred_W[(size_t)i * 2 + k], yc[i], o[5 + k]);
+        }
+    }
+    #pragma unroll
+    for (int k = 0; k < 7; ++k) {
+        o[k] += __shfl_xor(o[k], 1, 64);
+        o[k] += __shfl_xor(o[k], 2, 64);
+    }
+    if (r < cnt && part == 0) {
+        float* out = H7 + (size_t)rows[r] * 7;
         #pragma unroll
-        for (int k = 0; k < 7; ++k) {
-            float v = part[k];
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-            part[k] = v;
-        }
-        if (t == 0) {
-            float* o = H7 + (size_t)g * 7;
-            #pragma unroll
-            for (int k = 0; k < 4; ++k) o[k] = part[k] + hp.reg_pred_b[k];
-            o[4] = part[4] + hp.obj_pred_b[0];
-            o[5] = part[5] + hp.cls_pred_b[0];
-            o[6] = part[6] + hp.cls_pred_b[1];
-        }
+        for (int k = 0; k < 4; ++k) out[k] = o[k] + hp.reg_pred_b[k];
+        out[4] = o[4] + hp.obj_pred_b[0];
+        out[5] = o[5] + hp.cls_pred_b[0];
+        out[6] = o[6] + hp.cls_pred_b[1];
     }
 }
 
@@ -671,7 +702,9 @@ __global__ void k_emit(int E, const BlockDesc* __restrict__ bd, int nb,
                        const unsigned char* __restrict__ pass3,
                        const float* __restrict__ X4, const float* __restrict__ H7,
                        int have_head) {
-    const int g = blockIdx.x;
+    // one wave per record, four records per workgroup
+    const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (g >= E) return;
     const int b = find_block(bd, nb, g);
     const int k = g - bd[b].offset;
@@ -680,17 +713,16 @@ __global__ void k_emit(int E, const BlockDesc* __restrict__ bd, int nb,
     HybridS2S3OutputSlot* out = bd[b].out;
     if (out) {
         HybridS2S3OutputSlot& s = out[k];
-        if (threadIdx.x == 0) {
+        if (lane == 0) {
             s.pass2 = !valid ? -2 : (own ? (p2 ? 1 : 0) : -1);
             s.pass3 = !valid ? -2 : (own ? (p3 ? 1 : 0) : -1);
         }
-        for (int i = threadIdx.x; i < SSLA_C3; i += blockDim.x)
+        for (int i = lane; i < SSLA_C3; i += 64)
             s.s3_feat[i] = p3 ? X4[(size_t)g * SSLA_C3 + i] : 0.f;
     }
     float* ho = bd[b].head_out;
-    if (ho && threadIdx.x < 7)
-        ho[(size_t)k * 7 + threadIdx.x] =
-            (have_head && p3 && own) ? H7[(size_t)g * 7 + threadIdx.x] : 0.f;
+    if (ho && lane < 7)
+        ho[(size_t)k * 7 + lane] = (have_head && p3 && own) ? H7[(size_t)g * 7 + lane] : 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -1112,8 +1144,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                     cfg->head_cls_pred_b, cfg->head_reg_conv_W, cfg->head_reg_conv_b,
                     cfg->head_reg_pred_W, cfg->head_reg_pred_b, cfg->head_obj_pred_W,
                     cfg->head_obj_pred_b};
-        hipLaunchKernelGGL(k_head, dim3(E), dim3(128), 0, st, (const int*)(w.counts + 1),
-                           w.list3, w.owner, w.X4, hp, w.H7);
+        hipLaunchKernelGGL(k_head, dim3(tilesE), dim3(256), 0, st, (const int*)(w.counts + 1),
+                           w.list3, w.X4, hp, w.H7);
         hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.last3, -1);
         hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.cnt3, 0);
         hipLaunchKernelGGL(k_pred_last, dim3(grid1(E, 256)), dim3(256), 0, st,
@@ -1123,7 +1155,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                            w.cnt3, w.bd, G, w.H7);
     }
     MARK();
-    hipLaunchKernelGGL(k_emit, dim3(E), dim3(64), 0, st, E, w.bd, nb, w.cell2, w.owner,
+    hipLaunchKernelGGL(k_emit, dim3(grid1(E, 4)), dim3(256), 0, st, E, w.bd, nb, w.cell2, w.owner,
                        w.pass2, w.pass3, w.X4, w.H7, have_head ? 1 : 0);
     HIPCHK(hipGetLastError());
     MARK();
