@@ -430,22 +430,26 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
 
 // ---------------------------------------------------------------------------
 // O: per record y = sum_delta goW[delta]^T qh + residual, fp64 LayerNorm.
-// One workgroup = 64 records.  The contraction over K = 9*OUT (+ IN) runs in
-// parts at delta boundaries: each part's rows (the records' q*h rows at that
-// delta, zeros where out of bounds; or their inputs for input_proj) are
-// staged in LDS and each wave accumulates its 16-column tiles for all four
-// row tiles by MFMA, with the next part's weights loading meanwhile.
+// One workgroup = 64 records, one wave per 16-column output tile (OUT / 16
+// waves).  The contraction over K = 9*OUT (+ IN) runs in parts at delta
+// boundaries: each part's rows (the records' q*h rows at that delta, zeros
+// where out of bounds; or their inputs for input_proj) are fetched into
+// registers while the previous part's MFMAs run, then written to the other
+// of two LDS buffers; each wave accumulates its column tile for all four
+// row tiles.
 // ---------------------------------------------------------------------------
 template <int IN, int OUT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(OUT / kMT * 64)
 k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
       const float* __restrict__ X, const int* __restrict__ pos,
       const float* __restrict__ QVG, const float* __restrict__ po,
       const float* __restrict__ gamma, const float* __restrict__ beta, float* __restrict__ Y) {
     using O = OutPackD<IN, OUT>;
-    constexpr int NC = 3 * OUT, QST = OUT + 4, TPW = (O::NT + 3) / 4;
+    // one wave per 16-column tile of the output
+    constexpr int NTH = O::NT * 64, NC = 3 * OUT, QST = OUT + 4;
     constexpr int O4 = OUT / 4, I4 = IN / 4;
-    __shared__ __align__(16) float qs[kTM * QST];
+    constexpr int PRE = (kTM * O4 + NTH - 1) / NTH;   // float4 per thread per part
+    __shared__ __align__(16) float qs[2][kTM * QST];
     __shared__ float ys[kTM][OUT + 1];
     __shared__ double stat[kTM][2];
     __shared__ int rows[kTM];
@@ -457,88 +461,95 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
     const int tid = threadIdx.x;
     if (tid < kTM) rows[tid] = tid < cnt ? (list ? list[base + tid] : base + tid) : -1;
     __syncthreads();
-    for (int t = tid; t < kTM * kPatch; t += 256) {
+    for (int t = tid; t < kTM * kPatch; t += NTH) {
         const int r = t / kPatch, d = t - r * kPatch;
         const int g = rows[r];
         prow[d][r] = g >= 0 ? pos[(size_t)g * kPatch + d] : -1;
     }
+    __syncthreads();
     const int lane = tid & 63, wv = tid >> 6, li = lane & 15, lk = lane >> 4;
     const int mtiles = (cnt + kMT - 1) / kMT;
-    f32x4 acc[TPW][4];
+    f32x4 acc[4];
     #pragma unroll
-    for (int u = 0; u < TPW; ++u)
+    for (int m = 0; m < 4; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // a part's rows: the records' q*h rows at that delta (zeros out of
+    // bounds), or their inputs for input_proj; fetched into registers while
+    // the previous part computes, then written to the other LDS buffer
+    float4 pre[PRE];
+    auto fetch = [&](int part) {
         #pragma unroll
-        for (int m = 0; m < 4; ++m) acc[u][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto stage = [&](int part) {
-        if (part < kPatch) {
-            for (int t = tid; t < kTM * O4; t += 256) {
+        for (int u = 0; u < PRE; ++u) {
+            const int t = tid + u * NTH;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (t < kTM * O4) {
                 const int r = t / O4, q = t - r * O4;
-                const int pr = prow[part][r];
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (pr >= 0) v = reinterpret_cast<const float4*>(QVG + (size_t)pr * NC)[q];
-                *reinterpret_cast<float4*>(&qs[r * QST + 4 * q]) = v;
+                if (part < kPatch) {
+                    const int pr = prow[part][r];
+                    if (pr >= 0) v = reinterpret_cast<const float4*>(QVG + (size_t)pr * NC)[q];
+                } else {
+                    const int g = rows[r];
+                    if (g >= 0 && q < I4) v = reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q];
+                }
             }
-        } else {
-            for (int t = tid; t < kTM * O4; t += 256) {
+            pre[u] = v;
+        }
+    };
+    auto put = [&](float* buf) {
+        #pragma unroll
+        for (int u = 0; u < PRE; ++u) {
+            const int t = tid + u * NTH;
+            if (t < kTM * O4) {
                 const int r = t / O4, q = t - r * O4;
-                const int g = rows[r];
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (g >= 0 && q < I4) v = reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q];
-                *reinterpret_cast<float4*>(&qs[r * QST + 4 * q]) = v;
+                *reinterpret_cast<float4*>(&buf[r * QST + 4 * q]) = pre[u];
             }
         }
     };
-    auto loadb = [&](int part, float (&b)[TPW][O::SD]) {
+    // the four row tiles' accumulation chains interleaved step by step, so
+    // consecutive MFMAs are independent (rows past cnt hold zeros)
+    auto compute = [&](const float* buf, const float (&b)[O::SD]) {
+        const float* a = &buf[li * QST + lk];
         #pragma unroll
-        for (int u = 0; u < TPW; ++u)
-            if (wv + 4 * u < O::NT) O::load(po, wv + 4 * u, part, lane, b[u]);
-    };
-    auto compute = [&](const float (&b)[TPW][O::SD]) {
-        #pragma unroll
-        for (int u = 0; u < TPW; ++u) {
-            if (wv + 4 * u >= O::NT) continue;
+        for (int s = 0; s < O::SD; ++s)
             #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                if (m >= mtiles) continue;
-                const float* a = &qs[(m * kMT + li) * QST + lk];
-                f32x4 c = acc[u][m];
-                #pragma unroll
-                for (int s = 0; s < O::SD; ++s)
-                    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s], b[u][s], c, 0, 0, 0);
-                acc[u][m] = c;
-            }
-        }
+            for (int m = 0; m < 4; ++m)
+                acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m * kMT * QST + 4 * s], b[s], acc[m],
+                                                              0, 0, 0);
     };
-    float b0[TPW][O::SD], b1[TPW][O::SD];
-    loadb(0, b0);
+    float b0[O::SD], b1[O::SD];
+    fetch(0);
+    O::load(po, wv, 0, lane, b0);
+    put(qs[0]);
+    __syncthreads();
     #pragma unroll 1
     for (int part = 0; part < O::PARTS; part += 2) {
-        __syncthreads();                  // previous part's rows fully read
-        stage(part);
-        __syncthreads();
-        if (part + 1 < O::PARTS) loadb(part + 1, b1);
-        compute(b0);
+        // even part in qs[0] with b0
+        if (part + 1 < O::PARTS) {
+            fetch(part + 1);
+            O::load(po, wv, part + 1, lane, b1);
+        }
+        compute(qs[0], b0);
         if (part + 1 >= O::PARTS) break;
+        put(qs[1]);
         __syncthreads();
-        stage(part + 1);
+        // odd part in qs[1] with b1
+        if (part + 2 < O::PARTS) {
+            fetch(part + 2);
+            O::load(po, wv, part + 2, lane, b0);
+        }
+        compute(qs[1], b1);
+        if (part + 2 >= O::PARTS) break;
+        put(qs[0]);
         __syncthreads();
-        if (part + 2 < O::PARTS) loadb(part + 2, b0);
-        compute(b1);
     }
     #pragma unroll
-    for (int u = 0; u < TPW; ++u) {
-        const int nt = wv + 4 * u;
-        if (nt >= O::NT) continue;
+    for (int m = 0; m < 4; ++m) {
+        if (m >= mtiles) continue;
         #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            if (m >= mtiles) continue;
-            #pragma unroll
-            for (int r = 0; r < 4; ++r) ys[m * kMT + 4 * lk + r][nt * kMT + li] = acc[u][m][r];
-        }
+        for (int r = 0; r < 4; ++r) ys[m * kMT + 4 * lk + r][wv * kMT + li] = acc[m][r];
     }
     __syncthreads();
     if (!O::IP) {
-        for (int t = tid; t < cnt * OUT; t += 256) {
+        for (int t = tid; t < cnt * OUT; t += NTH) {
             const int r = t / OUT, o = t - r * OUT;
             ys[r][o] += X[(size_t)rows[r] * OUT + o];
         }
@@ -559,7 +570,7 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
         stat[r][1] = 1.0 / sqrt(var + 1e-5);
     }
     __syncthreads();
-    for (int t = tid; t < cnt * OUT; t += 256) {
+    for (int t = tid; t < cnt * OUT; t += NTH) {
         const int r = t / OUT, o = t - r * OUT;
         const double v = ((double)ys[r][o] - stat[r][0]) * stat[r][1];
         Y[(size_t)rows[r] * OUT + o] = (float)(v * (double)gamma[o] + (double)beta[o]);
@@ -1073,7 +1084,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, (const unsigned char*)nullptr, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_out<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_out<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(SSLA_C2 / kMT * 64), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, pk.po[0],
                        L[0].ln_gamma, L[0].ln_beta, w.X1);
     MARK();
@@ -1095,7 +1106,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, w.pass2, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(SSLA_C2 / kMT * 64), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, pk.po[1],
                        L[1].ln_gamma, L[1].ln_beta, w.X2);
     MARK();
@@ -1113,7 +1124,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, (const unsigned char*)nullptr, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(SSLA_C3 / kMT * 64), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, pk.po[2],
                        L[2].ln_gamma, L[2].ln_beta, w.X3);
     MARK();
@@ -1133,7 +1144,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, w.pass3, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_out<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_out<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(SSLA_C3 / kMT * 64), 0, st, E,
                        (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, pk.po[3],
                        L[3].ln_gamma, L[3].ln_beta, w.X4);
     MARK();
