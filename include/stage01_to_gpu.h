@@ -96,6 +96,13 @@ S01gReplay* s01g_replay_start(int n_rings, void* const* ring_bufs,
                               void* const* ring_heads, unsigned long long ring_mask,
                               const void* const* records, const int* counts,
                               double rate_rec_s, int pin_core);
+/* Same, paced by the records' own times: the rings are merged in record-time
+ * order (t in us) and a record goes out (t - t_first) / speed us after the
+ * start, so copies of one record in several rings go out together. */
+S01gReplay* s01g_replay_start_timed(int n_rings, void* const* ring_bufs,
+                                    void* const* ring_heads, unsigned long long ring_mask,
+                                    const void* const* records, const int* counts,
+                                    double speed, int pin_core);
 int  s01g_replay_done(S01gReplay* r);                 /* 1 when all are published */
 unsigned long long s01g_replay_published(S01gReplay* r);
 void s01g_replay_stop(S01gReplay* r);                 /* joins and frees */

@@ -656,12 +656,62 @@ struct S01gReplay {
     std::vector<int> counts;
     std::uint64_t mask = 0;
     double period_ns = 0.0;
+    double speed = 0.0;          // > 0: timed mode, record t (us) paces publishing
     int core = -1;
     std::atomic<bool> stop{false}, done{false};
     std::atomic<std::uint64_t> published{0};
     std::thread th;
 
+    void put(size_t b, const HybridInputRec& r) {
+        const std::uint64_t slot = __atomic_fetch_add(heads[b], 1ull, __ATOMIC_RELAXED);
+        HybridInputRec* d = bufs[b] + (slot & mask);
+        d->t = r.t;
+        d->x = r.x;
+        d->y = r.y;
+        std::memcpy(d->feat1, r.feat1, sizeof(float) * SSLA_C1);
+        const std::uint64_t now = ssla::mono_ns();
+        d->t_push_ns = now;
+        d->t_emit_ns = now;
+        __atomic_store_n(&d->seq_done, slot + 1ull, __ATOMIC_RELEASE);
+        published.fetch_add(1, std::memory_order_relaxed);
+    }
+
+    // timed mode: all rings merged in record-time order (ties to the lower
+    // ring); a record with time t is published (t - t_first) / speed us
+    // after the start, so records that sit in several rings (halo copies)
+    // go out together
+    void run_timed() {
+        ssla::pin_self(core);
+        std::vector<int> cur(bufs.size(), 0);
+        double t_first = 1e300;
+        for (size_t b = 0; b < bufs.size(); ++b)
+            if (counts[b] > 0) t_first = std::min(t_first, (double)recs[b][0].t);
+        const double start = (double)ssla::mono_ns();
+        while (!stop.load(std::memory_order_relaxed)) {
+            int best = -1;
+            double tb = 0.0;
+            for (size_t b = 0; b < bufs.size(); ++b) {
+                if (cur[b] >= counts[b]) continue;
+                const double t = recs[b][cur[b]].t;
+                if (best < 0 || t < tb) {
+                    best = (int)b;
+                    tb = t;
+                }
+            }
+            if (best < 0) break;
+            const double due = start + (tb - t_first) * 1e3 / speed;
+            while ((double)ssla::mono_ns() < due) ssla::cpu_relax();
+            put((size_t)best, recs[best][cur[best]]);
+            ++cur[best];
+        }
+        done.store(true, std::memory_order_release);
+    }
+
     void run() {
+        if (speed > 0.0) {
+            run_timed();
+            return;
+        }
         ssla::pin_self(core);
         int most = 0;
         for (int c : counts) most = std::max(most, c);
@@ -673,18 +723,7 @@ struct S01gReplay {
                     while ((double)ssla::mono_ns() < next) ssla::cpu_relax();
                     next += period_ns;
                 }
-                const std::uint64_t slot = __atomic_fetch_add(heads[b], 1ull, __ATOMIC_RELAXED);
-                HybridInputRec* d = bufs[b] + (slot & mask);
-                const HybridInputRec& r = recs[b][k];
-                d->t = r.t;
-                d->x = r.x;
-                d->y = r.y;
-                std::memcpy(d->feat1, r.feat1, sizeof(float) * SSLA_C1);
-                const std::uint64_t now = ssla::mono_ns();
-                d->t_push_ns = now;
-                d->t_emit_ns = now;
-                __atomic_store_n(&d->seq_done, slot + 1ull, __ATOMIC_RELEASE);
-                published.fetch_add(1, std::memory_order_relaxed);
+                put(b, recs[b][k]);
             }
         }
         done.store(true, std::memory_order_release);
@@ -693,9 +732,28 @@ struct S01gReplay {
 
 extern "C" {
 
+static S01gReplay* replay_start(int n_rings, void* const* ring_bufs, void* const* ring_heads,
+                                unsigned long long ring_mask, const void* const* records,
+                                const int* counts, double rate_rec_s, double speed, int pin_core);
+
 S01gReplay* s01g_replay_start(int n_rings, void* const* ring_bufs, void* const* ring_heads,
                               unsigned long long ring_mask, const void* const* records,
                               const int* counts, double rate_rec_s, int pin_core) {
+    return replay_start(n_rings, ring_bufs, ring_heads, ring_mask, records, counts, rate_rec_s, 0.0,
+                        pin_core);
+}
+
+S01gReplay* s01g_replay_start_timed(int n_rings, void* const* ring_bufs, void* const* ring_heads,
+                                    unsigned long long ring_mask, const void* const* records,
+                                    const int* counts, double speed, int pin_core) {
+    if (!(speed > 0.0)) return nullptr;
+    return replay_start(n_rings, ring_bufs, ring_heads, ring_mask, records, counts, 0.0, speed,
+                        pin_core);
+}
+
+static S01gReplay* replay_start(int n_rings, void* const* ring_bufs, void* const* ring_heads,
+                                unsigned long long ring_mask, const void* const* records,
+                                const int* counts, double rate_rec_s, double speed, int pin_core) {
     if (n_rings <= 0 || n_rings > 64 || !ring_bufs || !ring_heads || !records || !counts)
         return nullptr;
     if ((ring_mask & (ring_mask + 1)) != 0) return nullptr;
@@ -712,6 +770,7 @@ S01gReplay* s01g_replay_start(int n_rings, void* const* ring_bufs, void* const* 
     }
     r->mask = ring_mask;
     r->period_ns = rate_rec_s > 0 ? 1e9 / rate_rec_s : 0.0;
+    r->speed = speed;
     r->core = pin_core;
     r->th = std::thread([r]() { r->run(); });
     return r;

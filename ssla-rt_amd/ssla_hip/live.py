@@ -228,18 +228,22 @@ class ReplayResult:
 def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity: int = 1 << 16,
                timing_capacity: int = 1 << 18, max_batch: int = 32, spin_ns: int = 200,
                pin_core: Optional[int] = None, profile: bool = True, expect_p3=None,
-               drain_timeout_s: float = 60.0) -> ReplayResult:
-    """Several streams live on one GPU: pre-built ring records (one array per
-    stream) replayed into one ring each at rate_per_stream records/s, one
-    persistent workgroup per stream.  Latency is push -> prediction (the
-    records are published at their emit time).  expect_p3 (optional, one
-    pass-3 flag array per stream) gives each stream's drop drift: records
-    whose timing-slot owner flag differs from it."""
+               drain_timeout_s: float = 60.0, strips=None,
+               speed: Optional[float] = None) -> ReplayResult:
+    """Several rings live on one GPU: pre-built ring records (one array per
+    ring) replayed into one ring each, one persistent workgroup per ring.
+    Independent streams: rate_per_stream records/s each, round-robin.  One
+    stream split into owned strips (strips = owned s2 boxes, the arrays
+    holding each strip's processed-window records): speed paces all rings by
+    the records' own times, (t - t_first) / speed us after the start.
+    Latency is push -> prediction (records are published at their emit
+    time).  expect_p3 (optional, one flag array per ring) gives each ring's
+    drop drift: records whose timing-slot owner flag differs from it."""
     from .producer import Replay
     nb = len(streams)
     if pin_core is None:
         pin_core, _ = pick_cores(1)
-    drain = Drain.from_weights_dir(weights_dir, n_blocks=nb)
+    drain = Drain.from_weights_dir(weights_dir, n_blocks=nb, strips=strips)
     rings = HostRings(nb, ring_capacity)
     live = rp = None
     try:
@@ -254,9 +258,13 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
             raise RuntimeError("the live kernel did not start")
         t_start = time.monotonic()
         rp = Replay([b.ptr for b in rings.bufs], rings.head_ptrs(), ring_capacity - 1, streams,
-                    rate_per_stream * nb, pin_core)
-        t_end = time.monotonic() + sum(s.size for s in streams) / max(1.0, rate_per_stream * nb) \
-            + drain_timeout_s
+                    rate_per_stream * nb, pin_core, speed=speed)
+        if speed is not None:
+            ts = [float(x["t"][-1]) - float(x["t"][0]) for x in streams if x.size]
+            span_s = (max(ts) if ts else 0.0) / 1e6 / speed
+        else:
+            span_s = sum(x.size for x in streams) / max(1.0, rate_per_stream * nb)
+        t_end = time.monotonic() + span_s + drain_timeout_s
         while not rp.done() and time.monotonic() < t_end:
             time.sleep(0.001)
         duration = time.monotonic() - t_start

@@ -47,6 +47,7 @@ _TO_GPU_SIGNATURES = {
     "s01g_synthetic_n_pushed": (_u64, [_vp]),
     "s01g_start_synthetic_blobs": (None, [_vp, _d, _i, _u64, _i, _d, _d]),
     "s01g_replay_start": (_vp, [_i, _vpp, _vpp, _u64, _vpp, _ip, _d, _i]),
+    "s01g_replay_start_timed": (_vp, [_i, _vpp, _vpp, _u64, _vpp, _ip, _d, _i]),
     "s01g_replay_done": (_i, [_vp]),
     "s01g_replay_published": (_u64, [_vp]),
     "s01g_replay_stop": (None, [_vp]),
@@ -210,7 +211,11 @@ class Replay:
     """Paced replay of ring-record arrays into rings (s01g_replay_*)."""
 
     def __init__(self, ring_bufs, ring_heads, ring_mask: int, records, rate_rec_s: float,
-                 pin_core: int = -1, lib_path: Optional[os.PathLike] = None):
+                 pin_core: int = -1, lib_path: Optional[os.PathLike] = None,
+                 speed: Optional[float] = None):
+        """rate_rec_s: aggregate rate, rings round-robin.  speed (instead):
+        publish in merged record-time order, (t - t_first) / speed us after
+        the start."""
         self.lib = load_to_gpu(lib_path)
         n = len(ring_bufs)
         self._recs = [np.ascontiguousarray(r) for r in records]   # kept alive until stop
@@ -218,8 +223,12 @@ class Replay:
         heads = (ctypes.c_void_p * n)(*[int(p) for p in ring_heads])
         recp = (ctypes.c_void_p * n)(*[r.ctypes.data for r in self._recs])
         counts = (ctypes.c_int * n)(*[int(r.size) for r in self._recs])
-        self.h = self.lib.s01g_replay_start(n, bufs, heads, ring_mask, recp, counts,
-                                            rate_rec_s, pin_core)
+        if speed is not None:
+            self.h = self.lib.s01g_replay_start_timed(n, bufs, heads, ring_mask, recp, counts,
+                                                      float(speed), pin_core)
+        else:
+            self.h = self.lib.s01g_replay_start(n, bufs, heads, ring_mask, recp, counts,
+                                                rate_rec_s, pin_core)
         if not self.h:
             raise RuntimeError("s01g_replay_start rejected its arguments")
 

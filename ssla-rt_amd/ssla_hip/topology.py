@@ -4,7 +4,8 @@
 Same splits as orin/orin/multi_block.py:36-127 (BlockTopo, the balanced
 split that gives boundary strips HALO extra owned cells so every strip
 processes the same width, and the 2W x 1H / 2W x 2H / 2W x 4H presets for
-2 / 4 / 8 blocks), plus n_blocks = 1 (the whole grid, no halo).
+2 / 4 / 8 blocks), plus n_blocks = 1 (the whole grid, no halo) and 16
+(4W x 4H, for the full-resolution grid).
 """
 from __future__ import annotations
 
@@ -65,14 +66,16 @@ def balanced_splits(extent: int, n_strips: int, halo: int = HALO) -> List[int]:
     return out
 
 
-_PRESETS = {1: (1, 1), 2: (2, 1), 4: (2, 2), 8: (2, 4)}
+# blocks -> (x strips, y strips); 16 (4 x 4) has no counterpart in the
+# reference, whose live runner offers 2, 4 and 8
+_PRESETS = {1: (1, 1), 2: (2, 1), 4: (2, 2), 8: (2, 4), 16: (4, 4)}
 
 
 def grid_topology(n_blocks: int, W2: int, H2: int, halo: int = HALO) -> List[BlockTopo]:
     """Blocks in x-major order (all y strips of the first x strip first),
     owned boxes disjoint and covering the grid."""
     if n_blocks not in _PRESETS:
-        raise ValueError(f"unsupported n_blocks={n_blocks}; use 1, 2, 4 or 8")
+        raise ValueError(f"unsupported n_blocks={n_blocks}; use 1, 2, 4, 8 or 16")
     nw, nh = _PRESETS[n_blocks]
     xs, ys = balanced_splits(W2, nw, halo), balanced_splits(H2, nh, halo)
     out = []

@@ -21,7 +21,7 @@ def test_producer_libraries_export_every_declared_symbol():
     from ssla_hip import producer
     g = producer.load_to_gpu()
     names = declared("stage01_to_gpu.h", "s01g_")
-    assert len(names) == 17 and sorted(producer.EXPORTED_TO_GPU) == names
+    assert len(names) == 18 and sorted(producer.EXPORTED_TO_GPU) == names
     for n in names:
         assert hasattr(g, n), n
     c = producer.load_capi()

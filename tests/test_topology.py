@@ -36,7 +36,7 @@ def test_equal_processed_width_when_even(extent, n):
 
 
 @pytest.mark.parametrize("nb,W2,H2", [(1, 20, 16), (2, 20, 16), (4, 20, 16), (8, 20, 16),
-                                      (8, 160, 120)])
+                                      (8, 160, 120), (16, 160, 120)])
 def test_grid_topology_covers_grid(nb, W2, H2):
     topo = grid_topology(nb, W2, H2)
     assert len(topo) == nb
