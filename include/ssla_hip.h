@@ -54,6 +54,11 @@ int ssla_hip_free_host(void* p);
 int ssla_hip_memcpy(void* dst, const void* src, size_t nbytes);
 int ssla_hip_memset(void* dst, int value, size_t nbytes);
 int ssla_hip_device_synchronize(void);
+/* Non-blocking HIP streams at default priority for the drain entry points
+ * (the reference's harness made them with cuda-python, cuda_util.py). */
+int ssla_hip_stream_create(void** out);
+int ssla_hip_stream_destroy(void* stream);
+int ssla_hip_stream_synchronize(void* stream);
 
 /* ---- weight directory (tools/make_ssla_stub.py schema) ----------------
  * Host-only readers (no GPU): replace vendor/src/weights_loader.cpp:162-252

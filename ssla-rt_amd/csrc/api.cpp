@@ -251,6 +251,26 @@ int ssla_hip_device_synchronize(void) {
     return SSLA_OK;
 }
 
+int ssla_hip_stream_create(void** out) {
+    if (!out) { set_error("null out"); return SSLA_ERR_ARG; }
+    *out = nullptr;
+    hipStream_t s = nullptr;
+    API_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *out = s;
+    return SSLA_OK;
+}
+
+int ssla_hip_stream_destroy(void* stream) {
+    if (!stream) return SSLA_OK;
+    API_HIP(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+    return SSLA_OK;
+}
+
+int ssla_hip_stream_synchronize(void* stream) {
+    API_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return SSLA_OK;
+}
+
 long long ssla_hip_npz_read(const char* dir, const char* key, float* out, long long cap,
                             long long* shape, int* ndim) {
     if (!dir || !key) { set_error("null argument"); return SSLA_ERR_ARG; }

@@ -882,6 +882,7 @@ LiveDesc* g_bdesc_host = nullptr;
 hipEvent_t g_bcopied = nullptr;
 unsigned long long* g_bprof = nullptr;
 float* g_bpack = nullptr;
+hipEvent_t g_bdone = nullptr;   // the last batch drain's kernel
 unsigned long long* g_bprof_host = nullptr;
 
 }  // namespace
@@ -985,8 +986,12 @@ int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
         LHIP(hipMalloc(&g_bdesc, sizeof(LiveDesc) * SSLA_MAX_BLOCKS));
         LHIP(hipHostMalloc((void**)&g_bdesc_host, sizeof(LiveDesc) * SSLA_MAX_BLOCKS, hipHostMallocDefault));
         LHIP(hipEventCreateWithFlags(&g_bcopied, hipEventDisableTiming));
+        LHIP(hipEventCreateWithFlags(&g_bdone, hipEventDisableTiming));
         LHIP(hipDeviceSynchronize());
     }
+    // calls share the scratch rows and weight copies: a call on another
+    // stream runs after the previous call's kernel (device-side wait)
+    LHIP(hipStreamWaitEvent(st, g_bdone, 0));
     LHIP(hipEventSynchronize(g_bcopied));
     std::memset(g_bdesc_host, 0, sizeof(LiveDesc) * SSLA_MAX_BLOCKS);
     for (int b = 0; b < nb; ++b) {
@@ -1006,6 +1011,7 @@ int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     LHIP(pack_weights(W.L, g_bpack, &W.pk, st));
     hipLaunchKernelGGL(k_batch_drain, dim3(nb), dim3(LT), 0, st, g_bdesc, W, G, batch);
     LHIP(hipGetLastError());
+    LHIP(hipEventRecord(g_bdone, st));
     if (sync) LHIP(hipStreamSynchronize(st));
     if (phase_us) {
         LHIP(hipMemcpy(g_bprof_host, g_bprof, sizeof(unsigned long long) * NPROF * nb,

@@ -758,6 +758,7 @@ struct Workspace {
     BlockDesc* bd;
     BlockDesc* bd_host = nullptr;      // pinned staging of the block table
     hipEvent_t bd_copied = nullptr;    // the last staging copy has been read
+    hipEvent_t done = nullptr;         // the last drain's work on the workspace
     void* temp;
     size_t temp_bytes;
     float* packed = nullptr;           // fragment-order weight copies (packed_weight_floats_d)
@@ -865,6 +866,7 @@ int ensure_workspace(int E, int nkeys) {
         HIPCHK(hipHostMalloc((void**)&w.bd_host, sizeof(BlockDesc) * SSLA_MAX_BLOCKS,
                              hipHostMallocDefault));
         HIPCHK(hipEventCreateWithFlags(&w.bd_copied, hipEventDisableTiming));
+        HIPCHK(hipEventCreateWithFlags(&w.done, hipEventDisableTiming));
         HIPCHK(hipMalloc(&w.packed, sizeof(float) * packed_weight_floats_d()));
     }
     w.base = base;
@@ -974,6 +976,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // blocks with n == 0 must not capture records: move their offset past E.
     for (int b = 0; b < nb; ++b)
         if (hbd[b].n == 0) hbd[b].offset = E + 1;
+    // Calls share one workspace: a call on another stream runs after the
+    // previous call's kernels (device-side wait, the host does not block).
+    HIPCHK(hipStreamWaitEvent(st, w.done, 0));
     // The staging buffer may still be the source of the previous call's
     // copy; wait for that copy before overwriting it.
     HIPCHK(hipEventSynchronize(w.bd_copied));
@@ -1171,6 +1176,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     HIPCHK(hipGetLastError());
     MARK();
 #undef MARK
+    HIPCHK(hipEventRecord(w.done, st));
     if (sync) HIPCHK(hipStreamSynchronize(st));
     if (phase_ms) {
         for (int k = 0; k + 1 < n_ev && k < SSLA_DRAIN_PHASES; ++k) {

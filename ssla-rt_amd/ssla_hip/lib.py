@@ -30,6 +30,9 @@ _SIGNATURES = {
     "ssla_hip_memcpy": (_I, [_VP, _VP, ctypes.c_size_t]),
     "ssla_hip_memset": (_I, [_VP, _I, ctypes.c_size_t]),
     "ssla_hip_device_synchronize": (_I, []),
+    "ssla_hip_stream_create": (_I, [ctypes.POINTER(_VP)]),
+    "ssla_hip_stream_destroy": (_I, [_VP]),
+    "ssla_hip_stream_synchronize": (_I, [_VP]),
     "ssla_hip_npz_read": (_LL, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float),
                                 _LL, ctypes.POINTER(_LL), ctypes.POINTER(_I)]),
     "ssla_hip_meta_read": (_I, [ctypes.c_char_p, ctypes.POINTER(_I)]),

@@ -202,6 +202,45 @@ def test_trained_checkpoint_weights(H, trained_dir):
     assert dh <= HEAD_TOL
 
 
+def test_async_drains_on_two_streams(H, stub_dir):
+    """Two instances drained without waiting, on two HIP streams: the calls
+    share the library's workspace, so the second runs after the first on
+    the device, and both give what they give alone."""
+    import ctypes
+    from ssla_hip import lib
+    say("async drains on two streams")
+    ra = [events.to_records(events.blob_records(60_000, seed=71))]
+    rb = [events.to_records(events.blob_records(90_000, seed=72))]
+    alone = []
+    for recs in (ra, rb):
+        with H.Drain.from_weights_dir(stub_dir) as d:
+            outs, heads = d.drain(recs, want_head=True)
+            alone.append((outs[0], heads[0], d.hidden(0, 3), d.preds(0)))
+    L = lib.load()
+    s1, s2 = ctypes.c_void_p(), ctypes.c_void_p()
+    lib.check(L.ssla_hip_stream_create(ctypes.byref(s1)))
+    lib.check(L.ssla_hip_stream_create(ctypes.byref(s2)))
+    with H.Drain.from_weights_dir(stub_dir) as da, H.Drain.from_weights_dir(stub_dir) as db:
+        da.load_rings(ra, want_head=True)
+        db.load_rings(rb, want_head=True)
+        for rep in range(3):
+            da.reset()
+            db.reset()
+            da.run(stream=s1.value, sync=False)
+            db.run(stream=s2.value, sync=False)
+            lib.check(L.ssla_hip_stream_synchronize(s1))
+            lib.check(L.ssla_hip_stream_synchronize(s2))
+            for d, (o, h, hid, pr) in zip((da, db), alone):
+                outs, heads = d.results()
+                assert np.array_equal(outs[0], o) and np.array_equal(heads[0], h), rep
+                assert np.array_equal(d.hidden(0, 3), hid), rep
+                p, v = d.preds(0)
+                assert np.array_equal(p, pr[0]), rep     # versions keep counting across calls
+                assert np.array_equal(v, pr[1] * (rep + 1)), rep
+    lib.check(L.ssla_hip_stream_destroy(s1))
+    lib.check(L.ssla_hip_stream_destroy(s2))
+
+
 def test_sixteen_streams(H, stub_dir, stub_npz):
     n = 4000
     say("sixteen_streams", n)
