@@ -303,41 +303,26 @@ struct ProjTile : ProjPack<IN, OUT> {
     using ProjPack<IN, OUT>::TQ;
     using ProjPack<IN, OUT>::KS;
     using ProjPack<IN, OUT>::NC;
-    static constexpr int NMT = (LB + MT - 1) / MT;   // row tiles of a full batch
-    // acc[m] = rows [16m, 16m+16) of item `it` (rows beyond the item's count
-    // are computed from a repeated row and never stored)
-    static __device__ __forceinline__ int rows(const Lds& S, int it) {
+    static __device__ __forceinline__ void run(Lds& S, int it, int li, int lk, const float* b,
+                                               float* __restrict__ scratch) {
         const int d = it / T, t = it - d * T;
-        return t < TQ ? S.dcnto[d] : S.dcnt[d];
-    }
-    static __device__ __forceinline__ void mma(const Lds& S, int it, int n, int li, int lk,
-                                               const float* b, f32x4* acc) {
-        const int d = it / T, t = it - d * T;
-        const int* list = t < TQ ? S.devo[d] : S.dev[d];
-        const float* X = &S.X[0][0];
-        #pragma unroll
-        for (int m = 0; m < NMT; ++m) {
-            acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (m * MT < n) {
-                const int xr = list[min(m * MT + li, n - 1)] * XS + lk;
-                #pragma unroll
-                for (int s = 0; s < KS; ++s)
-                    acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(X[xr + s * 4], b[s], acc[m], 0, 0, 0);
-            }
-        }
-    }
-    static __device__ __forceinline__ void store(const Lds& S, int it, int n, int li, int lk,
-                                                 const f32x4* acc, float* __restrict__ scratch) {
-        const int d = it / T, t = it - d * T;
-        const int* list = t < TQ ? S.devo[d] : S.dev[d];
+        const bool qt = t < TQ;
+        const int n = qt ? S.dcnto[d] : S.dcnt[d];
+        const int* list = qt ? S.devo[d] : S.dev[d];
         const int col = t * MT + li;
-        #pragma unroll
-        for (int m = 0; m < NMT; ++m)
+        const float* X = &S.X[0][0];
+        for (int m0 = 0; m0 < n; m0 += MT) {
+            const int xr = list[min(m0 + li, n - 1)] * XS + lk;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            #pragma unroll
+            for (int s = 0; s < KS; ++s)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(X[xr + s * 4], b[s], acc, 0, 0, 0);
             #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int rr = m * MT + 4 * lk + r;
-                if (rr < n) gstore(scratch + (size_t)S.pidx[list[rr]][d] * NC + col, acc[m][r]);
+                const int rr = m0 + 4 * lk + r;
+                if (rr < n) gstore(scratch + (size_t)S.pidx[list[rr]][d] * NC + col, acc[r]);
             }
+        }
     }
 };
 
@@ -348,40 +333,19 @@ __device__ __forceinline__ void phase_proj(Lds& S, const float* __restrict__ pp,
     static_assert(OUT % MT == 0 && IN % 4 == 0, "tile shapes");
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int li = lane & 15, lk = lane >> 4;
-    // A wave takes its items in groups of G.  Per group: MFMAs from the
-    // group's weights (loaded during the previous group), then the next
-    // group's weight loads are issued, then this group's row stores.  Loads
-    // and stores share one in-order completion counter, so issuing the loads
-    // first lets the next group wait for its weights without waiting for
-    // the stores (at live batch sizes an item is a handful of MFMAs and the
-    // phase otherwise runs at store latency).
-    constexpr int PER = P::KS4 * 4;
-    constexpr int G = PER <= 8 ? 4 : PER <= 12 ? 4 : 2;
-    float b[G][PER];
-    f32x4 acc[G][P::NMT];
-    #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const int it = wv + g * NW;
-        if (it < P::N) P::load(pp, it, lane, b[g]);
-    }
-    for (int it0 = wv; it0 < P::N; it0 += G * NW) {
-        int n[G];
-        #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const int it = it0 + g * NW;
-            n[g] = it < P::N ? P::rows(S, it) : 0;
-            if (it < P::N) P::mma(S, it, n[g], li, lk, b[g], acc[g]);
-        }
-        #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const int nx = it0 + (G + g) * NW;
-            if (nx < P::N) P::load(pp, nx, lane, b[g]);
-        }
-        #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const int it = it0 + g * NW;
-            if (it < P::N) P::store(S, it, n[g], li, lk, acc[g], scratch);
-        }
+    // two items in flight per wave: the next item's weights load while the
+    // current item's tiles run
+    float b0[P::KS4 * 4], b1[P::KS4 * 4];
+    int it = wv;
+    if (it < P::N) P::load(pp, it, lane, b0);
+    while (it < P::N) {
+        const int i1 = it + NW, i2 = i1 + NW;
+        if (i1 < P::N) P::load(pp, i1, lane, b1);
+        P::run(S, it, li, lk, b0, scratch);
+        if (i1 >= P::N) break;
+        if (i2 < P::N) P::load(pp, i2, lane, b0);
+        P::run(S, i1, li, lk, b1, scratch);
+        it = i2;
     }
 }
 
