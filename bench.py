@@ -14,7 +14,8 @@ value = output-producing records (owner & pass2 & pass3) per second, in
 kev/s, over exactly --steps timed steps.  Alongside: ring-record kev/s (the
 unit of the reference's 247 kev/s Orin figure), the roofline of the
 dominant kernel from HIP events on the drain's stream, and the CPU baseline
-(the oracle's fp32 path, single thread) on a bounded sample.
+on bounded samples (the oracle's fp32 s2 + s3 + head on one core; s0 + s1 on
+6 shard threads; the 50,000-event CPU reference case end to end on one core).
 
 The metric's latency half comes from the live pipeline, run after the timed
 region: the host producer (6 shards, halo 2) fed by its paced synthetic
@@ -111,33 +112,160 @@ def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20, chunk=64):
     return flops, byts, total_mac
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _pin(cores) -> bool:
+    try:
+        os.sched_setaffinity(0, set(cores))
+        return True
+    except (AttributeError, OSError):
+        return False
+
+
+SEGMENTS = ("preprocess", "s0", "tdrop0", "s1", "tdrop1", "push")
+
+
+def _stage01(stub_dir, ev, n_shards, base_core, submit_cores, spawn_cores, W2, H2, ring=False):
+    """s0 + s1 of `ev` (raw [t, x, y, p] events) on n_shards shard threads
+    (halo 2; pinned to base_core, base_core + 1, ... or, when base_core < 0,
+    left on `spawn_cores`), submitted from this thread pinned to
+    `submit_cores`.
+    With `ring`, one host ring covering the whole s2 grid receives the
+    records.  Returns (seconds from submit to the last shard done, stats
+    slots, records or None)."""
+    from ssla_hip import producer as P
+    from ssla_hip.abi import INPUT_DTYPE
+    api = P.S01gAPI()
+    _pin(spawn_cores)                  # shard threads start with this mask
+    api.init(stub_dir, n_shards, 2, base_core, 1 << 14)
+    buf = head = None
+    try:
+        if ring:
+            cap = 1 << max(1, int(np.ceil(np.log2(len(ev)))))   # no wrap
+            buf = np.zeros(cap, INPUT_DTYPE)
+            head = np.zeros(1, np.uint64)
+            api.attach_multi([buf.ctypes.data], [head.ctypes.data], cap - 1, W2, H2,
+                             [0], [W2], [0], [H2])
+        n_halo = P.halo_count(ev[:, 1], 4 * W2, n_shards, 2)
+        _pin(submit_cores)
+        api.reset()
+        t0 = time.perf_counter()
+        acc = api.submit(ev)
+        st = api.wait_processed(acc, n_halo, timeout_s=120.0)
+        dt = time.perf_counter() - t0
+    finally:
+        api.shutdown()
+    return dt, st, (buf[:int(head[0])] if ring else None)
+
+
+def _segments(st, n_events):
+    """Per-segment mean time: us per item the segment handled and us per
+    submitted event (stats slots 16..27)."""
+    out = {}
+    for k, name in enumerate(SEGMENTS):
+        ns, cnt = st[16 + k], st[22 + k]
+        if cnt > 0:
+            out[name] = {"us_per_item": round(ns / cnt / 1e3, 4),
+                         "us_per_event": round(ns / n_events / 1e3, 4), "items": int(cnt)}
+    return out
+
+
 def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20):
-    """The oracle's fp32 path (the generic C++ reference path restated),
-    one thread pinned to one core, on the first records of the workload."""
+    """The CPU path timed on this host:
+      value       the oracle's fp32 s2 + s3 + head (the generic C++
+                  reference path restated), one pinned thread, on the first
+                  records of the GPU workload -- output-producing kev/s,
+                  the unit of the GPU value;
+      stage01     s0 + s1 of raw uniform events at 80x64 / 2 Mev/s on 6
+                  shard threads (cores 1-6, submission from core 0, when
+                  this process may use them);
+      end_to_end  the 50,000-event CPU reference case on one core: s0 + s1
+                  on one shard, then the records through the fp32 oracle.
+    About budget_s seconds of CPU work in all."""
     from oracle import oracle as O
+    from ssla_hip import events as E
+    all_cores = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else [0]
+    core0 = all_cores[0]
     w = O.load_npz(stub_dir)
     layers = O.layers_from_npz(w)
     head = O.head_from_npz(w)
-    try:
-        os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
-    except (AttributeError, OSError):
-        pass
+
+    # s2 + s3 + head, one thread
+    _pin([core0])
     st = O.S2S3(layers, H2, W2, 4, head=head)
     k = 4000
     t0 = time.perf_counter()
     st.run(rec.x[:k], rec.y[:k], rec.feat1[:k], precision=32, want_feat=False, want_head=True)
     rate = k / (time.perf_counter() - t0)
-    n = int(min(rec.x.size, max(k, rate * budget_s)))
+    n = int(min(rec.x.size, max(k, rate * 0.55 * budget_s)))
     st = O.S2S3(layers, H2, W2, 4, head=head)
     t0 = time.perf_counter()
     p2, p3, _, _ = st.run(rec.x[:n], rec.y[:n], rec.feat1[:n], precision=32,
                           want_feat=False, want_head=True)
     dt = time.perf_counter() - t0
     n_out = int((p3 == 1).sum())
-    return {"value": round(n_out / dt / 1e3, 4), "unit": "kev/s", "cores": 1, "kind": "port",
-            "sample": f"first {n} of the {rec.x.size} records (fp32 oracle path, "
-                      f"-O3 -ffast-math, one pinned thread); {n_out} output-producing in {dt:.2f} s",
-            "ring_record_kev_s": round(n / dt / 1e3, 3)}
+    res = {"value": round(n_out / dt / 1e3, 4), "unit": "kev/s", "cores": 1, "kind": "port",
+           "sample": f"first {n} of the {rec.x.size} records (fp32 oracle path, "
+                     f"-O3 -ffast-math -march=x86-64-v3, one pinned thread); "
+                     f"{n_out} output-producing in {dt:.2f} s",
+           "ring_record_kev_s": round(n / dt / 1e3, 3),
+           "s2s3_head_us_per_record": round(dt / n * 1e6, 3),
+           "host": {"cpu_model": _cpu_model(), "nproc": os.cpu_count(),
+                    "usable_cores": len(all_cores)},
+           "compiler_flags": {
+               "oracle_fp32": "gcc -O3 -ffast-math -march=x86-64-v3",
+               "stage01": "g++ -O3 -march=x86-64-v3 -funroll-loops -ffast-math "
+                          "-fno-finite-math-only"}}
+
+    # s0 + s1 on 6 shards
+    want = list(range(core0, core0 + 7))
+    pinned = all(c in all_cores for c in want)
+    base, sub = (core0 + 1, [core0]) if pinned else (-1, all_cores)
+    ev = E.raw_uniform(200_000, seed=2)
+    dt, _, _ = _stage01(stub_dir, ev, 6, base, sub, all_cores, W2, H2)
+    n_ev = int(min(16_000_000, max(200_000, 200_000 / dt * 0.3 * budget_s)))
+    ev = E.raw_uniform(n_ev, seed=3)
+    dt, s, _ = _stage01(stub_dir, ev, 6, base, sub, all_cores, W2, H2)
+    res["stage01"] = {
+        "events_per_s": round(n_ev / dt, 1), "events": n_ev, "seconds": round(dt, 3),
+        "shards": 6, "halo": 2,
+        "cores": (f"shards on {base}-{base + 5}, submit on {core0}" if pinned
+                  else f"unpinned over {len(all_cores)} usable cores"),
+        "pass_s0": int(s[2]), "pass_s1": int(s[13]),
+        "segments": _segments(s, n_ev),
+        "sample": f"{n_ev} raw uniform events, 80x64, 2 Mev/s timestamps, seed 3"}
+
+    # the 50k-event CPU reference case, end to end on one core
+    ev = E.raw_uniform(50_000, seed=1)
+    t01, s, recs = _stage01(stub_dir, ev, 1, core0, [core0], all_cores, W2, H2, ring=True)
+    _pin([core0])
+    st = O.S2S3(layers, H2, W2, 4, head=head)
+    t0 = time.perf_counter()
+    p2, p3, _, _ = st.run(recs["x"], recs["y"], recs["feat1"], precision=32,
+                          want_feat=False, want_head=True)
+    t23 = time.perf_counter() - t0
+    n_out = int((p3 == 1).sum())
+    res["end_to_end"] = {
+        "events_per_s": round(len(ev) / (t01 + t23), 1), "events": len(ev),
+        "records": int(len(recs)), "output_producing": n_out,
+        "output_kev_s": round(n_out / (t01 + t23) / 1e3, 4),
+        "stage01_s": round(t01, 4), "s2s3_head_s": round(t23, 4), "cores": 1,
+        "us_per_event": {"stage01": round(t01 / len(ev) * 1e6, 4),
+                         "s2s3_head": round(t23 / len(ev) * 1e6, 4)},
+        "segments": _segments(s, len(ev)),
+        "sample": "50,000 raw uniform events at 80x64, 2 Mev/s, seed 1; one shard "
+                  f"thread and the oracle on core {core0}"}
+    _pin(all_cores)
+    return res
 
 
 # kernel of each timed launch of the whole-ring drain (ssla-rt_amd/csrc/drain_scan.hip)

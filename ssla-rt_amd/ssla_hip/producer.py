@@ -117,6 +117,21 @@ def routing(x, W: int, n_shards: int, halo: int):
     return owner, halo_to
 
 
+def halo_count(x, W: int, n_shards: int, halo: int) -> int:
+    """len(routing(x, W, n_shards, halo)[1]), without building the list."""
+    x = np.asarray(x, np.int64)
+    strip = (W + n_shards - 1) // n_shards
+    home = x // strip
+    owner = np.minimum(home, n_shards - 1)
+    n = 0
+    for dk in (-1, 0, 1):
+        k = home + dk
+        ok = (k >= 0) & (k < n_shards) & (k != owner)
+        ok &= (x >= k * strip - halo) & (x < (k + 1) * strip + halo)
+        n += int(ok.sum())
+    return n
+
+
 class S01gAPI:
     """One libstage01_to_gpu.so handle (hybrid_common.py:468-605)."""
 

@@ -274,6 +274,23 @@ def test_sharded_matches_oracle_per_shard(stub_dir, stub_npz, n_shards, halo):
     _check_records(rings.records(0), ev, p1, feat)
 
 
+@pytest.mark.parametrize("n_shards,halo", [(1, 2), (3, 2), (6, 2), (8, 4)])
+def test_halo_count_matches_routing(n_shards, halo):
+    x = np.arange(-3, W0 + 3)
+    want = len(P.routing(x, W0, n_shards, halo)[1])
+    assert P.halo_count(x, W0, n_shards, halo) == want
+    # brute force over shard strips: every shard whose halo-widened strip
+    # holds x, other than the owner
+    strip = (W0 + n_shards - 1) // n_shards
+    brute = 0
+    for xi in x:
+        own = min(xi // strip, n_shards - 1)
+        for k in range(n_shards):
+            if k != own and abs(k - xi // strip) <= 1 and k * strip - halo <= xi < (k + 1) * strip + halo:
+                brute += 1
+    assert want == brute
+
+
 def test_ring_boxes(stub_dir, stub_npz):
     """Two rings over overlapping s2 x ranges (block_proc_range with halo 2):
     each record goes to every ring whose box holds its s2 cell."""
