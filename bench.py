@@ -416,6 +416,37 @@ def split_replay_latency(stub_dir, rec, H2, W2, n_blocks=16, speed=1.0):
     }
 
 
+def batch_bench(a, d, recs, n, S, steps, warmup, desc, tmp) -> int:
+    """Offline drain through the live kernel's batch loop (the persistent
+    kernel's code path, fed from pre-filled rings)."""
+    from ssla_hip import lib
+    for _ in range(warmup):
+        d.reset(sync=False)
+        d.run(sync=True, batch=a.batch)
+    lib.check(lib.load().ssla_hip_device_synchronize())
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        d.reset(sync=False)
+        d.run(sync=True, batch=a.batch)
+    lib.check(lib.load().ssla_hip_device_synchronize())
+    dt = time.perf_counter() - t0
+    outs, _ = d.results()
+    n_out = sum(int((o["pass3"] == 1).sum()) for o in outs)
+    d.close()
+    tmp.cleanup()
+    print(json.dumps({
+        "metric": METRIC, "value": round(n_out * max(steps, 1) / dt / 1e3, 3) if steps else None,
+        "unit": "kev/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(dt * 1e3 / steps, 4) if steps else None,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": desc, "records": n * S, "instances": S,
+                   "mode": f"in-kernel batches of {a.batch} (live kernel), one workgroup "
+                           "per instance", "output_producing_per_step": n_out},
+        "ring_record_kev_s": round(n * S * steps / dt / 1e3, 2) if steps else None}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -432,7 +463,14 @@ def main() -> int:
     ap.add_argument("--live-seconds", type=float, default=8.0)
     ap.add_argument("--live-blocks", type=int, default=8, choices=[1, 2, 4, 8],
                     help="GPU blocks (owned strips) of the live run")
+    ap.add_argument("--batch", type=int, default=0,
+                    help="1..32: drain through the live kernel's in-kernel batches of this "
+                         "many records (one workgroup per instance) instead of the whole-ring "
+                         "drain; reports throughput only")
     a = ap.parse_args()
+    if not 0 <= a.batch <= 32:
+        print("bench.py: --batch must be 0..32", file=sys.stderr)
+        return 2
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (one drain instance set per "
               "device, no collectives); run with --gpus 1", file=sys.stderr)
@@ -463,6 +501,8 @@ def main() -> int:
 
     d = hybrid.Drain.from_weights_dir(tmp.name, n_blocks=S)
     d.load_rings([events.to_records(r) for r in recs], want_head=True)
+    if a.batch:
+        return batch_bench(a, d, recs, n, S, steps, warmup, desc, tmp)
     nph = len(abi.DRAIN_PHASES)
     for _ in range(warmup):
         d.reset(sync=False)

@@ -31,6 +31,7 @@
 // Device layouts are those of include/ssla_abi.h.
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
+#include <rocprim/device/device_radix_sort.hpp>
 
 #include <cstdint>
 #include <cstdio>
@@ -210,13 +211,24 @@ __global__ void k_pair_pos(int n, const uint32_t* __restrict__ keys,
 // ---------------------------------------------------------------------------
 constexpr int kTM = 64;     // records per projection / contraction workgroup
 
+// Row stride of the LDS tiles read as MFMA A operands, a[(16 m + li) ST + lk
+// + 4 s] with li = lane % 16, lk = lane / 16: a stride of 2 (mod 4) puts the
+// 32 lanes of each half-wave on 32 distinct banks (a multiple of 4 pairs row
+// li with row li + 8).  Rows are then 8-byte aligned: written as float2.
+constexpr int lds_stride(int n) { return n + 2; }    // n % 4 == 0
+
+__device__ __forceinline__ void lds_put4(float* p, float4 v) {
+    reinterpret_cast<float2*>(p)[0] = make_float2(v.x, v.y);
+    reinterpret_cast<float2*>(p)[1] = make_float2(v.z, v.w);
+}
+
 template <int IN, int OUT>
 __global__ void __launch_bounds__(256)
 k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
       const float* __restrict__ X, const int* __restrict__ pos, const float* __restrict__ pp,
       float* __restrict__ QVG, int tlo, int thi) {
     using P = ProjPack<IN, OUT>;
-    constexpr int NC = P::NC, XST = IN + 4;
+    constexpr int NC = P::NC, XST = lds_stride(IN);
     __shared__ __align__(16) float xs[kTM * XST];
     __shared__ int prow[kPatch][kTM];
     const int n = n_dev ? *n_dev : n_max;
@@ -232,7 +244,7 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
             const int g = list ? list[base + r] : base + r;
             v = reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q];
         }
-        *reinterpret_cast<float4*>(&xs[r * XST + 4 * q]) = v;
+        lds_put4(&xs[r * XST + 4 * q], v);
     }
     for (int t = tid; t < kTM * kPatch; t += 256) {
         const int r = t / kPatch, d = t - r * kPatch;
@@ -446,7 +458,7 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
       const float* __restrict__ gamma, const float* __restrict__ beta, float* __restrict__ Y) {
     using O = OutPackD<IN, OUT>;
     // one wave per 16-column tile of the output
-    constexpr int NTH = O::NT * 64, NC = 3 * OUT, QST = OUT + 4;
+    constexpr int NTH = O::NT * 64, NC = 3 * OUT, QST = lds_stride(OUT);
     constexpr int O4 = OUT / 4, I4 = IN / 4;
     constexpr int PRE = (kTM * O4 + NTH - 1) / NTH;   // float4 per thread per part
     __shared__ __align__(16) float qs[2][kTM * QST];
@@ -500,7 +512,7 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
             const int t = tid + u * NTH;
             if (t < kTM * O4) {
                 const int r = t / O4, q = t - r * O4;
-                *reinterpret_cast<float4*>(&buf[r * QST + 4 * q]) = pre[u];
+                lds_put4(&buf[r * QST + 4 * q], pre[u]);
             }
         }
     };
@@ -589,7 +601,7 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 __global__ void __launch_bounds__(256)
 k_head(const int* __restrict__ n_dev, const int* __restrict__ list,
        const float* __restrict__ X, HeadPtrs hp, float* __restrict__ H7) {
-    constexpr int C = SSLA_C3, XST = C + 4, HST = 2 * C + 4, CT = 2 * C / kMT;
+    constexpr int C = SSLA_C3, XST = lds_stride(C), HST = 2 * C + 4, CT = 2 * C / kMT;
     __shared__ __align__(16) float xs[kTM * XST];
     __shared__ float hs[kTM * HST];           // [yc | yr] per record
     __shared__ int rows[kTM];
@@ -605,7 +617,7 @@ k_head(const int* __restrict__ n_dev, const int* __restrict__ list,
         const int r = t / C4, q = t - r * C4;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (rows[r] >= 0) v = reinterpret_cast<const float4*>(X)[(size_t)rows[r] * C4 + q];
-        *reinterpret_cast<float4*>(&xs[r * XST + 4 * q]) = v;
+        lds_put4(&xs[r * XST + 4 * q], v);
     }
     __syncthreads();
     const int lane = tid & 63, wv = tid >> 6, li = lane & 15, lk = lane >> 4;
@@ -778,6 +790,19 @@ Workspace g_ws;
 
 size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 
+// Stable LSD radix sort of (key, value) pairs on bits [0, bits).  rocPRIM's
+// default configuration sorts up to 1 M pairs of 32-bit keys by block sort
+// plus a merge pass per doubling (16 launches at 200 k records); the
+// Onesweep path needs one launch per 8 key bits plus a histogram.
+using SortConfig = rocprim::radix_sort_config<rocprim::default_config, rocprim::default_config,
+                                              rocprim::default_config, 0>;
+
+hipError_t sort_pairs(void* temp, size_t& bytes, const uint32_t* ki, uint32_t* ko,
+                      const uint32_t* vi, uint32_t* vo, int n, int bits, hipStream_t st) {
+    return rocprim::radix_sort_pairs<SortConfig>(temp, bytes, ki, ko, vi, vo, (size_t)n, 0u,
+                                                 (unsigned)bits, st);
+}
+
 int ensure_workspace(int E, int nkeys) {
     if (E <= g_ws.cap && nkeys <= g_ws.cap_keys) return SSLA_OK;
     if (g_ws.base) {
@@ -791,9 +816,7 @@ int ensure_workspace(int E, int nkeys) {
     const size_t P = (size_t)cap * kPatch;
     // temp storage: radix sort of P pairs and the flagged selections.
     size_t t_sort = 0, t_sel = 0;
-    HIPCHK(hipcub::DeviceRadixSort::SortPairs(nullptr, t_sort, (uint32_t*)nullptr,
-                                               (uint32_t*)nullptr, (uint32_t*)nullptr,
-                                               (uint32_t*)nullptr, (int)P, 0, 32));
+    HIPCHK(sort_pairs(nullptr, t_sort, nullptr, nullptr, nullptr, nullptr, (int)P, 32, nullptr));
     HIPCHK(hipcub::DeviceSelect::Flagged(nullptr, t_sel, hipcub::CountingInputIterator<int>(0),
                                           (unsigned char*)nullptr, (int*)nullptr,
                                           (int*)nullptr, cap));
@@ -1008,8 +1031,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // ---- decode; tdrop_s2 from a stable sort of records by centre cell ----
     hipLaunchKernelGGL(k_decode, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, w.X0,
                        w.cell2, w.owner, w.ka, w.va);
-    HIPCHK(hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, E, 0,
-                                               bits2, st));
+    HIPCHK(sort_pairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, E, bits2, st));
     hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.st2, 0);
     hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.en2, 0);
     hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, nk2, w.st2, w.en2);
@@ -1020,8 +1042,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // ---- s2 pair order: (record, delta) pairs sorted by patch cell ----------
     hipLaunchKernelGGL(k_pairs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, 2,
                        w.cell2, w.pass2, w.kb, w.vb);
-    HIPCHK(hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, 0,
-                                               bits2, st));
+    HIPCHK(sort_pairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, bits2, st));
     hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.pst2, 0);
     hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.pen2, 0);
     hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, nk2, w.pst2, w.pen2);
@@ -1030,8 +1051,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // ---- tdrop_s3 over pass2 records, by s3 centre cell ---------------------
     hipLaunchKernelGGL(k_keys3, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, w.cell2,
                        w.pass2, w.key3g, w.ka, w.va);
-    HIPCHK(hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, E, 0,
-                                               bits3, st));
+    HIPCHK(sort_pairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, E, bits3, st));
     hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.st3, 0);
     hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.en3, 0);
     hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, nk3, w.st3, w.en3);
@@ -1042,8 +1062,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // ---- s3 pair order ---------------------------------------------------------
     hipLaunchKernelGGL(k_pairs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, 3,
                        w.cell2, w.pass2, w.kb, w.vb);
-    HIPCHK(hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, 0,
-                                               bits3, st));
+    HIPCHK(sort_pairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, bits3, st));
     hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.pst3, 0);
     hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.pen3, 0);
     hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, nk3, w.pst3, w.pen3);
