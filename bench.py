@@ -179,7 +179,7 @@ def _segments(st, n_events):
     return out
 
 
-def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20):
+def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20, gpu_flags=None):
     """The CPU path timed on this host:
       value       the oracle's fp32 s2 + s3 + head (the generic C++
                   reference path restated), one pinned thread, on the first
@@ -190,6 +190,9 @@ def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20):
                   this process may use them);
       end_to_end  the 50,000-event CPU reference case on one core: s0 + s1
                   on one shard, then the records through the fp32 oracle.
+    gpu_flags = (pass2, pass3) of the drain's first step over `rec` (from
+    reset state): the oracle's decisions over the same records are compared
+    with them (drop drift, bit for bit).
     About budget_s seconds of CPU work in all."""
     from oracle import oracle as O
     from ssla_hip import events as E
@@ -218,6 +221,10 @@ def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20):
                      f"-O3 -ffast-math -march=x86-64-v3, one pinned thread); "
                      f"{n_out} output-producing in {dt:.2f} s",
            "ring_record_kev_s": round(n / dt / 1e3, 3),
+           "drop_drift_vs_oracle": None if gpu_flags is None else {
+               "records_checked": n,
+               "pass2_differ": int(((gpu_flags[0][:n] == 1) != (p2 == 1)).sum()),
+               "pass3_differ": int(((gpu_flags[1][:n] == 1) != (p3 == 1)).sum())},
            "s2s3_head_us_per_record": round(dt / n * 1e6, 3),
            "host": {"cpu_model": _cpu_model(), "nproc": os.cpu_count(),
                     "usable_cores": len(all_cores)},
@@ -380,21 +387,22 @@ def split_replay_latency(stub_dir, rec, H2, W2, n_blocks=16, speed=1.0):
     reference's multi-block layout, 4 x 4 here): every strip's ring gets the
     records of its processed window (halo copies included), all rings
     replayed by the records' own times at `speed`; push -> prediction per
-    strip and drop drift against each strip's own decision schedule."""
-    from oracle import oracle as O
-    from ssla_hip import events, live
+    strip and drop drift against each strip's own decision schedule (the
+    whole-ring drain of the same strip rings)."""
+    from ssla_hip import events, hybrid, live
     from ssla_hip.topology import grid_topology
     topo = grid_topology(n_blocks, W2, H2)
     full = events.to_records(rec)
     x, y = rec.x.astype(np.int64), rec.y.astype(np.int64)
-    rings, expect = [], []
+    rings = []
     for t in topo:
         m = (x >= t.proc_x_lo) & (x < t.proc_x_hi) & (y >= t.proc_y_lo) & (y < t.proc_y_hi)
-        xb, yb = x[m], y[m]
-        own = (xb >= t.owned_x_lo) & (xb < t.owned_x_hi) & (yb >= t.owned_y_lo) & (yb < t.owned_y_hi)
-        _, p3, _, _ = O.decisions(xb, yb, H2, W2, 4)
         rings.append(full[m])
-        expect.append((own & (p3 == 1)).astype(np.int8))
+    with hybrid.Drain.from_weights_dir(stub_dir, n_blocks=len(topo),
+                                       strips=[t.owned for t in topo]) as d:
+        d.drain(rings)
+        outs, _ = d.results()
+    expect = [(o["pass3"] == 1).astype(np.int8) for o in outs]
     cap = 1 << max(16, int(np.ceil(np.log2(max(r.size for r in rings) + 1))))
     r = live.run_replay(stub_dir, rings, 0.0, strips=[t.owned for t in topo], speed=speed,
                         timing_capacity=cap, expect_p3=expect)
@@ -571,7 +579,8 @@ def main() -> int:
     if a.workload == "640x480" and not a.no_live:
         res["latency_us"] = split_replay_latency(tmp.name, recs[0], H2, W2)
     if not a.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(tmp.name, recs[0], a.cpu_seconds, H2, W2)
+        res["cpu_baseline"] = cpu_baseline(tmp.name, recs[0], a.cpu_seconds, H2, W2,
+                                           (outs[0]["pass2"], outs[0]["pass3"]))
     tmp.cleanup()
     print(json.dumps(res))
     return 0
