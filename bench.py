@@ -179,7 +179,25 @@ def _segments(st, n_events):
     return out
 
 
-def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20, gpu_flags=None):
+def _compare(gpu_out, n, p2, p3, feat, head7):
+    """The drain's first-step outputs against the oracle's fp32 path over the
+    first n records: decisions bit for bit, s3_feat and raw head outputs of
+    records both mark pass-3 (and the drain owns)."""
+    out, head = gpu_out
+    g2, g3 = out["pass2"][:n] == 1, out["pass3"][:n] == 1
+    m = g3 & (p3 == 1)
+    res = {"records_checked": int(n), "pass2_differ": int((g2 != (p2 == 1)).sum()),
+           "pass3_differ": int((g3 != (p3 == 1)).sum()), "pass3_records": int(m.sum())}
+    if m.any():
+        d = np.abs(out["s3_feat"][:n][m] - feat[m])
+        res["s3_feat_max_abs_diff"] = float(d.max())
+        res["s3_feat_max_rel_diff"] = float(d.max() / max(np.abs(feat[m]).max(), 1e-30))
+        if head is not None:
+            res["head_max_abs_diff"] = float(np.abs(head[:n][m] - head7[m]).max())
+    return res
+
+
+def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20, gpu_out=None):
     """The CPU path timed on this host:
       value       the oracle's fp32 s2 + s3 + head (the generic C++
                   reference path restated), one pinned thread, on the first
@@ -190,9 +208,8 @@ def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20, gpu_flags=None):
                   this process may use them);
       end_to_end  the 50,000-event CPU reference case on one core: s0 + s1
                   on one shard, then the records through the fp32 oracle.
-    gpu_flags = (pass2, pass3) of the drain's first step over `rec` (from
-    reset state): the oracle's decisions over the same records are compared
-    with them (drop drift, bit for bit).
+    gpu_out = (output slots, head rows) of the drain's first step over `rec`
+    (from reset state), compared with the oracle over the same records.
     About budget_s seconds of CPU work in all."""
     from oracle import oracle as O
     from ssla_hip import events as E
@@ -212,8 +229,8 @@ def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20, gpu_flags=None):
     n = int(min(rec.x.size, max(k, rate * 0.55 * budget_s)))
     st = O.S2S3(layers, H2, W2, 4, head=head)
     t0 = time.perf_counter()
-    p2, p3, _, _ = st.run(rec.x[:n], rec.y[:n], rec.feat1[:n], precision=32,
-                          want_feat=False, want_head=True)
+    p2, p3, feat, head7 = st.run(rec.x[:n], rec.y[:n], rec.feat1[:n], precision=32,
+                                 want_feat=True, want_head=True)
     dt = time.perf_counter() - t0
     n_out = int((p3 == 1).sum())
     res = {"value": round(n_out / dt / 1e3, 4), "unit": "kev/s", "cores": 1, "kind": "port",
@@ -221,10 +238,8 @@ def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20, gpu_flags=None):
                      f"-O3 -ffast-math -march=x86-64-v3, one pinned thread); "
                      f"{n_out} output-producing in {dt:.2f} s",
            "ring_record_kev_s": round(n / dt / 1e3, 3),
-           "drop_drift_vs_oracle": None if gpu_flags is None else {
-               "records_checked": n,
-               "pass2_differ": int(((gpu_flags[0][:n] == 1) != (p2 == 1)).sum()),
-               "pass3_differ": int(((gpu_flags[1][:n] == 1) != (p3 == 1)).sum())},
+           "parity_vs_oracle": None if gpu_out is None else _compare(gpu_out, n, p2, p3,
+                                                                          feat, head7),
            "s2s3_head_us_per_record": round(dt / n * 1e6, 3),
            "host": {"cpu_model": _cpu_model(), "nproc": os.cpu_count(),
                     "usable_cores": len(all_cores)},
@@ -515,7 +530,7 @@ def main() -> int:
     for _ in range(warmup):
         d.reset(sync=False)
         d.run(sync=True)
-    outs, _ = d.results()
+    outs, heads = d.results()
     n_out = sum(int((o["pass3"] == 1).sum()) for o in outs)
 
     phase = np.zeros(nph, np.float32)
@@ -580,7 +595,7 @@ def main() -> int:
         res["latency_us"] = split_replay_latency(tmp.name, recs[0], H2, W2)
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(tmp.name, recs[0], a.cpu_seconds, H2, W2,
-                                           (outs[0]["pass2"], outs[0]["pass3"]))
+                                           (outs[0], heads[0]))
     tmp.cleanup()
     print(json.dumps(res))
     return 0

@@ -73,21 +73,27 @@ __device__ __forceinline__ int find_block(const BlockDesc* bd, int nb, int g) {
 // ---------------------------------------------------------------------------
 // decode: ring records -> compact features, centre cells, sort keys
 // ---------------------------------------------------------------------------
-__global__ void k_decode(int E, const BlockDesc* __restrict__ bd, Geometry G,
-                         float* __restrict__ X0, int* __restrict__ cell2,
-                         unsigned char* __restrict__ owner,
-                         uint32_t* __restrict__ key2, uint32_t* __restrict__ val2) {
-    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+// Eight lanes per 128-byte record, one 16-byte load each: lanes 1..6 move the
+// feat1 quarters, lane 0 also writes the keys.
+constexpr int kDecRec = 32;          // records per 256-thread workgroup
+
+__global__ void __launch_bounds__(256)
+k_decode(int E, const BlockDesc* __restrict__ bd, Geometry G,
+         float* __restrict__ X0, int* __restrict__ cell2,
+         unsigned char* __restrict__ owner,
+         uint32_t* __restrict__ key2, uint32_t* __restrict__ val2) {
+    const int g = blockIdx.x * kDecRec + (threadIdx.x >> 3);
+    const int c = threadIdx.x & 7;
     if (g >= E) return;
     const int b = find_block(bd, G.nb, g);
-    const HybridInputRec& r = bd[b].ring[g - bd[b].offset];
-    const int x = r.x, y = r.y;
+    const HybridInputRec* r = bd[b].ring + (g - bd[b].offset);
+    const float4 v = reinterpret_cast<const float4*>(r)[c];
+    const int x = r->x, y = r->y;
     const bool valid = x < G.W2 && y < G.H2;
-    float4* dst = reinterpret_cast<float4*>(X0 + (size_t)g * SSLA_C1);
-    const float4* src = reinterpret_cast<const float4*>(r.feat1);
-    #pragma unroll
-    for (int i = 0; i < SSLA_C1 / 4; ++i)
-        dst[i] = valid ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c >= 1 && c <= SSLA_C1 / 4)
+        reinterpret_cast<float4*>(X0 + (size_t)g * SSLA_C1)[c - 1] =
+            valid ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c != 0) return;
     const HybridStrip& s = bd[b].strip;
     owner[g] = (valid && x >= s.owned_lo && x < s.owned_hi &&
                 y >= s.owned_y_lo && y < s.owned_y_hi) ? 1 : 0;
@@ -142,9 +148,18 @@ __global__ void k_pairs(int E, const BlockDesc* __restrict__ bd, Geometry G,
     }
 }
 
-__global__ void k_fill_i32(int n, int* __restrict__ p, int v) {
+// Up to kFills int arrays set to a value each, one launch (blockIdx.y = array).
+constexpr int kFills = 10;
+struct FillSet {
+    int* p[kFills];
+    int n[kFills];
+    int v[kFills];
+};
+
+__global__ void k_fill_set(FillSet f) {
+    const int a = blockIdx.y;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = v;
+    if (i < f.n[a]) f.p[a][i] = f.v[a];
 }
 
 // [start, end) of every key present in a sorted key array.
@@ -718,34 +733,64 @@ __global__ void k_pred_write(const int* __restrict__ n_dev, const int* __restric
 }
 
 // Output slots (...celled.cuh:1233-1247 conventions) and raw head rows.
-__global__ void k_emit(int E, const BlockDesc* __restrict__ bd, int nb,
-                       const int* __restrict__ cell2,
-                       const unsigned char* __restrict__ owner,
-                       const unsigned char* __restrict__ pass2,
-                       const unsigned char* __restrict__ pass3,
-                       const float* __restrict__ X4, const float* __restrict__ H7,
-                       int have_head) {
-    // one wave per record, four records per workgroup
-    const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (g >= E) return;
-    const int b = find_block(bd, nb, g);
-    const int k = g - bd[b].offset;
-    const bool valid = cell2[g] >= 0;
-    const bool p2 = valid && pass2[g], p3 = p2 && pass3[g], own = owner[g];
-    HybridS2S3OutputSlot* out = bd[b].out;
-    if (out) {
-        HybridS2S3OutputSlot& s = out[k];
-        if (lane == 0) {
-            s.pass2 = !valid ? -2 : (own ? (p2 ? 1 : 0) : -1);
-            s.pass3 = !valid ? -2 : (own ? (p3 ? 1 : 0) : -1);
+// Output slots (392 B = 49 eight-byte words) and head rows as coalesced
+// 8-byte stores: 32 records per 256-thread workgroup.
+constexpr int kEmitRec = 32;
+
+__global__ void __launch_bounds__(256)
+k_emit(int E, const BlockDesc* __restrict__ bd, int nb,
+       const int* __restrict__ cell2,
+       const unsigned char* __restrict__ owner,
+       const unsigned char* __restrict__ pass2,
+       const unsigned char* __restrict__ pass3,
+       const float* __restrict__ X4, const float* __restrict__ H7,
+       int have_head) {
+    constexpr int NW = (int)(sizeof(HybridS2S3OutputSlot) / 8);
+    static_assert(sizeof(HybridS2S3OutputSlot) % 8 == 0 && SSLA_C3 % 2 == 0, "slot words");
+    __shared__ int sb[kEmitRec], sk[kEmitRec], sp2[kEmitRec], sp3[kEmitRec];
+    __shared__ unsigned char sfeat[kEmitRec], shead[kEmitRec];
+    const int g0 = blockIdx.x * kEmitRec;
+    const int t = threadIdx.x;
+    if (t < kEmitRec) {
+        const int g = g0 + t;
+        int b = 0, k = -1, q2 = -2, q3 = -2;
+        bool feat = false, head = false;
+        if (g < E) {
+            b = find_block(bd, nb, g);
+            k = g - bd[b].offset;
+            const bool valid = cell2[g] >= 0;
+            const bool p2 = valid && pass2[g], p3 = p2 && pass3[g], own = owner[g];
+            if (valid) {
+                q2 = own ? (p2 ? 1 : 0) : -1;
+                q3 = own ? (p3 ? 1 : 0) : -1;
+            }
+            feat = p3;
+            head = have_head && p3 && own;
         }
-        for (int i = lane; i < SSLA_C3; i += 64)
-            s.s3_feat[i] = p3 ? X4[(size_t)g * SSLA_C3 + i] : 0.f;
+        sb[t] = b; sk[t] = k; sp2[t] = q2; sp3[t] = q3;
+        sfeat[t] = feat; shead[t] = head;
     }
-    float* ho = bd[b].head_out;
-    if (ho && lane < 7)
-        ho[(size_t)k * 7 + lane] = (have_head && p3 && own) ? H7[(size_t)g * 7 + lane] : 0.f;
+    __syncthreads();
+    for (int j = t; j < kEmitRec * NW; j += 256) {
+        const int r = j / NW, w = j - r * NW;
+        const int k = sk[r];
+        HybridS2S3OutputSlot* out = k >= 0 ? bd[sb[r]].out : nullptr;
+        if (!out) continue;
+        if (w == 0) {
+            reinterpret_cast<int2*>(out + k)[0] = make_int2(sp2[r], sp3[r]);
+        } else {
+            const int i = 2 * (w - 1);
+            float2 f = make_float2(0.f, 0.f);
+            if (sfeat[r]) f = *reinterpret_cast<const float2*>(X4 + (size_t)(g0 + r) * SSLA_C3 + i);
+            reinterpret_cast<float2*>(out[k].s3_feat)[w - 1] = f;
+        }
+    }
+    for (int j = t; j < kEmitRec * 7; j += 256) {
+        const int r = j / 7, c = j - r * 7;
+        const int k = sk[r];
+        float* ho = k >= 0 ? bd[sb[r]].head_out : nullptr;
+        if (ho) ho[(size_t)k * 7 + c] = shead[r] ? H7[(size_t)(g0 + r) * 7 + c] : 0.f;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1028,12 +1073,26 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     const int bits2 = bits_for(nk2), bits3 = bits_for(nk3);
     size_t tb = w.temp_bytes;
 
+    // run bounds (filled by k_runs where a key occurs) and the head's
+    // per-cell tables start from these values
+    {
+        FillSet f{};
+        int* arr[kFills] = {w.st2, w.en2, w.pst2, w.pen2, w.st3, w.en3, w.pst3, w.pen3,
+                            w.last3, w.cnt3};
+        const int len[kFills] = {(int)nk2, (int)nk2, (int)nk2, (int)nk2, (int)nk3, (int)nk3,
+                                 (int)nk3, (int)nk3, have_head ? (int)nk3 : 0,
+                                 have_head ? (int)nk3 : 0};
+        for (int i = 0; i < kFills; ++i) {
+            f.p[i] = arr[i];
+            f.n[i] = len[i];
+            f.v[i] = i == 8 ? -1 : 0;
+        }
+        hipLaunchKernelGGL(k_fill_set, dim3(grid1(nk2, 256), kFills), dim3(256), 0, st, f);
+    }
     // ---- decode; tdrop_s2 from a stable sort of records by centre cell ----
-    hipLaunchKernelGGL(k_decode, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, w.X0,
+    hipLaunchKernelGGL(k_decode, dim3(grid1(E, kDecRec)), dim3(256), 0, st, E, w.bd, G, w.X0,
                        w.cell2, w.owner, w.ka, w.va);
     HIPCHK(sort_pairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, E, bits2, st));
-    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.st2, 0);
-    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.en2, 0);
     hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, nk2, w.st2, w.en2);
     hipLaunchKernelGGL(k_tdrop, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, w.vb, nk2,
                        G.C2, w.st2, w.bd, 2, G.window, w.pass2);
@@ -1043,8 +1102,6 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL(k_pairs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, 2,
                        w.cell2, w.pass2, w.kb, w.vb);
     HIPCHK(sort_pairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, bits2, st));
-    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.pst2, 0);
-    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk2, 256)), dim3(256), 0, st, (int)nk2, w.pen2, 0);
     hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, nk2, w.pst2, w.pen2);
     hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, w.va, nk2,
                        w.pos2, w.prec2);
@@ -1052,8 +1109,6 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL(k_keys3, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, w.cell2,
                        w.pass2, w.key3g, w.ka, w.va);
     HIPCHK(sort_pairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, E, bits3, st));
-    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.st3, 0);
-    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.en3, 0);
     hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, nk3, w.st3, w.en3);
     hipLaunchKernelGGL(k_tdrop, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, w.vb, nk3,
                        G.C3, w.st3, w.bd, 3, G.window, w.pass3);
@@ -1063,8 +1118,6 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL(k_pairs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, 3,
                        w.cell2, w.pass2, w.kb, w.vb);
     HIPCHK(sort_pairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, bits3, st));
-    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.pst3, 0);
-    hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.pen3, 0);
     hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, nk3, w.pst3, w.pen3);
     hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, w.va, nk3,
                        w.pos3, w.prec3);
@@ -1181,8 +1234,6 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                     cfg->head_obj_pred_b};
         hipLaunchKernelGGL(k_head, dim3(tilesE), dim3(256), 0, st, (const int*)(w.counts + 1),
                            w.list3, w.X4, hp, w.H7);
-        hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.last3, -1);
-        hipLaunchKernelGGL(k_fill_i32, dim3(grid1(nk3, 256)), dim3(256), 0, st, (int)nk3, w.cnt3, 0);
         hipLaunchKernelGGL(k_pred_last, dim3(grid1(E, 256)), dim3(256), 0, st,
                            (const int*)(w.counts + 1), w.list3, w.owner, w.key3g, w.last3, w.cnt3);
         hipLaunchKernelGGL(k_pred_write, dim3(grid1(E, 256)), dim3(256), 0, st,
@@ -1190,7 +1241,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                            w.cnt3, w.bd, G, w.H7);
     }
     MARK();
-    hipLaunchKernelGGL(k_emit, dim3(grid1(E, 4)), dim3(256), 0, st, E, w.bd, nb, w.cell2, w.owner,
+    hipLaunchKernelGGL(k_emit, dim3(grid1(E, kEmitRec)), dim3(256), 0, st, E, w.bd, nb, w.cell2, w.owner,
                        w.pass2, w.pass3, w.X4, w.H7, have_head ? 1 : 0);
     HIPCHK(hipGetLastError());
     MARK();

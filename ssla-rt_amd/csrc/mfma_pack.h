@@ -105,26 +105,22 @@ struct OutPackD {
 
 // element (item, group g, lane, j) = qvgIn[delta][(4g + j) * 4 + lane / 16][t * 16 + lane % 16]
 template <int IN, int OUT>
-__global__ void k_pack_proj(const float* __restrict__ qvgIn, float* __restrict__ pp) {
+__device__ __forceinline__ float proj_elem(const float* __restrict__ qvgIn, size_t q) {
     using P = ProjPack<IN, OUT>;
-    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= P::PACKED) return;
     const int j = (int)(q & 3), lane = (int)((q >> 2) & 63);
     const size_t r = q >> 8;
     const int g = (int)(r % P::KS4), it = (int)(r / P::KS4);
     const int d = it / P::T, t = it - d * P::T;
     const int k = (4 * g + j) * 4 + lane / 16, c = t * kMT + lane % 16;
-    pp[q] = k < IN ? qvgIn[((size_t)d * IN + k) * P::NC + c] : 0.f;
+    return k < IN ? qvgIn[((size_t)d * IN + k) * P::NC + c] : 0.f;
 }
 
 // element (item (nt, ks), group g, lane, j) = B[k][nt * 16 + lane % 16] with
 // k = (ks * SPER + 4g + j) * 4 + lane / 16; zero past the part or past K
 template <int IN, int OUT>
-__global__ void k_pack_out(const float* __restrict__ goW, const float* __restrict__ ip,
-                           float* __restrict__ po) {
+__device__ __forceinline__ float out_elem(const float* __restrict__ goW,
+                                          const float* __restrict__ ip, size_t q) {
     using O = OutPack<IN, OUT>;
-    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= O::PACKED) return;
     const int j = (int)(q & 3), lane = (int)((q >> 2) & 63);
     const size_t r = q >> 8;
     const int g = (int)(r % O::SP4), it = (int)(r / O::SP4);
@@ -134,17 +130,15 @@ __global__ void k_pack_out(const float* __restrict__ goW, const float* __restric
     float v = 0.f;
     if (step < O::SPER && s < O::STEPS)
         v = k < O::KQ ? goW[(size_t)k * OUT + c] : ip[(size_t)(k - O::KQ) * OUT + c];
-    po[q] = v;
+    return v;
 }
 
 // element ((nt, part), group g, lane, j): local row kl = (4g + j) * 4 + lane / 16,
 // column c = nt * 16 + lane % 16; goW[part * OUT + kl][c] or input_proj[kl][c]
 template <int IN, int OUT>
-__global__ void k_pack_out_d(const float* __restrict__ goW, const float* __restrict__ ip,
-                             float* __restrict__ po) {
+__device__ __forceinline__ float out_d_elem(const float* __restrict__ goW,
+                                            const float* __restrict__ ip, size_t q) {
     using O = OutPackD<IN, OUT>;
-    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= O::PACKED) return;
     const int j = (int)(q & 3), lane = (int)((q >> 2) & 63);
     const size_t r = q >> 8;
     const int g = (int)(r % O::SD4), it = (int)(r / O::SD4);
@@ -153,7 +147,7 @@ __global__ void k_pack_out_d(const float* __restrict__ goW, const float* __restr
     float v = 0.f;
     if (part < 9) v = goW[((size_t)part * OUT + kl) * OUT + c];
     else if (kl < IN) v = ip[(size_t)kl * OUT + c];
-    po[q] = v;
+    return v;
 }
 
 // Packed copies of the four layers L4..L7.
@@ -162,72 +156,98 @@ struct PackedWeights {
     const float* po[4];
 };
 
-inline size_t packed_weight_floats() {
-    return ProjPack<SSLA_C1, SSLA_C2>::PACKED + ProjPack<SSLA_C2, SSLA_C2>::PACKED +
-           ProjPack<SSLA_C2, SSLA_C3>::PACKED + ProjPack<SSLA_C3, SSLA_C3>::PACKED +
-           OutPack<SSLA_C1, SSLA_C2>::PACKED + OutPack<SSLA_C2, SSLA_C2>::PACKED +
-           OutPack<SSLA_C2, SSLA_C3>::PACKED + OutPack<SSLA_C3, SSLA_C3>::PACKED;
+// Source weights of the four layers, by value for the packing kernel.
+struct PackSrc {
+    const float* qvgIn[4];
+    const float* goW[4];
+    const float* ip[4];
+};
+
+// Floats of one layer's projection copy and contraction copy.
+template <int IN, int OUT, bool D>
+struct LayerPack {
+    static constexpr size_t NP = ProjPack<IN, OUT>::PACKED;
+    static constexpr size_t NO = D ? OutPackD<IN, OUT>::PACKED : OutPack<IN, OUT>::PACKED;
+};
+
+// Buffer order: L4 projection, L4 contraction, L5 ..., L7 contraction.
+// D selects the contraction split at delta boundaries (whole-ring drain)
+// instead of the K split of the batch kernels.
+template <bool D>
+struct PackLayout {
+    using A = LayerPack<SSLA_C1, SSLA_C2, D>;
+    using B = LayerPack<SSLA_C2, SSLA_C2, D>;
+    using C = LayerPack<SSLA_C2, SSLA_C3, D>;
+    using E = LayerPack<SSLA_C3, SSLA_C3, D>;
+    static constexpr size_t off[9] = {0,
+                                      A::NP, A::NP + A::NO,
+                                      A::NP + A::NO + B::NP, A::NP + A::NO + B::NP + B::NO,
+                                      A::NP + A::NO + B::NP + B::NO + C::NP,
+                                      A::NP + A::NO + B::NP + B::NO + C::NP + C::NO,
+                                      A::NP + A::NO + B::NP + B::NO + C::NP + C::NO + E::NP,
+                                      A::NP + A::NO + B::NP + B::NO + C::NP + C::NO + E::NP +
+                                          E::NO};
+};
+
+template <int IN, int OUT, bool D>
+__device__ __forceinline__ float out_any(const float* goW, const float* ip, size_t q) {
+    if constexpr (D) return out_d_elem<IN, OUT>(goW, ip, q);
+    else return out_elem<IN, OUT>(goW, ip, q);
 }
 
-template <int IN, int OUT>
-inline float* pack_layer(const LayerWeightsS2S3& L, float* dst, const float** pp, const float** po,
-                         hipStream_t st) {
+// All eight copies in one launch, one thread per packed float.
+template <bool D>
+__global__ void k_pack_all(PackSrc s, float* __restrict__ buf) {
+    using L = PackLayout<D>;
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= L::off[8]) return;
+    float v;
+    if (q < L::off[1]) v = proj_elem<SSLA_C1, SSLA_C2>(s.qvgIn[0], q);
+    else if (q < L::off[2]) v = out_any<SSLA_C1, SSLA_C2, D>(s.goW[0], s.ip[0], q - L::off[1]);
+    else if (q < L::off[3]) v = proj_elem<SSLA_C2, SSLA_C2>(s.qvgIn[1], q - L::off[2]);
+    else if (q < L::off[4]) v = out_any<SSLA_C2, SSLA_C2, D>(s.goW[1], s.ip[1], q - L::off[3]);
+    else if (q < L::off[5]) v = proj_elem<SSLA_C2, SSLA_C3>(s.qvgIn[2], q - L::off[4]);
+    else if (q < L::off[6]) v = out_any<SSLA_C2, SSLA_C3, D>(s.goW[2], s.ip[2], q - L::off[5]);
+    else if (q < L::off[7]) v = proj_elem<SSLA_C3, SSLA_C3>(s.qvgIn[3], q - L::off[6]);
+    else v = out_any<SSLA_C3, SSLA_C3, D>(s.goW[3], s.ip[3], q - L::off[7]);
+    buf[q] = v;
+}
+
+template <bool D>
+inline size_t packed_floats() { return PackLayout<D>::off[8]; }
+
+inline size_t packed_weight_floats() { return packed_floats<false>(); }
+inline size_t packed_weight_floats_d() { return packed_floats<true>(); }
+
+template <bool D>
+inline hipError_t pack_all(const LayerWeightsS2S3* L, float* buf, PackedWeights* out,
+                           hipStream_t st) {
+    using PL = PackLayout<D>;
+    PackSrc s{};
+    for (int i = 0; i < 4; ++i) {
+        s.qvgIn[i] = L[i].qvgIn;
+        s.goW[i] = L[i].goW;
+        s.ip[i] = L[i].input_proj;
+        out->pp[i] = buf + PL::off[2 * i];
+        out->po[i] = buf + PL::off[2 * i + 1];
+    }
     constexpr int TB = 256;
-    const size_t np = ProjPack<IN, OUT>::PACKED, no = OutPack<IN, OUT>::PACKED;
-    hipLaunchKernelGGL((k_pack_proj<IN, OUT>), dim3((unsigned)((np + TB - 1) / TB)), dim3(TB), 0,
-                       st, L.qvgIn, dst);
-    *pp = dst;
-    dst += np;
-    hipLaunchKernelGGL((k_pack_out<IN, OUT>), dim3((unsigned)((no + TB - 1) / TB)), dim3(TB), 0,
-                       st, L.goW, L.input_proj, dst);
-    *po = dst;
-    return dst + no;
+    hipLaunchKernelGGL((k_pack_all<D>), dim3((unsigned)((PL::off[8] + TB - 1) / TB)), dim3(TB), 0,
+                       st, s, buf);
+    return hipGetLastError();
 }
 
-// Copies for the whole-ring drain: projection as above, contraction split
-// at delta boundaries.
-inline size_t packed_weight_floats_d() {
-    return ProjPack<SSLA_C1, SSLA_C2>::PACKED + ProjPack<SSLA_C2, SSLA_C2>::PACKED +
-           ProjPack<SSLA_C2, SSLA_C3>::PACKED + ProjPack<SSLA_C3, SSLA_C3>::PACKED +
-           OutPackD<SSLA_C1, SSLA_C2>::PACKED + OutPackD<SSLA_C2, SSLA_C2>::PACKED +
-           OutPackD<SSLA_C2, SSLA_C3>::PACKED + OutPackD<SSLA_C3, SSLA_C3>::PACKED;
-}
-
-template <int IN, int OUT>
-inline float* pack_layer_d(const LayerWeightsS2S3& L, float* dst, const float** pp,
-                           const float** po, hipStream_t st) {
-    constexpr int TB = 256;
-    const size_t np = ProjPack<IN, OUT>::PACKED, no = OutPackD<IN, OUT>::PACKED;
-    hipLaunchKernelGGL((k_pack_proj<IN, OUT>), dim3((unsigned)((np + TB - 1) / TB)), dim3(TB), 0,
-                       st, L.qvgIn, dst);
-    *pp = dst;
-    dst += np;
-    hipLaunchKernelGGL((k_pack_out_d<IN, OUT>), dim3((unsigned)((no + TB - 1) / TB)), dim3(TB),
-                       0, st, L.goW, L.input_proj, dst);
-    *po = dst;
-    return dst + no;
-}
-
+// Fills `out` from layers L[0..3] (L4..L7) into buf (packed_weight_floats_d()
+// floats), on stream st; returns the launch status.
 inline hipError_t pack_weights_d(const LayerWeightsS2S3* L, float* buf, PackedWeights* out,
                                  hipStream_t st) {
-    float* p = buf;
-    p = pack_layer_d<SSLA_C1, SSLA_C2>(L[0], p, &out->pp[0], &out->po[0], st);
-    p = pack_layer_d<SSLA_C2, SSLA_C2>(L[1], p, &out->pp[1], &out->po[1], st);
-    p = pack_layer_d<SSLA_C2, SSLA_C3>(L[2], p, &out->pp[2], &out->po[2], st);
-    p = pack_layer_d<SSLA_C3, SSLA_C3>(L[3], p, &out->pp[3], &out->po[3], st);
-    return hipGetLastError();
+    return pack_all<true>(L, buf, out, st);
 }
 
-// Fills `out` from layers L[0..3] (L4..L7) into buf (packed_weight_floats()
-// floats), on stream st; returns the launch status.
+// Same for the batch kernels (packed_weight_floats() floats).
 inline hipError_t pack_weights(const LayerWeightsS2S3* L, float* buf, PackedWeights* out,
                                hipStream_t st) {
-    float* p = buf;
-    p = pack_layer<SSLA_C1, SSLA_C2>(L[0], p, &out->pp[0], &out->po[0], st);
-    p = pack_layer<SSLA_C2, SSLA_C2>(L[1], p, &out->pp[1], &out->po[1], st);
-    p = pack_layer<SSLA_C2, SSLA_C3>(L[2], p, &out->pp[2], &out->po[2], st);
-    p = pack_layer<SSLA_C3, SSLA_C3>(L[3], p, &out->pp[3], &out->po[3], st);
-    return hipGetLastError();
+    return pack_all<false>(L, buf, out, st);
 }
 
 }  // namespace ssla
