@@ -70,40 +70,39 @@ def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20, chunk=64):
     S2, S2p, S3p, S3pp = n2.sum(), n2[m2].sum(), n3[m2].sum(), n3[m3].sum()
     N, N2, N3 = x.size, int(m2.sum()), int(m3.sum())
     F = 4.0
+    # projections compute v, g for every pair entering the layer; the
+    # contraction computes q for the pairs of its output records, then
+    # q*h through goW, and the residual (input_proj where IN != OUT)
     mac = {
-        "L4.proj": S2 * C1 * 3 * C2,
-        "L4.out": S2 * C2 * C2 + N * C1 * C2,
-        "L5.proj_vg": S2 * C2 * 2 * C2,
-        "L5.proj_q": S2p * C2 * C2,
-        "L5.out": S2p * C2 * C2,
-        "L6.proj": S3p * C2 * 3 * C3,
-        "L6.out": S3p * C3 * C3 + N2 * C2 * C3,
-        "L7.proj_vg": S3p * C3 * 2 * C3,
-        "L7.proj_q": S3pp * C3 * C3,
-        "L7.out": S3pp * C3 * C3,
+        "L4.proj": S2 * C1 * 2 * C2,
+        "L4.out": S2 * C1 * C2 + S2 * C2 * C2 + N * C1 * C2,
+        "L5.proj": S2 * C2 * 2 * C2,
+        "L5.out": S2p * C2 * C2 + S2p * C2 * C2,
+        "L6.proj": S3p * C2 * 2 * C3,
+        "L6.out": S3p * C2 * C3 + S3p * C3 * C3 + N2 * C2 * C3,
+        "L7.proj": S3p * C3 * 2 * C3,
+        "L7.out": S3pp * C3 * C3 + S3pp * C3 * C3,
         "head": int((m3 & (owner == 1)).sum()) * (2 * C3 * C3 + 7 * C3),
     }
     flops = {k: 2.0 * v for k, v in mac.items()}
     byts = {
-        "L4.proj": F * (N * C1 + S2 * 3 * C2),
+        "L4.proj": F * (N * C1 + S2 * 2 * C2),
         "L4.out": F * (S2 * C2 + N * C1 + N * C2),
-        "L5.proj_vg": F * (N * C2 + S2 * 2 * C2),
-        "L5.proj_q": F * (N2 * C2 + S2p * C2),
+        "L5.proj": F * (N * C2 + S2 * 2 * C2),
         "L5.out": F * (S2p * C2 + 2 * N2 * C2),
-        "L6.proj": F * (N2 * C2 + S3p * 3 * C3),
+        "L6.proj": F * (N2 * C2 + S3p * 2 * C3),
         "L6.out": F * (S3p * C3 + N2 * C2 + N2 * C3),
-        "L7.proj_vg": F * (N2 * C3 + S3p * 2 * C3),
-        "L7.proj_q": F * (N3 * C3 + S3pp * C3),
+        "L7.proj": F * (N2 * C3 + S3p * 2 * C3),
         "L7.out": F * (S3pp * C3 + 2 * N3 * C3),
     }
     # scan passes: summary reads v, g; carry touches each chunk's map and
-    # start state; apply reads v, g (and q where consumed) and writes q*h there
+    # start state; apply reads v, g and writes h where consumed
     for L, pairs, need, out in (("L4", S2, S2, C2), ("L5", S2, S2p, C2),
                                 ("L6", S3p, S3p, C3), ("L7", S3p, S3pp, C3)):
         chunks = pairs / chunk
         byts[f"{L}.sum"] = F * (pairs * 2 * out + chunks * 2 * out)
         byts[f"{L}.carry"] = F * chunks * 3 * out
-        byts[f"{L}.apply"] = F * (pairs * 2 * out + 2 * need * out + chunks * out)
+        byts[f"{L}.apply"] = F * (pairs * 2 * out + need * out + chunks * out)
         flops[f"{L}.sum"] = 4.0 * pairs * out
         flops[f"{L}.carry"] = 2.0 * chunks * out
         flops[f"{L}.apply"] = 4.0 * pairs * out
@@ -293,8 +292,7 @@ def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20, gpu_out=None):
 # kernel of each timed launch of the whole-ring drain (ssla-rt_amd/csrc/drain_scan.hip)
 PHASE_KERNEL = {"order": "ordering kernels", "head": "k_head + k_pred_*", "emit": "k_emit"}
 for _L, (_i, _o) in zip(("L4", "L5", "L6", "L7"), ((C1, C2), (C2, C2), (C2, C3), (C3, C3))):
-    for _ph in ("proj", "proj_vg", "proj_q"):
-        PHASE_KERNEL[f"{_L}.{_ph}"] = f"k_qvg<{_i}, {_o}>"
+    PHASE_KERNEL[f"{_L}.proj"] = f"k_qvg<{_i}, {_o}>"
     PHASE_KERNEL[f"{_L}.sum"] = f"k_scan_summary<{_o}>"
     PHASE_KERNEL[f"{_L}.carry"] = f"k_scan_carry<{_o}>"
     PHASE_KERNEL[f"{_L}.apply"] = f"k_scan_apply<{_o}>"

@@ -147,15 +147,12 @@ int ssla_hip_drain_n2(const HybridS2S3Config* cfg,
                       int n0, int n1,
                       HybridS2S3OutputSlot* out0, HybridS2S3OutputSlot* out1);
 
-#define SSLA_DRAIN_PHASES 25
+#define SSLA_DRAIN_PHASES 23
 /* Phase order of SslaHipDrainOpts.phase_ms (one kernel launch each, except
- * 0, 23): 0 ordering (decode, sorts, tdrop decisions, chunk tables);
- * L4: 1 projection, 2 scan summary, 3 scan carry, 4 scan apply,
- * 5 contraction + LayerNorm; L5: 6 projection of v, g, 7 projection of q
- * (pass-2 records), 8-10 scan, 11 contraction; L6: 12 projection, 13-15
- * scan, 16 contraction; L7: 17 projection of v, g, 18 projection of q
- * (pass-3 records), 19-21 scan, 22 contraction; 23 head and prediction
- * grid, 24 output slots. */
+ * 0, 21): 0 ordering (decode, sorts, tdrop decisions, chunk tables); per
+ * layer a projection of v, g, the scan summary, carry and apply, then the
+ * contraction (q, q*h, goW, residual, LayerNorm): L4 1-5, L5 6-10, L6
+ * 11-15, L7 16-20; 21 head and prediction grid, 22 output slots. */
 
 #define SSLA_BATCH_PHASES 32
 /* Slots of the in-kernel batch profile (batch-mode and live drains), summed

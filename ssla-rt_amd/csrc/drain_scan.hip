@@ -15,13 +15,14 @@
 // Only the h_c recurrence is ordered, and only among events touching the
 // same cell.  Per layer the drain therefore runs three phases over all
 // records of all rings:
-//   P  (k_qvg)   q, v, g for every (record, delta) pair as MFMA tiles,
+//   P  (k_qvg)   v, g for every (record, delta) pair as MFMA tiles,
 //                written in per-cell ring order (pair rows sorted by
-//                target cell); q only where the layer's output is used
-//   S  (k_scan)  chunked per-cell scan: turns (q, v, g) rows into q*h rows
-//                in place, in ring order
-//   O  (k_out)   per record: the <= 9 q*h rows contracted with goW by
-//                MFMA, residual, fp64 LayerNorm
+//                target cell)
+//   S  (k_scan)  chunked per-cell scan: turns (v, g) rows into h rows in
+//                place, in ring order, where the layer's output is used
+//   O  (k_out)   per output record: q = qvgIn[delta] x by MFMA, times the
+//                <= 9 h rows, contracted with goW by MFMA, residual, fp64
+//                LayerNorm
 // The temporal-dropout decisions (ssla_ref.py:190-195) depend only on the
 // per-cell arrival rank of a record, so they come from a stable sort of
 // records by cell: pass = ((counter + rank) mod 256) % window == 0.
@@ -215,14 +216,15 @@ __global__ void k_pair_pos(int n, const uint32_t* __restrict__ keys,
 }
 
 // ---------------------------------------------------------------------------
-// P: q, v, g rows as 16 x 16 MFMA tiles (v_mfma_f32_16x16x4_f32, operand
-// layout in mfma_pack.h).  One workgroup = 64 records (rows, staged in LDS)
-// x all 9 deltas x the column tiles [tlo, thi) of [q | v | g]; each wave
-// owns (delta, column tile) items, loads an item's weights (fragment order,
-// one float4 per four k-steps) while the previous item's four row tiles run,
-// and writes each row to the pair's sorted position.  (Staging whole rows in
-// LDS for 16-byte stores measured slower: the extra barriers cost more than
-// the partial-line writes.)
+// P: v, g rows as 16 x 16 MFMA tiles (v_mfma_f32_16x16x4_f32, operand layout
+// in mfma_pack.h).  One workgroup = 64 records (rows, staged in LDS) x all 9
+// deltas x the v and g column tiles of qvgIn; each wave owns (delta, column
+// tile) items, loads an item's weights (fragment order, one float4 per four
+// k-steps) while the previous item's four row tiles run, and writes each
+// [v | g] row (2 * OUT floats) to the pair's sorted position.  q is not
+// stored: the contraction recomputes it from the record's input.  (Staging
+// whole rows in LDS for 16-byte stores measured slower: the extra barriers
+// cost more than the partial-line writes.)
 // ---------------------------------------------------------------------------
 constexpr int kTM = 64;     // records per projection / contraction workgroup
 
@@ -241,9 +243,10 @@ template <int IN, int OUT>
 __global__ void __launch_bounds__(256)
 k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
       const float* __restrict__ X, const int* __restrict__ pos, const float* __restrict__ pp,
-      float* __restrict__ QVG, int tlo, int thi) {
+      float* __restrict__ QVG) {
     using P = ProjPack<IN, OUT>;
-    constexpr int NC = P::NC, XST = lds_stride(IN);
+    constexpr int XST = lds_stride(IN), NCW = 2 * OUT;
+    constexpr int tlo = P::TQ, thi = P::T;      // the v and g column tiles
     __shared__ __align__(16) float xs[kTM * XST];
     __shared__ int prow[kPatch][kTM];
     const int n = n_dev ? *n_dev : n_max;
@@ -285,7 +288,7 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
             #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int pr = prow[d][m * kMT + 4 * lk + r];
-                if (pr >= 0) gstore(QVG + (size_t)pr * NC + col, acc[r]);
+                if (pr >= 0) gstore(QVG + (size_t)pr * NCW + (col - OUT), acc[r]);
             }
         }
     };
@@ -312,8 +315,8 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 //   B (k_scan_carry)   per cell: walks its chunks in order, records each
 //                      chunk's start state, stores the final state
 //   C (k_scan_apply)   per chunk: replays the chunk from its start state and
-//                      replaces q by q*h in place for pairs whose record
-//                      needs this layer's output
+//                      replaces v by h in place for pairs whose record needs
+//                      this layer's output
 // One lane per channel in all three passes.
 // ---------------------------------------------------------------------------
 constexpr int kCH = 64;
@@ -358,12 +361,12 @@ __global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
 k_scan_summary(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
                const int* __restrict__ cend, const float* __restrict__ QVG,
                float* __restrict__ Asum, float* __restrict__ Bsum) {
-    constexpr int NC = 3 * OUT;
+    constexpr int NC = 2 * OUT;
     const int j = blockIdx.x;
     const int c = threadIdx.x;
     if (j >= *n_chunks || c >= OUT) return;
     const int s = cbeg[j], e = cend[j];
-    const float* row = QVG + (size_t)s * NC + OUT + c;     // v at +0, g at +OUT
+    const float* row = QVG + (size_t)s * NC + c;           // v at +0, g at +OUT
     float A = 1.f, B = 0.f;
     constexpr int U = 16;        // pairs whose v, g are in flight together
     for (int p0 = s; p0 < e; p0 += U, row += U * NC) {
@@ -426,61 +429,67 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
              const int* __restrict__ cend, const float* __restrict__ Hs,
              const int* __restrict__ pair_rec, const unsigned char* __restrict__ need,
              float* __restrict__ QVG) {
-    constexpr int NC = 3 * OUT;
+    constexpr int NC = 2 * OUT;
     const int j = blockIdx.x;
     const int c = threadIdx.x;
     if (j >= *n_chunks || c >= OUT) return;
     const int s = cbeg[j], e = cend[j];
     float h = Hs[(size_t)j * OUT + c];
     float* row = QVG + (size_t)s * NC + c;
-    constexpr int U = 8;         // pairs whose q, v, g are in flight together
+    constexpr int U = 8;         // pairs whose v, g are in flight together
     for (int p0 = s; p0 < e; p0 += U, row += U * NC) {
-        float q[U], v[U], g[U];
+        float v[U], g[U];
         bool use[U];
         #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int k = p0 + u < e ? u : 0;
             use[u] = p0 + u < e && (!need || need[pair_rec[p0 + k]]);
-            q[u] = use[u] ? gload(row + (size_t)k * NC) : 0.f;
-            v[u] = gload(row + (size_t)k * NC + OUT);
-            g[u] = gload(row + (size_t)k * NC + 2 * OUT);
+            v[u] = gload(row + (size_t)k * NC);
+            g[u] = gload(row + (size_t)k * NC + OUT);
         }
         #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (p0 + u < e) {
                 h = fmaf(sigmoid_fast(g[u]), h, v[u]);
-                if (use[u]) gstore(row + (size_t)u * NC, q[u] * h);
+                if (use[u]) gstore(row + (size_t)u * NC, h);
             }
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// O: per record y = sum_delta goW[delta]^T qh + residual, fp64 LayerNorm.
-// One workgroup = 64 records, one wave per 16-column output tile (OUT / 16
-// waves).  The contraction over K = 9*OUT (+ IN) runs in parts at delta
-// boundaries: each part's rows (the records' q*h rows at that delta, zeros
-// where out of bounds; or their inputs for input_proj) are fetched into
-// registers while the previous part's MFMAs run, then written to the other
-// of two LDS buffers; each wave accumulates its column tile for all four
-// row tiles.
+// O: per record y = sum_delta goW[delta]^T (q_delta * h_delta) + residual,
+// fp64 LayerNorm.  One workgroup = 64 records, one wave per 16-column output
+// tile (OUT / 16 waves); the records' inputs stay in LDS.  The contraction
+// over K = 9*OUT (+ IN) runs in parts at delta boundaries.  A part's rows
+// (the records' h rows at that delta, zeros where out of bounds; or their
+// inputs for input_proj) are fetched into registers while the previous
+// part's MFMAs run and written to the other of two LDS buffers.  Each wave
+// then computes its 16 columns of q = qvgIn[delta]^T x for the 64 records
+// (MFMA, weights from the projection copy) and multiplies them into the
+// buffer; after a barrier every wave accumulates its column tile over the
+// part's q*h rows, all four row tiles.
 // ---------------------------------------------------------------------------
 template <int IN, int OUT>
 __global__ void __launch_bounds__(OUT / kMT * 64)
 k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
       const float* __restrict__ X, const int* __restrict__ pos,
-      const float* __restrict__ QVG, const float* __restrict__ po,
+      const float* __restrict__ HR, const float* __restrict__ pp, const float* __restrict__ po,
       const float* __restrict__ gamma, const float* __restrict__ beta, float* __restrict__ Y) {
     using O = OutPackD<IN, OUT>;
+    using P = ProjPack<IN, OUT>;
+    static_assert(P::TQ == O::NT, "one q column tile per wave");
     // one wave per 16-column tile of the output
-    constexpr int NTH = O::NT * 64, NC = 3 * OUT, QST = lds_stride(OUT);
-    constexpr int O4 = OUT / 4, I4 = IN / 4;
-    constexpr int PRE = (kTM * O4 + NTH - 1) / NTH;   // float4 per thread per part
+    constexpr int NTH = O::NT * 64, NC = 2 * OUT, QST = lds_stride(OUT), XST = lds_stride(IN);
+    constexpr int I4 = IN / 4, YST = OUT + 1;
+    constexpr int XY = kTM * (XST > YST ? XST : YST);
     __shared__ __align__(16) float qs[2][kTM * QST];
-    __shared__ float ys[kTM][OUT + 1];
+    // the records' inputs while the parts run, then the pre-LayerNorm sums
+    __shared__ __align__(16) float xy[XY];
     __shared__ double stat[kTM][2];
     __shared__ int rows[kTM];
     __shared__ int prow[kPatch][kTM];
+    float* const xs = xy;
     const int n = n_dev ? *n_dev : n_max;
     const int base = blockIdx.x * kTM;
     if (base >= n) return;
@@ -493,43 +502,63 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
         const int g = rows[r];
         prow[d][r] = g >= 0 ? pos[(size_t)g * kPatch + d] : -1;
     }
+    for (int t = tid; t < kTM * I4; t += NTH) {
+        const int r = t / I4, q = t - r * I4;
+        const int g = rows[r];
+        const float4 v = g >= 0 ? reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        lds_put4(&xs[r * XST + 4 * q], v);
+    }
     __syncthreads();
     const int lane = tid & 63, wv = tid >> 6, li = lane & 15, lk = lane >> 4;
     const int mtiles = (cnt + kMT - 1) / kMT;
     f32x4 acc[4];
     #pragma unroll
     for (int m = 0; m < 4; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // a part's rows: the records' q*h rows at that delta (zeros out of
-    // bounds), or their inputs for input_proj; fetched into registers while
-    // the previous part computes, then written to the other LDS buffer
-    float4 pre[PRE];
+    // Each wave fetches, stores and scales its own 16 columns of a part's 64
+    // rows (4 float4 per lane), so the q product needs no barrier before it;
+    // one barrier per part then publishes all columns to the contraction.
+    float4 pre[4];
     auto fetch = [&](int part) {
         #pragma unroll
-        for (int u = 0; u < PRE; ++u) {
-            const int t = tid + u * NTH;
+        for (int u = 0; u < 4; ++u) {
+            const int idx = lane + 64 * u, r = idx >> 2, q = wv * 4 + (idx & 3);
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (t < kTM * O4) {
-                const int r = t / O4, q = t - r * O4;
-                if (part < kPatch) {
-                    const int pr = prow[part][r];
-                    if (pr >= 0) v = reinterpret_cast<const float4*>(QVG + (size_t)pr * NC)[q];
-                } else {
-                    const int g = rows[r];
-                    if (g >= 0 && q < I4) v = reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q];
-                }
+            if (part < kPatch) {
+                const int pr = prow[part][r];
+                if (pr >= 0) v = reinterpret_cast<const float4*>(HR + (size_t)pr * NC)[q];
+            } else {
+                const int g = rows[r];
+                if (g >= 0 && q < I4) v = reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q];
             }
             pre[u] = v;
         }
     };
     auto put = [&](float* buf) {
         #pragma unroll
-        for (int u = 0; u < PRE; ++u) {
-            const int t = tid + u * NTH;
-            if (t < kTM * O4) {
-                const int r = t / O4, q = t - r * O4;
-                lds_put4(&buf[r * QST + 4 * q], pre[u]);
-            }
+        for (int u = 0; u < 4; ++u) {
+            const int idx = lane + 64 * u, r = idx >> 2, q = wv * 4 + (idx & 3);
+            lds_put4(&buf[r * QST + 4 * q], pre[u]);
         }
+    };
+    // this wave's 16 columns of q for the 64 records (rows past cnt are
+    // zero), multiplied into its columns of the h rows in place
+    auto qmul = [&](float* buf, const float* qb) {
+        f32x4 q[4];
+        #pragma unroll
+        for (int m = 0; m < 4; ++m) q[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const float* a = &xs[li * XST + lk];
+        #pragma unroll
+        for (int s = 0; s < P::KS; ++s)
+            #pragma unroll
+            for (int m = 0; m < 4; ++m)
+                q[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m * kMT * XST + 4 * s], qb[s], q[m],
+                                                            0, 0, 0);
+        #pragma unroll
+        for (int m = 0; m < 4; ++m)
+            #pragma unroll
+            for (int r = 0; r < 4; ++r)
+                buf[(m * kMT + 4 * lk + r) * QST + wv * kMT + li] *= q[m][r];
     };
     // the four row tiles' accumulation chains interleaved step by step, so
     // consecutive MFMAs are independent (rows past cnt hold zeros)
@@ -542,10 +571,17 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
                 acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m * kMT * QST + 4 * s], b[s], acc[m],
                                                               0, 0, 0);
     };
+    // part k: put + q product into qs[k % 2], barrier, contraction; the next
+    // part's rows and weights load while the contraction runs.  A buffer is
+    // rewritten two parts later, after the barrier that every wave reaches
+    // only once its contraction over that buffer is done.
     float b0[O::SD], b1[O::SD];
+    float qb[P::KS4 * 4];
     fetch(0);
     O::load(po, wv, 0, lane, b0);
+    P::load(pp, wv, lane, qb);                       // item (delta 0, q tile wv)
     put(qs[0]);
+    qmul(qs[0], qb);
     __syncthreads();
     #pragma unroll 1
     for (int part = 0; part < O::PARTS; part += 2) {
@@ -553,43 +589,50 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
         if (part + 1 < O::PARTS) {
             fetch(part + 1);
             O::load(po, wv, part + 1, lane, b1);
+            if (part + 1 < kPatch) P::load(pp, (part + 1) * P::T + wv, lane, qb);
         }
         compute(qs[0], b0);
         if (part + 1 >= O::PARTS) break;
         put(qs[1]);
+        if (part + 1 < kPatch) qmul(qs[1], qb);
         __syncthreads();
         // odd part in qs[1] with b1
         if (part + 2 < O::PARTS) {
             fetch(part + 2);
             O::load(po, wv, part + 2, lane, b0);
+            if (part + 2 < kPatch) P::load(pp, (part + 2) * P::T + wv, lane, qb);
         }
         compute(qs[1], b1);
         if (part + 2 >= O::PARTS) break;
         put(qs[0]);
+        if (part + 2 < kPatch) qmul(qs[0], qb);
         __syncthreads();
     }
+    // every wave has passed the barrier after the last q product, so the
+    // inputs in xy are no longer read
+    auto ys = [&](int r, int o) -> float& { return xy[r * YST + o]; };
     #pragma unroll
     for (int m = 0; m < 4; ++m) {
         if (m >= mtiles) continue;
         #pragma unroll
-        for (int r = 0; r < 4; ++r) ys[m * kMT + 4 * lk + r][wv * kMT + li] = acc[m][r];
+        for (int r = 0; r < 4; ++r) ys(m * kMT + 4 * lk + r, wv * kMT + li) = acc[m][r];
     }
     __syncthreads();
     if (!O::IP) {
         for (int t = tid; t < cnt * OUT; t += NTH) {
             const int r = t / OUT, o = t - r * OUT;
-            ys[r][o] += X[(size_t)rows[r] * OUT + o];
+            ys(r, o) += X[(size_t)rows[r] * OUT + o];
         }
         __syncthreads();
     }
     if (tid < cnt) {
         const int r = tid;
         double s = 0.0;
-        for (int i = 0; i < OUT; ++i) s += (double)ys[r][i];
+        for (int i = 0; i < OUT; ++i) s += (double)ys(r, i);
         const double mean = s / (double)OUT;
         double var = 0.0;
         for (int i = 0; i < OUT; ++i) {
-            const double dd = (double)ys[r][i] - mean;
+            const double dd = (double)ys(r, i) - mean;
             var += dd * dd;
         }
         var /= (double)OUT;
@@ -599,7 +642,7 @@ k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
     __syncthreads();
     for (int t = tid; t < cnt * OUT; t += NTH) {
         const int r = t / OUT, o = t - r * OUT;
-        const double v = ((double)ys[r][o] - stat[r][0]) * stat[r][1];
+        const double v = ((double)ys(r, o) - stat[r][0]) * stat[r][1];
         Y[(size_t)rows[r] * OUT + o] = (float)(v * (double)gamma[o] + (double)beta[o]);
     }
 }
@@ -1145,12 +1188,10 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     MARK();
     const LayerWeightsS2S3* L = cfg->layers[0];
     const unsigned tilesE = grid1(E, kTM);
-    constexpr int T2 = ProjPack<SSLA_C2, SSLA_C2>::T, Q2 = ProjPack<SSLA_C2, SSLA_C2>::TQ;
-    constexpr int T3 = ProjPack<SSLA_C3, SSLA_C3>::T, Q3 = ProjPack<SSLA_C3, SSLA_C3>::TQ;
+    const unsigned char* all = nullptr;             // every pair's record needs h
     // ---- L4: 24 -> 48, all records ----------------------------------------
     hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
-                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, pk.pp[0], w.QVG,
-                       0, ProjPack<SSLA_C1, SSLA_C2>::T);
+                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, pk.pp[0], w.QVG);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
@@ -1159,20 +1200,15 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        w.coff2, w.ccnt2, w.bd, 0, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
-                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, (const unsigned char*)nullptr, w.QVG);
+                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, all, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_out<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(SSLA_C2 / kMT * 64), 0, st, E,
-                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, pk.po[0],
-                       L[0].ln_gamma, L[0].ln_beta, w.X1);
+                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, pk.pp[0],
+                       pk.po[0], L[0].ln_gamma, L[0].ln_beta, w.X1);
     MARK();
     // ---- L5: 48 -> 48, state for all records, output for pass2 ---------------
-    // v, g for every record; q only for pass2 records (the consumed ones)
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
-                       (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, pk.pp[1], w.QVG,
-                       Q2, T2);
-    MARK();
-    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, pk.pp[1], w.QVG, 0, Q2);
+                       (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, pk.pp[1], w.QVG);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
@@ -1184,13 +1220,12 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, w.pass2, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(SSLA_C2 / kMT * 64), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, pk.po[1],
-                       L[1].ln_gamma, L[1].ln_beta, w.X2);
+                       (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, pk.pp[1],
+                       pk.po[1], L[1].ln_gamma, L[1].ln_beta, w.X2);
     MARK();
     // ---- L6: 48 -> 96, pass2 records ------------------------------------------
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, pk.pp[2], w.QVG,
-                       0, ProjPack<SSLA_C2, SSLA_C3>::T);
+                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, pk.pp[2], w.QVG);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
@@ -1199,18 +1234,15 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        w.coff3, w.ccnt3, w.bd, 2, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
-                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, (const unsigned char*)nullptr, w.QVG);
+                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, all, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(SSLA_C3 / kMT * 64), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, pk.po[2],
-                       L[2].ln_gamma, L[2].ln_beta, w.X3);
+                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, pk.pp[2],
+                       pk.po[2], L[2].ln_gamma, L[2].ln_beta, w.X3);
     MARK();
     // ---- L7: 96 -> 96, state for pass2, output for pass3 ----------------------
     hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, pk.pp[3], w.QVG, Q3, T3);
-    MARK();
-    hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
-                       (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, pk.pp[3], w.QVG, 0, Q3);
+                       (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, pk.pp[3], w.QVG);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
@@ -1222,8 +1254,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, w.pass3, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_out<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(SSLA_C3 / kMT * 64), 0, st, E,
-                       (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, pk.po[3],
-                       L[3].ln_gamma, L[3].ln_beta, w.X4);
+                       (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, pk.pp[3],
+                       pk.po[3], L[3].ln_gamma, L[3].ln_beta, w.X4);
     MARK();
     HIPCHK(hipGetLastError());
     // ---- head ------------------------------------------------------------------

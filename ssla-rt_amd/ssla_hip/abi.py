@@ -125,9 +125,9 @@ OEVA_VERSION = 1
 
 DRAIN_PHASES = ("order",
                 "L4.proj", "L4.sum", "L4.carry", "L4.apply", "L4.out",
-                "L5.proj_vg", "L5.proj_q", "L5.sum", "L5.carry", "L5.apply", "L5.out",
+                "L5.proj", "L5.sum", "L5.carry", "L5.apply", "L5.out",
                 "L6.proj", "L6.sum", "L6.carry", "L6.apply", "L6.out",
-                "L7.proj_vg", "L7.proj_q", "L7.sum", "L7.carry", "L7.apply", "L7.out",
+                "L7.proj", "L7.sum", "L7.carry", "L7.apply", "L7.out",
                 "head", "emit")
 
 # in-kernel profile of the batch-mode and live drains (SSLA_BATCH_PHASES);
