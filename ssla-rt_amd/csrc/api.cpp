@@ -471,14 +471,26 @@ int ssla_hip_config_bind(const SslaHipModel* m, int n_blocks, HybridS2S3Config* 
 int ssla_hip_state_alloc(HybridS2S3Config* cfg, int blk) {
     if (!cfg || blk < 0 || blk >= SSLA_MAX_BLOCKS) { set_error("bad block"); return SSLA_ERR_ARG; }
     if (cfg->H2 <= 0 || cfg->W2 <= 0) { set_error("config has no grid"); return SSLA_ERR_STATE; }
+    {
+        std::lock_guard<std::mutex> lk(g_alloc_mu);
+        if (cfg->hidden[blk][0] && g_state_bases.count(cfg->hidden[blk][0])) {
+            set_error("state of this block is already allocated (ssla_hip_state_free first)");
+            return SSLA_ERR_STATE;
+        }
+    }
     const size_t c2 = (size_t)cfg->H2 * cfg->W2, c3 = (size_t)cfg->H3 * cfg->W3;
     const size_t sz[6] = {c2 * 48 * 4, c2 * 48 * 4, c3 * 96 * 4, c3 * 96 * 4, c2, c3};
     size_t total = 0;
     for (size_t s : sz) total += (s + 255) & ~size_t(255);
     void* base = nullptr;
     API_HIP(hipMalloc(&base, total));
-    API_HIP(hipMemset(base, 0, total));
-    API_HIP(hipStreamSynchronize(nullptr));
+    hipError_t e = hipMemset(base, 0, total);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+        set_error(std::string("state_alloc: clearing the state: ") + hipGetErrorString(e));
+        (void)hipFree(base);
+        return SSLA_ERR_HIP;
+    }
     char* p = static_cast<char*>(base);
     void* parts[6];
     for (int i = 0; i < 6; ++i) {
@@ -541,6 +553,13 @@ int ssla_hip_preds_alloc(HybridS2S3Config* cfg, int blk) {
     const HybridStrip& s = cfg->strip[blk];
     const int w = s.s3_owned_hi - s.s3_owned_lo, h = s.s3_owned_y_hi - s.s3_owned_y_lo;
     if (w <= 0 || h <= 0) { set_error("block has an empty s3 owned box"); return SSLA_ERR_STATE; }
+    {
+        std::lock_guard<std::mutex> lk(g_alloc_mu);
+        if (cfg->preds[blk] && g_pred_bases.count(cfg->preds[blk])) {
+            set_error("predictions of this block are already allocated (ssla_hip_preds_free first)");
+            return SSLA_ERR_STATE;
+        }
+    }
     const size_t cells = (size_t)w * h;
     const size_t pb = (cells * 7 * 4 + 255) & ~size_t(255);
     void* base = nullptr;
@@ -609,10 +628,22 @@ int ssla_hip_timing_alloc(HybridS2S3Config* cfg, int blk, unsigned int capacity)
         set_error("all blocks share one timing capacity");
         return SSLA_ERR_ARG;
     }
+    {
+        std::lock_guard<std::mutex> lk(g_alloc_mu);
+        if (cfg->timing[blk] && g_state_bases.count(cfg->timing[blk])) {
+            set_error("timing of this block is already allocated (ssla_hip_timing_free first)");
+            return SSLA_ERR_STATE;
+        }
+    }
     void* t = nullptr;
     API_HIP(hipMalloc(&t, sizeof(GpuTimingSlot) * (size_t)capacity));
-    API_HIP(hipMemset(t, 0, sizeof(GpuTimingSlot) * (size_t)capacity));
-    API_HIP(hipStreamSynchronize(nullptr));
+    hipError_t e = hipMemset(t, 0, sizeof(GpuTimingSlot) * (size_t)capacity);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+        set_error(std::string("timing_alloc: clearing the ring: ") + hipGetErrorString(e));
+        (void)hipFree(t);
+        return SSLA_ERR_HIP;
+    }
     void* clk = nullptr;
     if (hipHostMalloc(&clk, 16, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess) {
         (void)hipFree(t);

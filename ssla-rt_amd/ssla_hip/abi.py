@@ -118,6 +118,9 @@ class SslaHipOevaDiff(ctypes.Structure):
                 ("max_abs_delta", ctypes.c_double), ("n_mismatched_cp", ctypes.c_size_t)]
 
 
+# return codes of the C ABI (include/ssla_hip.h)
+SSLA_OK, SSLA_ERR_ARG, SSLA_ERR_HIP, SSLA_ERR_IO, SSLA_ERR_FORMAT, SSLA_ERR_STATE = 0, -1, -2, -3, -4, -5
+
 PRED_BUSY = 0x80000000
 OEVA_MAGIC = 0x4F455641
 OEVA_VERSION = 1

@@ -56,3 +56,18 @@ def test_errors_do_not_cross_the_boundary():
     m = ctypes.c_void_p()
     assert L.ssla_hip_model_load(b"/nonexistent/dir", ctypes.byref(m)) < 0
     assert not m.value
+
+
+def test_constants_match_the_header():
+    """Return codes, phase counts and prediction constants of ssla_hip.h
+    against the Python mirror."""
+    import re
+    text = (ROOT / "include" / "ssla_hip.h").read_text()
+    defs = {}
+    for name, val in re.findall(r"#define\s+(SSLA_\w+)\s+\(?(-?(?:0x)?[0-9A-Fa-f]+)u?\)?", text):
+        defs[name] = int(val, 0)
+    for name in ("SSLA_OK", "SSLA_ERR_ARG", "SSLA_ERR_HIP", "SSLA_ERR_IO", "SSLA_ERR_FORMAT",
+                 "SSLA_ERR_STATE"):
+        assert defs[name] == getattr(abi, name), name
+    assert defs["SSLA_DRAIN_PHASES"] == len(abi.DRAIN_PHASES)
+    assert defs["SSLA_PRED_BUSY"] == abi.PRED_BUSY

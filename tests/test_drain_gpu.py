@@ -268,6 +268,24 @@ def test_state_carries_across_calls(H, stub_dir, stub_npz):
         compare(np.concatenate([a, b]), p2, p3, feat, "two calls")
 
 
+def test_second_alloc_of_a_block_is_refused(H, stub_dir):
+    """state / preds / timing buffers of a block are allocated once; a second
+    allocation without a free is an error (the first stays in place)."""
+    import ctypes
+    from ssla_hip import lib
+    L = lib.load()
+    say("double allocation refused")
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        d.alloc_timing(1024)
+        cfg = ctypes.byref(d.cfg)
+        before = (d.cfg.hidden[0][0], d.cfg.preds[0], d.cfg.timing[0])
+        assert L.ssla_hip_state_alloc(cfg, 0) == abi.SSLA_ERR_STATE
+        assert L.ssla_hip_preds_alloc(cfg, 0) == abi.SSLA_ERR_STATE
+        assert L.ssla_hip_timing_alloc(cfg, 0, 1024) == abi.SSLA_ERR_STATE
+        assert b"already allocated" in L.ssla_hip_last_error()
+        assert (d.cfg.hidden[0][0], d.cfg.preds[0], d.cfg.timing[0]) == before
+
+
 def test_edge_cases(H, stub_dir, stub_npz):
     layers = O.layers_from_npz(stub_npz)
     with H.Drain.from_weights_dir(stub_dir) as d:
