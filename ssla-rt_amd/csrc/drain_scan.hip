@@ -859,6 +859,9 @@ struct Workspace {
     BlockDesc* bd_host = nullptr;      // pinned staging of the block table
     hipEvent_t bd_copied = nullptr;    // the last staging copy has been read
     hipEvent_t done = nullptr;         // the last drain's work on the workspace
+    hipStream_t side = nullptr;        // s3 ordering, concurrent with L4 and L5
+    hipEvent_t s2_ordered = nullptr;   // s2 tables and pass2 are complete
+    hipEvent_t s3_ordered = nullptr;   // s3 tables and pass3 are complete
     void* temp;
     size_t temp_bytes;
     float* packed = nullptr;           // fragment-order weight copies (packed_weight_floats_d)
@@ -978,6 +981,9 @@ int ensure_workspace(int E, int nkeys) {
                              hipHostMallocDefault));
         HIPCHK(hipEventCreateWithFlags(&w.bd_copied, hipEventDisableTiming));
         HIPCHK(hipEventCreateWithFlags(&w.done, hipEventDisableTiming));
+        HIPCHK(hipEventCreateWithFlags(&w.s2_ordered, hipEventDisableTiming));
+        HIPCHK(hipEventCreateWithFlags(&w.s3_ordered, hipEventDisableTiming));
+        HIPCHK(hipStreamCreateWithFlags(&w.side, hipStreamNonBlocking));
         HIPCHK(hipMalloc(&w.packed, sizeof(float) * packed_weight_floats_d()));
     }
     w.base = base;
@@ -1148,41 +1154,48 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, nk2, w.pst2, w.pen2);
     hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, w.va, nk2,
                        w.pos2, w.prec2);
-    // ---- tdrop_s3 over pass2 records, by s3 centre cell ---------------------
-    hipLaunchKernelGGL(k_keys3, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, w.cell2,
-                       w.pass2, w.key3g, w.ka, w.va);
-    HIPCHK(sort_pairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, E, bits3, st));
-    hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, nk3, w.st3, w.en3);
-    hipLaunchKernelGGL(k_tdrop, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, w.vb, nk3,
-                       G.C3, w.st3, w.bd, 3, G.window, w.pass3);
-    hipLaunchKernelGGL(k_tdrop_commit, dim3(grid1(nk3, 256)), dim3(256), 0, st, nk3, G.C3,
-                       w.st3, w.en3, w.bd, 3);
-    // ---- s3 pair order ---------------------------------------------------------
-    hipLaunchKernelGGL(k_pairs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, 3,
-                       w.cell2, w.pass2, w.kb, w.vb);
-    HIPCHK(sort_pairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, bits3, st));
-    hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, nk3, w.pst3, w.pen3);
-    hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, w.va, nk3,
-                       w.pos3, w.prec3);
-    // ---- chunk tables of the per-cell pair runs ---------------------------------
+    // ---- s2 chunk tables and the pass2 record list ------------------------------
     hipLaunchKernelGGL(k_chunk_count, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, w.pst2,
                        w.pen2, w.ccnt2);
     HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt2, w.coff2, (int)nk2, st));
     hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(w.max_chunks, 256)), dim3(256), 0, st, nk2,
                        w.max_chunks, w.pst2,
                        w.pen2, w.ccnt2, w.coff2, w.ckey2, w.cbeg2, w.cend2, w.counts + 2);
-    hipLaunchKernelGGL(k_chunk_count, dim3(grid1(nk3, 256)), dim3(256), 0, st, nk3, w.pst3,
-                       w.pen3, w.ccnt3);
-    HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt3, w.coff3, (int)nk3, st));
-    hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(w.max_chunks, 256)), dim3(256), 0, st, nk3,
-                       w.max_chunks, w.pst3,
-                       w.pen3, w.ccnt3, w.coff3, w.ckey3, w.cbeg3, w.cend3, w.counts + 3);
-    // ---- record lists: pass2 records, pass3 records (ring order) --------------
     HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
                                           w.pass2, w.list2, w.counts + 0, E, st));
+    // The s3 ordering needs only pass2 and the centre cells, so it runs on the
+    // side stream while L4 and L5 run here; L6 waits for it.  Nothing on this
+    // stream touches the sort buffers, the scratch storage or any s3 table
+    // until then.
+    HIPCHK(hipEventRecord(w.s2_ordered, st));
+    hipStream_t s3 = w.side;
+    HIPCHK(hipStreamWaitEvent(s3, w.s2_ordered, 0));
+    // ---- tdrop_s3 over pass2 records, by s3 centre cell ---------------------
+    hipLaunchKernelGGL(k_keys3, dim3(grid1(E, 256)), dim3(256), 0, s3, E, w.bd, G, w.cell2,
+                       w.pass2, w.key3g, w.ka, w.va);
+    HIPCHK(sort_pairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, E, bits3, s3));
+    hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, s3, E, w.kb, nk3, w.st3, w.en3);
+    hipLaunchKernelGGL(k_tdrop, dim3(grid1(E, 256)), dim3(256), 0, s3, E, w.kb, w.vb, nk3,
+                       G.C3, w.st3, w.bd, 3, G.window, w.pass3);
+    hipLaunchKernelGGL(k_tdrop_commit, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, G.C3,
+                       w.st3, w.en3, w.bd, 3);
+    // ---- s3 pair order, chunk tables, pass3 record list -----------------------
+    hipLaunchKernelGGL(k_pairs, dim3(grid1(E, 256)), dim3(256), 0, s3, E, w.bd, G, 3,
+                       w.cell2, w.pass2, w.kb, w.vb);
+    HIPCHK(sort_pairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, bits3, s3));
+    hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, s3, P, w.ka, nk3, w.pst3, w.pen3);
+    hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P, 256)), dim3(256), 0, s3, P, w.ka, w.va, nk3,
+                       w.pos3, w.prec3);
+    hipLaunchKernelGGL(k_chunk_count, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, w.pst3,
+                       w.pen3, w.ccnt3);
+    HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt3, w.coff3, (int)nk3, s3));
+    hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(w.max_chunks, 256)), dim3(256), 0, s3, nk3,
+                       w.max_chunks, w.pst3,
+                       w.pen3, w.ccnt3, w.coff3, w.ckey3, w.cbeg3, w.cend3, w.counts + 3);
     // k_tdrop wrote pass3 = 0 for records that did not pass tdrop_s2.
     HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
-                                          w.pass3, w.list3, w.counts + 1, E, st));
+                                          w.pass3, w.list3, w.counts + 1, E, s3));
+    HIPCHK(hipEventRecord(w.s3_ordered, s3));
     HIPCHK(hipGetLastError());
 
     MARK();
@@ -1224,6 +1237,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        pk.po[1], L[1].ln_gamma, L[1].ln_beta, w.X2);
     MARK();
     // ---- L6: 48 -> 96, pass2 records ------------------------------------------
+    HIPCHK(hipStreamWaitEvent(st, w.s3_ordered, 0));
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, pk.pp[2], w.QVG);
     MARK();
