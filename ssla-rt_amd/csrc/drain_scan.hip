@@ -923,7 +923,7 @@ int ensure_workspace(int E, int nkeys) {
         {(void**)&w.X2, sizeof(float) * (size_t)cap * SSLA_C2},
         {(void**)&w.X3, sizeof(float) * (size_t)cap * SSLA_C3},
         {(void**)&w.X4, sizeof(float) * (size_t)cap * SSLA_C3},
-        {(void**)&w.QVG, sizeof(float) * P * 3 * SSLA_C3},
+        {(void**)&w.QVG, sizeof(float) * P * 2 * SSLA_C3},     // [v | g] rows
         {(void**)&w.H7, sizeof(float) * (size_t)cap * 7},
         {(void**)&w.cell2, sizeof(int) * (size_t)cap},
         {(void**)&w.pos2, sizeof(int) * P},
