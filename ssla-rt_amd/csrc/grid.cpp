@@ -17,6 +17,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <exception>
 #include <string>
 #include <vector>
 
@@ -99,10 +100,24 @@ int oeva_load(const char* path, OevaFile& f, bool body) {
     f.na = hdr[2];
     f.cols = hdr[3];
     f.ncp = hdr[4];
+    const size_t per = size_t(f.na) * f.cols;
+    // a corrupt header must not turn into a huge allocation (here or in a
+    // caller sizing its buffers from the header): a dump's checkpoints stay
+    // far below 4 Gi floats
+    if (per > (size_t(1) << 28) || size_t(f.ncp) * per > (size_t(1) << 32)) {
+        std::fclose(fp);
+        set_error(std::string("oeva: implausible header sizes: ") + path);
+        return SSLA_ERR_FORMAT;
+    }
     if (body) {
-        const size_t per = size_t(f.na) * f.cols;
-        f.idx.assign(f.ncp, 0);
-        f.preds.assign(size_t(f.ncp) * per, 0.0f);
+        try {
+            f.idx.assign(f.ncp, 0);
+            f.preds.assign(size_t(f.ncp) * per, 0.0f);
+        } catch (const std::exception&) {
+            std::fclose(fp);
+            set_error(std::string("oeva: out of memory reading ") + path);
+            return SSLA_ERR_IO;
+        }
         for (uint32_t i = 0; i < f.ncp; ++i) {
             if (std::fread(&f.idx[i], 8, 1, fp) != 1) break;
             if (std::fread(f.preds.data() + i * per, sizeof(float), per, fp) != per) break;

@@ -254,6 +254,12 @@ def test_oeva_roundtrip_and_errors(tmp_path):
     (tmp_path / "s.oeva").write_bytes(raw[:12])
     with pytest.raises(lib.SslaHipError, match="header"):
         grid.read_dump(tmp_path / "s.oeva")
+    # a corrupt header (2^32 - 1 checkpoints of 12 x 7) is refused before
+    # anything is allocated from it
+    huge = np.array([0x4F455641, 1, 12, 7, 0xFFFFFFFF], "<u4").tobytes() + raw[20:]
+    (tmp_path / "h.oeva").write_bytes(huge)
+    with pytest.raises(lib.SslaHipError, match="implausible"):
+        grid.read_dump(tmp_path / "h.oeva")
     with pytest.raises(lib.SslaHipError, match="cannot open"):
         grid.diff_dumps(path, tmp_path / "missing.oeva")
 
