@@ -178,7 +178,13 @@ int ssla_hip_grid_decode(const HybridS2S3Config* cfg, const float* zero_row, int
     const int W3 = cfg->W3, H3 = cfg->H3;
     // Untouched cells hold the head's output for an all-zero feature, as a
     // freshly built CPU pipeline does (src/ssla_kernels.cpp:966-987).
-    std::vector<float> raw(size_t(H3) * W3 * cols);
+    std::vector<float> raw;
+    try {
+        raw.resize(size_t(H3) * W3 * cols);
+    } catch (const std::exception&) {
+        set_error("grid_decode: cannot hold the s3 grid");
+        return SSLA_ERR_ARG;
+    }
     for (size_t c = 0; c < size_t(H3) * W3; ++c) std::memcpy(&raw[c * cols], zero_row, sizeof(float) * cols);
     int torn = 0;
     std::vector<float> cell(cols);
