@@ -22,6 +22,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <exception>
 #include <memory>
 #include <random>
 #include <thread>
@@ -441,8 +442,16 @@ Producer* make_producer(const char* dir, int n_shards, int halo, int base_core, 
     P->strip = (P->W + n_shards - 1) / n_shards;
     P->t0 = std::chrono::steady_clock::now();
     Producer* raw = P.release();
-    for (int k = 0; k < n_shards; ++k)
-        raw->threads.emplace_back([raw, k, to_gpu]() { raw->work(raw->shards[k].get(), to_gpu); });
+    try {
+        for (int k = 0; k < n_shards; ++k)
+            raw->threads.emplace_back([raw, k, to_gpu]() { raw->work(raw->shards[k].get(), to_gpu); });
+    } catch (const std::exception& e) {
+        // threads already started take their end-of-stream message and exit
+        std::fprintf(stderr, "[%s] shard threads: %s\n", tag, e.what());
+        raw->shutdown();
+        delete raw;
+        return nullptr;
+    }
     return raw;
 }
 
@@ -540,7 +549,12 @@ void synth_loop(Producer* P, double rate_mev, int core, std::uint64_t seed, int 
     if (P->synth.joinable()) P->synth.join();
     P->synth_n = 0;
     P->synth_on = true;
-    P->synth = std::thread(synth_loop, P, rate, core, seed, n_blobs, sigma, bg);
+    try {
+        P->synth = std::thread(synth_loop, P, rate, core, seed, n_blobs, sigma, bg);
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "[s01g] synthetic source thread: %s\n", e.what());
+        P->synth_on = false;
+    }
 }
 
 }  // namespace
@@ -772,7 +786,13 @@ static S01gReplay* replay_start(int n_rings, void* const* ring_bufs, void* const
     r->period_ns = rate_rec_s > 0 ? 1e9 / rate_rec_s : 0.0;
     r->speed = speed;
     r->core = pin_core;
-    r->th = std::thread([r]() { r->run(); });
+    try {
+        r->th = std::thread([r]() { r->run(); });
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "[s01g] replay thread: %s\n", e.what());
+        delete r;
+        return nullptr;
+    }
     return r;
 }
 
