@@ -403,7 +403,7 @@ k_scan_carry(int C, const int* __restrict__ start, const int* __restrict__ end,
     float* hp = bd[b].hidden[li] + (size_t)cell * OUT + c;
     float h = *hp;
     const int c0 = coff[k], nc = cnt[k];
-    constexpr int U = 16;        // chunks whose maps are in flight together
+    constexpr int U = 32;        // chunks whose maps are in flight together
     for (int q0 = 0; q0 < nc; q0 += U) {
         float a[U], b[U];
         #pragma unroll
@@ -436,7 +436,7 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
     const int s = cbeg[j], e = cend[j];
     float h = Hs[(size_t)j * OUT + c];
     float* row = QVG + (size_t)s * NC + c;
-    constexpr int U = 8;         // pairs whose v, g are in flight together
+    constexpr int U = 16;        // pairs whose v, g are in flight together
     for (int p0 = s; p0 < e; p0 += U, row += U * NC) {
         float v[U], g[U];
         bool use[U];
