@@ -141,14 +141,67 @@ __device__ __forceinline__ void mark(Lds& S, int slot) {
     }
 }
 
+// Wave-wide sums (all 64 lanes active) from DPP moves inside each 16-lane
+// row (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), a ds_swizzle
+// swap of the 16-lane halves of each 32-lane group, and the two 32-lane
+// group sums read from lanes 0 and 32 (wave-uniform result).
+namespace dppc {
+constexpr int kXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kHalfMirror = 0x141; // row_half_mirror: lane i <- 7 - i in each 8
+constexpr int kMirror = 0x140;     // row_mirror: lane i <- 15 - i in each 16
+constexpr int kSwap16 = 0x401F;    // ds_swizzle bit mode, xor 16 within 32
+}  // namespace dppc
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+    const unsigned lo = (unsigned)dpp_i<CTRL>((int)(unsigned)b);
+    const unsigned hi = (unsigned)dpp_i<CTRL>((int)(unsigned)(b >> 32));
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
+__device__ __forceinline__ double swap16_d(double v) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_ds_swizzle((int)(unsigned)b, dppc::kSwap16);
+    const unsigned hi = (unsigned)__builtin_amdgcn_ds_swizzle((int)(unsigned)(b >> 32), dppc::kSwap16);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
+__device__ __forceinline__ double lane_d(double v, int l) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
 __device__ __forceinline__ double wave_sum(double v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    v += dpp_d<dppc::kXor1>(v);
+    v += dpp_d<dppc::kXor2>(v);
+    v += dpp_d<dppc::kHalfMirror>(v);
+    v += dpp_d<dppc::kMirror>(v);
+    v += swap16_d(v);
+    return lane_d(v, 0) + lane_d(v, 32);
 }
 
 __device__ __forceinline__ float wave_sumf(float v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    v += dpp_f<dppc::kXor1>(v);
+    v += dpp_f<dppc::kXor2>(v);
+    v += dpp_f<dppc::kHalfMirror>(v);
+    v += dpp_f<dppc::kMirror>(v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), dppc::kSwap16));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
+           __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
 }
 
 // A float4 of an LDS row: x is 16-byte aligned and `at` a multiple of 4.
