@@ -482,7 +482,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-live", action="store_true", help="skip the live latency run")
     ap.add_argument("--live-seconds", type=float, default=8.0)
-    ap.add_argument("--live-blocks", type=int, default=8, choices=[1, 2, 4, 8],
+    ap.add_argument("--live-blocks", type=int, default=8, choices=[1, 2, 4, 8, 16],
                     help="GPU blocks (owned strips) of the live run")
     ap.add_argument("--batch", type=int, default=0,
                     help="1..32: drain through the live kernel's in-kernel batches of this "

@@ -102,7 +102,7 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
              spin_ns: int = 200, profile: bool = True, drain_timeout_s: float = 30.0,
              back_pressure: bool = False) -> LiveResult:
     """One live run on one GPU.  back_pressure makes the producer wait for
-    each ring's tail instead of overwriting unread slots.  gpu_blocks (1, 2, 4, 8; the reference's
+    each ring's tail instead of overwriting unread slots.  gpu_blocks (1, 2, 4, 8, 16; the reference's
     default is 8) splits the s2 grid into owned strips with a 2-cell halo
     (topology.grid_topology); each strip has its own ring, hidden state and
     prediction grid and is drained by its own workgroup.  Halo records are
