@@ -150,7 +150,7 @@ __global__ void k_pairs(int E, const BlockDesc* __restrict__ bd, Geometry G,
 }
 
 // Up to kFills int arrays set to a value each, one launch (blockIdx.y = array).
-constexpr int kFills = 10;
+constexpr int kFills = 8;
 struct FillSet {
     int* p[kFills];
     int n[kFills];
@@ -735,18 +735,34 @@ k_head(const int* __restrict__ n_dev, const int* __restrict__ list,
     }
 }
 
-// Last owned pass-3 record per s3 cell and number of such records.
-__global__ void k_pred_last(const int* __restrict__ n_dev, const int* __restrict__ list,
-                            const unsigned char* __restrict__ owner,
-                            const uint32_t* __restrict__ key3_by_g,
-                            int* __restrict__ last, int* __restrict__ count) {
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= *n_dev) return;
-    const int g = list[j];
-    if (!owner[g]) return;
-    const uint32_t k = key3_by_g[g];
-    atomicMax(&last[k], g);
-    atomicAdd(&count[k], 1);
+// Per s3 key, from its run in the s3 record sort (ring order): the last
+// owned pass-3 record (-1 if none) and the number of owned pass-3 records.
+// One wave per key, four keys per workgroup.
+__global__ void __launch_bounds__(256)
+k_pred_runs(uint32_t nk, const int* __restrict__ start, const int* __restrict__ end,
+            const uint32_t* __restrict__ vals, const unsigned char* __restrict__ pass3,
+            const unsigned char* __restrict__ owner, int* __restrict__ last,
+            int* __restrict__ count) {
+    const uint32_t k = blockIdx.x * 4u + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (k >= nk) return;
+    const int s = start[k], e = end[k];
+    int lst = -1, cnt = 0;
+    for (int p = s + lane; p < e; p += 64) {
+        const int g = (int)vals[p];
+        if (pass3[g] && owner[g]) {
+            lst = max(lst, g);
+            ++cnt;
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        lst = max(lst, __shfl_xor(lst, off, 64));
+        cnt += __shfl_xor(cnt, off, 64);
+    }
+    if (lane == 0) {
+        last[k] = lst;
+        count[k] = cnt;
+    }
 }
 
 __global__ void k_pred_write(const int* __restrict__ n_dev, const int* __restrict__ list,
@@ -1122,19 +1138,16 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     const int bits2 = bits_for(nk2), bits3 = bits_for(nk3);
     size_t tb = w.temp_bytes;
 
-    // run bounds (filled by k_runs where a key occurs) and the head's
-    // per-cell tables start from these values
+    // run bounds start at zero; k_runs fills them where a key occurs
     {
         FillSet f{};
-        int* arr[kFills] = {w.st2, w.en2, w.pst2, w.pen2, w.st3, w.en3, w.pst3, w.pen3,
-                            w.last3, w.cnt3};
+        int* arr[kFills] = {w.st2, w.en2, w.pst2, w.pen2, w.st3, w.en3, w.pst3, w.pen3};
         const int len[kFills] = {(int)nk2, (int)nk2, (int)nk2, (int)nk2, (int)nk3, (int)nk3,
-                                 (int)nk3, (int)nk3, have_head ? (int)nk3 : 0,
-                                 have_head ? (int)nk3 : 0};
+                                 (int)nk3, (int)nk3};
         for (int i = 0; i < kFills; ++i) {
             f.p[i] = arr[i];
             f.n[i] = len[i];
-            f.v[i] = i == 8 ? -1 : 0;
+            f.v[i] = 0;
         }
         hipLaunchKernelGGL(k_fill_set, dim3(grid1(nk2, 256), kFills), dim3(256), 0, st, f);
     }
@@ -1179,6 +1192,10 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        G.C3, w.st3, w.bd, 3, G.window, w.pass3);
     hipLaunchKernelGGL(k_tdrop_commit, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, G.C3,
                        w.st3, w.en3, w.bd, 3);
+    // prediction-grid writers: the last owned pass-3 record of each s3 cell
+    if (have_head)
+        hipLaunchKernelGGL(k_pred_runs, dim3(grid1(nk3, 4)), dim3(256), 0, s3, nk3, w.st3, w.en3,
+                           w.vb, w.pass3, w.owner, w.last3, w.cnt3);
     // ---- s3 pair order, chunk tables, pass3 record list -----------------------
     hipLaunchKernelGGL(k_pairs, dim3(grid1(E, 256)), dim3(256), 0, s3, E, w.bd, G, 3,
                        w.cell2, w.pass2, w.kb, w.vb);
@@ -1280,8 +1297,6 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                     cfg->head_obj_pred_b};
         hipLaunchKernelGGL(k_head, dim3(tilesE), dim3(256), 0, st, (const int*)(w.counts + 1),
                            w.list3, w.X4, hp, w.H7);
-        hipLaunchKernelGGL(k_pred_last, dim3(grid1(E, 256)), dim3(256), 0, st,
-                           (const int*)(w.counts + 1), w.list3, w.owner, w.key3g, w.last3, w.cnt3);
         hipLaunchKernelGGL(k_pred_write, dim3(grid1(E, 256)), dim3(256), 0, st,
                            (const int*)(w.counts + 1), w.list3, w.owner, w.key3g, w.last3,
                            w.cnt3, w.bd, G, w.H7);
