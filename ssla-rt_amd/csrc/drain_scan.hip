@@ -249,6 +249,8 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
     constexpr int tlo = P::TQ, thi = P::T;      // the v and g column tiles
     __shared__ __align__(16) float xs[kTM * XST];
     __shared__ int prow[kPatch][kTM];
+    constexpr int TST = kMT + 4;                 // transpose tile row stride (16-byte rows)
+    __shared__ __align__(16) float tt[4][kMT * TST];   // one 16 x 16 tile per wave
     const int n = n_dev ? *n_dev : n_max;
     const int base = blockIdx.x * kTM;
     if (base >= n) return;
@@ -277,8 +279,12 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
     const int lane = tid & 63, wv = tid >> 6, li = lane & 15, lk = lane >> 4;
     const int nti = thi - tlo, N = kPatch * nti, mtiles = (cnt + kMT - 1) / kMT;
     auto item = [&](int it) { const int d = it / nti; return d * P::T + tlo + (it - d * nti); };
+    // each 16 x 16 result tile goes through the wave's LDS tile so that a
+    // lane stores one float4 of a row (lane l: row l / 4, columns 4 (l % 4))
+    float* tw = tt[wv];
+    const int trow = lane >> 2, tq = lane & 3;
     auto run = [&](int it, const float* b) {
-        const int d = it / nti, t = tlo + (it - d * nti), col = t * kMT + li;
+        const int d = it / nti, t = tlo + (it - d * nti), c0 = t * kMT - OUT + 4 * tq;
         for (int m = 0; m < mtiles; ++m) {
             const float* a = &xs[(m * kMT + li) * XST + lk];
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -286,10 +292,13 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
             for (int s = 0; s < P::KS; ++s)
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s], b[s], acc, 0, 0, 0);
             #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int pr = prow[d][m * kMT + 4 * lk + r];
-                if (pr >= 0) gstore(QVG + (size_t)pr * NCW + (col - OUT), acc[r]);
-            }
+            for (int r = 0; r < 4; ++r) tw[(4 * lk + r) * TST + li] = acc[r];
+            __builtin_amdgcn_wave_barrier();
+            const float4 v = *reinterpret_cast<const float4*>(&tw[trow * TST + 4 * tq]);
+            __builtin_amdgcn_wave_barrier();
+            const int pr = prow[d][m * kMT + trow];
+            if (pr >= 0)
+                *reinterpret_cast<float4*>(QVG + (size_t)pr * NCW + c0) = v;
         }
     };
     float b0[P::KS4 * 4], b1[P::KS4 * 4];
