@@ -222,9 +222,11 @@ __global__ void k_pair_pos(int n, const uint32_t* __restrict__ keys,
 // tile) items, loads an item's weights (fragment order, one float4 per four
 // k-steps) while the previous item's four row tiles run, and writes each
 // [v | g] row (2 * OUT floats) to the pair's sorted position.  q is not
-// stored: the contraction recomputes it from the record's input.  (Staging
-// whole rows in LDS for 16-byte stores measured slower: the extra barriers
-// cost more than the partial-line writes.)
+// stored: the contraction recomputes it from the record's input.  Each
+// 16 x 16 result tile passes through a wave-private LDS tile so that lanes
+// store whole 16-byte pieces of rows; no workgroup barrier is involved
+// (staging whole rows across waves measured slower: the barriers cost more
+// than the partial-line writes).
 // ---------------------------------------------------------------------------
 constexpr int kTM = 64;     // records per projection / contraction workgroup
 
