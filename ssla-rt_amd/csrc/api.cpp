@@ -27,6 +27,7 @@ thread_local std::string t_err;
 
 std::mutex g_alloc_mu;
 std::set<void*> g_state_bases;   // blocks allocated by ssla_hip_state_alloc
+std::map<void*, size_t> g_state_bytes;   // their sizes: one allocation holds a block's state
 std::set<void*> g_pred_bases;    // preds allocated by ssla_hip_preds_alloc
 }  // namespace
 
@@ -502,6 +503,7 @@ int ssla_hip_state_alloc(HybridS2S3Config* cfg, int blk) {
     cfg->tdrop_s3[blk] = static_cast<unsigned char*>(parts[5]);
     std::lock_guard<std::mutex> lk(g_alloc_mu);
     g_state_bases.insert(base);
+    g_state_bytes[base] = total;
     return SSLA_OK;
 }
 
@@ -523,6 +525,20 @@ int ssla_hip_state_reset(const HybridS2S3Config* cfg, int blk) {
 int ssla_hip_state_reset_async(const HybridS2S3Config* cfg, int blk, void* stream) {
     if (!cfg || blk < 0 || blk >= SSLA_MAX_BLOCKS) { set_error("bad block"); return SSLA_ERR_ARG; }
     hipStream_t st = static_cast<hipStream_t>(stream);
+    {
+        // state from ssla_hip_state_alloc: hidden layers and counters are
+        // one allocation, cleared by one fill
+        size_t bytes = 0;
+        {
+            std::lock_guard<std::mutex> lk(g_alloc_mu);
+            const auto it = g_state_bytes.find(cfg->hidden[blk][0]);
+            if (it != g_state_bytes.end()) bytes = it->second;
+        }
+        if (bytes) {
+            API_HIP(hipMemsetAsync(cfg->hidden[blk][0], 0, bytes, st));
+            return SSLA_OK;
+        }
+    }
     const size_t c2 = (size_t)cfg->H2 * cfg->W2, c3 = (size_t)cfg->H3 * cfg->W3;
     const size_t sz[4] = {c2 * 48 * 4, c2 * 48 * 4, c3 * 96 * 4, c3 * 96 * 4};
     for (int li = 0; li < 4; ++li) {
@@ -541,6 +557,7 @@ void ssla_hip_state_free(HybridS2S3Config* cfg, int blk) {
     {
         std::lock_guard<std::mutex> lk(g_alloc_mu);
         if (!base || !g_state_bases.erase(base)) return;
+        g_state_bytes.erase(base);
     }
     (void)hipFree(base);
     for (int li = 0; li < 4; ++li) cfg->hidden[blk][li] = nullptr;
