@@ -482,6 +482,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-live", action="store_true", help="skip the live latency run")
     ap.add_argument("--live-seconds", type=float, default=8.0)
+    ap.add_argument("--live-rate", type=float, default=2.0,
+                    help="raw event rate of the live run's synthetic source, Mev/s")
     ap.add_argument("--live-blocks", type=int, default=8, choices=[1, 2, 4, 8, 16],
                     help="GPU blocks (owned strips) of the live run")
     ap.add_argument("--batch", type=int, default=0,
@@ -586,7 +588,7 @@ def main() -> int:
     }
     d.close()
     if a.workload == "80x64" and not a.no_live:
-        res["latency_us"] = live_latency(tmp.name, 2.0, a.live_seconds, a.live_blocks)
+        res["latency_us"] = live_latency(tmp.name, a.live_rate, a.live_seconds, a.live_blocks)
     if a.workload == "16streams" and not a.no_live:
         res["latency_us"] = replay_latency(tmp.name, recs, [o["pass3"] for o in outs])
     if a.workload == "640x480" and not a.no_live:
