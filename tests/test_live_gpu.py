@@ -400,6 +400,21 @@ def test_run_live_short(stub_dir):
     assert r.lat_us["kernel_p50"] > 0
 
 
+def test_run_live_sixteen_blocks(stub_dir):
+    """The 4 x 4 strip topology (16 rings, 16 workgroups of one persistent
+    kernel) fed by the host producer: every published record (halo copies
+    included) is drained and output-producing records carry latencies."""
+    from ssla_hip import live as LV
+    say("run_live 0.5 Mev/s 1 s, 16 blocks")
+    r = LV.run_live(stub_dir, rate_mev=0.5, duration_s=1.0, n_shards=2, halo=2,
+                    timing_capacity=1 << 16, gpu_blocks=16)
+    say(f"run_live 16: status {r.status} ring {r.ring_records} drained {r.drained} "
+        f"out {r.output_records}")
+    assert r.status == 0 and r.gpu_blocks == 16
+    assert r.drained == r.ring_records > 0 and r.output_records > 0
+    assert r.lat_us["kernel_p50"] > 0
+
+
 def test_replay_four_streams_live(stub_dir, stub_npz):
     """Four streams replayed into four rings of one persistent kernel: every
     record drained, drop drift 0 per stream against the oracle's schedule."""
