@@ -587,18 +587,33 @@ def main() -> int:
         "roofline": roof,
     }
     d.close()
+    # The latency and CPU legs run after the timed drain; a failure in one is
+    # reported in its field and in the exit status, after the line is printed.
+    failed = []
+
+    def leg(name, fn):
+        try:
+            return fn()
+        except Exception as e:            # noqa: BLE001 - reported, not hidden
+            failed.append(name)
+            print(f"bench.py: {name} failed: {e!r}", file=sys.stderr)
+            return {"error": f"{type(e).__name__}: {e}"}
+
     if a.workload == "80x64" and not a.no_live:
-        res["latency_us"] = live_latency(tmp.name, a.live_rate, a.live_seconds, a.live_blocks)
+        res["latency_us"] = leg("live", lambda: live_latency(tmp.name, a.live_rate,
+                                                             a.live_seconds, a.live_blocks))
     if a.workload == "16streams" and not a.no_live:
-        res["latency_us"] = replay_latency(tmp.name, recs, [o["pass3"] for o in outs])
+        res["latency_us"] = leg("replay", lambda: replay_latency(
+            tmp.name, recs, [o["pass3"] for o in outs]))
     if a.workload == "640x480" and not a.no_live:
-        res["latency_us"] = split_replay_latency(tmp.name, recs[0], H2, W2)
+        res["latency_us"] = leg("split replay", lambda: split_replay_latency(
+            tmp.name, recs[0], H2, W2))
     if not a.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(tmp.name, recs[0], a.cpu_seconds, H2, W2,
-                                           (outs[0], heads[0]))
+        res["cpu_baseline"] = leg("cpu baseline", lambda: cpu_baseline(
+            tmp.name, recs[0], a.cpu_seconds, H2, W2, (outs[0], heads[0])))
     tmp.cleanup()
     print(json.dumps(res))
-    return 0
+    return 1 if failed else 0
 
 
 if __name__ == "__main__":
