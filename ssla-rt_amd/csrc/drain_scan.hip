@@ -328,7 +328,10 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 //   C (k_scan_apply)   per chunk: replays the chunk from its start state and
 //                      replaces v by h in place for pairs whose record needs
 //                      this layer's output
-// One lane per channel in all three passes.
+// One lane per channel in all three passes.  Passes A and C read the v, g
+// rows with nontemporal loads: the rows are read once per pass and the
+// projection has just left up to 0.7 GB of them in the caches; streaming
+// them past the L2 made pass A 35-40% faster and pass C 2-9%.
 // ---------------------------------------------------------------------------
 constexpr int kCH = 64;
 
@@ -385,8 +388,8 @@ k_scan_summary(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
         #pragma unroll
         for (int q = 0; q < U; ++q) {
             const int k = p0 + q < e ? q : 0;
-            v[q] = gload(row + (size_t)k * NC);
-            g[q] = gload(row + (size_t)k * NC + OUT);
+            v[q] = __builtin_nontemporal_load(row + (size_t)k * NC);
+            g[q] = __builtin_nontemporal_load(row + (size_t)k * NC + OUT);
         }
         #pragma unroll
         for (int q = 0; q < U; ++q) {
@@ -455,8 +458,8 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
         for (int u = 0; u < U; ++u) {
             const int k = p0 + u < e ? u : 0;
             use[u] = p0 + u < e && (!need || need[pair_rec[p0 + k]]);
-            v[u] = gload(row + (size_t)k * NC);
-            g[u] = gload(row + (size_t)k * NC + OUT);
+            v[u] = __builtin_nontemporal_load(row + (size_t)k * NC);
+            g[u] = __builtin_nontemporal_load(row + (size_t)k * NC + OUT);
         }
         #pragma unroll
         for (int u = 0; u < U; ++u) {
