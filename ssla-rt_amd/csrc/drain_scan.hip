@@ -126,12 +126,17 @@ __global__ void k_keys3(int E, const BlockDesc* __restrict__ bd, Geometry G,
 // (record, delta) pair keys: the patch cell the pair updates, or the
 // sentinel nb*C when the cell is off the grid or the record does not enter
 // the level (level 3 takes pass2 records only).  delta = (1-dy)*3 + (1-dx).
+// With `list` (level 3: the pass2 records, n_dev of them), slot j of the
+// output holds the pairs of record list[j]; the pair values stay
+// record * 9 + delta either way.
 __global__ void k_pairs(int E, const BlockDesc* __restrict__ bd, Geometry G,
                         int level, const int* __restrict__ cell2,
                         const unsigned char* __restrict__ pass2,
+                        const int* __restrict__ n_dev, const int* __restrict__ list,
                         uint32_t* __restrict__ pkey, uint32_t* __restrict__ pval) {
-    const int g = blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= E) return;
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= (list ? *n_dev : E)) return;
+    const int g = list ? list[j] : j;
     const int b = find_block(bd, G.nb, g);
     const int c = cell2[g];
     const bool live = c >= 0 && (level == 2 || pass2[g]);
@@ -144,8 +149,8 @@ __global__ void k_pairs(int E, const BlockDesc* __restrict__ bd, Geometry G,
     for (int d = 0; d < kPatch; ++d) {
         const int ty = y + 1 - d / 3, tx = x + 1 - d % 3;
         const bool in = live && ty >= 0 && ty < H && tx >= 0 && tx < W;
-        pkey[(size_t)g * kPatch + d] = in ? (uint32_t)(b * C + ty * W + tx) : none;
-        pval[(size_t)g * kPatch + d] = (uint32_t)(g * kPatch + d);
+        pkey[(size_t)j * kPatch + d] = in ? (uint32_t)(b * C + ty * W + tx) : none;
+        pval[(size_t)j * kPatch + d] = (uint32_t)(g * kPatch + d);
     }
 }
 
@@ -892,6 +897,8 @@ struct Workspace {
     hipStream_t side = nullptr;        // s3 ordering, concurrent with L4 and L5
     hipEvent_t s2_ordered = nullptr;   // s2 tables and pass2 are complete
     hipEvent_t s3_ordered = nullptr;   // s3 tables and pass3 are complete
+    hipEvent_t n2_ready = nullptr;     // the pass2 count has reached n2_host
+    int* n2_host = nullptr;            // pinned copy of the pass2 count
     void* temp;
     size_t temp_bytes;
     float* packed = nullptr;           // fragment-order weight copies (packed_weight_floats_d)
@@ -1013,6 +1020,8 @@ int ensure_workspace(int E, int nkeys) {
         HIPCHK(hipEventCreateWithFlags(&w.done, hipEventDisableTiming));
         HIPCHK(hipEventCreateWithFlags(&w.s2_ordered, hipEventDisableTiming));
         HIPCHK(hipEventCreateWithFlags(&w.s3_ordered, hipEventDisableTiming));
+        HIPCHK(hipEventCreateWithFlags(&w.n2_ready, hipEventDisableTiming));
+        HIPCHK(hipHostMalloc((void**)&w.n2_host, sizeof(int), hipHostMallocDefault));
         HIPCHK(hipStreamCreateWithFlags(&w.side, hipStreamNonBlocking));
         HIPCHK(hipMalloc(&w.packed, sizeof(float) * packed_weight_floats_d()));
     }
@@ -1176,7 +1185,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        w.st2, w.en2, w.bd, 2);
     // ---- s2 pair order: (record, delta) pairs sorted by patch cell ----------
     hipLaunchKernelGGL(k_pairs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, 2,
-                       w.cell2, w.pass2, w.kb, w.vb);
+                       w.cell2, w.pass2, (const int*)nullptr, (const int*)nullptr, w.kb, w.vb);
     HIPCHK(sort_pairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, bits2, st));
     hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, nk2, w.pst2, w.pen2);
     hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, w.va, nk2,
@@ -1193,10 +1202,13 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // The s3 ordering needs only pass2 and the centre cells, so it runs on the
     // side stream while L4 and L5 run here; L6 waits for it.  Nothing on this
     // stream touches the sort buffers, the scratch storage or any s3 table
-    // until then.
+    // until then.  The pass2 count goes to the host first: the s3 pair order
+    // is sized by it once L4 and L5 are queued.
     HIPCHK(hipEventRecord(w.s2_ordered, st));
     hipStream_t s3 = w.side;
     HIPCHK(hipStreamWaitEvent(s3, w.s2_ordered, 0));
+    HIPCHK(hipMemcpyAsync(w.n2_host, w.counts + 0, sizeof(int), hipMemcpyDeviceToHost, s3));
+    HIPCHK(hipEventRecord(w.n2_ready, s3));
     // ---- tdrop_s3 over pass2 records, by s3 centre cell ---------------------
     hipLaunchKernelGGL(k_keys3, dim3(grid1(E, 256)), dim3(256), 0, s3, E, w.bd, G, w.cell2,
                        w.pass2, w.key3g, w.ka, w.va);
@@ -1210,23 +1222,10 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     if (have_head)
         hipLaunchKernelGGL(k_pred_runs, dim3(grid1(nk3, 4)), dim3(256), 0, s3, nk3, w.st3, w.en3,
                            w.vb, w.pass3, w.owner, w.last3, w.cnt3);
-    // ---- s3 pair order, chunk tables, pass3 record list -----------------------
-    hipLaunchKernelGGL(k_pairs, dim3(grid1(E, 256)), dim3(256), 0, s3, E, w.bd, G, 3,
-                       w.cell2, w.pass2, w.kb, w.vb);
-    HIPCHK(sort_pairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, bits3, s3));
-    hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, s3, P, w.ka, nk3, w.pst3, w.pen3);
-    hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P, 256)), dim3(256), 0, s3, P, w.ka, w.va, nk3,
-                       w.pos3, w.prec3);
-    hipLaunchKernelGGL(k_chunk_count, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, w.pst3,
-                       w.pen3, w.ccnt3);
-    HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt3, w.coff3, (int)nk3, s3));
-    hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(w.max_chunks, 256)), dim3(256), 0, s3, nk3,
-                       w.max_chunks, w.pst3,
-                       w.pen3, w.ccnt3, w.coff3, w.ckey3, w.cbeg3, w.cend3, w.counts + 3);
+    // ---- pass3 record list ---------------------------------------------------
     // k_tdrop wrote pass3 = 0 for records that did not pass tdrop_s2.
     HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
                                           w.pass3, w.list3, w.counts + 1, E, s3));
-    HIPCHK(hipEventRecord(w.s3_ordered, s3));
     HIPCHK(hipGetLastError());
 
     MARK();
@@ -1267,6 +1266,36 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, pk.pp[1],
                        pk.po[1], L[1].ln_gamma, L[1].ln_beta, w.X2);
     MARK();
+    // ---- [side] s3 pair order over the pass2 records only ------------------------
+    // L4 and L5 are queued; the host waits for the pass2 count (known once
+    // tdrop_s2 has run) so the s3 pair sort covers 9 * N2 pairs rather than
+    // 9 * E, most of which would be placeholders.
+    {
+        HIPCHK(hipEventSynchronize(w.n2_ready));
+        const int N2 = *w.n2_host;
+        if (N2 < 0 || N2 > E) {
+            set_error("drain: inconsistent pass2 count");
+            return SSLA_ERR_STATE;
+        }
+        const int P3 = N2 * kPatch;
+        if (P3 > 0) {
+            hipLaunchKernelGGL(k_pairs, dim3(grid1(N2, 256)), dim3(256), 0, s3, E, w.bd, G, 3,
+                               w.cell2, w.pass2, (const int*)(w.counts + 0), w.list2, w.kb, w.vb);
+            HIPCHK(sort_pairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P3, bits3, s3));
+            hipLaunchKernelGGL(k_runs, dim3(grid1(P3, 256)), dim3(256), 0, s3, P3, w.ka, nk3,
+                               w.pst3, w.pen3);
+            hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P3, 256)), dim3(256), 0, s3, P3, w.ka, w.va,
+                               nk3, w.pos3, w.prec3);
+        }
+        hipLaunchKernelGGL(k_chunk_count, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, w.pst3,
+                           w.pen3, w.ccnt3);
+        HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt3, w.coff3, (int)nk3, s3));
+        hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(w.max_chunks, 256)), dim3(256), 0, s3, nk3,
+                           w.max_chunks, w.pst3,
+                           w.pen3, w.ccnt3, w.coff3, w.ckey3, w.cbeg3, w.cend3, w.counts + 3);
+        HIPCHK(hipEventRecord(w.s3_ordered, s3));
+        HIPCHK(hipGetLastError());
+    }
     // ---- L6: 48 -> 96, pass2 records ------------------------------------------
     HIPCHK(hipStreamWaitEvent(st, w.s3_ordered, 0));
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
