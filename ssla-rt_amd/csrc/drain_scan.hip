@@ -106,21 +106,21 @@ k_decode(int E, const BlockDesc* __restrict__ bd, Geometry G,
 
 // s3 centre keys of records that passed tdrop_s2 (sentinel otherwise);
 // key3g keeps a per-record copy for the head, ks/vs feed the sort.
-__global__ void k_keys3(int E, const BlockDesc* __restrict__ bd, Geometry G,
-                        const int* __restrict__ cell2,
-                        const unsigned char* __restrict__ pass2,
+// Over the pass2 list (n records): sort slot j holds record list[j].
+__global__ void k_keys3(int n, const int* __restrict__ list, const BlockDesc* __restrict__ bd,
+                        Geometry G, const int* __restrict__ cell2,
                         uint32_t* __restrict__ key3g, uint32_t* __restrict__ ks,
                         uint32_t* __restrict__ vs) {
-    const int g = blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= E) return;
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    const int g = list[j];
     const int b = find_block(bd, G.nb, g);
-    const int c = cell2[g];
-    const bool live = c >= 0 && pass2[g];
+    const int c = cell2[g];                  // a pass2 record is on the grid
     const int x = (c % G.W2) >> 1, y = (c / G.W2) >> 1;
-    const uint32_t k = live ? (uint32_t)(b * G.C3 + y * G.W3 + x) : (uint32_t)(G.nb * G.C3);
+    const uint32_t k = (uint32_t)(b * G.C3 + y * G.W3 + x);
     key3g[g] = k;
-    ks[g] = k;
-    vs[g] = (uint32_t)g;
+    ks[j] = k;
+    vs[j] = (uint32_t)g;
 }
 
 // (record, delta) pair keys: the patch cell the pair updates, or the
@@ -1209,25 +1209,6 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     HIPCHK(hipStreamWaitEvent(s3, w.s2_ordered, 0));
     HIPCHK(hipMemcpyAsync(w.n2_host, w.counts + 0, sizeof(int), hipMemcpyDeviceToHost, s3));
     HIPCHK(hipEventRecord(w.n2_ready, s3));
-    // ---- tdrop_s3 over pass2 records, by s3 centre cell ---------------------
-    hipLaunchKernelGGL(k_keys3, dim3(grid1(E, 256)), dim3(256), 0, s3, E, w.bd, G, w.cell2,
-                       w.pass2, w.key3g, w.ka, w.va);
-    HIPCHK(sort_pairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, E, bits3, s3));
-    hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, s3, E, w.kb, nk3, w.st3, w.en3);
-    hipLaunchKernelGGL(k_tdrop, dim3(grid1(E, 256)), dim3(256), 0, s3, E, w.kb, w.vb, nk3,
-                       G.C3, w.st3, w.bd, 3, G.window, w.pass3);
-    hipLaunchKernelGGL(k_tdrop_commit, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, G.C3,
-                       w.st3, w.en3, w.bd, 3);
-    // prediction-grid writers: the last owned pass-3 record of each s3 cell
-    if (have_head)
-        hipLaunchKernelGGL(k_pred_runs, dim3(grid1(nk3, 4)), dim3(256), 0, s3, nk3, w.st3, w.en3,
-                           w.vb, w.pass3, w.owner, w.last3, w.cnt3);
-    // ---- pass3 record list ---------------------------------------------------
-    // k_tdrop wrote pass3 = 0 for records that did not pass tdrop_s2.
-    HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
-                                          w.pass3, w.list3, w.counts + 1, E, s3));
-    HIPCHK(hipGetLastError());
-
     MARK();
     const LayerWeightsS2S3* L = cfg->layers[0];
     const unsigned tilesE = grid1(E, kTM);
@@ -1277,6 +1258,26 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
             set_error("drain: inconsistent pass2 count");
             return SSLA_ERR_STATE;
         }
+        // ---- tdrop_s3 over the pass2 records, by s3 centre cell -------------------
+        HIPCHK(hipMemsetAsync(w.pass3, 0, (size_t)E, s3));
+        if (N2 > 0) {
+            hipLaunchKernelGGL(k_keys3, dim3(grid1(N2, 256)), dim3(256), 0, s3, N2, w.list2, w.bd,
+                               G, w.cell2, w.key3g, w.ka, w.va);
+            HIPCHK(sort_pairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, N2, bits3, s3));
+            hipLaunchKernelGGL(k_runs, dim3(grid1(N2, 256)), dim3(256), 0, s3, N2, w.kb, nk3,
+                               w.st3, w.en3);
+            hipLaunchKernelGGL(k_tdrop, dim3(grid1(N2, 256)), dim3(256), 0, s3, N2, w.kb, w.vb,
+                               nk3, G.C3, w.st3, w.bd, 3, G.window, w.pass3);
+        }
+        hipLaunchKernelGGL(k_tdrop_commit, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, G.C3,
+                           w.st3, w.en3, w.bd, 3);
+        // prediction-grid writers: the last owned pass-3 record of each s3 cell
+        if (have_head)
+            hipLaunchKernelGGL(k_pred_runs, dim3(grid1(nk3, 4)), dim3(256), 0, s3, nk3, w.st3,
+                               w.en3, w.vb, w.pass3, w.owner, w.last3, w.cnt3);
+        HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
+                                              w.pass3, w.list3, w.counts + 1, E, s3));
+        // ---- s3 pair order ----------------------------------------------------------
         const int P3 = N2 * kPatch;
         if (P3 > 0) {
             hipLaunchKernelGGL(k_pairs, dim3(grid1(N2, 256)), dim3(256), 0, s3, E, w.bd, G, 3,
