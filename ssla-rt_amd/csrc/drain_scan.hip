@@ -123,39 +123,8 @@ __global__ void k_keys3(int n, const int* __restrict__ list, const BlockDesc* __
     vs[j] = (uint32_t)g;
 }
 
-// (record, delta) pair keys: the patch cell the pair updates, or the
-// sentinel nb*C when the cell is off the grid or the record does not enter
-// the level (level 3 takes pass2 records only).  delta = (1-dy)*3 + (1-dx).
-// With `list` (level 3: the pass2 records, n_dev of them), slot j of the
-// output holds the pairs of record list[j]; the pair values stay
-// record * 9 + delta either way.
-__global__ void k_pairs(int E, const BlockDesc* __restrict__ bd, Geometry G,
-                        int level, const int* __restrict__ cell2,
-                        const unsigned char* __restrict__ pass2,
-                        const int* __restrict__ n_dev, const int* __restrict__ list,
-                        uint32_t* __restrict__ pkey, uint32_t* __restrict__ pval) {
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= (list ? *n_dev : E)) return;
-    const int g = list ? list[j] : j;
-    const int b = find_block(bd, G.nb, g);
-    const int c = cell2[g];
-    const bool live = c >= 0 && (level == 2 || pass2[g]);
-    const int sh = level == 2 ? 0 : 1;
-    const int H = level == 2 ? G.H2 : G.H3, W = level == 2 ? G.W2 : G.W3;
-    const int C = H * W;
-    const int x = (c % G.W2) >> sh, y = (c / G.W2) >> sh;
-    const uint32_t none = (uint32_t)(G.nb * C);
-    #pragma unroll
-    for (int d = 0; d < kPatch; ++d) {
-        const int ty = y + 1 - d / 3, tx = x + 1 - d % 3;
-        const bool in = live && ty >= 0 && ty < H && tx >= 0 && tx < W;
-        pkey[(size_t)j * kPatch + d] = in ? (uint32_t)(b * C + ty * W + tx) : none;
-        pval[(size_t)j * kPatch + d] = (uint32_t)(g * kPatch + d);
-    }
-}
-
 // Up to kFills int arrays set to a value each, one launch (blockIdx.y = array).
-constexpr int kFills = 8;
+constexpr int kFills = 4;
 struct FillSet {
     int* p[kFills];
     int n[kFills];
@@ -208,16 +177,120 @@ __global__ void k_tdrop_commit(uint32_t nk, int C, const int* __restrict__ start
     td[cell] = (unsigned char)(((unsigned)td[cell] + (unsigned)len) & 255u);
 }
 
-// position of every (record, delta) pair in the sorted pair order, -1 if
-// the patch cell is outside the grid (or the record does not enter).
-__global__ void k_pair_pos(int n, const uint32_t* __restrict__ keys,
-                           const uint32_t* __restrict__ vals, uint32_t nk,
-                           int* __restrict__ pos, int* __restrict__ pair_rec) {
-    const int p = blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= n) return;
-    const bool in = keys[p] < nk;
-    pos[vals[p]] = in ? p : -1;
-    pair_rec[p] = in ? (int)(vals[p] / kPatch) : 0;
+constexpr int kCH = 64;     // pairs per scan chunk
+
+// Pair order without a pair sort.  Pair (record g, delta d) updates the
+// patch cell t = (y + 1 - d / 3, x + 1 - d % 3) of g's centre cell (x, y),
+// delta = (1 - dy) * 3 + (1 - dx), when t is on the grid.  Pairs are ordered
+// by t, and inside t by g: a record adds at most one pair to a cell, so this
+// is the stable order of (t, g * 9 + d).  With the records sorted stably by
+// centre cell (run [st, en) of ascending record ids per key), t's pair count
+// is the sum of the run lengths over its 3 x 3 neighbourhood, and a pair's
+// rank inside t is the number of records below g in those nine runs.
+
+// pair count of every key, written to `cnt` (the end array, finished by
+// k_pair_bounds once the start offsets are scanned)
+__global__ void k_pair_count(uint32_t nk, int C, int W, int H, const int* __restrict__ st,
+                             const int* __restrict__ en, int* __restrict__ cnt) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nk) return;
+    const int b = (int)t / C, cell = (int)t % C, ty = cell / W, tx = cell % W;
+    int n = 0;
+    #pragma unroll
+    for (int oy = -1; oy <= 1; ++oy) {
+        #pragma unroll
+        for (int ox = -1; ox <= 1; ++ox) {
+            const int sy = ty + oy, sx = tx + ox;
+            if (sy < 0 || sy >= H || sx < 0 || sx >= W) continue;
+            const int s = b * C + sy * W + sx;
+            n += en[s] - st[s];
+        }
+    }
+    cnt[t] = n;
+}
+
+// end = start + count, and the key's chunk count
+__global__ void k_pair_bounds(uint32_t nk, const int* __restrict__ pst, int* __restrict__ pen,
+                              int* __restrict__ ccnt) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nk) return;
+    const int len = pen[t];
+    pen[t] = pst[t] + len;
+    ccnt[t] = (len + kCH - 1) / kCH;
+}
+
+// One thread per sorted record i (record g = vals[i], key k = keys[i]): the
+// ranks of g in the 5 x 5 runs around its centre cell, one row of five runs
+// at a time (its own run gives i - st[k]; the others come from interleaved
+// binary searches over the sorted record ids), each row folded at once into
+// its three horizontal 3-sums; a delta's rank is the sum of three of them.
+// pos[g * 9 + d] = the pair's place in the pair order (-1 when the target is
+// off the grid or the record has no key), pair_rec[place] = g.
+__global__ void __launch_bounds__(256)
+k_pair_rank(int n, const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
+            uint32_t nk, int C, int W, int H, const int* __restrict__ st,
+            const int* __restrict__ en, const int* __restrict__ pst,
+            int* __restrict__ pos, int* __restrict__ pair_rec) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t k = keys[i];
+    const uint32_t g = vals[i];
+    int* pg = pos + (size_t)g * kPatch;
+    if (k >= nk) {
+        #pragma unroll
+        for (int d = 0; d < kPatch; ++d) pg[d] = -1;
+        return;
+    }
+    const int b = (int)k / C, cell = (int)k % C, y = cell / W, x = cell % W;
+    int hs[5][3];                  // hs[row][dx + 1]: runs (row, dx - 1 .. dx + 1)
+    #pragma unroll
+    for (int row = 0; row < 5; ++row) {
+        const int sy = y + row - 2;
+        int lo[5], len[5], r[5];
+        #pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            const int sx = x + j - 2;
+            const bool on = (row != 2 || j != 2) && sy >= 0 && sy < H && sx >= 0 && sx < W;
+            const int s = on ? b * C + sy * W + sx : 0;
+            lo[j] = r[j] = on ? st[s] : 0;
+            len[j] = on ? en[s] - lo[j] : 0;
+        }
+        for (;;) {
+            int active = 0;
+            #pragma unroll
+            for (int j = 0; j < 5; ++j) {
+                if (len[j] > 0) {
+                    const int half = len[j] >> 1;
+                    if (vals[lo[j] + half] < g) {
+                        lo[j] += half + 1;
+                        len[j] -= half + 1;
+                    } else {
+                        len[j] = half;
+                    }
+                }
+                active |= len[j];
+            }
+            if (!active) break;
+        }
+        #pragma unroll
+        for (int j = 0; j < 5; ++j) r[j] = lo[j] - r[j];
+        if (row == 2) r[2] = i - st[k];
+        #pragma unroll
+        for (int c = 0; c < 3; ++c) hs[row][c] = r[c] + r[c + 1] + r[c + 2];
+    }
+    #pragma unroll
+    for (int d = 0; d < kPatch; ++d) {
+        const int dy = 1 - d / 3, dx = 1 - d % 3;      // target offset from the centre
+        const int ty = y + dy, tx = x + dx;
+        if (ty < 0 || ty >= H || tx < 0 || tx >= W) {
+            pg[d] = -1;
+            continue;
+        }
+        const int rank = hs[dy + 1][dx + 1] + hs[dy + 2][dx + 1] + hs[dy + 3][dx + 1];
+        const int p = pst[b * C + ty * W + tx] + rank;
+        pg[d] = p;
+        pair_rec[p] = (int)g;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -338,17 +411,7 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 // projection has just left up to 0.7 GB of them in the caches; streaming
 // them past the L2 made pass A 35-40% faster and pass C 2-9%.
 // ---------------------------------------------------------------------------
-constexpr int kCH = 64;
-
 // chunk table of every key: ckey / cbeg / cend, count in *n_chunks
-__global__ void k_chunk_count(uint32_t nk, const int* __restrict__ start,
-                              const int* __restrict__ end, int* __restrict__ cnt) {
-    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-    if (k >= nk) return;
-    const int len = end[k] - start[k];
-    cnt[k] = len > 0 ? (len + kCH - 1) / kCH : 0;
-}
-
 // One thread per chunk slot j < max_chunks: its key is the last k with
 // coff[k] <= j among keys that have chunks (binary search over the
 // exclusive scan of the chunk counts).
@@ -942,9 +1005,10 @@ int ensure_workspace(int E, int nkeys) {
     const int cap = std::max(E, std::max(g_ws.cap, 1024));
     const int ck = std::max(nkeys, g_ws.cap_keys);
     const size_t P = (size_t)cap * kPatch;
-    // temp storage: radix sort of P pairs and the flagged selections.
+    // temp storage: radix sort of the records, the flagged selections and the
+    // key scans.
     size_t t_sort = 0, t_sel = 0;
-    HIPCHK(sort_pairs(nullptr, t_sort, nullptr, nullptr, nullptr, nullptr, (int)P, 32, nullptr));
+    HIPCHK(sort_pairs(nullptr, t_sort, nullptr, nullptr, nullptr, nullptr, cap, 32, nullptr));
     HIPCHK(hipcub::DeviceSelect::Flagged(nullptr, t_sel, hipcub::CountingInputIterator<int>(0),
                                           (unsigned char*)nullptr, (int*)nullptr,
                                           (int*)nullptr, cap));
@@ -981,10 +1045,10 @@ int ensure_workspace(int E, int nkeys) {
         {(void**)&w.owner, (size_t)cap},
         {(void**)&w.pass2, (size_t)cap},
         {(void**)&w.pass3, (size_t)cap},
-        {(void**)&w.ka, sizeof(uint32_t) * P},
-        {(void**)&w.kb, sizeof(uint32_t) * P},
-        {(void**)&w.va, sizeof(uint32_t) * P},
-        {(void**)&w.vb, sizeof(uint32_t) * P},
+        {(void**)&w.ka, sizeof(uint32_t) * (size_t)cap},
+        {(void**)&w.kb, sizeof(uint32_t) * (size_t)cap},
+        {(void**)&w.va, sizeof(uint32_t) * (size_t)cap},
+        {(void**)&w.vb, sizeof(uint32_t) * (size_t)cap},
         {(void**)&w.key3g, sizeof(uint32_t) * (size_t)cap},
         {(void**)&w.prec2, sizeof(int) * P},
         {(void**)&w.prec3, sizeof(int) * P},
@@ -1164,9 +1228,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // run bounds start at zero; k_runs fills them where a key occurs
     {
         FillSet f{};
-        int* arr[kFills] = {w.st2, w.en2, w.pst2, w.pen2, w.st3, w.en3, w.pst3, w.pen3};
-        const int len[kFills] = {(int)nk2, (int)nk2, (int)nk2, (int)nk2, (int)nk3, (int)nk3,
-                                 (int)nk3, (int)nk3};
+        int* arr[kFills] = {w.st2, w.en2, w.st3, w.en3};
+        const int len[kFills] = {(int)nk2, (int)nk2, (int)nk3, (int)nk3};
         for (int i = 0; i < kFills; ++i) {
             f.p[i] = arr[i];
             f.n[i] = len[i];
@@ -1183,20 +1246,19 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        G.C2, w.st2, w.bd, 2, G.window, w.pass2);
     hipLaunchKernelGGL(k_tdrop_commit, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, G.C2,
                        w.st2, w.en2, w.bd, 2);
-    // ---- s2 pair order: (record, delta) pairs sorted by patch cell ----------
-    hipLaunchKernelGGL(k_pairs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.bd, G, 2,
-                       w.cell2, w.pass2, (const int*)nullptr, (const int*)nullptr, w.kb, w.vb);
-    HIPCHK(sort_pairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P, bits2, st));
-    hipLaunchKernelGGL(k_runs, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, nk2, w.pst2, w.pen2);
-    hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P, 256)), dim3(256), 0, st, P, w.ka, w.va, nk2,
-                       w.pos2, w.prec2);
-    // ---- s2 chunk tables and the pass2 record list ------------------------------
-    hipLaunchKernelGGL(k_chunk_count, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, w.pst2,
+    // ---- s2 pair order and chunk tables, from the record order ---------------
+    hipLaunchKernelGGL(k_pair_count, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, G.C2, G.W2,
+                       G.H2, w.st2, w.en2, w.pen2);
+    HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.pen2, w.pst2, (int)nk2, st));
+    hipLaunchKernelGGL(k_pair_bounds, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, w.pst2,
                        w.pen2, w.ccnt2);
+    hipLaunchKernelGGL(k_pair_rank, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, w.vb, nk2,
+                       G.C2, G.W2, G.H2, w.st2, w.en2, w.pst2, w.pos2, w.prec2);
     HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt2, w.coff2, (int)nk2, st));
     hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(w.max_chunks, 256)), dim3(256), 0, st, nk2,
                        w.max_chunks, w.pst2,
                        w.pen2, w.ccnt2, w.coff2, w.ckey2, w.cbeg2, w.cend2, w.counts + 2);
+    // the pass2 record list
     HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
                                           w.pass2, w.list2, w.counts + 0, E, st));
     // The s3 ordering needs only pass2 and the centre cells, so it runs on the
@@ -1277,19 +1339,16 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                                w.en3, w.vb, w.pass3, w.owner, w.last3, w.cnt3);
         HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
                                               w.pass3, w.list3, w.counts + 1, E, s3));
-        // ---- s3 pair order ----------------------------------------------------------
-        const int P3 = N2 * kPatch;
-        if (P3 > 0) {
-            hipLaunchKernelGGL(k_pairs, dim3(grid1(N2, 256)), dim3(256), 0, s3, E, w.bd, G, 3,
-                               w.cell2, w.pass2, (const int*)(w.counts + 0), w.list2, w.kb, w.vb);
-            HIPCHK(sort_pairs(w.temp, tb, w.kb, w.ka, w.vb, w.va, P3, bits3, s3));
-            hipLaunchKernelGGL(k_runs, dim3(grid1(P3, 256)), dim3(256), 0, s3, P3, w.ka, nk3,
-                               w.pst3, w.pen3);
-            hipLaunchKernelGGL(k_pair_pos, dim3(grid1(P3, 256)), dim3(256), 0, s3, P3, w.ka, w.va,
-                               nk3, w.pos3, w.prec3);
-        }
-        hipLaunchKernelGGL(k_chunk_count, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, w.pst3,
+        // ---- s3 pair order and chunk tables, from the s3 record order --------------
+        hipLaunchKernelGGL(k_pair_count, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, G.C3,
+                           G.W3, G.H3, w.st3, w.en3, w.pen3);
+        HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.pen3, w.pst3, (int)nk3, s3));
+        hipLaunchKernelGGL(k_pair_bounds, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, w.pst3,
                            w.pen3, w.ccnt3);
+        if (N2 > 0)
+            hipLaunchKernelGGL(k_pair_rank, dim3(grid1(N2, 256)), dim3(256), 0, s3, N2, w.kb,
+                               w.vb, nk3, G.C3, G.W3, G.H3, w.st3, w.en3, w.pst3, w.pos3,
+                               w.prec3);
         HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt3, w.coff3, (int)nk3, s3));
         hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(w.max_chunks, 256)), dim3(256), 0, s3, nk3,
                            w.max_chunks, w.pst3,
