@@ -219,22 +219,51 @@ __global__ void k_pair_bounds(uint32_t nk, const int* __restrict__ pst, int* __r
     ccnt[t] = (len + kCH - 1) / kCH;
 }
 
+// Lower bound of g in vals[lo, lo + len): the index of the first value >= g.
+__device__ __forceinline__ int lower_bound_u32(const uint32_t* __restrict__ vals, int lo, int len,
+                                               uint32_t g) {
+    while (len > 0) {
+        const int half = len >> 1;
+        if (vals[lo + half] < g) {
+            lo += half + 1;
+            len -= half + 1;
+        } else {
+            len = half;
+        }
+    }
+    return lo;
+}
+
+constexpr int kRankWindow = 256;   // widest neighbour window searched cooperatively
+
 // One thread per sorted record i (record g = vals[i], key k = keys[i]): the
-// ranks of g in the 5 x 5 runs around its centre cell, one row of five runs
-// at a time (its own run gives i - st[k]; the others come from interleaved
-// binary searches over the sorted record ids), each row folded at once into
-// its three horizontal 3-sums; a delta's rank is the sum of three of them.
-// pos[g * 9 + d] = the pair's place in the pair order (-1 when the target is
-// off the grid or the record has no key), pair_rec[place] = g.
+// ranks of g in the 5 x 5 runs around its centre cell (its own run gives
+// i - st[k]), folded row by row into three horizontal 3-sums; a delta's rank
+// is the sum of three of them.  pos[g * 9 + d] = the pair's place in the pair
+// order (-1 when the target is off the grid or the record has no key),
+// pair_rec[place] = g.
+//
+// A wave whose 64 records share one centre cell (the usual case: records are
+// sorted by cell) ranks them together.  Its lanes' ids increase, so in each
+// neighbour run every lane's lower bound lies between those of the first and
+// the last lane: 48 lanes find these 2 x 24 bounds by binary search at once,
+// then the wave loads the window between them 64 values at a time and each
+// lane counts the values below its id by a six-step search across the lanes
+// (ds_bpermute).  A window wider than kRankWindow is searched per lane inside
+// its bounds.  Other waves (cell boundaries, the tail) search per lane.
 __global__ void __launch_bounds__(256)
 k_pair_rank(int n, const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
             uint32_t nk, int C, int W, int H, const int* __restrict__ st,
             const int* __restrict__ en, const int* __restrict__ pst,
             int* __restrict__ pos, int* __restrict__ pair_rec) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const uint32_t k = keys[i];
-    const uint32_t g = vals[i];
+    const int lane = threadIdx.x & 63;
+    const bool valid = i < n;
+    const uint32_t k = valid ? keys[i] : nk;
+    const uint32_t g = valid ? vals[i] : 0u;
+    const uint32_t k0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)k);
+    const bool together = __all(valid && k == k0 && k < nk);
+    if (!valid) return;
     int* pg = pos + (size_t)g * kPatch;
     if (k >= nk) {
         #pragma unroll
@@ -242,41 +271,94 @@ k_pair_rank(int n, const uint32_t* __restrict__ keys, const uint32_t* __restrict
         return;
     }
     const int b = (int)k / C, cell = (int)k % C, y = cell / W, x = cell % W;
+    const int own = i - st[k];
     int hs[5][3];                  // hs[row][dx + 1]: runs (row, dx - 1 .. dx + 1)
-    #pragma unroll
-    for (int row = 0; row < 5; ++row) {
-        const int sy = y + row - 2;
-        int lo[5], len[5], r[5];
-        #pragma unroll
-        for (int j = 0; j < 5; ++j) {
-            const int sx = x + j - 2;
-            const bool on = (row != 2 || j != 2) && sy >= 0 && sy < H && sx >= 0 && sx < W;
-            const int s = on ? b * C + sy * W + sx : 0;
-            lo[j] = r[j] = on ? st[s] : 0;
-            len[j] = on ? en[s] - lo[j] : 0;
+    if (together) {
+        // lanes c and 32 + c (c < 25): run c's bounds for the first and last id
+        const uint32_t g_first = (uint32_t)__builtin_amdgcn_readlane((int)g, 0);
+        const uint32_t g_last = (uint32_t)__builtin_amdgcn_readlane((int)g, 63);
+        int bnd = 0, s0 = 0;
+        {
+            const int c = lane & 31;
+            const int sy = y + c / 5 - 2, sx = x + c % 5 - 2;
+            if (c < 25 && c != 12 && sy >= 0 && sy < H && sx >= 0 && sx < W) {
+                const int s = b * C + sy * W + sx;
+                s0 = st[s];
+                bnd = lower_bound_u32(vals, s0, en[s] - s0, lane < 32 ? g_first : g_last);
+            }
         }
-        for (;;) {
-            int active = 0;
+        #pragma unroll
+        for (int row = 0; row < 5; ++row) {
+            int r[5];
             #pragma unroll
             for (int j = 0; j < 5; ++j) {
-                if (len[j] > 0) {
-                    const int half = len[j] >> 1;
-                    if (vals[lo[j] + half] < g) {
-                        lo[j] += half + 1;
-                        len[j] -= half + 1;
-                    } else {
-                        len[j] = half;
+                const int c = row * 5 + j;
+                if (c == 12) {
+                    r[j] = own;
+                    continue;
+                }
+                const int wa = __builtin_amdgcn_readlane(bnd, c);
+                const int we = __builtin_amdgcn_readlane(bnd, 32 + c);
+                const int ws = __builtin_amdgcn_readlane(s0, c);
+                int cnt = 0;
+                if (we - wa > kRankWindow) {
+                    cnt = lower_bound_u32(vals, wa, we - wa, g) - wa;
+                } else {
+                    for (int base = wa; base < we; base += 64) {
+                        const uint32_t v = base + lane < we ? vals[base + lane] : 0xffffffffu;
+                        int lo = 0;
+                        #pragma unroll
+                        for (int step = 32; step > 0; step >>= 1) {
+                            const uint32_t p = (uint32_t)__builtin_amdgcn_ds_bpermute(
+                                (lo + step - 1) << 2, (int)v);
+                            if (p < g) lo += step;
+                        }
+                        const uint32_t p = (uint32_t)__builtin_amdgcn_ds_bpermute(lo << 2, (int)v);
+                        cnt += lo + (p < g ? 1 : 0);
                     }
                 }
-                active |= len[j];
+                r[j] = wa - ws + cnt;
             }
-            if (!active) break;
+            #pragma unroll
+            for (int c = 0; c < 3; ++c) hs[row][c] = r[c] + r[c + 1] + r[c + 2];
         }
+    } else {
         #pragma unroll
-        for (int j = 0; j < 5; ++j) r[j] = lo[j] - r[j];
-        if (row == 2) r[2] = i - st[k];
-        #pragma unroll
-        for (int c = 0; c < 3; ++c) hs[row][c] = r[c] + r[c + 1] + r[c + 2];
+        for (int row = 0; row < 5; ++row) {
+            const int sy = y + row - 2;
+            int lo[5], len[5], r[5];
+            #pragma unroll
+            for (int j = 0; j < 5; ++j) {
+                const int sx = x + j - 2;
+                const bool on = (row != 2 || j != 2) && sy >= 0 && sy < H && sx >= 0 && sx < W;
+                const int s = on ? b * C + sy * W + sx : 0;
+                lo[j] = r[j] = on ? st[s] : 0;
+                len[j] = on ? en[s] - lo[j] : 0;
+            }
+            // one step of each of the five searches per pass
+            for (;;) {
+                int active = 0;
+                #pragma unroll
+                for (int j = 0; j < 5; ++j) {
+                    if (len[j] > 0) {
+                        const int half = len[j] >> 1;
+                        if (vals[lo[j] + half] < g) {
+                            lo[j] += half + 1;
+                            len[j] -= half + 1;
+                        } else {
+                            len[j] = half;
+                        }
+                    }
+                    active |= len[j];
+                }
+                if (!active) break;
+            }
+            #pragma unroll
+            for (int j = 0; j < 5; ++j) r[j] = lo[j] - r[j];
+            if (row == 2) r[2] = own;
+            #pragma unroll
+            for (int c = 0; c < 3; ++c) hs[row][c] = r[c] + r[c + 1] + r[c + 2];
+        }
     }
     #pragma unroll
     for (int d = 0; d < kPatch; ++d) {
