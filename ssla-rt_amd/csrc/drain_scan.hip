@@ -1066,12 +1066,26 @@ size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 // Stable LSD radix sort of (key, value) pairs on bits [0, bits).  rocPRIM's
 // default configuration sorts up to 1 M pairs of 32-bit keys by block sort
 // plus a merge pass per doubling (16 launches at 200 k records); the
-// Onesweep path needs one launch per 8 key bits plus a histogram.
+// Onesweep path needs one launch per 8 key bits plus a histogram.  Its
+// default tiles (1024 threads x 16 keys) give a 200 k-record sort 13
+// workgroups; below 1 M records 512 x 8 tiles spread it over more CUs
+// (80x64 ordering 0.198 -> 0.167 ms; at 3.2 M records the default was
+// faster).
 using SortConfig = rocprim::radix_sort_config<rocprim::default_config, rocprim::default_config,
                                               rocprim::default_config, 0>;
+using SortConfigSmall = rocprim::radix_sort_config<
+    rocprim::default_config, rocprim::default_config,
+    rocprim::radix_sort_onesweep_config<rocprim::kernel_config<512, 8>,
+                                        rocprim::kernel_config<512, 8>, 8,
+                                        rocprim::block_radix_rank_algorithm::match>,
+    0>;
+constexpr int kSmallSort = 1 << 20;
 
 hipError_t sort_pairs(void* temp, size_t& bytes, const uint32_t* ki, uint32_t* ko,
                       const uint32_t* vi, uint32_t* vo, int n, int bits, hipStream_t st) {
+    if (n < kSmallSort)
+        return rocprim::radix_sort_pairs<SortConfigSmall>(temp, bytes, ki, ko, vi, vo, (size_t)n,
+                                                          0u, (unsigned)bits, st);
     return rocprim::radix_sort_pairs<SortConfig>(temp, bytes, ki, ko, vi, vo, (size_t)n, 0u,
                                                  (unsigned)bits, st);
 }
@@ -1091,6 +1105,12 @@ int ensure_workspace(int E, int nkeys) {
     // key scans.
     size_t t_sort = 0, t_sel = 0;
     HIPCHK(sort_pairs(nullptr, t_sort, nullptr, nullptr, nullptr, nullptr, cap, 32, nullptr));
+    {
+        size_t t_small = 0;         // the small-sort tiles below the size switch
+        HIPCHK(sort_pairs(nullptr, t_small, nullptr, nullptr, nullptr, nullptr,
+                          std::min(cap, kSmallSort - 1), 32, nullptr));
+        t_sort = std::max(t_sort, t_small);
+    }
     HIPCHK(hipcub::DeviceSelect::Flagged(nullptr, t_sel, hipcub::CountingInputIterator<int>(0),
                                           (unsigned char*)nullptr, (int*)nullptr,
                                           (int*)nullptr, cap));
