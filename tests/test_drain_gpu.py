@@ -319,6 +319,25 @@ def test_edge_cases(H, stub_dir, stub_npz):
         p2, p3, feat, _ = st.run(r.x, r.y, r.feat1)
         assert np.all(out["pass2"][p2 == -2] == -2)
         compare(out, p2, p3, feat, "off-grid")
+        d.reset()
+        # 128 records on cell (10, 8) among 800 on each of its 8 neighbours,
+        # shuffled in time: the pair order then interleaves nine dense runs,
+        # and 64 consecutive centre records span ~400 records of each
+        # neighbour run
+        say("sparse cell inside a dense ring (wide neighbour windows)")
+        rng = np.random.default_rng(5)
+        ox = np.array([-1, 0, 1, -1, 1, -1, 0, 1])
+        oy = np.array([-1, -1, -1, 0, 0, 1, 1, 1])
+        cx = np.r_[np.full(128, 10), np.repeat(10 + ox, 800)]
+        cy = np.r_[np.full(128, 8), np.repeat(8 + oy, 800)]
+        perm = rng.permutation(cx.size)
+        ring = events.Records(np.zeros(cx.size, np.float32), cx[perm].astype(np.uint16),
+                              cy[perm].astype(np.uint16),
+                              rng.normal(0, 0.5, (cx.size, 24)).astype(np.float32))
+        (out,), _ = d.drain([events.to_records(ring)])
+        st = O.S2S3(layers, 16, 20, 4)
+        p2, p3, feat, _ = st.run(ring.x, ring.y, ring.feat1)
+        compare(out, p2, p3, feat, "dense ring")
 
 
 def test_window_one_passes_everything(H):
