@@ -183,6 +183,24 @@ int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg,
                         HybridS2S3OutputSlot* const* outs,
                         const SslaHipDrainOpts* opts);
 
+/* The whole-ring drain keeps one workspace per process (device memory
+ * sized for the largest call so far; about 4 KB per record).  A call with
+ * more records than it holds regrows it, which waits for the previous
+ * drain call to finish and frees and allocates device memory.  Call this
+ * once up front -- in particular before ssla_hip_persistent_start, while no
+ * other kernel of the caller's runs -- to size it for calls of up to
+ * max_records records in total over cfg's blocks and grid.  No counterpart
+ * in the reference (its drain kernel works in shared memory only).
+ *
+ * The drain also keeps fragment-order copies of the layer weights
+ * (reordered for the matrix cores).  They are rebuilt when a layer weight
+ * pointer of cfg changes, or after any call of this library that may write
+ * device memory (ssla_hip_memcpy, _memset, _free_device, _model_load,
+ * _model_free).  A caller that rewrites weight memory in place by other
+ * means calls ssla_hip_memset(p, 0, 0) (it writes nothing) before the next
+ * drain. */
+int ssla_hip_drain_reserve(const HybridS2S3Config* cfg, int max_records);
+
 /* Ticks per millisecond of the constant-rate GPU clock used by batch_clks
  * and GpuTimingSlot (s_memrealtime). */
 int ssla_hip_wall_clock_khz(int* out);
@@ -330,14 +348,6 @@ typedef struct SslaHipOevaDiff {
  * differs (comparison stops there); NaN deltas are passed over. */
 int ssla_hip_oeva_diff(const char* path_a, const char* path_b, double tol_abs,
                        SslaHipOevaDiff* out);
-
-/* ---- measured HBM ceilings (no counterpart in the reference) ----------
- * Times three traffic patterns on the current device and writes GB/s into
- * gbs[0..2]: streaming 16-byte writes over 1 GiB; a streaming copy (read and
- * write bytes counted); 576-byte rows written as MFMA-tile column segments at
- * a random permutation of 1.8 M row positions.  Allocates and frees 2 GiB.
- * Used by bench.py to state what a write-dominated kernel can reach. */
-int ssla_hip_hbm_ceiling(double* gbs, int n);
 
 #ifdef __cplusplus
 }

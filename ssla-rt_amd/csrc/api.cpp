@@ -223,6 +223,7 @@ int ssla_hip_malloc_host(size_t nbytes, void** out) {
 }
 
 int ssla_hip_free_device(void* p) {
+    weights_touched();
     if (p) API_HIP(hipFree(p));
     return SSLA_OK;
 }
@@ -233,6 +234,7 @@ int ssla_hip_free_host(void* p) {
 }
 
 int ssla_hip_memcpy(void* dst, const void* src, size_t nbytes) {
+    weights_touched();
     if (!nbytes) return SSLA_OK;
     if (!dst || !src) { set_error("null pointer"); return SSLA_ERR_ARG; }
     API_HIP(hipMemcpy(dst, src, nbytes, hipMemcpyDefault));
@@ -240,6 +242,7 @@ int ssla_hip_memcpy(void* dst, const void* src, size_t nbytes) {
 }
 
 int ssla_hip_memset(void* dst, int value, size_t nbytes) {
+    weights_touched();
     if (!nbytes) return SSLA_OK;
     if (!dst) { set_error("null pointer"); return SSLA_ERR_ARG; }
     API_HIP(hipMemsetAsync(dst, value, nbytes, nullptr));
@@ -312,6 +315,7 @@ int ssla_hip_meta_read(const char* dir, int* out) {
 
 int ssla_hip_model_load(const char* dir, SslaHipModel** out) {
     if (!dir || !out) { set_error("null argument"); return SSLA_ERR_ARG; }
+    weights_touched();
     *out = nullptr;
     ModelMeta meta;
     std::map<std::string, NpzTensor> W;
@@ -440,6 +444,7 @@ int ssla_hip_model_info(const SslaHipModel* m, SslaHipModelInfo* out) {
 
 void ssla_hip_model_free(SslaHipModel* m) {
     if (!m) return;
+    weights_touched();
     if (m->dev) (void)hipFree(m->dev);
     delete m;
 }
@@ -617,6 +622,10 @@ int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg, const HybridInputRec* const
     }
     if (bph) { set_error("batch_phase_us is only measured by the batch-mode drain"); return SSLA_ERR_ARG; }
     return scan_drain(cfg, rings, ns, outs, opts ? opts->head_outs : nullptr, st, sync, phase_ms);
+}
+
+int ssla_hip_drain_reserve(const HybridS2S3Config* cfg, int max_records) {
+    return drain_reserve(cfg, max_records);
 }
 
 int ssla_hip_drain_n(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,

@@ -22,4 +22,13 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                float* const* head_outs, hipStream_t st, bool sync,
                float* phase_ms);
 
+// Sizes the whole-ring workspace for calls of up to max_records records over
+// cfg's blocks and grid (ssla_hip_drain_reserve).
+int drain_reserve(const HybridS2S3Config* cfg, int max_records);
+
+// Marks the layer weights as possibly rewritten: the next drain rebuilds its
+// fragment-order copy.  Called by every ABI entry point that may write device
+// memory.
+void weights_touched();
+
 }  // namespace ssla

@@ -36,6 +36,7 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -1044,9 +1045,15 @@ struct Workspace {
     hipEvent_t s3_ordered = nullptr;   // s3 tables and pass3 are complete
     hipEvent_t n2_ready = nullptr;     // the pass2 count has reached n2_host
     int* n2_host = nullptr;            // pinned copy of the pass2 count
+    hipEvent_t side_done = nullptr;    // the side stream's last work of a call
     void* temp;
     size_t temp_bytes;
     float* packed = nullptr;           // fragment-order weight copies (packed_weight_floats_d)
+    // What `packed` was built from: the layer weight pointers and the weight
+    // generation (bumped by every library call that may write device memory).
+    PackSrc packed_src = {};
+    unsigned long long packed_gen = ~0ull;
+    PackedWeights pk = {};
 };
 
 std::mutex g_ws_mu;
@@ -1093,7 +1100,9 @@ hipError_t sort_pairs(void* temp, size_t& bytes, const uint32_t* ki, uint32_t* k
 int ensure_workspace(int E, int nkeys) {
     if (E <= g_ws.cap && nkeys <= g_ws.cap_keys) return SSLA_OK;
     if (g_ws.base) {
-        HIPCHK(hipDeviceSynchronize());
+        // the last drain's kernels (both streams, joined into `done`) are the
+        // only users of the old workspace
+        HIPCHK(hipEventSynchronize(g_ws.done));
         HIPCHK(hipFree(g_ws.base));
         g_ws.base = nullptr;
         g_ws.cap = 0;
@@ -1187,6 +1196,7 @@ int ensure_workspace(int E, int nkeys) {
         HIPCHK(hipEventCreateWithFlags(&w.s2_ordered, hipEventDisableTiming));
         HIPCHK(hipEventCreateWithFlags(&w.s3_ordered, hipEventDisableTiming));
         HIPCHK(hipEventCreateWithFlags(&w.n2_ready, hipEventDisableTiming));
+        HIPCHK(hipEventCreateWithFlags(&w.side_done, hipEventDisableTiming));
         HIPCHK(hipHostMalloc((void**)&w.n2_host, sizeof(int), hipHostMallocDefault));
         HIPCHK(hipStreamCreateWithFlags(&w.side, hipStreamNonBlocking));
         HIPCHK(hipMalloc(&w.packed, sizeof(float) * packed_weight_floats_d()));
@@ -1208,7 +1218,39 @@ int bits_for(uint32_t v) {
 
 inline unsigned grid1(long long n, int bs) { return (unsigned)((n + bs - 1) / bs); }
 
+// Every return of a call after its first launch passes through finish():
+// the side stream's work joins `st`, and `done` marks the end of the call's
+// use of the workspace, so the next call (on any stream) and a workspace
+// regrowth wait for all of it -- also when the call stops at an error.
+struct CallEnd {
+    Workspace& w;
+    hipStream_t st;
+    bool ended = false;
+    void finish() {
+        if (ended) return;
+        ended = true;
+        (void)hipEventRecord(w.side_done, w.side);
+        (void)hipStreamWaitEvent(st, w.side_done, 0);
+        (void)hipEventRecord(w.done, st);
+    }
+    ~CallEnd() { finish(); }
+};
+
+std::atomic<unsigned long long> g_weights_gen{0};
+
 }  // namespace
+
+void weights_touched() { g_weights_gen.fetch_add(1, std::memory_order_relaxed); }
+
+int drain_reserve(const HybridS2S3Config* cfg, int max_records) {
+    if (!cfg || cfg->n_blocks < 1 || cfg->n_blocks > SSLA_MAX_BLOCKS || cfg->H2 <= 0 ||
+        cfg->W2 <= 0 || max_records < 0 || (long long)max_records * kPatch > 0x7fffffffLL) {
+        set_error("drain_reserve: bad configuration or record count");
+        return SSLA_ERR_ARG;
+    }
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    return ensure_workspace(std::max(max_records, 1), cfg->n_blocks * cfg->H2 * cfg->W2 + 1);
+}
 
 int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                const int* ns, HybridS2S3OutputSlot* const* outs,
@@ -1277,6 +1319,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
         if (rc) return rc;
     }
     Workspace& w = g_ws;
+    CallEnd end{w, st};
 
     BlockDesc hbd[SSLA_MAX_BLOCKS] = {};
     int off = 0;
@@ -1308,10 +1351,16 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     HIPCHK(hipMemcpyAsync(w.bd, w.bd_host, sizeof(hbd), hipMemcpyHostToDevice, st));
     HIPCHK(hipEventRecord(w.bd_copied, st));
 
-    const int P = E * kPatch;
     // Phase timing: events recorded on `st` between phases (optional).
     hipEvent_t ev[SSLA_DRAIN_PHASES + 1] = {};
     int n_ev = 0;
+    struct EvFree {
+        hipEvent_t* ev;
+        int& n;
+        ~EvFree() {
+            for (int k = 0; k < n; ++k) (void)hipEventDestroy(ev[k]);
+        }
+    } ev_free{ev, n_ev};
     auto mark = [&]() -> int {
         if (!phase_ms) return SSLA_OK;
         if (!ev[n_ev]) HIPCHK(hipEventCreate(&ev[n_ev]));
@@ -1320,9 +1369,24 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
         return SSLA_OK;
     };
 #define MARK() do { const int rc_ = mark(); if (rc_) return rc_; } while (0)
-    // fragment-order copies of the layer weights for the MFMA kernels
-    PackedWeights pk;
-    HIPCHK(pack_weights_d(cfg->layers[0], w.packed, &pk, st));
+    // fragment-order copies of the layer weights for the MFMA kernels, rebuilt
+    // when a weight pointer or the weight generation has changed
+    {
+        PackSrc src{};
+        for (int i = 0; i < 4; ++i) {
+            src.qvgIn[i] = cfg->layers[0][i].qvgIn;
+            src.goW[i] = cfg->layers[0][i].goW;
+            src.ip[i] = cfg->layers[0][i].input_proj;
+        }
+        const unsigned long long gen = g_weights_gen.load(std::memory_order_relaxed);
+        if (gen != w.packed_gen || std::memcmp(&src, &w.packed_src, sizeof src) != 0) {
+            w.packed_gen = ~0ull;
+            HIPCHK(pack_weights_d(cfg->layers[0], w.packed, &w.pk, st));
+            w.packed_src = src;
+            w.packed_gen = gen;
+        }
+    }
+    const PackedWeights& pk = w.pk;
     MARK();
     const int bits2 = bits_for(nk2), bits3 = bits_for(nk3);
     size_t tb = w.temp_bytes;
@@ -1512,7 +1576,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     HIPCHK(hipGetLastError());
     MARK();
 #undef MARK
-    HIPCHK(hipEventRecord(w.done, st));
+    end.finish();
     if (sync) HIPCHK(hipStreamSynchronize(st));
     if (phase_ms) {
         for (int k = 0; k + 1 < n_ev && k < SSLA_DRAIN_PHASES; ++k) {
@@ -1520,7 +1584,6 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
             HIPCHK(hipEventElapsedTime(&ms, ev[k], ev[k + 1]));
             phase_ms[k] += ms;
         }
-        for (int k = 0; k < n_ev; ++k) (void)hipEventDestroy(ev[k]);
     }
     return SSLA_OK;
 }

@@ -9,7 +9,10 @@
 //      1.8 M positions, each row written as 16-float segments the way an
 //      MFMA 16x16 output tile leaves a wave (lane l: row 4*(l/16)+r,
 //      column l%16).
-// No counterpart in the reference; used by bench.py only.
+// No counterpart in the reference.  Built as libssla_probe.so, apart from the
+// drain library, and loaded by bench.py only.  Entry point:
+//   int ssla_probe_hbm_ceiling(double* gbs, int n)   0, or -1 (n < 3) /
+//       -2 (HIP failure; ssla_probe_last_error() names the call)
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -19,13 +22,9 @@
 #include <string>
 #include <vector>
 
-#include "ssla_hip.h"
-
-namespace ssla {
-void set_error(const std::string& msg);
-}  // namespace ssla
-
 namespace {
+
+std::string g_err;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
@@ -58,20 +57,22 @@ __global__ void k_probe_rows(float* __restrict__ out, const int* __restrict__ pe
     do {                                                                      \
         hipError_t e_ = (call);                                               \
         if (e_ != hipSuccess) {                                               \
-            ssla::set_error(std::string(#call) + ": " + hipGetErrorString(e_)); \
-            rc = SSLA_ERR_HIP;                                                \
+            g_err = std::string(#call) + ": " + hipGetErrorString(e_);       \
+            rc = -2;                                                          \
             goto done;                                                        \
         }                                                                     \
     } while (0)
 
 }  // namespace
 
-extern "C" int ssla_hip_hbm_ceiling(double* gbs, int n) {
+extern "C" const char* ssla_probe_last_error(void) { return g_err.c_str(); }
+
+extern "C" int ssla_probe_hbm_ceiling(double* gbs, int n) {
     if (!gbs || n < 3) {
-        ssla::set_error("hbm_ceiling: need 3 slots");
-        return SSLA_ERR_ARG;
+        g_err = "hbm_ceiling: need 3 slots";
+        return -1;
     }
-    int rc = SSLA_OK;
+    int rc = 0;
     const size_t bytes = 1ull << 30;
     const int nrows = 1800000;           // 1.8 M x 576 B = 1.04 GB < 1 GiB buffer
     f4 *a = nullptr, *b = nullptr;

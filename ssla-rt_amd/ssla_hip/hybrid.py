@@ -300,6 +300,15 @@ class Drain:
         lib.check(lib.load().ssla_hip_drain_n_ex(ctypes.byref(self.cfg), rings, ns, outs,
                                                  ctypes.byref(opts)), "drain_n_ex")
 
+    def run_two_rings(self) -> None:
+        """ssla_hip_drain_n2 over the two loaded rings (the reference's P1
+        two-ring entry, orin/bench_s2_s3_head_celled.py:234-244)."""
+        if self.cfg.n_blocks != 2 or len(self._rings) != 2:
+            raise ValueError("run_two_rings needs two blocks and two loaded rings")
+        lib.check(lib.load().ssla_hip_drain_n2(
+            ctypes.byref(self.cfg), self._rings[0].ptr, self._rings[1].ptr, self._ns[0],
+            self._ns[1], self._outs[0].ptr, self._outs[1].ptr), "drain_n2")
+
     def results(self):
         outs, heads = [], []
         for b in range(self.cfg.n_blocks):

@@ -52,6 +52,7 @@ _SIGNATURES = {
     "ssla_hip_drain_n_ex": (_I, [ctypes.POINTER(abi.HybridS2S3Config), ctypes.POINTER(_VP),
                                  ctypes.POINTER(_I), ctypes.POINTER(_VP),
                                  ctypes.POINTER(abi.SslaHipDrainOpts)]),
+    "ssla_hip_drain_reserve": (_I, [ctypes.POINTER(abi.HybridS2S3Config), _I]),
     "ssla_hip_wall_clock_khz": (_I, [ctypes.POINTER(_I)]),
     "ssla_hip_timing_alloc": (_I, [ctypes.POINTER(abi.HybridS2S3Config), _I, ctypes.c_uint]),
     "ssla_hip_timing_free": (None, [ctypes.POINTER(abi.HybridS2S3Config), _I]),
@@ -74,7 +75,6 @@ _SIGNATURES = {
                                 ctypes.c_uint]),
     "ssla_hip_oeva_diff": (_I, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_double,
                                 ctypes.POINTER(abi.SslaHipOevaDiff)]),
-    "ssla_hip_hbm_ceiling": (_I, [ctypes.POINTER(ctypes.c_double), _I]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

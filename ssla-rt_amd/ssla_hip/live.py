@@ -15,7 +15,7 @@ from __future__ import annotations
 
 import time
 from dataclasses import dataclass, field
-from typing import Dict, Optional
+from typing import Callable, Dict, Optional
 
 import numpy as np
 
@@ -100,14 +100,18 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
              n_blobs: int = 8, sigma_px: float = 3.0, bg_frac: float = 0.1,
              ring_capacity: int = 1 << 16, timing_capacity: int = 1 << 22, max_batch: int = 32,
              spin_ns: int = 200, profile: bool = True, drain_timeout_s: float = 30.0,
-             back_pressure: bool = False) -> LiveResult:
+             back_pressure: bool = False,
+             inspect: Optional[Callable] = None) -> LiveResult:
     """One live run on one GPU.  back_pressure makes the producer wait for
     each ring's tail instead of overwriting unread slots.  gpu_blocks (1, 2, 4, 8, 16; the reference's
     default is 8) splits the s2 grid into owned strips with a 2-cell halo
     (topology.grid_topology); each strip has its own ring, hidden state and
     prediction grid and is drained by its own workgroup.  Halo records are
     published to every strip whose processed window holds them; latency
-    covers the records that produce a prediction (owner, pass2, pass3)."""
+    covers the records that produce a prediction (owner, pass2, pass3).
+    inspect(drain, rings, heads, topo), when given, is called once the kernel
+    has stopped and before any buffer is freed (heads: records published per
+    ring), e.g. to check the rings' contents and the final state."""
     if base_core is None or synth_core is None:
         sc, bc = pick_cores(n_shards)
         synth_core = sc if synth_core is None else synth_core
@@ -165,6 +169,8 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
         phase = live.phase_us
         live = None
         prod_stats = prod.stats()
+        if inspect is not None:
+            inspect(drain, rings, heads, topo)
         cols = {k: [] for k in ("e2d", "e2p", "p2d", "kern", "own", "ok")}
         for b in range(nb):
             # per-block two-point calibration of the GPU clock
@@ -229,7 +235,8 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
                timing_capacity: int = 1 << 18, max_batch: int = 32, spin_ns: int = 200,
                pin_core: Optional[int] = None, profile: bool = True, expect_p3=None,
                drain_timeout_s: float = 60.0, strips=None,
-               speed: Optional[float] = None) -> ReplayResult:
+               speed: Optional[float] = None,
+               inspect: Optional[Callable] = None) -> ReplayResult:
     """Several rings live on one GPU: pre-built ring records (one array per
     ring) replayed into one ring each, one persistent workgroup per ring.
     Independent streams: rate_per_stream records/s each, round-robin.  One
@@ -238,7 +245,9 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
     the records' own times, (t - t_first) / speed us after the start.
     Latency is push -> prediction (records are published at their emit
     time).  expect_p3 (optional, one flag array per ring) gives each ring's
-    drop drift: records whose timing-slot owner flag differs from it."""
+    drop drift: records whose timing-slot owner flag differs from it.
+    inspect(drain), when given, is called once the kernel has stopped and
+    before the state is freed."""
     from .producer import Replay
     nb = len(streams)
     if pin_core is None:
@@ -280,6 +289,8 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
         status = live.wait()
         phase = live.phase_us
         live = None
+        if inspect is not None:
+            inspect(drain)
         ns_per_tick = (t1_cpu - t0_cpu) / max(1, (k1 - k0)) if k1 else 10.0
         out = []
         for b in range(nb):

@@ -58,6 +58,25 @@ def test_errors_do_not_cross_the_boundary():
     assert not m.value
 
 
+def test_two_ring_drain_and_reserve_reject_bad_arguments():
+    """ssla_hip_drain_n2 is the two-ring form: any other block count is an
+    argument error, reported before any device work (no GPU needed)."""
+    L = lib.load()
+    cfg = abi.HybridS2S3Config()
+    cfg.H2, cfg.W2, cfg.H3, cfg.W3 = 16, 20, 8, 10
+    for nb in (0, 1, 3, 16):
+        cfg.n_blocks = nb
+        rc = L.ssla_hip_drain_n2(ctypes.byref(cfg), None, None, 0, 0, None, None)
+        assert rc == abi.SSLA_ERR_ARG, nb
+        assert b"n_blocks == 2" in L.ssla_hip_last_error()
+    assert L.ssla_hip_drain_n2(None, None, None, 0, 0, None, None) == abi.SSLA_ERR_ARG
+    cfg.n_blocks = 1
+    assert L.ssla_hip_drain_reserve(ctypes.byref(cfg), -1) == abi.SSLA_ERR_ARG
+    cfg.n_blocks = 17
+    assert L.ssla_hip_drain_reserve(ctypes.byref(cfg), 10) == abi.SSLA_ERR_ARG
+    assert L.ssla_hip_drain_reserve(None, 10) == abi.SSLA_ERR_ARG
+
+
 def test_constants_match_the_header():
     """Return codes, phase counts and prediction constants of ssla_hip.h
     against the Python mirror."""

@@ -118,6 +118,20 @@ def test_p1_two_blocks_halo_split(H):
         g2 = sum(int((o["pass2"] == 1).sum()) for o in outs)
         g3 = sum(int((o["pass3"] == 1).sum()) for o in outs)
         say(f"owned pass counts {g2} / {g3}; single domain {int((d2 == 1).sum())} / {int((d3 == 1).sum())}")
+        state_n = [[d.hidden(b, li) for li in range(4)] + list(d.counters(b)) for b in range(2)]
+    # The reference's two-ring entry (ssla_hip_drain_n2) on a fresh instance
+    # with the same rings and initial state: the same kernels, so outputs,
+    # hidden state and counters equal drain_n's bit for bit.
+    w2, d2n, _ = p1_setup(H, n, n_blocks=2, strips=strips)
+    with d2n:
+        d2n.load_rings(recs)
+        d2n.run_two_rings()
+        outs2, _ = d2n.results()
+        for b in range(2):
+            assert np.array_equal(outs2[b], outs[b]), b
+            got = [d2n.hidden(b, li) for li in range(4)] + list(d2n.counters(b))
+            assert all(np.array_equal(a, e) for a, e in zip(got, state_n[b])), b
+        say("drain_n2: identical to drain_n on both strips")
 
 
 def test_stub_weights_blob_stream_with_head(H, stub_dir, stub_npz):
@@ -338,6 +352,12 @@ def test_edge_cases(H, stub_dir, stub_npz):
         st = O.S2S3(layers, 16, 20, 4)
         p2, p3, feat, _ = st.run(ring.x, ring.y, ring.feat1)
         compare(out, p2, p3, feat, "dense ring")
+        # every cell's final state depends on the order of all its pairs,
+        # not only on those of the pass-3 records
+        for li in range(4):
+            assert hidden_close(d.hidden(0, li), st.H[li]), li
+        td2, td3 = d.counters(0)
+        assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3)
 
 
 def test_window_one_passes_everything(H):

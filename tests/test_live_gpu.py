@@ -431,3 +431,126 @@ def test_replay_four_streams_live(stub_dir, stub_npz):
     for s in res.streams:
         assert s["drained"] == n and s["drop_drift"] == 0
         assert s["output_records"] > 0 and 0 < s["push_to_done_p50"] < 1e5
+
+
+def _oracle_rings(stub_npz, jobs):
+    """Runs the fp64 oracle (with head) over several rings at once, one
+    thread each (the C oracle keeps no global state and ctypes releases the
+    GIL).  jobs: (x, y, feat1, owner-or-None); returns (state, p2, p3, ref7)."""
+    from concurrent.futures import ThreadPoolExecutor
+    layers, head = O.layers_from_npz(stub_npz), O.head_from_npz(stub_npz)
+
+    def one(job):
+        x, y, f, own = job
+        st = O.S2S3(layers, 16, 20, 4, head=head)
+        p2, p3, _, ref7 = st.run(x, y, f, owner=own, want_head=True)
+        return st, p2, p3, ref7
+
+    with ThreadPoolExecutor(max_workers=min(16, len(jobs))) as ex:
+        return list(ex.map(one, jobs))
+
+
+def _check_block_preds(preds, version, x, y, own, p3, ref7, owned):
+    """Prediction cells of a block's owned s3 box: version = owned pass-3
+    records of the cell, values = the last one's head outputs."""
+    x3l, x3h, y3l, y3h = owned[0] >> 1, owned[1] >> 1, owned[2] >> 1, owned[3] >> 1
+    w3 = x3h - x3l
+    hit = own & (p3 == 1) & ((x >> 1) >= x3l) & ((x >> 1) < x3h) & ((y >> 1) >= y3l) \
+        & ((y >> 1) < y3h)
+    cell = ((y >> 1) - y3l) * w3 + ((x >> 1) - x3l)
+    for c in range(version.size):
+        k = np.nonzero(hit & (cell == c))[0]
+        assert version[c] == k.size, c
+        if k.size:
+            assert np.abs(preds[c] - ref7[k[-1]]).max() <= HEAD_TOL, c
+
+
+@pytest.mark.parametrize("gpu_blocks", [1, 8])
+def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks):
+    """The live configuration as stated: the producer's paced blob source at
+    2.0 Mev/s -> 6 host shards for stages 0 + 1 (halo 2) -> fine-grained
+    rings -> the persistent kernel, 2 s (orin/hybrid_runner_multi.py:314-754).
+    One ownership domain (1 block) and the reference's 8-strip topology.
+    Every published record is drained with no overrun, and each ring's
+    contents, run through the oracle with that block's ownership, give the
+    kernel's pass flags (timing-slot owner flags), tdrop counters, final
+    hidden state and prediction grid."""
+    from ssla_hip import live as LV
+    say(f"config 2: 2.0 Mev/s, 6 shards, halo 2, 2 s, {gpu_blocks} GPU block(s)")
+    cap = 1 << 19 if gpu_blocks == 1 else 1 << 18
+    seen = {}
+
+    def inspect(drain, rings, heads, topo):
+        jobs, meta = [], []
+        for b, t in enumerate(topo):
+            n = heads[b]
+            assert 0 < n <= rings.capacity, (b, n)
+            assert int(rings.done[b]) == n, b
+            recs = rings.rings[b][:n].copy()
+            assert np.array_equal(recs["seq_done"], np.arange(1, n + 1, dtype=np.uint64)), b
+            x, y = recs["x"].astype(int), recs["y"].astype(int)
+            own = (x >= t.owned_x_lo) & (x < t.owned_x_hi) & (y >= t.owned_y_lo) \
+                & (y < t.owned_y_hi)
+            jobs.append((recs["x"], recs["y"], recs["feat1"], own))
+            meta.append((b, t, x, y, own, drain.timing(b)[:n],
+                         [drain.hidden(b, li) for li in range(4)], drain.counters(b),
+                         drain.preds(b)))
+        say(f"config 2: records per ring {heads}; running the oracle")
+        for (st, p2, p3, ref7), (b, t, x, y, own, ts, hid, (td2, td3), (pr, ver)) in zip(
+                _oracle_rings(stub_npz, jobs), meta):
+            assert np.array_equal(ts["owner"], (own & (p3 == 1)).astype(np.uint32)), b
+            for li in range(4):
+                assert hidden_close(hid[li], st.H[li]), (b, li)
+            assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3), b
+            _check_block_preds(pr, ver, x, y, own, p3, ref7, t.owned)
+        seen["blocks"] = len(topo)
+
+    r = LV.run_live(stub_dir, rate_mev=2.0, duration_s=2.0, n_shards=6, halo=2,
+                    gpu_blocks=gpu_blocks, ring_capacity=cap, timing_capacity=cap,
+                    inspect=inspect)
+    say(f"config 2: status {r.status}, {r.synth_events} events, {r.ring_records} ring records, "
+        f"{r.drained} drained, {r.output_records} output-producing, "
+        f"emit->prediction p50 {r.lat_us['emit_to_done_p50']:.1f} us "
+        f"p99 {r.lat_us['emit_to_done_p99']:.1f} us")
+    assert r.status == 0 and seen.get("blocks") == gpu_blocks
+    assert r.drained == r.ring_records > 0 and r.output_records > 0
+    # about 2 Mev/s x 2 s raw events; ~1/16 of them reach a single-domain ring
+    assert r.synth_events > 3_000_000
+
+
+def test_config4_sixteen_rings_one_persistent_kernel(stub_dir, stub_npz):
+    """Config 4: 16 independent 80x64 instances sharing the stub weights in
+    one persistent kernel (...celled.cuh:82 MAX_BLOCKS = 16, :1547), each fed
+    its own seeded blob stream (seeds 1..16) through its own ring at 125k
+    records/s (2.0 Mev/s raw / 16).  Per stream: every record drained, drop
+    drift 0, tdrop counters, final hidden state and prediction grid equal to
+    the oracle's."""
+    from ssla_hip import live as LV
+    n = 40_000
+    say(f"config 4: 16 rings x {n} records at 125k records/s each")
+    recs = [events.blob_records(n, seed=1 + s) for s in range(16)]
+    expect = [O.decisions(r.x, r.y, 16, 20, 4)[1] for r in recs]
+    state = {}
+
+    def inspect(drain):
+        for b in range(16):
+            state[b] = ([drain.hidden(b, li) for li in range(4)], drain.counters(b),
+                        drain.preds(b))
+
+    res = LV.run_replay(stub_dir, [events.to_records(r) for r in recs], 125_000.0,
+                        ring_capacity=1 << 16, timing_capacity=1 << 16, expect_p3=expect,
+                        inspect=inspect)
+    say("config 4: status", res.status, "per stream (drained, drift, p50 us, p99 us):",
+        [(s["drained"], s["drop_drift"], round(s["push_to_done_p50"], 1),
+          round(s["push_to_done_p99"], 1)) for s in res.streams])
+    assert res.status == 0 and len(state) == 16
+    for s in res.streams:
+        assert s["drained"] == n and s["drop_drift"] == 0
+    got = _oracle_rings(stub_npz, [(r.x, r.y, r.feat1, None) for r in recs])
+    for b, (st, p2, p3, ref7) in enumerate(got):
+        hid, (td2, td3), (pr, ver) = state[b]
+        assert np.array_equal(p3, expect[b])
+        for li in range(4):
+            assert hidden_close(hid[li], st.H[li]), (b, li)
+        assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3), b
+        check_preds(pr, ver, recs[b], p3, ref7)
