@@ -183,6 +183,27 @@ int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg,
                         HybridS2S3OutputSlot* const* outs,
                         const SslaHipDrainOpts* opts);
 
+/* The batch-mode drain (ssla_hip_drain_n_ex with opts->batch = batch) for
+ * callers that cannot allocate device memory: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  No
+ * counterpart in the reference.  It makes no hipMalloc / hipFree /
+ * allocating call: the memory its kernel needs beyond the caller's inputs
+ * and outputs (each block's pair rows, the fragment-order weight copy, the
+ * block table; 7.8 MiB) is a static array of the library, one per
+ * device, held until the process ends.  Limits: cfg->n_blocks <= 16,
+ * 1 <= batch <= 32 (SSLA_ERR_ARG beyond).  All calls on one device share
+ * that array: calls that overlap on one device (other streams or threads)
+ * race and must be ordered by the caller.  The first call on a device
+ * looks up the array's device address; make it before any graph capture.
+ * head_outs as in SslaHipDrainOpts.  Enqueued on `stream` (hipStream_t or
+ * NULL); waits for completion when sync is nonzero.  Results equal
+ * ssla_hip_drain_n_ex's with the same batch. */
+int ssla_hip_drain_batch_noalloc(const HybridS2S3Config* cfg,
+                                 const HybridInputRec* const* rings, const int* ns,
+                                 HybridS2S3OutputSlot* const* outs,
+                                 float* const* head_outs, int batch,
+                                 void* stream, int sync);
+
 /* The whole-ring drain keeps one workspace per process (device memory
  * sized for the largest call so far; about 4 KB per record).  A call with
  * more records than it holds regrows it, which waits for the previous

@@ -624,6 +624,17 @@ int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg, const HybridInputRec* const
     return scan_drain(cfg, rings, ns, outs, opts ? opts->head_outs : nullptr, st, sync, phase_ms);
 }
 
+int ssla_hip_drain_batch_noalloc(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
+                                 const int* ns, HybridS2S3OutputSlot* const* outs,
+                                 float* const* head_outs, int batch, void* stream, int sync) {
+    if (!cfg || !rings || !ns) { set_error("null argument"); return SSLA_ERR_ARG; }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int rc = batch_drain_noalloc(cfg, rings, ns, outs, head_outs, batch, st);
+    if (rc) return rc;
+    if (sync) API_HIP(hipStreamSynchronize(st));
+    return SSLA_OK;
+}
+
 int ssla_hip_drain_reserve(const HybridS2S3Config* cfg, int max_records) {
     return drain_reserve(cfg, max_records);
 }

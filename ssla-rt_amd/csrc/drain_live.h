@@ -23,6 +23,14 @@ int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                 unsigned long long* const* batch_clks, int batch, hipStream_t st, bool sync,
                 double* phase_us);
 
+// The batch drain with the device memory it needs beyond its inputs and
+// outputs in a static per-device array (noalloc_scratch_bytes() bytes,
+// up to SSLA_MAX_BLOCKS blocks): allocates nothing.  Asynchronous on st.
+int batch_drain_noalloc(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
+                        const int* ns, HybridS2S3OutputSlot* const* outs,
+                        float* const* head_outs, int batch, hipStream_t st);
+size_t noalloc_scratch_bytes();
+
 struct LiveSession;
 
 int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,

@@ -1039,6 +1039,119 @@ int batch_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
 }
 
 // ---------------------------------------------------------------------------
+// batch drain that allocates nothing (ssla_hip_drain_batch_noalloc)
+// ---------------------------------------------------------------------------
+namespace {
+
+// Device memory the batch kernel uses beyond its inputs and outputs, for up
+// to kNaMaxBlocks blocks: each block's pair rows (LP x NCMAX floats), the
+// fragment-order weight copy and the block table.  One array per device,
+// held until the process ends; every call on a device shares it, so calls
+// that overlap on one device race.  Nothing in it has to start at zero: a
+// batch writes every pair row it reads, and each call rewrites the weight
+// copy and the block table before its kernel runs.
+constexpr int kNaMaxBlocks = SSLA_MAX_BLOCKS;
+constexpr size_t kNaRowFloats = (size_t)LP * NCMAX;                     // per block
+constexpr size_t kNaPackOff = sizeof(float) * kNaRowFloats * kNaMaxBlocks;
+constexpr size_t kNaDescOff =
+    (kNaPackOff + sizeof(float) * PackLayout<false>::off[8] + 255) & ~size_t(255);
+constexpr size_t kNaBytes = kNaDescOff + sizeof(LiveDesc) * kNaMaxBlocks;
+static_assert(kNaBytes <= (size_t)16 << 20, "the no-allocation scratch stays modest");
+
+static __device__ __align__(256) unsigned char scratch[kNaBytes];
+
+// The block table travels as kernel arguments, eight entries per launch.
+constexpr int kNaDescChunk = 8;
+struct DescChunk {
+    LiveDesc d[kNaDescChunk];
+};
+static_assert(sizeof(DescChunk) <= 3072, "kernel argument block");
+
+__global__ void k_put_desc(DescChunk c, int n, LiveDesc* __restrict__ dst) {
+    if ((int)threadIdx.x < n) dst[threadIdx.x] = c.d[threadIdx.x];
+}
+
+constexpr int kNaMaxDevices = 64;
+std::mutex g_na_mu;
+unsigned char* g_na_ptr[kNaMaxDevices] = {};
+
+// The device address of the current device's `scratch` (host code may not
+// use the symbol itself: its host-side name is not a device address).
+int na_scratch(unsigned char** out) {
+    int dev = 0;
+    LHIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kNaMaxDevices) {
+        set_error("drain_batch_noalloc: device index out of range");
+        return SSLA_ERR_ARG;
+    }
+    std::lock_guard<std::mutex> lk(g_na_mu);
+    if (!g_na_ptr[dev]) {
+        void* p = nullptr;
+        LHIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_na_ptr[dev] = static_cast<unsigned char*>(p);
+    }
+    *out = g_na_ptr[dev];
+    return SSLA_OK;
+}
+
+}  // namespace
+
+size_t noalloc_scratch_bytes() { return kNaBytes; }
+
+int batch_drain_noalloc(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
+                        const int* ns, HybridS2S3OutputSlot* const* outs,
+                        float* const* head_outs, int batch, hipStream_t st) {
+    LiveWeights W;
+    Geometry G;
+    int rc = live_weights(cfg, &W, &G);
+    if (rc) return rc;
+    const int nb = cfg->n_blocks;
+    if (nb > kNaMaxBlocks) {
+        set_error("drain_batch_noalloc: n_blocks exceeds the scratch's " +
+                  std::to_string(kNaMaxBlocks) + " blocks");
+        return SSLA_ERR_ARG;
+    }
+    if (batch < 1 || batch > LB) {
+        set_error("drain_batch_noalloc: batch must be in [1, 32]");
+        return SSLA_ERR_ARG;
+    }
+    for (int b = 0; b < nb; ++b)
+        if (ns[b] < 0 || (ns[b] > 0 && !rings[b])) {
+            set_error("drain_batch_noalloc: bad ring / count for block " + std::to_string(b));
+            return SSLA_ERR_ARG;
+        }
+    unsigned char* base = nullptr;
+    rc = na_scratch(&base);
+    if (rc) return rc;
+    float* rows = reinterpret_cast<float*>(base);
+    float* pack = reinterpret_cast<float*>(base + kNaPackOff);
+    LiveDesc* desc = reinterpret_cast<LiveDesc*>(base + kNaDescOff);
+    for (int c0 = 0; c0 < nb; c0 += kNaDescChunk) {
+        DescChunk c;
+        std::memset(&c, 0, sizeof c);
+        const int n = std::min(kNaDescChunk, nb - c0);
+        for (int k = 0; k < n; ++k) {
+            const int b = c0 + k;
+            LiveDesc& d = c.d[k];
+            live_desc_state(cfg, b, &d);
+            d.ring = rings[b];
+            d.ring_mask = ~0ull;
+            d.n = ns[b];
+            d.scratch = rows + kNaRowFloats * b;
+            d.out = outs ? outs[b] : nullptr;
+            d.head_out = head_outs ? head_outs[b] : nullptr;
+        }
+        hipLaunchKernelGGL(k_put_desc, dim3(1), dim3(64), 0, st, c, n, desc + c0);
+    }
+    LHIP(hipGetLastError());
+    LHIP(pack_weights(W.L, pack, &W.pk, st));
+    hipLaunchKernelGGL(k_batch_drain, dim3(nb), dim3(LT), 0, st, (const LiveDesc*)desc, W, G,
+                       batch);
+    LHIP(hipGetLastError());
+    return SSLA_OK;
+}
+
+// ---------------------------------------------------------------------------
 // persistent session
 // ---------------------------------------------------------------------------
 struct LiveSession {

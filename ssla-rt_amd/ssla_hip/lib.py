@@ -53,6 +53,9 @@ _SIGNATURES = {
                                  ctypes.POINTER(_I), ctypes.POINTER(_VP),
                                  ctypes.POINTER(abi.SslaHipDrainOpts)]),
     "ssla_hip_drain_reserve": (_I, [ctypes.POINTER(abi.HybridS2S3Config), _I]),
+    "ssla_hip_drain_batch_noalloc": (_I, [ctypes.POINTER(abi.HybridS2S3Config),
+                                          ctypes.POINTER(_VP), ctypes.POINTER(_I),
+                                          ctypes.POINTER(_VP), ctypes.POINTER(_VP), _I, _VP, _I]),
     "ssla_hip_wall_clock_khz": (_I, [ctypes.POINTER(_I)]),
     "ssla_hip_timing_alloc": (_I, [ctypes.POINTER(abi.HybridS2S3Config), _I, ctypes.c_uint]),
     "ssla_hip_timing_free": (None, [ctypes.POINTER(abi.HybridS2S3Config), _I]),
