@@ -297,7 +297,7 @@ for _L, (_i, _o) in zip(("L4", "L5", "L6", "L7"), ((C1, C2), (C2, C2), (C2, C3),
     PHASE_KERNEL[f"{_L}.sum"] = f"k_scan_summary<{_o}>"
     PHASE_KERNEL[f"{_L}.carry"] = f"k_scan_carry<{_o}>"
     PHASE_KERNEL[f"{_L}.apply"] = f"k_scan_apply<{_o}>"
-    PHASE_KERNEL[f"{_L}.out"] = f"k_out<{_i}, {_o}>"
+    PHASE_KERNEL[f"{_L}.out"] = f"k_outt<{_i}, {_o}>"
 RIDGE = PEAK_FP32_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)     # FLOP/B
 
 

@@ -624,191 +624,207 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
 
 // ---------------------------------------------------------------------------
 // O: per record y = sum_delta goW[delta]^T (q_delta * h_delta) + residual,
-// fp64 LayerNorm.  One workgroup = 64 records, one wave per 16-column output
-// tile (OUT / 16 waves); the records' inputs stay in LDS.  The contraction
-// over K = 9*OUT (+ IN) runs in parts at delta boundaries.  A part's rows
-// (the records' h rows at that delta, zeros where out of bounds; or their
-// inputs for input_proj) are fetched into registers while the previous
-// part's MFMAs run and written to the other of two LDS buffers.  Each wave
-// then computes its 16 columns of q = qvgIn[delta]^T x for the 64 records
-// (MFMA, weights from the projection copy) and multiplies them into the
-// buffer; after a barrier every wave accumulates its column tile over the
-// part's q*h rows, all four row tiles.
+// fp64 LayerNorm -- computed transposed, with the weights as MFMA A operands
+// and the records as columns (layouts in mfma_pack.h, OutPackT):
+//   q^T tile (16 channels x 16 records) = Wq[delta]^T X^T
+//   Y^T     += goW[delta]^T (q^T * h^T)        for every output tile
+//   Y^T     += input_proj^T X^T (IN != OUT) or + X (IN == OUT)
+// Each wave owns RT tiles of 16 records and runs every K part itself, so no
+// LDS and no barrier are involved: a lane keeps its record's input row
+// (the B operand of q and input_proj, one float4 per four steps) in
+// registers for the whole kernel; the h values arrive as one float4 per
+// lane in the MFMA output layout of the q tile and are multiplied there;
+// and with the K order of OutPackT those four products are the lane's B
+// values of the goW steps.  The weights stream from the L2 (shared by all
+// waves) one (delta, channel tile) item ahead.  LayerNorm in fp64 over the
+// four lanes that hold a record's outputs (ds_swizzle and ds_bpermute sums).
 // ---------------------------------------------------------------------------
-template <int IN, int OUT>
-__global__ void __launch_bounds__(OUT / kMT * 64)
-k_out(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
-      const float* __restrict__ X, const int* __restrict__ pos,
-      const float* __restrict__ HR, const float* __restrict__ pp, const float* __restrict__ po,
-      const float* __restrict__ gamma, const float* __restrict__ beta, float* __restrict__ Y) {
-    using O = OutPackD<IN, OUT>;
-    using P = ProjPack<IN, OUT>;
-    static_assert(P::TQ == O::NT, "one q column tile per wave");
-    // one wave per 16-column tile of the output
-    constexpr int NTH = O::NT * 64, NC = 2 * OUT, QST = lds_stride(OUT), XST = lds_stride(IN);
-    constexpr int I4 = IN / 4, YST = OUT + 1;
-    constexpr int XY = kTM * (XST > YST ? XST : YST);
-    __shared__ __align__(16) float qs[2][kTM * QST];
-    // the records' inputs while the parts run, then the pre-LayerNorm sums
-    __shared__ __align__(16) float xy[XY];
-    __shared__ double stat[kTM][2];
-    __shared__ int rows[kTM];
-    __shared__ int prow[kPatch][kTM];
-    float* const xs = xy;
+__device__ __forceinline__ double xor_lanes_d(double v, int pattern_or_lane, bool swizzle) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+    unsigned lo, hi;
+    if (swizzle) {
+        lo = (unsigned)__builtin_amdgcn_ds_swizzle((int)(unsigned)b, 0x401F);       // xor 16
+        hi = (unsigned)__builtin_amdgcn_ds_swizzle((int)(unsigned)(b >> 32), 0x401F);
+    } else {
+        lo = (unsigned)__builtin_amdgcn_ds_bpermute(pattern_or_lane, (int)(unsigned)b);
+        hi = (unsigned)__builtin_amdgcn_ds_bpermute(pattern_or_lane, (int)(unsigned)(b >> 32));
+    }
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
+// sum over lanes j, j + 16, j + 32, j + 48 (all 64 lanes active)
+__device__ __forceinline__ double sum4_lanes(double v, int lane) {
+    v += xor_lanes_d(v, 0, true);
+    return v + xor_lanes_d(v, (lane ^ 32) << 2, false);
+}
+
+template <int IN, int OUT, int RT, int KS>
+__global__ void __launch_bounds__(64 * KS)
+k_outt(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
+       const float* __restrict__ X, const int* __restrict__ pos, const float* __restrict__ HR,
+       const float* __restrict__ po, const float* __restrict__ gamma,
+       const float* __restrict__ beta, float* __restrict__ Y) {
+    using O = OutPackT<IN, OUT>;
+    constexpr int NT = O::NT, KG = O::KG, NC = 2 * OUT, R = 16 * RT;
+    // the workgroup's pair rows, and the partial sums of waves 1..KS-1
+    __shared__ int sp[R][kPatch];
+    __shared__ f32x4 part[KS > 1 ? KS - 1 : 1][RT * NT][64];
     const int n = n_dev ? *n_dev : n_max;
-    const int base = blockIdx.x * kTM;
+    const int base = blockIdx.x * R;
     if (base >= n) return;
-    const int cnt = min(kTM, n - base);
-    const int tid = threadIdx.x;
-    if (tid < kTM) rows[tid] = tid < cnt ? (list ? list[base + tid] : base + tid) : -1;
-    __syncthreads();
-    for (int t = tid; t < kTM * kPatch; t += NTH) {
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
+    for (int t = threadIdx.x; t < R * kPatch; t += 64 * KS) {
         const int r = t / kPatch, d = t - r * kPatch;
-        const int g = rows[r];
-        prow[d][r] = g >= 0 ? pos[(size_t)g * kPatch + d] : -1;
+        const int q = base + r;
+        const int rr = q < n ? (list ? list[q] : q) : -1;
+        sp[r][d] = rr >= 0 ? pos[(size_t)rr * kPatch + d] : -1;
     }
-    for (int t = tid; t < kTM * I4; t += NTH) {
-        const int r = t / I4, q = t - r * I4;
-        const int g = rows[r];
-        const float4 v = g >= 0 ? reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q]
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
-        lds_put4(&xs[r * XST + 4 * q], v);
-    }
-    __syncthreads();
-    const int lane = tid & 63, wv = tid >> 6, li = lane & 15, lk = lane >> 4;
-    const int mtiles = (cnt + kMT - 1) / kMT;
-    f32x4 acc[4];
+    int rec[RT];
     #pragma unroll
-    for (int m = 0; m < 4; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // Each wave fetches, stores and scales its own 16 columns of a part's 64
-    // rows (4 float4 per lane), so the q product needs no barrier before it;
-    // one barrier per part then publishes all columns to the contraction.
-    float4 pre[4];
-    auto fetch = [&](int part) {
+    for (int rt = 0; rt < RT; ++rt) {
+        const int r = base + 16 * rt + j;
+        rec[rt] = r < n ? (list ? list[r] : r) : -1;
+    }
+    // this lane's B values of the input steps: X[rec][16 t + 4 g .. + 3]
+    f32x4 xr[RT][KG];
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
         #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int idx = lane + 64 * u, r = idx >> 2, q = wv * 4 + (idx & 3);
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (part < kPatch) {
-                const int pr = prow[part][r];
-                if (pr >= 0) v = reinterpret_cast<const float4*>(HR + (size_t)pr * NC)[q];
-            } else {
-                const int g = rows[r];
-                if (g >= 0 && q < I4) v = reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q];
-            }
-            pre[u] = v;
+        for (int t = 0; t < KG; ++t) {
+            const int c = 16 * t + 4 * g;
+            xr[rt][t] = (rec[rt] >= 0 && c < IN)
+                            ? *(const SSLA_GLOBAL f32x4*)(X + (size_t)rec[rt] * IN + c)
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
         }
-    };
-    auto put = [&](float* buf) {
+    f32x4 acc[RT][NT];
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
         #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int idx = lane + 64 * u, r = idx >> 2, q = wv * 4 + (idx & 3);
-            lds_put4(&buf[r * QST + 4 * q], pre[u]);
-        }
-    };
-    // this wave's 16 columns of q for the 64 records (rows past cnt are
-    // zero), multiplied into its columns of the h rows in place
-    auto qmul = [&](float* buf, const float* qb) {
-        f32x4 q[4];
-        #pragma unroll
-        for (int m = 0; m < 4; ++m) q[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const float* a = &xs[li * XST + lk];
-        #pragma unroll
-        for (int s = 0; s < P::KS; ++s)
-            #pragma unroll
-            for (int m = 0; m < 4; ++m)
-                q[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m * kMT * XST + 4 * s], qb[s], q[m],
-                                                            0, 0, 0);
-        #pragma unroll
-        for (int m = 0; m < 4; ++m)
-            #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                buf[(m * kMT + 4 * lk + r) * QST + wv * kMT + li] *= q[m][r];
-    };
-    // the four row tiles' accumulation chains interleaved step by step, so
-    // consecutive MFMAs are independent (rows past cnt hold zeros)
-    auto compute = [&](const float* buf, const float (&b)[O::SD]) {
-        const float* a = &buf[li * QST + lk];
-        #pragma unroll
-        for (int s = 0; s < O::SD; ++s)
-            #pragma unroll
-            for (int m = 0; m < 4; ++m)
-                acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m * kMT * QST + 4 * s], b[s], acc[m],
-                                                              0, 0, 0);
-    };
-    // part k: put + q product into qs[k % 2], barrier, contraction; the next
-    // part's rows and weights load while the contraction runs.  A buffer is
-    // rewritten two parts later, after the barrier that every wave reaches
-    // only once its contraction over that buffer is done.
-    float b0[O::SD], b1[O::SD];
-    float qb[P::KS4 * 4];
-    fetch(0);
-    O::load(po, wv, 0, lane, b0);
-    P::load(pp, wv, lane, qb);                       // item (delta 0, q tile wv)
-    put(qs[0]);
-    qmul(qs[0], qb);
+        for (int ot = 0; ot < NT; ++ot) acc[rt][ot] = f32x4{0.f, 0.f, 0.f, 0.f};
     __syncthreads();
+
+    const SSLA_GLOBAL f32x4* wq = (const SSLA_GLOBAL f32x4*)po + lane;
+    const SSLA_GLOBAL f32x4* wg = (const SSLA_GLOBAL f32x4*)(po + O::Q) + lane;
+    // item it = delta * NT + ct: its q and goW fragments and the h values
+    auto load = [&](int it, f32x4 (&aq)[KG], f32x4 (&ag)[NT], f32x4 (&hv)[RT]) {
+        const int d = it / NT, ct = it - d * NT;
+        #pragma unroll
+        for (int t = 0; t < KG; ++t) aq[t] = wq[((size_t)it * KG + t) * 64];
+        #pragma unroll
+        for (int ot = 0; ot < NT; ++ot) ag[ot] = wg[((size_t)it * NT + ot) * 64];
+        #pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const int p = sp[16 * rt + j][d];
+            hv[rt] = p >= 0 ? *(const SSLA_GLOBAL f32x4*)(HR + (size_t)p * NC + 16 * ct + 4 * g)
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    auto compute = [&](const f32x4 (&aq)[KG], const f32x4 (&ag)[NT], const f32x4 (&hv)[RT]) {
+        f32x4 q[RT];
+        #pragma unroll
+        for (int rt = 0; rt < RT; ++rt) q[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        #pragma unroll
+        for (int t = 0; t < KG; ++t)
+            #pragma unroll
+            for (int i = 0; i < 4; ++i)
+                #pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+                    q[rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[t][i], xr[rt][t][i], q[rt],
+                                                                 0, 0, 0);
+        #pragma unroll
+        for (int rt = 0; rt < RT; ++rt) q[rt] *= hv[rt];
+        #pragma unroll
+        for (int i = 0; i < 4; ++i)
+            #pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                #pragma unroll
+                for (int ot = 0; ot < NT; ++ot)
+                    acc[rt][ot] = __builtin_amdgcn_mfma_f32_16x16x4f32(ag[ot][i], q[rt][i],
+                                                                       acc[rt][ot], 0, 0, 0);
+    };
+    // this wave's items: deltas [d0, d1), the K parts split over the KS waves;
+    // the next item's weights and h values load while the current one runs
+    const int i0 = (wv * kPatch / KS) * NT, i1 = ((wv + 1) * kPatch / KS) * NT;
+    f32x4 aq0[KG], ag0[NT], hv0[RT], aq1[KG], ag1[NT], hv1[RT];
+    load(i0, aq0, ag0, hv0);
     #pragma unroll 1
-    for (int part = 0; part < O::PARTS; part += 2) {
-        // even part in qs[0] with b0
-        if (part + 1 < O::PARTS) {
-            fetch(part + 1);
-            O::load(po, wv, part + 1, lane, b1);
-            if (part + 1 < kPatch) P::load(pp, (part + 1) * P::T + wv, lane, qb);
-        }
-        compute(qs[0], b0);
-        if (part + 1 >= O::PARTS) break;
-        put(qs[1]);
-        if (part + 1 < kPatch) qmul(qs[1], qb);
-        __syncthreads();
-        // odd part in qs[1] with b1
-        if (part + 2 < O::PARTS) {
-            fetch(part + 2);
-            O::load(po, wv, part + 2, lane, b0);
-            if (part + 2 < kPatch) P::load(pp, (part + 2) * P::T + wv, lane, qb);
-        }
-        compute(qs[1], b1);
-        if (part + 2 >= O::PARTS) break;
-        put(qs[0]);
-        if (part + 2 < kPatch) qmul(qs[0], qb);
-        __syncthreads();
+    for (int it = i0; it < i1; it += 2) {
+        if (it + 1 < i1) load(it + 1, aq1, ag1, hv1);
+        compute(aq0, ag0, hv0);
+        if (it + 1 >= i1) break;
+        if (it + 2 < i1) load(it + 2, aq0, ag0, hv0);
+        compute(aq1, ag1, hv1);
     }
-    // every wave has passed the barrier after the last q product, so the
-    // inputs in xy are no longer read
-    auto ys = [&](int r, int o) -> float& { return xy[r * YST + o]; };
-    #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        if (m >= mtiles) continue;
+    if constexpr (KS > 1) {
+        if (wv > 0) {
+            #pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                #pragma unroll
+                for (int ot = 0; ot < NT; ++ot) part[wv - 1][rt * NT + ot][lane] = acc[rt][ot];
+        }
+        __syncthreads();
+        if (wv > 0) return;
         #pragma unroll
-        for (int r = 0; r < 4; ++r) ys(m * kMT + 4 * lk + r, wv * kMT + li) = acc[m][r];
+        for (int w = 0; w < KS - 1; ++w)
+            #pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                #pragma unroll
+                for (int ot = 0; ot < NT; ++ot) acc[rt][ot] += part[w][rt * NT + ot][lane];
     }
-    __syncthreads();
-    if (!O::IP) {
-        for (int t = tid; t < cnt * OUT; t += NTH) {
-            const int r = t / OUT, o = t - r * OUT;
-            ys(r, o) += X[(size_t)rows[r] * OUT + o];
+    if constexpr (O::IP) {
+        const SSLA_GLOBAL f32x4* wi = (const SSLA_GLOBAL f32x4*)(po + O::Q + O::GO) + lane;
+        #pragma unroll
+        for (int ot = 0; ot < NT; ++ot) {
+            f32x4 ai[KG];
+            #pragma unroll
+            for (int t = 0; t < KG; ++t) ai[t] = wi[((size_t)ot * KG + t) * 64];
+            #pragma unroll
+            for (int t = 0; t < KG; ++t)
+                #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    #pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+                        acc[rt][ot] = __builtin_amdgcn_mfma_f32_16x16x4f32(ai[t][i], xr[rt][t][i],
+                                                                           acc[rt][ot], 0, 0, 0);
         }
-        __syncthreads();
+    } else {
+        // residual: the lane holds X[rec][16 ot + 4 g + i] as xr[rt][ot][i]
+        #pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+            #pragma unroll
+            for (int ot = 0; ot < NT; ++ot) acc[rt][ot] += xr[rt][ot];
     }
-    if (tid < cnt) {
-        const int r = tid;
+    // fp64 LayerNorm (eps 1e-5): lane (g, j) holds outputs 16 ot + 4 g + i of
+    // record j of each tile; the record's sums are over lanes j + 16 g
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
         double s = 0.0;
-        for (int i = 0; i < OUT; ++i) s += (double)ys(r, i);
-        const double mean = s / (double)OUT;
-        double var = 0.0;
-        for (int i = 0; i < OUT; ++i) {
-            const double dd = (double)ys(r, i) - mean;
-            var += dd * dd;
+        #pragma unroll
+        for (int ot = 0; ot < NT; ++ot)
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) s += (double)acc[rt][ot][i];
+        const double mean = sum4_lanes(s, lane) / (double)OUT;
+        double v = 0.0;
+        #pragma unroll
+        for (int ot = 0; ot < NT; ++ot)
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const double dd = (double)acc[rt][ot][i] - mean;
+                v += dd * dd;
+            }
+        const double inv = 1.0 / sqrt(sum4_lanes(v, lane) / (double)OUT + 1e-5);
+        #pragma unroll
+        for (int ot = 0; ot < NT && rec[rt] >= 0; ++ot) {
+            const int c = 16 * ot + 4 * g;
+            const f32x4 ga = *(const SSLA_GLOBAL f32x4*)(gamma + c);
+            const f32x4 be = *(const SSLA_GLOBAL f32x4*)(beta + c);
+            f32x4 o;
+            #pragma unroll
+            for (int i = 0; i < 4; ++i)
+                o[i] = (float)(((double)acc[rt][ot][i] - mean) * inv * (double)ga[i] +
+                               (double)be[i]);
+            *(SSLA_GLOBAL f32x4*)(Y + (size_t)rec[rt] * OUT + c) = o;
         }
-        var /= (double)OUT;
-        stat[r][0] = mean;
-        stat[r][1] = 1.0 / sqrt(var + 1e-5);
-    }
-    __syncthreads();
-    for (int t = tid; t < cnt * OUT; t += NTH) {
-        const int r = t / OUT, o = t - r * OUT;
-        const double v = ((double)ys(r, o) - stat[r][0]) * stat[r][1];
-        Y[(size_t)rows[r] * OUT + o] = (float)(v * (double)gamma[o] + (double)beta[o]);
     }
 }
 
@@ -1454,9 +1470,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, all, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_out<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(SSLA_C2 / kMT * 64), 0, st, E,
-                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, pk.pp[0],
-                       pk.po[0], L[0].ln_gamma, L[0].ln_beta, w.X1);
+    hipLaunchKernelGGL((k_outt<SSLA_C1, SSLA_C2, 2, 1>), dim3(grid1(E, 32)), dim3(64), 0, st, E,
+                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, pk.po[0],
+                       L[0].ln_gamma, L[0].ln_beta, w.X1);
     MARK();
     // ---- L5: 48 -> 48, state for all records, output for pass2 ---------------
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
@@ -1471,9 +1487,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, w.pass2, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(SSLA_C2 / kMT * 64), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, pk.pp[1],
-                       pk.po[1], L[1].ln_gamma, L[1].ln_beta, w.X2);
+    hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C2, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
+                       (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, pk.po[1],
+                       L[1].ln_gamma, L[1].ln_beta, w.X2);
     MARK();
     // ---- [side] s3 pair order over the pass2 records only ------------------------
     // L4 and L5 are queued; the host waits for the pass2 count (known once
@@ -1536,9 +1552,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, all, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_out<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(SSLA_C3 / kMT * 64), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, pk.pp[2],
-                       pk.po[2], L[2].ln_gamma, L[2].ln_beta, w.X3);
+    hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C3, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
+                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, pk.po[2],
+                       L[2].ln_gamma, L[2].ln_beta, w.X3);
     MARK();
     // ---- L7: 96 -> 96, state for pass2, output for pass3 ----------------------
     hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
@@ -1553,9 +1569,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, w.pass3, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_out<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(SSLA_C3 / kMT * 64), 0, st, E,
-                       (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, pk.pp[3],
-                       pk.po[3], L[3].ln_gamma, L[3].ln_beta, w.X4);
+    hipLaunchKernelGGL((k_outt<SSLA_C3, SSLA_C3, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
+                       (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, pk.po[3],
+                       L[3].ln_gamma, L[3].ln_beta, w.X4);
     MARK();
     HIPCHK(hipGetLastError());
     // ---- head ------------------------------------------------------------------

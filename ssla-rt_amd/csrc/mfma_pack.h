@@ -13,7 +13,9 @@
 //               [q | v | g]); B[k][c] = qvgIn[delta][k][c], k < IN
 //   contraction (OutPack):  items (16-column tile, K part of kKSplit);
 //               B = [goW as (9*OUT) x OUT, delta-major; input_proj (IN x OUT)
-//               when IN != OUT]
+//               when IN != OUT]  (batch and live kernels)
+//   transposed contraction (OutPackT): the whole-ring drain's A operands,
+//               with q recomputed from the record inputs (below)
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -79,29 +81,61 @@ struct OutPack {
     }
 };
 
-// The contraction split at delta boundaries (whole-ring drain): items
-// (16-column tile nt, part), parts 0..8 the rows of goW[delta] (OUT / 4
-// steps), part 9 (when IN != OUT) input_proj (IN / 4 steps, zero padded).
+// The transposed contraction of the whole-ring drain (k_outt):
+//   q^T = Wq[delta]^T X^T,  Y^T = sum_delta goW[delta]^T (q^T * h^T) + input_proj^T X^T,
+// with the weights as the A operands and record tiles as the columns.  Per
+// layer one region holds three A-operand copies (g = lane / 16, j = lane % 16):
+//   q:   items (delta, channel tile ct), groups t < KG, lane, i < 4:
+//          qvgIn[delta][16 t + 4 g + i][16 ct + j]        (0 at or past IN)
+//   goW: items (delta, ct, output tile ot), lane, i < 4:
+//          goW[delta][16 ct + 4 g + i][16 ot + j]
+//   ip:  items ot, groups t < KG, lane, i < 4 (IN != OUT only):
+//          input_proj[16 t + 4 g + i][16 ot + j]          (0 at or past IN)
+// Step 4 t + i of a chain pairs lane group g with input channel
+// 16 t + 4 g + i instead of 4 (4 t + i) + g.  The sum over K does not depend
+// on its order, and with this order a lane's B values are one float4 of a
+// record's input row (q, input_proj), or the four q*h values it already holds
+// in the MFMA output layout (rows 4 g .. 4 g + 3 of the q tile) for goW.
 template <int IN, int OUT>
-struct OutPackD {
+struct OutPackT {
     static constexpr bool IP = IN != OUT;
-    static constexpr int NT = OUT / kMT, PARTS = 9 + (IP ? 1 : 0);
-    static constexpr int SD = OUT / 4, SD4 = SD / 4;   // steps and float4 groups per part
-    static constexpr int N = NT * PARTS;
-    static constexpr size_t PACKED = (size_t)N * SD4 * 256;   // floats
-    static_assert(OUT % 16 == 0 && IN <= OUT, "part shapes");
-    static __device__ __forceinline__ void load(const float* __restrict__ po, int nt, int part,
-                                                int lane, float* b) {
-        const SSLA_GLOBAL f32x4* src =
-            (const SSLA_GLOBAL f32x4*)po + (size_t)(nt * PARTS + part) * SD4 * 64 + lane;
-        #pragma unroll
-        for (int g = 0; g < SD4; ++g) {
-            const f32x4 v = src[g * 64];
-            #pragma unroll
-            for (int j = 0; j < 4; ++j) b[4 * g + j] = v[j];
-        }
-    }
+    static constexpr int NT = OUT / kMT, KG = (IN + 15) / 16;
+    static constexpr size_t Q = (size_t)9 * NT * KG * 256;    // floats
+    static constexpr size_t GO = (size_t)9 * NT * NT * 256;
+    static constexpr size_t IPF = IP ? (size_t)NT * KG * 256 : 0;
+    static constexpr size_t PACKED = Q + GO + IPF;
+    static_assert(OUT % kMT == 0 && IN % 4 == 0 && (IP || IN == OUT), "tile shapes");
 };
+
+// element q of a layer's OutPackT region
+template <int IN, int OUT>
+__device__ __forceinline__ float outt_elem(const float* __restrict__ qvgIn,
+                                           const float* __restrict__ goW,
+                                           const float* __restrict__ ip, size_t q) {
+    using O = OutPackT<IN, OUT>;
+    const int i = (int)(q & 3), lane = (int)((q >> 2) & 63), g = lane >> 4, j = lane & 15;
+    if (q < O::Q) {
+        size_t r = q >> 8;
+        const int t = (int)(r % O::KG);
+        r /= O::KG;
+        const int ct = (int)(r % O::NT), d = (int)(r / O::NT);
+        const int k = 16 * t + 4 * g + i;
+        return k < IN ? qvgIn[((size_t)d * IN + k) * (3 * OUT) + 16 * ct + j] : 0.f;
+    }
+    q -= O::Q;
+    if (q < O::GO) {
+        size_t r = q >> 8;
+        const int ot = (int)(r % O::NT);
+        r /= O::NT;
+        const int ct = (int)(r % O::NT), d = (int)(r / O::NT);
+        return goW[((size_t)d * OUT + 16 * ct + 4 * g + i) * OUT + 16 * ot + j];
+    }
+    q -= O::GO;
+    const size_t r = q >> 8;
+    const int t = (int)(r % O::KG), ot = (int)(r / O::KG);
+    const int k = 16 * t + 4 * g + i;
+    return k < IN ? ip[(size_t)k * OUT + 16 * ot + j] : 0.f;
+}
 
 // element (item, group g, lane, j) = qvgIn[delta][(4g + j) * 4 + lane / 16][t * 16 + lane % 16]
 template <int IN, int OUT>
@@ -133,23 +167,6 @@ __device__ __forceinline__ float out_elem(const float* __restrict__ goW,
     return v;
 }
 
-// element ((nt, part), group g, lane, j): local row kl = (4g + j) * 4 + lane / 16,
-// column c = nt * 16 + lane % 16; goW[part * OUT + kl][c] or input_proj[kl][c]
-template <int IN, int OUT>
-__device__ __forceinline__ float out_d_elem(const float* __restrict__ goW,
-                                            const float* __restrict__ ip, size_t q) {
-    using O = OutPackD<IN, OUT>;
-    const int j = (int)(q & 3), lane = (int)((q >> 2) & 63);
-    const size_t r = q >> 8;
-    const int g = (int)(r % O::SD4), it = (int)(r / O::SD4);
-    const int nt = it / O::PARTS, part = it - nt * O::PARTS;
-    const int kl = (4 * g + j) * 4 + lane / 16, c = nt * kMT + lane % 16;
-    float v = 0.f;
-    if (part < 9) v = goW[((size_t)part * OUT + kl) * OUT + c];
-    else if (kl < IN) v = ip[(size_t)kl * OUT + c];
-    return v;
-}
-
 // Packed copies of the four layers L4..L7.
 struct PackedWeights {
     const float* pp[4];
@@ -167,11 +184,11 @@ struct PackSrc {
 template <int IN, int OUT, bool D>
 struct LayerPack {
     static constexpr size_t NP = ProjPack<IN, OUT>::PACKED;
-    static constexpr size_t NO = D ? OutPackD<IN, OUT>::PACKED : OutPack<IN, OUT>::PACKED;
+    static constexpr size_t NO = D ? OutPackT<IN, OUT>::PACKED : OutPack<IN, OUT>::PACKED;
 };
 
 // Buffer order: L4 projection, L4 contraction, L5 ..., L7 contraction.
-// D selects the contraction split at delta boundaries (whole-ring drain)
+// D selects the transposed contraction of the whole-ring drain (OutPackT)
 // instead of the K split of the batch kernels.
 template <bool D>
 struct PackLayout {
@@ -190,8 +207,9 @@ struct PackLayout {
 };
 
 template <int IN, int OUT, bool D>
-__device__ __forceinline__ float out_any(const float* goW, const float* ip, size_t q) {
-    if constexpr (D) return out_d_elem<IN, OUT>(goW, ip, q);
+__device__ __forceinline__ float out_any(const float* qvgIn, const float* goW, const float* ip,
+                                         size_t q) {
+    if constexpr (D) return outt_elem<IN, OUT>(qvgIn, goW, ip, q);
     else return out_elem<IN, OUT>(goW, ip, q);
 }
 
@@ -203,13 +221,13 @@ __global__ void k_pack_all(PackSrc s, float* __restrict__ buf) {
     if (q >= L::off[8]) return;
     float v;
     if (q < L::off[1]) v = proj_elem<SSLA_C1, SSLA_C2>(s.qvgIn[0], q);
-    else if (q < L::off[2]) v = out_any<SSLA_C1, SSLA_C2, D>(s.goW[0], s.ip[0], q - L::off[1]);
+    else if (q < L::off[2]) v = out_any<SSLA_C1, SSLA_C2, D>(s.qvgIn[0], s.goW[0], s.ip[0], q - L::off[1]);
     else if (q < L::off[3]) v = proj_elem<SSLA_C2, SSLA_C2>(s.qvgIn[1], q - L::off[2]);
-    else if (q < L::off[4]) v = out_any<SSLA_C2, SSLA_C2, D>(s.goW[1], s.ip[1], q - L::off[3]);
+    else if (q < L::off[4]) v = out_any<SSLA_C2, SSLA_C2, D>(s.qvgIn[1], s.goW[1], s.ip[1], q - L::off[3]);
     else if (q < L::off[5]) v = proj_elem<SSLA_C2, SSLA_C3>(s.qvgIn[2], q - L::off[4]);
-    else if (q < L::off[6]) v = out_any<SSLA_C2, SSLA_C3, D>(s.goW[2], s.ip[2], q - L::off[5]);
+    else if (q < L::off[6]) v = out_any<SSLA_C2, SSLA_C3, D>(s.qvgIn[2], s.goW[2], s.ip[2], q - L::off[5]);
     else if (q < L::off[7]) v = proj_elem<SSLA_C3, SSLA_C3>(s.qvgIn[3], q - L::off[6]);
-    else v = out_any<SSLA_C3, SSLA_C3, D>(s.goW[3], s.ip[3], q - L::off[7]);
+    else v = out_any<SSLA_C3, SSLA_C3, D>(s.qvgIn[3], s.goW[3], s.ip[3], q - L::off[7]);
     buf[q] = v;
 }
 
