@@ -31,8 +31,6 @@
 //
 // Device layouts are those of include/ssla_abi.h.
 #include <hip/hip_runtime.h>
-#include <hipcub/hipcub.hpp>
-#include <rocprim/device/device_radix_sort.hpp>
 
 #include <cstdint>
 #include <cstdio>
@@ -105,27 +103,8 @@ k_decode(int E, const BlockDesc* __restrict__ bd, Geometry G,
     val2[g] = (uint32_t)g;
 }
 
-// s3 centre keys of records that passed tdrop_s2 (sentinel otherwise);
-// key3g keeps a per-record copy for the head, ks/vs feed the sort.
-// Over the pass2 list (n records): sort slot j holds record list[j].
-__global__ void k_keys3(int n, const int* __restrict__ list, const BlockDesc* __restrict__ bd,
-                        Geometry G, const int* __restrict__ cell2,
-                        uint32_t* __restrict__ key3g, uint32_t* __restrict__ ks,
-                        uint32_t* __restrict__ vs) {
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= n) return;
-    const int g = list[j];
-    const int b = find_block(bd, G.nb, g);
-    const int c = cell2[g];                  // a pass2 record is on the grid
-    const int x = (c % G.W2) >> 1, y = (c / G.W2) >> 1;
-    const uint32_t k = (uint32_t)(b * G.C3 + y * G.W3 + x);
-    key3g[g] = k;
-    ks[j] = k;
-    vs[j] = (uint32_t)g;
-}
-
 // Up to kFills int arrays set to a value each, one launch (blockIdx.y = array).
-constexpr int kFills = 4;
+constexpr int kFills = 5;
 struct FillSet {
     int* p[kFills];
     int n[kFills];
@@ -136,6 +115,246 @@ __global__ void k_fill_set(FillSet f) {
     const int a = blockIdx.y;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < f.n[a]) f.p[a][i] = f.v[a];
+}
+
+// ---------------------------------------------------------------------------
+// Stable LSD radix sort of (key, record) pairs, digits of up to 9 bits.
+// Records are taken in tiles of kRTile (256 threads x 16 rounds, round r =
+// records base + 256 r .. + 255).  Per pass:
+//   k_rs_hist     digit counts of every tile            -> bh[digit * T + tile]
+//   k_exscan      exclusive scan of bh (digit-major)    -> first slot of every
+//                                                          (digit, tile)
+//   k_rs_scatter  each record to its (digit, tile) start + its rank among
+//                 the tile's earlier records of the digit: inside a wave from
+//                 the lanes whose digit equals its own (one ballot per digit
+//                 bit), across the round's waves and rounds from LDS counts.
+// ---------------------------------------------------------------------------
+constexpr int kRThreads = 256, kRRounds = 16, kRTile = kRThreads * kRRounds;
+constexpr int kRMaxBits = 9;
+
+__global__ void __launch_bounds__(kRThreads)
+k_rs_hist(int n, const uint32_t* __restrict__ keys, int shift, int bits, int T,
+          int* __restrict__ bh) {
+    __shared__ int h[1 << kRMaxBits];
+    const int nb = 1 << bits, tid = threadIdx.x;
+    for (int i = tid; i < nb; i += kRThreads) h[i] = 0;
+    __syncthreads();
+    const int base = blockIdx.x * kRTile;
+    #pragma unroll 4
+    for (int r = 0; r < kRRounds; ++r) {
+        const int idx = base + r * kRThreads + tid;
+        if (idx < n) atomicAdd(&h[(keys[idx] >> shift) & (nb - 1)], 1);
+    }
+    __syncthreads();
+    for (int i = tid; i < nb; i += kRThreads) bh[(size_t)i * T + blockIdx.x] = h[i];
+}
+
+// vin null: the values are the record indices.  sidx (last pass, optional):
+// sidx[value] = the value's sorted position.
+__global__ void __launch_bounds__(kRThreads)
+k_rs_scatter(int n, const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
+             uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int* __restrict__ sidx,
+             int shift, int bits, int T, const int* __restrict__ boff) {
+    __shared__ int cnt[1 << kRMaxBits];
+    __shared__ int wcnt[kRThreads / 64][1 << kRMaxBits];
+    const int nb = 1 << bits, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    for (int i = tid; i < nb; i += kRThreads) {
+        cnt[i] = boff[(size_t)i * T + blockIdx.x];
+        #pragma unroll
+        for (int w = 0; w < kRThreads / 64; ++w) wcnt[w][i] = 0;
+    }
+    __syncthreads();
+    const unsigned long long below = (1ull << lane) - 1ull;
+    const int base = blockIdx.x * kRTile;
+    for (int r = 0; r < kRRounds; ++r) {
+        const int idx = base + r * kRThreads + tid;
+        const bool valid = idx < n;
+        const uint32_t key = valid ? kin[idx] : 0u;
+        const int dig = (int)((key >> shift) & (uint32_t)(nb - 1));
+        unsigned long long peers = __ballot(valid);
+        for (int b = 0; b < bits; ++b) {
+            const bool bit = (dig >> b) & 1;
+            const unsigned long long m = __ballot(bit);
+            peers &= bit ? m : ~m;
+        }
+        const int rank = __popcll(peers & below), size = __popcll(peers);
+        const bool leader = valid && rank == 0;
+        if (leader) wcnt[wv][dig] = size;
+        __syncthreads();
+        if (valid) {
+            int pos = cnt[dig] + rank;
+            for (int w = 0; w < wv; ++w) pos += wcnt[w][dig];
+            const uint32_t v = vin ? vin[idx] : (uint32_t)idx;
+            kout[pos] = key;
+            vout[pos] = v;
+            if (sidx) sidx[v] = pos;
+        }
+        __syncthreads();
+        if (leader) {
+            atomicAdd(&cnt[dig], size);
+            wcnt[wv][dig] = 0;
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// One workgroup scans arrays of any length in rounds of kScanThreads x 8
+// elements: each thread loads 8 consecutive elements with two 16-byte loads,
+// the thread totals are scanned in LDS, and a running carry joins the rounds.
+// Arrays are 256-byte aligned workspace buffers (16-byte loads stay in them;
+// elements at or past n read as zero and are not written).
+// ---------------------------------------------------------------------------
+constexpr int kScanThreads = 1024, kScanPer = 8, kScanRound = kScanThreads * kScanPer;
+
+// exclusive prefix of v over the workgroup; *total receives the sum
+__device__ __forceinline__ int block_exscan(int v, int* lds, int* total) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    int x = v;
+    #pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) lds[wv] = x;
+    __syncthreads();
+    if (wv == 0) {
+        int w = lane < kScanThreads / 64 ? lds[lane] : 0;
+        #pragma unroll
+        for (int o = 1; o < kScanThreads / 64; o <<= 1) {
+            const int y = __shfl_up(w, o, 64);
+            if (lane >= o) w += y;
+        }
+        if (lane < kScanThreads / 64) lds[kScanThreads / 64 + lane] = w;
+    }
+    __syncthreads();
+    const int before = (wv ? lds[kScanThreads / 64 + wv - 1] : 0) + x - v;
+    *total = lds[2 * (kScanThreads / 64) - 1];
+    __syncthreads();
+    return before;
+}
+
+__device__ __forceinline__ void load8(const int* a, int i0, int n, int (&v)[kScanPer]) {
+    if (i0 + kScanPer <= n) {
+        const int4 x = reinterpret_cast<const int4*>(a + i0)[0];
+        const int4 y = reinterpret_cast<const int4*>(a + i0)[1];
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+        v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+    } else {
+        #pragma unroll
+        for (int q = 0; q < kScanPer; ++q) v[q] = i0 + q < n ? a[i0 + q] : 0;
+    }
+}
+
+__device__ __forceinline__ void store8(int* a, int i0, int n, const int (&v)[kScanPer]) {
+    if (i0 + kScanPer <= n) {
+        reinterpret_cast<int4*>(a + i0)[0] = make_int4(v[0], v[1], v[2], v[3]);
+        reinterpret_cast<int4*>(a + i0)[1] = make_int4(v[4], v[5], v[6], v[7]);
+    } else {
+        #pragma unroll
+        for (int q = 0; q < kScanPer; ++q)
+            if (i0 + q < n) a[i0 + q] = v[q];
+    }
+}
+
+// in place: a[i] <- sum of a[0 .. i)
+__global__ void __launch_bounds__(kScanThreads) k_exscan(int n, int* __restrict__ a) {
+    __shared__ int lds[2 * (kScanThreads / 64)];
+    int carry = 0;
+    for (int r0 = 0; r0 < n; r0 += kScanRound) {
+        const int i0 = r0 + (int)threadIdx.x * kScanPer;
+        int v[kScanPer];
+        load8(a, i0, n, v);
+        int sum = 0;
+        #pragma unroll
+        for (int q = 0; q < kScanPer; ++q) sum += v[q];
+        int total;
+        int run = carry + block_exscan(sum, lds, &total);
+        #pragma unroll
+        for (int q = 0; q < kScanPer; ++q) {
+            const int x = v[q];
+            v[q] = run;
+            run += x;
+        }
+        store8(a, i0, n, v);
+        carry += total;
+    }
+}
+
+// Per-key tables from per-key counts (k < nk), in one launch:
+//   cnt  -> start (exclusive scan), end = start + cnt (end may be cnt itself);
+//           with coff: coff[k] = the key's first chunk of kCH, *n_chunks;
+//   cnt2 (optional) -> off2 (exclusive scan), *total2.
+constexpr int kCH = 64;     // pairs per scan chunk
+
+__global__ void __launch_bounds__(kScanThreads)
+k_keyscan(int nk, const int* cnt, int* __restrict__ start, int* end, int* __restrict__ coff,
+          int* __restrict__ n_chunks, const int* __restrict__ cnt2, int* __restrict__ off2,
+          int* __restrict__ total2) {
+    __shared__ int lds[2 * (kScanThreads / 64)];
+    int carry = 0, ccarry = 0, carry2 = 0;
+    for (int r0 = 0; r0 < nk; r0 += kScanRound) {
+        const int i0 = r0 + (int)threadIdx.x * kScanPer;
+        int v[kScanPer], c[kScanPer], u[kScanPer];
+        load8(cnt, i0, nk, v);
+        if (cnt2) load8(cnt2, i0, nk, u);
+        int s = 0, sc = 0, su = 0;
+        #pragma unroll
+        for (int q = 0; q < kScanPer; ++q) {
+            s += v[q];
+            c[q] = (v[q] + kCH - 1) / kCH;
+            sc += c[q];
+            if (cnt2) su += u[q];
+        }
+        int total;
+        int run = carry + block_exscan(s, lds, &total);
+        carry += total;
+        int crun = 0, urun = 0;
+        if (coff) {
+            crun = ccarry + block_exscan(sc, lds, &total);
+            ccarry += total;
+        }
+        if (cnt2) {
+            urun = carry2 + block_exscan(su, lds, &total);
+            carry2 += total;
+        }
+        int st[kScanPer], en[kScanPer];
+        #pragma unroll
+        for (int q = 0; q < kScanPer; ++q) {
+            st[q] = run;
+            run += v[q];
+            en[q] = run;
+            const int x = c[q];
+            c[q] = crun;
+            crun += x;
+            const int y = u[q];
+            u[q] = urun;
+            urun += y;
+        }
+        store8(start, i0, nk, st);
+        store8(end, i0, nk, en);
+        if (coff) store8(coff, i0, nk, c);
+        if (cnt2) store8(off2, i0, nk, u);
+    }
+    if (threadIdx.x == 0) {
+        if (coff) *n_chunks = ccarry;
+        if (cnt2) *total2 = carry2;
+    }
+}
+
+// Chunk tables: one wave per key writes its chunks (ckey, cbeg, cend).
+__global__ void __launch_bounds__(256)
+k_chunks(uint32_t nk, const int* __restrict__ start, const int* __restrict__ end,
+         const int* __restrict__ coff, int* __restrict__ ckey, int* __restrict__ cbeg,
+         int* __restrict__ cend) {
+    const uint32_t k = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (k >= nk) return;
+    const int s = start[k], e = end[k], c0 = coff[k];
+    for (int q = threadIdx.x & 63; s + q * kCH < e; q += 64) {
+        ckey[c0 + q] = (int)k;
+        cbeg[c0 + q] = s + q * kCH;
+        cend[c0 + q] = min(e, s + (q + 1) * kCH);
+    }
 }
 
 // [start, end) of every key present in a sorted key array.
@@ -149,75 +368,92 @@ __global__ void k_runs(int n, const uint32_t* __restrict__ keys, uint32_t nk,
     if (p == n - 1 || keys[p + 1] != k) end[k] = p + 1;
 }
 
-// tdrop decision from the arrival rank inside the cell's run.
-__global__ void k_tdrop(int n, const uint32_t* __restrict__ keys,
-                        const uint32_t* __restrict__ vals, uint32_t nk, int C,
-                        const int* __restrict__ start,
-                        const BlockDesc* __restrict__ bd, int level, int window,
-                        unsigned char* __restrict__ pass) {
+// ---------------------------------------------------------------------------
+// Temporal dropout (ssla_ref.py:190-195): a cell's counter c (uint8) takes
+// pre = c + rank (mod 256) for the record of arrival rank `rank`, and the
+// record passes when window <= 1 or pre % window == 0.  passes(c, r, w) is
+// the number of passing ranks in [0, r): with F(x) = the number of
+// u in [0, x) whose (u mod 256) is a multiple of w,
+//   F(x) = (x / 256) (255 / w + 1) + ceil((x mod 256) / w),
+// passes(c, r, w) = F(c + r) - F(c).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool tdrop_pass(unsigned c, unsigned rank, int window) {
+    return window <= 1 || ((c + rank) & 255u) % (unsigned)window == 0u;
+}
+
+__device__ __forceinline__ int tdrop_passes(unsigned c, int r, int window) {
+    if (window <= 1) return r;
+    const unsigned w = (unsigned)window, per = 255u / w + 1u;
+    auto F = [&](unsigned x) { return (x >> 8) * per + ((x & 255u) + w - 1u) / w; };
+    return (int)(F(c + (unsigned)r) - F(c));
+}
+
+// tdrop_s2 over the sorted records (position p, record g, rank r in the
+// key's run, counter c before the call): pass2[g], and the pass-2 list in
+// s2 order -- the record's place is the key's offset plus the number of
+// passing ranks below r.
+__global__ void __launch_bounds__(256)
+k_tdrop2(int n, const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
+         uint32_t nk, const int* __restrict__ start, const unsigned char* __restrict__ old,
+         const int* __restrict__ off, int window, unsigned char* __restrict__ pass,
+         int* __restrict__ list) {
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= n) return;
     const uint32_t k = keys[p];
-    const uint32_t g = vals[p];
-    if (k >= nk) { pass[g] = 0; return; }
-    const int b = (int)k / C, cell = (int)k % C;
-    const unsigned char* td = level == 2 ? bd[b].td2 : bd[b].td3;
-    const unsigned pre = ((unsigned)td[cell] + (unsigned)(p - start[k])) & 255u;
-    pass[g] = (window <= 1 || pre % (unsigned)window == 0u) ? 1 : 0;
+    const int g = (int)vals[p];
+    if (k >= nk) {
+        pass[g] = 0;
+        return;
+    }
+    const int r = p - start[k];
+    const unsigned c = old[k];
+    const bool take = tdrop_pass(c, (unsigned)r, window);
+    pass[g] = take ? 1 : 0;
+    if (take) list[off[k] + tdrop_passes(c, r, window)] = g;
 }
 
-__global__ void k_tdrop_commit(uint32_t nk, int C, const int* __restrict__ start,
-                               const int* __restrict__ end,
-                               const BlockDesc* __restrict__ bd, int level) {
-    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-    if (k >= nk) return;
-    const int len = end[k] - start[k];
-    if (len <= 0) return;
-    const int b = (int)k / C, cell = (int)k % C;
-    unsigned char* td = level == 2 ? bd[b].td2 : bd[b].td3;
-    td[cell] = (unsigned char)(((unsigned)td[cell] + (unsigned)len) & 255u);
-}
-
-constexpr int kCH = 64;     // pairs per scan chunk
-
-// Pair order without a pair sort.  Pair (record g, delta d) updates the
-// patch cell t = (y + 1 - d / 3, x + 1 - d % 3) of g's centre cell (x, y),
-// delta = (1 - dy) * 3 + (1 - dx), when t is on the grid.  Pairs are ordered
-// by t, and inside t by g: a record adds at most one pair to a cell, so this
-// is the stable order of (t, g * 9 + d).  With the records sorted stably by
-// centre cell (run [st, en) of ascending record ids per key), t's pair count
-// is the sum of the run lengths over its 3 x 3 neighbourhood, and a pair's
-// rank inside t is the number of records below g in those nine runs.
-
-// pair count of every key, written to `cnt` (the end array, finished by
-// k_pair_bounds once the start offsets are scanned)
-__global__ void k_pair_count(uint32_t nk, int C, int W, int H, const int* __restrict__ st,
-                             const int* __restrict__ en, int* __restrict__ cnt) {
+// Per s2 key: the counter before this call (old[k]), the counter after it,
+// the number of pass-2 records of the run (n2[k]) and the pair count of the
+// key (the run lengths of its 3 x 3 neighbourhood).
+__global__ void k_keys2(uint32_t nk, int C, int W, int H, const int* __restrict__ st,
+                        const int* __restrict__ en, const BlockDesc* __restrict__ bd, int window,
+                        unsigned char* __restrict__ old, int* __restrict__ n2,
+                        int* __restrict__ pcnt) {
     const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= nk) return;
     const int b = (int)t / C, cell = (int)t % C, ty = cell / W, tx = cell % W;
-    int n = 0;
+    const int len = en[t] - st[t];
+    unsigned char* td = bd[b].td2 + cell;
+    const unsigned c = *td;
+    old[t] = (unsigned char)c;
+    n2[t] = tdrop_passes(c, len, window);
+    *td = (unsigned char)((c + (unsigned)len) & 255u);
+    int np = 0;
     #pragma unroll
-    for (int oy = -1; oy <= 1; ++oy) {
+    for (int oy = -1; oy <= 1; ++oy)
         #pragma unroll
         for (int ox = -1; ox <= 1; ++ox) {
             const int sy = ty + oy, sx = tx + ox;
             if (sy < 0 || sy >= H || sx < 0 || sx >= W) continue;
             const int s = b * C + sy * W + sx;
-            n += en[s] - st[s];
+            np += en[s] - st[s];
         }
-    }
-    cnt[t] = n;
+    pcnt[t] = np;
 }
 
-// end = start + count, and the key's chunk count
-__global__ void k_pair_bounds(uint32_t nk, const int* __restrict__ pst, int* __restrict__ pen,
-                              int* __restrict__ ccnt) {
-    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= nk) return;
-    const int len = pen[t];
-    pen[t] = pst[t] + len;
-    ccnt[t] = (len + kCH - 1) / kCH;
+// Per s3 key: the number of pass-2 records of its four s2 cells (t3, the
+// length of its run in the s3 order) and how many of them pass tdrop_s3.
+__global__ void k_keys3a(uint32_t nk3, Geometry G, const int* __restrict__ n2,
+                         const BlockDesc* __restrict__ bd, int* __restrict__ t3,
+                         int* __restrict__ n3) {
+    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= nk3) return;
+    const int b = (int)k / G.C3, cell = (int)k % G.C3;
+    const int x = 2 * (cell % G.W3), y = 2 * (cell / G.W3);
+    const int s = b * G.C2 + y * G.W2 + x;
+    const int t = n2[s] + n2[s + 1] + n2[s + G.W2] + n2[s + G.W2 + 1];
+    t3[k] = t;
+    n3[k] = tdrop_passes(bd[b].td3[cell], t, G.window);
 }
 
 // Lower bound of g in vals[lo, lo + len): the index of the first value >= g.
@@ -234,6 +470,101 @@ __device__ __forceinline__ int lower_bound_u32(const uint32_t* __restrict__ vals
     }
     return lo;
 }
+
+// The s3 order of the pass-2 records without a sort: a pass-2 record's rank
+// in its s3 cell is the number of pass-2 records before it (record order)
+// in the four s2 runs of that cell.  In its own run that is the number of
+// passing ranks below its own; in the other three it is the number of
+// passing ranks below its lower bound there.  Slot = start3 + rank:
+// keys3 / vals3 is the s3 record order, key3g the record's s3 key.
+__global__ void __launch_bounds__(256)
+k_place3(const int* __restrict__ n_dev, const int* __restrict__ list,
+         const BlockDesc* __restrict__ bd, Geometry G, const int* __restrict__ cell2,
+         const int* __restrict__ sidx, const uint32_t* __restrict__ vals2,
+         const int* __restrict__ st2, const int* __restrict__ en2,
+         const unsigned char* __restrict__ old2, const int* __restrict__ st3,
+         uint32_t* __restrict__ keys3, uint32_t* __restrict__ vals3,
+         uint32_t* __restrict__ key3g) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= *n_dev) return;
+    const int g = list[j];
+    const int b = find_block(bd, G.nb, g);
+    const int cell = cell2[g], x = cell % G.W2, y = cell / G.W2;
+    const int k2 = b * G.C2 + cell;
+    const int x0 = x & ~1, y0 = y & ~1;
+    const uint32_t k3 = (uint32_t)(b * G.C3 + (y >> 1) * G.W3 + (x >> 1));
+    int rank = 0;
+    #pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int s = b * G.C2 + (y0 + (q >> 1)) * G.W2 + x0 + (q & 1);
+        const int lo = st2[s];
+        const int r = s == k2 ? sidx[g] - lo
+                              : lower_bound_u32(vals2, lo, en2[s] - lo, (uint32_t)g) - lo;
+        rank += tdrop_passes(old2[s], r, G.window);
+    }
+    const int slot = st3[k3] + rank;
+    if (slot < 0 || slot >= *n_dev) return;     // (ranks are a permutation of [0, n))
+    keys3[slot] = k3;
+    vals3[slot] = (uint32_t)g;
+    key3g[g] = k3;
+}
+
+// tdrop_s3 over the s3 record order: pass3, the pass-3 list (placed as in
+// k_tdrop2; the counters are committed afterwards by k_keys3b) and, for the
+// head, each s3 key's last owned pass-3 record (largest record index) and
+// their number.
+__global__ void __launch_bounds__(256)
+k_tdrop3(const int* __restrict__ n_dev, const uint32_t* __restrict__ keys,
+         const uint32_t* __restrict__ vals, uint32_t nk, int C, const int* __restrict__ start,
+         const int* __restrict__ off, const BlockDesc* __restrict__ bd, int window,
+         const unsigned char* __restrict__ owner, int have_head, unsigned char* __restrict__ pass,
+         int* __restrict__ list, int* __restrict__ last, int* __restrict__ count) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= *n_dev) return;
+    const uint32_t k = keys[p];
+    if (k >= nk) return;
+    const int g = (int)vals[p];
+    const int b = (int)k / C, cell = (int)k % C;
+    const int r = p - start[k];
+    const unsigned c = bd[b].td3[cell];
+    const bool take = tdrop_pass(c, (unsigned)r, window);
+    pass[g] = take ? 1 : 0;
+    if (!take) return;
+    list[off[k] + tdrop_passes(c, r, window)] = g;
+    if (have_head && owner[g]) {
+        atomicMax(last + k, g);
+        atomicAdd(count + k, 1);
+    }
+}
+
+// Per s3 key: commit the counter and the pair count of the key.
+__global__ void k_keys3b(uint32_t nk3, Geometry G, const int* __restrict__ t3,
+                         const BlockDesc* __restrict__ bd, int* __restrict__ pcnt) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nk3) return;
+    const int b = (int)t / G.C3, cell = (int)t % G.C3, ty = cell / G.W3, tx = cell % G.W3;
+    unsigned char* td = bd[b].td3 + cell;
+    *td = (unsigned char)(((unsigned)*td + (unsigned)t3[t]) & 255u);
+    int np = 0;
+    #pragma unroll
+    for (int oy = -1; oy <= 1; ++oy)
+        #pragma unroll
+        for (int ox = -1; ox <= 1; ++ox) {
+            const int sy = ty + oy, sx = tx + ox;
+            if (sy < 0 || sy >= G.H3 || sx < 0 || sx >= G.W3) continue;
+            np += t3[b * G.C3 + sy * G.W3 + sx];
+        }
+    pcnt[t] = np;
+}
+
+// Pair order without a pair sort.  Pair (record g, delta d) updates the
+// patch cell t = (y + 1 - d / 3, x + 1 - d % 3) of g's centre cell (x, y),
+// delta = (1 - dy) * 3 + (1 - dx), when t is on the grid.  Pairs are ordered
+// by t, and inside t by g: a record adds at most one pair to a cell, so this
+// is the stable order of (t, g * 9 + d).  With the records sorted stably by
+// centre cell (run [st, en) of ascending record ids per key), t's pair count
+// is the sum of the run lengths over its 3 x 3 neighbourhood, and a pair's
+// rank inside t is the number of records below g in those nine runs.
 
 constexpr int kRankWindow = 256;   // widest neighbour window searched cooperatively
 
@@ -253,10 +584,11 @@ constexpr int kRankWindow = 256;   // widest neighbour window searched cooperati
 // (ds_bpermute).  A window wider than kRankWindow is searched per lane inside
 // its bounds.  Other waves (cell boundaries, the tail) search per lane.
 __global__ void __launch_bounds__(256)
-k_pair_rank(int n, const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
-            uint32_t nk, int C, int W, int H, const int* __restrict__ st,
-            const int* __restrict__ en, const int* __restrict__ pst,
+k_pair_rank(int n_max, const int* __restrict__ n_dev, const uint32_t* __restrict__ keys,
+            const uint32_t* __restrict__ vals, uint32_t nk, int C, int W, int H,
+            const int* __restrict__ st, const int* __restrict__ en, const int* __restrict__ pst,
             int* __restrict__ pos, int* __restrict__ pair_rec) {
+    const int n = n_dev ? *n_dev : n_max;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     const int lane = threadIdx.x & 63;
     const bool valid = i < n;
@@ -273,7 +605,9 @@ k_pair_rank(int n, const uint32_t* __restrict__ keys, const uint32_t* __restrict
     }
     const int b = (int)k / C, cell = (int)k % C, y = cell / W, x = cell % W;
     const int own = i - st[k];
-    int hs[5][3];                  // hs[row][dx + 1]: runs (row, dx - 1 .. dx + 1)
+    // r25[c]: the number of records below g in run c of the 5 x 5 block
+    // (c = 5 row + column, c = 12 the record's own run)
+    int r25[25];
     if (together) {
         // lanes c and 32 + c (c < 25): run c's bounds for the first and last id
         const uint32_t g_first = (uint32_t)__builtin_amdgcn_readlane((int)g, 0);
@@ -288,79 +622,85 @@ k_pair_rank(int n, const uint32_t* __restrict__ keys, const uint32_t* __restrict
                 bnd = lower_bound_u32(vals, s0, en[s] - s0, lane < 32 ? g_first : g_last);
             }
         }
+        // the first 64 values of every window, all loads in flight together
+        uint32_t pv[25];
         #pragma unroll
-        for (int row = 0; row < 5; ++row) {
-            int r[5];
+        for (int c = 0; c < 25; ++c) {
+            const int wa = __builtin_amdgcn_readlane(bnd, c);
+            const int we = __builtin_amdgcn_readlane(bnd, 32 + c);
+            pv[c] = (c != 12 && we - wa <= kRankWindow && wa + lane < we) ? vals[wa + lane]
+                                                                          : 0xffffffffu;
+        }
+        // values below g among 64 ascending lane values (six steps across lanes)
+        auto below = [&](uint32_t v) {
+            int lo = 0;
             #pragma unroll
-            for (int j = 0; j < 5; ++j) {
-                const int c = row * 5 + j;
-                if (c == 12) {
-                    r[j] = own;
-                    continue;
-                }
-                const int wa = __builtin_amdgcn_readlane(bnd, c);
-                const int we = __builtin_amdgcn_readlane(bnd, 32 + c);
-                const int ws = __builtin_amdgcn_readlane(s0, c);
-                int cnt = 0;
-                if (we - wa > kRankWindow) {
-                    cnt = lower_bound_u32(vals, wa, we - wa, g) - wa;
-                } else {
-                    for (int base = wa; base < we; base += 64) {
-                        const uint32_t v = base + lane < we ? vals[base + lane] : 0xffffffffu;
-                        int lo = 0;
-                        #pragma unroll
-                        for (int step = 32; step > 0; step >>= 1) {
-                            const uint32_t p = (uint32_t)__builtin_amdgcn_ds_bpermute(
-                                (lo + step - 1) << 2, (int)v);
-                            if (p < g) lo += step;
-                        }
-                        const uint32_t p = (uint32_t)__builtin_amdgcn_ds_bpermute(lo << 2, (int)v);
-                        cnt += lo + (p < g ? 1 : 0);
-                    }
-                }
-                r[j] = wa - ws + cnt;
+            for (int step = 32; step > 0; step >>= 1) {
+                const uint32_t q = (uint32_t)__builtin_amdgcn_ds_bpermute((lo + step - 1) << 2,
+                                                                          (int)v);
+                if (q < g) lo += step;
             }
-            #pragma unroll
-            for (int c = 0; c < 3; ++c) hs[row][c] = r[c] + r[c + 1] + r[c + 2];
+            const uint32_t q = (uint32_t)__builtin_amdgcn_ds_bpermute(lo << 2, (int)v);
+            return lo + (q < g ? 1 : 0);
+        };
+        #pragma unroll
+        for (int c = 0; c < 25; ++c) {
+            if (c == 12) {
+                r25[c] = own;
+                continue;
+            }
+            const int wa = __builtin_amdgcn_readlane(bnd, c);
+            const int we = __builtin_amdgcn_readlane(bnd, 32 + c);
+            const int ws = __builtin_amdgcn_readlane(s0, c);
+            int cnt;
+            if (we - wa > kRankWindow) {
+                cnt = lower_bound_u32(vals, wa, we - wa, g) - wa;
+            } else {
+                cnt = below(pv[c]);
+                for (int base = wa + 64; base < we; base += 64)
+                    cnt += below(base + lane < we ? vals[base + lane] : 0xffffffffu);
+            }
+            r25[c] = wa - ws + cnt;
         }
     } else {
+        // per lane: the 24 binary searches advance together, one step each
+        // per pass, so their loads are in flight at once
+        int lo[25], len[25];
         #pragma unroll
-        for (int row = 0; row < 5; ++row) {
-            const int sy = y + row - 2;
-            int lo[5], len[5], r[5];
-            #pragma unroll
-            for (int j = 0; j < 5; ++j) {
-                const int sx = x + j - 2;
-                const bool on = (row != 2 || j != 2) && sy >= 0 && sy < H && sx >= 0 && sx < W;
-                const int s = on ? b * C + sy * W + sx : 0;
-                lo[j] = r[j] = on ? st[s] : 0;
-                len[j] = on ? en[s] - lo[j] : 0;
-            }
-            // one step of each of the five searches per pass
-            for (;;) {
-                int active = 0;
-                #pragma unroll
-                for (int j = 0; j < 5; ++j) {
-                    if (len[j] > 0) {
-                        const int half = len[j] >> 1;
-                        if (vals[lo[j] + half] < g) {
-                            lo[j] += half + 1;
-                            len[j] -= half + 1;
-                        } else {
-                            len[j] = half;
-                        }
-                    }
-                    active |= len[j];
-                }
-                if (!active) break;
-            }
-            #pragma unroll
-            for (int j = 0; j < 5; ++j) r[j] = lo[j] - r[j];
-            if (row == 2) r[2] = own;
-            #pragma unroll
-            for (int c = 0; c < 3; ++c) hs[row][c] = r[c] + r[c + 1] + r[c + 2];
+        for (int c = 0; c < 25; ++c) {
+            const int sy = y + c / 5 - 2, sx = x + c % 5 - 2;
+            const bool on = c != 12 && sy >= 0 && sy < H && sx >= 0 && sx < W;
+            const int s = on ? b * C + sy * W + sx : 0;
+            lo[c] = r25[c] = on ? st[s] : 0;
+            len[c] = on ? en[s] - lo[c] : 0;
         }
+        for (;;) {
+            int active = 0;
+            #pragma unroll
+            for (int c = 0; c < 25; ++c) {
+                if (len[c] > 0) {
+                    const int half = len[c] >> 1;
+                    if (vals[lo[c] + half] < g) {
+                        lo[c] += half + 1;
+                        len[c] -= half + 1;
+                    } else {
+                        len[c] = half;
+                    }
+                }
+                active |= len[c];
+            }
+            if (!active) break;
+        }
+        #pragma unroll
+        for (int c = 0; c < 25; ++c) r25[c] = lo[c] - r25[c];
+        r25[12] = own;
     }
+    int hs[5][3];                  // hs[row][dx + 1]: runs (row, dx - 1 .. dx + 1)
+    #pragma unroll
+    for (int row = 0; row < 5; ++row)
+        #pragma unroll
+        for (int c = 0; c < 3; ++c)
+            hs[row][c] = r25[5 * row + c] + r25[5 * row + c + 1] + r25[5 * row + c + 2];
     #pragma unroll
     for (int d = 0; d < kPatch; ++d) {
         const int dy = 1 - d / 3, dx = 1 - d % 3;      // target offset from the centre
@@ -494,33 +834,6 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 // projection has just left up to 0.7 GB of them in the caches; streaming
 // them past the L2 made pass A 35-40% faster and pass C 2-9%.
 // ---------------------------------------------------------------------------
-// chunk table of every key: ckey / cbeg / cend, count in *n_chunks
-// One thread per chunk slot j < max_chunks: its key is the last k with
-// coff[k] <= j among keys that have chunks (binary search over the
-// exclusive scan of the chunk counts).
-__global__ void k_chunk_fill(uint32_t nk, int max_chunks, const int* __restrict__ start,
-                             const int* __restrict__ end, const int* __restrict__ cnt,
-                             const int* __restrict__ coff, int* __restrict__ ckey,
-                             int* __restrict__ cbeg, int* __restrict__ cend,
-                             int* __restrict__ n_chunks) {
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    const int total = coff[nk - 1] + cnt[nk - 1];
-    if (j == 0) *n_chunks = total;
-    if (j >= total || j >= max_chunks) return;
-    int lo = 0, hi = (int)nk - 1;          // largest k with coff[k] <= j
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (coff[mid] <= j) lo = mid; else hi = mid - 1;
-    }
-    // (a key without chunks shares its coff with the next key, so the
-    // largest such k always has chunks; the step below only guards that)
-    while (lo + 1 < (int)nk && cnt[lo] == 0) ++lo;
-    const int c = j - coff[lo], s = start[lo], e = end[lo];
-    ckey[j] = lo;
-    cbeg[j] = s + c * kCH;
-    cend[j] = min(e, s + (c + 1) * kCH);
-}
-
 template <int OUT>
 __global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
 k_scan_summary(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
@@ -558,8 +871,8 @@ k_scan_summary(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
 template <int OUT>
 __global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
 k_scan_carry(int C, const int* __restrict__ start, const int* __restrict__ end,
-             const int* __restrict__ coff, const int* __restrict__ cnt,
-             const BlockDesc* __restrict__ bd, int li, const float* __restrict__ Asum,
+             const int* __restrict__ coff, const BlockDesc* __restrict__ bd, int li,
+             const float* __restrict__ Asum,
              const float* __restrict__ Bsum, float* __restrict__ Hs) {
     const int k = blockIdx.x;
     const int c = threadIdx.x;
@@ -567,7 +880,7 @@ k_scan_carry(int C, const int* __restrict__ start, const int* __restrict__ end,
     const int b = k / C, cell = k % C;
     float* hp = bd[b].hidden[li] + (size_t)cell * OUT + c;
     float h = *hp;
-    const int c0 = coff[k], nc = cnt[k];
+    const int c0 = coff[k], nc = (end[k] - start[k] + kCH - 1) / kCH;
     constexpr int U = 32;        // chunks whose maps are in flight together
     for (int q0 = 0; q0 < nc; q0 += U) {
         float a[U], b[U];
@@ -916,36 +1229,6 @@ k_head(const int* __restrict__ n_dev, const int* __restrict__ list,
     }
 }
 
-// Per s3 key, from its run in the s3 record sort (ring order): the last
-// owned pass-3 record (-1 if none) and the number of owned pass-3 records.
-// One wave per key, four keys per workgroup.
-__global__ void __launch_bounds__(256)
-k_pred_runs(uint32_t nk, const int* __restrict__ start, const int* __restrict__ end,
-            const uint32_t* __restrict__ vals, const unsigned char* __restrict__ pass3,
-            const unsigned char* __restrict__ owner, int* __restrict__ last,
-            int* __restrict__ count) {
-    const uint32_t k = blockIdx.x * 4u + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (k >= nk) return;
-    const int s = start[k], e = end[k];
-    int lst = -1, cnt = 0;
-    for (int p = s + lane; p < e; p += 64) {
-        const int g = (int)vals[p];
-        if (pass3[g] && owner[g]) {
-            lst = max(lst, g);
-            ++cnt;
-        }
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-        lst = max(lst, __shfl_xor(lst, off, 64));
-        cnt += __shfl_xor(cnt, off, 64);
-    }
-    if (lane == 0) {
-        last[k] = lst;
-        count[k] = cnt;
-    }
-}
-
 __global__ void k_pred_write(const int* __restrict__ n_dev, const int* __restrict__ list,
                              const unsigned char* __restrict__ owner,
                              const uint32_t* __restrict__ key3_by_g,
@@ -1046,8 +1329,13 @@ struct Workspace {
     int *cell2, *pos2, *pos3, *list2, *list3, *counts;
     int *st2, *en2, *st3, *en3, *pst2, *pen2, *pst3, *pen3, *last3, *cnt3;
     int *prec2, *prec3;                        // record of each sorted pair
-    int *ccnt2, *coff2, *ccnt3, *coff3;        // chunks per key, offsets
+    int *coff2, *coff3;                        // first chunk of every key
     int *ckey2, *cbeg2, *cend2, *ckey3, *cbeg3, *cend3;
+    int *sidx;                                 // sorted s2 position of every record
+    int *n2, *t3, *n3;                         // pass-2 records per s2 / s3 key, pass-3 per s3 key
+    int *off2, *off3;                          // first pass-2 / pass-3 list slot of every key
+    int *bh;                                   // radix-sort tile histograms
+    unsigned char* old2;                       // s2 counters before the call
     float *Asum, *Bsum, *Hs;
     int max_chunks = 0;
     unsigned char *owner, *pass2, *pass3;
@@ -1059,11 +1347,8 @@ struct Workspace {
     hipStream_t side = nullptr;        // s3 ordering, concurrent with L4 and L5
     hipEvent_t s2_ordered = nullptr;   // s2 tables and pass2 are complete
     hipEvent_t s3_ordered = nullptr;   // s3 tables and pass3 are complete
-    hipEvent_t n2_ready = nullptr;     // the pass2 count has reached n2_host
-    int* n2_host = nullptr;            // pinned copy of the pass2 count
     hipEvent_t side_done = nullptr;    // the side stream's last work of a call
-    void* temp;
-    size_t temp_bytes;
+    int bh_ints = 0;
     float* packed = nullptr;           // fragment-order weight copies (packed_weight_floats_d)
     // What `packed` was built from: the layer weight pointers and the weight
     // generation (bumped by every library call that may write device memory).
@@ -1086,33 +1371,6 @@ Workspace g_ws;
 
 size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 
-// Stable LSD radix sort of (key, value) pairs on bits [0, bits).  rocPRIM's
-// default configuration sorts up to 1 M pairs of 32-bit keys by block sort
-// plus a merge pass per doubling (16 launches at 200 k records); the
-// Onesweep path needs one launch per 8 key bits plus a histogram.  Its
-// default tiles (1024 threads x 16 keys) give a 200 k-record sort 13
-// workgroups; below 1 M records 512 x 8 tiles spread it over more CUs
-// (80x64 ordering 0.198 -> 0.167 ms; at 3.2 M records the default was
-// faster).
-using SortConfig = rocprim::radix_sort_config<rocprim::default_config, rocprim::default_config,
-                                              rocprim::default_config, 0>;
-using SortConfigSmall = rocprim::radix_sort_config<
-    rocprim::default_config, rocprim::default_config,
-    rocprim::radix_sort_onesweep_config<rocprim::kernel_config<512, 8>,
-                                        rocprim::kernel_config<512, 8>, 8,
-                                        rocprim::block_radix_rank_algorithm::match>,
-    0>;
-constexpr int kSmallSort = 1 << 20;
-
-hipError_t sort_pairs(void* temp, size_t& bytes, const uint32_t* ki, uint32_t* ko,
-                      const uint32_t* vi, uint32_t* vo, int n, int bits, hipStream_t st) {
-    if (n < kSmallSort)
-        return rocprim::radix_sort_pairs<SortConfigSmall>(temp, bytes, ki, ko, vi, vo, (size_t)n,
-                                                          0u, (unsigned)bits, st);
-    return rocprim::radix_sort_pairs<SortConfig>(temp, bytes, ki, ko, vi, vo, (size_t)n, 0u,
-                                                 (unsigned)bits, st);
-}
-
 int ensure_workspace(int E, int nkeys) {
     if (E <= g_ws.cap && nkeys <= g_ws.cap_keys) return SSLA_OK;
     if (g_ws.base) {
@@ -1126,23 +1384,9 @@ int ensure_workspace(int E, int nkeys) {
     const int cap = std::max(E, std::max(g_ws.cap, 1024));
     const int ck = std::max(nkeys, g_ws.cap_keys);
     const size_t P = (size_t)cap * kPatch;
-    // temp storage: radix sort of the records, the flagged selections and the
-    // key scans.
-    size_t t_sort = 0, t_sel = 0;
-    HIPCHK(sort_pairs(nullptr, t_sort, nullptr, nullptr, nullptr, nullptr, cap, 32, nullptr));
-    {
-        size_t t_small = 0;         // the small-sort tiles below the size switch
-        HIPCHK(sort_pairs(nullptr, t_small, nullptr, nullptr, nullptr, nullptr,
-                          std::min(cap, kSmallSort - 1), 32, nullptr));
-        t_sort = std::max(t_sort, t_small);
-    }
-    HIPCHK(hipcub::DeviceSelect::Flagged(nullptr, t_sel, hipcub::CountingInputIterator<int>(0),
-                                          (unsigned char*)nullptr, (int*)nullptr,
-                                          (int*)nullptr, cap));
-    size_t t_scan = 0;
-    HIPCHK(hipcub::DeviceScan::ExclusiveSum(nullptr, t_scan, (int*)nullptr, (int*)nullptr, ck));
-    const size_t temp = std::max(std::max(t_sort, t_sel), t_scan);
     const size_t mc = P / kCH + (size_t)ck + 1;    // chunk bound: full chunks + one tail per key
+    // radix-sort tile histograms: (1 << kRMaxBits) digits x tiles
+    const size_t bh = ((size_t)1 << kRMaxBits) * (size_t)((cap + kRTile - 1) / kRTile);
     struct Item { void** dst; size_t bytes; };
     Workspace& w = g_ws;
     std::vector<Item> items = {
@@ -1179,10 +1423,16 @@ int ensure_workspace(int E, int nkeys) {
         {(void**)&w.key3g, sizeof(uint32_t) * (size_t)cap},
         {(void**)&w.prec2, sizeof(int) * P},
         {(void**)&w.prec3, sizeof(int) * P},
-        {(void**)&w.ccnt2, sizeof(int) * (size_t)ck},
+        {(void**)&w.sidx, sizeof(int) * (size_t)cap},
         {(void**)&w.coff2, sizeof(int) * (size_t)ck},
-        {(void**)&w.ccnt3, sizeof(int) * (size_t)ck},
         {(void**)&w.coff3, sizeof(int) * (size_t)ck},
+        {(void**)&w.n2, sizeof(int) * (size_t)ck},
+        {(void**)&w.t3, sizeof(int) * (size_t)ck},
+        {(void**)&w.n3, sizeof(int) * (size_t)ck},
+        {(void**)&w.off2, sizeof(int) * (size_t)ck},
+        {(void**)&w.off3, sizeof(int) * (size_t)ck},
+        {(void**)&w.bh, sizeof(int) * bh},
+        {(void**)&w.old2, (size_t)ck},
         {(void**)&w.ckey2, sizeof(int) * mc},
         {(void**)&w.cbeg2, sizeof(int) * mc},
         {(void**)&w.cend2, sizeof(int) * mc},
@@ -1193,7 +1443,6 @@ int ensure_workspace(int E, int nkeys) {
         {(void**)&w.Bsum, sizeof(float) * mc * SSLA_C3},
         {(void**)&w.Hs, sizeof(float) * mc * SSLA_C3},
         {(void**)&w.bd, sizeof(BlockDesc) * SSLA_MAX_BLOCKS},
-        {(void**)&w.temp, temp},
     };
     size_t total = 0;
     for (auto& it : items) total += align_up(it.bytes);
@@ -1211,9 +1460,7 @@ int ensure_workspace(int E, int nkeys) {
         HIPCHK(hipEventCreateWithFlags(&w.done, hipEventDisableTiming));
         HIPCHK(hipEventCreateWithFlags(&w.s2_ordered, hipEventDisableTiming));
         HIPCHK(hipEventCreateWithFlags(&w.s3_ordered, hipEventDisableTiming));
-        HIPCHK(hipEventCreateWithFlags(&w.n2_ready, hipEventDisableTiming));
         HIPCHK(hipEventCreateWithFlags(&w.side_done, hipEventDisableTiming));
-        HIPCHK(hipHostMalloc((void**)&w.n2_host, sizeof(int), hipHostMallocDefault));
         HIPCHK(hipStreamCreateWithFlags(&w.side, hipStreamNonBlocking));
         HIPCHK(hipMalloc(&w.packed, sizeof(float) * packed_weight_floats_d()));
     }
@@ -1221,7 +1468,7 @@ int ensure_workspace(int E, int nkeys) {
     w.bytes = total;
     w.cap = cap;
     w.cap_keys = ck;
-    w.temp_bytes = temp;
+    w.bh_ints = (int)bh;
     w.max_chunks = (int)mc;
     return SSLA_OK;
 }
@@ -1404,55 +1651,73 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     }
     const PackedWeights& pk = w.pk;
     MARK();
-    const int bits2 = bits_for(nk2), bits3 = bits_for(nk3);
-    size_t tb = w.temp_bytes;
-
-    // run bounds start at zero; k_runs fills them where a key occurs
+    // per-call fills: run bounds of the s2 keys (k_runs writes those that
+    // occur), the list and chunk counters, the prediction-grid writers
     {
         FillSet f{};
-        int* arr[kFills] = {w.st2, w.en2, w.st3, w.en3};
-        const int len[kFills] = {(int)nk2, (int)nk2, (int)nk3, (int)nk3};
+        int* arr[kFills] = {w.st2, w.en2, w.counts, w.last3, w.cnt3};
+        const int len[kFills] = {(int)nk2, (int)nk2, 8, have_head ? (int)nk3 : 0,
+                                 have_head ? (int)nk3 : 0};
+        const int val[kFills] = {0, 0, 0, -1, 0};
         for (int i = 0; i < kFills; ++i) {
             f.p[i] = arr[i];
             f.n[i] = len[i];
-            f.v[i] = 0;
+            f.v[i] = val[i];
         }
-        hipLaunchKernelGGL(k_fill_set, dim3(grid1(nk2, 256), kFills), dim3(256), 0, st, f);
+        hipLaunchKernelGGL(k_fill_set, dim3(grid1(std::max<int>((int)nk2, 8), 256), kFills),
+                           dim3(256), 0, st, f);
     }
-    // ---- decode; tdrop_s2 from a stable sort of records by centre cell ----
+    // ---- decode; stable radix sort of the records by s2 key ------------------
     hipLaunchKernelGGL(k_decode, dim3(grid1(E, kDecRec)), dim3(256), 0, st, E, w.bd, G, w.X0,
                        w.cell2, w.owner, w.ka, w.va);
-    HIPCHK(sort_pairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, E, bits2, st));
-    hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, nk2, w.st2, w.en2);
-    hipLaunchKernelGGL(k_tdrop, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, w.vb, nk2,
-                       G.C2, w.st2, w.bd, 2, G.window, w.pass2);
-    hipLaunchKernelGGL(k_tdrop_commit, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, G.C2,
-                       w.st2, w.en2, w.bd, 2);
-    // ---- s2 pair order and chunk tables, from the record order ---------------
-    hipLaunchKernelGGL(k_pair_count, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, G.C2, G.W2,
-                       G.H2, w.st2, w.en2, w.pen2);
-    HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.pen2, w.pst2, (int)nk2, st));
-    hipLaunchKernelGGL(k_pair_bounds, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, w.pst2,
-                       w.pen2, w.ccnt2);
-    hipLaunchKernelGGL(k_pair_rank, dim3(grid1(E, 256)), dim3(256), 0, st, E, w.kb, w.vb, nk2,
-                       G.C2, G.W2, G.H2, w.st2, w.en2, w.pst2, w.pos2, w.prec2);
-    HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt2, w.coff2, (int)nk2, st));
-    hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(w.max_chunks, 256)), dim3(256), 0, st, nk2,
-                       w.max_chunks, w.pst2,
-                       w.pen2, w.ccnt2, w.coff2, w.ckey2, w.cbeg2, w.cend2, w.counts + 2);
-    // the pass2 record list
-    HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
-                                          w.pass2, w.list2, w.counts + 0, E, st));
-    // The s3 ordering needs only pass2 and the centre cells, so it runs on the
-    // side stream while L4 and L5 run here; L6 waits for it.  Nothing on this
-    // stream touches the sort buffers, the scratch storage or any s3 table
-    // until then.  The pass2 count goes to the host first: the s3 pair order
-    // is sized by it once L4 and L5 are queued.
+    const int bits2 = bits_for(nk2);
+    const int passes = (bits2 + kRMaxBits - 1) / kRMaxBits;
+    const int T = (int)grid1(E, kRTile);
+    uint32_t *kin = w.ka, *vin = nullptr, *kout = w.kb, *vout = w.vb;
+    for (int ps = 0, shift = 0; ps < passes; ++ps) {
+        const int bits = (bits2 - shift + (passes - ps) - 1) / (passes - ps);
+        if ((1 << bits) * T > w.bh_ints) {
+            set_error("drain: radix histogram larger than its workspace");
+            return SSLA_ERR_STATE;
+        }
+        hipLaunchKernelGGL(k_rs_hist, dim3(T), dim3(kRThreads), 0, st, E, kin, shift, bits, T,
+                           w.bh);
+        hipLaunchKernelGGL(k_exscan, dim3(1), dim3(kScanThreads), 0, st, (1 << bits) * T, w.bh);
+        hipLaunchKernelGGL(k_rs_scatter, dim3(T), dim3(kRThreads), 0, st, E, kin, vin, kout, vout,
+                           ps == passes - 1 ? w.sidx : nullptr, shift, bits, T, w.bh);
+        shift += bits;
+        // the next pass writes the pair of buffers this pass read from
+        uint32_t* const k2 = kout == w.kb ? w.ka : w.kb;
+        uint32_t* const v2 = vout == w.vb ? w.va : w.vb;
+        kin = kout;
+        vin = vout;
+        kout = k2;
+        vout = v2;
+    }
+    // the sorted s2 order, and the buffers the s3 order is placed in
+    uint32_t* const K2 = kin;
+    uint32_t* const V2 = vin;
+    uint32_t* const K3 = kout;
+    uint32_t* const V3 = vout;
+    // ---- counters, tdrop_s2, the pass-2 list, s2 pair and chunk tables -----
+    hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, st, E, K2, nk2, w.st2, w.en2);
+    hipLaunchKernelGGL(k_keys2, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, G.C2, G.W2, G.H2,
+                       w.st2, w.en2, w.bd, G.window, w.old2, w.n2, w.pen2);
+    hipLaunchKernelGGL(k_keyscan, dim3(1), dim3(kScanThreads), 0, st, (int)nk2, w.pen2, w.pst2,
+                       w.pen2, w.coff2, w.counts + 2, w.n2, w.off2, w.counts + 0);
+    hipLaunchKernelGGL(k_tdrop2, dim3(grid1(E, 256)), dim3(256), 0, st, E, K2, V2, nk2, w.st2,
+                       w.old2, w.off2, G.window, w.pass2, w.list2);
+    // The s3 ordering needs only the s2 order, pass2 and the old counters, so
+    // it runs on the side stream while the s2 pair ranks, L4 and L5 run here;
+    // L6 waits for it.  Every launch is sized by E; the pass-2 count stays on
+    // the device.  The side stream's launches are enqueued after L4's.
     HIPCHK(hipEventRecord(w.s2_ordered, st));
     hipStream_t s3 = w.side;
     HIPCHK(hipStreamWaitEvent(s3, w.s2_ordered, 0));
-    HIPCHK(hipMemcpyAsync(w.n2_host, w.counts + 0, sizeof(int), hipMemcpyDeviceToHost, s3));
-    HIPCHK(hipEventRecord(w.n2_ready, s3));
+    hipLaunchKernelGGL(k_pair_rank, dim3(grid1(E, 256)), dim3(256), 0, st, E, (const int*)nullptr,
+                       K2, V2, nk2, G.C2, G.W2, G.H2, w.st2, w.en2, w.pst2, w.pos2, w.prec2);
+    hipLaunchKernelGGL(k_chunks, dim3(grid1(nk2, 4)), dim3(256), 0, st, nk2, w.pst2, w.pen2,
+                       w.coff2, w.ckey2, w.cbeg2, w.cend2);
     MARK();
     const LayerWeightsS2S3* L = cfg->layers[0];
     const unsigned tilesE = grid1(E, kTM);
@@ -1465,7 +1730,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
     MARK();
     hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
-                       w.coff2, w.ccnt2, w.bd, 0, w.Asum, w.Bsum, w.Hs);
+                       w.coff2, w.bd, 0, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, all, w.QVG);
@@ -1474,6 +1739,31 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, pk.po[0],
                        L[0].ln_gamma, L[0].ln_beta, w.X1);
     MARK();
+    // ---- [side] the s3 record order, tdrop_s3, s3 pair and chunk tables ---
+    // (enqueued after L4's launches: the host needs a few microseconds per
+    // launch, and L4 keeps the device busy meanwhile)
+    hipLaunchKernelGGL(k_keys3a, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, G, w.n2, w.bd,
+                       w.t3, w.n3);
+    hipLaunchKernelGGL(k_keyscan, dim3(1), dim3(kScanThreads), 0, s3, (int)nk3, w.t3, w.st3,
+                       w.en3, (int*)nullptr, (int*)nullptr, w.n3, w.off3, w.counts + 1);
+    hipLaunchKernelGGL(k_place3, dim3(grid1(E, 256)), dim3(256), 0, s3, (const int*)(w.counts + 0),
+                       w.list2, w.bd, G, w.cell2, w.sidx, V2, w.st2, w.en2, w.old2, w.st3, K3, V3,
+                       w.key3g);
+    hipLaunchKernelGGL(k_tdrop3, dim3(grid1(E, 256)), dim3(256), 0, s3, (const int*)(w.counts + 0),
+                       K3, V3, nk3, G.C3, w.st3, w.off3, w.bd, G.window, w.owner,
+                       have_head ? 1 : 0, w.pass3, w.list3, w.last3, w.cnt3);
+    hipLaunchKernelGGL(k_keys3b, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, G, w.t3, w.bd,
+                       w.pen3);
+    hipLaunchKernelGGL(k_keyscan, dim3(1), dim3(kScanThreads), 0, s3, (int)nk3, w.pen3, w.pst3,
+                       w.pen3, w.coff3, w.counts + 3, (const int*)nullptr, (int*)nullptr,
+                       (int*)nullptr);
+    hipLaunchKernelGGL(k_chunks, dim3(grid1(nk3, 4)), dim3(256), 0, s3, nk3, w.pst3, w.pen3,
+                       w.coff3, w.ckey3, w.cbeg3, w.cend3);
+    hipLaunchKernelGGL(k_pair_rank, dim3(grid1(E, 256)), dim3(256), 0, s3, E,
+                       (const int*)(w.counts + 0), K3, V3, nk3, G.C3, G.W3, G.H3, w.st3, w.en3,
+                       w.pst3, w.pos3, w.prec3);
+    HIPCHK(hipEventRecord(w.s3_ordered, s3));
+    HIPCHK(hipGetLastError());
     // ---- L5: 48 -> 48, state for all records, output for pass2 ---------------
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, pk.pp[1], w.QVG);
@@ -1482,7 +1772,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
     MARK();
     hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
-                       w.coff2, w.ccnt2, w.bd, 1, w.Asum, w.Bsum, w.Hs);
+                       w.coff2, w.bd, 1, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, w.pass2, w.QVG);
@@ -1491,53 +1781,6 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, pk.po[1],
                        L[1].ln_gamma, L[1].ln_beta, w.X2);
     MARK();
-    // ---- [side] s3 pair order over the pass2 records only ------------------------
-    // L4 and L5 are queued; the host waits for the pass2 count (known once
-    // tdrop_s2 has run) so the s3 pair sort covers 9 * N2 pairs rather than
-    // 9 * E, most of which would be placeholders.
-    {
-        HIPCHK(hipEventSynchronize(w.n2_ready));
-        const int N2 = *w.n2_host;
-        if (N2 < 0 || N2 > E) {
-            set_error("drain: inconsistent pass2 count");
-            return SSLA_ERR_STATE;
-        }
-        // ---- tdrop_s3 over the pass2 records, by s3 centre cell -------------------
-        HIPCHK(hipMemsetAsync(w.pass3, 0, (size_t)E, s3));
-        if (N2 > 0) {
-            hipLaunchKernelGGL(k_keys3, dim3(grid1(N2, 256)), dim3(256), 0, s3, N2, w.list2, w.bd,
-                               G, w.cell2, w.key3g, w.ka, w.va);
-            HIPCHK(sort_pairs(w.temp, tb, w.ka, w.kb, w.va, w.vb, N2, bits3, s3));
-            hipLaunchKernelGGL(k_runs, dim3(grid1(N2, 256)), dim3(256), 0, s3, N2, w.kb, nk3,
-                               w.st3, w.en3);
-            hipLaunchKernelGGL(k_tdrop, dim3(grid1(N2, 256)), dim3(256), 0, s3, N2, w.kb, w.vb,
-                               nk3, G.C3, w.st3, w.bd, 3, G.window, w.pass3);
-        }
-        hipLaunchKernelGGL(k_tdrop_commit, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, G.C3,
-                           w.st3, w.en3, w.bd, 3);
-        // prediction-grid writers: the last owned pass-3 record of each s3 cell
-        if (have_head)
-            hipLaunchKernelGGL(k_pred_runs, dim3(grid1(nk3, 4)), dim3(256), 0, s3, nk3, w.st3,
-                               w.en3, w.vb, w.pass3, w.owner, w.last3, w.cnt3);
-        HIPCHK(hipcub::DeviceSelect::Flagged(w.temp, tb, hipcub::CountingInputIterator<int>(0),
-                                              w.pass3, w.list3, w.counts + 1, E, s3));
-        // ---- s3 pair order and chunk tables, from the s3 record order --------------
-        hipLaunchKernelGGL(k_pair_count, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, G.C3,
-                           G.W3, G.H3, w.st3, w.en3, w.pen3);
-        HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.pen3, w.pst3, (int)nk3, s3));
-        hipLaunchKernelGGL(k_pair_bounds, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, w.pst3,
-                           w.pen3, w.ccnt3);
-        if (N2 > 0)
-            hipLaunchKernelGGL(k_pair_rank, dim3(grid1(N2, 256)), dim3(256), 0, s3, N2, w.kb,
-                               w.vb, nk3, G.C3, G.W3, G.H3, w.st3, w.en3, w.pst3, w.pos3,
-                               w.prec3);
-        HIPCHK(hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.ccnt3, w.coff3, (int)nk3, s3));
-        hipLaunchKernelGGL(k_chunk_fill, dim3(grid1(w.max_chunks, 256)), dim3(256), 0, s3, nk3,
-                           w.max_chunks, w.pst3,
-                           w.pen3, w.ccnt3, w.coff3, w.ckey3, w.cbeg3, w.cend3, w.counts + 3);
-        HIPCHK(hipEventRecord(w.s3_ordered, s3));
-        HIPCHK(hipGetLastError());
-    }
     // ---- L6: 48 -> 96, pass2 records ------------------------------------------
     HIPCHK(hipStreamWaitEvent(st, w.s3_ordered, 0));
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
@@ -1547,7 +1790,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
     MARK();
     hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
-                       w.coff3, w.ccnt3, w.bd, 2, w.Asum, w.Bsum, w.Hs);
+                       w.coff3, w.bd, 2, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, all, w.QVG);
@@ -1564,7 +1807,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
     MARK();
     hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
-                       w.coff3, w.ccnt3, w.bd, 3, w.Asum, w.Bsum, w.Hs);
+                       w.coff3, w.bd, 3, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, w.pass3, w.QVG);
