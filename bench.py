@@ -28,6 +28,7 @@ start / exit stamps.
 import argparse
 import ctypes
 import json
+import re
 import os
 import sys
 import tempfile
@@ -511,6 +512,147 @@ def batch_bench(a, d, recs, n, S, steps, warmup, desc, tmp) -> int:
     return 0
 
 
+# ---- rocprofv3 summaries (the files under profiles/ are made by these) ------
+# whole-ring drain launches per call, in launch order, by kernel name; names
+# launched twice per call belong to the two layers in turn; the ordering
+# kernels are summed into "order"
+TRAFFIC_PHASES = {
+    "k_qvg<24, 48>": ["L4.proj"], "k_qvg<48, 48>": ["L5.proj"], "k_qvg<48, 96>": ["L6.proj"],
+    "k_qvg<96, 96>": ["L7.proj"],
+    "k_scan_summary<48>": ["L4.sum", "L5.sum"], "k_scan_carry<48>": ["L4.carry", "L5.carry"],
+    "k_scan_apply<48>": ["L4.apply", "L5.apply"],
+    "k_scan_summary<96>": ["L6.sum", "L7.sum"], "k_scan_carry<96>": ["L6.carry", "L7.carry"],
+    "k_scan_apply<96>": ["L6.apply", "L7.apply"],
+    "k_outt<24, 48, 2, 1>": ["L4.out"], "k_outt<48, 48, 1, 3>": ["L5.out"],
+    "k_outt<48, 96, 1, 3>": ["L6.out"], "k_outt<96, 96, 1, 3>": ["L7.out"],
+    "k_head": ["head"], "k_pred_write": ["head"], "k_emit": ["emit"],
+}
+ORDER_KERNELS = ("k_fill_set", "k_decode", "k_rs_hist", "k_exscan", "k_rs_scatter", "k_runs",
+                 "k_keys2", "k_keyscan", "k_tdrop2", "k_pair_rank", "k_chunks", "k_keys3a",
+                 "k_place3", "k_tdrop3", "k_keys3b")
+
+
+def _kname(n: str) -> str:
+    n = n.replace("ssla::(anonymous namespace)::", "").replace("ssla::", "").replace("void ", "")
+    return re.sub(r"\(.*", "", n).strip()
+
+
+def pmc_summary(fetch_dir, write_dir, cfetch_dir, cwrite_dir, copy_bytes, command):
+    """Per-launch HBM bytes of the whole-ring drain from rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE runs of bench.py (counters in KiB per dispatch),
+    each scaled by what the same counter reads for a plain device copy of
+    copy_bytes bytes (cfetch / cwrite runs)."""
+    import collections
+    import csv
+    import glob
+
+    def rows(d):
+        f = glob.glob(f"{d}/**/*counter_collection.csv", recursive=True)[0]
+        return sorted(csv.DictReader(open(f)), key=lambda r: int(r["Dispatch_Id"]))
+
+    def per_phase(rs):
+        seen, out = collections.Counter(), collections.defaultdict(float)
+        calls = sum(1 for r in rs if _kname(r["Kernel_Name"]) == "k_fill_set")
+        for r in rs:
+            k = _kname(r["Kernel_Name"])
+            v = float(r["Counter_Value"]) * 1024.0
+            if k in ORDER_KERNELS:
+                out["order"] += v / max(1, calls)
+            elif k in TRAFFIC_PHASES:
+                ph = TRAFFIC_PHASES[k]
+                out[ph[seen[k] % len(ph)]] += v / max(1, calls)
+                seen[k] += 1
+        return out
+
+    cf = max(float(r["Counter_Value"]) for r in rows(cfetch_dir)) * 1024.0
+    cw = max(float(r["Counter_Value"]) for r in rows(cwrite_dir)) * 1024.0
+    fs, ws = copy_bytes / cf, copy_bytes / cw
+    fetch, write = per_phase(rows(fetch_dir)), per_phase(rows(write_dir))
+    res = {"copy_bytes": copy_bytes, "fetch_scale": round(fs, 4), "write_scale": round(ws, 4),
+           "command": command,
+           "workload": "bench.py defaults: 200,000 ring records at 80x64, stub weights seed 1",
+           "launches": {}}
+    for ph in sorted(set(fetch) | set(write)):
+        f, w = fetch.get(ph, 0.0) * fs, write.get(ph, 0.0) * ws
+        res["launches"][ph] = {"fetch_bytes": int(f), "write_bytes": int(w),
+                               "hbm_bytes": int(f + w)}
+    return res
+
+
+def stats_summary(csv_path, title, workload, command, calls_note, top=30):
+    """Markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv."""
+    import csv
+    rs = list(csv.DictReader(open(csv_path)))
+    tot = sum(float(r["TotalDurationNs"]) for r in rs)
+    out = [f"# {title}", "", f"Workload: {workload}", "",
+           "Command (repo root on the MI355X box; `cd /tmp && export TMPDIR=/tmp` first):", "",
+           "```", command, "```", "",
+           f"## Kernel stats ({calls_note}; top {top} by total time)", "",
+           "| kernel | calls | avg µs | % of GPU time |", "|---|---:|---:|---:|"]
+    for r in sorted(rs, key=lambda r: -float(r["TotalDurationNs"]))[:top]:
+        out.append(f"| {_kname(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                   f"{float(r['Percentage']):.2f} |")
+    out += ["", f"Total kernel time: {tot / 1e6:.2f} ms over "
+                f"{sum(int(r['Calls']) for r in rs)} launches."]
+    return "\n".join(out)
+
+
+def sq_summary(dir_a, dir_b, xcc=8, cus=256, slots=32, ghz=2.4):
+    """Per-kernel SQ metrics (markdown) from the two rocprofv3 --pmc passes
+    listed in profiles/drain_80x64_200k_sq_counters.md, summed over each
+    kernel's launches, with rocprofv3's metric formulas.  GRBM_GUI_ACTIVE is
+    summed over the XCDs, so it is divided by their number."""
+    import collections
+    import csv
+    import glob
+
+    def load(d):
+        f = glob.glob(f"{d}/**/*counter_collection.csv", recursive=True)[0]
+        out = collections.OrderedDict()
+        for r in csv.DictReader(open(f)):
+            e = out.setdefault(int(r["Dispatch_Id"]), {
+                "name": _kname(r["Kernel_Name"]), "lds": int(r["LDS_Block_Size"]),
+                "vgpr": int(r["VGPR_Count"]), "agpr": int(r["Accum_VGPR_Count"])})
+            e[r["Counter_Name"]] = float(r["Counter_Value"])
+        return out
+
+    A, B = load(dir_a), load(dir_b)
+    agg = collections.OrderedDict()
+    for k, e in A.items():
+        g = agg.setdefault(e["name"], collections.Counter())
+        g["n"] += 1
+        for c, v in e.items():
+            if isinstance(v, float):
+                g["A_" + c] += v
+        for c, v in B.get(k, {}).items():
+            if isinstance(v, float):
+                g["B_" + c] += v
+        g["vgpr"], g["agpr"], g["lds"] = e["vgpr"], e["agpr"], e["lds"]
+    simds = 4 * cus
+    rows = ["| kernel | launches | µs/launch | occupancy % | VALU busy % | MFMA busy % | "
+            "LDS busy % | LDS bank conflicts / access | wave time waiting % | "
+            "VALU / MFMA / LDS / VMEM-rd / VMEM-wr instr per wave | VGPR + AGPR | LDS B |",
+            "|---|---:|---:|---:|---:|---:|---:|---:|---:|---|---:|---:|"]
+    for nm, g in sorted(agg.items(), key=lambda kv: -kv[1]["A_GRBM_GUI_ACTIVE"]):
+        grbm = g["A_GRBM_GUI_ACTIVE"] / xcc
+        if grbm <= 0:
+            continue
+        occ = 400 * g["A_SQ_WAVE_CYCLES"] / grbm / cus / slots   # WAVE_CYCLES: units of 4
+        valu = 100 * g["A_SQ_ACTIVE_INST_VALU"] / cus / grbm
+        mfma = 100 * g["A_SQ_VALU_MFMA_BUSY_CYCLES"] / (grbm * simds)
+        lds = 100 * g["A_SQ_LDS_IDX_ACTIVE"] / (grbm * cus)
+        conf = g["A_SQ_LDS_BANK_CONFLICT"] / max(1.0, g["A_SQ_LDS_IDX_ACTIVE"]
+                                                  - g["A_SQ_LDS_BANK_CONFLICT"])
+        wait = 100 * g["B_SQ_WAIT_ANY"] / max(1.0, g["B_SQ_WAVE_CYCLES"] or g["A_SQ_WAVE_CYCLES"])
+        w = max(1.0, g["B_SQ_WAVES"] or g["A_SQ_WAVES"])
+        ins = "/".join(str(int(g["B_SQ_INSTS_" + x] / w))
+                       for x in ("VALU", "MFMA", "LDS", "VMEM_RD", "VMEM_WR"))
+        rows.append(f"| `{nm}` | {g['n']} | {grbm / g['n'] / (ghz * 1e3):.1f} | {occ:.1f} | "
+                    f"{valu:.1f} | {mfma:.1f} | {lds:.1f} | {conf:.3f} | {wait:.1f} | {ins} | "
+                    f"{g['vgpr']} + {g['agpr']} | {g['lds']} |")
+    return "\n".join(rows)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -533,7 +675,28 @@ def main() -> int:
                     help="1..32: drain through the live kernel's in-kernel batches of this "
                          "many records (one workgroup per instance) instead of the whole-ring "
                          "drain; reports throughput only")
+    ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "CFETCH", "CWRITE"),
+                    help="print the per-launch HBM traffic JSON from rocprofv3 --pmc output "
+                         "directories (drain FETCH_SIZE, WRITE_SIZE, copy FETCH_SIZE, WRITE_SIZE)")
+    ap.add_argument("--copy-bytes", type=int, default=256 << 20)
+    ap.add_argument("--stats-summary", nargs=5,
+                    metavar=("CSV", "TITLE", "WORKLOAD", "COMMAND", "CALLS"),
+                    help="print a markdown table of a rocprofv3 kernel_stats.csv")
+    ap.add_argument("--sq-summary", nargs=2, metavar=("PASS_A", "PASS_B"),
+                    help="print per-kernel SQ metrics from the two rocprofv3 --pmc passes")
     a = ap.parse_args()
+    if a.sq_summary:
+        print(sq_summary(*a.sq_summary))
+        return 0
+    if a.pmc_summary:
+        print(json.dumps(pmc_summary(*a.pmc_summary, a.copy_bytes,
+                                     "rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) -f csv -d <dir> "
+                                     "-- python3 bench.py --steps 2 --warmup 1 --no-live "
+                                     "--no-cpu-baseline"), indent=1))
+        return 0
+    if a.stats_summary:
+        print(stats_summary(*a.stats_summary))
+        return 0
     if not 0 <= a.batch <= 32:
         print("bench.py: --batch must be 0..32", file=sys.stderr)
         return 2

@@ -539,10 +539,7 @@ int ssla_hip_state_reset_async(const HybridS2S3Config* cfg, int blk, void* strea
             const auto it = g_state_bytes.find(cfg->hidden[blk][0]);
             if (it != g_state_bytes.end()) bytes = it->second;
         }
-        if (bytes) {
-            API_HIP(hipMemsetAsync(cfg->hidden[blk][0], 0, bytes, st));
-            return SSLA_OK;
-        }
+        if (bytes) return zero_async(cfg->hidden[blk][0], bytes, st);
     }
     const size_t c2 = (size_t)cfg->H2 * cfg->W2, c3 = (size_t)cfg->H3 * cfg->W3;
     const size_t sz[4] = {c2 * 48 * 4, c2 * 48 * 4, c3 * 96 * 4, c3 * 96 * 4};

@@ -26,6 +26,10 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
 // cfg's blocks and grid (ssla_hip_drain_reserve).
 int drain_reserve(const HybridS2S3Config* cfg, int max_records);
 
+// Zeroes nbytes at p (16-byte aligned device memory) with a kernel on st,
+// without waiting.
+int zero_async(void* p, size_t nbytes, hipStream_t st);
+
 // Marks the layer weights as possibly rewritten: the next drain rebuilds its
 // fragment-order copy.  Called by every ABI entry point that may write device
 // memory.

@@ -1505,6 +1505,33 @@ std::atomic<unsigned long long> g_weights_gen{0};
 
 void weights_touched() { g_weights_gen.fetch_add(1, std::memory_order_relaxed); }
 
+namespace {
+// zero fill of n bytes at p (16-byte stores for the aligned body)
+__global__ void k_zero_bytes(unsigned char* __restrict__ p, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t n16 = n >> 4;
+    if (i < n16) reinterpret_cast<uint4*>(p)[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (i < (n & 15)) p[(n16 << 4) + i] = 0;
+}
+}  // namespace
+
+int zero_async(void* p, size_t nbytes, hipStream_t st) {
+    if (!nbytes) return SSLA_OK;
+    if (!p || (reinterpret_cast<uintptr_t>(p) & 15)) {
+        set_error("zero_async: null or unaligned pointer");
+        return SSLA_ERR_ARG;
+    }
+    const size_t n16 = std::max<size_t>(nbytes >> 4, 16);
+    hipLaunchKernelGGL(k_zero_bytes, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, st,
+                       static_cast<unsigned char*>(p), nbytes);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error(std::string("zero_async: ") + hipGetErrorString(e));
+        return SSLA_ERR_HIP;
+    }
+    return SSLA_OK;
+}
+
 int drain_reserve(const HybridS2S3Config* cfg, int max_records) {
     if (!cfg || cfg->n_blocks < 1 || cfg->n_blocks > SSLA_MAX_BLOCKS || cfg->H2 <= 0 ||
         cfg->W2 <= 0 || max_records < 0 || (long long)max_records * kPatch > 0x7fffffffLL) {
