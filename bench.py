@@ -321,13 +321,14 @@ def _per_batch(phase_us):
     if phase_us is None or phase_us[25] <= 0:
         return None
     nb = float(phase_us[25])
-    return {k: round(float(phase_us[i]) / nb, 2) for i, k in enumerate(abi.BATCH_PHASES[:25])}
+    return {k: round(float(phase_us[i]) / nb, 2) for i, k in enumerate(abi.BATCH_PHASES)
+            if k not in ("batches", "records") and (i < 25 or phase_us[i] > 0)}
 
 
-def live_latency(stub_dir, rate_mev=2.0, duration_s=8.0, gpu_blocks=8):
+def live_latency(stub_dir, rate_mev=2.0, duration_s=8.0, gpu_blocks=8, group=0):
     from ssla_hip import live
     r = live.run_live(stub_dir, rate_mev=rate_mev, duration_s=duration_s, n_shards=6, halo=2,
-                      gpu_blocks=gpu_blocks)
+                      gpu_blocks=gpu_blocks, group=group)
     lat = r.lat_us
     return {
         "p50": round(lat["emit_to_done_p50"], 2), "p99": round(lat["emit_to_done_p99"], 2),
@@ -343,9 +344,14 @@ def live_latency(stub_dir, rate_mev=2.0, duration_s=8.0, gpu_blocks=8):
         "records": r.ring_records, "drained": r.drained, "kernel_status": r.status,
         "kernel_phase_us_per_batch": _per_batch(r.phase_us),
         "config": f"live: paced blob source {rate_mev} Mev/s -> 6 host shards (halo 2) -> "
-                  f"{r.gpu_blocks} GPU blocks (owned s2 strips, halo 2), one fine-grained ring "
-                  f"and persistent workgroup each, {r.duration_s:.1f} s; "
-                  f"{r.synth_events} events emitted",
+                  + (f"{r.gpu_blocks} GPU blocks (owned s2 strips, halo 2), one fine-grained ring "
+                     f"each" if r.gpu_blocks > 1 else "one ownership domain (the whole grid, no "
+                     "halo), one fine-grained ring")
+                  + (f", each drained by a group of {group} workgroups (16-channel slices, "
+                     f"partial sums exchanged per layer)" if group > 1
+                     else ", one persistent workgroup each")
+                  + f", {r.duration_s:.1f} s; {r.synth_events} events emitted",
+        "gpu_blocks": r.gpu_blocks, "group": group,
     }
 
 
@@ -669,8 +675,12 @@ def main() -> int:
     ap.add_argument("--live-seconds", type=float, default=8.0)
     ap.add_argument("--live-rate", type=float, default=2.0,
                     help="raw event rate of the live run's synthetic source, Mev/s")
-    ap.add_argument("--live-blocks", type=int, default=8, choices=[1, 2, 4, 8, 16],
-                    help="GPU blocks (owned strips) of the live run")
+    ap.add_argument("--live-blocks", type=int, default=1, choices=[1, 2, 4, 8, 16],
+                    help="GPU blocks (owned strips) of the live run; 1 = one ownership domain")
+    ap.add_argument("--live-group", type=int, default=6, choices=[0, 3, 4, 5, 6],
+                    help="workgroups per block of the live run (0 = one)")
+    ap.add_argument("--no-live-strips", action="store_true",
+                    help="skip the second live run on the reference's 8-strip topology")
     ap.add_argument("--batch", type=int, default=0,
                     help="1..32: drain through the live kernel's in-kernel batches of this "
                          "many records (one workgroup per instance) instead of the whole-ring "
@@ -811,7 +821,11 @@ def main() -> int:
 
     if a.workload == "80x64" and not a.no_live:
         res["latency_us"] = leg("live", lambda: live_latency(tmp.name, a.live_rate,
-                                                             a.live_seconds, a.live_blocks))
+                                                             a.live_seconds, a.live_blocks,
+                                                             a.live_group))
+        if not a.no_live_strips:
+            res["latency_us_8_strips"] = leg("live 8 strips", lambda: live_latency(
+                tmp.name, a.live_rate, a.live_seconds, 8, 0))
     if a.workload == "16streams" and not a.no_live:
         res["latency_us"] = leg("replay", lambda: replay_latency(
             tmp.name, recs, [o["pass3"] for o in outs]))

@@ -160,7 +160,9 @@ int ssla_hip_drain_n2(const HybridS2S3Config* cfg,
  * 3-6 L4 (projection, recurrence, contraction, LayerNorm), 7-10 L5,
  * 11 pool + tdrop s3, 12 s3 pairs, 13-16 L6, 17-20 L7, 21 head hidden,
  * 22 head outputs, 23 prediction grid, 24 outputs / publish; then counts:
- * 25 batches, 26 records; 27-31 unused. */
+ * 25 batches, 26 records; then, for group drains only, 27-30 the exchange
+ * waits of L4-L7 (slots 5, 9, 15, 19 then hold the contraction up to the
+ * member's own partial sums); 31 unused. */
 
 typedef struct SslaHipDrainOpts {
     void*         stream;      /* hipStream_t; NULL = default stream */
@@ -176,6 +178,11 @@ typedef struct SslaHipDrainOpts {
     double*       batch_phase_us; /* NULL or host double[SSLA_BATCH_PHASES]:
                                   batch mode only (needs sync); adds the
                                   in-kernel wall-clock profile */
+    int           group;       /* batch mode: 0 or 1 = one workgroup per
+                                  block; 3..6 = that many workgroups per
+                                  block, each owning 16-channel slices of
+                                  every layer (see ssla_hip_persistent_start);
+                                  runs synchronously */
 } SslaHipDrainOpts;
 
 int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg,
@@ -228,7 +235,12 @@ int ssla_hip_wall_clock_khz(int* out);
 
 /* Timing ring of block blk: `capacity` (power of two) GpuTimingSlot in HBM,
  * timing_mask = capacity - 1, and kernel_start_clk / kernel_end_clk anchors
- * in fine-grained host memory (hybrid_common.py:274-310).  All zeroed. */
+ * in fine-grained host memory (hybrid_common.py:274-310).  All zeroed.
+ * The anchors are words 0 and 1 of four: while the live kernel runs, a
+ * host that writes a new value into word 2 (kernel_start_clk[blk][2]) gets,
+ * within a poll, word 3 = (GPU wall clock << 8) | (that value & 0xff),
+ * read after the kernel saw the new value -- a clock reading the host can
+ * bracket between two of its own. */
 int  ssla_hip_timing_alloc(HybridS2S3Config* cfg, int blk, unsigned int capacity);
 void ssla_hip_timing_free(HybridS2S3Config* cfg, int blk);
 
@@ -245,6 +257,15 @@ void ssla_hip_timing_free(HybridS2S3Config* cfg, int blk);
  * sleep between polls.  The kernel returns when *stop_flag becomes
  * nonzero, when a producer laps the ring (status 2), or after
  * opts->idle_timeout_ms without a ready record (status 3).
+ * With opts->group = G in 3..6, each block is drained by G workgroups
+ * instead of one: member k owns the 16-channel slices k, k + G, ... of
+ * every layer (projection, recurrence, its part of the contraction), and
+ * the members exchange partial pre-LayerNorm sums through device memory
+ * once per layer.  Results are those of one workgroup up to fp32 summation
+ * order; each block's weights stream through G compute units.  All
+ * n_blocks x G workgroups must fit on the device at once (SSLA_ERR_ARG
+ * otherwise); a member whose wait for another runs out (2 s inside a
+ * batch) ends the kernel with status 4.
  * The kernel runs on its own non-blocking stream; do not call
  * ssla_hip_device_synchronize while it runs. */
 typedef struct SslaHipLive SslaHipLive;
@@ -253,7 +274,10 @@ typedef struct SslaHipLiveOpts {
     int          max_batch;        /* 1..32; default 32 */
     unsigned int idle_timeout_ms;  /* default 30000 */
     double*      phase_us;         /* NULL or host double[SSLA_BATCH_PHASES]:
-                                      filled (added to) by persistent_wait */
+                                      filled (added to) by persistent_wait
+                                      (member 0's profile with groups) */
+    int          group;            /* 0 or 1: one workgroup per block;
+                                      3..6: workgroups per block */
 } SslaHipLiveOpts;
 
 int ssla_hip_persistent_start(const HybridS2S3Config* cfg,
@@ -268,7 +292,8 @@ int ssla_hip_persistent_start(const HybridS2S3Config* cfg,
 
 /* Waits (up to timeout_ms, < 0 = forever) for the kernel to return after
  * the caller set *stop_flag, then frees the session.  *status: 0 stopped
- * by the flag, 2 ring overrun, 3 idle timeout.  Returns SSLA_ERR_STATE if
+ * by the flag, 2 ring overrun, 3 idle timeout, 4 a group member's wait
+ * ran out.  Returns SSLA_ERR_STATE if
  * the kernel is still running at the timeout (the session stays valid). */
 int ssla_hip_persistent_wait(SslaHipLive* h, int timeout_ms, int* status);
 

@@ -29,9 +29,16 @@ std::mutex g_alloc_mu;
 std::set<void*> g_state_bases;   // blocks allocated by ssla_hip_state_alloc
 std::map<void*, size_t> g_state_bytes;   // their sizes: one allocation holds a block's state
 std::set<void*> g_pred_bases;    // preds allocated by ssla_hip_preds_alloc
+std::set<void*> g_clock_blocks;  // clock anchor blocks of ssla_hip_timing_alloc (4 words)
 }  // namespace
 
 void set_error(const std::string& msg) { t_err = msg; }
+
+unsigned long long* timing_clock_sync(const HybridS2S3Config* cfg, int blk) {
+    unsigned long long* c = cfg->kernel_start_clk[blk];
+    std::lock_guard<std::mutex> lk(g_alloc_mu);
+    return (c && cfg->kernel_end_clk[blk] == c + 1 && g_clock_blocks.count(c)) ? c + 2 : nullptr;
+}
 
 namespace {
 
@@ -613,10 +620,14 @@ int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg, const HybridInputRec* const
     if (phase_ms && !sync) { set_error("phase_ms needs sync"); return SSLA_ERR_ARG; }
     const int batch = opts ? opts->batch : 0;
     double* bph = opts ? opts->batch_phase_us : nullptr;
+    const int group = opts ? opts->group : 0;
     if (batch != 0) {
         if (phase_ms) { set_error("phase_ms is only measured by the whole-ring drain"); return SSLA_ERR_ARG; }
+        if (group > 1)
+            return batch_drain_group(cfg, rings, ns, outs, opts->head_outs, batch, group, st, bph);
         return batch_drain(cfg, rings, ns, outs, opts->head_outs, nullptr, batch, st, sync, bph);
     }
+    if (group > 1) { set_error("group is a batch-mode option"); return SSLA_ERR_ARG; }
     if (bph) { set_error("batch_phase_us is only measured by the batch-mode drain"); return SSLA_ERR_ARG; }
     return scan_drain(cfg, rings, ns, outs, opts ? opts->head_outs : nullptr, st, sync, phase_ms);
 }
@@ -678,13 +689,14 @@ int ssla_hip_timing_alloc(HybridS2S3Config* cfg, int blk, unsigned int capacity)
         (void)hipFree(t);
         return SSLA_ERR_HIP;
     }
+    // [start, end, ping, pong] (the last two: the live kernels' clock handshake)
     void* clk = nullptr;
-    if (hipHostMalloc(&clk, 16, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess) {
+    if (hipHostMalloc(&clk, 32, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess) {
         (void)hipFree(t);
         set_error("hipHostMalloc of clock anchors failed");
         return SSLA_ERR_HIP;
     }
-    std::memset(clk, 0, 16);
+    std::memset(clk, 0, 32);
     cfg->timing[blk] = static_cast<GpuTimingSlot*>(t);
     cfg->timing_mask = capacity - 1;
     cfg->kernel_start_clk[blk] = static_cast<unsigned long long*>(clk);
@@ -692,6 +704,7 @@ int ssla_hip_timing_alloc(HybridS2S3Config* cfg, int blk, unsigned int capacity)
     std::lock_guard<std::mutex> lk(g_alloc_mu);
     g_state_bases.insert(t);
     g_pred_bases.insert(clk);
+    g_clock_blocks.insert(clk);
     return SSLA_OK;
 }
 
@@ -704,6 +717,7 @@ void ssla_hip_timing_free(HybridS2S3Config* cfg, int blk) {
         (void)hipFree(t);
         cfg->timing[blk] = nullptr;
     }
+    g_clock_blocks.erase(clk);
     if (clk && g_pred_bases.erase(clk)) {
         (void)hipHostFree(clk);
         cfg->kernel_start_clk[blk] = nullptr;
@@ -718,9 +732,10 @@ int ssla_hip_persistent_start(const HybridS2S3Config* cfg, HybridInputRec* const
     if (!cfg || !rings || !tails || !out) { set_error("null argument"); return SSLA_ERR_ARG; }
     const int max_batch = (opts && opts->max_batch) ? opts->max_batch : kLiveBatchMax;
     const unsigned idle = (opts && opts->idle_timeout_ms) ? opts->idle_timeout_ms : 30000u;
+    const int group = opts ? opts->group : 0;
     LiveSession* s = nullptr;
     const int rc = live_start(cfg, rings, ring_mask, tails, stop_flag, events_done, spin_ns,
-                              max_batch, idle, opts ? opts->phase_us : nullptr, &s);
+                              max_batch, idle, opts ? opts->phase_us : nullptr, group, &s);
     *out = reinterpret_cast<SslaHipLive*>(s);
     return rc;
 }

@@ -77,8 +77,10 @@ struct LiveDesc {
     unsigned int pad1;
     unsigned long long* kstart;
     unsigned long long* kend;
+    unsigned long long* clk_sync;       // live: [ping, pong] after kend, or null
     unsigned long long* prof;           // SSLA_BATCH_PHASES sums, or null
     HybridStrip strip;
+    unsigned long long t0;              // live, groups: the tail at launch
 };
 
 namespace {
@@ -98,9 +100,10 @@ constexpr int NPROF = SSLA_BATCH_PHASES;
 enum {
     PF_LOAD = 0, PF_TD2, PF_PAIRS2, PF_L4, PF_L5 = PF_L4 + 4, PF_TD3 = PF_L5 + 4, PF_PAIRS3,
     PF_L6, PF_L7 = PF_L6 + 4, PF_HEADH = PF_L7 + 4, PF_HEADO, PF_PREDS, PF_PUBLISH,
-    PF_BATCHES, PF_RECORDS
+    PF_BATCHES, PF_RECORDS,
+    PF_XWAIT                            // groups: exchange waits of L4..L7 (4 slots)
 };
-static_assert(PF_RECORDS < NPROF, "profile slots");
+static_assert(PF_XWAIT + 4 <= NPROF, "profile slots");
 
 struct alignas(16) Lds {
     float X[LB][XS];                     // layer input (becomes the layer output)
@@ -133,7 +136,8 @@ struct alignas(16) Lds {
 // ds_read_b128.
 __shared__ Lds g_lds;
 
-__device__ __forceinline__ void mark(Lds& S, int slot) {
+template <class SL>
+__device__ __forceinline__ void mark(SL& S, int slot) {
     if (S.prof_on && threadIdx.x == 0) {
         const unsigned long long t = (unsigned long long)wall_clock64();
         S.prof[slot] += t - S.tprev;
@@ -242,7 +246,8 @@ __device__ __forceinline__ void coldot8(const float* __restrict__ w, int ws, con
 // Arrival-rank tdrop for one batch (wave 0; lane = record).  All lanes read
 // the counter in one load before the last record of each cell stores the
 // advanced value.
-__device__ __forceinline__ void batch_tdrop(Lds& S, int B, unsigned char* td, const int* cell,
+template <class SL>
+__device__ __forceinline__ void batch_tdrop(SL& S, int B, unsigned char* td, const int* cell,
                             const unsigned char* mask, unsigned char* pass, int window) {
     if (threadIdx.x >= 64) return;
     const int e = threadIdx.x;
@@ -269,7 +274,8 @@ __device__ __forceinline__ void batch_tdrop(Lds& S, int B, unsigned char* td, co
 // (record, delta) pairs of the records in `set` on an Hl x Wl grid, in
 // record order; per-delta record lists; successor links and one leader per
 // cell.  Ends with a barrier.
-__device__ __forceinline__ void build_pairs(Lds& S, int B, const unsigned char* set, int Hl, int Wl) {
+template <class SL, bool PL = false>
+__device__ __forceinline__ void build_pairs(SL& S, int B, const unsigned char* set, int Hl, int Wl) {
     const int tid = threadIdx.x;
     if (tid < 64) {
         const int e = tid;
@@ -289,25 +295,28 @@ __device__ __forceinline__ void build_pairs(Lds& S, int B, const unsigned char* 
             if (e >= off) incl += v;
         }
         int k = incl - cnt;
-        if (e < LB) {
-            #pragma unroll
-            for (int d = 0; d < kPatch; ++d) {
-                int pi = -1;
-                if (bits & (1u << d)) {
-                    const int ty = S.ey[e] + 1 - d / 3, tx = S.ex[e] + 1 - d % 3;
-                    S.pe[k] = e;
-                    S.pc[k] = ty * Wl + tx;
-                    pi = k++;
-                }
-                S.pidx[e][d] = pi;
+        int pis[kPatch];
+        #pragma unroll
+        for (int d = 0; d < kPatch; ++d) {
+            int pi = -1;
+            if (bits & (1u << d)) {
+                const int ty = S.ey[e] + 1 - d / 3, tx = S.ex[e] + 1 - d % 3;
+                S.pe[k] = e;
+                S.pc[k] = ty * Wl + tx;
+                pi = k++;
             }
+            pis[d] = pi;
+            if (e < LB) S.pidx[e][d] = pi;
         }
         const unsigned long long lt = (1ull << e) - 1ull;
         #pragma unroll
         for (int d = 0; d < kPatch; ++d) {
             const bool has = (bits >> d) & 1u;
             const unsigned long long bal = __ballot(has);
-            if (has) S.dev[d][__popcll(bal & lt)] = e;
+            if (has) {
+                S.dev[d][__popcll(bal & lt)] = e;
+                if constexpr (PL) S.devp[d][__popcll(bal & lt)] = pis[d];
+            }
             if (e == 0) S.dcnt[d] = __popcll(bal);
         }
         const int total = __shfl(incl, 63, 64);
@@ -578,7 +587,8 @@ __device__ __forceinline__ void batch_layer(Lds& S, int B, const unsigned char* 
 // Head of the owned pass-3 records: hidden layers y = SiLU(W x + b) of both
 // branches (one thread per weight column), then the seven outputs
 // [reg0..3, obj, cls0, cls1] (one wave per record) and the prediction grid.
-__device__ __forceinline__ void batch_head(Lds& S, int B, const LiveDesc& d, const LiveWeights& W) {
+template <class SL>
+__device__ __forceinline__ void batch_head(SL& S, int B, const LiveDesc& d, const LiveWeights& W) {
     constexpr int C = SSLA_C3;
     const int tid = threadIdx.x;
     if (tid < 64) {
@@ -693,20 +703,39 @@ __device__ __noinline__ void process_batch(int B, const LiveDesc& d, const LiveW
     if (W.have_head) batch_head(S, B, d, W);
 }
 
-__device__ __forceinline__ void prof_begin(Lds& S, const LiveDesc& d) {
+template <class SL>
+__device__ __forceinline__ void prof_begin(SL& S, const LiveDesc& d) {
     if (threadIdx.x == 0) {
         S.prof_on = d.prof != nullptr;
         for (int k = 0; k < NPROF; ++k) S.prof[k] = 0;
     }
 }
 
-__device__ __forceinline__ void prof_end(Lds& S, const LiveDesc& d) {
+template <class SL>
+__device__ __forceinline__ void prof_end(SL& S, const LiveDesc& d) {
     if (threadIdx.x == 0 && d.prof)
         for (int k = 0; k < NPROF; ++k) d.prof[k] = S.prof[k];
 }
 
+// Clock handshake with the host (live kernels, poll wave lane 0): when the
+// host's ping word (a sequence number) changes, answer in the pong word
+// with (wall clock << 8) | (sequence & 0xff), one 64-bit store, so the host
+// can bracket a GPU clock reading between its own clock readings.
+__device__ __forceinline__ void clock_sync(unsigned long long* cs, unsigned long long& last) {
+    if (!cs) return;
+    const unsigned long long ping = __hip_atomic_load(cs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (ping != last) {
+        const unsigned long long now = (unsigned long long)wall_clock64();
+        __hip_atomic_store(cs + 1, (now << 8) | (ping & 0xffull), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+        last = ping;
+    }
+}
+
+
 // Loads B records starting at ring slot `first` (slots wrap with `mask`).
-__device__ __forceinline__ void load_batch(Lds& S, int B, const HybridInputRec* ring, unsigned long long first,
+template <class SL>
+__device__ __forceinline__ void load_batch(SL& S, int B, const HybridInputRec* ring, unsigned long long first,
                            unsigned long long mask, const HybridStrip& s, const Geometry& G) {
     const int tid = threadIdx.x;
     for (int t = tid; t < B * SSLA_C1; t += LT) {
@@ -796,9 +825,14 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
     const unsigned long long mask = d.ring_mask;
     unsigned long long t = __hip_atomic_load(d.tail, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
     unsigned long long last_work = (unsigned long long)wall_clock64();
+    // The host pairs the kernel's start and end clocks with its own clock at
+    // the moment it sees them, so they are stored relaxed: a release would
+    // first write back the L2, and the host would see the value late by as
+    // much as that takes (tens of microseconds at the end of a run).
     if (tid == 0 && d.kstart)
-        __hip_atomic_store(d.kstart, last_work, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(d.kstart, last_work, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     const int sleep_iters = (int)(spin_ns / 40u) + 1;
+    unsigned long long ping_seen = 0;
     while (true) {
         // every wave has read the previous round's flag / batch size
         __syncthreads();
@@ -814,6 +848,7 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
             // a tag beyond this round's sequence means the producer lapped the ring
             const bool lapped = (tid == 0) && s > t + 1ull;
             if (tid == 0) {
+                clock_sync(d.clk_sync, ping_seen);
                 const int stop = __hip_atomic_load(stop_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 const unsigned long long now = (unsigned long long)wall_clock64();
                 int f = 0;
@@ -830,7 +865,7 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
             if (tid == 0) {
                 if (flag > 1) atomicMax(status, flag);
                 if (d.kend)
-                    __hip_atomic_store(d.kend, (unsigned long long)wall_clock64(), __ATOMIC_RELEASE,
+                    __hip_atomic_store(d.kend, (unsigned long long)wall_clock64(), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_SYSTEM);
             }
             prof_end(S, d);
@@ -879,6 +914,566 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
         }
     }
 }
+
+// ---------------------------------------------------------------------------
+// Channel-sliced groups: G workgroups (kGroupMin..kGroupMax) drain one block.
+//
+// A layer's OUT channels form OUT / 16 slices; member k of the group owns
+// slices k, k + G, ...  Every member repeats the per-batch bookkeeping (ring
+// load, tdrop, pair lists, LayerNorm) on the whole batch, with its own copy
+// of the tdrop counters, so all members take the same decisions.  Per layer
+// a member
+//   P  projects q, v, g of its slices for the batch's pairs (16 x 16 MFMA
+//      tiles, ProjPack weights) into pair rows in LDS;
+//   S  runs the recurrence of its slices' channels over the pairs, on its
+//      own channels of the block's hidden state (members write disjoint
+//      state);
+//   O  contracts its slices' q*h with the matching rows of goW (OutPackT's
+//      goW fragments as the A operand, the q*h of 16 output records as B):
+//      a partial pre-LayerNorm sum over its K slice for every output
+//      channel.
+// The members then exchange the partial sums.  Each value travels with the
+// exchange's sequence number in the high half of one 64-bit word (relaxed
+// agent-scope atomics: a reader that sees the tag sees the value), and
+// every member adds the partials in member order and then the residual, so
+// all members hold the same pre-LayerNorm rows and the same layer output.
+// Two word sets alternate by sequence parity.  A member writes exchange
+// n + 2 only after reading exchange n + 1 from every member, each of which
+// wrote it after reading exchange n, so no word is overwritten before every
+// member has read it.  Every exchange (also one without output records)
+// carries a header word per member; the L4 exchange of each batch is thus
+// a group barrier, and member 0 advances the ring tail and broadcasts the
+// next batch only after every member has loaded this one.  Every wait is
+// bounded on the wall clock: a member whose wait runs out sets status 4
+// and leaves, and the others' waits then run out in turn.
+// ---------------------------------------------------------------------------
+constexpr int GSL = 2;                       // slices per member, at most (96 / 16 / kGroupMin)
+constexpr int PRS = 3 * GSL * MT + 4;        // LDS pair row: [q | v | g] x GSL slices (+4: banks)
+constexpr int XW = SSLA_C3;                  // words per record in an exchange set
+constexpr size_t kXSet = (size_t)kGroupMax * LB * XW;        // one set, all members
+constexpr size_t kXHdr = 2 * kXSet;                          // headers: [parity][member]
+constexpr size_t kXBc = kXHdr + 2 * kGroupMax;               // member 0's batch word
+constexpr size_t kXStride = (kXBc + 1 + 31) & ~(size_t)31;   // words per block
+static_assert(kGroupMin * GSL * MT >= SSLA_C3, "slices per member");
+
+struct alignas(16) LdsG {
+    union {
+        float PR[LP][PRS];               // pair rows of the member's slices
+        float R[LB][XS];                 // head reg hidden (after the last layer)
+    };
+    float X[LB][XS];                     // layer input (becomes the layer output)
+    float Y[LB][XS];                     // pre-LayerNorm sums / head cls hidden
+    float H7[LB][8];
+    unsigned long long tpush[LB], temit[LB];
+    int ex[LB], ey[LB];
+    int c2[LB], c3[LB];
+    unsigned char vld[LB], own[LB], p2[LB], p3[LB];
+    int pidx[LB][kPatch];
+    int pe[LP], pc[LP], pnext[LP], lead[LP];
+    unsigned pk[LB];
+    int dcnt[kPatch], dcnto[kPatch];
+    int dev[kPatch][LB];                 // records with a pair at delta
+    int devp[kPatch][LB];                // ... and that pair
+    int ol[LB];
+    int npair, nlead, nout, bsize, flag, prof_on, abort_;
+    unsigned xseq;                       // exchanges done by the group
+    unsigned long long t_pop, tprev;
+    unsigned long long prof[NPROF];
+};
+
+__shared__ LdsG g_ldsg;
+
+struct GroupCtx {
+    unsigned long long* xb;              // the block's exchange words
+    unsigned long long wait_ticks;       // limit of one wait inside a batch
+    int k, G;
+};
+
+__device__ __forceinline__ unsigned long long xword(unsigned payload, unsigned tag) {
+    return (unsigned long long)payload | ((unsigned long long)tag << 32);
+}
+
+__device__ __forceinline__ void xput(unsigned long long* w, unsigned long long v) {
+    __hip_atomic_store(w, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The word at w once it carries `tag`; sets `late` (and returns what it
+// read) when the wall clock passes `deadline` first.
+__device__ __forceinline__ unsigned long long xwait(unsigned long long* w, unsigned tag,
+                                                    unsigned long long deadline, bool& late) {
+    unsigned long long v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    while ((unsigned)(v >> 32) != tag) {
+        if ((unsigned long long)wall_clock64() > deadline) {
+            late = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return v;
+}
+
+// One layer for one member; false when a wait of the exchange ran out.
+template <int IN, int OUT>
+__device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char* set,
+                                            const unsigned char* outm, const LayerWeightsS2S3& L,
+                                            const float* __restrict__ pp,
+                                            const float* __restrict__ goT,
+                                            const float* __restrict__ ipT,
+                                            float* __restrict__ hidden, const GroupCtx& gc,
+                                            int slot) {
+    using P = ProjPack<IN, OUT>;
+    constexpr int NSL = OUT / MT;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int li = lane & 15, lk = lane >> 4;
+    if (tid < 64) {
+        const bool o = tid < B && set[tid] && (outm == nullptr || outm[tid]);
+        const unsigned long long bal = __ballot(o);
+        if (o) S.ol[__popcll(bal & ((1ull << tid) - 1ull))] = tid;
+        if (tid == 0) S.nout = __popcll(bal);
+    }
+    const int k = gc.k, G = gc.G;
+    const int ns = k < NSL ? (NSL - 1 - k) / G + 1 : 0;      // own slices k, k + G, ...
+    // P: units (delta, own slice): the records with a pair at delta (A)
+    // times the slice's q, v and g weight columns, three MFMA chains over
+    // one A tile.  q is written for every pair; the recurrence reads it only
+    // for output pairs.
+    for (int u = wv; u < kPatch * ns; u += NW) {
+        const int d = u / ns, js = u - d * ns;
+        const int n = S.dcnt[d];
+        if (n == 0) continue;
+        const int j = k + js * G;
+        float bq[P::KS4 * 4], bv[P::KS4 * 4], bg[P::KS4 * 4];
+        P::load(pp, d * P::T + j, lane, bq);
+        P::load(pp, d * P::T + NSL + j, lane, bv);
+        P::load(pp, d * P::T + 2 * NSL + j, lane, bg);
+        const float* X = &S.X[0][0];
+        for (int m0 = 0; m0 < n; m0 += MT) {
+            const int xr = S.dev[d][min(m0 + li, n - 1)] * XS + lk;
+            f32x4 aq = {0.f, 0.f, 0.f, 0.f}, av = aq, ag = aq;
+            #pragma unroll
+            for (int s = 0; s < P::KS; ++s) {
+                const float x = X[xr + s * 4];
+                aq = __builtin_amdgcn_mfma_f32_16x16x4f32(x, bq[s], aq, 0, 0, 0);
+                av = __builtin_amdgcn_mfma_f32_16x16x4f32(x, bv[s], av, 0, 0, 0);
+                ag = __builtin_amdgcn_mfma_f32_16x16x4f32(x, bg[s], ag, 0, 0, 0);
+            }
+            #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int rr = m0 + 4 * lk + r;
+                if (rr < n) {
+                    float* row = S.PR[S.devp[d][rr]];
+                    row[js * MT + li] = aq[r];
+                    row[(GSL + js) * MT + li] = av[r];
+                    row[(2 * GSL + js) * MT + li] = ag[r];
+                }
+            }
+        }
+    }
+    __syncthreads();
+    mark(S, slot + 0);
+    // S: one lane per (cell, own channel); q*h replaces q for output pairs
+    {
+        constexpr int CH = 8;
+        const int w16 = MT * ns, nl = S.nlead;
+        for (int t = tid; t < nl * w16; t += LT) {
+            const int kq = t / w16, c = t - kq * w16, js = c >> 4, cc = c & 15;
+            const int qc = js * MT + cc, vc = (GSL + js) * MT + cc, gcl = (2 * GSL + js) * MT + cc;
+            int q = S.lead[kq];
+            float* hp = hidden + (size_t)S.pc[q] * OUT + (k + js * G) * MT + cc;
+            float h = gload(hp);
+            while (q >= 0) {
+                int qs[CH];
+                #pragma unroll
+                for (int j = 0; j < CH; ++j) {
+                    qs[j] = q;
+                    if (q >= 0) q = S.pnext[q];
+                }
+                #pragma unroll
+                for (int j = 0; j < CH; ++j) {
+                    if (qs[j] >= 0) {
+                        float* row = S.PR[qs[j]];
+                        h = fmaf(sigmoid_fast(row[gcl]), h, row[vc]);
+                        if (outm == nullptr || outm[S.pe[qs[j]]]) row[qc] *= h;
+                    }
+                }
+            }
+            gstore(hp, h);
+        }
+    }
+    __syncthreads();
+    mark(S, slot + 1);
+    // O: the member's partial sums, then its header word
+    const unsigned tag = S.xseq + 1u;
+    const int par = (int)(S.xseq & 1u);
+    unsigned long long* xs = gc.xb + (size_t)par * kXSet;
+    unsigned long long* xh = gc.xb + kXHdr + (size_t)par * kGroupMax;
+    const int no = S.nout;
+    // the input_proj residual (IN != OUT) is one member's extra K slice: the
+    // first member without a channel slice, else member 0
+    constexpr bool IPR = IN != OUT;
+    constexpr int KG = (IN + 15) / 16;
+    const int mres = NSL < G ? NSL : 0;
+    const bool has_res = IPR && k == mres;
+    if (ns > 0 || has_res) {
+        const int nit = NSL * ((no + MT - 1) / MT);
+        for (int it = wv; it < nit; it += NW) {
+            const int ot = it % NSL, r = (it / NSL) * MT + li;
+            const int e = r < no ? S.ol[r] : -1;
+            // per own slice: its nine goW fragments first, then three
+            // independent MFMA chains (deltas d mod 3), added at the end
+            f32x4 c3[3];
+            #pragma unroll
+            for (int q = 0; q < 3; ++q) c3[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int js = 0; js < ns; ++js) {
+                f32x4 a[kPatch];
+                #pragma unroll
+                for (int d = 0; d < kPatch; ++d)
+                    a[d] = ((const SSLA_GLOBAL f32x4*)goT)[((size_t)(d * NSL + k + js * G) * NSL + ot) * 64 + lane];
+                #pragma unroll
+                for (int d = 0; d < kPatch; ++d) {
+                    const int p = e >= 0 ? S.pidx[e][d] : -1;
+                    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+                    if (p >= 0) v = *reinterpret_cast<const f32x4*>(&S.PR[p][js * MT + 4 * lk]);
+                    #pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        c3[d % 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[d][i], v[i], c3[d % 3], 0, 0, 0);
+                }
+            }
+            f32x4 acc = c3[0] + c3[1] + c3[2];
+            if (has_res) {
+                // input_proj's fragments; B: the record's input, channels
+                // 16 t + 4 lk + i (0 past IN)
+                f32x4 ar[KG];
+                #pragma unroll
+                for (int t = 0; t < KG; ++t)
+                    ar[t] = ((const SSLA_GLOBAL f32x4*)ipT)[((size_t)ot * KG + t) * 64 + lane];
+                #pragma unroll
+                for (int t = 0; t < KG; ++t) {
+                    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+                    if (e >= 0 && 16 * t + 4 * lk < IN) v = *reinterpret_cast<const f32x4*>(&S.X[e][16 * t + 4 * lk]);
+                    #pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ar[t][i], v[i], acc, 0, 0, 0);
+                }
+            }
+            if (r < no) {
+                unsigned long long* w = xs + ((size_t)k * LB + r) * XW + ot * MT + 4 * lk;
+                #pragma unroll
+                for (int i = 0; i < 4; ++i) xput(w + i, xword(__float_as_uint(acc[i]), tag));
+            }
+        }
+    }
+    if (tid == 0) xput(xh + k, xword(0u, tag));
+    mark(S, slot + 2);
+    // sums of the members' partials (member order), then the identity residual
+    const int ncon = (G < NSL ? G : NSL) + (IPR && NSL < G ? 1 : 0);
+    const unsigned long long deadline = (unsigned long long)wall_clock64() + gc.wait_ticks;
+    bool late = false;
+    for (int t = tid; t < no * OUT; t += LT) {
+        const int r = t / OUT, ch = t - r * OUT, e = S.ol[r];
+        const float res = IPR ? 0.f : S.X[e][ch];
+        // all contributors' words in flight at once, then the stragglers
+        unsigned long long w[kGroupMax];
+        #pragma unroll
+        for (int kk = 0; kk < kGroupMax; ++kk)
+            if (kk < ncon)
+                w[kk] = __hip_atomic_load(xs + ((size_t)kk * LB + r) * XW + ch, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        float sum = 0.f;
+        #pragma unroll
+        for (int kk = 0; kk < kGroupMax; ++kk)
+            if (kk < ncon) {
+                if ((unsigned)(w[kk] >> 32) != tag)
+                    w[kk] = xwait(xs + ((size_t)kk * LB + r) * XW + ch, tag, deadline, late);
+                sum += __uint_as_float((unsigned)w[kk]);
+            }
+        S.Y[e][ch] = sum + res;
+    }
+    if (tid < G) (void)xwait(xh + tid, tag, deadline, late);
+    if (late) S.abort_ = 1;
+    __syncthreads();
+    if (S.abort_) return false;
+    if (tid == 0) S.xseq = tag;
+    mark(S, PF_XWAIT + (slot == PF_L4 ? 0 : slot == PF_L5 ? 1 : slot == PF_L6 ? 2 : 3));
+    // fp64 LayerNorm, one wave per output record
+    for (int r = wv; r < no; r += NW) {
+        const int e = S.ol[r];
+        const float a = lane < OUT ? S.Y[e][lane] : 0.f;
+        const float b = lane + 64 < OUT ? S.Y[e][lane + 64] : 0.f;
+        const double mean = wave_sum((double)a + (double)b) / (double)OUT;
+        const double da = lane < OUT ? (double)a - mean : 0.0;
+        const double db = lane + 64 < OUT ? (double)b - mean : 0.0;
+        const double var = wave_sum(da * da + db * db) / (double)OUT;
+        const double inv = 1.0 / sqrt(var + 1e-5);
+        if (lane < OUT)
+            S.X[e][lane] = (float)(da * inv * (double)L.ln_gamma[lane] + (double)L.ln_beta[lane]);
+        if (lane + 64 < OUT)
+            S.X[e][lane + 64] = (float)(db * inv * (double)L.ln_gamma[lane + 64] + (double)L.ln_beta[lane + 64]);
+    }
+    __syncthreads();
+    mark(S, slot + 3);
+    return true;
+}
+
+// One batch for one member (the schedule of process_batch); false when an
+// exchange wait ran out.  Member 0 also runs the head.
+__device__ __forceinline__ bool process_group(int B, const LiveDesc& d, const LiveWeights& W,
+                                           const Geometry& G, GroupCtx gc,
+                                           const float* const* goT, const float* const* ipT,
+                                           unsigned char* td2,
+                                           unsigned char* td3) {
+    LdsG& S = g_ldsg;
+    const int tid = threadIdx.x;
+    batch_tdrop(S, B, td2, S.c2, nullptr, S.p2, G.window);
+    __syncthreads();
+    mark(S, PF_TD2);
+    build_pairs<LdsG, true>(S, B, S.vld, G.H2, G.W2);
+    mark(S, PF_PAIRS2);
+    if (!group_layer<SSLA_C1, SSLA_C2>(S, B, S.vld, nullptr, W.L[0], W.pk.pp[0], goT[0], ipT[0], d.hidden[0], gc, PF_L4))
+        return false;
+    if (!group_layer<SSLA_C2, SSLA_C2>(S, B, S.vld, S.p2, W.L[1], W.pk.pp[1], goT[1], ipT[1], d.hidden[1], gc, PF_L5))
+        return false;
+    if (tid < B) {
+        S.ex[tid] >>= 1;
+        S.ey[tid] >>= 1;
+        S.c3[tid] = S.vld[tid] ? S.ey[tid] * G.W3 + S.ex[tid] : -1;
+    }
+    __syncthreads();
+    batch_tdrop(S, B, td3, S.c3, S.p2, S.p3, G.window);
+    __syncthreads();
+    mark(S, PF_TD3);
+    build_pairs<LdsG, true>(S, B, S.p2, G.H3, G.W3);
+    mark(S, PF_PAIRS3);
+    if (!group_layer<SSLA_C2, SSLA_C3>(S, B, S.p2, nullptr, W.L[2], W.pk.pp[2], goT[2], ipT[2], d.hidden[2], gc, PF_L6))
+        return false;
+    if (!group_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], W.pk.pp[3], goT[3], ipT[3], d.hidden[3], gc, PF_L7))
+        return false;
+    if (gc.k == 0 && W.have_head) batch_head(S, B, d, W);
+    return true;
+}
+
+struct GroupArgs {
+    unsigned long long* xb;              // exchange words, kXStride per block (zeroed)
+    unsigned char* tdrep;                // counters of members 1..G-1: (G - 1) x (C2 + C3) per block
+    const float* goT[4];                 // OutPackT goW fragments of L4..L7
+    const float* ipT[4];                 // OutPackT input_proj fragments (L4, L6; else null)
+    unsigned long long wait_ticks;
+    int G;
+};
+
+// Batch mode (LIVE false: d.n records in batches of max_batch) or the
+// persistent live drain; blocks of G consecutive workgroups.
+template <bool LIVE>
+__global__ void __launch_bounds__(LT)
+k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga,
+        const int* stop_flag, unsigned int spin_ns, unsigned long long idle_ticks, int max_batch,
+        int* __restrict__ status) {
+    LdsG& S = g_ldsg;
+    const int tid = threadIdx.x;
+    const int b = blockIdx.x / ga.G, k = blockIdx.x - b * ga.G;
+    const LiveDesc& d = ld[b];
+    const GroupCtx gc{ga.xb + (size_t)b * kXStride, ga.wait_ticks, k, ga.G};
+    unsigned char* td2 = d.td2;
+    unsigned char* td3 = d.td3;
+    if (k > 0) {
+        td2 = ga.tdrep + ((size_t)b * (ga.G - 1) + (k - 1)) * (size_t)(G.C2 + G.C3);
+        td3 = td2 + G.C2;
+    }
+    if (k == 0) prof_begin(S, d);
+    if (tid == 0) {
+        if (k != 0) S.prof_on = 0;
+        S.abort_ = 0;
+        S.xseq = 0;
+    }
+    __syncthreads();
+    if constexpr (!LIVE) {
+        int bi = 0;
+        for (int base = 0; base < d.n; base += max_batch, ++bi) {
+            const int B = min(max_batch, d.n - base);
+            if (tid == 0) {
+                S.t_pop = (unsigned long long)wall_clock64();
+                S.tprev = S.t_pop;
+            }
+            load_batch(S, B, d.ring, (unsigned long long)base, ~0ull, d.strip, G);
+            __syncthreads();
+            mark(S, PF_LOAD);
+            if (!process_group(B, d, W, G, gc, ga.goT, ga.ipT, td2, td3)) {
+                if (tid == 0) atomicMax(status, 4);
+                return;
+            }
+            if (k == 0) {
+                for (int t = tid; t < B * SSLA_C3; t += LT) {
+                    const int e = t / SSLA_C3, i = t % SSLA_C3;
+                    if (d.out) d.out[base + e].s3_feat[i] = (S.vld[e] && S.p3[e]) ? S.X[e][i] : 0.f;
+                }
+                if (tid < B) {
+                    const int e = tid;
+                    const bool v = S.vld[e], own = S.own[e];
+                    if (d.out) {
+                        d.out[base + e].pass2 = !v ? -2 : (own ? (int)S.p2[e] : -1);
+                        d.out[base + e].pass3 = !v ? -2 : (own ? (int)S.p3[e] : -1);
+                    }
+                    if (d.head_out) {
+                        const bool hv = W.have_head && own && S.p3[e];
+                        #pragma unroll
+                        for (int q = 0; q < 7; ++q) d.head_out[(size_t)(base + e) * 7 + q] = hv ? S.H7[e][q] : 0.f;
+                    }
+                }
+                if (tid == 0 && d.batch_clk) {
+                    d.batch_clk[(size_t)bi * 2 + 0] = S.t_pop;
+                    d.batch_clk[(size_t)bi * 2 + 1] = (unsigned long long)wall_clock64();
+                }
+            }
+            __syncthreads();
+            mark(S, PF_PUBLISH);
+            if (tid == 0) {
+                S.prof[PF_BATCHES] += 1;
+                S.prof[PF_RECORDS] += (unsigned long long)B;
+            }
+        }
+        if (k == 0) prof_end(S, d);
+        return;
+    }
+    const unsigned long long mask = d.ring_mask;
+    unsigned long long t = d.t0;
+    unsigned long long last_work = (unsigned long long)wall_clock64();
+    if (k == 0 && tid == 0 && d.kstart)
+        __hip_atomic_store(d.kstart, last_work, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const int sleep_iters = (int)(spin_ns / 40u) + 1;
+    unsigned long long* bc = gc.xb + kXBc;
+    unsigned bseq = 0;                   // batches broadcast
+    unsigned long long ping_seen = 0;
+    while (true) {
+        __syncthreads();
+        if (k == 0) {
+            // poll: wave 0 probes 64 consecutive tags (as k_live)
+            if (tid < 64) {
+                unsigned long long* tag = const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done);
+                const unsigned long long s = __hip_atomic_load(tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                const bool ready = s == t + (unsigned long long)tid + 1ull;
+                const unsigned long long bal = __ballot(ready);
+                const int lead = (int)__ffsll((long long)~bal) - 1;
+                int n = lead < 0 ? 64 : lead;
+                if (n > max_batch) n = max_batch;
+                const bool lapped = (tid == 0) && s > t + 1ull;
+                if (tid == 0) {
+                    clock_sync(d.clk_sync, ping_seen);
+                    const int stop = __hip_atomic_load(stop_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    const unsigned long long now = (unsigned long long)wall_clock64();
+                    int f = 0;
+                    if (stop) f = 1;
+                    else if (lapped) f = 2;
+                    else if (n == 0 && now - last_work > idle_ticks) f = 3;
+                    S.flag = f;
+                    S.bsize = n;
+                    if (f || n) xput(bc, xword((unsigned)n | ((unsigned)f << 8), bseq + 1u));
+                }
+            }
+            __syncthreads();
+            if (S.flag == 0 && S.bsize == 0) {
+                for (int i = 0; i < sleep_iters; ++i) __builtin_amdgcn_s_sleep(1);
+                continue;
+            }
+        } else {
+            if (tid == 0) {
+                // member 0 broadcasts at least once per idle timeout (then it stops)
+                const unsigned long long dl = last_work + idle_ticks + gc.wait_ticks;
+                unsigned long long v = __hip_atomic_load(bc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                bool late = false;
+                while ((unsigned)(v >> 32) != bseq + 1u) {
+                    if ((unsigned long long)wall_clock64() > dl) {
+                        late = true;
+                        break;
+                    }
+                    for (int i = 0; i < sleep_iters; ++i) __builtin_amdgcn_s_sleep(1);
+                    v = __hip_atomic_load(bc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                S.flag = late ? 4 : (int)((v >> 8) & 0xffu);
+                S.bsize = (int)(v & 0xffu);
+            }
+            __syncthreads();
+        }
+        const int flag = S.flag, B = S.bsize;
+        ++bseq;
+        if (flag) {
+            if (tid == 0) {
+                if ((k == 0 && flag > 1) || flag == 4) atomicMax(status, flag);
+                if (k == 0 && d.kend)
+                    __hip_atomic_store(d.kend, (unsigned long long)wall_clock64(), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            if (k == 0) prof_end(S, d);
+            return;
+        }
+        if (k != 0 && tid < B) {
+            // the producer's tags of this batch (member 0 has seen them)
+            unsigned long long* tag = const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done);
+            const unsigned long long want = t + (unsigned long long)tid + 1ull;
+            const unsigned long long dl = (unsigned long long)wall_clock64() + gc.wait_ticks;
+            while (__hip_atomic_load(tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != want) {
+                if ((unsigned long long)wall_clock64() > dl) {
+                    S.abort_ = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        __syncthreads();
+        if (S.abort_) {
+            if (tid == 0) atomicMax(status, 4);
+            return;
+        }
+        // pairs with the producer's release store of the tags
+        __atomic_thread_fence(__ATOMIC_ACQUIRE);
+        if (tid == 0) {
+            S.t_pop = (unsigned long long)wall_clock64();
+            S.tprev = S.t_pop;
+        }
+        load_batch(S, B, d.ring, t, mask, d.strip, G);
+        __syncthreads();
+        mark(S, PF_LOAD);
+        if (!process_group(B, d, W, G, gc, ga.goT, ga.ipT, td2, td3)) {
+            if (tid == 0) {
+                atomicMax(status, 4);
+                if (k == 0 && d.kend)
+                    __hip_atomic_store(d.kend, (unsigned long long)wall_clock64(), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            if (k == 0) prof_end(S, d);
+            return;
+        }
+        const unsigned long long t_done = (unsigned long long)wall_clock64();
+        if (k == 0) {
+            if (tid < B && d.timing) {
+                const unsigned long long seq = t + (unsigned long long)tid;
+                GpuTimingSlot& ts = d.timing[seq & d.timing_mask];
+                ts.t_pop_clk = S.t_pop;
+                ts.t_done_clk = t_done;
+                ts.seq = (unsigned int)seq;
+                ts.owner = (S.own[tid] && S.p2[tid] && S.p3[tid]) ? 1u : 0u;
+                ts.t_push_ns = S.tpush[tid];
+                ts.t_emit_ns = S.temit[tid];
+            }
+            __threadfence_system();
+            __syncthreads();
+            if (tid == 0) {
+                __hip_atomic_store(d.tail, t + (unsigned long long)B, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+                if (d.events_done)
+                    __hip_atomic_store(d.events_done, t + (unsigned long long)B, __ATOMIC_RELEASE,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            mark(S, PF_PUBLISH);
+            if (tid == 0) {
+                S.prof[PF_BATCHES] += 1;
+                S.prof[PF_RECORDS] += (unsigned long long)B;
+            }
+        }
+        t += (unsigned long long)B;
+        last_work = t_done;
+    }
+}
+
 
 #define LHIP(call)                                                            \
     do {                                                                      \
@@ -1152,6 +1747,155 @@ int batch_drain_noalloc(const HybridS2S3Config* cfg, const HybridInputRec* const
 }
 
 // ---------------------------------------------------------------------------
+// group launches: device resources and checks
+// ---------------------------------------------------------------------------
+// Exchange words, the tdrop counter copies of members 1..G-1 and both weight
+// packings (ProjPack for the projections, OutPackT for the goW fragments).
+struct GroupRes {
+    unsigned long long* xb = nullptr;
+    unsigned char* tdrep = nullptr;
+    float* pack = nullptr;
+    float* packT = nullptr;
+    void release() {
+        if (xb) (void)hipFree(xb);
+        if (tdrep) (void)hipFree(tdrep);
+        if (pack) (void)hipFree(pack);
+        if (packT) (void)hipFree(packT);
+        *this = GroupRes{};
+    }
+};
+
+// Every member of every group must be resident at once: members wait on
+// each other.
+static int group_check(int nb, int group) {
+    if (group < kGroupMin || group > kGroupMax) {
+        set_error("group must be 1 or in [" + std::to_string(kGroupMin) + ", " +
+                  std::to_string(kGroupMax) + "]");
+        return SSLA_ERR_ARG;
+    }
+    int per_cu = 0, cus = 0, dev = 0;
+    LHIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_group<true>, LT, 0));
+    LHIP(hipGetDevice(&dev));
+    LHIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    if ((long long)nb * group > (long long)per_cu * cus) {
+        set_error("n_blocks x group workgroups (" + std::to_string(nb * group) +
+                  ") do not fit on the device at once (" + std::to_string(per_cu * cus) + ")");
+        return SSLA_ERR_ARG;
+    }
+    return SSLA_OK;
+}
+
+// Allocates r, clears the exchange words, copies each block's counters for
+// members 1..group-1 and packs the weights, all on st; fills ga and W->pk.
+// On error the caller releases r.
+static int group_setup(const HybridS2S3Config* cfg, const Geometry& G, int group, hipStream_t st,
+                       LiveWeights* W, GroupRes* r, GroupArgs* ga) {
+    const int nb = G.nb;
+    const size_t xbytes = sizeof(unsigned long long) * kXStride * nb;
+    const size_t per = (size_t)(G.C2 + G.C3);
+    LHIP(hipMalloc(&r->xb, xbytes));
+    LHIP(hipMalloc(&r->tdrep, (size_t)nb * (group - 1) * per));
+    LHIP(hipMalloc(&r->pack, sizeof(float) * packed_weight_floats()));
+    LHIP(hipMalloc(&r->packT, sizeof(float) * packed_weight_floats_d()));
+    LHIP(hipMemsetAsync(r->xb, 0, xbytes, st));
+    for (int b = 0; b < nb; ++b)
+        for (int m = 0; m < group - 1; ++m) {
+            unsigned char* dst = r->tdrep + ((size_t)b * (group - 1) + m) * per;
+            LHIP(hipMemcpyAsync(dst, cfg->tdrop_s2[b], (size_t)G.C2, hipMemcpyDeviceToDevice, st));
+            LHIP(hipMemcpyAsync(dst + G.C2, cfg->tdrop_s3[b], (size_t)G.C3, hipMemcpyDeviceToDevice, st));
+        }
+    LHIP(pack_weights(W->L, r->pack, &W->pk, st));
+    PackedWeights pt{};
+    LHIP(pack_weights_d(W->L, r->packT, &pt, st));
+    ga->xb = r->xb;
+    ga->tdrep = r->tdrep;
+    ga->goT[0] = pt.po[0] + OutPackT<SSLA_C1, SSLA_C2>::Q;
+    ga->goT[1] = pt.po[1] + OutPackT<SSLA_C2, SSLA_C2>::Q;
+    ga->goT[2] = pt.po[2] + OutPackT<SSLA_C2, SSLA_C3>::Q;
+    ga->goT[3] = pt.po[3] + OutPackT<SSLA_C3, SSLA_C3>::Q;
+    ga->ipT[0] = ga->goT[0] + OutPackT<SSLA_C1, SSLA_C2>::GO;
+    ga->ipT[1] = nullptr;
+    ga->ipT[2] = ga->goT[2] + OutPackT<SSLA_C2, SSLA_C3>::GO;
+    ga->ipT[3] = nullptr;
+    int khz = 0;
+    LHIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, 0));
+    if (khz <= 0) khz = 100000;
+    ga->wait_ticks = 2000ull * (unsigned long long)khz;   // 2 s
+    ga->G = group;
+    return SSLA_OK;
+}
+
+int batch_drain_group(const HybridS2S3Config* cfg, const HybridInputRec* const* rings, const int* ns,
+                      HybridS2S3OutputSlot* const* outs, float* const* head_outs, int batch,
+                      int group, hipStream_t st, double* phase_us) {
+    LiveWeights W;
+    Geometry G;
+    int rc = live_weights(cfg, &W, &G);
+    if (rc) return rc;
+    if (batch < 1 || batch > LB) {
+        set_error("batch must be in [1, 32]");
+        return SSLA_ERR_ARG;
+    }
+    const int nb = cfg->n_blocks;
+    for (int b = 0; b < nb; ++b)
+        if (ns[b] < 0 || (ns[b] > 0 && !rings[b])) {
+            set_error("bad ring / count for block " + std::to_string(b));
+            return SSLA_ERR_ARG;
+        }
+    if ((rc = group_check(nb, group))) return rc;
+    std::lock_guard<std::mutex> lk(g_bmu);
+    GroupRes r;
+    LiveDesc* desc = nullptr;
+    int* status = nullptr;
+    unsigned long long* prof = nullptr;
+    auto run = [&]() -> int {
+        GroupArgs ga{};
+        int rc2 = group_setup(cfg, G, group, st, &W, &r, &ga);
+        if (rc2) return rc2;
+        LHIP(hipMalloc(&desc, sizeof(LiveDesc) * nb));
+        LHIP(hipMalloc(&status, sizeof(int)));
+        LHIP(hipMemsetAsync(status, 0, sizeof(int), st));
+        if (phase_us) LHIP(hipMalloc(&prof, sizeof(unsigned long long) * NPROF * nb));
+        std::vector<LiveDesc> hd(nb);
+        std::memset(hd.data(), 0, sizeof(LiveDesc) * nb);
+        for (int b = 0; b < nb; ++b) {
+            LiveDesc& d = hd[b];
+            live_desc_state(cfg, b, &d);
+            d.ring = rings[b];
+            d.ring_mask = ~0ull;
+            d.n = ns[b];
+            d.out = outs ? outs[b] : nullptr;
+            d.head_out = head_outs ? head_outs[b] : nullptr;
+            d.prof = prof ? prof + (size_t)NPROF * b : nullptr;
+        }
+        LHIP(hipMemcpyAsync(desc, hd.data(), sizeof(LiveDesc) * nb, hipMemcpyHostToDevice, st));
+        hipLaunchKernelGGL(k_group<false>, dim3(nb * group), dim3(LT), 0, st, desc, W, G, ga,
+                           (const int*)nullptr, 0u, 0ull, batch, status);
+        LHIP(hipGetLastError());
+        LHIP(hipStreamSynchronize(st));
+        int hs = 0;
+        LHIP(hipMemcpy(&hs, status, sizeof(int), hipMemcpyDeviceToHost));
+        if (hs) {
+            set_error("group drain: a member's wait ran out (status " + std::to_string(hs) + ")");
+            return SSLA_ERR_STATE;
+        }
+        if (phase_us) {
+            std::vector<unsigned long long> h((size_t)NPROF * nb);
+            LHIP(hipMemcpy(h.data(), prof, sizeof(unsigned long long) * h.size(), hipMemcpyDeviceToHost));
+            add_profile(h.data(), nb, phase_us);
+        }
+        return SSLA_OK;
+    };
+    rc = run();
+    (void)hipStreamSynchronize(st);
+    r.release();
+    if (desc) (void)hipFree(desc);
+    if (status) (void)hipFree(status);
+    if (prof) (void)hipFree(prof);
+    return rc;
+}
+
+// ---------------------------------------------------------------------------
 // persistent session
 // ---------------------------------------------------------------------------
 struct LiveSession {
@@ -1163,12 +1907,13 @@ struct LiveSession {
     double* phase_us = nullptr;
     float* pack = nullptr;
     int nb = 0;
+    GroupRes grp;                       // group > 1 only
 };
 
 int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
                unsigned long long ring_mask, unsigned long long* const* tails, int* stop_flag,
                unsigned long long* const* events_done, unsigned int spin_ns, int max_batch,
-               unsigned int idle_timeout_ms, double* phase_us, LiveSession** out) {
+               unsigned int idle_timeout_ms, double* phase_us, int group, LiveSession** out) {
     *out = nullptr;
     LiveWeights W;
     Geometry G;
@@ -1187,6 +1932,7 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
         return SSLA_ERR_ARG;
     }
     const int nb = cfg->n_blocks;
+    if (group > 1 && (rc = group_check(nb, group))) return rc;
     for (int b = 0; b < nb; ++b) {
         if (!rings[b] || !tails[b]) {
             set_error("every block needs a ring and a tail");
@@ -1210,6 +1956,7 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
         if (s->status) (void)hipFree(s->status);
         if (s->prof) (void)hipFree(s->prof);
         if (s->pack) (void)hipFree(s->pack);
+        s->grp.release();
         delete s;
         return SSLA_ERR_HIP;
     };
@@ -1218,8 +1965,13 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
     if (hipMalloc(&s->scratch, sbytes) != hipSuccess) return fail("scratch");
     if (hipMalloc(&s->desc, sizeof(LiveDesc) * nb) != hipSuccess) return fail("desc");
     if (hipMalloc(&s->status, sizeof(int)) != hipSuccess) return fail("status");
-    if (hipMalloc(&s->pack, sizeof(float) * packed_weight_floats()) != hipSuccess) return fail("weights");
-    if (pack_weights(W.L, s->pack, &W.pk, s->stream) != hipSuccess) return fail("weight packing");
+    GroupArgs ga{};
+    if (group > 1) {
+        if (group_setup(cfg, G, group, s->stream, &W, &s->grp, &ga) != SSLA_OK) return fail("group set-up");
+    } else {
+        if (hipMalloc(&s->pack, sizeof(float) * packed_weight_floats()) != hipSuccess) return fail("weights");
+        if (pack_weights(W.L, s->pack, &W.pk, s->stream) != hipSuccess) return fail("weight packing");
+    }
     if (phase_us) {
         if (hipMalloc(&s->prof, sizeof(unsigned long long) * NPROF * nb) != hipSuccess) return fail("profile");
         s->phase_us = phase_us;
@@ -1238,7 +1990,10 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
         d.timing_mask = cfg->timing_mask;
         d.kstart = cfg->kernel_start_clk[b];
         d.kend = cfg->kernel_end_clk[b];
+        d.clk_sync = timing_clock_sync(cfg, b);
         d.prof = s->prof ? s->prof + (size_t)NPROF * b : nullptr;
+        // the tail (host memory) does not move while no kernel drains the ring
+        d.t0 = *reinterpret_cast<volatile unsigned long long*>(tails[b]);
     }
     if (hipMemsetAsync(s->scratch, 0, sbytes, s->stream) != hipSuccess) return fail("memset");
     if (hipMemsetAsync(s->status, 0, sizeof(int), s->stream) != hipSuccess) return fail("memset");
@@ -1246,8 +2001,12 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
         return fail("copy");
     if (hipStreamSynchronize(s->stream) != hipSuccess) return fail("sync");
     const unsigned long long idle = (unsigned long long)idle_timeout_ms * (unsigned long long)khz;
-    hipLaunchKernelGGL(k_live, dim3(nb), dim3(LT), 0, s->stream, s->desc, W, G, stop_flag, spin_ns,
-                       idle, max_batch, s->status);
+    if (group > 1)
+        hipLaunchKernelGGL(k_group<true>, dim3(nb * group), dim3(LT), 0, s->stream, s->desc, W, G, ga,
+                           stop_flag, spin_ns, idle, max_batch, s->status);
+    else
+        hipLaunchKernelGGL(k_live, dim3(nb), dim3(LT), 0, s->stream, s->desc, W, G, stop_flag, spin_ns,
+                           idle, max_batch, s->status);
     if (hipGetLastError() != hipSuccess) return fail("launch");
     *out = s;
     return SSLA_OK;
@@ -1282,7 +2041,8 @@ int live_wait(LiveSession* s, int timeout_ms, int* status_out) {
         add_profile(h.data(), s->nb, s->phase_us);
         (void)hipFree(s->prof);
     }
-    (void)hipFree(s->pack);
+    if (s->pack) (void)hipFree(s->pack);
+    s->grp.release();
     (void)hipStreamDestroy(s->stream);
     (void)hipFree(s->desc);
     (void)hipFree(s->scratch);

@@ -105,12 +105,13 @@ class SslaHipDrainOpts(ctypes.Structure):
         ("head_outs", ctypes.POINTER(ctypes.c_void_p)),
         ("phase_ms", ctypes.POINTER(ctypes.c_float)),
         ("batch_phase_us", ctypes.POINTER(ctypes.c_double)),
+        ("group", ctypes.c_int),
     ]
 
 
 class SslaHipLiveOpts(ctypes.Structure):
     _fields_ = [("max_batch", ctypes.c_int), ("idle_timeout_ms", ctypes.c_uint),
-                ("phase_us", ctypes.POINTER(ctypes.c_double))]
+                ("phase_us", ctypes.POINTER(ctypes.c_double)), ("group", ctypes.c_int)]
 
 
 class SslaHipOevaDiff(ctypes.Structure):
@@ -139,7 +140,8 @@ BATCH_PHASES = ("load", "tdrop2", "pairs2",
                 "L4.proj", "L4.scan", "L4.out", "L4.ln", "L5.proj", "L5.scan", "L5.out", "L5.ln",
                 "tdrop3", "pairs3",
                 "L6.proj", "L6.scan", "L6.out", "L6.ln", "L7.proj", "L7.scan", "L7.out", "L7.ln",
-                "head.hidden", "head.out", "preds", "publish", "batches", "records")
+                "head.hidden", "head.out", "preds", "publish", "batches", "records",
+                "L4.xwait", "L5.xwait", "L6.xwait", "L7.xwait")
 N_BATCH_PHASES = 32
 
 

@@ -274,9 +274,10 @@ class Drain:
             self._heads.append(DeviceBuffer(n * 7 * 4) if want_head else None)
 
     def run(self, stream: int = 0, sync: bool = True, phase_ms: Optional[np.ndarray] = None,
-            batch: int = 0, batch_phase_us: Optional[np.ndarray] = None) -> None:
+            batch: int = 0, batch_phase_us: Optional[np.ndarray] = None, group: int = 0) -> None:
         """One drain call over the loaded rings.  phase_ms (float32 array of
-        len(abi.DRAIN_PHASES)) accumulates per-phase GPU time (needs sync)."""
+        len(abi.DRAIN_PHASES)) accumulates per-phase GPU time (needs sync).
+        group (batch mode): workgroups per block, 3..6 (0 = one)."""
         nb = self.cfg.n_blocks
         if len(self._rings) != nb:
             raise ValueError(f"load_rings needs {nb} rings")
@@ -287,6 +288,7 @@ class Drain:
         opts.stream = stream or None
         opts.sync = 1 if sync else 0
         opts.batch = batch
+        opts.group = group
         heads = None
         if self._heads and self._heads[0] is not None:
             heads = (ctypes.c_void_p * nb)(*[b.ptr for b in self._heads])
@@ -318,11 +320,12 @@ class Drain:
             heads.append(h.download(np.float32, n * 7).reshape(n, 7) if h is not None else None)
         return outs, heads
 
-    def drain(self, records: Sequence[np.ndarray], want_head: bool = False, batch: int = 0):
+    def drain(self, records: Sequence[np.ndarray], want_head: bool = False, batch: int = 0,
+              group: int = 0):
         """Drain pre-filled rings; batch 0 = whole-ring drain, 1..32 = in-kernel
-        batches of that many records."""
+        batches of that many records (group: workgroups per block, 3..6)."""
         self.load_rings(records, want_head=want_head)
-        self.run(batch=batch)
+        self.run(batch=batch, group=group)
         return self.results()
 
     def drain_recorded(self, records: Sequence[np.ndarray], recorder: "grid.OracleRecorder",
@@ -470,13 +473,14 @@ class LiveDrain:
     """A running persistent drain over HostRings (ssla_hip_persistent_start)."""
 
     def __init__(self, drain: Drain, rings: HostRings, spin_ns: int = 200, max_batch: int = 32,
-                 idle_timeout_ms: int = 30000, profile: bool = False):
+                 idle_timeout_ms: int = 30000, profile: bool = False, group: int = 0):
         self.rings = rings
         self.h = ctypes.c_void_p()
         bufs, tails, dones = rings.ptrs()
         # in-kernel phase profile, filled by wait() (abi.BATCH_PHASES order)
         self.phase_us = np.zeros(abi.N_BATCH_PHASES, np.float64) if profile else None
         opts = abi.SslaHipLiveOpts(max_batch, idle_timeout_ms)
+        opts.group = group
         if profile:
             opts.phase_us = self.phase_us.ctypes.data_as(ctypes.POINTER(ctypes.c_double))
         lib.check(lib.load().ssla_hip_persistent_start(

@@ -5,11 +5,16 @@ Mirrors the reference's live runner (orin/hybrid_runner_multi.py:430-760):
 the producer (libstage01_to_gpu.so) runs stages 0 + 1 on CPU shards fed by
 its paced synthetic source and publishes records to one ring per block; the
 persistent kernel drains them and writes a GpuTimingSlot per record.  GPU
-clock stamps are put on the host clock with a two-point calibration: the
-kernel's start and exit stamps, each observed by a host thread spinning on
-the fine-grained word the kernel writes (hybrid_runner_multi.py:525-534,
-688-760).  Latency statistics cover output-producing records (owner, pass2
-and pass3), as the reference reports them.
+clock stamps are put on the host clock with a two-point calibration
+(hybrid_runner_multi.py:525-534, 688-760).  Each point is a clock
+handshake with the running kernel (the host writes a ping word, the kernel
+answers with its clock), bracketed by two host clock readings; the
+sample with the tightest bracket is kept, before the source starts and
+after the rings have drained.  (The kernel's own start and exit stamps,
+observed by a host thread spinning on them, remain the fallback: the host
+can see them late, e.g. when the kernel started before the host began to
+spin.)  Latency statistics cover output-producing records (owner, pass2 and
+pass3), as the reference reports them.
 """
 from __future__ import annotations
 
@@ -48,6 +53,37 @@ def _spin_nonzero(read, timeout_s: float) -> int:
             return v
         if time.monotonic() > t_end:
             return 0
+
+
+def clock_pair(drain: Drain, blk: int, tries: int = 32, timeout_s: float = 0.05):
+    """(host ns, GPU wall-clock ticks) of one instant from the live kernel's
+    clock handshake on block blk (ssla_hip_timing_alloc's ping / pong words),
+    and the host bracket in ns; None when the kernel does not answer."""
+    words = np.ctypeslib.as_array(
+        (np.ctypeslib.ctypes.c_ulonglong * 4).from_address(drain.cfg.kernel_start_clk[blk]))
+    best = None
+    for _ in range(tries):
+        seq = (int(words[2]) + 1) & 0xffffffff or 1
+        ta = _now_ns()
+        words[2] = seq
+        t_end = time.monotonic() + timeout_s
+        while (int(words[3]) & 0xff) != (seq & 0xff):
+            if time.monotonic() > t_end:
+                return best
+        tb = _now_ns()
+        clk = int(words[3]) >> 8
+        if best is None or tb - ta < best[2]:
+            best = ((ta + tb) // 2, clk, tb - ta)
+    return best
+
+
+def _calibration(p0, p1, k0: int, t0_cpu: int, k1: int, t1_cpu: int):
+    """(host ns at GPU tick k_ref, k_ref, ns per tick): from two handshake
+    points when both exist, else from the kernel's start and exit stamps."""
+    if p0 is not None and p1 is not None and p1[1] > p0[1]:
+        return p0[0], p0[1], (p1[0] - p0[0]) / (p1[1] - p0[1])
+    npt = (t1_cpu - t0_cpu) / max(1, (k1 - k0)) if k1 else 10.0
+    return t0_cpu, k0, npt
 
 
 def pct(a: np.ndarray, q: float) -> float:
@@ -100,7 +136,7 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
              n_blobs: int = 8, sigma_px: float = 3.0, bg_frac: float = 0.1,
              ring_capacity: int = 1 << 16, timing_capacity: int = 1 << 22, max_batch: int = 32,
              spin_ns: int = 200, profile: bool = True, drain_timeout_s: float = 30.0,
-             back_pressure: bool = False,
+             back_pressure: bool = False, group: int = 0,
              inspect: Optional[Callable] = None) -> LiveResult:
     """One live run on one GPU.  back_pressure makes the producer wait for
     each ring's tail instead of overwriting unread slots.  gpu_blocks (1, 2, 4, 8, 16; the reference's
@@ -111,7 +147,9 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
     covers the records that produce a prediction (owner, pass2, pass3).
     inspect(drain, rings, heads, topo), when given, is called once the kernel
     has stopped and before any buffer is freed (heads: records published per
-    ring), e.g. to check the rings' contents and the final state."""
+    ring), e.g. to check the rings' contents and the final state.  group
+    (3..6) drains each strip with that many workgroups, each owning channel
+    slices of every layer (0: one workgroup per strip)."""
     if base_core is None or synth_core is None:
         sc, bc = pick_cores(n_shards)
         synth_core = sc if synth_core is None else synth_core
@@ -135,13 +173,14 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
             prod.set_ring_tails(rings.tail_ptrs(), timeout_ms=1000.0 * drain_timeout_s)
         live = LiveDrain(drain, rings, spin_ns=spin_ns, max_batch=max_batch,
                          idle_timeout_ms=int((duration_s + drain_timeout_s + 30) * 1000),
-                         profile=profile)
+                         profile=profile, group=group)
         clks = [np.ctypeslib.as_array((np.ctypeslib.ctypes.c_ulonglong * 2).from_address(
             c.kernel_start_clk[b])) for b in range(nb)]
         k0 = [_spin_nonzero(lambda a=a: int(a[0]), 30.0) for a in clks]
         t0_cpu = _now_ns()
         if not all(k0):
             raise RuntimeError("the live kernel did not start")
+        sync0 = [clock_pair(drain, b) for b in range(nb)]
         prod.reset()
         t_start = time.monotonic()
         prod.start_synthetic_blobs(rate_mev, synth_core, seed, n_blobs, sigma_px, bg_frac)
@@ -162,6 +201,7 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
         while any(int(rings.done[b]) < heads[b] for b in range(nb)) and time.monotonic() < t_end:
             time.sleep(0.0005)
         drained = [int(rings.done[b]) for b in range(nb)]
+        sync1 = [clock_pair(drain, b) for b in range(nb)]
         rings.stop()
         k1 = [_spin_nonzero(lambda a=a: int(a[1]), 30.0) for a in clks]
         t1_cpu = _now_ns()
@@ -174,12 +214,12 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
         cols = {k: [] for k in ("e2d", "e2p", "p2d", "kern", "own", "ok")}
         for b in range(nb):
             # per-block two-point calibration of the GPU clock
-            ns_per_tick = (t1_cpu - t0_cpu) / max(1, (k1[b] - k0[b])) if k1[b] else 1e6 / 1e5
+            h_ref, k_ref, ns_per_tick = _calibration(sync0[b], sync1[b], k0[b], t0_cpu, k1[b], t1_cpu)
             tv = drain.timing(b)
             n_keep = min(drained[b], tv.size)
             tv = tv[(np.arange(drained[b] - n_keep, drained[b]) & (tv.size - 1))] if n_keep else tv[:0]
             ok = (tv["t_done_clk"] != 0) & (tv["t_emit_ns"] != 0) & (tv["t_push_ns"] != 0)
-            t_done = t0_cpu + (tv["t_done_clk"].astype(np.float64) - k0[b]) * ns_per_tick
+            t_done = h_ref + (tv["t_done_clk"].astype(np.float64) - k_ref) * ns_per_tick
             cols["e2d"].append((t_done - tv["t_emit_ns"].astype(np.float64)) / 1e3)
             cols["e2p"].append((tv["t_push_ns"].astype(np.float64)
                                 - tv["t_emit_ns"].astype(np.float64)) / 1e3)
@@ -235,7 +275,7 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
                timing_capacity: int = 1 << 18, max_batch: int = 32, spin_ns: int = 200,
                pin_core: Optional[int] = None, profile: bool = True, expect_p3=None,
                drain_timeout_s: float = 60.0, strips=None,
-               speed: Optional[float] = None,
+               speed: Optional[float] = None, group: int = 0,
                inspect: Optional[Callable] = None) -> ReplayResult:
     """Several rings live on one GPU: pre-built ring records (one array per
     ring) replayed into one ring each, one persistent workgroup per ring.
@@ -247,7 +287,7 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
     time).  expect_p3 (optional, one flag array per ring) gives each ring's
     drop drift: records whose timing-slot owner flag differs from it.
     inspect(drain), when given, is called once the kernel has stopped and
-    before the state is freed."""
+    before the state is freed.  group as in run_live."""
     from .producer import Replay
     nb = len(streams)
     if pin_core is None:
@@ -259,12 +299,14 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
         drain.alloc_timing(timing_capacity)
         c = drain.cfg
         live = LiveDrain(drain, rings, spin_ns=spin_ns, max_batch=max_batch,
-                         idle_timeout_ms=int((drain_timeout_s + 60) * 1000), profile=profile)
+                         idle_timeout_ms=int((drain_timeout_s + 60) * 1000), profile=profile,
+                         group=group)
         clk = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_ulonglong * 2).from_address(c.kernel_start_clk[0]))
         k0 = _spin_nonzero(lambda: int(clk[0]), 30.0)
         t0_cpu = _now_ns()
         if not k0:
             raise RuntimeError("the live kernel did not start")
+        sync0 = clock_pair(drain, 0)
         t_start = time.monotonic()
         rp = Replay([b.ptr for b in rings.bufs], rings.head_ptrs(), ring_capacity - 1, streams,
                     rate_per_stream * nb, pin_core, speed=speed)
@@ -283,6 +325,7 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
         drained = [int(rings.done[b]) for b in range(nb)]
         rp.stop()
         rp = None
+        sync1 = clock_pair(drain, 0)
         rings.stop()
         k1 = _spin_nonzero(lambda: int(clk[1]), 30.0)
         t1_cpu = _now_ns()
@@ -291,13 +334,13 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
         live = None
         if inspect is not None:
             inspect(drain)
-        ns_per_tick = (t1_cpu - t0_cpu) / max(1, (k1 - k0)) if k1 else 10.0
+        h_ref, k_ref, ns_per_tick = _calibration(sync0, sync1, k0, t0_cpu, k1, t1_cpu)
         out = []
         for b in range(nb):
             n = min(drained[b], timing_capacity)
             tv = drain.timing(b)[:n]
             own = tv["owner"] == 1
-            t_done = t0_cpu + (tv["t_done_clk"].astype(np.float64) - k0) * ns_per_tick
+            t_done = h_ref + (tv["t_done_clk"].astype(np.float64) - k_ref) * ns_per_tick
             lat = (t_done - tv["t_push_ns"].astype(np.float64)) / 1e3
             kern = (tv["t_done_clk"].astype(np.float64) - tv["t_pop_clk"].astype(np.float64)) \
                 * ns_per_tick / 1e3

@@ -465,18 +465,20 @@ def _check_block_preds(preds, version, x, y, own, p3, ref7, owned):
             assert np.abs(preds[c] - ref7[k[-1]]).max() <= HEAD_TOL, c
 
 
-@pytest.mark.parametrize("gpu_blocks", [1, 8])
-def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks):
+@pytest.mark.parametrize("gpu_blocks,group", [(1, 0), (8, 0), (1, 6)])
+def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks, group):
     """The live configuration as stated: the producer's paced blob source at
     2.0 Mev/s -> 6 host shards for stages 0 + 1 (halo 2) -> fine-grained
     rings -> the persistent kernel, 2 s (orin/hybrid_runner_multi.py:314-754).
-    One ownership domain (1 block) and the reference's 8-strip topology.
+    One ownership domain (1 block) and the reference's 8-strip topology,
+    one workgroup per block; and one domain drained by a group of 6
+    workgroups (channel slices, exact: no halo).
     Every published record is drained with no overrun, and each ring's
     contents, run through the oracle with that block's ownership, give the
     kernel's pass flags (timing-slot owner flags), tdrop counters, final
     hidden state and prediction grid."""
     from ssla_hip import live as LV
-    say(f"config 2: 2.0 Mev/s, 6 shards, halo 2, 2 s, {gpu_blocks} GPU block(s)")
+    say(f"config 2: 2.0 Mev/s, 6 shards, halo 2, 2 s, {gpu_blocks} GPU block(s), group {group}")
     cap = 1 << 19 if gpu_blocks == 1 else 1 << 18
     seen = {}
 
@@ -507,7 +509,7 @@ def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks):
 
     r = LV.run_live(stub_dir, rate_mev=2.0, duration_s=2.0, n_shards=6, halo=2,
                     gpu_blocks=gpu_blocks, ring_capacity=cap, timing_capacity=cap,
-                    inspect=inspect)
+                    group=group, inspect=inspect)
     say(f"config 2: status {r.status}, {r.synth_events} events "
         f"({r.synth_events / r.duration_s / 1e6:.2f} Mev/s achieved), {r.ring_records} ring records, "
         f"{r.drained} drained, {r.output_records} output-producing, "
@@ -520,7 +522,8 @@ def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks):
     assert r.synth_events > 0.5 * 2.0e6 * r.duration_s
 
 
-def test_config4_sixteen_rings_one_persistent_kernel(stub_dir, stub_npz):
+@pytest.mark.parametrize("group", [0, 6])
+def test_config4_sixteen_rings_one_persistent_kernel(stub_dir, stub_npz, group):
     """Config 4: 16 independent 80x64 instances sharing the stub weights in
     one persistent kernel (...celled.cuh:82 MAX_BLOCKS = 16, :1547), each fed
     its own seeded blob stream (seeds 1..16) through its own ring at 125k
@@ -529,7 +532,7 @@ def test_config4_sixteen_rings_one_persistent_kernel(stub_dir, stub_npz):
     the oracle's."""
     from ssla_hip import live as LV
     n = 40_000
-    say(f"config 4: 16 rings x {n} records at 125k records/s each")
+    say(f"config 4: 16 rings x {n} records at 125k records/s each, group {group}")
     recs = [events.blob_records(n, seed=1 + s) for s in range(16)]
     expect = [O.decisions(r.x, r.y, 16, 20, 4)[1] for r in recs]
     state = {}
@@ -541,7 +544,7 @@ def test_config4_sixteen_rings_one_persistent_kernel(stub_dir, stub_npz):
 
     res = LV.run_replay(stub_dir, [events.to_records(r) for r in recs], 125_000.0,
                         ring_capacity=1 << 16, timing_capacity=1 << 16, expect_p3=expect,
-                        inspect=inspect)
+                        group=group, inspect=inspect)
     say("config 4: status", res.status, "per stream (drained, drift, p50 us, p99 us):",
         [(s["drained"], s["drop_drift"], round(s["push_to_done_p50"], 1),
           round(s["push_to_done_p99"], 1)) for s in res.streams])
