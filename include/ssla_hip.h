@@ -183,6 +183,10 @@ typedef struct SslaHipDrainOpts {
                                   block, each owning 16-channel slices of
                                   every layer (see ssla_hip_persistent_start);
                                   runs synchronously */
+    unsigned long long phase_mask; /* with phase_ms: time only the phases
+                                  whose bit is set (bit k = phase k); 0 =
+                                  all.  Each timed phase boundary costs a
+                                  few microseconds of queue time */
 } SslaHipDrainOpts;
 
 int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg,

@@ -629,7 +629,8 @@ int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg, const HybridInputRec* const
     }
     if (group > 1) { set_error("group is a batch-mode option"); return SSLA_ERR_ARG; }
     if (bph) { set_error("batch_phase_us is only measured by the batch-mode drain"); return SSLA_ERR_ARG; }
-    return scan_drain(cfg, rings, ns, outs, opts ? opts->head_outs : nullptr, st, sync, phase_ms);
+    return scan_drain(cfg, rings, ns, outs, opts ? opts->head_outs : nullptr, st, sync, phase_ms,
+                      opts ? opts->phase_mask : 0ull);
 }
 
 int ssla_hip_drain_batch_noalloc(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,

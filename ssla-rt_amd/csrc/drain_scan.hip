@@ -77,11 +77,26 @@ __device__ __forceinline__ int find_block(const BlockDesc* bd, int nb, int g) {
 // feat1 quarters, lane 0 also writes the keys.
 constexpr int kDecRec = 32;          // records per 256-thread workgroup
 
+// Up to kFills int arrays set to a value each (k_decode's extra blocks).
+constexpr int kFills = 5;
+struct FillSet {
+    int* p[kFills];
+    int n[kFills];
+    int v[kFills];
+};
+
 __global__ void __launch_bounds__(256)
 k_decode(int E, const BlockDesc* __restrict__ bd, Geometry G,
          float* __restrict__ X0, int* __restrict__ cell2,
          unsigned char* __restrict__ owner,
-         uint32_t* __restrict__ key2, uint32_t* __restrict__ val2) {
+         uint32_t* __restrict__ key2, uint32_t* __restrict__ val2, int ndec, FillSet f, int fblk) {
+    if ((int)blockIdx.x >= ndec) {
+        // the call's fills: fblk blocks of 256 per array
+        const int fb = (int)blockIdx.x - ndec, a = fb / fblk;
+        const int i = (fb - a * fblk) * 256 + (int)threadIdx.x;
+        if (i < f.n[a]) f.p[a][i] = f.v[a];
+        return;
+    }
     const int g = blockIdx.x * kDecRec + (threadIdx.x >> 3);
     const int c = threadIdx.x & 7;
     if (g >= E) return;
@@ -103,19 +118,7 @@ k_decode(int E, const BlockDesc* __restrict__ bd, Geometry G,
     val2[g] = (uint32_t)g;
 }
 
-// Up to kFills int arrays set to a value each, one launch (blockIdx.y = array).
-constexpr int kFills = 5;
-struct FillSet {
-    int* p[kFills];
-    int n[kFills];
-    int v[kFills];
-};
 
-__global__ void k_fill_set(FillSet f) {
-    const int a = blockIdx.y;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < f.n[a]) f.p[a][i] = f.v[a];
-}
 
 // ---------------------------------------------------------------------------
 // Stable LSD radix sort of (key, record) pairs, digits of up to 9 bits.
@@ -281,66 +284,7 @@ __global__ void __launch_bounds__(kScanThreads) k_exscan(int n, int* __restrict_
     }
 }
 
-// Per-key tables from per-key counts (k < nk), in one launch:
-//   cnt  -> start (exclusive scan), end = start + cnt (end may be cnt itself);
-//           with coff: coff[k] = the key's first chunk of kCH, *n_chunks;
-//   cnt2 (optional) -> off2 (exclusive scan), *total2.
 constexpr int kCH = 64;     // pairs per scan chunk
-
-__global__ void __launch_bounds__(kScanThreads)
-k_keyscan(int nk, const int* cnt, int* __restrict__ start, int* end, int* __restrict__ coff,
-          int* __restrict__ n_chunks, const int* __restrict__ cnt2, int* __restrict__ off2,
-          int* __restrict__ total2) {
-    __shared__ int lds[2 * (kScanThreads / 64)];
-    int carry = 0, ccarry = 0, carry2 = 0;
-    for (int r0 = 0; r0 < nk; r0 += kScanRound) {
-        const int i0 = r0 + (int)threadIdx.x * kScanPer;
-        int v[kScanPer], c[kScanPer], u[kScanPer];
-        load8(cnt, i0, nk, v);
-        if (cnt2) load8(cnt2, i0, nk, u);
-        int s = 0, sc = 0, su = 0;
-        #pragma unroll
-        for (int q = 0; q < kScanPer; ++q) {
-            s += v[q];
-            c[q] = (v[q] + kCH - 1) / kCH;
-            sc += c[q];
-            if (cnt2) su += u[q];
-        }
-        int total;
-        int run = carry + block_exscan(s, lds, &total);
-        carry += total;
-        int crun = 0, urun = 0;
-        if (coff) {
-            crun = ccarry + block_exscan(sc, lds, &total);
-            ccarry += total;
-        }
-        if (cnt2) {
-            urun = carry2 + block_exscan(su, lds, &total);
-            carry2 += total;
-        }
-        int st[kScanPer], en[kScanPer];
-        #pragma unroll
-        for (int q = 0; q < kScanPer; ++q) {
-            st[q] = run;
-            run += v[q];
-            en[q] = run;
-            const int x = c[q];
-            c[q] = crun;
-            crun += x;
-            const int y = u[q];
-            u[q] = urun;
-            urun += y;
-        }
-        store8(start, i0, nk, st);
-        store8(end, i0, nk, en);
-        if (coff) store8(coff, i0, nk, c);
-        if (cnt2) store8(off2, i0, nk, u);
-    }
-    if (threadIdx.x == 0) {
-        if (coff) *n_chunks = ccarry;
-        if (cnt2) *total2 = carry2;
-    }
-}
 
 // Chunk tables: one wave per key writes its chunks (ckey, cbeg, cend).
 __global__ void __launch_bounds__(256)
@@ -392,12 +336,11 @@ __device__ __forceinline__ int tdrop_passes(unsigned c, int r, int window) {
 // key's run, counter c before the call): pass2[g], and the pass-2 list in
 // s2 order -- the record's place is the key's offset plus the number of
 // passing ranks below r.
-__global__ void __launch_bounds__(256)
-k_tdrop2(int n, const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
-         uint32_t nk, const int* __restrict__ start, const unsigned char* __restrict__ old,
-         const int* __restrict__ off, int window, unsigned char* __restrict__ pass,
-         int* __restrict__ list) {
-    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void
+tdrop2_at(int p, int n, const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
+          uint32_t nk, const int* __restrict__ start, const unsigned char* __restrict__ old,
+          const int* __restrict__ off, int window, unsigned char* __restrict__ pass,
+          int* __restrict__ list) {
     if (p >= n) return;
     const uint32_t k = keys[p];
     const int g = (int)vals[p];
@@ -411,6 +354,7 @@ k_tdrop2(int n, const uint32_t* __restrict__ keys, const uint32_t* __restrict__ 
     pass[g] = take ? 1 : 0;
     if (take) list[off[k] + tdrop_passes(c, r, window)] = g;
 }
+
 
 // Per s2 key: the counter before this call (old[k]), the counter after it,
 // the number of pass-2 records of the run (n2[k]) and the pair count of the
@@ -439,6 +383,127 @@ __global__ void k_keys2(uint32_t nk, int C, int W, int H, const int* __restrict_
             np += en[s] - st[s];
         }
     pcnt[t] = np;
+}
+
+// The per-key tables of k_keys2 (and k_runs) for a one-pass record sort,
+// whose digit is the whole key: the scanned tile histogram bh (bin-major, T
+// tiles) holds the run bounds, key t's run being [bh[t T], bh[(t + 1) T]).
+// key2_at writes st / en / old and the committed counter, and returns the
+// key's pair count and pass-2 count (used by k_keyscan<true>).
+struct KeyHist {
+    int C, W, H, T, window;
+    const int* bh;
+    int* st;
+    int* en;
+    const BlockDesc* bd;
+    unsigned char* old;
+};
+
+__device__ __forceinline__ void key2_at(uint32_t t, const KeyHist& kh, int& pc, int& n2v) {
+    const int b = (int)t / kh.C, cell = (int)t % kh.C, ty = cell / kh.W, tx = cell % kh.W;
+    const int s0 = kh.bh[(size_t)t * kh.T], len = kh.bh[(size_t)(t + 1) * kh.T] - s0;
+    kh.st[t] = s0;
+    kh.en[t] = s0 + len;
+    unsigned char* td = kh.bd[b].td2 + cell;
+    const unsigned c = *td;
+    kh.old[t] = (unsigned char)c;
+    n2v = tdrop_passes(c, len, kh.window);
+    *td = (unsigned char)((c + (unsigned)len) & 255u);
+    int np = 0;
+    #pragma unroll
+    for (int oy = -1; oy <= 1; ++oy)
+        #pragma unroll
+        for (int ox = -1; ox <= 1; ++ox) {
+            const int sy = ty + oy, sx = tx + ox;
+            if (sy < 0 || sy >= kh.H || sx < 0 || sx >= kh.W) continue;
+            const size_t q = (size_t)(b * kh.C + sy * kh.W + sx);
+            np += kh.bh[(q + 1) * kh.T] - kh.bh[q * kh.T];
+        }
+    pc = np;
+}
+
+// Per-key tables from per-key counts (k < nk), in one launch:
+//   cnt  -> start (exclusive scan), end = start + cnt (end may be cnt itself);
+//           with coff: coff[k] = the key's first chunk of kCH, *n_chunks;
+//   cnt2 (optional) -> off2 (exclusive scan), *total2.
+// KH: the counts come from key2_at (a one-pass sort's histogram, kh; nk <=
+// kScanThreads) instead of cnt / cnt2, and cnt2 then receives the pass-2
+// counts.
+template <bool KH>
+__global__ void __launch_bounds__(kScanThreads)
+k_keyscan(int nk, const int* cnt, int* __restrict__ start, int* end, int* __restrict__ coff,
+          int* __restrict__ n_chunks, const int* __restrict__ cnt2, int* __restrict__ off2,
+          int* __restrict__ total2, KeyHist kh) {
+    __shared__ int lds[2 * (kScanThreads / 64)];
+    __shared__ int kv[KH ? kScanThreads : 1], ku[KH ? kScanThreads : 1];
+    int carry = 0, ccarry = 0, carry2 = 0;
+    for (int r0 = 0; r0 < nk; r0 += kScanRound) {
+        const int i0 = r0 + (int)threadIdx.x * kScanPer;
+        int v[kScanPer], c[kScanPer], u[kScanPer];
+        if constexpr (KH) {
+            // one key per thread (nk <= kScanThreads), through LDS into the
+            // eight-per-thread layout of the scan
+            const int t = (int)threadIdx.x;
+            int pc = 0, p2 = 0;
+            if (t < nk) {
+                key2_at((uint32_t)t, kh, pc, p2);
+                const_cast<int*>(cnt2)[t] = p2;
+            }
+            kv[t] = pc;
+            ku[t] = p2;
+            __syncthreads();
+            #pragma unroll
+            for (int q = 0; q < kScanPer; ++q) {
+                const bool in = i0 + q < kScanThreads;
+                v[q] = in ? kv[i0 + q] : 0;
+                u[q] = in ? ku[i0 + q] : 0;
+            }
+        } else {
+            load8(cnt, i0, nk, v);
+            if (cnt2) load8(cnt2, i0, nk, u);
+        }
+        int s = 0, sc = 0, su = 0;
+        #pragma unroll
+        for (int q = 0; q < kScanPer; ++q) {
+            s += v[q];
+            c[q] = (v[q] + kCH - 1) / kCH;
+            sc += c[q];
+            if (cnt2) su += u[q];
+        }
+        int total;
+        int run = carry + block_exscan(s, lds, &total);
+        carry += total;
+        int crun = 0, urun = 0;
+        if (coff) {
+            crun = ccarry + block_exscan(sc, lds, &total);
+            ccarry += total;
+        }
+        if (cnt2) {
+            urun = carry2 + block_exscan(su, lds, &total);
+            carry2 += total;
+        }
+        int st[kScanPer], en[kScanPer];
+        #pragma unroll
+        for (int q = 0; q < kScanPer; ++q) {
+            st[q] = run;
+            run += v[q];
+            en[q] = run;
+            const int x = c[q];
+            c[q] = crun;
+            crun += x;
+            const int y = u[q];
+            u[q] = urun;
+            urun += y;
+        }
+        store8(start, i0, nk, st);
+        store8(end, i0, nk, en);
+        if (coff) store8(coff, i0, nk, c);
+        if (cnt2) store8(off2, i0, nk, u);
+    }
+    if (threadIdx.x == 0) {
+        if (coff) *n_chunks = ccarry;
+        if (cnt2) *total2 = carry2;
+    }
 }
 
 // Per s3 key: the number of pass-2 records of its four s2 cells (t3, the
@@ -565,106 +630,161 @@ __global__ void k_keys3b(uint32_t nk3, Geometry G, const int* __restrict__ t3,
 // centre cell (run [st, en) of ascending record ids per key), t's pair count
 // is the sum of the run lengths over its 3 x 3 neighbourhood, and a pair's
 // rank inside t is the number of records below g in those nine runs.
-
-constexpr int kRankWindow = 256;   // widest neighbour window searched cooperatively
-
+//
 // One thread per sorted record i (record g = vals[i], key k = keys[i]): the
 // ranks of g in the 5 x 5 runs around its centre cell (its own run gives
 // i - st[k]), folded row by row into three horizontal 3-sums; a delta's rank
 // is the sum of three of them.  pos[g * 9 + d] = the pair's place in the pair
 // order (-1 when the target is off the grid or the record has no key),
-// pair_rec[place] = g.
-//
-// A wave whose 64 records share one centre cell (the usual case: records are
-// sorted by cell) ranks them together.  Its lanes' ids increase, so in each
-// neighbour run every lane's lower bound lies between those of the first and
-// the last lane: 48 lanes find these 2 x 24 bounds by binary search at once,
-// then the wave loads the window between them 64 values at a time and each
-// lane counts the values below its id by a six-step search across the lanes
-// (ds_bpermute).  A window wider than kRankWindow is searched per lane inside
-// its bounds.  Other waves (cell boundaries, the tail) search per lane.
-__global__ void __launch_bounds__(256)
-k_pair_rank(int n_max, const int* __restrict__ n_dev, const uint32_t* __restrict__ keys,
-            const uint32_t* __restrict__ vals, uint32_t nk, int C, int W, int H,
-            const int* __restrict__ st, const int* __restrict__ en, const int* __restrict__ pst,
-            int* __restrict__ pos, int* __restrict__ pair_rec) {
-    const int n = n_dev ? *n_dev : n_max;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+// pair_rec[place] = g.  The lanes of a wave that share a centre cell (records
+// are sorted by cell) rank together: every load then serves the whole
+// segment, which keeps the L2 request count low.
+constexpr int kSegMax = 4;   // cell segments of a wave ranked together; more: per lane
+constexpr int kChunkWide = 512;   // widest window counted in 64-value chunks
+
+// r25[c] for the lanes `in` of one segment (lanes l0..l1 holding records of
+// key ks, ids ascending): in each neighbour run c of the 5 x 5 block, every
+// such lane's lower bound lies between those of lanes l0 and l1, which 48
+// lanes find by binary search at once.  The windows are then read 64 values
+// at a time, one coalesced load per window (chunk j of every window together),
+// and each lane counts the values below its id by a six-step search across
+// the lanes (ds_bpermute), the 24 windows' searches interleaved.  Windows
+// wider than kChunkWide are searched per lane inside their bounds, all of
+// them advanced together.  Every lane of the wave takes part.
+__device__ __forceinline__ void
+rank_segment(uint32_t ks, int l0, int l1, bool in, uint32_t g, const uint32_t* __restrict__ vals,
+             int C, int W, int H, const int* __restrict__ st, const int* __restrict__ en,
+             int* r25) {
+    const int lane = threadIdx.x & 63;
+    const int b = (int)ks / C, cell = (int)ks % C, y = cell / W, x = cell % W;
+    const uint32_t g_first = (uint32_t)__builtin_amdgcn_readlane((int)g, l0);
+    const uint32_t g_last = (uint32_t)__builtin_amdgcn_readlane((int)g, l1);
+    // lanes c and 32 + c (c < 25): run c's bounds for the first and last id
+    int bnd = 0, s0 = 0;
+    {
+        const int c = lane & 31;
+        const int sy = y + c / 5 - 2, sx = x + c % 5 - 2;
+        if (c < 25 && c != 12 && sy >= 0 && sy < H && sx >= 0 && sx < W) {
+            const int s = b * C + sy * W + sx;
+            s0 = st[s];
+            bnd = lower_bound_u32(vals, s0, en[s] - s0, lane < 32 ? g_first : g_last);
+        }
+    }
+    // windows up to kChunkWide values: read 64 values at a time, one coalesced
+    // load per window (chunk j of every window together); each lane counts
+    // the values below its id by a six-step search across the lanes
+    // (ds_bpermute), the 24 windows' searches interleaved
+    int wmax = 0;
+    #pragma unroll
+    for (int c = 0; c < 25; ++c) {
+        const int wa = __builtin_amdgcn_readlane(bnd, c);
+        const int we = __builtin_amdgcn_readlane(bnd, 32 + c);
+        if (c != 12 && we - wa <= kChunkWide) wmax = max(wmax, we - wa);
+    }
+    int lo25[25];
+    #pragma unroll
+    for (int c = 0; c < 25; ++c) lo25[c] = 0;
+    for (int base = 0; base < wmax; base += 64) {
+        uint32_t pw[25];
+        #pragma unroll
+        for (int c = 0; c < 25; ++c) {
+            const int wa = __builtin_amdgcn_readlane(bnd, c);
+            const int we = __builtin_amdgcn_readlane(bnd, 32 + c);
+            pw[c] = (c != 12 && we - wa <= kChunkWide && wa + base + lane < we)
+                        ? vals[wa + base + lane] : 0xffffffffu;
+        }
+        int lc[25];
+        #pragma unroll
+        for (int c = 0; c < 25; ++c) lc[c] = 0;
+        #pragma unroll
+        for (int step = 32; step > 0; step >>= 1) {
+            #pragma unroll
+            for (int c = 0; c < 25; ++c) {
+                const uint32_t q = (uint32_t)__builtin_amdgcn_ds_bpermute(
+                    (lc[c] + step - 1) << 2, (int)pw[c]);
+                if (q < g) lc[c] += step;
+            }
+        }
+        #pragma unroll
+        for (int c = 0; c < 25; ++c) {
+            const uint32_t q = (uint32_t)__builtin_amdgcn_ds_bpermute(lc[c] << 2, (int)pw[c]);
+            lo25[c] += lc[c] + (q < g ? 1 : 0);
+        }
+    }
+    // wider still: per-lane binary searches inside the windows, all of them
+    // advanced together
+    int wlo[25], wlen[25];
+    bool wide = false;
+    #pragma unroll
+    for (int c = 0; c < 25; ++c) {
+        const int wa = __builtin_amdgcn_readlane(bnd, c);
+        const int we = __builtin_amdgcn_readlane(bnd, 32 + c);
+        wlo[c] = wa;
+        wlen[c] = (in && c != 12 && we - wa > kChunkWide) ? we - wa : 0;
+        wide |= c != 12 && we - wa > kChunkWide;
+    }
+    if (wide) {
+        for (;;) {
+            int active = 0;
+            #pragma unroll
+            for (int c = 0; c < 25; ++c) {
+                if (wlen[c] > 0) {
+                    const int half = wlen[c] >> 1;
+                    if (vals[wlo[c] + half] < g) {
+                        wlo[c] += half + 1;
+                        wlen[c] -= half + 1;
+                    } else {
+                        wlen[c] = half;
+                    }
+                }
+                active |= wlen[c];
+            }
+            if (!active) break;
+        }
+    }
+    #pragma unroll
+    for (int c = 0; c < 25; ++c) {
+        const int wa = __builtin_amdgcn_readlane(bnd, c);
+        const int we = __builtin_amdgcn_readlane(bnd, 32 + c);
+        const int ws = __builtin_amdgcn_readlane(s0, c);
+        if (in && c != 12) r25[c] = wa - ws + (we - wa > kChunkWide ? wlo[c] - wa : lo25[c]);
+    }
+}
+
+// A wave's lanes are consecutive records of the sorted order.  When they
+// span at most kSegMax keys (the usual case), each key's segment is ranked
+// by rank_segment; otherwise each lane searches the 24 whole runs, all 24
+// binary searches advanced together.
+__device__ __forceinline__ void
+pair_rank_at(int i, int n, const uint32_t* __restrict__ keys,
+             const uint32_t* __restrict__ vals, uint32_t nk, int C, int W, int H,
+             const int* __restrict__ st, const int* __restrict__ en, const int* __restrict__ pst,
+             int* __restrict__ pos, int* __restrict__ pair_rec) {
     const int lane = threadIdx.x & 63;
     const bool valid = i < n;
     const uint32_t k = valid ? keys[i] : nk;
     const uint32_t g = valid ? vals[i] : 0u;
-    const uint32_t k0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)k);
-    const bool together = __all(valid && k == k0 && k < nk);
-    if (!valid) return;
-    int* pg = pos + (size_t)g * kPatch;
-    if (k >= nk) {
-        #pragma unroll
-        for (int d = 0; d < kPatch; ++d) pg[d] = -1;
-        return;
-    }
-    const int b = (int)k / C, cell = (int)k % C, y = cell / W, x = cell % W;
-    const int own = i - st[k];
+    const bool keyed = valid && k < nk;
+    const uint32_t kprev = (uint32_t)__builtin_amdgcn_ds_bpermute(((lane + 63) & 63) << 2, (int)k);
+    const unsigned long long kmask = __ballot(keyed);
+    const int nseg = __popcll(__ballot(keyed && (lane == 0 || kprev != k)));
     // r25[c]: the number of records below g in run c of the 5 x 5 block
     // (c = 5 row + column, c = 12 the record's own run)
     int r25[25];
-    if (together) {
-        // lanes c and 32 + c (c < 25): run c's bounds for the first and last id
-        const uint32_t g_first = (uint32_t)__builtin_amdgcn_readlane((int)g, 0);
-        const uint32_t g_last = (uint32_t)__builtin_amdgcn_readlane((int)g, 63);
-        int bnd = 0, s0 = 0;
-        {
-            const int c = lane & 31;
-            const int sy = y + c / 5 - 2, sx = x + c % 5 - 2;
-            if (c < 25 && c != 12 && sy >= 0 && sy < H && sx >= 0 && sx < W) {
-                const int s = b * C + sy * W + sx;
-                s0 = st[s];
-                bnd = lower_bound_u32(vals, s0, en[s] - s0, lane < 32 ? g_first : g_last);
-            }
+    #pragma unroll
+    for (int c = 0; c < 25; ++c) r25[c] = 0;
+    if (nseg <= kSegMax) {
+        unsigned long long left = kmask;
+        while (left) {
+            const int l0 = (int)__ffsll((long long)left) - 1;
+            const uint32_t ks = (uint32_t)__builtin_amdgcn_readlane((int)k, l0);
+            const unsigned long long seg = __ballot(keyed && k == ks);
+            const int l1 = 63 - (int)__clzll((long long)seg);
+            rank_segment(ks, l0, l1, (seg >> lane) & 1ull, g, vals, C, W, H, st, en, r25);
+            left &= ~seg;
         }
-        // the first 64 values of every window, all loads in flight together
-        uint32_t pv[25];
-        #pragma unroll
-        for (int c = 0; c < 25; ++c) {
-            const int wa = __builtin_amdgcn_readlane(bnd, c);
-            const int we = __builtin_amdgcn_readlane(bnd, 32 + c);
-            pv[c] = (c != 12 && we - wa <= kRankWindow && wa + lane < we) ? vals[wa + lane]
-                                                                          : 0xffffffffu;
-        }
-        // values below g among 64 ascending lane values (six steps across lanes)
-        auto below = [&](uint32_t v) {
-            int lo = 0;
-            #pragma unroll
-            for (int step = 32; step > 0; step >>= 1) {
-                const uint32_t q = (uint32_t)__builtin_amdgcn_ds_bpermute((lo + step - 1) << 2,
-                                                                          (int)v);
-                if (q < g) lo += step;
-            }
-            const uint32_t q = (uint32_t)__builtin_amdgcn_ds_bpermute(lo << 2, (int)v);
-            return lo + (q < g ? 1 : 0);
-        };
-        #pragma unroll
-        for (int c = 0; c < 25; ++c) {
-            if (c == 12) {
-                r25[c] = own;
-                continue;
-            }
-            const int wa = __builtin_amdgcn_readlane(bnd, c);
-            const int we = __builtin_amdgcn_readlane(bnd, 32 + c);
-            const int ws = __builtin_amdgcn_readlane(s0, c);
-            int cnt;
-            if (we - wa > kRankWindow) {
-                cnt = lower_bound_u32(vals, wa, we - wa, g) - wa;
-            } else {
-                cnt = below(pv[c]);
-                for (int base = wa + 64; base < we; base += 64)
-                    cnt += below(base + lane < we ? vals[base + lane] : 0xffffffffu);
-            }
-            r25[c] = wa - ws + cnt;
-        }
-    } else {
-        // per lane: the 24 binary searches advance together, one step each
-        // per pass, so their loads are in flight at once
+    } else if (keyed) {
+        const int b = (int)k / C, cell = (int)k % C, y = cell / W, x = cell % W;
         int lo[25], len[25];
         #pragma unroll
         for (int c = 0; c < 25; ++c) {
@@ -693,8 +813,16 @@ k_pair_rank(int n_max, const int* __restrict__ n_dev, const uint32_t* __restrict
         }
         #pragma unroll
         for (int c = 0; c < 25; ++c) r25[c] = lo[c] - r25[c];
-        r25[12] = own;
     }
+    if (!valid) return;
+    int* pg = pos + (size_t)g * kPatch;
+    if (k >= nk) {
+        #pragma unroll
+        for (int d = 0; d < kPatch; ++d) pg[d] = -1;
+        return;
+    }
+    const int b = (int)k / C, cell = (int)k % C, y = cell / W, x = cell % W;
+    r25[12] = i - st[k];
     int hs[5][3];                  // hs[row][dx + 1]: runs (row, dx - 1 .. dx + 1)
     #pragma unroll
     for (int row = 0; row < 5; ++row)
@@ -714,6 +842,43 @@ k_pair_rank(int n_max, const int* __restrict__ n_dev, const uint32_t* __restrict
         pg[d] = p;
         pair_rec[p] = (int)g;
     }
+}
+
+__global__ void __launch_bounds__(256)
+k_pair_rank(int n_max, const int* __restrict__ n_dev, const uint32_t* __restrict__ keys,
+            const uint32_t* __restrict__ vals, uint32_t nk, int C, int W, int H,
+            const int* __restrict__ st, const int* __restrict__ en, const int* __restrict__ pst,
+            int* __restrict__ pos, int* __restrict__ pair_rec) {
+    pair_rank_at(blockIdx.x * blockDim.x + threadIdx.x, n_dev ? *n_dev : n_max, keys, vals, nk,
+                 C, W, H, st, en, pst, pos, pair_rec);
+}
+
+// The s2 level's tables that need only the sorted order and the key scan, in
+// one launch: per sorted record (blocks [0, nbr)) its tdrop_s2 decision and
+// list slot (k_tdrop2) and its pair ranks (k_pair_rank); per key (blocks
+// nbr.., one wave each) its chunk table (k_chunks).
+__global__ void __launch_bounds__(256)
+k_s2_tables(int n, int nbr, const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
+            uint32_t nk, int C, int W, int H, const int* __restrict__ st,
+            const int* __restrict__ en, const int* __restrict__ pst, const int* __restrict__ pen,
+            const int* __restrict__ coff, const unsigned char* __restrict__ old,
+            const int* __restrict__ off, int window, unsigned char* __restrict__ pass,
+            int* __restrict__ list, int* __restrict__ pos, int* __restrict__ pair_rec,
+            int* __restrict__ ckey, int* __restrict__ cbeg, int* __restrict__ cend) {
+    if ((int)blockIdx.x >= nbr) {
+        const uint32_t k = (blockIdx.x - (unsigned)nbr) * 4u + (threadIdx.x >> 6);
+        if (k >= nk) return;
+        const int s0 = pst[k], e = pen[k], c0 = coff[k];
+        for (int q = threadIdx.x & 63; s0 + q * kCH < e; q += 64) {
+            ckey[c0 + q] = (int)k;
+            cbeg[c0 + q] = s0 + q * kCH;
+            cend[c0 + q] = min(e, s0 + (q + 1) * kCH);
+        }
+        return;
+    }
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    tdrop2_at(i, n, keys, vals, nk, st, old, off, window, pass, list);
+    pair_rank_at(i, n, keys, vals, nk, C, W, H, st, en, pst, pos, pair_rec);
 }
 
 // ---------------------------------------------------------------------------
@@ -1545,7 +1710,7 @@ int drain_reserve(const HybridS2S3Config* cfg, int max_records) {
 int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                const int* ns, HybridS2S3OutputSlot* const* outs,
                float* const* head_outs, hipStream_t st, bool sync,
-               float* phase_ms) {
+               float* phase_ms, unsigned long long phase_mask) {
     const int nb = cfg->n_blocks;
     if (nb < 1 || nb > SSLA_MAX_BLOCKS) {
         set_error("n_blocks must be in [1, 16]");
@@ -1641,21 +1806,25 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     HIPCHK(hipMemcpyAsync(w.bd, w.bd_host, sizeof(hbd), hipMemcpyHostToDevice, st));
     HIPCHK(hipEventRecord(w.bd_copied, st));
 
-    // Phase timing: events recorded on `st` between phases (optional).
+    // Phase timing (optional): events recorded on `st` at the boundaries of
+    // the phases in pmask only -- each event costs a few microseconds of
+    // queue time between the kernels it separates.
     hipEvent_t ev[SSLA_DRAIN_PHASES + 1] = {};
-    int n_ev = 0;
+    int n_mark = 0;
+    const unsigned long long pmask = phase_ms ? (phase_mask ? phase_mask : ~0ull) : 0ull;
     struct EvFree {
         hipEvent_t* ev;
-        int& n;
         ~EvFree() {
-            for (int k = 0; k < n; ++k) (void)hipEventDestroy(ev[k]);
+            for (int k = 0; k <= SSLA_DRAIN_PHASES; ++k)
+                if (ev[k]) (void)hipEventDestroy(ev[k]);
         }
-    } ev_free{ev, n_ev};
+    } ev_free{ev};
     auto mark = [&]() -> int {
-        if (!phase_ms) return SSLA_OK;
-        if (!ev[n_ev]) HIPCHK(hipEventCreate(&ev[n_ev]));
-        HIPCHK(hipEventRecord(ev[n_ev], st));
-        ++n_ev;
+        const int b = n_mark++;                       // boundary b opens phase b
+        if (b > SSLA_DRAIN_PHASES) return SSLA_OK;
+        if (!((pmask >> b) & 1ull) && !(b > 0 && ((pmask >> (b - 1)) & 1ull))) return SSLA_OK;
+        HIPCHK(hipEventCreate(&ev[b]));
+        HIPCHK(hipEventRecord(ev[b], st));
         return SSLA_OK;
     };
 #define MARK() do { const int rc_ = mark(); if (rc_) return rc_; } while (0)
@@ -1680,8 +1849,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     MARK();
     // per-call fills: run bounds of the s2 keys (k_runs writes those that
     // occur), the list and chunk counters, the prediction-grid writers
+    FillSet f{};
     {
-        FillSet f{};
         int* arr[kFills] = {w.st2, w.en2, w.counts, w.last3, w.cnt3};
         const int len[kFills] = {(int)nk2, (int)nk2, 8, have_head ? (int)nk3 : 0,
                                  have_head ? (int)nk3 : 0};
@@ -1691,12 +1860,13 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
             f.n[i] = len[i];
             f.v[i] = val[i];
         }
-        hipLaunchKernelGGL(k_fill_set, dim3(grid1(std::max<int>((int)nk2, 8), 256), kFills),
-                           dim3(256), 0, st, f);
     }
-    // ---- decode; stable radix sort of the records by s2 key ------------------
-    hipLaunchKernelGGL(k_decode, dim3(grid1(E, kDecRec)), dim3(256), 0, st, E, w.bd, G, w.X0,
-                       w.cell2, w.owner, w.ka, w.va);
+    // ---- decode (and the fills); stable radix sort of the records by s2 key --
+    {
+        const int ndec = (int)grid1(E, kDecRec), fblk = (int)grid1(std::max<int>((int)nk2, 8), 256);
+        hipLaunchKernelGGL(k_decode, dim3(ndec + fblk * kFills), dim3(256), 0, st, E, w.bd, G,
+                           w.X0, w.cell2, w.owner, w.ka, w.va, ndec, f, fblk);
+    }
     const int bits2 = bits_for(nk2);
     const int passes = (bits2 + kRMaxBits - 1) / kRMaxBits;
     const int T = (int)grid1(E, kRTile);
@@ -1727,24 +1897,29 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     uint32_t* const K3 = kout;
     uint32_t* const V3 = vout;
     // ---- counters, tdrop_s2, the pass-2 list, s2 pair and chunk tables -----
-    hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, st, E, K2, nk2, w.st2, w.en2);
-    hipLaunchKernelGGL(k_keys2, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, G.C2, G.W2, G.H2,
-                       w.st2, w.en2, w.bd, G.window, w.old2, w.n2, w.pen2);
-    hipLaunchKernelGGL(k_keyscan, dim3(1), dim3(kScanThreads), 0, st, (int)nk2, w.pen2, w.pst2,
-                       w.pen2, w.coff2, w.counts + 2, w.n2, w.off2, w.counts + 0);
-    hipLaunchKernelGGL(k_tdrop2, dim3(grid1(E, 256)), dim3(256), 0, st, E, K2, V2, nk2, w.st2,
-                       w.old2, w.off2, G.window, w.pass2, w.list2);
-    // The s3 ordering needs only the s2 order, pass2 and the old counters, so
-    // it runs on the side stream while the s2 pair ranks, L4 and L5 run here;
-    // L6 waits for it.  Every launch is sized by E; the pass-2 count stays on
-    // the device.  The side stream's launches are enqueued after L4's.
-    HIPCHK(hipEventRecord(w.s2_ordered, st));
-    hipStream_t s3 = w.side;
-    HIPCHK(hipStreamWaitEvent(s3, w.s2_ordered, 0));
-    hipLaunchKernelGGL(k_pair_rank, dim3(grid1(E, 256)), dim3(256), 0, st, E, (const int*)nullptr,
-                       K2, V2, nk2, G.C2, G.W2, G.H2, w.st2, w.en2, w.pst2, w.pos2, w.prec2);
-    hipLaunchKernelGGL(k_chunks, dim3(grid1(nk2, 4)), dim3(256), 0, st, nk2, w.pst2, w.pen2,
-                       w.coff2, w.ckey2, w.cbeg2, w.cend2);
+    if (passes == 1 && nk2 <= (uint32_t)kScanThreads) {
+        // the one pass's histogram holds the run bounds: the key tables and
+        // their scans in one workgroup
+        const KeyHist kh{G.C2, G.W2, G.H2, T, G.window, (const int*)w.bh, w.st2, w.en2, w.bd,
+                         w.old2};
+        hipLaunchKernelGGL(k_keyscan<true>, dim3(1), dim3(kScanThreads), 0, st, (int)nk2,
+                           (const int*)nullptr, w.pst2, w.pen2, w.coff2, w.counts + 2, w.n2,
+                           w.off2, w.counts + 0, kh);
+    } else {
+        hipLaunchKernelGGL(k_runs, dim3(grid1(E, 256)), dim3(256), 0, st, E, K2, nk2, w.st2, w.en2);
+        hipLaunchKernelGGL(k_keys2, dim3(grid1(nk2, 256)), dim3(256), 0, st, nk2, G.C2, G.W2, G.H2,
+                           w.st2, w.en2, w.bd, G.window, w.old2, w.n2, w.pen2);
+        hipLaunchKernelGGL(k_keyscan<false>, dim3(1), dim3(kScanThreads), 0, st, (int)nk2, w.pen2,
+                           w.pst2, w.pen2, w.coff2, w.counts + 2, w.n2, w.off2, w.counts + 0,
+                           KeyHist{});
+    }
+    {
+        const unsigned nbr = grid1(E, 256);
+        hipLaunchKernelGGL(k_s2_tables, dim3(nbr + grid1(nk2, 4)), dim3(256), 0, st, E, (int)nbr,
+                           K2, V2, nk2, G.C2, G.W2, G.H2, w.st2, w.en2, w.pst2, w.pen2, w.coff2,
+                           w.old2, w.off2, G.window, w.pass2, w.list2, w.pos2, w.prec2, w.ckey2,
+                           w.cbeg2, w.cend2);
+    }
     MARK();
     const LayerWeightsS2S3* L = cfg->layers[0];
     const unsigned tilesE = grid1(E, kTM);
@@ -1752,6 +1927,14 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // ---- L4: 24 -> 48, all records ----------------------------------------
     hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, pk.pp[0], w.QVG);
+    // The s3 ordering needs only the s2 order, pass2 and the old counters, so
+    // it runs on the side stream while L4 and L5 run here; L6 waits for it.
+    // Every launch is sized by E; the pass-2 count stays on the device.  Its
+    // event follows L4's projection, where the queue gap it costs overlaps
+    // nothing on this stream's critical path but the projection's own tail.
+    HIPCHK(hipEventRecord(w.s2_ordered, st));
+    hipStream_t s3 = w.side;
+    HIPCHK(hipStreamWaitEvent(s3, w.s2_ordered, 0));
     MARK();
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
@@ -1771,8 +1954,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // launch, and L4 keeps the device busy meanwhile)
     hipLaunchKernelGGL(k_keys3a, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, G, w.n2, w.bd,
                        w.t3, w.n3);
-    hipLaunchKernelGGL(k_keyscan, dim3(1), dim3(kScanThreads), 0, s3, (int)nk3, w.t3, w.st3,
-                       w.en3, (int*)nullptr, (int*)nullptr, w.n3, w.off3, w.counts + 1);
+    hipLaunchKernelGGL(k_keyscan<false>, dim3(1), dim3(kScanThreads), 0, s3, (int)nk3, w.t3, w.st3,
+                       w.en3, (int*)nullptr, (int*)nullptr, w.n3, w.off3, w.counts + 1,
+                       KeyHist{});
     hipLaunchKernelGGL(k_place3, dim3(grid1(E, 256)), dim3(256), 0, s3, (const int*)(w.counts + 0),
                        w.list2, w.bd, G, w.cell2, w.sidx, V2, w.st2, w.en2, w.old2, w.st3, K3, V3,
                        w.key3g);
@@ -1781,9 +1965,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        have_head ? 1 : 0, w.pass3, w.list3, w.last3, w.cnt3);
     hipLaunchKernelGGL(k_keys3b, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, G, w.t3, w.bd,
                        w.pen3);
-    hipLaunchKernelGGL(k_keyscan, dim3(1), dim3(kScanThreads), 0, s3, (int)nk3, w.pen3, w.pst3,
+    hipLaunchKernelGGL(k_keyscan<false>, dim3(1), dim3(kScanThreads), 0, s3, (int)nk3, w.pen3, w.pst3,
                        w.pen3, w.coff3, w.counts + 3, (const int*)nullptr, (int*)nullptr,
-                       (int*)nullptr);
+                       (int*)nullptr, KeyHist{});
     hipLaunchKernelGGL(k_chunks, dim3(grid1(nk3, 4)), dim3(256), 0, s3, nk3, w.pst3, w.pen3,
                        w.coff3, w.ckey3, w.cbeg3, w.cend3);
     hipLaunchKernelGGL(k_pair_rank, dim3(grid1(E, 256)), dim3(256), 0, s3, E,
@@ -1865,7 +2049,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     end.finish();
     if (sync) HIPCHK(hipStreamSynchronize(st));
     if (phase_ms) {
-        for (int k = 0; k + 1 < n_ev && k < SSLA_DRAIN_PHASES; ++k) {
+        for (int k = 0; k < SSLA_DRAIN_PHASES; ++k) {
+            if (!((pmask >> k) & 1ull) || !ev[k] || !ev[k + 1]) continue;
             float ms = 0.f;
             HIPCHK(hipEventElapsedTime(&ms, ev[k], ev[k + 1]));
             phase_ms[k] += ms;

@@ -106,6 +106,7 @@ class SslaHipDrainOpts(ctypes.Structure):
         ("phase_ms", ctypes.POINTER(ctypes.c_float)),
         ("batch_phase_us", ctypes.POINTER(ctypes.c_double)),
         ("group", ctypes.c_int),
+        ("phase_mask", ctypes.c_ulonglong),
     ]
 
 

@@ -274,10 +274,12 @@ class Drain:
             self._heads.append(DeviceBuffer(n * 7 * 4) if want_head else None)
 
     def run(self, stream: int = 0, sync: bool = True, phase_ms: Optional[np.ndarray] = None,
-            batch: int = 0, batch_phase_us: Optional[np.ndarray] = None, group: int = 0) -> None:
+            batch: int = 0, batch_phase_us: Optional[np.ndarray] = None, group: int = 0,
+            phase_mask: int = 0) -> None:
         """One drain call over the loaded rings.  phase_ms (float32 array of
-        len(abi.DRAIN_PHASES)) accumulates per-phase GPU time (needs sync).
-        group (batch mode): workgroups per block, 3..6 (0 = one)."""
+        len(abi.DRAIN_PHASES)) accumulates per-phase GPU time (needs sync) of
+        the phases in phase_mask (bit k = phase k; 0 = all).  group (batch
+        mode): workgroups per block, 3..6 (0 = one)."""
         nb = self.cfg.n_blocks
         if len(self._rings) != nb:
             raise ValueError(f"load_rings needs {nb} rings")
@@ -289,6 +291,7 @@ class Drain:
         opts.sync = 1 if sync else 0
         opts.batch = batch
         opts.group = group
+        opts.phase_mask = phase_mask
         heads = None
         if self._heads and self._heads[0] is not None:
             heads = (ctypes.c_void_p * nb)(*[b.ptr for b in self._heads])
