@@ -122,7 +122,7 @@ k_decode(int E, const BlockDesc* __restrict__ bd, Geometry G,
 
 // ---------------------------------------------------------------------------
 // Stable LSD radix sort of (key, record) pairs, digits of up to 9 bits.
-// Records are taken in tiles of kRTile (256 threads x 16 rounds, round r =
+// Records are taken in tiles of kRTile (256 threads x 8 rounds, round r =
 // records base + 256 r .. + 255).  Per pass:
 //   k_rs_hist     digit counts of every tile            -> bh[digit * T + tile]
 //   k_exscan      exclusive scan of bh (digit-major)    -> first slot of every
@@ -132,11 +132,11 @@ k_decode(int E, const BlockDesc* __restrict__ bd, Geometry G,
 //                 the lanes whose digit equals its own (one ballot per digit
 //                 bit), across the round's waves and rounds from LDS counts.
 // ---------------------------------------------------------------------------
-constexpr int kRThreads = 256, kRRounds = 16, kRTile = kRThreads * kRRounds;
+constexpr int kRThreads = 256, kRRounds = 8, kRTile = kRThreads * kRRounds;
 constexpr int kRMaxBits = 9;
 
 __global__ void __launch_bounds__(kRThreads)
-k_rs_hist(int n, const uint32_t* __restrict__ keys, int shift, int bits, int T,
+k_rs_hist(int n, const uint32_t* __restrict__ keys, int shift, int bits, int nbins, int T,
           int* __restrict__ bh) {
     __shared__ int h[1 << kRMaxBits];
     const int nb = 1 << bits, tid = threadIdx.x;
@@ -149,7 +149,7 @@ k_rs_hist(int n, const uint32_t* __restrict__ keys, int shift, int bits, int T,
         if (idx < n) atomicAdd(&h[(keys[idx] >> shift) & (nb - 1)], 1);
     }
     __syncthreads();
-    for (int i = tid; i < nb; i += kRThreads) bh[(size_t)i * T + blockIdx.x] = h[i];
+    for (int i = tid; i < nbins; i += kRThreads) bh[(size_t)i * T + blockIdx.x] = h[i];
 }
 
 // vin null: the values are the record indices.  sidx (last pass, optional):
@@ -157,11 +157,11 @@ k_rs_hist(int n, const uint32_t* __restrict__ keys, int shift, int bits, int T,
 __global__ void __launch_bounds__(kRThreads)
 k_rs_scatter(int n, const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
              uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int* __restrict__ sidx,
-             int shift, int bits, int T, const int* __restrict__ boff) {
+             int shift, int bits, int nbins, int T, const int* __restrict__ boff) {
     __shared__ int cnt[1 << kRMaxBits];
     __shared__ int wcnt[kRThreads / 64][1 << kRMaxBits];
     const int nb = 1 << bits, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
-    for (int i = tid; i < nb; i += kRThreads) {
+    for (int i = tid; i < nbins; i += kRThreads) {
         cnt[i] = boff[(size_t)i * T + blockIdx.x];
         #pragma unroll
         for (int w = 0; w < kRThreads / 64; ++w) wcnt[w][i] = 0;
@@ -1877,11 +1877,14 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
             set_error("drain: radix histogram larger than its workspace");
             return SSLA_ERR_STATE;
         }
-        hipLaunchKernelGGL(k_rs_hist, dim3(T), dim3(kRThreads), 0, st, E, kin, shift, bits, T,
-                           w.bh);
-        hipLaunchKernelGGL(k_exscan, dim3(1), dim3(kScanThreads), 0, st, (1 << bits) * T, w.bh);
+        // a one-pass sort's digit is the whole key: bins for the keys present
+        // (nk2 values and the keyless records' nk2) only
+        const int nbins = passes == 1 ? (int)nk2 + 1 : 1 << bits;
+        hipLaunchKernelGGL(k_rs_hist, dim3(T), dim3(kRThreads), 0, st, E, kin, shift, bits, nbins,
+                           T, w.bh);
+        hipLaunchKernelGGL(k_exscan, dim3(1), dim3(kScanThreads), 0, st, nbins * T, w.bh);
         hipLaunchKernelGGL(k_rs_scatter, dim3(T), dim3(kRThreads), 0, st, E, kin, vin, kout, vout,
-                           ps == passes - 1 ? w.sidx : nullptr, shift, bits, T, w.bh);
+                           ps == passes - 1 ? w.sidx : nullptr, shift, bits, nbins, T, w.bh);
         shift += bits;
         // the next pass writes the pair of buffers this pass read from
         uint32_t* const k2 = kout == w.kb ? w.ka : w.kb;
