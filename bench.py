@@ -537,9 +537,9 @@ TRAFFIC_PHASES = {
     "k_outt<48, 96, 1, 3>": ["L6.out"], "k_outt<96, 96, 1, 3>": ["L7.out"],
     "k_head": ["head"], "k_pred_write": ["head"], "k_emit": ["emit"],
 }
-ORDER_KERNELS = ("k_fill_set", "k_decode", "k_rs_hist", "k_exscan", "k_rs_scatter", "k_runs",
-                 "k_keys2", "k_keyscan", "k_tdrop2", "k_pair_rank", "k_chunks", "k_keys3a",
-                 "k_place3", "k_tdrop3", "k_keys3b")
+ORDER_KERNELS = ("k_decode", "k_rs_hist", "k_exscan", "k_rs_scatter", "k_runs", "k_keys2",
+                 "k_keyscan", "k_s2_tables", "k_pair_rank", "k_chunks", "k_keys3a", "k_place3",
+                 "k_tdrop3", "k_keys3b")
 
 
 def _kname(n: str) -> str:
@@ -562,11 +562,11 @@ def pmc_summary(fetch_dir, write_dir, cfetch_dir, cwrite_dir, copy_bytes, comman
 
     def per_phase(rs):
         seen, out = collections.Counter(), collections.defaultdict(float)
-        calls = sum(1 for r in rs if _kname(r["Kernel_Name"]) == "k_fill_set")
+        calls = sum(1 for r in rs if _kname(r["Kernel_Name"]) == "k_decode")
         for r in rs:
             k = _kname(r["Kernel_Name"])
             v = float(r["Counter_Value"]) * 1024.0
-            if k in ORDER_KERNELS:
+            if k.split("<")[0] in ORDER_KERNELS:
                 out["order"] += v / max(1, calls)
             elif k in TRAFFIC_PHASES:
                 ph = TRAFFIC_PHASES[k]

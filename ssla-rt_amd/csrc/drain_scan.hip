@@ -1923,6 +1923,15 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                            w.old2, w.off2, G.window, w.pass2, w.list2, w.pos2, w.prec2, w.ckey2,
                            w.cbeg2, w.cend2);
     }
+    // The s3 ordering needs only the s2 order, pass2 and the old counters, so
+    // it runs on the side stream while L4 and L5 run here; L6 waits for it.
+    // Every launch is sized by E; the pass-2 count stays on the device.  Its
+    // event sits before L4's projection: started later, the side stream's
+    // small kernels overlap L4's carry pass, a latency-bound chain per cell
+    // that they slow down by more than the event's queue gap costs here.
+    HIPCHK(hipEventRecord(w.s2_ordered, st));
+    hipStream_t s3 = w.side;
+    HIPCHK(hipStreamWaitEvent(s3, w.s2_ordered, 0));
     MARK();
     const LayerWeightsS2S3* L = cfg->layers[0];
     const unsigned tilesE = grid1(E, kTM);
@@ -1930,14 +1939,6 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // ---- L4: 24 -> 48, all records ----------------------------------------
     hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, pk.pp[0], w.QVG);
-    // The s3 ordering needs only the s2 order, pass2 and the old counters, so
-    // it runs on the side stream while L4 and L5 run here; L6 waits for it.
-    // Every launch is sized by E; the pass-2 count stays on the device.  Its
-    // event follows L4's projection, where the queue gap it costs overlaps
-    // nothing on this stream's critical path but the projection's own tail.
-    HIPCHK(hipEventRecord(w.s2_ordered, st));
-    hipStream_t s3 = w.side;
-    HIPCHK(hipStreamWaitEvent(s3, w.s2_ordered, 0));
     MARK();
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
