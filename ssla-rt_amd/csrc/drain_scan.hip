@@ -888,11 +888,11 @@ k_s2_tables(int n, int nbr, const uint32_t* __restrict__ keys, const uint32_t* _
 // tile) items, loads an item's weights (fragment order, one float4 per four
 // k-steps) while the previous item's four row tiles run, and writes each
 // [v | g] row (2 * OUT floats) to the pair's sorted position.  q is not
-// stored: the contraction recomputes it from the record's input.  Each
-// 16 x 16 result tile passes through a wave-private LDS tile so that lanes
-// store whole 16-byte pieces of rows; no workgroup barrier is involved
-// (staging whole rows across waves measured slower: the barriers cost more
-// than the partial-line writes).
+// stored: the contraction recomputes it from the record's input.  With the
+// weights as the A operand a lane's four results are four consecutive
+// channels of one record, stored as one 16-byte piece of its row (staging
+// whole rows across waves measured slower: the barriers cost more than the
+// partial-line writes).
 // ---------------------------------------------------------------------------
 constexpr int kTM = 64;     // records per projection / contraction workgroup
 
@@ -917,8 +917,6 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
     constexpr int tlo = P::TQ, thi = P::T;      // the v and g column tiles
     __shared__ __align__(16) float xs[kTM * XST];
     __shared__ int prow[kPatch][kTM];
-    constexpr int TST = kMT + 4;                 // transpose tile row stride (16-byte rows)
-    __shared__ __align__(16) float tt[4][kMT * TST];   // one 16 x 16 tile per wave
     const int n = n_dev ? *n_dev : n_max;
     const int base = blockIdx.x * kTM;
     if (base >= n) return;
@@ -947,26 +945,21 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
     const int lane = tid & 63, wv = tid >> 6, li = lane & 15, lk = lane >> 4;
     const int nti = thi - tlo, N = kPatch * nti, mtiles = (cnt + kMT - 1) / kMT;
     auto item = [&](int it) { const int d = it / nti; return d * P::T + tlo + (it - d * nti); };
-    // each 16 x 16 result tile goes through the wave's LDS tile so that a
-    // lane stores one float4 of a row (lane l: row l / 4, columns 4 (l % 4))
-    float* tw = tt[wv];
-    const int trow = lane >> 2, tq = lane & 3;
+    // The weight fragment is the A operand and the records the B operand, so
+    // the 16 x 16 result is (channel, record): lane (li, lk) holds channels
+    // 4 lk .. 4 lk + 3 of record li -- one float4 of that record's row.
     auto run = [&](int it, const float* b) {
-        const int d = it / nti, t = tlo + (it - d * nti), c0 = t * kMT - OUT + 4 * tq;
+        const int d = it / nti, t = tlo + (it - d * nti), c0 = t * kMT - OUT + 4 * lk;
         for (int m = 0; m < mtiles; ++m) {
             const float* a = &xs[(m * kMT + li) * XST + lk];
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
             #pragma unroll
             for (int s = 0; s < P::KS; ++s)
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s], b[s], acc, 0, 0, 0);
-            #pragma unroll
-            for (int r = 0; r < 4; ++r) tw[(4 * lk + r) * TST + li] = acc[r];
-            __builtin_amdgcn_wave_barrier();
-            const float4 v = *reinterpret_cast<const float4*>(&tw[trow * TST + 4 * tq]);
-            __builtin_amdgcn_wave_barrier();
-            const int pr = prow[d][m * kMT + trow];
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(b[s], a[4 * s], acc, 0, 0, 0);
+            const int pr = prow[d][m * kMT + li];
             if (pr >= 0)
-                *reinterpret_cast<float4*>(QVG + (size_t)pr * NCW + c0) = v;
+                *reinterpret_cast<float4*>(QVG + (size_t)pr * NCW + c0) =
+                    make_float4(acc[0], acc[1], acc[2], acc[3]);
         }
     };
     float b0[P::KS4 * 4], b1[P::KS4 * 4];
