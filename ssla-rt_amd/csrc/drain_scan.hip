@@ -883,7 +883,7 @@ k_s2_tables(int n, int nbr, const uint32_t* __restrict__ keys, const uint32_t* _
 
 // ---------------------------------------------------------------------------
 // P: v, g rows as 16 x 16 MFMA tiles (v_mfma_f32_16x16x4_f32, operand layout
-// in mfma_pack.h).  One workgroup = 64 records (rows, staged in LDS) x all 9
+// in mfma_pack.h).  A record tile = 64 records (rows, staged in LDS) x all 9
 // deltas x the v and g column tiles of qvgIn; each wave owns (delta, column
 // tile) items, loads an item's weights (fragment order, one float4 per four
 // k-steps) while the previous item's four row tiles run, and writes each
@@ -893,6 +893,13 @@ k_s2_tables(int n, int nbr, const uint32_t* __restrict__ keys, const uint32_t* _
 // channels of one record, stored as one 16-byte piece of its row (staging
 // whole rows across waves measured slower: the barriers cost more than the
 // partial-line writes).
+//
+// PT (the layers over all records): a workgroup loops over record tiles
+// (tile += gridDim.x) and loads the next tile's rows and pair positions into
+// registers while the current tile runs, so the load latency of a tile is
+// not paid at the start of a workgroup.  The grid is sized per layer from the
+// CU count (scan_drain).  The pass-2 layers keep one tile per workgroup: the
+// prefetch registers cost L7 (IN = 96) a wave per SIMD.
 // ---------------------------------------------------------------------------
 constexpr int kTM = 64;     // records per projection / contraction workgroup
 
@@ -907,43 +914,16 @@ __device__ __forceinline__ void lds_put4(float* p, float4 v) {
     reinterpret_cast<float2*>(p)[1] = make_float2(v.z, v.w);
 }
 
+// The items of one staged record tile (mtiles row tiles of 16 records).
 template <int IN, int OUT>
-__global__ void __launch_bounds__(256)
-k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
-      const float* __restrict__ X, const int* __restrict__ pos, const float* __restrict__ pp,
-      float* __restrict__ QVG) {
+__device__ __forceinline__ void qvg_items(const float* __restrict__ xs, const int (*prow)[kTM],
+                                          int mtiles, const float* __restrict__ pp,
+                                          float* __restrict__ QVG) {
     using P = ProjPack<IN, OUT>;
     constexpr int XST = lds_stride(IN), NCW = 2 * OUT;
     constexpr int tlo = P::TQ, thi = P::T;      // the v and g column tiles
-    __shared__ __align__(16) float xs[kTM * XST];
-    __shared__ int prow[kPatch][kTM];
-    const int n = n_dev ? *n_dev : n_max;
-    const int base = blockIdx.x * kTM;
-    if (base >= n) return;
-    const int cnt = min(kTM, n - base);
-    const int tid = threadIdx.x;
-    constexpr int I4 = IN / 4;
-    for (int t = tid; t < kTM * I4; t += 256) {
-        const int r = t / I4, q = t - r * I4;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (r < cnt) {
-            const int g = list ? list[base + r] : base + r;
-            v = reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q];
-        }
-        lds_put4(&xs[r * XST + 4 * q], v);
-    }
-    for (int t = tid; t < kTM * kPatch; t += 256) {
-        const int r = t / kPatch, d = t - r * kPatch;
-        int pr = -1;
-        if (r < cnt) {
-            const int g = list ? list[base + r] : base + r;
-            pr = pos[(size_t)g * kPatch + d];
-        }
-        prow[d][r] = pr;
-    }
-    __syncthreads();
-    const int lane = tid & 63, wv = tid >> 6, li = lane & 15, lk = lane >> 4;
-    const int nti = thi - tlo, N = kPatch * nti, mtiles = (cnt + kMT - 1) / kMT;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, lk = lane >> 4;
+    constexpr int nti = thi - tlo, N = kPatch * nti;
     auto item = [&](int it) { const int d = it / nti; return d * P::T + tlo + (it - d * nti); };
     // The weight fragment is the A operand and the records the B operand, so
     // the 16 x 16 result is (channel, record): lane (li, lk) holds channels
@@ -973,6 +953,90 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
         if (i2 < N) P::load(pp, item(i2), lane, b0);
         run(i1, b1);
         it = i2;
+    }
+}
+
+template <int IN, int OUT, bool PT>
+__global__ void __launch_bounds__(256)
+k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
+      const float* __restrict__ X, const int* __restrict__ pos, const float* __restrict__ pp,
+      float* __restrict__ QVG) {
+    constexpr int XST = lds_stride(IN), I4 = IN / 4;
+    __shared__ __align__(16) float xs[kTM * XST];
+    __shared__ int prow[kPatch][kTM];
+    const int n = n_dev ? *n_dev : n_max;
+    const int ntiles = (n + kTM - 1) / kTM;
+    int tile = blockIdx.x;
+    if (tile >= ntiles) return;
+    const int tid = threadIdx.x;
+    if constexpr (!PT) {
+        const int base = tile * kTM, cnt = min(kTM, n - base);
+        for (int t = tid; t < kTM * I4; t += 256) {
+            const int r = t / I4, q = t - r * I4;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < cnt) {
+                const int g = list ? list[base + r] : base + r;
+                v = reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q];
+            }
+            lds_put4(&xs[r * XST + 4 * q], v);
+        }
+        for (int t = tid; t < kTM * kPatch; t += 256) {
+            const int r = t / kPatch, d = t - r * kPatch;
+            int pr = -1;
+            if (r < cnt) {
+                const int g = list ? list[base + r] : base + r;
+                pr = pos[(size_t)g * kPatch + d];
+            }
+            prow[d][r] = pr;
+        }
+        __syncthreads();
+        qvg_items<IN, OUT>(xs, prow, (cnt + kMT - 1) / kMT, pp, QVG);
+    } else {
+        // this thread's share of a tile: XL float4 of input rows, PL positions
+        constexpr int XL = (kTM * I4 + 255) / 256, PL = (kTM * kPatch + 255) / 256;
+        float4 xv[XL];
+        int pv[PL];
+        auto fetch = [&](int tl) {
+            const int base = tl * kTM, cnt = min(kTM, n - base);
+            #pragma unroll
+            for (int j = 0; j < XL; ++j) {
+                const int t = tid + 256 * j, r = t / I4, q = t - r * I4;
+                xv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (t < kTM * I4 && r < cnt) {
+                    const int g = list ? list[base + r] : base + r;
+                    xv[j] = reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q];
+                }
+            }
+            #pragma unroll
+            for (int j = 0; j < PL; ++j) {
+                const int t = tid + 256 * j, r = t / kPatch, d = t - r * kPatch;
+                pv[j] = -1;
+                if (t < kTM * kPatch && r < cnt) {
+                    const int g = list ? list[base + r] : base + r;
+                    pv[j] = pos[(size_t)g * kPatch + d];
+                }
+            }
+        };
+        fetch(tile);
+        while (true) {
+            #pragma unroll
+            for (int j = 0; j < XL; ++j) {
+                const int t = tid + 256 * j, r = t / I4, q = t - r * I4;
+                if (t < kTM * I4) lds_put4(&xs[r * XST + 4 * q], xv[j]);
+            }
+            #pragma unroll
+            for (int j = 0; j < PL; ++j) {
+                const int t = tid + 256 * j, r = t / kPatch, d = t - r * kPatch;
+                if (t < kTM * kPatch) prow[d][r] = pv[j];
+            }
+            __syncthreads();
+            const int cnt = min(kTM, n - tile * kTM), next = tile + (int)gridDim.x;
+            if (next < ntiles) fetch(next);
+            qvg_items<IN, OUT>(xs, prow, (cnt + kMT - 1) / kMT, pp, QVG);
+            if (next >= ntiles) break;
+            __syncthreads();          // every wave is done with the tile
+            tile = next;
+        }
     }
 }
 
@@ -1109,6 +1173,9 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
 // values of the goW steps.  The weights stream from the L2 (shared by all
 // waves) one (delta, channel tile) item ahead.  LayerNorm in fp64 over the
 // four lanes that hold a record's outputs (ds_swizzle and ds_bpermute sums).
+// WPS asks the compiler for that many waves per SIMD: for L4 (RT = 2) 3
+// instead of the 2 it picks by itself (178 registers to 154, no spills) made
+// the launch 7% faster; 4 spills and is twice as slow.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ double xor_lanes_d(double v, int pattern_or_lane, bool swizzle) {
     const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
@@ -1129,8 +1196,8 @@ __device__ __forceinline__ double sum4_lanes(double v, int lane) {
     return v + xor_lanes_d(v, (lane ^ 32) << 2, false);
 }
 
-template <int IN, int OUT, int RT, int KS>
-__global__ void __launch_bounds__(64 * KS)
+template <int IN, int OUT, int RT, int KS, int WPS = 1>
+__global__ void __launch_bounds__(64 * KS, WPS)
 k_outt(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
        const float* __restrict__ X, const int* __restrict__ pos, const float* __restrict__ HR,
        const float* __restrict__ po, const float* __restrict__ gamma,
@@ -1507,6 +1574,7 @@ struct Workspace {
     hipEvent_t s3_ordered = nullptr;   // s3 tables and pass3 are complete
     hipEvent_t side_done = nullptr;    // the side stream's last work of a call
     int bh_ints = 0;
+    int cus = 0;                       // compute units of the device
     float* packed = nullptr;           // fragment-order weight copies (packed_weight_floats_d)
     // What `packed` was built from: the layer weight pointers and the weight
     // generation (bumped by every library call that may write device memory).
@@ -1621,6 +1689,9 @@ int ensure_workspace(int E, int nkeys) {
         HIPCHK(hipEventCreateWithFlags(&w.side_done, hipEventDisableTiming));
         HIPCHK(hipStreamCreateWithFlags(&w.side, hipStreamNonBlocking));
         HIPCHK(hipMalloc(&w.packed, sizeof(float) * packed_weight_floats_d()));
+        int dev = 0;
+        HIPCHK(hipGetDevice(&dev));
+        HIPCHK(hipDeviceGetAttribute(&w.cus, hipDeviceAttributeMultiprocessorCount, dev));
     }
     w.base = base;
     w.bytes = total;
@@ -1928,9 +1999,15 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     MARK();
     const LayerWeightsS2S3* L = cfg->layers[0];
     const unsigned tilesE = grid1(E, kTM);
+    // persistent projection grids (record tiles loop over the workgroups):
+    // measured at 200k records, L4 is fastest with 8 workgroups per CU (all
+    // resident), L5 with 6.5 per CU; both beat one tile per workgroup.
+    const unsigned cus = w.cus > 0 ? (unsigned)w.cus : tilesE;
+    const unsigned gridP4 = std::min(tilesE, 8u * cus);
+    const unsigned gridP5 = std::min(tilesE, 13u * cus / 2u);
     const unsigned char* all = nullptr;             // every pair's record needs h
     // ---- L4: 24 -> 48, all records ----------------------------------------
-    hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2, true>), dim3(gridP4), dim3(256), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, pk.pp[0], w.QVG);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
@@ -1942,7 +2019,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, all, w.QVG);
     MARK();
-    hipLaunchKernelGGL((k_outt<SSLA_C1, SSLA_C2, 2, 1>), dim3(grid1(E, 32)), dim3(64), 0, st, E,
+    hipLaunchKernelGGL((k_outt<SSLA_C1, SSLA_C2, 2, 1, 3>), dim3(grid1(E, 32)), dim3(64), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, pk.po[0],
                        L[0].ln_gamma, L[0].ln_beta, w.X1);
     MARK();
@@ -1973,7 +2050,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     HIPCHK(hipEventRecord(w.s3_ordered, s3));
     HIPCHK(hipGetLastError());
     // ---- L5: 48 -> 48, state for all records, output for pass2 ---------------
-    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2>), dim3(tilesE), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2, true>), dim3(gridP5), dim3(256), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, pk.pp[1], w.QVG);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
@@ -1991,7 +2068,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     MARK();
     // ---- L6: 48 -> 96, pass2 records ------------------------------------------
     HIPCHK(hipStreamWaitEvent(st, w.s3_ordered, 0));
-    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3, false>), dim3(tilesE), dim3(256), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, pk.pp[2], w.QVG);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
@@ -2008,7 +2085,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        L[2].ln_gamma, L[2].ln_beta, w.X3);
     MARK();
     // ---- L7: 96 -> 96, state for pass2, output for pass3 ----------------------
-    hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3>), dim3(tilesE), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3, false>), dim3(tilesE), dim3(256), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, pk.pp[3], w.QVG);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
