@@ -335,24 +335,25 @@ __device__ __forceinline__ int tdrop_passes(unsigned c, int r, int window) {
 // tdrop_s2 over the sorted records (position p, record g, rank r in the
 // key's run, counter c before the call): pass2[g], and the pass-2 list in
 // s2 order -- the record's place is the key's offset plus the number of
-// passing ranks below r.
-__device__ __forceinline__ void
+// passing ranks below r.  Returns pass2[g].
+__device__ __forceinline__ bool
 tdrop2_at(int p, int n, const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
           uint32_t nk, const int* __restrict__ start, const unsigned char* __restrict__ old,
           const int* __restrict__ off, int window, unsigned char* __restrict__ pass,
           int* __restrict__ list) {
-    if (p >= n) return;
+    if (p >= n) return false;
     const uint32_t k = keys[p];
     const int g = (int)vals[p];
     if (k >= nk) {
         pass[g] = 0;
-        return;
+        return false;
     }
     const int r = p - start[k];
     const unsigned c = old[k];
     const bool take = tdrop_pass(c, (unsigned)r, window);
     pass[g] = take ? 1 : 0;
     if (take) list[off[k] + tdrop_passes(c, r, window)] = g;
+    return take;
 }
 
 
@@ -635,10 +636,13 @@ __global__ void k_keys3b(uint32_t nk3, Geometry G, const int* __restrict__ t3,
 // ranks of g in the 5 x 5 runs around its centre cell (its own run gives
 // i - st[k]), folded row by row into three horizontal 3-sums; a delta's rank
 // is the sum of three of them.  pos[g * 9 + d] = the pair's place in the pair
-// order (-1 when the target is off the grid or the record has no key),
-// pair_rec[place] = g.  The lanes of a wave that share a centre cell (records
-// are sorted by cell) rank together: every load then serves the whole
-// segment, which keeps the L2 request count low.
+// order (-1 when the target is off the grid or the record has no key), and
+// pair_need[place] = whether g needs the layer's output (pass[g], or `take`
+// when pass is null: the tdrop decision the same thread just made), so the
+// scan's apply pass reads one byte per pair in its own order instead of a
+// record id and then that record's flag.  The lanes of a wave that share a
+// centre cell (records are sorted by cell) rank together: every load then
+// serves the whole segment, which keeps the L2 request count low.
 constexpr int kSegMax = 4;   // cell segments of a wave ranked together; more: per lane
 constexpr int kChunkWide = 512;   // widest window counted in 64-value chunks
 
@@ -759,7 +763,8 @@ __device__ __forceinline__ void
 pair_rank_at(int i, int n, const uint32_t* __restrict__ keys,
              const uint32_t* __restrict__ vals, uint32_t nk, int C, int W, int H,
              const int* __restrict__ st, const int* __restrict__ en, const int* __restrict__ pst,
-             int* __restrict__ pos, int* __restrict__ pair_rec) {
+             int* __restrict__ pos, unsigned char* __restrict__ pair_need,
+             const unsigned char* __restrict__ pass, bool take) {
     const int lane = threadIdx.x & 63;
     const bool valid = i < n;
     const uint32_t k = valid ? keys[i] : nk;
@@ -822,6 +827,7 @@ pair_rank_at(int i, int n, const uint32_t* __restrict__ keys,
         return;
     }
     const int b = (int)k / C, cell = (int)k % C, y = cell / W, x = cell % W;
+    const unsigned char need = pass ? pass[g] : (unsigned char)take;
     r25[12] = i - st[k];
     int hs[5][3];                  // hs[row][dx + 1]: runs (row, dx - 1 .. dx + 1)
     #pragma unroll
@@ -840,7 +846,7 @@ pair_rank_at(int i, int n, const uint32_t* __restrict__ keys,
         const int rank = hs[dy + 1][dx + 1] + hs[dy + 2][dx + 1] + hs[dy + 3][dx + 1];
         const int p = pst[b * C + ty * W + tx] + rank;
         pg[d] = p;
-        pair_rec[p] = (int)g;
+        pair_need[p] = need;
     }
 }
 
@@ -848,9 +854,10 @@ __global__ void __launch_bounds__(256)
 k_pair_rank(int n_max, const int* __restrict__ n_dev, const uint32_t* __restrict__ keys,
             const uint32_t* __restrict__ vals, uint32_t nk, int C, int W, int H,
             const int* __restrict__ st, const int* __restrict__ en, const int* __restrict__ pst,
-            int* __restrict__ pos, int* __restrict__ pair_rec) {
+            int* __restrict__ pos, unsigned char* __restrict__ pair_need,
+            const unsigned char* __restrict__ pass) {
     pair_rank_at(blockIdx.x * blockDim.x + threadIdx.x, n_dev ? *n_dev : n_max, keys, vals, nk,
-                 C, W, H, st, en, pst, pos, pair_rec);
+                 C, W, H, st, en, pst, pos, pair_need, pass, false);
 }
 
 // The s2 level's tables that need only the sorted order and the key scan, in
@@ -863,7 +870,7 @@ k_s2_tables(int n, int nbr, const uint32_t* __restrict__ keys, const uint32_t* _
             const int* __restrict__ en, const int* __restrict__ pst, const int* __restrict__ pen,
             const int* __restrict__ coff, const unsigned char* __restrict__ old,
             const int* __restrict__ off, int window, unsigned char* __restrict__ pass,
-            int* __restrict__ list, int* __restrict__ pos, int* __restrict__ pair_rec,
+            int* __restrict__ list, int* __restrict__ pos, unsigned char* __restrict__ pair_need,
             int* __restrict__ ckey, int* __restrict__ cbeg, int* __restrict__ cend) {
     if ((int)blockIdx.x >= nbr) {
         const uint32_t k = (blockIdx.x - (unsigned)nbr) * 4u + (threadIdx.x >> 6);
@@ -877,8 +884,8 @@ k_s2_tables(int n, int nbr, const uint32_t* __restrict__ keys, const uint32_t* _
         return;
     }
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    tdrop2_at(i, n, keys, vals, nk, st, old, off, window, pass, list);
-    pair_rank_at(i, n, keys, vals, nk, C, W, H, st, en, pst, pos, pair_rec);
+    const bool take = tdrop2_at(i, n, keys, vals, nk, st, old, off, window, pass, list);
+    pair_rank_at(i, n, keys, vals, nk, C, W, H, st, en, pst, pos, pair_need, nullptr, take);
 }
 
 // ---------------------------------------------------------------------------
@@ -1127,7 +1134,7 @@ template <int OUT>
 __global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
 k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
              const int* __restrict__ cend, const float* __restrict__ Hs,
-             const int* __restrict__ pair_rec, const unsigned char* __restrict__ need,
+             const unsigned char* __restrict__ pair_need,
              float* __restrict__ QVG) {
     constexpr int NC = 2 * OUT;
     const int j = blockIdx.x;
@@ -1143,7 +1150,7 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
         #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int k = p0 + u < e ? u : 0;
-            use[u] = p0 + u < e && (!need || need[pair_rec[p0 + k]]);
+            use[u] = p0 + u < e && (!pair_need || pair_need[p0 + k]);
             v[u] = __builtin_nontemporal_load(row + (size_t)k * NC);
             g[u] = __builtin_nontemporal_load(row + (size_t)k * NC + OUT);
         }
@@ -1553,7 +1560,7 @@ struct Workspace {
     float *X0, *X1, *X2, *X3, *X4, *QVG, *H7;
     int *cell2, *pos2, *pos3, *list2, *list3, *counts;
     int *st2, *en2, *st3, *en3, *pst2, *pen2, *pst3, *pen3, *last3, *cnt3;
-    int *prec2, *prec3;                        // record of each sorted pair
+    unsigned char *pneed2, *pneed3;            // per sorted pair: its record needs the output
     int *coff2, *coff3;                        // first chunk of every key
     int *ckey2, *cbeg2, *cend2, *ckey3, *cbeg3, *cend3;
     int *sidx;                                 // sorted s2 position of every record
@@ -1647,8 +1654,8 @@ int ensure_workspace(int E, int nkeys) {
         {(void**)&w.va, sizeof(uint32_t) * (size_t)cap},
         {(void**)&w.vb, sizeof(uint32_t) * (size_t)cap},
         {(void**)&w.key3g, sizeof(uint32_t) * (size_t)cap},
-        {(void**)&w.prec2, sizeof(int) * P},
-        {(void**)&w.prec3, sizeof(int) * P},
+        {(void**)&w.pneed2, P},
+        {(void**)&w.pneed3, P},
         {(void**)&w.sidx, sizeof(int) * (size_t)cap},
         {(void**)&w.coff2, sizeof(int) * (size_t)ck},
         {(void**)&w.coff3, sizeof(int) * (size_t)ck},
@@ -1984,7 +1991,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
         const unsigned nbr = grid1(E, 256);
         hipLaunchKernelGGL(k_s2_tables, dim3(nbr + grid1(nk2, 4)), dim3(256), 0, st, E, (int)nbr,
                            K2, V2, nk2, G.C2, G.W2, G.H2, w.st2, w.en2, w.pst2, w.pen2, w.coff2,
-                           w.old2, w.off2, G.window, w.pass2, w.list2, w.pos2, w.prec2, w.ckey2,
+                           w.old2, w.off2, G.window, w.pass2, w.list2, w.pos2, w.pneed2, w.ckey2,
                            w.cbeg2, w.cend2);
     }
     // The s3 ordering needs only the s2 order, pass2 and the old counters, so
@@ -2017,7 +2024,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        w.coff2, w.bd, 0, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
-                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, all, w.QVG);
+                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, all, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_outt<SSLA_C1, SSLA_C2, 2, 1, 3>), dim3(grid1(E, 32)), dim3(64), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, pk.po[0],
@@ -2046,7 +2053,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        w.coff3, w.ckey3, w.cbeg3, w.cend3);
     hipLaunchKernelGGL(k_pair_rank, dim3(grid1(E, 256)), dim3(256), 0, s3, E,
                        (const int*)(w.counts + 0), K3, V3, nk3, G.C3, G.W3, G.H3, w.st3, w.en3,
-                       w.pst3, w.pos3, w.prec3);
+                       w.pst3, w.pos3, w.pneed3, w.pass3);
     HIPCHK(hipEventRecord(w.s3_ordered, s3));
     HIPCHK(hipGetLastError());
     // ---- L5: 48 -> 48, state for all records, output for pass2 ---------------
@@ -2060,7 +2067,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        w.coff2, w.bd, 1, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
-                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.prec2, w.pass2, w.QVG);
+                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.pneed2, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C2, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, pk.po[1],
@@ -2078,7 +2085,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        w.coff3, w.bd, 2, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
-                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, all, w.QVG);
+                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, all, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C3, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, pk.po[2],
@@ -2095,7 +2102,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        w.coff3, w.bd, 3, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
-                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.prec3, w.pass3, w.QVG);
+                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.pneed3, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_outt<SSLA_C3, SSLA_C3, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
                        (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, pk.po[3],
