@@ -1056,8 +1056,11 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 //   B (k_scan_carry)   per cell: walks its chunks in order, records each
 //                      chunk's start state, stores the final state
 //   C (k_scan_apply)   per chunk: replays the chunk from its start state and
-//                      replaces v by h in place for pairs whose record needs
-//                      this layer's output
+//                      writes h for pairs whose record needs this layer's
+//                      output: rows of HS floats at Hout -- in place of v
+//                      (Hout = the pair rows, HS = 2 OUT) for L6 and L7, a
+//                      compact (pairs, OUT) array behind the rows for L4 and
+//                      L5, whose contractions gather h 10% faster from it
 // One lane per channel in all three passes.  Passes A and C read the v, g
 // rows with nontemporal loads: the rows are read once per pass and the
 // projection has just left up to 0.7 GB of them in the caches; streaming
@@ -1130,21 +1133,22 @@ k_scan_carry(int C, const int* __restrict__ start, const int* __restrict__ end,
     *hp = h;
 }
 
-template <int OUT>
+template <int OUT, int HS>
 __global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
 k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
              const int* __restrict__ cend, const float* __restrict__ Hs,
              const unsigned char* __restrict__ pair_need,
-             float* __restrict__ QVG) {
+             const float* __restrict__ QVG, float* __restrict__ Hout) {
     constexpr int NC = 2 * OUT;
     const int j = blockIdx.x;
     const int c = threadIdx.x;
     if (j >= *n_chunks || c >= OUT) return;
     const int s = cbeg[j], e = cend[j];
     float h = Hs[(size_t)j * OUT + c];
-    float* row = QVG + (size_t)s * NC + c;
+    const float* row = QVG + (size_t)s * NC + c;
+    float* hp = Hout + (size_t)s * HS + c;
     constexpr int U = 16;        // pairs whose v, g are in flight together
-    for (int p0 = s; p0 < e; p0 += U, row += U * NC) {
+    for (int p0 = s; p0 < e; p0 += U, row += U * NC, hp += U * HS) {
         float v[U], g[U];
         bool use[U];
         #pragma unroll
@@ -1158,7 +1162,7 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
         for (int u = 0; u < U; ++u) {
             if (p0 + u < e) {
                 h = fmaf(sigmoid_fast(g[u]), h, v[u]);
-                if (use[u]) gstore(row + (size_t)u * NC, h);
+                if (use[u]) gstore(hp + (size_t)u * HS, h);
             }
         }
     }
@@ -1180,6 +1184,7 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
 // values of the goW steps.  The weights stream from the L2 (shared by all
 // waves) one (delta, channel tile) item ahead.  LayerNorm in fp64 over the
 // four lanes that hold a record's outputs (ds_swizzle and ds_bpermute sums).
+// HR rows are HS floats apart (the scan's h output rows).
 // WPS asks the compiler for that many waves per SIMD: for L4 (RT = 2) 3
 // instead of the 2 it picks by itself (178 registers to 154, no spills) made
 // the launch 7% faster; 4 spills and is twice as slow.
@@ -1203,14 +1208,14 @@ __device__ __forceinline__ double sum4_lanes(double v, int lane) {
     return v + xor_lanes_d(v, (lane ^ 32) << 2, false);
 }
 
-template <int IN, int OUT, int RT, int KS, int WPS = 1>
+template <int IN, int OUT, int RT, int KS, int WPS = 1, int HS = 2 * OUT>
 __global__ void __launch_bounds__(64 * KS, WPS)
 k_outt(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
        const float* __restrict__ X, const int* __restrict__ pos, const float* __restrict__ HR,
        const float* __restrict__ po, const float* __restrict__ gamma,
        const float* __restrict__ beta, float* __restrict__ Y) {
     using O = OutPackT<IN, OUT>;
-    constexpr int NT = O::NT, KG = O::KG, NC = 2 * OUT, R = 16 * RT;
+    constexpr int NT = O::NT, KG = O::KG, R = 16 * RT;
     // the workgroup's pair rows, and the partial sums of waves 1..KS-1
     __shared__ int sp[R][kPatch];
     __shared__ f32x4 part[KS > 1 ? KS - 1 : 1][RT * NT][64];
@@ -1260,7 +1265,7 @@ k_outt(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
         #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const int p = sp[16 * rt + j][d];
-            hv[rt] = p >= 0 ? *(const SSLA_GLOBAL f32x4*)(HR + (size_t)p * NC + 16 * ct + 4 * g)
+            hv[rt] = p >= 0 ? *(const SSLA_GLOBAL f32x4*)(HR + (size_t)p * HS + 16 * ct + 4 * g)
                             : f32x4{0.f, 0.f, 0.f, 0.f};
         }
     };
@@ -2013,6 +2018,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     const unsigned gridP4 = std::min(tilesE, 8u * cus);
     const unsigned gridP5 = std::min(tilesE, 13u * cus / 2u);
     const unsigned char* all = nullptr;             // every pair's record needs h
+    // L4's and L5's h, compact (pairs, 48), behind their (pairs, 96) rows
+    float* const Hc = w.QVG + (size_t)w.cap * kPatch * 2 * SSLA_C2;
     // ---- L4: 24 -> 48, all records ----------------------------------------
     hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2, true>), dim3(gridP4), dim3(256), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, pk.pp[0], w.QVG);
@@ -2023,11 +2030,11 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
                        w.coff2, w.bd, 0, w.Asum, w.Bsum, w.Hs);
     MARK();
-    hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
-                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, all, w.QVG);
+    hipLaunchKernelGGL((k_scan_apply<48, 48>), dim3(w.max_chunks), dim3(64), 0, st,
+                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, all, w.QVG, Hc);
     MARK();
-    hipLaunchKernelGGL((k_outt<SSLA_C1, SSLA_C2, 2, 1, 3>), dim3(grid1(E, 32)), dim3(64), 0, st, E,
-                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, w.QVG, pk.po[0],
+    hipLaunchKernelGGL((k_outt<SSLA_C1, SSLA_C2, 2, 1, 3, SSLA_C2>), dim3(grid1(E, 32)), dim3(64), 0,
+                       st, E, (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, Hc, pk.po[0],
                        L[0].ln_gamma, L[0].ln_beta, w.X1);
     MARK();
     // ---- [side] the s3 record order, tdrop_s3, s3 pair and chunk tables ---
@@ -2066,11 +2073,11 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
                        w.coff2, w.bd, 1, w.Asum, w.Bsum, w.Hs);
     MARK();
-    hipLaunchKernelGGL((k_scan_apply<48>), dim3(w.max_chunks), dim3(64), 0, st,
-                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.pneed2, w.QVG);
+    hipLaunchKernelGGL((k_scan_apply<48, 48>), dim3(w.max_chunks), dim3(64), 0, st,
+                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.pneed2, w.QVG, Hc);
     MARK();
-    hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C2, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, w.QVG, pk.po[1],
+    hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C2, 1, 3, 1, SSLA_C2>), dim3(grid1(E, 16)), dim3(192), 0,
+                       st, E, (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, Hc, pk.po[1],
                        L[1].ln_gamma, L[1].ln_beta, w.X2);
     MARK();
     // ---- L6: 48 -> 96, pass2 records ------------------------------------------
@@ -2084,8 +2091,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
                        w.coff3, w.bd, 2, w.Asum, w.Bsum, w.Hs);
     MARK();
-    hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
-                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, all, w.QVG);
+    hipLaunchKernelGGL((k_scan_apply<96, 192>), dim3(w.max_chunks), dim3(128), 0, st,
+                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, all, w.QVG, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C3, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, pk.po[2],
@@ -2101,8 +2108,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
                        w.coff3, w.bd, 3, w.Asum, w.Bsum, w.Hs);
     MARK();
-    hipLaunchKernelGGL((k_scan_apply<96>), dim3(w.max_chunks), dim3(128), 0, st,
-                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.pneed3, w.QVG);
+    hipLaunchKernelGGL((k_scan_apply<96, 192>), dim3(w.max_chunks), dim3(128), 0, st,
+                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.pneed3, w.QVG, w.QVG);
     MARK();
     hipLaunchKernelGGL((k_outt<SSLA_C3, SSLA_C3, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
                        (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, pk.po[3],
