@@ -904,11 +904,14 @@ k_s2_tables(int n, int nbr, const uint32_t* __restrict__ keys, const uint32_t* _
 // PT (the layers over all records): a workgroup loops over record tiles
 // (tile += gridDim.x) and loads the next tile's rows and pair positions into
 // registers while the current tile runs, so the load latency of a tile is
-// not paid at the start of a workgroup.  The grid is sized per layer from the
-// CU count (scan_drain).  The pass-2 layers keep one tile per workgroup: the
-// prefetch registers cost L7 (IN = 96) a wave per SIMD.
+// not paid at the start of a workgroup.  The tiles are 80 records and the
+// grid is sized per layer from the CU count (scan_drain) so that each
+// workgroup runs about two of them; the launch bounds ask for 5 waves per
+// SIMD (L5: 4 waves to 5).  The pass-2 layers keep one 64-record tile per
+// workgroup: the prefetch registers cost L7 (IN = 96) a wave per SIMD.
 // ---------------------------------------------------------------------------
 constexpr int kTM = 64;     // records per projection / contraction workgroup
+constexpr int kTMP = 80;    // records per tile of the persistent projection
 
 // Row stride of the LDS tiles read as MFMA A operands, a[(16 m + li) ST + lk
 // + 4 s] with li = lane % 16, lk = lane / 16: a stride of 2 (mod 4) puts the
@@ -921,9 +924,9 @@ __device__ __forceinline__ void lds_put4(float* p, float4 v) {
     reinterpret_cast<float2*>(p)[1] = make_float2(v.z, v.w);
 }
 
-// The items of one staged record tile (mtiles row tiles of 16 records).
-template <int IN, int OUT>
-__device__ __forceinline__ void qvg_items(const float* __restrict__ xs, const int (*prow)[kTM],
+// The items of one staged record tile of TM records (mtiles row tiles of 16).
+template <int IN, int OUT, int TM>
+__device__ __forceinline__ void qvg_items(const float* __restrict__ xs, const int (*prow)[TM],
                                           int mtiles, const float* __restrict__ pp,
                                           float* __restrict__ QVG) {
     using P = ProjPack<IN, OUT>;
@@ -963,22 +966,22 @@ __device__ __forceinline__ void qvg_items(const float* __restrict__ xs, const in
     }
 }
 
-template <int IN, int OUT, bool PT>
-__global__ void __launch_bounds__(256)
+template <int IN, int OUT, bool PT, int TM = kTM>
+__global__ void __launch_bounds__(256, PT ? 5 : 1)
 k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
       const float* __restrict__ X, const int* __restrict__ pos, const float* __restrict__ pp,
       float* __restrict__ QVG) {
     constexpr int XST = lds_stride(IN), I4 = IN / 4;
-    __shared__ __align__(16) float xs[kTM * XST];
-    __shared__ int prow[kPatch][kTM];
+    __shared__ __align__(16) float xs[TM * XST];
+    __shared__ int prow[kPatch][TM];
     const int n = n_dev ? *n_dev : n_max;
-    const int ntiles = (n + kTM - 1) / kTM;
+    const int ntiles = (n + TM - 1) / TM;
     int tile = blockIdx.x;
     if (tile >= ntiles) return;
     const int tid = threadIdx.x;
     if constexpr (!PT) {
-        const int base = tile * kTM, cnt = min(kTM, n - base);
-        for (int t = tid; t < kTM * I4; t += 256) {
+        const int base = tile * TM, cnt = min(TM, n - base);
+        for (int t = tid; t < TM * I4; t += 256) {
             const int r = t / I4, q = t - r * I4;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
             if (r < cnt) {
@@ -987,7 +990,7 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
             }
             lds_put4(&xs[r * XST + 4 * q], v);
         }
-        for (int t = tid; t < kTM * kPatch; t += 256) {
+        for (int t = tid; t < TM * kPatch; t += 256) {
             const int r = t / kPatch, d = t - r * kPatch;
             int pr = -1;
             if (r < cnt) {
@@ -997,19 +1000,19 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
             prow[d][r] = pr;
         }
         __syncthreads();
-        qvg_items<IN, OUT>(xs, prow, (cnt + kMT - 1) / kMT, pp, QVG);
+        qvg_items<IN, OUT, TM>(xs, prow, (cnt + kMT - 1) / kMT, pp, QVG);
     } else {
         // this thread's share of a tile: XL float4 of input rows, PL positions
-        constexpr int XL = (kTM * I4 + 255) / 256, PL = (kTM * kPatch + 255) / 256;
+        constexpr int XL = (TM * I4 + 255) / 256, PL = (TM * kPatch + 255) / 256;
         float4 xv[XL];
         int pv[PL];
         auto fetch = [&](int tl) {
-            const int base = tl * kTM, cnt = min(kTM, n - base);
+            const int base = tl * TM, cnt = min(TM, n - base);
             #pragma unroll
             for (int j = 0; j < XL; ++j) {
                 const int t = tid + 256 * j, r = t / I4, q = t - r * I4;
                 xv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (t < kTM * I4 && r < cnt) {
+                if (t < TM * I4 && r < cnt) {
                     const int g = list ? list[base + r] : base + r;
                     xv[j] = reinterpret_cast<const float4*>(X)[(size_t)g * I4 + q];
                 }
@@ -1018,7 +1021,7 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
             for (int j = 0; j < PL; ++j) {
                 const int t = tid + 256 * j, r = t / kPatch, d = t - r * kPatch;
                 pv[j] = -1;
-                if (t < kTM * kPatch && r < cnt) {
+                if (t < TM * kPatch && r < cnt) {
                     const int g = list ? list[base + r] : base + r;
                     pv[j] = pos[(size_t)g * kPatch + d];
                 }
@@ -1029,17 +1032,17 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
             #pragma unroll
             for (int j = 0; j < XL; ++j) {
                 const int t = tid + 256 * j, r = t / I4, q = t - r * I4;
-                if (t < kTM * I4) lds_put4(&xs[r * XST + 4 * q], xv[j]);
+                if (t < TM * I4) lds_put4(&xs[r * XST + 4 * q], xv[j]);
             }
             #pragma unroll
             for (int j = 0; j < PL; ++j) {
                 const int t = tid + 256 * j, r = t / kPatch, d = t - r * kPatch;
-                if (t < kTM * kPatch) prow[d][r] = pv[j];
+                if (t < TM * kPatch) prow[d][r] = pv[j];
             }
             __syncthreads();
-            const int cnt = min(kTM, n - tile * kTM), next = tile + (int)gridDim.x;
+            const int cnt = min(TM, n - tile * TM), next = tile + (int)gridDim.x;
             if (next < ntiles) fetch(next);
-            qvg_items<IN, OUT>(xs, prow, (cnt + kMT - 1) / kMT, pp, QVG);
+            qvg_items<IN, OUT, TM>(xs, prow, (cnt + kMT - 1) / kMT, pp, QVG);
             if (next >= ntiles) break;
             __syncthreads();          // every wave is done with the tile
             tile = next;
@@ -1150,19 +1153,22 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
     constexpr int U = 16;        // pairs whose v, g are in flight together
     for (int p0 = s; p0 < e; p0 += U, row += U * NC, hp += U * HS) {
         float v[U], g[U];
-        bool use[U];
         #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int k = p0 + u < e ? u : 0;
-            use[u] = p0 + u < e && (!pair_need || pair_need[p0 + k]);
             v[u] = __builtin_nontemporal_load(row + (size_t)k * NC);
             g[u] = __builtin_nontemporal_load(row + (size_t)k * NC + OUT);
         }
+        // lane l of the wave reads pair p0 + l % 16's flag; bit u of the
+        // ballot is pair p0 + u's (lanes 0..15 are active in every wave)
+        const int kf = p0 + (c & 15);
+        const unsigned long long use =
+            __ballot(kf < e && (!pair_need || pair_need[kf]));
         #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (p0 + u < e) {
                 h = fmaf(sigmoid_fast(g[u]), h, v[u]);
-                if (use[u]) gstore(hp + (size_t)u * HS, h);
+                if ((use >> u) & 1ull) gstore(hp + (size_t)u * HS, h);
             }
         }
     }
@@ -2011,17 +2017,19 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     MARK();
     const LayerWeightsS2S3* L = cfg->layers[0];
     const unsigned tilesE = grid1(E, kTM);
-    // persistent projection grids (record tiles loop over the workgroups):
-    // measured at 200k records, L4 is fastest with 8 workgroups per CU (all
-    // resident), L5 with 6.5 per CU; both beat one tile per workgroup.
-    const unsigned cus = w.cus > 0 ? (unsigned)w.cus : tilesE;
-    const unsigned gridP4 = std::min(tilesE, 8u * cus);
-    const unsigned gridP5 = std::min(tilesE, 13u * cus / 2u);
+    // persistent projection grids (80-record tiles loop over the workgroups):
+    // measured at 200k records (2500 tiles), L4 is fastest with 6 workgroups
+    // per CU, L5 with 5 (both: all resident, about two tiles each); 64-record
+    // tiles (3125, some workgroups running a third) were 10% slower.
+    const unsigned tilesP = grid1(E, kTMP);
+    const unsigned cus = w.cus > 0 ? (unsigned)w.cus : tilesP;
+    const unsigned gridP4 = std::min(tilesP, 6u * cus);
+    const unsigned gridP5 = std::min(tilesP, 5u * cus);
     const unsigned char* all = nullptr;             // every pair's record needs h
     // L4's and L5's h, compact (pairs, 48), behind their (pairs, 96) rows
     float* const Hc = w.QVG + (size_t)w.cap * kPatch * 2 * SSLA_C2;
     // ---- L4: 24 -> 48, all records ----------------------------------------
-    hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2, true>), dim3(gridP4), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2, true, kTMP>), dim3(gridP4), dim3(256), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, pk.pp[0], w.QVG);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
@@ -2064,7 +2072,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     HIPCHK(hipEventRecord(w.s3_ordered, s3));
     HIPCHK(hipGetLastError());
     // ---- L5: 48 -> 48, state for all records, output for pass2 ---------------
-    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2, true>), dim3(gridP5), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2, true, kTMP>), dim3(gridP5), dim3(256), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, pk.pp[1], w.QVG);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
