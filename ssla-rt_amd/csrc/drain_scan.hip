@@ -909,6 +909,9 @@ k_s2_tables(int n, int nbr, const uint32_t* __restrict__ keys, const uint32_t* _
 // workgroup runs about two of them; the launch bounds ask for 5 waves per
 // SIMD (L5: 4 waves to 5).  The pass-2 layers keep one 64-record tile per
 // workgroup: the prefetch registers cost L7 (IN = 96) a wave per SIMD.
+// Their tiles are few (the pass-2 records: ~800 tiles at 200k), so NP
+// workgroups share a tile, each running 1/NP of its items (L6: 2, L7: 4):
+// with 3-4 tiles per CU, a third of the CUs had one more tile than the rest.
 // ---------------------------------------------------------------------------
 constexpr int kTM = 64;     // records per projection / contraction workgroup
 constexpr int kTMP = 80;    // records per tile of the persistent projection
@@ -928,12 +931,13 @@ __device__ __forceinline__ void lds_put4(float* p, float4 v) {
 template <int IN, int OUT, int TM>
 __device__ __forceinline__ void qvg_items(const float* __restrict__ xs, const int (*prow)[TM],
                                           int mtiles, const float* __restrict__ pp,
-                                          float* __restrict__ QVG) {
+                                          float* __restrict__ QVG, int part = 0, int nparts = 1) {
     using P = ProjPack<IN, OUT>;
     constexpr int XST = lds_stride(IN), NCW = 2 * OUT;
     constexpr int tlo = P::TQ, thi = P::T;      // the v and g column tiles
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, lk = lane >> 4;
-    constexpr int nti = thi - tlo, N = kPatch * nti;
+    constexpr int nti = thi - tlo, NI = kPatch * nti;
+    const int N = NI * (part + 1) / nparts;
     auto item = [&](int it) { const int d = it / nti; return d * P::T + tlo + (it - d * nti); };
     // The weight fragment is the A operand and the records the B operand, so
     // the 16 x 16 result is (channel, record): lane (li, lk) holds channels
@@ -953,7 +957,7 @@ __device__ __forceinline__ void qvg_items(const float* __restrict__ xs, const in
         }
     };
     float b0[P::KS4 * 4], b1[P::KS4 * 4];
-    int it = wv;
+    int it = NI * part / nparts + wv;
     if (it < N) P::load(pp, item(it), lane, b0);
     while (it < N) {
         const int i1 = it + 4, i2 = i1 + 4;
@@ -966,7 +970,7 @@ __device__ __forceinline__ void qvg_items(const float* __restrict__ xs, const in
     }
 }
 
-template <int IN, int OUT, bool PT, int TM = kTM>
+template <int IN, int OUT, bool PT, int TM = kTM, int NP = 1>
 __global__ void __launch_bounds__(256, PT ? 5 : 1)
 k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
       const float* __restrict__ X, const int* __restrict__ pos, const float* __restrict__ pp,
@@ -976,7 +980,7 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
     __shared__ int prow[kPatch][TM];
     const int n = n_dev ? *n_dev : n_max;
     const int ntiles = (n + TM - 1) / TM;
-    int tile = blockIdx.x;
+    int tile = PT ? (int)blockIdx.x : (int)blockIdx.x / NP;
     if (tile >= ntiles) return;
     const int tid = threadIdx.x;
     if constexpr (!PT) {
@@ -1000,7 +1004,7 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
             prow[d][r] = pr;
         }
         __syncthreads();
-        qvg_items<IN, OUT, TM>(xs, prow, (cnt + kMT - 1) / kMT, pp, QVG);
+        qvg_items<IN, OUT, TM>(xs, prow, (cnt + kMT - 1) / kMT, pp, QVG, (int)blockIdx.x % NP, NP);
     } else {
         // this thread's share of a tile: XL float4 of input rows, PL positions
         constexpr int XL = (TM * I4 + 255) / 256, PL = (TM * kPatch + 255) / 256;
@@ -2090,7 +2094,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     MARK();
     // ---- L6: 48 -> 96, pass2 records ------------------------------------------
     HIPCHK(hipStreamWaitEvent(st, w.s3_ordered, 0));
-    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3, false>), dim3(tilesE), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3, false, kTM, 2>), dim3(tilesE * 2), dim3(256), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, pk.pp[2], w.QVG);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
@@ -2107,7 +2111,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        L[2].ln_gamma, L[2].ln_beta, w.X3);
     MARK();
     // ---- L7: 96 -> 96, state for pass2, output for pass3 ----------------------
-    hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3, false>), dim3(tilesE), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3, false, kTM, 4>), dim3(tilesE * 4), dim3(256), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, pk.pp[3], w.QVG);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
