@@ -542,6 +542,18 @@ ORDER_KERNELS = ("k_decode", "k_rs_hist", "k_exscan", "k_rs_scatter", "k_runs", 
                  "k_tdrop3", "k_keys3b")
 
 
+def _traffic_key(k: str):
+    """The TRAFFIC_PHASES key of kernel name k: the key itself, or a key
+    whose template arguments are the first arguments of k's (the launch
+    parameters that follow them -- tile sizes, waves per SIMD, row strides --
+    do not change the phase)."""
+    for key in TRAFFIC_PHASES:
+        base = key[:-1]
+        if k == key or (key.endswith(">") and k.startswith(base) and k[len(base)] in ",>"):
+            return key
+    return None
+
+
 def _kname(n: str) -> str:
     n = n.replace("ssla::(anonymous namespace)::", "").replace("ssla::", "").replace("void ", "")
     return re.sub(r"\(.*", "", n).strip()
@@ -566,12 +578,13 @@ def pmc_summary(fetch_dir, write_dir, cfetch_dir, cwrite_dir, copy_bytes, comman
         for r in rs:
             k = _kname(r["Kernel_Name"])
             v = float(r["Counter_Value"]) * 1024.0
+            key = _traffic_key(k)
             if k.split("<")[0] in ORDER_KERNELS:
                 out["order"] += v / max(1, calls)
-            elif k in TRAFFIC_PHASES:
-                ph = TRAFFIC_PHASES[k]
-                out[ph[seen[k] % len(ph)]] += v / max(1, calls)
-                seen[k] += 1
+            elif key is not None:
+                ph = TRAFFIC_PHASES[key]
+                out[ph[seen[key] % len(ph)]] += v / max(1, calls)
+                seen[key] += 1
         return out
 
     cf = max(float(r["Counter_Value"]) for r in rows(cfetch_dir)) * 1024.0
