@@ -268,6 +268,27 @@ def test_sixteen_streams(H, stub_dir, stub_npz):
             compare(outs[s], p2, p3, feat, f"stream {s}")
 
 
+def test_projection_tiles_ragged(H, stub_dir, stub_npz):
+    """130,017 records: L4's and L5's projection workgroups each loop over
+    more than one 80-record tile (1,626 tiles over 6 or 5 workgroups per
+    CU), the last tile holds 17 records, and L6's and L7's items are split
+    over 2 and 4 workgroups per tile; every record and every cell's final
+    state is checked."""
+    n = 130_017
+    say("ragged projection tiles", n)
+    rec = events.blob_records(n, seed=9)
+    layers = O.layers_from_npz(stub_npz)
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        (out,), _ = d.drain([events.to_records(rec)])
+        st = O.S2S3(layers, 16, 20, 4)
+        p2, p3, feat, _ = st.run(rec.x, rec.y, rec.feat1)
+        compare(out, p2, p3, feat, "ragged tiles")
+        for li in range(4):
+            assert hidden_close(d.hidden(0, li), st.H[li]), li
+        td2, td3 = d.counters(0)
+        assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3)
+
+
 def test_state_carries_across_calls(H, stub_dir, stub_npz):
     n = 6000
     say("carry_across_calls", n)
