@@ -697,7 +697,8 @@ def main() -> int:
     ap.add_argument("--live-group", type=int, default=6, choices=[0, 3, 4, 5, 6],
                     help="workgroups per block of the live run (0 = one)")
     ap.add_argument("--no-live-strips", action="store_true",
-                    help="skip the second live run on the reference's 8-strip topology")
+                    help="skip the second live run on the reference's 8-strip topology "
+                         "(2 x 4 owned strips, halo 2, each drained by --live-group workgroups)")
     ap.add_argument("--batch", type=int, default=0,
                     help="1..32: drain through the live kernel's in-kernel batches of this "
                          "many records (one workgroup per instance) instead of the whole-ring "
@@ -857,7 +858,7 @@ def main() -> int:
                                                              a.live_group))
         if not a.no_live_strips:
             res["latency_us_8_strips"] = leg("live 8 strips", lambda: live_latency(
-                tmp.name, a.live_rate, a.live_seconds, 8, 0))
+                tmp.name, a.live_rate, a.live_seconds, 8, a.live_group))
     if a.workload == "16streams" and not a.no_live:
         res["latency_us"] = leg("replay", lambda: replay_latency(
             tmp.name, recs, [o["pass3"] for o in outs]))
