@@ -465,14 +465,15 @@ def _check_block_preds(preds, version, x, y, own, p3, ref7, owned):
             assert np.abs(preds[c] - ref7[k[-1]]).max() <= HEAD_TOL, c
 
 
-@pytest.mark.parametrize("gpu_blocks,group", [(1, 0), (8, 0), (1, 6)])
+@pytest.mark.parametrize("gpu_blocks,group", [(1, 0), (8, 0), (1, 6), (8, 6)])
 def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks, group):
     """The live configuration as stated: the producer's paced blob source at
     2.0 Mev/s -> 6 host shards for stages 0 + 1 (halo 2) -> fine-grained
     rings -> the persistent kernel, 2 s (orin/hybrid_runner_multi.py:314-754).
     One ownership domain (1 block) and the reference's 8-strip topology,
-    one workgroup per block; and one domain drained by a group of 6
-    workgroups (channel slices, exact: no halo).
+    one workgroup per block; one domain drained by a group of 6 workgroups
+    (channel slices, exact: no halo); and the 8 strips drained by a group of
+    6 each (48 workgroups).
     Every published record is drained with no overrun, and each ring's
     contents, run through the oracle with that block's ownership, give the
     kernel's pass flags (timing-slot owner flags), tdrop counters, final
