@@ -1388,6 +1388,16 @@ k_outt(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
     }
 }
 
+// The sum over each quad of lanes, in every lane of it: DPP quad_perm moves
+// (xor 1, then xor 2) instead of LDS-permute shuffles.
+__device__ __forceinline__ float quad_sum(float v) {
+    v += __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    return v;
+}
+
 // ---------------------------------------------------------------------------
 // head: raw [reg0..3, obj, cls0, cls1] for pass-3 records
 // (...celled.cuh:841-902).  One workgroup = 64 records (list order): their
@@ -1462,10 +1472,7 @@ k_head(const int* __restrict__ n_dev, const int* __restrict__ list,
         }
     }
     #pragma unroll
-    for (int k = 0; k < 7; ++k) {
-        o[k] += __shfl_xor(o[k], 1, 64);
-        o[k] += __shfl_xor(o[k], 2, 64);
-    }
+    for (int k = 0; k < 7; ++k) o[k] = quad_sum(o[k]);
     if (r < cnt && part == 0) {
         float* out = H7 + (size_t)rows[r] * 7;
         #pragma unroll
