@@ -1142,8 +1142,9 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
             }
             f32x4 acc = c3[0] + c3[1] + c3[2];
             if (has_res) {
-                // input_proj's fragments; B: the record's input, channels
-                // 16 t + 4 lk + i (0 past IN)
+                // input_proj's fragments (OutPackT order); B: the record's
+                // input, channels OutPackT::kidx(t, lk, i)
+                using OT = OutPackT<IN, OUT>;
                 f32x4 ar[KG];
                 #pragma unroll
                 for (int t = 0; t < KG; ++t)
@@ -1151,9 +1152,13 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
                 #pragma unroll
                 for (int t = 0; t < KG; ++t) {
                     f32x4 v = {0.f, 0.f, 0.f, 0.f};
-                    if (e >= 0 && 16 * t + 4 * lk < IN) v = *reinterpret_cast<const f32x4*>(&S.X[e][16 * t + 4 * lk]);
+                    if (e >= 0) {
+                        const float* xe = &S.X[e][OT::kidx(t, lk, 0)];
+                        #pragma unroll
+                        for (int i = 0; i < OT::steps(t); ++i) v[i] = xe[i];
+                    }
                     #pragma unroll
-                    for (int i = 0; i < 4; ++i)
+                    for (int i = 0; i < OT::steps(t); ++i)
                         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ar[t][i], v[i], acc, 0, 0, 0);
                 }
             }

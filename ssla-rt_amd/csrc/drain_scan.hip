@@ -1246,15 +1246,23 @@ k_outt(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
         rec[rt] = r < n ? (list ? list[r] : r) : -1;
     }
     // this lane's B values of the input steps: X[rec][16 t + 4 g .. + 3]
+    // (a half group: X[rec][16 t + 2 g .. + 1])
     f32x4 xr[RT][KG];
     #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
         #pragma unroll
         for (int t = 0; t < KG; ++t) {
-            const int c = 16 * t + 4 * g;
-            xr[rt][t] = (rec[rt] >= 0 && c < IN)
-                            ? *(const SSLA_GLOBAL f32x4*)(X + (size_t)rec[rt] * IN + c)
-                            : f32x4{0.f, 0.f, 0.f, 0.f};
+            const float* xp = X + (size_t)(rec[rt] < 0 ? 0 : rec[rt]) * IN + O::kidx(t, g, 0);
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if (rec[rt] >= 0) {
+                if (O::steps(t) == 4) {
+                    v = *(const SSLA_GLOBAL f32x4*)xp;
+                } else {
+                    v[0] = gload(xp);
+                    v[1] = gload(xp + 1);
+                }
+            }
+            xr[rt][t] = v;
         }
     f32x4 acc[RT][NT];
     #pragma unroll
@@ -1286,7 +1294,7 @@ k_outt(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
         #pragma unroll
         for (int t = 0; t < KG; ++t)
             #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < O::steps(t); ++i)
                 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt)
                     q[rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[t][i], xr[rt][t][i], q[rt],
@@ -1341,7 +1349,7 @@ k_outt(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
             #pragma unroll
             for (int t = 0; t < KG; ++t)
                 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < O::steps(t); ++i)
                     #pragma unroll
                     for (int rt = 0; rt < RT; ++rt)
                         acc[rt][ot] = __builtin_amdgcn_mfma_f32_16x16x4f32(ai[t][i], xr[rt][t][i],

@@ -96,10 +96,20 @@ struct OutPack {
 // on its order, and with this order a lane's B values are one float4 of a
 // record's input row (q, input_proj), or the four q*h values it already holds
 // in the MFMA output layout (rows 4 g .. 4 g + 3 of the q tile) for goW.
+// An input of 16 t + 8 channels (IN = 24) ends in a half group: its two steps
+// pair lane group g with channels 16 t + 2 g + i (i < 2), one float2 of the
+// row, so no step multiplies padding (steps(t) = 2 there, else 4).
 template <int IN, int OUT>
 struct OutPackT {
     static constexpr bool IP = IN != OUT;
     static constexpr int NT = OUT / kMT, KG = (IN + 15) / 16;
+    static constexpr bool TAIL8 = IN % 16 == 8;
+    static_assert(IN % 16 == 0 || TAIL8, "input widths: multiples of 16, or of 16 plus 8");
+    static __host__ __device__ constexpr int steps(int t) { return TAIL8 && t == KG - 1 ? 2 : 4; }
+    // the input channel of step i of group t for lane group g
+    static __host__ __device__ constexpr int kidx(int t, int g, int i) {
+        return TAIL8 && t == KG - 1 ? 16 * t + 2 * g + i : 16 * t + 4 * g + i;
+    }
     static constexpr size_t Q = (size_t)9 * NT * KG * 256;    // floats
     static constexpr size_t GO = (size_t)9 * NT * NT * 256;
     static constexpr size_t IPF = IP ? (size_t)NT * KG * 256 : 0;
@@ -119,8 +129,9 @@ __device__ __forceinline__ float outt_elem(const float* __restrict__ qvgIn,
         const int t = (int)(r % O::KG);
         r /= O::KG;
         const int ct = (int)(r % O::NT), d = (int)(r / O::NT);
-        const int k = 16 * t + 4 * g + i;
-        return k < IN ? qvgIn[((size_t)d * IN + k) * (3 * OUT) + 16 * ct + j] : 0.f;
+        const int k = O::kidx(t, g, i);
+        return i < O::steps(t) && k < IN ? qvgIn[((size_t)d * IN + k) * (3 * OUT) + 16 * ct + j]
+                                         : 0.f;
     }
     q -= O::Q;
     if (q < O::GO) {
@@ -133,8 +144,8 @@ __device__ __forceinline__ float outt_elem(const float* __restrict__ qvgIn,
     q -= O::GO;
     const size_t r = q >> 8;
     const int t = (int)(r % O::KG), ot = (int)(r / O::KG);
-    const int k = 16 * t + 4 * g + i;
-    return k < IN ? ip[(size_t)k * OUT + 16 * ot + j] : 0.f;
+    const int k = O::kidx(t, g, i);
+    return i < O::steps(t) && k < IN ? ip[(size_t)k * OUT + 16 * ot + j] : 0.f;
 }
 
 // element (item, group g, lane, j) = qvgIn[delta][(4g + j) * 4 + lane / 16][t * 16 + lane % 16]
