@@ -733,28 +733,39 @@ __device__ __forceinline__ void clock_sync(unsigned long long* cs, unsigned long
 }
 
 
-// Loads B records starting at ring slot `first` (slots wrap with `mask`).
+// Loads B records starting at ring slot `first` (slots wrap with `mask`):
+// eight threads per record, each reading one 16-byte piece of it (the ring
+// is fine-grained host memory, where every load is a PCIe read request:
+// 8 per record instead of 30 separate 4- and 8-byte ones).  Piece 0 holds
+// the tag, t and the s2 coordinates, pieces 1..6 feat1, piece 7 the two
+// timestamps.
 template <class SL>
 __device__ __forceinline__ void load_batch(SL& S, int B, const HybridInputRec* ring, unsigned long long first,
                            unsigned long long mask, const HybridStrip& s, const Geometry& G) {
+    static_assert(sizeof(HybridInputRec) == 128, "eight 16-byte pieces per record");
     const int tid = threadIdx.x;
-    for (int t = tid; t < B * SSLA_C1; t += LT) {
-        const int e = t / SSLA_C1, i = t % SSLA_C1;
-        S.X[e][i] = ring[(first + e) & mask].feat1[i];
-    }
-    if (tid < B) {
-        const HybridInputRec& r = ring[(first + tid) & mask];
-        const int x = r.x, y = r.y;
-        const bool v = x < G.W2 && y < G.H2;
-        S.vld[tid] = v ? 1 : 0;
-        S.ex[tid] = x;
-        S.ey[tid] = y;
-        S.c2[tid] = v ? y * G.W2 + x : -1;
-        S.own[tid] = (v && x >= s.owned_lo && x < s.owned_hi && y >= s.owned_y_lo && y < s.owned_y_hi) ? 1 : 0;
-        S.p2[tid] = 0;
-        S.p3[tid] = 0;
-        S.tpush[tid] = r.t_push_ns;
-        S.temit[tid] = r.t_emit_ns;
+    if (tid < B * 8) {
+        const int e = tid >> 3, q = tid & 7;
+        const uint4 v = reinterpret_cast<const uint4*>(&ring[(first + e) & mask])[q];
+        if (q >= 1 && q <= 6) {
+            *reinterpret_cast<float4*>(&S.X[e][4 * (q - 1)]) =
+                make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
+                            __uint_as_float(v.w));
+        } else if (q == 0) {
+            const int x = (int)(v.w & 0xffffu), y = (int)(v.w >> 16);    // bytes 12..15
+            const bool ok = x < G.W2 && y < G.H2;
+            S.vld[e] = ok ? 1 : 0;
+            S.ex[e] = x;
+            S.ey[e] = y;
+            S.c2[e] = ok ? y * G.W2 + x : -1;
+            S.own[e] = (ok && x >= s.owned_lo && x < s.owned_hi && y >= s.owned_y_lo &&
+                        y < s.owned_y_hi) ? 1 : 0;
+            S.p2[e] = 0;
+            S.p3[e] = 0;
+        } else {
+            S.tpush[e] = (unsigned long long)v.x | ((unsigned long long)v.y << 32);
+            S.temit[e] = (unsigned long long)v.z | ((unsigned long long)v.w << 32);
+        }
     }
 }
 
