@@ -497,12 +497,12 @@ def batch_bench(a, d, recs, n, S, steps, warmup, desc, tmp) -> int:
     from ssla_hip import lib
     for _ in range(warmup):
         d.reset(sync=False)
-        d.run(sync=True, batch=a.batch)
+        d.run(sync=True, batch=a.batch, group=a.batch_group)
     lib.check(lib.load().ssla_hip_device_synchronize())
     t0 = time.perf_counter()
     for _ in range(steps):
         d.reset(sync=False)
-        d.run(sync=True, batch=a.batch)
+        d.run(sync=True, batch=a.batch, group=a.batch_group)
     lib.check(lib.load().ssla_hip_device_synchronize())
     dt = time.perf_counter() - t0
     outs, _ = d.results()
@@ -516,8 +516,10 @@ def batch_bench(a, d, recs, n, S, steps, warmup, desc, tmp) -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": desc, "records": n * S, "instances": S,
-                   "mode": f"in-kernel batches of {a.batch} (live kernel), one workgroup "
-                           "per instance", "output_producing_per_step": n_out},
+                   "mode": f"in-kernel batches of {a.batch} (live kernel), "
+                           + (f"a group of {a.batch_group} workgroups" if a.batch_group > 1
+                              else "one workgroup") + " per instance",
+                   "output_producing_per_step": n_out},
         "ring_record_kev_s": round(n * S * steps / dt / 1e3, 2) if steps else None}))
     return 0
 
@@ -703,6 +705,9 @@ def main() -> int:
                     help="1..32: drain through the live kernel's in-kernel batches of this "
                          "many records (one workgroup per instance) instead of the whole-ring "
                          "drain; reports throughput only")
+    ap.add_argument("--batch-group", type=int, default=0, choices=[0, 3, 4, 5, 6],
+                    help="with --batch: drain each instance with a group of this many "
+                         "workgroups (channel slices; 0 = one workgroup)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "CFETCH", "CWRITE"),
                     help="print the per-launch HBM traffic JSON from rocprofv3 --pmc output "
                          "directories (drain FETCH_SIZE, WRITE_SIZE, copy FETCH_SIZE, WRITE_SIZE)")
