@@ -1195,9 +1195,8 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
 // waves) one (delta, channel tile) item ahead.  LayerNorm in fp64 over the
 // four lanes that hold a record's outputs (ds_swizzle and ds_bpermute sums).
 // HR rows are HS floats apart (the scan's h output rows).
-// WPS asks the compiler for that many waves per SIMD: for L4 (RT = 2) 3
-// instead of the 2 it picks by itself (178 registers to 154, no spills) made
-// the launch 7% faster; 4 spills and is twice as slow.
+// WPS asks the compiler for at least that many waves per SIMD; with the
+// unrolled item loop L4 (RT = 2) compiles to 120 registers, 4 waves per SIMD.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ double xor_lanes_d(double v, int pattern_or_lane, bool swizzle) {
     const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
@@ -1273,21 +1272,34 @@ k_outt(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 
     const SSLA_GLOBAL f32x4* wq = (const SSLA_GLOBAL f32x4*)po + lane;
     const SSLA_GLOBAL f32x4* wg = (const SSLA_GLOBAL f32x4*)(po + O::Q) + lane;
-    // item it = delta * NT + ct: its q and goW fragments and the h values
-    auto load = [&](int it, f32x4 (&aq)[KG], f32x4 (&ag)[NT], f32x4 (&hv)[RT]) {
+    // item it = delta * NT + ct: its q and goW fragments and the h values (an
+    // absent pair, p < 0, reads row 0 and is zeroed where it is used, so the
+    // loads carry no branch and the next item's stay in flight)
+    auto load = [&](int it, f32x4 (&aq)[KG], f32x4 (&ag)[NT], f32x4 (&hv)[RT], int (&pv)[RT]) {
         const int d = it / NT, ct = it - d * NT;
         #pragma unroll
-        for (int t = 0; t < KG; ++t) aq[t] = wq[((size_t)it * KG + t) * 64];
+        for (int t = 0; t < KG; ++t) {
+            const SSLA_GLOBAL f32x4* src = wq + ((size_t)it * KG + t) * 64;
+            if (O::steps(t) == 4) {
+                aq[t] = *src;
+            } else {
+                // a half group: the two live values only (a 16-byte load
+                // would keep two dead registers in flight)
+                const f32x2 v = *(const SSLA_GLOBAL f32x2*)src;
+                aq[t] = f32x4{v[0], v[1], 0.f, 0.f};
+            }
+        }
         #pragma unroll
         for (int ot = 0; ot < NT; ++ot) ag[ot] = wg[((size_t)it * NT + ot) * 64];
         #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const int p = sp[16 * rt + j][d];
-            hv[rt] = p >= 0 ? *(const SSLA_GLOBAL f32x4*)(HR + (size_t)p * HS + 16 * ct + 4 * g)
-                            : f32x4{0.f, 0.f, 0.f, 0.f};
+            pv[rt] = p;
+            hv[rt] = *(const SSLA_GLOBAL f32x4*)(HR + (size_t)(p < 0 ? 0 : p) * HS + 16 * ct + 4 * g);
         }
     };
-    auto compute = [&](const f32x4 (&aq)[KG], const f32x4 (&ag)[NT], const f32x4 (&hv)[RT]) {
+    auto compute = [&](const f32x4 (&aq)[KG], const f32x4 (&ag)[NT], const f32x4 (&hv)[RT],
+                       const int (&pv)[RT]) {
         f32x4 q[RT];
         #pragma unroll
         for (int rt = 0; rt < RT; ++rt) q[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1300,7 +1312,8 @@ k_outt(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
                     q[rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[t][i], xr[rt][t][i], q[rt],
                                                                  0, 0, 0);
         #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) q[rt] *= hv[rt];
+        for (int rt = 0; rt < RT; ++rt)
+            q[rt] = pv[rt] >= 0 ? q[rt] * hv[rt] : f32x4{0.f, 0.f, 0.f, 0.f};
         #pragma unroll
         for (int i = 0; i < 4; ++i)
             #pragma unroll
@@ -1310,18 +1323,24 @@ k_outt(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
                     acc[rt][ot] = __builtin_amdgcn_mfma_f32_16x16x4f32(ag[ot][i], q[rt][i],
                                                                        acc[rt][ot], 0, 0, 0);
     };
-    // this wave's items: deltas [d0, d1), the K parts split over the KS waves;
-    // the next item's weights and h values load while the current one runs
-    const int i0 = (wv * kPatch / KS) * NT, i1 = ((wv + 1) * kPatch / KS) * NT;
-    f32x4 aq0[KG], ag0[NT], hv0[RT], aq1[KG], ag1[NT], hv1[RT];
-    load(i0, aq0, ag0, hv0);
-    #pragma unroll 1
-    for (int it = i0; it < i1; it += 2) {
-        if (it + 1 < i1) load(it + 1, aq1, ag1, hv1);
-        compute(aq0, ag0, hv0);
-        if (it + 1 >= i1) break;
-        if (it + 2 < i1) load(it + 2, aq0, ag0, hv0);
-        compute(aq1, ag1, hv1);
+    // this wave's items: deltas [wv * 9 / KS, (wv + 1) * 9 / KS), the K parts
+    // split over the KS waves.  The loop is unrolled (a fixed trip count, no
+    // branches), and the scheduling barriers keep item k + 1's loads ahead of
+    // item k's MFMAs: the wait before item k then covers only its own loads,
+    // issued one item earlier.
+    static_assert(kPatch % KS == 0, "K parts of whole deltas");
+    constexpr int NI = kPatch / KS * NT;
+    const int i0 = wv * NI;
+    f32x4 aqb[2][KG], agb[2][NT], hvb[2][RT];
+    int pvb[2][RT];
+    load(i0, aqb[0], agb[0], hvb[0], pvb[0]);
+    #pragma unroll
+    for (int k = 0; k < NI; ++k) {
+        if (k + 1 < NI)
+            load(i0 + k + 1, aqb[(k + 1) & 1], agb[(k + 1) & 1], hvb[(k + 1) & 1], pvb[(k + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(aqb[k & 1], agb[k & 1], hvb[k & 1], pvb[k & 1]);
+        if constexpr (KS == 1) __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (KS > 1) {
         if (wv > 0) {

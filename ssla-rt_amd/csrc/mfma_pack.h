@@ -28,6 +28,7 @@ constexpr int kMT = 16;       // MFMA tile rows / columns
 constexpr int kKSplit = 8;    // K parts of the contraction
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // Global-memory accesses through address-space-1 pointers: pointers that
 // reach device code as generic values (loaded from descriptor tables) would
