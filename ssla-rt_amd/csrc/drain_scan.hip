@@ -927,54 +927,80 @@ __device__ __forceinline__ void lds_put4(float* p, float4 v) {
     reinterpret_cast<float2*>(p)[1] = make_float2(v.z, v.w);
 }
 
-// The items of one staged record tile of TM records (mtiles row tiles of 16).
-template <int IN, int OUT, int TM>
+// The items of one staged record tile of TM records (TM / 16 row tiles; rows
+// past the tile's records are zero in LDS and their pair positions -1), part
+// `part` of NP: items [NI part / NP, NI (part + 1) / NP), wave wv taking every
+// fourth from the part's item wv.  The item loop is unrolled with a fixed trip
+// count and its loads and stores carry no branch: the next item's weights are
+// in flight while the current item runs, and the wait before an item covers
+// only its own loads.  A result row with no pair (position -1) is written to
+// `trash` (one 16-byte slot per lane, never read) instead of being skipped.
+template <int IN, int OUT, int TM, int NP>
 __device__ __forceinline__ void qvg_items(const float* __restrict__ xs, const int (*prow)[TM],
-                                          int mtiles, const float* __restrict__ pp,
-                                          float* __restrict__ QVG, int part = 0, int nparts = 1) {
+                                          const float* __restrict__ pp, float* __restrict__ QVG,
+                                          float* __restrict__ trash, int part, int tid) {
     using P = ProjPack<IN, OUT>;
-    constexpr int XST = lds_stride(IN), NCW = 2 * OUT;
-    constexpr int tlo = P::TQ, thi = P::T;      // the v and g column tiles
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, lk = lane >> 4;
-    constexpr int nti = thi - tlo, NI = kPatch * nti;
-    const int N = NI * (part + 1) / nparts;
-    auto item = [&](int it) { const int d = it / nti; return d * P::T + tlo + (it - d * nti); };
+    constexpr int XST = lds_stride(IN), NCW = 2 * OUT, MT = TM / kMT, KS = P::KS;
+    constexpr int tlo = P::TQ, nti = P::T - tlo, NI = kPatch * nti;
+    static_assert(NI % NP == 0 && TM % kMT == 0, "item parts, row tiles");
+    constexpr int NPI = NI / NP, KF = NPI / 4, KR = NPI % 4;
+    const int lane = tid & 63, wv = tid >> 6, li = lane & 15, lk = lane >> 4;
+    const int ib = NPI * part + wv;            // this wave's items: ib + 4 k
+    // the weight fragment of an item: KS values per lane, as float4 groups (a
+    // final group of two steps as a float2, so no dead register is in flight)
+    auto load = [&](int k, float (&b)[KS]) {
+        const int it = ib + 4 * k, d = it / nti, t = tlo + (it - d * nti);
+        const SSLA_GLOBAL f32x4* src =
+            (const SSLA_GLOBAL f32x4*)pp + (size_t)(d * P::T + t) * P::KS4 * 64 + lane;
+        #pragma unroll
+        for (int g = 0; g < P::KS4; ++g) {
+            if (KS - 4 * g >= 4) {
+                const f32x4 v = src[g * 64];
+                #pragma unroll
+                for (int j = 0; j < 4; ++j) b[4 * g + j] = v[j];
+            } else {
+                const f32x2 v = *(const SSLA_GLOBAL f32x2*)(src + g * 64);
+                b[4 * g] = v[0];
+                b[4 * g + 1] = v[1];
+            }
+        }
+    };
     // The weight fragment is the A operand and the records the B operand, so
     // the 16 x 16 result is (channel, record): lane (li, lk) holds channels
     // 4 lk .. 4 lk + 3 of record li -- one float4 of that record's row.
-    auto run = [&](int it, const float* b) {
-        const int d = it / nti, t = tlo + (it - d * nti), c0 = t * kMT - OUT + 4 * lk;
-        for (int m = 0; m < mtiles; ++m) {
+    auto run = [&](int k, const float (&b)[KS]) {
+        const int it = ib + 4 * k, d = it / nti, t = tlo + (it - d * nti);
+        const int c0 = t * kMT - OUT + 4 * lk;
+        #pragma unroll
+        for (int m = 0; m < MT; ++m) {
             const float* a = &xs[(m * kMT + li) * XST + lk];
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
             #pragma unroll
-            for (int s = 0; s < P::KS; ++s)
+            for (int s = 0; s < KS; ++s)
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(b[s], a[4 * s], acc, 0, 0, 0);
             const int pr = prow[d][m * kMT + li];
-            if (pr >= 0)
-                *reinterpret_cast<float4*>(QVG + (size_t)pr * NCW + c0) =
-                    make_float4(acc[0], acc[1], acc[2], acc[3]);
+            float* dst = pr >= 0 ? QVG + (size_t)pr * NCW + c0 : trash + 4 * lane;
+            *(SSLA_GLOBAL f32x4*)dst = acc;
         }
     };
-    float b0[P::KS4 * 4], b1[P::KS4 * 4];
-    int it = NI * part / nparts + wv;
-    if (it < N) P::load(pp, item(it), lane, b0);
-    while (it < N) {
-        const int i1 = it + 4, i2 = i1 + 4;
-        if (i1 < N) P::load(pp, item(i1), lane, b1);
-        run(it, b0);
-        if (i1 >= N) break;
-        if (i2 < N) P::load(pp, item(i2), lane, b0);
-        run(i1, b1);
-        it = i2;
+    float bb[2][KS];
+    load(0, bb[0]);
+    #pragma unroll
+    for (int k = 0; k < KF; ++k) {
+        if (k + 1 < KF) load(k + 1, bb[(k + 1) & 1]);
+        else if (wv < KR) load(KF, bb[KF & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        run(k, bb[k & 1]);
+        __builtin_amdgcn_sched_barrier(0);
     }
+    if (wv < KR) run(KF, bb[KF & 1]);
 }
 
 template <int IN, int OUT, bool PT, int TM = kTM, int NP = 1>
 __global__ void __launch_bounds__(256, PT ? 5 : 1)
 k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
       const float* __restrict__ X, const int* __restrict__ pos, const float* __restrict__ pp,
-      float* __restrict__ QVG) {
+      float* __restrict__ QVG, float* __restrict__ trash) {
     constexpr int XST = lds_stride(IN), I4 = IN / 4;
     __shared__ __align__(16) float xs[TM * XST];
     __shared__ int prow[kPatch][TM];
@@ -1004,7 +1030,7 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
             prow[d][r] = pr;
         }
         __syncthreads();
-        qvg_items<IN, OUT, TM>(xs, prow, (cnt + kMT - 1) / kMT, pp, QVG, (int)blockIdx.x % NP, NP);
+        qvg_items<IN, OUT, TM, NP>(xs, prow, pp, QVG, trash, (int)blockIdx.x % NP, tid);
     } else {
         // this thread's share of a tile: XL float4 of input rows, PL positions
         constexpr int XL = (TM * I4 + 255) / 256, PL = (TM * kPatch + 255) / 256;
@@ -1044,9 +1070,14 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
                 if (t < TM * kPatch) prow[d][r] = pv[j];
             }
             __syncthreads();
-            const int cnt = min(TM, n - tile * TM), next = tile + (int)gridDim.x;
+            const int next = tile + (int)gridDim.x;
             if (next < ntiles) fetch(next);
-            qvg_items<IN, OUT, TM>(xs, prow, (cnt + kMT - 1) / kMT, pp, QVG);
+            // the thread index passes through an empty asm each tile, so the
+            // compiler does not hoist the items' addresses out of the tile
+            // loop (kept live across it, they spilled)
+            int tid_t = tid;
+            asm volatile("" : "+v"(tid_t));
+            qvg_items<IN, OUT, TM, 1>(xs, prow, pp, QVG, trash, 0, tid_t);
             if (next >= ntiles) break;
             __syncthreads();          // every wave is done with the tile
             tile = next;
@@ -1618,6 +1649,7 @@ struct Workspace {
     int *bh;                                   // radix-sort tile histograms
     unsigned char* old2;                       // s2 counters before the call
     float *Asum, *Bsum, *Hs;
+    float* trash;                              // sink of the projection's absent rows
     int max_chunks = 0;
     unsigned char *owner, *pass2, *pass3;
     uint32_t *ka, *kb, *va, *vb, *key3g;
@@ -1724,6 +1756,7 @@ int ensure_workspace(int E, int nkeys) {
         {(void**)&w.Asum, sizeof(float) * mc * SSLA_C3},
         {(void**)&w.Bsum, sizeof(float) * mc * SSLA_C3},
         {(void**)&w.Hs, sizeof(float) * mc * SSLA_C3},
+        {(void**)&w.trash, sizeof(float) * 4 * 64},
         {(void**)&w.bd, sizeof(BlockDesc) * SSLA_MAX_BLOCKS},
     };
     size_t total = 0;
@@ -2068,7 +2101,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     float* const Hc = w.QVG + (size_t)w.cap * kPatch * 2 * SSLA_C2;
     // ---- L4: 24 -> 48, all records ----------------------------------------
     hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2, true, kTMP>), dim3(gridP4), dim3(256), 0, st, E,
-                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, pk.pp[0], w.QVG);
+                       (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, pk.pp[0], w.QVG, w.trash);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
@@ -2111,7 +2144,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     HIPCHK(hipGetLastError());
     // ---- L5: 48 -> 48, state for all records, output for pass2 ---------------
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2, true, kTMP>), dim3(gridP5), dim3(256), 0, st, E,
-                       (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, pk.pp[1], w.QVG);
+                       (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, pk.pp[1], w.QVG, w.trash);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
@@ -2129,7 +2162,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // ---- L6: 48 -> 96, pass2 records ------------------------------------------
     HIPCHK(hipStreamWaitEvent(st, w.s3_ordered, 0));
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3, false, kTM, 2>), dim3(tilesE * 2), dim3(256), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, pk.pp[2], w.QVG);
+                       (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, pk.pp[2], w.QVG, w.trash);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
@@ -2146,7 +2179,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     MARK();
     // ---- L7: 96 -> 96, state for pass2, output for pass3 ----------------------
     hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3, false, kTM, 4>), dim3(tilesE * 4), dim3(256), 0, st, E,
-                       (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, pk.pp[3], w.QVG);
+                       (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, pk.pp[3], w.QVG, w.trash);
     MARK();
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
