@@ -586,20 +586,36 @@ k_tdrop3(const int* __restrict__ n_dev, const uint32_t* __restrict__ keys,
          const unsigned char* __restrict__ owner, int have_head, unsigned char* __restrict__ pass,
          int* __restrict__ list, int* __restrict__ last, int* __restrict__ count) {
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= *n_dev) return;
-    const uint32_t k = keys[p];
-    if (k >= nk) return;
-    const int g = (int)vals[p];
-    const int b = (int)k / C, cell = (int)k % C;
-    const int r = p - start[k];
-    const unsigned c = bd[b].td3[cell];
-    const bool take = tdrop_pass(c, (unsigned)r, window);
-    pass[g] = take ? 1 : 0;
-    if (!take) return;
-    list[off[k] + tdrop_passes(c, r, window)] = g;
-    if (have_head && owner[g]) {
-        atomicMax(last + k, g);
-        atomicAdd(count + k, 1);
+    const uint32_t k = p < *n_dev ? keys[p] : nk;
+    const bool valid = k < nk;
+    int g = -1;
+    bool own = false;
+    if (valid) {
+        g = (int)vals[p];
+        const int b = (int)k / C, cell = (int)k % C;
+        const int r = p - start[k];
+        const unsigned c = bd[b].td3[cell];
+        const bool take = tdrop_pass(c, (unsigned)r, window);
+        pass[g] = take ? 1 : 0;
+        if (take) list[off[k] + tdrop_passes(c, r, window)] = g;
+        own = take && have_head && owner[g];
+    }
+    // last / count per key: the records are sorted by key, so a wave holds a
+    // few key segments; one lane per segment adds its count and maximum (a
+    // per-record atomic put thousands of updates on each of the few keys)
+    unsigned long long m = __ballot(own);
+    while (m) {
+        const uint32_t kl = (uint32_t)__builtin_amdgcn_readlane((int)k, __builtin_ctzll(m));
+        const bool in = own && k == kl;
+        const unsigned long long sm = __ballot(in);
+        int gm = in ? g : -1;
+        #pragma unroll
+        for (int o = 32; o > 0; o >>= 1) gm = max(gm, __shfl_xor(gm, o));
+        if ((threadIdx.x & 63) == __builtin_ctzll(sm)) {
+            atomicMax(last + kl, gm);
+            atomicAdd(count + kl, __popcll(sm));
+        }
+        m &= ~sm;
     }
 }
 
