@@ -426,14 +426,15 @@ WORKLOADS = {
 }
 
 
-def replay_latency(stub_dir, recs, offline_p3, rate_per_stream=125_000.0):
+def replay_latency(stub_dir, recs, offline_p3, rate_per_stream=125_000.0, group=0):
     """Live multi-stream run: each stream's ring records replayed at the
-    2 Mev/s stream's record rate into its own ring of one persistent kernel;
+    2 Mev/s stream's record rate into its own ring of one persistent kernel
+    (each ring drained by one workgroup, or by a group of `group`);
     push -> prediction latency per stream and drop drift against the same
     records' offline decisions."""
     from ssla_hip import events, live
     r = live.run_replay(stub_dir, [events.to_records(x) for x in recs], rate_per_stream,
-                        timing_capacity=1 << 18, expect_p3=offline_p3)
+                        timing_capacity=1 << 18, expect_p3=offline_p3, group=group)
     st = r.streams
     p50 = [s["push_to_done_p50"] for s in st]
     p99 = [s["push_to_done_p99"] for s in st]
@@ -444,12 +445,14 @@ def replay_latency(stub_dir, recs, offline_p3, rate_per_stream=125_000.0):
         "aggregate_drain_kev_s": round(r.drained / r.duration_s / 1e3, 2),
         "kernel_status": r.status, "kernel_phase_us_per_batch": _per_batch(r.phase_us),
         "config": f"live: {len(recs)} rings replayed at {rate_per_stream:.0f} records/s each "
-                  "(post-stage-1 records, published at emit) -> one persistent kernel, one "
-                  "workgroup per stream; latency push -> prediction",
+                  "(post-stage-1 records, published at emit) -> one persistent kernel, "
+                  + (f"a group of {group} workgroups per stream" if group else
+                     "one workgroup per stream") + "; latency push -> prediction",
+        "group": group,
     }
 
 
-def split_replay_latency(stub_dir, rec, H2, W2, n_blocks=16, speed=1.0):
+def split_replay_latency(stub_dir, rec, H2, W2, n_blocks=16, speed=1.0, group=0):
     """Live run of one full-resolution stream split over owned strips (the
     reference's multi-block layout, 4 x 4 here): every strip's ring gets the
     records of its processed window (halo copies included), all rings
@@ -472,7 +475,7 @@ def split_replay_latency(stub_dir, rec, H2, W2, n_blocks=16, speed=1.0):
     expect = [(o["pass3"] == 1).astype(np.int8) for o in outs]
     cap = 1 << max(16, int(np.ceil(np.log2(max(r.size for r in rings) + 1))))
     r = live.run_replay(stub_dir, rings, 0.0, strips=[t.owned for t in topo], speed=speed,
-                        timing_capacity=cap, expect_p3=expect)
+                        timing_capacity=cap, expect_p3=expect, group=group)
     st = r.streams
     p50 = [s["push_to_done_p50"] for s in st]
     p99 = [s["push_to_done_p99"] for s in st]
@@ -486,8 +489,10 @@ def split_replay_latency(stub_dir, rec, H2, W2, n_blocks=16, speed=1.0):
         "config": f"live: the full-resolution stream split into {n_blocks} owned strips "
                   f"({len(set(t.owned_x_lo for t in topo))} x {len(set(t.owned_y_lo for t in topo))}, "
                   "halo 2), each strip's records (halo copies included) replayed into its own "
-                  f"ring by record time at {speed:g}x real time -> one persistent kernel, one "
-                  "workgroup per strip; latency push -> prediction",
+                  f"ring by record time at {speed:g}x real time -> one persistent kernel, "
+                  + (f"a group of {group} workgroups per strip" if group else
+                     "one workgroup per strip") + "; latency push -> prediction",
+        "group": group,
     }
 
 
@@ -866,10 +871,10 @@ def main() -> int:
                 tmp.name, a.live_rate, a.live_seconds, 8, a.live_group))
     if a.workload == "16streams" and not a.no_live:
         res["latency_us"] = leg("replay", lambda: replay_latency(
-            tmp.name, recs, [o["pass3"] for o in outs]))
+            tmp.name, recs, [o["pass3"] for o in outs], group=a.live_group))
     if a.workload == "640x480" and not a.no_live:
         res["latency_us"] = leg("split replay", lambda: split_replay_latency(
-            tmp.name, recs[0], H2, W2))
+            tmp.name, recs[0], H2, W2, group=a.live_group))
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = leg("cpu baseline", lambda: cpu_baseline(
             tmp.name, recs[0], a.cpu_seconds, H2, W2, (outs[0], heads[0])))

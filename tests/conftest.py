@@ -31,6 +31,15 @@ def stub_npz(stub_dir):
     return oracle.load_npz(stub_dir)
 
 
+@pytest.fixture(scope="session")
+def stub_640(tmp_path_factory):
+    """Stub weight directory at 640x480 (s2 160 x 120), seed 1, tdrop 4."""
+    from ssla_hip import stub
+    d = tmp_path_factory.mktemp("stub_640x480")
+    stub.write_stub(str(d), height=480, width=640, seed=1, tdrop=4)
+    return str(d)
+
+
 def make_trained_checkpoint(path, seed: int = 3, tdrop: int = 6, with_ema: bool = True):
     """A Lightning-style checkpoint with the tensor names of a trained SSLA-S
     model: SSLA layers at slots 0,1,4,5,8,9,12,13, 4-D head convs with

@@ -428,14 +428,6 @@ def test_full_size_properties(H, stub_dir):
             assert hidden_close(d.hidden(0, li), h_a[li]), li
 
 
-@pytest.fixture(scope="module")
-def stub_640(tmp_path_factory):
-    from ssla_hip import stub
-    d = tmp_path_factory.mktemp("stub_640x480")
-    stub.write_stub(str(d), height=480, width=640, seed=1, tdrop=4)
-    return str(d)
-
-
 def test_640x480_matches_oracle(H, stub_640):
     """Full-resolution grid (s2 160 x 120, s3 80 x 60): edge blobs plus hot
     pixels, whole-ring drain and in-kernel batches against the oracle."""

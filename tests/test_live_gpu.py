@@ -433,7 +433,7 @@ def test_replay_four_streams_live(stub_dir, stub_npz):
         assert s["output_records"] > 0 and 0 < s["push_to_done_p50"] < 1e5
 
 
-def _oracle_rings(stub_npz, jobs):
+def _oracle_rings(stub_npz, jobs, H2=16, W2=20):
     """Runs the fp64 oracle (with head) over several rings at once, one
     thread each (the C oracle keeps no global state and ctypes releases the
     GIL).  jobs: (x, y, feat1, owner-or-None); returns (state, p2, p3, ref7)."""
@@ -442,7 +442,7 @@ def _oracle_rings(stub_npz, jobs):
 
     def one(job):
         x, y, f, own = job
-        st = O.S2S3(layers, 16, 20, 4, head=head)
+        st = O.S2S3(layers, H2, W2, 4, head=head)
         p2, p3, _, ref7 = st.run(x, y, f, owner=own, want_head=True)
         return st, p2, p3, ref7
 
@@ -560,3 +560,55 @@ def test_config4_sixteen_rings_one_persistent_kernel(stub_dir, stub_npz, group):
             assert hidden_close(hid[li], st.H[li]), (b, li)
         assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3), b
         check_preds(pr, ver, recs[b], p3, ref7)
+
+
+def test_640x480_strips_live_group(stub_640):
+    """The 640x480 stream live in the reference's multi-block form: the
+    full-resolution records split into 16 owned strips (4 x 4, halo 2), each
+    strip's processed-window records (halo copies included) replayed by
+    record time into its own ring of one persistent kernel, each ring
+    drained by a group of 6 workgroups (96 workgroups).  Per strip, against
+    the fp64 oracle run on that ring with the strip's ownership: every record
+    drained, owner flags (drop drift 0), tdrop counters, final hidden state
+    and the owned box's prediction cells."""
+    from ssla_hip import live as LV
+    from ssla_hip.topology import grid_topology
+    n = 40_000
+    say(f"640x480 live: {n} edge-blob records over 16 strips, group 6")
+    npz = O.load_npz(stub_640)
+    rec = events.edge_blob_records(n, seed=3)
+    full = events.to_records(rec)
+    x, y = rec.x.astype(np.int64), rec.y.astype(np.int64)
+    topo = grid_topology(16, 160, 120)
+    rings, jobs = [], []
+    for t in topo:
+        m = (x >= t.proc_x_lo) & (x < t.proc_x_hi) & (y >= t.proc_y_lo) & (y < t.proc_y_hi)
+        rings.append(full[m])
+        xs, ys = x[m], y[m]
+        own = (xs >= t.owned_x_lo) & (xs < t.owned_x_hi) & (ys >= t.owned_y_lo) \
+            & (ys < t.owned_y_hi)
+        jobs.append((rec.x[m], rec.y[m], rec.feat1[m], own))
+    got = _oracle_rings(npz, jobs, H2=120, W2=160)
+    expect = [(j[3] & (g[2] == 1)).astype(np.int8) for j, g in zip(jobs, got)]
+    state = {}
+
+    def inspect(drain):
+        for b in range(len(topo)):
+            state[b] = ([drain.hidden(b, li) for li in range(4)], drain.counters(b),
+                        drain.preds(b))
+
+    res = LV.run_replay(stub_640, rings, 0.0, strips=[t.owned for t in topo], speed=1.0,
+                        ring_capacity=1 << 14, timing_capacity=1 << 14, expect_p3=expect,
+                        group=6, inspect=inspect)
+    say("640x480 live: status", res.status, "per strip (drained, drift, p50 us):",
+        [(s["drained"], s["drop_drift"], round(s["push_to_done_p50"], 1)) for s in res.streams])
+    assert res.status == 0 and len(state) == len(topo)
+    for b, (s, r, (st, p2, p3, ref7), (xs, ys, _, own)) in enumerate(
+            zip(res.streams, rings, got, jobs)):
+        assert s["drained"] == r.size and s["drop_drift"] == 0, b
+        hid, (td2, td3), (pr, ver) = state[b]
+        for li in range(4):
+            assert hidden_close(hid[li], st.H[li]), (b, li)
+        assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3), b
+        _check_block_preds(pr, ver, xs.astype(int), ys.astype(int), own, p3, ref7,
+                           topo[b].owned)
