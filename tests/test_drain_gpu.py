@@ -445,6 +445,17 @@ def test_640x480_matches_oracle(H, stub_640):
         assert np.abs(h7[m] - ref7[m]).max() <= HEAD_TOL
         for li in range(4):
             assert hidden_close(d.hidden(0, li), st.H[li]), li
+        # prediction grid (s3 80 x 60): per cell, version = pass-3 records and
+        # values = the last one's head; at ~4 records per cell a wave of the
+        # s3 tdrop spans many cells, each counted by one lane
+        preds, version = d.preds(0)
+        c3 = (rec.y.astype(np.int64) >> 1) * 80 + (rec.x.astype(np.int64) >> 1)
+        cnt = np.bincount(c3[m], minlength=80 * 60)
+        assert np.array_equal(version[:80 * 60], cnt)
+        last = np.full(80 * 60, -1)
+        last[c3[m]] = np.nonzero(m)[0]          # later records overwrite earlier ones
+        hit = last >= 0
+        assert np.abs(preds[:80 * 60][hit] - ref7[last[hit]]).max() <= HEAD_TOL
         d.reset()
         (out,), (h7,) = d.drain([events.to_records(rec)], want_head=True, batch=32)
         compare(out, p2, p3, feat, "640x480 batches of 32")
