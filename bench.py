@@ -325,10 +325,10 @@ def _per_batch(phase_us):
             if k not in ("batches", "records") and (i < 25 or phase_us[i] > 0)}
 
 
-def live_latency(stub_dir, rate_mev=2.0, duration_s=8.0, gpu_blocks=8, group=0):
+def live_latency(stub_dir, rate_mev=2.0, duration_s=8.0, gpu_blocks=8, group=0, stages=1):
     from ssla_hip import live
     r = live.run_live(stub_dir, rate_mev=rate_mev, duration_s=duration_s, n_shards=6, halo=2,
-                      gpu_blocks=gpu_blocks, group=group)
+                      gpu_blocks=gpu_blocks, group=group, stages=stages)
     lat = r.lat_us
     return {
         "p50": round(lat["emit_to_done_p50"], 2), "p99": round(lat["emit_to_done_p99"], 2),
@@ -350,8 +350,10 @@ def live_latency(stub_dir, rate_mev=2.0, duration_s=8.0, gpu_blocks=8, group=0):
                   + (f", each drained by a group of {group} workgroups (16-channel slices, "
                      f"partial sums exchanged per layer)" if group > 1
                      else ", one persistent workgroup each")
+                  + (" in two pipelined stages (L4-L5 of a batch beside L6-head of the "
+                     "previous one, 2 groups per ring)" if stages == 2 else "")
                   + f", {r.duration_s:.1f} s; {r.synth_events} events emitted",
-        "gpu_blocks": r.gpu_blocks, "group": group,
+        "gpu_blocks": r.gpu_blocks, "group": group, "stages": stages,
     }
 
 
@@ -426,7 +428,7 @@ WORKLOADS = {
 }
 
 
-def replay_latency(stub_dir, recs, offline_p3, rate_per_stream=125_000.0, group=0):
+def replay_latency(stub_dir, recs, offline_p3, rate_per_stream=125_000.0, group=0, stages=1):
     """Live multi-stream run: each stream's ring records replayed at the
     2 Mev/s stream's record rate into its own ring of one persistent kernel
     (each ring drained by one workgroup, or by a group of `group`);
@@ -434,7 +436,8 @@ def replay_latency(stub_dir, recs, offline_p3, rate_per_stream=125_000.0, group=
     records' offline decisions."""
     from ssla_hip import events, live
     r = live.run_replay(stub_dir, [events.to_records(x) for x in recs], rate_per_stream,
-                        timing_capacity=1 << 18, expect_p3=offline_p3, group=group)
+                        timing_capacity=1 << 18, expect_p3=offline_p3, group=group,
+                        stages=stages)
     st = r.streams
     p50 = [s["push_to_done_p50"] for s in st]
     p99 = [s["push_to_done_p99"] for s in st]
@@ -447,12 +450,14 @@ def replay_latency(stub_dir, recs, offline_p3, rate_per_stream=125_000.0, group=
         "config": f"live: {len(recs)} rings replayed at {rate_per_stream:.0f} records/s each "
                   "(post-stage-1 records, published at emit) -> one persistent kernel, "
                   + (f"a group of {group} workgroups per stream" if group else
-                     "one workgroup per stream") + "; latency push -> prediction",
-        "group": group,
+                     "one workgroup per stream")
+                  + (" in two pipelined stages" if stages == 2 else "")
+                  + "; latency push -> prediction",
+        "group": group, "stages": stages,
     }
 
 
-def split_replay_latency(stub_dir, rec, H2, W2, n_blocks=16, speed=1.0, group=0):
+def split_replay_latency(stub_dir, rec, H2, W2, n_blocks=16, speed=1.0, group=0, stages=1):
     """Live run of one full-resolution stream split over owned strips (the
     reference's multi-block layout, 4 x 4 here): every strip's ring gets the
     records of its processed window (halo copies included), all rings
@@ -475,7 +480,7 @@ def split_replay_latency(stub_dir, rec, H2, W2, n_blocks=16, speed=1.0, group=0)
     expect = [(o["pass3"] == 1).astype(np.int8) for o in outs]
     cap = 1 << max(16, int(np.ceil(np.log2(max(r.size for r in rings) + 1))))
     r = live.run_replay(stub_dir, rings, 0.0, strips=[t.owned for t in topo], speed=speed,
-                        timing_capacity=cap, expect_p3=expect, group=group)
+                        timing_capacity=cap, expect_p3=expect, group=group, stages=stages)
     st = r.streams
     p50 = [s["push_to_done_p50"] for s in st]
     p99 = [s["push_to_done_p99"] for s in st]
@@ -491,8 +496,10 @@ def split_replay_latency(stub_dir, rec, H2, W2, n_blocks=16, speed=1.0, group=0)
                   "halo 2), each strip's records (halo copies included) replayed into its own "
                   f"ring by record time at {speed:g}x real time -> one persistent kernel, "
                   + (f"a group of {group} workgroups per strip" if group else
-                     "one workgroup per strip") + "; latency push -> prediction",
-        "group": group,
+                     "one workgroup per strip")
+                  + (" in two pipelined stages" if stages == 2 else "")
+                  + "; latency push -> prediction",
+        "group": group, "stages": stages,
     }
 
 
@@ -703,6 +710,11 @@ def main() -> int:
                     help="GPU blocks (owned strips) of the live run; 1 = one ownership domain")
     ap.add_argument("--live-group", type=int, default=6, choices=[0, 3, 4, 5, 6],
                     help="workgroups per block of the live run (0 = one)")
+    ap.add_argument("--live-stages", type=int, default=None, choices=[1, 2],
+                    help="2: two groups per block in a pipeline (L4-L5 of a batch beside "
+                         "L6-head of the previous one); default 2 for the 80x64 live legs, "
+                         "1 for the 16-ring ones (16 streams, 640x480 strips), as measured "
+                         "fastest")
     ap.add_argument("--no-live-strips", action="store_true",
                     help="skip the second live run on the reference's 8-strip topology "
                          "(2 x 4 owned strips, halo 2, each drained by --live-group workgroups)")
@@ -862,19 +874,22 @@ def main() -> int:
             print(f"bench.py: {name} failed: {e!r}", file=sys.stderr)
             return {"error": f"{type(e).__name__}: {e}"}
 
+    if a.live_stages is None:
+        a.live_stages = 2 if a.workload == "80x64" and a.live_group > 1 else 1
     if a.workload == "80x64" and not a.no_live:
         res["latency_us"] = leg("live", lambda: live_latency(tmp.name, a.live_rate,
                                                              a.live_seconds, a.live_blocks,
-                                                             a.live_group))
+                                                             a.live_group, a.live_stages))
         if not a.no_live_strips:
             res["latency_us_8_strips"] = leg("live 8 strips", lambda: live_latency(
-                tmp.name, a.live_rate, a.live_seconds, 8, a.live_group))
+                tmp.name, a.live_rate, a.live_seconds, 8, a.live_group, a.live_stages))
     if a.workload == "16streams" and not a.no_live:
         res["latency_us"] = leg("replay", lambda: replay_latency(
-            tmp.name, recs, [o["pass3"] for o in outs], group=a.live_group))
+            tmp.name, recs, [o["pass3"] for o in outs], group=a.live_group,
+            stages=a.live_stages))
     if a.workload == "640x480" and not a.no_live:
         res["latency_us"] = leg("split replay", lambda: split_replay_latency(
-            tmp.name, recs[0], H2, W2, group=a.live_group))
+            tmp.name, recs[0], H2, W2, group=a.live_group, stages=a.live_stages))
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = leg("cpu baseline", lambda: cpu_baseline(
             tmp.name, recs[0], a.cpu_seconds, H2, W2, (outs[0], heads[0])))

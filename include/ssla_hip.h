@@ -269,7 +269,13 @@ void ssla_hip_timing_free(HybridS2S3Config* cfg, int blk);
  * order; each block's weights stream through G compute units.  All
  * n_blocks x G workgroups must fit on the device at once (SSLA_ERR_ARG
  * otherwise); a member whose wait for another runs out (2 s inside a
- * batch) ends the kernel with status 4.
+ * batch) ends the kernel with status 4.  With opts->stages = 2 each block
+ * has two such groups in a pipeline (n_blocks x G x 2 workgroups): the
+ * first loads a batch and runs tdrop_s2, L4 and L5, then hands the batch
+ * (through device memory) to the second, which runs tdrop_s3, L6, L7, the
+ * head and the predictions while the first takes the next batch.  The
+ * ring tail advances once the first group holds a batch; events_done and
+ * the timing slots once the second has finished it.
  * The kernel runs on its own non-blocking stream; do not call
  * ssla_hip_device_synchronize while it runs. */
 typedef struct SslaHipLive SslaHipLive;
@@ -282,6 +288,11 @@ typedef struct SslaHipLiveOpts {
                                       (member 0's profile with groups) */
     int          group;            /* 0 or 1: one workgroup per block;
                                       3..6: workgroups per block */
+    int          stages;           /* 0 or 1: each group runs every layer of
+                                      a batch; 2 (with group 3..6): a second
+                                      group of as many workgroups runs L6, L7
+                                      and the head of batch k while the first
+                                      runs L4 and L5 of batch k + 1 */
 } SslaHipLiveOpts;
 
 int ssla_hip_persistent_start(const HybridS2S3Config* cfg,

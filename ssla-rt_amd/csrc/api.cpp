@@ -734,9 +734,10 @@ int ssla_hip_persistent_start(const HybridS2S3Config* cfg, HybridInputRec* const
     const int max_batch = (opts && opts->max_batch) ? opts->max_batch : kLiveBatchMax;
     const unsigned idle = (opts && opts->idle_timeout_ms) ? opts->idle_timeout_ms : 30000u;
     const int group = opts ? opts->group : 0;
+    const int stages = (opts && opts->stages) ? opts->stages : 1;
     LiveSession* s = nullptr;
     const int rc = live_start(cfg, rings, ring_mask, tails, stop_flag, events_done, spin_ns,
-                              max_batch, idle, opts ? opts->phase_us : nullptr, group, &s);
+                              max_batch, idle, opts ? opts->phase_us : nullptr, group, stages, &s);
     *out = reinterpret_cast<SslaHipLive*>(s);
     return rc;
 }

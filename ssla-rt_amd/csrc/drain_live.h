@@ -39,11 +39,13 @@ size_t noalloc_scratch_bytes();
 struct LiveSession;
 
 // group 1: one workgroup per block (k_live); kGroupMin..kGroupMax: that
-// many workgroups per block, each owning channel slices (k_group).
+// many workgroups per block, each owning channel slices (k_group); stages 2
+// (with a group): two such groups per block in a pipeline, L4-L5 and L6-head.
 int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
                unsigned long long ring_mask, unsigned long long* const* tails, int* stop_flag,
                unsigned long long* const* events_done, unsigned int spin_ns, int max_batch,
-               unsigned int idle_timeout_ms, double* phase_us, int group, LiveSession** out);
+               unsigned int idle_timeout_ms, double* phase_us, int group, int stages,
+               LiveSession** out);
 
 // The batch drain with `group` workgroups per block (kGroupMin..kGroupMax);
 // synchronous on st.

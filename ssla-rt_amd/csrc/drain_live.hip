@@ -711,10 +711,18 @@ __device__ __forceinline__ void prof_begin(SL& S, const LiveDesc& d) {
     }
 }
 
+// The profile slots stage B of a two-stage group fills (its member 0 writes
+// them; stage A's member 0 writes the others).
+__device__ __forceinline__ bool prof_stage_b(int k) {
+    return (k >= PF_TD3 && k <= PF_PUBLISH) || k == PF_XWAIT + 2 || k == PF_XWAIT + 3;
+}
+
+// stage: -1 every slot, 0 / 1 the slots of stage A / B of a two-stage group
 template <class SL>
-__device__ __forceinline__ void prof_end(SL& S, const LiveDesc& d) {
+__device__ __forceinline__ void prof_end(SL& S, const LiveDesc& d, int stage = -1) {
     if (threadIdx.x == 0 && d.prof)
-        for (int k = 0; k < NPROF; ++k) d.prof[k] = S.prof[k];
+        for (int k = 0; k < NPROF; ++k)
+            if (stage < 0 || (stage == 1) == prof_stage_b(k)) d.prof[k] = S.prof[k];
 }
 
 // Clock handshake with the host (live kernels, poll wave lane 0): when the
@@ -1234,13 +1242,13 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
 
 // One batch for one member (the schedule of process_batch); false when an
 // exchange wait ran out.  Member 0 also runs the head.
-__device__ __forceinline__ bool process_group(int B, const LiveDesc& d, const LiveWeights& W,
-                                           const Geometry& G, GroupCtx gc,
-                                           const float* const* goT, const float* const* ipT,
-                                           unsigned char* td2,
-                                           unsigned char* td3) {
+// Stage A of a group's batch: tdrop_s2, the s2 pairs, L4 and L5 (leaves L5's
+// outputs in S.X for the pass-2 records).
+__device__ __forceinline__ bool group_stage_a(int B, const LiveDesc& d, const LiveWeights& W,
+                                             const Geometry& G, GroupCtx gc,
+                                             const float* const* goT, const float* const* ipT,
+                                             unsigned char* td2) {
     LdsG& S = g_ldsg;
-    const int tid = threadIdx.x;
     batch_tdrop(S, B, td2, S.c2, nullptr, S.p2, G.window);
     __syncthreads();
     mark(S, PF_TD2);
@@ -1248,8 +1256,19 @@ __device__ __forceinline__ bool process_group(int B, const LiveDesc& d, const Li
     mark(S, PF_PAIRS2);
     if (!group_layer<SSLA_C1, SSLA_C2>(S, B, S.vld, nullptr, W.L[0], W.pk.pp[0], goT[0], ipT[0], d.hidden[0], gc, PF_L4))
         return false;
-    if (!group_layer<SSLA_C2, SSLA_C2>(S, B, S.vld, S.p2, W.L[1], W.pk.pp[1], goT[1], ipT[1], d.hidden[1], gc, PF_L5))
-        return false;
+    return group_layer<SSLA_C2, SSLA_C2>(S, B, S.vld, S.p2, W.L[1], W.pk.pp[1], goT[1], ipT[1], d.hidden[1], gc, PF_L5);
+}
+
+// Stage B: pooling to s3, tdrop_s3, the s3 pairs, L6, L7 and (member 0) the
+// head.  `l6_done` (may be null) runs once L6's exchange has completed, i.e.
+// once every member of the group has read the batch's inputs.
+template <class F>
+__device__ __forceinline__ bool group_stage_b(int B, const LiveDesc& d, const LiveWeights& W,
+                                             const Geometry& G, GroupCtx gc,
+                                             const float* const* goT, const float* const* ipT,
+                                             unsigned char* td3, F l6_done) {
+    LdsG& S = g_ldsg;
+    const int tid = threadIdx.x;
     if (tid < B) {
         S.ex[tid] >>= 1;
         S.ey[tid] >>= 1;
@@ -1263,37 +1282,224 @@ __device__ __forceinline__ bool process_group(int B, const LiveDesc& d, const Li
     mark(S, PF_PAIRS3);
     if (!group_layer<SSLA_C2, SSLA_C3>(S, B, S.p2, nullptr, W.L[2], W.pk.pp[2], goT[2], ipT[2], d.hidden[2], gc, PF_L6))
         return false;
+    l6_done();
     if (!group_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], W.pk.pp[3], goT[3], ipT[3], d.hidden[3], gc, PF_L7))
         return false;
     if (gc.k == 0 && W.have_head) batch_head(S, B, d, W);
     return true;
 }
 
+// One group running both stages of a batch.
+__device__ __forceinline__ bool process_group(int B, const LiveDesc& d, const LiveWeights& W,
+                                           const Geometry& G, GroupCtx gc,
+                                           const float* const* goT, const float* const* ipT,
+                                           unsigned char* td2,
+                                           unsigned char* td3) {
+    if (!group_stage_a(B, d, W, G, gc, goT, ipT, td2)) return false;
+    return group_stage_b(B, d, W, G, gc, goT, ipT, td3, [] {});
+}
+
+// Two-stage groups (live drain): per block a group A of G workgroups runs
+// the batch load, tdrop_s2, the s2 pairs, L4 and L5, then hands the batch
+// to a group B of G more workgroups, which runs tdrop_s3, the s3 pairs, L6,
+// L7, the head, the predictions and the timing slots -- while A takes the
+// next batch.  The hand-off goes through two slots of tagged words (as the
+// exchanges: each 64-bit word carries the hand-off's sequence number, so a
+// reader that sees the tag sees the value): a header (batch size and exit
+// flag), the batch's pop time, and per record its s2 coordinates and flags,
+// both timestamps and its L5 output row.  B's member 0 acknowledges a slot
+// once L6's exchange has completed (every member of B has read it); A's
+// member 0 writes hand-off n + 2 into the slot only after that
+// acknowledgement of hand-off n.  A advances the ring tail after its stage
+// (the ring slots are then free: A holds the records), B the events_done
+// counter after its stage.  Waits are bounded as the exchanges' are.
+constexpr int kHRec = 5 + SSLA_C2;                  // words per record
+constexpr size_t kHSlot = 3 + (size_t)LB * kHRec;   // header, pop time (2), records
+constexpr size_t kHAck = 2 * kHSlot;                // two acknowledgement words
+constexpr size_t kHStride = (kHAck + 2 + 31) & ~(size_t)31;   // words per block
+
 struct GroupArgs {
-    unsigned long long* xb;              // exchange words, kXStride per block (zeroed)
-    unsigned char* tdrep;                // counters of members 1..G-1: (G - 1) x (C2 + C3) per block
+    unsigned long long* xb;              // exchange words, kXStride per block and stage (zeroed)
+    unsigned char* tdrep;                // counters of members 1..G-1 of each stage:
+                                         // (G - 1) x (C2 + C3) per block and stage
+    unsigned long long* hb;              // hand-off words, kHStride per block (zeroed; 2 stages)
     const float* goT[4];                 // OutPackT goW fragments of L4..L7
     const float* ipT[4];                 // OutPackT input_proj fragments (L4, L6; else null)
     unsigned long long wait_ticks;
     int G;
+    int stages;                          // 1, or 2 (live drain only)
 };
 
+// Stage A's member 0: hand-off `hseq` (slot hseq & 1) of B records, or of an
+// exit flag; false when the slot's previous acknowledgement did not arrive.
+__device__ __forceinline__ bool handoff_put(LdsG& S, unsigned long long* hb, unsigned hseq, int B,
+                                            int flag, unsigned long long wait_ticks) {
+    const int tid = threadIdx.x;
+    unsigned long long* hs = hb + (size_t)(hseq & 1u) * kHSlot;
+    if (tid == 0) {
+        bool late = false;
+        if (hseq >= 2u) {
+            const unsigned long long dl = (unsigned long long)wall_clock64() + wait_ticks;
+            (void)xwait(hb + kHAck + (hseq & 1u), hseq - 1u, dl, late);
+        }
+        S.abort_ = late ? 1 : 0;
+    }
+    __syncthreads();
+    if (S.abort_) return false;
+    const unsigned tag = hseq + 1u;
+    for (int w = tid; w < B * kHRec; w += LT) {
+        const int e = w / kHRec, q = w - e * kHRec;
+        unsigned v;
+        if (q == 0)
+            v = (unsigned)S.ex[e] | ((unsigned)S.ey[e] << 12) | ((unsigned)S.vld[e] << 24) |
+                ((unsigned)S.own[e] << 25) | ((unsigned)S.p2[e] << 26);
+        else if (q == 1) v = (unsigned)S.tpush[e];
+        else if (q == 2) v = (unsigned)(S.tpush[e] >> 32);
+        else if (q == 3) v = (unsigned)S.temit[e];
+        else if (q == 4) v = (unsigned)(S.temit[e] >> 32);
+        else v = __float_as_uint(S.X[e][q - 5]);
+        xput(hs + 3 + w, xword(v, tag));
+    }
+    if (tid == 0) {
+        xput(hs + 1, xword((unsigned)S.t_pop, tag));
+        xput(hs + 2, xword((unsigned)(S.t_pop >> 32), tag));
+        xput(hs, xword((unsigned)B | ((unsigned)flag << 8), tag));
+    }
+    return true;
+}
+
+// Stage B of a two-stage live group: takes hand-offs in order, runs L6, L7
+// and the head, and publishes (timing slots, events_done; member 0).
+__device__ __forceinline__ void group_live_stage_b(LdsG& S, const LiveDesc& d,
+                                                   const LiveWeights& W, const Geometry& G,
+                                                   const GroupArgs& ga, GroupCtx gc,
+                                                   unsigned char* td3,
+                                                   unsigned long long idle_ticks,
+                                                   unsigned int spin_ns, int* status,
+                                                   unsigned long long* hb) {
+    const int tid = threadIdx.x, k = gc.k;
+    const int sleep_iters = (int)(spin_ns / 40u) + 1;
+    unsigned long long t = d.t0;
+    unsigned long long last_work = (unsigned long long)wall_clock64();
+    unsigned hseq = 0;
+    while (true) {
+        __syncthreads();
+        unsigned long long* hs = hb + (size_t)(hseq & 1u) * kHSlot;
+        const unsigned tag = hseq + 1u;
+        if (tid == 0) {
+            // stage A hands off at least once per idle timeout (then it stops)
+            const unsigned long long dl = last_work + idle_ticks + gc.wait_ticks;
+            unsigned long long v = __hip_atomic_load(hs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            bool late = false;
+            while ((unsigned)(v >> 32) != tag) {
+                if ((unsigned long long)wall_clock64() > dl) {
+                    late = true;
+                    break;
+                }
+                for (int i = 0; i < sleep_iters; ++i) __builtin_amdgcn_s_sleep(1);
+                v = __hip_atomic_load(hs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            S.flag = late ? 4 : (int)((v >> 8) & 0xffu);
+            S.bsize = (int)(v & 0xffu);
+            S.abort_ = 0;
+        }
+        __syncthreads();
+        const int flag = S.flag, B = S.bsize;
+        if (flag) {
+            if (tid == 0 && flag == 4) atomicMax(status, 4);
+            if (k == 0) prof_end(S, d, 1);
+            return;
+        }
+        {
+            const unsigned long long dl = (unsigned long long)wall_clock64() + gc.wait_ticks;
+            bool late = false;
+            for (int w = tid; w < B * kHRec; w += LT) {
+                const unsigned u = (unsigned)xwait(hs + 3 + w, tag, dl, late);
+                const int e = w / kHRec, q = w - e * kHRec;
+                if (q == 0) {
+                    S.ex[e] = (int)(u & 0xfffu);
+                    S.ey[e] = (int)((u >> 12) & 0xfffu);
+                    S.vld[e] = (unsigned char)((u >> 24) & 1u);
+                    S.own[e] = (unsigned char)((u >> 25) & 1u);
+                    S.p2[e] = (unsigned char)((u >> 26) & 1u);
+                    S.p3[e] = 0;
+                } else if (q <= 4) {
+                    unsigned* w2 = reinterpret_cast<unsigned*>(q <= 2 ? &S.tpush[e] : &S.temit[e]);
+                    w2[(q - 1) & 1] = u;
+                } else {
+                    S.X[e][q - 5] = __uint_as_float(u);
+                }
+            }
+            if (tid == 0) {
+                const unsigned lo = (unsigned)xwait(hs + 1, tag, dl, late);
+                const unsigned hi = (unsigned)xwait(hs + 2, tag, dl, late);
+                S.t_pop = (unsigned long long)lo | ((unsigned long long)hi << 32);
+                S.tprev = (unsigned long long)wall_clock64();
+            }
+            if (late) S.abort_ = 1;
+        }
+        __syncthreads();
+        if (S.abort_) {
+            if (tid == 0) atomicMax(status, 4);
+            if (k == 0) prof_end(S, d, 1);
+            return;
+        }
+        // L6's exchange has every member's partial sums, so every member has
+        // read the hand-off: member 0 acknowledges its slot
+        const bool ok = group_stage_b(B, d, W, G, gc, ga.goT, ga.ipT, td3, [&] {
+            if (k == 0 && threadIdx.x == 0) xput(hb + kHAck + (hseq & 1u), xword(0u, tag));
+        });
+        if (!ok) {
+            if (tid == 0) atomicMax(status, 4);
+            if (k == 0) prof_end(S, d, 1);
+            return;
+        }
+        const unsigned long long t_done = (unsigned long long)wall_clock64();
+        if (k == 0) {
+            if (tid < B && d.timing) {
+                const unsigned long long seq = t + (unsigned long long)tid;
+                GpuTimingSlot& ts = d.timing[seq & d.timing_mask];
+                ts.t_pop_clk = S.t_pop;
+                ts.t_done_clk = t_done;
+                ts.seq = (unsigned int)seq;
+                ts.owner = (S.own[tid] && S.p2[tid] && S.p3[tid]) ? 1u : 0u;
+                ts.t_push_ns = S.tpush[tid];
+                ts.t_emit_ns = S.temit[tid];
+            }
+            __threadfence_system();
+            __syncthreads();
+            if (tid == 0 && d.events_done)
+                __hip_atomic_store(d.events_done, t + (unsigned long long)B, __ATOMIC_RELEASE,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+            mark(S, PF_PUBLISH);
+        }
+        t += (unsigned long long)B;
+        last_work = t_done;
+        ++hseq;
+    }
+}
+
 // Batch mode (LIVE false: d.n records in batches of max_batch) or the
-// persistent live drain; blocks of G consecutive workgroups.
-template <bool LIVE>
+// persistent live drain; blocks of G consecutive workgroups (G per stage,
+// stage A first, with two stages).
+template <bool LIVE, int ST>
 __global__ void __launch_bounds__(LT)
 k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga,
         const int* stop_flag, unsigned int spin_ns, unsigned long long idle_ticks, int max_batch,
         int* __restrict__ status) {
     LdsG& S = g_ldsg;
     const int tid = threadIdx.x;
-    const int b = blockIdx.x / ga.G, k = blockIdx.x - b * ga.G;
+    // block b's workgroups: stage 0 (A) members 0..G-1, then stage 1 (B)
+    static_assert(ST == 1 || (ST == 2 && LIVE), "two stages: live drain only");
+    const int GS = ga.G * ST;
+    const int b = blockIdx.x / GS, m = blockIdx.x - b * GS;
+    const int stage = m / ga.G, k = m - stage * ga.G;
     const LiveDesc& d = ld[b];
-    const GroupCtx gc{ga.xb + (size_t)b * kXStride, ga.wait_ticks, k, ga.G};
+    const GroupCtx gc{ga.xb + ((size_t)b * ST + stage) * kXStride, ga.wait_ticks, k, ga.G};
     unsigned char* td2 = d.td2;
     unsigned char* td3 = d.td3;
     if (k > 0) {
-        td2 = ga.tdrep + ((size_t)b * (ga.G - 1) + (k - 1)) * (size_t)(G.C2 + G.C3);
+        td2 = ga.tdrep + (((size_t)b * ST + stage) * (ga.G - 1) + (k - 1)) * (size_t)(G.C2 + G.C3);
         td3 = td2 + G.C2;
     }
     if (k == 0) prof_begin(S, d);
@@ -1303,6 +1509,15 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
         S.xseq = 0;
     }
     __syncthreads();
+    if constexpr (ST == 2) {
+        if (stage == 1) {
+            group_live_stage_b(S, d, W, G, ga, gc, td3, idle_ticks, spin_ns, status,
+                               ga.hb + (size_t)b * kHStride);
+            return;
+        }
+    }
+    unsigned long long* const hb = ST == 2 ? ga.hb + (size_t)b * kHStride : nullptr;
+    const int pstage = ST == 2 ? 0 : -1;            // profile slots member 0 writes
     if constexpr (!LIVE) {
         int bi = 0;
         for (int base = 0; base < d.n; base += max_batch, ++bi) {
@@ -1359,6 +1574,7 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
     const int sleep_iters = (int)(spin_ns / 40u) + 1;
     unsigned long long* bc = gc.xb + kXBc;
     unsigned bseq = 0;                   // batches broadcast
+    unsigned hseq = 0;                   // hand-offs to stage B (two stages)
     unsigned long long ping_seen = 0;
     while (true) {
         __syncthreads();
@@ -1419,7 +1635,11 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
                     __hip_atomic_store(d.kend, (unsigned long long)wall_clock64(), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_SYSTEM);
             }
-            if (k == 0) prof_end(S, d);
+            // stage B ends on the same flag once it has taken every batch
+            if (ST == 2 && k == 0 && !handoff_put(S, hb, hseq, 0, flag, gc.wait_ticks) &&
+                tid == 0)
+                atomicMax(status, 4);
+            if (k == 0) prof_end(S, d, pstage);
             return;
         }
         if (k != 0 && tid < B) {
@@ -1449,15 +1669,41 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
         load_batch(S, B, d.ring, t, mask, d.strip, G);
         __syncthreads();
         mark(S, PF_LOAD);
-        if (!process_group(B, d, W, G, gc, ga.goT, ga.ipT, td2, td3)) {
+        bool ok;
+        if constexpr (ST == 2) ok = group_stage_a(B, d, W, G, gc, ga.goT, ga.ipT, td2);
+        else ok = process_group(B, d, W, G, gc, ga.goT, ga.ipT, td2, td3);
+        if (!ok) {
             if (tid == 0) {
                 atomicMax(status, 4);
                 if (k == 0 && d.kend)
                     __hip_atomic_store(d.kend, (unsigned long long)wall_clock64(), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_SYSTEM);
             }
-            if (k == 0) prof_end(S, d);
+            if (ST == 2 && k == 0) (void)handoff_put(S, hb, hseq, 0, 4, gc.wait_ticks);
+            if (k == 0) prof_end(S, d, pstage);
             return;
+        }
+        if constexpr (ST == 2) {
+            // stage A: the ring slots are free (every member holds the batch),
+            // and the batch goes to stage B
+            if (k == 0) {
+                if (tid == 0)
+                    __hip_atomic_store(d.tail, t + (unsigned long long)B, __ATOMIC_RELEASE,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+                if (!handoff_put(S, hb, hseq, B, 0, gc.wait_ticks)) {
+                    if (tid == 0) atomicMax(status, 4);
+                    prof_end(S, d, pstage);
+                    return;
+                }
+                if (tid == 0) {
+                    S.prof[PF_BATCHES] += 1;
+                    S.prof[PF_RECORDS] += (unsigned long long)B;
+                }
+            }
+            ++hseq;
+            t += (unsigned long long)B;
+            last_work = (unsigned long long)wall_clock64();
+            continue;
         }
         const unsigned long long t_done = (unsigned long long)wall_clock64();
         if (k == 0) {
@@ -1769,11 +2015,13 @@ int batch_drain_noalloc(const HybridS2S3Config* cfg, const HybridInputRec* const
 // packings (ProjPack for the projections, OutPackT for the goW fragments).
 struct GroupRes {
     unsigned long long* xb = nullptr;
+    unsigned long long* hb = nullptr;
     unsigned char* tdrep = nullptr;
     float* pack = nullptr;
     float* packT = nullptr;
     void release() {
         if (xb) (void)hipFree(xb);
+        if (hb) (void)hipFree(hb);
         if (tdrep) (void)hipFree(tdrep);
         if (pack) (void)hipFree(pack);
         if (packT) (void)hipFree(packT);
@@ -1783,48 +2031,60 @@ struct GroupRes {
 
 // Every member of every group must be resident at once: members wait on
 // each other.
-static int group_check(int nb, int group) {
+static int group_check(int nb, int group, int stages = 1) {
     if (group < kGroupMin || group > kGroupMax) {
         set_error("group must be 1 or in [" + std::to_string(kGroupMin) + ", " +
                   std::to_string(kGroupMax) + "]");
         return SSLA_ERR_ARG;
     }
+    if (stages != 1 && stages != 2) {
+        set_error("stages must be 1 or 2");
+        return SSLA_ERR_ARG;
+    }
     int per_cu = 0, cus = 0, dev = 0;
-    LHIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_group<true>, LT, 0));
+    LHIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_group<true, 1>, LT, 0));
     LHIP(hipGetDevice(&dev));
     LHIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    if ((long long)nb * group > (long long)per_cu * cus) {
-        set_error("n_blocks x group workgroups (" + std::to_string(nb * group) +
+    if ((long long)nb * group * stages > (long long)per_cu * cus) {
+        set_error("n_blocks x group x stages workgroups (" + std::to_string(nb * group * stages) +
                   ") do not fit on the device at once (" + std::to_string(per_cu * cus) + ")");
         return SSLA_ERR_ARG;
     }
     return SSLA_OK;
 }
 
-// Allocates r, clears the exchange words, copies each block's counters for
-// members 1..group-1 and packs the weights, all on st; fills ga and W->pk.
-// On error the caller releases r.
+// Allocates r, clears the exchange (and hand-off) words, copies each block's
+// counters for members 1..group-1 of each stage and packs the weights, all
+// on st; fills ga and W->pk.  On error the caller releases r.
 static int group_setup(const HybridS2S3Config* cfg, const Geometry& G, int group, hipStream_t st,
-                       LiveWeights* W, GroupRes* r, GroupArgs* ga) {
+                       LiveWeights* W, GroupRes* r, GroupArgs* ga, int stages = 1) {
     const int nb = G.nb;
-    const size_t xbytes = sizeof(unsigned long long) * kXStride * nb;
+    const size_t xbytes = sizeof(unsigned long long) * kXStride * nb * stages;
     const size_t per = (size_t)(G.C2 + G.C3);
     LHIP(hipMalloc(&r->xb, xbytes));
-    LHIP(hipMalloc(&r->tdrep, (size_t)nb * (group - 1) * per));
+    LHIP(hipMalloc(&r->tdrep, (size_t)nb * stages * (group - 1) * per));
     LHIP(hipMalloc(&r->pack, sizeof(float) * packed_weight_floats()));
     LHIP(hipMalloc(&r->packT, sizeof(float) * packed_weight_floats_d()));
     LHIP(hipMemsetAsync(r->xb, 0, xbytes, st));
-    for (int b = 0; b < nb; ++b)
+    if (stages == 2) {
+        const size_t hbytes = sizeof(unsigned long long) * kHStride * nb;
+        LHIP(hipMalloc(&r->hb, hbytes));
+        LHIP(hipMemsetAsync(r->hb, 0, hbytes, st));
+    }
+    for (int b = 0; b < nb * stages; ++b)
         for (int m = 0; m < group - 1; ++m) {
             unsigned char* dst = r->tdrep + ((size_t)b * (group - 1) + m) * per;
-            LHIP(hipMemcpyAsync(dst, cfg->tdrop_s2[b], (size_t)G.C2, hipMemcpyDeviceToDevice, st));
-            LHIP(hipMemcpyAsync(dst + G.C2, cfg->tdrop_s3[b], (size_t)G.C3, hipMemcpyDeviceToDevice, st));
+            const int blk = b / stages;
+            LHIP(hipMemcpyAsync(dst, cfg->tdrop_s2[blk], (size_t)G.C2, hipMemcpyDeviceToDevice, st));
+            LHIP(hipMemcpyAsync(dst + G.C2, cfg->tdrop_s3[blk], (size_t)G.C3, hipMemcpyDeviceToDevice, st));
         }
     LHIP(pack_weights(W->L, r->pack, &W->pk, st));
     PackedWeights pt{};
     LHIP(pack_weights_d(W->L, r->packT, &pt, st));
     ga->xb = r->xb;
+    ga->hb = r->hb;
     ga->tdrep = r->tdrep;
+    ga->stages = stages;
     ga->goT[0] = pt.po[0] + OutPackT<SSLA_C1, SSLA_C2>::Q;
     ga->goT[1] = pt.po[1] + OutPackT<SSLA_C2, SSLA_C2>::Q;
     ga->goT[2] = pt.po[2] + OutPackT<SSLA_C2, SSLA_C3>::Q;
@@ -1885,7 +2145,7 @@ int batch_drain_group(const HybridS2S3Config* cfg, const HybridInputRec* const* 
             d.prof = prof ? prof + (size_t)NPROF * b : nullptr;
         }
         LHIP(hipMemcpyAsync(desc, hd.data(), sizeof(LiveDesc) * nb, hipMemcpyHostToDevice, st));
-        hipLaunchKernelGGL(k_group<false>, dim3(nb * group), dim3(LT), 0, st, desc, W, G, ga,
+        hipLaunchKernelGGL((k_group<false, 1>), dim3(nb * group), dim3(LT), 0, st, desc, W, G, ga,
                            (const int*)nullptr, 0u, 0ull, batch, status);
         LHIP(hipGetLastError());
         LHIP(hipStreamSynchronize(st));
@@ -1929,7 +2189,8 @@ struct LiveSession {
 int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
                unsigned long long ring_mask, unsigned long long* const* tails, int* stop_flag,
                unsigned long long* const* events_done, unsigned int spin_ns, int max_batch,
-               unsigned int idle_timeout_ms, double* phase_us, int group, LiveSession** out) {
+               unsigned int idle_timeout_ms, double* phase_us, int group, int stages,
+               LiveSession** out) {
     *out = nullptr;
     LiveWeights W;
     Geometry G;
@@ -1948,7 +2209,12 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
         return SSLA_ERR_ARG;
     }
     const int nb = cfg->n_blocks;
-    if (group > 1 && (rc = group_check(nb, group))) return rc;
+    if (stages < 1) stages = 1;
+    if (stages > 1 && group <= 1) {
+        set_error("two stages need a group (3..6 workgroups per stage)");
+        return SSLA_ERR_ARG;
+    }
+    if (group > 1 && (rc = group_check(nb, group, stages))) return rc;
     for (int b = 0; b < nb; ++b) {
         if (!rings[b] || !tails[b]) {
             set_error("every block needs a ring and a tail");
@@ -1983,7 +2249,8 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
     if (hipMalloc(&s->status, sizeof(int)) != hipSuccess) return fail("status");
     GroupArgs ga{};
     if (group > 1) {
-        if (group_setup(cfg, G, group, s->stream, &W, &s->grp, &ga) != SSLA_OK) return fail("group set-up");
+        if (group_setup(cfg, G, group, s->stream, &W, &s->grp, &ga, stages) != SSLA_OK)
+            return fail("group set-up");
     } else {
         if (hipMalloc(&s->pack, sizeof(float) * packed_weight_floats()) != hipSuccess) return fail("weights");
         if (pack_weights(W.L, s->pack, &W.pk, s->stream) != hipSuccess) return fail("weight packing");
@@ -2017,8 +2284,11 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
         return fail("copy");
     if (hipStreamSynchronize(s->stream) != hipSuccess) return fail("sync");
     const unsigned long long idle = (unsigned long long)idle_timeout_ms * (unsigned long long)khz;
-    if (group > 1)
-        hipLaunchKernelGGL(k_group<true>, dim3(nb * group), dim3(LT), 0, s->stream, s->desc, W, G, ga,
+    if (group > 1 && stages == 2)
+        hipLaunchKernelGGL((k_group<true, 2>), dim3(nb * group * 2), dim3(LT), 0, s->stream, s->desc, W, G, ga,
+                           stop_flag, spin_ns, idle, max_batch, s->status);
+    else if (group > 1)
+        hipLaunchKernelGGL((k_group<true, 1>), dim3(nb * group), dim3(LT), 0, s->stream, s->desc, W, G, ga,
                            stop_flag, spin_ns, idle, max_batch, s->status);
     else
         hipLaunchKernelGGL(k_live, dim3(nb), dim3(LT), 0, s->stream, s->desc, W, G, stop_flag, spin_ns,

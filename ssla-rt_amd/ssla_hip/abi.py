@@ -112,7 +112,8 @@ class SslaHipDrainOpts(ctypes.Structure):
 
 class SslaHipLiveOpts(ctypes.Structure):
     _fields_ = [("max_batch", ctypes.c_int), ("idle_timeout_ms", ctypes.c_uint),
-                ("phase_us", ctypes.POINTER(ctypes.c_double)), ("group", ctypes.c_int)]
+                ("phase_us", ctypes.POINTER(ctypes.c_double)), ("group", ctypes.c_int),
+                ("stages", ctypes.c_int)]
 
 
 class SslaHipOevaDiff(ctypes.Structure):

@@ -476,7 +476,8 @@ class LiveDrain:
     """A running persistent drain over HostRings (ssla_hip_persistent_start)."""
 
     def __init__(self, drain: Drain, rings: HostRings, spin_ns: int = 200, max_batch: int = 32,
-                 idle_timeout_ms: int = 30000, profile: bool = False, group: int = 0):
+                 idle_timeout_ms: int = 30000, profile: bool = False, group: int = 0,
+                 stages: int = 1):
         self.rings = rings
         self.h = ctypes.c_void_p()
         bufs, tails, dones = rings.ptrs()
@@ -484,6 +485,7 @@ class LiveDrain:
         self.phase_us = np.zeros(abi.N_BATCH_PHASES, np.float64) if profile else None
         opts = abi.SslaHipLiveOpts(max_batch, idle_timeout_ms)
         opts.group = group
+        opts.stages = stages
         if profile:
             opts.phase_us = self.phase_us.ctypes.data_as(ctypes.POINTER(ctypes.c_double))
         lib.check(lib.load().ssla_hip_persistent_start(

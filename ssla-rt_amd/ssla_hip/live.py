@@ -136,7 +136,7 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
              n_blobs: int = 8, sigma_px: float = 3.0, bg_frac: float = 0.1,
              ring_capacity: int = 1 << 16, timing_capacity: int = 1 << 22, max_batch: int = 32,
              spin_ns: int = 200, profile: bool = True, drain_timeout_s: float = 30.0,
-             back_pressure: bool = False, group: int = 0,
+             back_pressure: bool = False, group: int = 0, stages: int = 1,
              inspect: Optional[Callable] = None) -> LiveResult:
     """One live run on one GPU.  back_pressure makes the producer wait for
     each ring's tail instead of overwriting unread slots.  gpu_blocks (1, 2, 4, 8, 16; the reference's
@@ -149,7 +149,9 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
     has stopped and before any buffer is freed (heads: records published per
     ring), e.g. to check the rings' contents and the final state.  group
     (3..6) drains each strip with that many workgroups, each owning channel
-    slices of every layer (0: one workgroup per strip)."""
+    slices of every layer (0: one workgroup per strip); stages 2 adds a second
+    such group per strip that runs L6, L7 and the head of a batch while the
+    first runs L4 and L5 of the next."""
     if base_core is None or synth_core is None:
         sc, bc = pick_cores(n_shards)
         synth_core = sc if synth_core is None else synth_core
@@ -173,7 +175,7 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
             prod.set_ring_tails(rings.tail_ptrs(), timeout_ms=1000.0 * drain_timeout_s)
         live = LiveDrain(drain, rings, spin_ns=spin_ns, max_batch=max_batch,
                          idle_timeout_ms=int((duration_s + drain_timeout_s + 30) * 1000),
-                         profile=profile, group=group)
+                         profile=profile, group=group, stages=stages)
         clks = [np.ctypeslib.as_array((np.ctypeslib.ctypes.c_ulonglong * 2).from_address(
             c.kernel_start_clk[b])) for b in range(nb)]
         k0 = [_spin_nonzero(lambda a=a: int(a[0]), 30.0) for a in clks]
@@ -275,7 +277,7 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
                timing_capacity: int = 1 << 18, max_batch: int = 32, spin_ns: int = 200,
                pin_core: Optional[int] = None, profile: bool = True, expect_p3=None,
                drain_timeout_s: float = 60.0, strips=None,
-               speed: Optional[float] = None, group: int = 0,
+               speed: Optional[float] = None, group: int = 0, stages: int = 1,
                inspect: Optional[Callable] = None) -> ReplayResult:
     """Several rings live on one GPU: pre-built ring records (one array per
     ring) replayed into one ring each, one persistent workgroup per ring.
@@ -287,7 +289,7 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
     time).  expect_p3 (optional, one flag array per ring) gives each ring's
     drop drift: records whose timing-slot owner flag differs from it.
     inspect(drain), when given, is called once the kernel has stopped and
-    before the state is freed.  group as in run_live."""
+    before the state is freed.  group and stages as in run_live."""
     from .producer import Replay
     nb = len(streams)
     if pin_core is None:
@@ -300,7 +302,7 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
         c = drain.cfg
         live = LiveDrain(drain, rings, spin_ns=spin_ns, max_batch=max_batch,
                          idle_timeout_ms=int((drain_timeout_s + 60) * 1000), profile=profile,
-                         group=group)
+                         group=group, stages=stages)
         clk = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_ulonglong * 2).from_address(c.kernel_start_clk[0]))
         k0 = _spin_nonzero(lambda: int(clk[0]), 30.0)
         t0_cpu = _now_ns()

@@ -77,16 +77,20 @@ def test_group_bad_sizes(H, stub_dir):
             d.run(batch=0, group=6)          # the whole-ring drain has no groups
 
 
-@pytest.mark.parametrize("group", [6, 3])
-def test_live_group_single_stream(H, stub_dir, stub_npz, group):
+@pytest.mark.parametrize("group,stages", [(6, 1), (3, 1), (6, 2), (3, 2)])
+def test_live_group_single_stream(H, stub_dir, stub_npz, group, stages):
+    """One stream drained by a group (stages 1) or by two groups in a
+    pipeline (stages 2: L4-L5 of a batch beside L6-head of the previous
+    one, the batch handed over through device memory)."""
     n = 3000
-    say("live group single stream", group, n)
+    say("live group single stream", group, stages, n)
     rec = events.blob_records(n, seed=13)
     recs = events.to_records(rec)
     with H.Drain.from_weights_dir(stub_dir) as d:
         d.alloc_timing(4096)
         rings = H.HostRings(1, capacity=1024)
-        live = H.LiveDrain(d, rings, idle_timeout_ms=15000, group=group, profile=True)
+        live = H.LiveDrain(d, rings, idle_timeout_ms=15000, group=group, stages=stages,
+                           profile=True)
         try:
             _produce(rings, 0, recs)
             _wait_done(rings, 0, n)
@@ -111,7 +115,7 @@ def test_live_group_single_stream(H, stub_dir, stub_npz, group):
         nbat = max(1.0, ph[abi.BATCH_PHASES.index("batches")])
         per = {k: round(ph[i] / nbat, 2) for i, k in enumerate(abi.BATCH_PHASES)
                if k not in ("batches", "records")}
-        say(f"live group {group}: per-batch kernel time p50 {np.median(lat_us):.1f} us, "
+        say(f"live group {group} x {stages}: per-batch kernel time p50 {np.median(lat_us):.1f} us, "
             f"max {lat_us.max():.1f} us; {nbat:.0f} batches of "
             f"{ph[abi.BATCH_PHASES.index('records')] / nbat:.1f} records; per batch (us) {per}")
         rings.free()
@@ -141,4 +145,15 @@ def test_clock_handshake(H, stub_dir, group):
         ns_per_tick = (p1[0] - p0[0]) / (p1[1] - p0[1])
         say(f"clock handshake group {group}: {ns_per_tick:.5f} ns/tick, brackets {p0[2]}, {p1[2]} ns")
         assert abs(ns_per_tick * khz.value / 1e6 - 1.0) < 1e-3
+        rings.free()
+
+
+def test_two_stages_bad_sizes(H, stub_dir):
+    """Two stages need a group, and n_blocks x group x 2 workgroups on the
+    device at once."""
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        rings = H.HostRings(1, capacity=256)
+        for g, st in ((0, 2), (6, 3)):
+            with pytest.raises(lib.SslaHipError):
+                H.LiveDrain(d, rings, idle_timeout_ms=2000, group=g, stages=st)
         rings.free()

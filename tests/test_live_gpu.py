@@ -523,8 +523,8 @@ def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks, group):
     assert r.synth_events > 0.5 * 2.0e6 * r.duration_s
 
 
-@pytest.mark.parametrize("group", [0, 6])
-def test_config4_sixteen_rings_one_persistent_kernel(stub_dir, stub_npz, group):
+@pytest.mark.parametrize("group,stages", [(0, 1), (6, 1), (6, 2)])
+def test_config4_sixteen_rings_one_persistent_kernel(stub_dir, stub_npz, group, stages):
     """Config 4: 16 independent 80x64 instances sharing the stub weights in
     one persistent kernel (...celled.cuh:82 MAX_BLOCKS = 16, :1547), each fed
     its own seeded blob stream (seeds 1..16) through its own ring at 125k
@@ -533,7 +533,8 @@ def test_config4_sixteen_rings_one_persistent_kernel(stub_dir, stub_npz, group):
     the oracle's."""
     from ssla_hip import live as LV
     n = 40_000
-    say(f"config 4: 16 rings x {n} records at 125k records/s each, group {group}")
+    say(f"config 4: 16 rings x {n} records at 125k records/s each, group {group}, "
+        f"stages {stages}")
     recs = [events.blob_records(n, seed=1 + s) for s in range(16)]
     expect = [O.decisions(r.x, r.y, 16, 20, 4)[1] for r in recs]
     state = {}
@@ -545,7 +546,7 @@ def test_config4_sixteen_rings_one_persistent_kernel(stub_dir, stub_npz, group):
 
     res = LV.run_replay(stub_dir, [events.to_records(r) for r in recs], 125_000.0,
                         ring_capacity=1 << 16, timing_capacity=1 << 16, expect_p3=expect,
-                        group=group, inspect=inspect)
+                        group=group, stages=stages, inspect=inspect)
     say("config 4: status", res.status, "per stream (drained, drift, p50 us, p99 us):",
         [(s["drained"], s["drop_drift"], round(s["push_to_done_p50"], 1),
           round(s["push_to_done_p99"], 1)) for s in res.streams])
@@ -562,7 +563,8 @@ def test_config4_sixteen_rings_one_persistent_kernel(stub_dir, stub_npz, group):
         check_preds(pr, ver, recs[b], p3, ref7)
 
 
-def test_640x480_strips_live_group(stub_640):
+@pytest.mark.parametrize("stages", [1, 2])
+def test_640x480_strips_live_group(stub_640, stages):
     """The 640x480 stream live in the reference's multi-block form: the
     full-resolution records split into 16 owned strips (4 x 4, halo 2), each
     strip's processed-window records (halo copies included) replayed by
@@ -574,7 +576,7 @@ def test_640x480_strips_live_group(stub_640):
     from ssla_hip import live as LV
     from ssla_hip.topology import grid_topology
     n = 40_000
-    say(f"640x480 live: {n} edge-blob records over 16 strips, group 6")
+    say(f"640x480 live: {n} edge-blob records over 16 strips, group 6, stages {stages}")
     npz = O.load_npz(stub_640)
     rec = events.edge_blob_records(n, seed=3)
     full = events.to_records(rec)
@@ -599,7 +601,7 @@ def test_640x480_strips_live_group(stub_640):
 
     res = LV.run_replay(stub_640, rings, 0.0, strips=[t.owned for t in topo], speed=1.0,
                         ring_capacity=1 << 14, timing_capacity=1 << 14, expect_p3=expect,
-                        group=6, inspect=inspect)
+                        group=6, stages=stages, inspect=inspect)
     say("640x480 live: status", res.status, "per strip (drained, drift, p50 us):",
         [(s["drained"], s["drop_drift"], round(s["push_to_done_p50"], 1)) for s in res.streams])
     assert res.status == 0 and len(state) == len(topo)
