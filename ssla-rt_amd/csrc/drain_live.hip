@@ -1413,8 +1413,23 @@ __device__ __forceinline__ void group_live_stage_b(LdsG& S, const LiveDesc& d,
         {
             const unsigned long long dl = (unsigned long long)wall_clock64() + gc.wait_ticks;
             bool late = false;
-            for (int w = tid; w < B * kHRec; w += LT) {
-                const unsigned u = (unsigned)xwait(hs + 3 + w, tag, dl, late);
+            // a thread's words are loaded together, then the ones whose tag
+            // has not arrived yet are waited for one by one
+            constexpr int NW = (LB * kHRec + LT - 1) / LT;
+            unsigned long long hv[NW];
+            #pragma unroll
+            for (int i = 0; i < NW; ++i) {
+                const int w = tid + i * LT;
+                hv[i] = w < B * kHRec ? __hip_atomic_load(hs + 3 + w, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT)
+                                      : 0ull;
+            }
+            #pragma unroll
+            for (int i = 0; i < NW; ++i) {
+                const int w = tid + i * LT;
+                if (w >= B * kHRec) continue;
+                if ((unsigned)(hv[i] >> 32) != tag) hv[i] = xwait(hs + 3 + w, tag, dl, late);
+                const unsigned u = (unsigned)hv[i];
                 const int e = w / kHRec, q = w - e * kHRec;
                 if (q == 0) {
                     S.ex[e] = (int)(u & 0xfffu);
