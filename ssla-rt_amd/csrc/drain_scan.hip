@@ -1586,7 +1586,7 @@ __global__ void k_pred_write(const int* __restrict__ n_dev, const int* __restric
 // Output slots (...celled.cuh:1233-1247 conventions) and raw head rows.
 // Output slots (392 B = 49 eight-byte words) and head rows as coalesced
 // 8-byte stores: 32 records per 256-thread workgroup.
-constexpr int kEmitRec = 32;
+constexpr int kEmitRec = 128;
 
 __global__ void __launch_bounds__(256)
 k_emit(int E, const BlockDesc* __restrict__ bd, int nb,
