@@ -465,21 +465,24 @@ def _check_block_preds(preds, version, x, y, own, p3, ref7, owned):
             assert np.abs(preds[c] - ref7[k[-1]]).max() <= HEAD_TOL, c
 
 
-@pytest.mark.parametrize("gpu_blocks,group", [(1, 0), (8, 0), (1, 6), (8, 6)])
-def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks, group):
+@pytest.mark.parametrize("gpu_blocks,group,stages",
+                         [(1, 0, 1), (8, 0, 1), (1, 6, 1), (8, 6, 1), (1, 6, 2), (8, 6, 2)])
+def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks, group, stages):
     """The live configuration as stated: the producer's paced blob source at
     2.0 Mev/s -> 6 host shards for stages 0 + 1 (halo 2) -> fine-grained
     rings -> the persistent kernel, 2 s (orin/hybrid_runner_multi.py:314-754).
     One ownership domain (1 block) and the reference's 8-strip topology,
     one workgroup per block; one domain drained by a group of 6 workgroups
-    (channel slices, exact: no halo); and the 8 strips drained by a group of
-    6 each (48 workgroups).
+    (channel slices, exact: no halo); the 8 strips drained by a group of 6
+    each (48 workgroups); and both with two pipelined groups per block
+    (stages 2: 12 and 96 workgroups).
     Every published record is drained with no overrun, and each ring's
     contents, run through the oracle with that block's ownership, give the
     kernel's pass flags (timing-slot owner flags), tdrop counters, final
     hidden state and prediction grid."""
     from ssla_hip import live as LV
-    say(f"config 2: 2.0 Mev/s, 6 shards, halo 2, 2 s, {gpu_blocks} GPU block(s), group {group}")
+    say(f"config 2: 2.0 Mev/s, 6 shards, halo 2, 2 s, {gpu_blocks} GPU block(s), group {group}, "
+        f"stages {stages}")
     cap = 1 << 19 if gpu_blocks == 1 else 1 << 18
     seen = {}
 
@@ -510,7 +513,7 @@ def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks, group):
 
     r = LV.run_live(stub_dir, rate_mev=2.0, duration_s=2.0, n_shards=6, halo=2,
                     gpu_blocks=gpu_blocks, ring_capacity=cap, timing_capacity=cap,
-                    group=group, inspect=inspect)
+                    group=group, stages=stages, inspect=inspect)
     say(f"config 2: status {r.status}, {r.synth_events} events "
         f"({r.synth_events / r.duration_s / 1e6:.2f} Mev/s achieved), {r.ring_records} ring records, "
         f"{r.drained} drained, {r.output_records} output-producing, "
