@@ -860,6 +860,13 @@ def main() -> int:
                          "events at every phase boundary (each adds a few us of queue time); "
                          "the timed loop records events around the roofline kernel only",
         "roofline": roof,
+        # every single-kernel phase against its own bound, from the per-phase
+        # loop's event times (these include a few us of queue time each)
+        "roofline_by_phase": {
+            k: {x: r[x] for x in ("bound", "achieved", "unit", "frac")}
+            for k, r in ((k, _roofline(per, flops, byts, k)) for k in per
+                         if k not in ("order", "head") and per[k] > 0
+                         and (flops.get(k, 0.0) > 0 or byts.get(k, 0.0) > 0))},
     }
     d.close()
     # The latency and CPU legs run after the timed drain; a failure in one is
