@@ -1107,7 +1107,8 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 // over many workgroups:
 //   A (k_scan_summary) per chunk: the chunk's map h -> Aj h + Bj, composed
 //                      from its (g, v) rows
-//   B (k_scan_carry)   per cell: walks its chunks in order, records each
+//   B (k_scan_carry)   per cell: composes its chunks' maps in order (slots
+//                      of a workgroup over contiguous ranges), records each
 //                      chunk's start state, stores the final state
 //   C (k_scan_apply)   per chunk: replays the chunk from its start state and
 //                      writes h for pairs whose record needs this layer's
@@ -1154,37 +1155,75 @@ k_scan_summary(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
     Bsum[(size_t)j * OUT + c] = B;
 }
 
+// Pass B runs one workgroup of 1024 threads per cell, cut into NW slots of
+// whole waves (one lane per channel).  Slot w takes a contiguous range of the
+// cell's chunks: it composes their maps, publishes the composition in LDS,
+// composes the earlier slots' maps onto the cell's incoming state, then walks
+// its range again storing each chunk's start state.  A cell under a blob holds
+// ~10x the mean number of chunks; a single walk over it set the pass's time.
+constexpr int kCarryThreads = 1024;
+
 template <int OUT>
-__global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
+__global__ void __launch_bounds__(kCarryThreads)
 k_scan_carry(int C, const int* __restrict__ start, const int* __restrict__ end,
              const int* __restrict__ coff, const BlockDesc* __restrict__ bd, int li,
              const float* __restrict__ Asum,
              const float* __restrict__ Bsum, float* __restrict__ Hs) {
+    constexpr int SL = ((OUT + 63) / 64) * 64;     // threads per slot
+    constexpr int NW = kCarryThreads / SL;         // slots per cell
+    __shared__ float sA[NW][OUT], sB[NW][OUT];
     const int k = blockIdx.x;
-    const int c = threadIdx.x;
-    if (c >= OUT || end[k] <= start[k]) return;
+    if (end[k] <= start[k]) return;                // uniform over the workgroup
+    const int w = threadIdx.x / SL, c = threadIdx.x - w * SL;
+    const bool on = c < OUT;
+    const int cc = on ? c : 0;
     const int b = k / C, cell = k % C;
-    float* hp = bd[b].hidden[li] + (size_t)cell * OUT + c;
-    float h = *hp;
+    float* hp = bd[b].hidden[li] + (size_t)cell * OUT + cc;
+    const float h0 = on ? *hp : 0.f;                // read by every slot before the barrier
     const int c0 = coff[k], nc = (end[k] - start[k] + kCH - 1) / kCH;
-    constexpr int U = 32;        // chunks whose maps are in flight together
-    for (int q0 = 0; q0 < nc; q0 += U) {
-        float a[U], b[U];
+    const int L = (nc + NW - 1) / NW;
+    const int qb = min(nc, w * L), qe = min(nc, qb + L);
+    constexpr int U = 16;        // chunks whose maps are in flight together
+    float A = 1.f, B = 0.f;
+    for (int q0 = qb; q0 < qe; q0 += U) {
+        float a[U], bb[U];
         #pragma unroll
         for (int q = 0; q < U; ++q) {
-            const size_t o = (size_t)(c0 + (q0 + q < nc ? q0 + q : q0)) * OUT + c;
+            const size_t o = (size_t)(c0 + (q0 + q < qe ? q0 + q : q0)) * OUT + cc;
             a[q] = gload(Asum + o);
-            b[q] = gload(Bsum + o);
+            bb[q] = gload(Bsum + o);
         }
         #pragma unroll
         for (int q = 0; q < U; ++q) {
-            if (q0 + q < nc) {
-                gstore(Hs + (size_t)(c0 + q0 + q) * OUT + c, h);
-                h = fmaf(a[q], h, b[q]);
+            if (q0 + q < qe) {
+                A *= a[q];
+                B = fmaf(a[q], B, bb[q]);
             }
         }
     }
-    *hp = h;
+    if (on) {
+        sA[w][c] = A;
+        sB[w][c] = B;
+    }
+    __syncthreads();
+    float h = h0;
+    for (int v = 0; v < w; ++v) h = fmaf(sA[v][cc], h, sB[v][cc]);
+    for (int q0 = qb; q0 < qe; q0 += U) {
+        float a[U], bb[U];
+        #pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const size_t o = (size_t)(c0 + (q0 + q < qe ? q0 + q : q0)) * OUT + cc;
+            a[q] = gload(Asum + o);
+            bb[q] = gload(Bsum + o);
+        }
+        #pragma unroll
+        for (int q = 0; q < U; ++q) {
+            if (on && q0 + q < qe) gstore(Hs + (size_t)(c0 + q0 + q) * OUT + c, h);
+            h = q0 + q < qe ? fmaf(a[q], h, bb[q]) : h;
+        }
+    }
+    // the last slot's range ends at the cell's last chunk
+    if (on && w == NW - 1) *hp = h;
 }
 
 template <int OUT, int HS>
@@ -2122,7 +2161,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
     MARK();
-    hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
+    hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(kCarryThreads), 0, st, G.C2, w.pst2, w.pen2,
                        w.coff2, w.bd, 0, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<48, 48>), dim3(w.max_chunks), dim3(64), 0, st,
@@ -2165,7 +2204,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
     MARK();
-    hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(64), 0, st, G.C2, w.pst2, w.pen2,
+    hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(kCarryThreads), 0, st, G.C2, w.pst2, w.pen2,
                        w.coff2, w.bd, 1, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<48, 48>), dim3(w.max_chunks), dim3(64), 0, st,
@@ -2183,7 +2222,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
     MARK();
-    hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
+    hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(kCarryThreads), 0, st, G.C3, w.pst3, w.pen3,
                        w.coff3, w.bd, 2, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<96, 192>), dim3(w.max_chunks), dim3(128), 0, st,
@@ -2200,7 +2239,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
     MARK();
-    hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(128), 0, st, G.C3, w.pst3, w.pen3,
+    hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(kCarryThreads), 0, st, G.C3, w.pst3, w.pen3,
                        w.coff3, w.bd, 3, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<96, 192>), dim3(w.max_chunks), dim3(128), 0, st,
