@@ -1155,13 +1155,24 @@ k_scan_summary(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
     Bsum[(size_t)j * OUT + c] = B;
 }
 
-// Pass B runs one workgroup of 1024 threads per cell, cut into NW slots of
-// whole waves (one lane per channel).  Slot w takes a contiguous range of the
-// cell's chunks: it composes their maps, publishes the composition in LDS,
-// composes the earlier slots' maps onto the cell's incoming state, then walks
-// its range again storing each chunk's start state.  A cell under a blob holds
-// ~10x the mean number of chunks; a single walk over it set the pass's time.
+// Pass B runs one workgroup per cell, cut into NW slots of whole waves (one
+// lane per channel; NW = blockDim / slot size, up to 1024 threads).  Slot w
+// takes a contiguous range of the cell's chunks: it composes their maps,
+// publishes the composition in LDS, composes the earlier slots' maps onto the
+// cell's incoming state, then walks its range again storing each chunk's start
+// state (the last slot's own composition is read by no one: it only walks).
+// At 80x64 a cell under a blob holds ~10x the mean number of chunks and one
+// walk over it set the pass's time; with thousands of cells (640x480, many
+// instances) the cells alone fill the device and one slot per cell is best.
 constexpr int kCarryThreads = 1024;
+
+// Threads per workgroup of the carry pass over `cells` cells with slots of
+// `sl` threads: slots double while the launch stays within ~8 waves per SIMD.
+int carry_threads(int cells, int sl) {
+    int nw = 1;
+    while (2 * nw * sl <= kCarryThreads && (long long)cells * 2 * nw * (sl / 64) <= 8192) nw *= 2;
+    return nw * sl;
+}
 
 template <int OUT>
 __global__ void __launch_bounds__(kCarryThreads)
@@ -1170,8 +1181,8 @@ k_scan_carry(int C, const int* __restrict__ start, const int* __restrict__ end,
              const float* __restrict__ Asum,
              const float* __restrict__ Bsum, float* __restrict__ Hs) {
     constexpr int SL = ((OUT + 63) / 64) * 64;     // threads per slot
-    constexpr int NW = kCarryThreads / SL;         // slots per cell
-    __shared__ float sA[NW][OUT], sB[NW][OUT];
+    __shared__ float sA[kCarryThreads / SL][OUT], sB[kCarryThreads / SL][OUT];
+    const int NW = (int)blockDim.x / SL;           // slots per cell
     const int k = blockIdx.x;
     if (end[k] <= start[k]) return;                // uniform over the workgroup
     const int w = threadIdx.x / SL, c = threadIdx.x - w * SL;
@@ -1185,7 +1196,7 @@ k_scan_carry(int C, const int* __restrict__ start, const int* __restrict__ end,
     const int qb = min(nc, w * L), qe = min(nc, qb + L);
     constexpr int U = 16;        // chunks whose maps are in flight together
     float A = 1.f, B = 0.f;
-    for (int q0 = qb; q0 < qe; q0 += U) {
+    for (int q0 = qb; q0 < (w < NW - 1 ? qe : qb); q0 += U) {
         float a[U], bb[U];
         #pragma unroll
         for (int q = 0; q < U; ++q) {
@@ -2161,7 +2172,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
     MARK();
-    hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(kCarryThreads), 0, st, G.C2, w.pst2, w.pen2,
+    hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(carry_threads(nk2, 64)), 0, st, G.C2, w.pst2, w.pen2,
                        w.coff2, w.bd, 0, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<48, 48>), dim3(w.max_chunks), dim3(64), 0, st,
@@ -2204,7 +2215,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
                        (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
     MARK();
-    hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(kCarryThreads), 0, st, G.C2, w.pst2, w.pen2,
+    hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(carry_threads(nk2, 64)), 0, st, G.C2, w.pst2, w.pen2,
                        w.coff2, w.bd, 1, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<48, 48>), dim3(w.max_chunks), dim3(64), 0, st,
@@ -2222,7 +2233,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
     MARK();
-    hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(kCarryThreads), 0, st, G.C3, w.pst3, w.pen3,
+    hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(carry_threads(nk3, 128)), 0, st, G.C3, w.pst3, w.pen3,
                        w.coff3, w.bd, 2, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<96, 192>), dim3(w.max_chunks), dim3(128), 0, st,
@@ -2239,7 +2250,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
                        (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
     MARK();
-    hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(kCarryThreads), 0, st, G.C3, w.pst3, w.pen3,
+    hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(carry_threads(nk3, 128)), 0, st, G.C3, w.pst3, w.pen3,
                        w.coff3, w.bd, 3, w.Asum, w.Bsum, w.Hs);
     MARK();
     hipLaunchKernelGGL((k_scan_apply<96, 192>), dim3(w.max_chunks), dim3(128), 0, st,
