@@ -1133,7 +1133,7 @@ k_scan_summary(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
     const int s = cbeg[j], e = cend[j];
     const float* row = QVG + (size_t)s * NC + c;           // v at +0, g at +OUT
     float A = 1.f, B = 0.f;
-    constexpr int U = 16;        // pairs whose v, g are in flight together
+    constexpr int U = 32;        // pairs whose v, g are in flight together
     for (int p0 = s; p0 < e; p0 += U, row += U * NC) {
         float v[U], g[U];
         #pragma unroll
@@ -1252,6 +1252,7 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
     const float* row = QVG + (size_t)s * NC + c;
     float* hp = Hout + (size_t)s * HS + c;
     constexpr int U = 16;        // pairs whose v, g are in flight together
+    static_assert(U <= 16, "the need-flag ballot below covers 16 pairs");
     for (int p0 = s; p0 < e; p0 += U, row += U * NC, hp += U * HS) {
         float v[U], g[U];
         #pragma unroll
