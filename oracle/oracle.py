@@ -36,7 +36,8 @@ class OracleLayer(ctypes.Structure):
 class OracleHead(ctypes.Structure):
     _fields_ = [(n, _FP) for n in ("cls_conv_W", "cls_conv_b", "cls_pred_W", "cls_pred_b",
                                    "reg_conv_W", "reg_conv_b", "reg_pred_W", "reg_pred_b",
-                                   "obj_pred_W", "obj_pred_b")] + [("C", ctypes.c_int)]
+                                   "obj_pred_W", "obj_pred_b")] + [("C", ctypes.c_int),
+                                                                   ("lin_W", _FP), ("lin_b", _FP)]
 
 
 class OracleS2S3(ctypes.Structure):
@@ -184,10 +185,29 @@ def fuse_conv_bn(W, b_conv, bn_w, bn_b, bn_mu, bn_var, eps: float = 1e-5):
 
 @dataclass
 class Head:
+    """Either head kind: the two-branch YOLOX head (BN folded, keys
+    cls_conv_W ... obj_pred_b) or the single-linear head (keys lin_W (96, 7)
+    in the device's (IN, OUT) layout and lin_b (7,))."""
     arrays: Dict[str, np.ndarray]
+
+    @classmethod
+    def linear(cls, W, b) -> "Head":
+        W, b = _f32(W), _f32(b)
+        if W.shape != (C3, 7) or b.shape != (7,):
+            raise ValueError("single-linear head needs W (96, 7) and b (7,)")
+        return cls({"lin_W": W, "lin_b": b})
+
+    @property
+    def is_linear(self) -> bool:
+        return "cls_conv_W" not in self.arrays
 
     def c(self) -> OracleHead:
         a = self.arrays
+        if self.is_linear:
+            h = OracleHead()
+            h.C = C3
+            h.lin_W, h.lin_b = _fp(a["lin_W"]), _fp(a["lin_b"])
+            return h
         return OracleHead(*[_fp(a[k]) for k in ("cls_conv_W", "cls_conv_b", "cls_pred_W",
                                                  "cls_pred_b", "reg_conv_W", "reg_conv_b",
                                                  "reg_pred_W", "reg_pred_b", "obj_pred_W",
@@ -378,6 +398,9 @@ def load_ref() -> Optional[ctypes.CDLL]:
     L.ref_lru_step.argtypes = [_FP, _FP, _FP, _FP, _FP, ctypes.c_int]
     L.ref_mm.restype = ctypes.c_int
     L.ref_mm.argtypes = [_FP, ctypes.c_int, ctypes.c_int, _FP, ctypes.c_int, _FP]
+    if hasattr(L, "ref_matvec96x7"):
+        L.ref_matvec96x7.restype = ctypes.c_int
+        L.ref_matvec96x7.argtypes = [_FP, _FP, _FP, _FP]
     if hasattr(L, "ref_oeva_record"):
         L.ref_oeva_record.restype = ctypes.c_int
         L.ref_oeva_record.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int,

@@ -13,6 +13,7 @@
 //   ref_layernorm   openeva::prim::layernorm_ct  vendor/openeva/prim/layernorm.h:40-60
 //   ref_lru_step    openeva::prim::lru_step      vendor/openeva/prim/rnn.h:79-90
 //   ref_mm          openeva::prim::mm            vendor/openeva/prim/matmul.h:22-38
+//   ref_matvec96x7  openeva::prim::matvec_ct<96, 7>  vendor/openeva/prim/linear.h:80-91
 //   ref_oeva_record deploy::OracleRecorder       include/oracle.h:35-89
 //   ref_oeva_diff   deploy::diff_dumps           include/oracle.h:90-150
 #include <cstring>
@@ -24,6 +25,7 @@
 #include "openeva/output.h"
 #include "openeva/heads/async_yolox.h"
 #include "openeva/prim/layernorm.h"
+#include "openeva/prim/linear.h"
 #include "openeva/prim/matmul.h"
 #include "openeva/prim/rnn.h"
 #include "src/weights_loader.h"
@@ -113,6 +115,12 @@ int ref_mm(const float* B, int bo, int bi, const float* A, int ai, float* C) {
     } catch (const std::exception&) {
         return -1;
     }
+}
+
+// y (7) = W x + bias with W (7, 96) row-major (bias may be NULL).
+int ref_matvec96x7(const float* x, const float* W, const float* bias, float* y) {
+    openeva::prim::matvec_ct<96, 7>(x, W, bias, y);
+    return 0;
 }
 
 // Feeds n (event_idx, predictions) pairs to an OracleRecorder(num_anchors,

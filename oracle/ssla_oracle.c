@@ -197,7 +197,21 @@ int oracle_tdrop(uint8_t* counter, int window, int idx) {
  * br) -> reg, obj; output [reg0..3, obj, cls0, cls1]                       */
 /* ------------------------------------------------------------------------ */
 
+/* single-linear head (…celled.cuh:1476-1481): matvec_w<C3, 7>
+ * (proto_layer_pair.cuh:39-58) reads W[i*7 + o], then head_b is added     */
+static void head_linear_f64(const OracleHead* h, const float* x, float out7[7]) {
+    for (int o = 0; o < 7; ++o) {
+        double s = 0.0;
+        for (int i = 0; i < h->C; ++i) s += (double)h->lin_W[(size_t)i * 7 + o] * (double)x[i];
+        out7[o] = (float)(s + (double)h->lin_b[o]);
+    }
+}
+
 void oracle_head_raw_f64(const OracleHead* h, const float* x, float out7[7]) {
+    if (!h->cls_conv_W) {
+        head_linear_f64(h, x, out7);
+        return;
+    }
     const int C = h->C;
     double yc[MAXD], yr[MAXD];
     for (int o = 0; o < C; ++o) {

@@ -19,6 +19,9 @@
  *                              schedule: L4, L5, tdrop_s2, L6, L7, tdrop_s3)
  *   - oracle_head_raw          orin/kernels/ssla_s2_s3_head_celled.cuh:841-902
  *                              (raw [reg4, obj, cls2] of the 2-branch head)
+ *                              and :1462-1500, 1715-1751 (single-linear head:
+ *                              matvec_w<C3, 7> of orin/kernels/
+ *                              proto_layer_pair.cuh:39-58 plus head_b)
  *   - oracle_fuse_conv_bn      orin/orin/hybrid_common.py:327-349
  *   - oracle_s01_run           one producer shard: preprocess
  *                              (src/ssla_kernels.cpp:288-309), stages 0 and 1
@@ -29,7 +32,9 @@
  * Pinning (see tests/): tdrop + schedule by the published P1 pass counts;
  * reshape by the per-position module forward identity; layer_step by the
  * module forward + LayerNorm closed forms; head by the reference's own
- * YOLOX decode compiled into oracle/_ref.
+ * YOLOX decode compiled into oracle/_ref; the single-linear head by one-hot
+ * and zero-feature closed forms (row i of lin_W plus lin_b, lin_b) and the
+ * reference's prim::matvec_ct compiled into oracle/_ref.
  */
 #ifndef SSLA_ORACLE_H
 #define SSLA_ORACLE_H
@@ -56,7 +61,10 @@ typedef struct {
     int K;
 } OracleLayer;
 
-/* Two-branch YOLOX head, BN already folded, PyTorch (out, in) layouts. */
+/* Head of the drain.  Two-branch YOLOX head (BN already folded, PyTorch
+ * (out, in) layouts) when cls_conv_W is set; otherwise the single-linear
+ * head of the reference's persistent kernels (lin_W in the device's
+ * (IN, OUT) = (C, 7) layout):  raw7[o] = lin_b[o] + sum_i lin_W[i*7+o] x[i]. */
 typedef struct {
     const float* cls_conv_W;   /* (C, C)  */
     const float* cls_conv_b;   /* (C,)    */
@@ -69,6 +77,8 @@ typedef struct {
     const float* obj_pred_W;   /* (1, C)  */
     const float* obj_pred_b;   /* (1,)    */
     int C;                     /* 96 */
+    const float* lin_W;        /* (C, 7)  single-linear head, or NULL */
+    const float* lin_b;        /* (7,)    */
 } OracleHead;
 
 /* State of one s2+s3 instance.  H[li] is (Hl*Wl, OUT) fp32, read and
@@ -157,7 +167,8 @@ int oracle_s01_run(OracleS01* st, const float* ev, const uint8_t* owner, int n,
                    int precision, int8_t* pass0, int8_t* pass1, float* feat1,
                    uint16_t* x2, uint16_t* y2);
 
-/* Raw head output [reg0..3, obj, cls0, cls1] for one 96-float feature.   */
+/* Raw head output [reg0..3, obj, cls0, cls1] for one 96-float feature
+ * (either head kind of OracleHead).                                       */
 void oracle_head_raw_f64(const OracleHead* h, const float* x, float out7[7]);
 void oracle_head_raw_f32(const OracleHead* h, const float* x, float out7[7]);
 

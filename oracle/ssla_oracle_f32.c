@@ -112,9 +112,19 @@ void oracle_layer_step_f32(const OracleLayer* L, const float* in,
     layernorm_ct(out, D, L->ln_gamma, L->ln_beta);
 }
 
-/* fp32 head: matvec with bias, SiLU = x * sigmoid(x) (activation.h:19). */
+/* fp32 head: matvec with bias, SiLU = x * sigmoid(x) (activation.h:19);
+ * the single-linear head accumulates in channel order as matvec_w does
+ * (proto_layer_pair.cuh:39-58), then adds head_b (…celled.cuh:1481). */
 void oracle_head_raw_f32(const OracleHead* h, const float* x, float out7[7]) {
     const int C = h->C;
+    if (!h->cls_conv_W) {
+        for (int o = 0; o < 7; ++o) {
+            float s = 0.0f;
+            for (int i = 0; i < C; ++i) s += h->lin_W[(size_t)i * 7 + o] * x[i];
+            out7[o] = s + h->lin_b[o];
+        }
+        return;
+    }
     float yc[MAXD], yr[MAXD];
     for (int o = 0; o < C; ++o) {
         float a = h->cls_conv_b[o], b = h->reg_conv_b[o];

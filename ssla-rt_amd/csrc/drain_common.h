@@ -19,12 +19,47 @@ struct Geometry {
     int window;
 };
 
-// Two-branch YOLOX head, BN folded, (IN, OUT) layouts (ssla_abi.h).
+// Head of a configuration (orin/kernels/ssla_s2_s3_head_celled.cuh:1462-1500,
+// 1715-1751): the two-branch YOLOX head when head_cls_conv_W is set, else
+// the single-linear head raw7 = head_W^T x + head_b when head_W is set,
+// else none.
+enum HeadKind : int { kHeadNone = 0, kHeadYolox = 1, kHeadLinear = 2 };
+
+// Head weights, (IN, OUT) layouts (ssla_abi.h): the two-branch YOLOX head
+// with BN folded, and the single-linear head (lin_W (C3, 7), lin_b (7)).
 struct HeadPtrs {
     const float *cls_conv_W, *cls_conv_b, *cls_pred_W, *cls_pred_b;
     const float *reg_conv_W, *reg_conv_b, *reg_pred_W, *reg_pred_b;
     const float *obj_pred_W, *obj_pred_b;
+    const float *lin_W, *lin_b;
 };
+
+inline int head_kind(const HybridS2S3Config* cfg) {
+    if (cfg->head_cls_conv_W) return kHeadYolox;
+    return cfg->head_W ? kHeadLinear : kHeadNone;
+}
+
+inline HeadPtrs head_ptrs(const HybridS2S3Config* cfg) {
+    return HeadPtrs{cfg->head_cls_conv_W, cfg->head_cls_conv_b, cfg->head_cls_pred_W,
+                    cfg->head_cls_pred_b, cfg->head_reg_conv_W, cfg->head_reg_conv_b,
+                    cfg->head_reg_pred_W, cfg->head_reg_pred_b, cfg->head_obj_pred_W,
+                    cfg->head_obj_pred_b, cfg->head_W, cfg->head_b};
+}
+
+// Which head weights a configuration must have bound for its kind; the
+// message names the first one missing, or is null.
+inline const char* head_missing(const HybridS2S3Config* cfg) {
+    const int k = head_kind(cfg);
+    if (k == kHeadLinear && !cfg->head_b) return "head_W is set but head_b is not";
+    if (k == kHeadYolox) {
+        const float* const need[9] = {cfg->head_cls_conv_b, cfg->head_cls_pred_W, cfg->head_cls_pred_b,
+                                      cfg->head_reg_conv_W, cfg->head_reg_conv_b, cfg->head_reg_pred_W,
+                                      cfg->head_reg_pred_b, cfg->head_obj_pred_W, cfg->head_obj_pred_b};
+        for (const float* p : need)
+            if (!p) return "head_cls_conv_W is set but another two-branch head weight is not";
+    }
+    return nullptr;
+}
 
 __device__ __forceinline__ float sigmoid_fast(float x) {
     return __fdividef(1.0f, 1.0f + __expf(-x));

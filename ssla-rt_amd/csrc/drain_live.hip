@@ -52,7 +52,7 @@ struct LiveWeights {
     LayerWeightsS2S3 L[4];
     PackedWeights pk;       // MFMA fragment-order copies of the layer weights
     HeadPtrs head;
-    int have_head;
+    int have_head;          // HeadKind
 };
 
 // Per-block view of the state, ring and outputs (device memory).
@@ -584,21 +584,13 @@ __device__ __forceinline__ void batch_layer(Lds& S, int B, const unsigned char* 
     mark(S, slot + 3);
 }
 
-// Head of the owned pass-3 records: hidden layers y = SiLU(W x + b) of both
-// branches (one thread per weight column), then the seven outputs
-// [reg0..3, obj, cls0, cls1] (one wave per record) and the prediction grid.
+// Two-branch YOLOX head of the nh records listed in S.ol: hidden layers
+// y = SiLU(W x + b) of both branches (one thread per weight column), then
+// the seven outputs [reg0..3, obj, cls0, cls1] (one wave per record).
 template <class SL>
-__device__ __forceinline__ void batch_head(SL& S, int B, const LiveDesc& d, const LiveWeights& W) {
+__device__ __forceinline__ void batch_head_yolox(SL& S, int nh, const LiveWeights& W) {
     constexpr int C = SSLA_C3;
     const int tid = threadIdx.x;
-    if (tid < 64) {
-        const bool o = tid < B && S.own[tid] && S.p3[tid];
-        const unsigned long long bal = __ballot(o);
-        if (o) S.ol[__popcll(bal & ((1ull << tid) - 1ull))] = tid;
-        if (tid == 0) S.nout = __popcll(bal);
-    }
-    __syncthreads();
-    const int nh = S.nout;
     if (tid < 2 * C) {
         const int br = tid / C, o = tid - br * C;
         const float* Wc = (br == 0 ? W.head.cls_conv_W : W.head.reg_conv_W) + o;
@@ -650,6 +642,48 @@ __device__ __forceinline__ void batch_head(SL& S, int B, const LiveDesc& d, cons
     }
     __syncthreads();
     mark(S, PF_HEADO);
+}
+
+// Head of the owned pass-3 records and the prediction grid.  Two-branch
+// YOLOX head: hidden layers y = SiLU(W x + b) of both branches (one thread
+// per weight column), then the seven outputs [reg0..3, obj, cls0, cls1]
+// (one wave per record).  Single-linear head (...celled.cuh:1476-1481):
+// raw7 = head_W^T x + head_b, one wave per record.
+template <class SL>
+__device__ __forceinline__ void batch_head(SL& S, int B, const LiveDesc& d, const LiveWeights& W) {
+    constexpr int C = SSLA_C3;
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const bool o = tid < B && S.own[tid] && S.p3[tid];
+        const unsigned long long bal = __ballot(o);
+        if (o) S.ol[__popcll(bal & ((1ull << tid) - 1ull))] = tid;
+        if (tid == 0) S.nout = __popcll(bal);
+    }
+    __syncthreads();
+    const int nh = S.nout;
+    if (W.have_head == kHeadLinear) {
+        const int wv = tid >> 6, lane = tid & 63;
+        for (int r = wv; r < nh; r += NW) {
+            const int e = S.ol[r];
+            float part[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int i = lane; i < C; i += 64) {
+                const float x = S.X[e][i];
+                #pragma unroll
+                for (int k = 0; k < 7; ++k) part[k] = fmaf(W.head.lin_W[(size_t)i * 7 + k], x, part[k]);
+            }
+            #pragma unroll
+            for (int k = 0; k < 7; ++k) part[k] = wave_sumf(part[k]);
+            if (lane == 0) {
+                #pragma unroll
+                for (int k = 0; k < 7; ++k) S.H7[e][k] = part[k] + W.head.lin_b[k];
+            }
+        }
+        __syncthreads();
+        mark(S, PF_HEADO);
+    } else {
+        batch_head_yolox(S, nh, W);
+    }
+
     // prediction grid: the last owned pass-3 record of each s3 cell writes
     if (tid < B && S.own[tid] && S.p3[tid]) {
         const int e = tid, c = S.c3[e];
@@ -1350,9 +1384,9 @@ __device__ __forceinline__ bool handoff_put(LdsG& S, unsigned long long* hb, uns
     for (int w = tid; w < B * kHRec; w += LT) {
         const int e = w / kHRec, q = w - e * kHRec;
         unsigned v;
-        if (q == 0)
-            v = (unsigned)S.ex[e] | ((unsigned)S.ey[e] << 12) | ((unsigned)S.vld[e] << 24) |
-                ((unsigned)S.own[e] << 25) | ((unsigned)S.p2[e] << 26);
+        if (q == 0)      // 12-bit s2 coordinates (W2, H2 <= 4096) of valid records only
+            v = (S.vld[e] ? ((unsigned)S.ex[e] & 0xfffu) | (((unsigned)S.ey[e] & 0xfffu) << 12) : 0u) |
+                ((unsigned)S.vld[e] << 24) | ((unsigned)S.own[e] << 25) | ((unsigned)S.p2[e] << 26);
         else if (q == 1) v = (unsigned)S.tpush[e];
         else if (q == 2) v = (unsigned)(S.tpush[e] >> 32);
         else if (q == 3) v = (unsigned)S.temit[e];
@@ -1808,11 +1842,12 @@ static int live_weights(const HybridS2S3Config* cfg, LiveWeights* W, Geometry* G
         return SSLA_ERR_ARG;
     }
     for (int li = 0; li < 4; ++li) W->L[li] = cfg->layers[0][li];
-    W->head = HeadPtrs{cfg->head_cls_conv_W, cfg->head_cls_conv_b, cfg->head_cls_pred_W,
-                       cfg->head_cls_pred_b, cfg->head_reg_conv_W, cfg->head_reg_conv_b,
-                       cfg->head_reg_pred_W, cfg->head_reg_pred_b, cfg->head_obj_pred_W,
-                       cfg->head_obj_pred_b};
-    W->have_head = cfg->head_cls_conv_W != nullptr;
+    if (const char* m = head_missing(cfg)) {
+        set_error(m);
+        return SSLA_ERR_ARG;
+    }
+    W->head = head_ptrs(cfg);
+    W->have_head = head_kind(cfg);
     G->H2 = cfg->H2; G->W2 = cfg->W2; G->H3 = cfg->H3; G->W3 = cfg->W3;
     G->C2 = G->H2 * G->W2; G->C3 = G->H3 * G->W3; G->nb = nb; G->window = cfg->tdrop_window;
     return SSLA_OK;
@@ -1823,7 +1858,7 @@ static void live_desc_state(const HybridS2S3Config* cfg, int b, LiveDesc* d) {
     d->td2 = cfg->tdrop_s2[b];
     d->td3 = cfg->tdrop_s3[b];
     d->strip = cfg->strip[b];
-    const bool head = cfg->head_cls_conv_W != nullptr;
+    const bool head = head_kind(cfg) != kHeadNone;
     d->preds = head ? cfg->preds[b] : nullptr;
     d->version = head ? cfg->version[b] : nullptr;
 }
@@ -2225,6 +2260,10 @@ int live_start(const HybridS2S3Config* cfg, HybridInputRec* const* rings,
     }
     const int nb = cfg->n_blocks;
     if (stages < 1) stages = 1;
+    if (stages > 1 && (cfg->W2 > 4096 || cfg->H2 > 4096)) {
+        set_error("two stages hand s2 coordinates over in 12 bits: W2 and H2 must be <= 4096");
+        return SSLA_ERR_ARG;
+    }
     if (stages > 1 && group <= 1) {
         set_error("two stages need a group (3..6 workgroups per stage)");
         return SSLA_ERR_ARG;

@@ -1608,6 +1608,40 @@ k_head(const int* __restrict__ n_dev, const int* __restrict__ list,
     }
 }
 
+// Single-linear head (...celled.cuh:1476-1481, matvec_w<C3, 7> over
+// head_W (C3, 7) row-major, plus head_b) for pass-3 records: 64 records per
+// workgroup in list order, four threads per record (channels part, part + 4,
+// ...), the quad's partial sums added with two DPP moves.
+__global__ void __launch_bounds__(256)
+k_head_linear(const int* __restrict__ n_dev, const int* __restrict__ list,
+              const float* __restrict__ X, HeadPtrs hp, float* __restrict__ H7) {
+    constexpr int C = SSLA_C3;
+    const int n = *n_dev;
+    const int base = blockIdx.x * kTM;
+    if (base >= n) return;
+    const int j = base + (threadIdx.x >> 2), part = threadIdx.x & 3;
+    const bool on = j < n;
+    const int g = on ? list[j] : 0;
+    float o[7];
+    #pragma unroll
+    for (int k = 0; k < 7; ++k) o[k] = 0.f;
+    if (on) {
+        const float* x = X + (size_t)g * C;
+        for (int i = part; i < C; i += 4) {
+            const float xi = x[i];
+            #pragma unroll
+            for (int k = 0; k < 7; ++k) o[k] = fmaf(hp.lin_W[(size_t)i * 7 + k], xi, o[k]);
+        }
+    }
+    #pragma unroll
+    for (int k = 0; k < 7; ++k) o[k] = quad_sum(o[k]);
+    if (on && part == 0) {
+        float* out = H7 + (size_t)g * 7;
+        #pragma unroll
+        for (int k = 0; k < 7; ++k) out[k] = o[k] + hp.lin_b[k];
+    }
+}
+
 __global__ void k_pred_write(const int* __restrict__ n_dev, const int* __restrict__ list,
                              const unsigned char* __restrict__ owner,
                              const uint32_t* __restrict__ key3_by_g,
@@ -1985,7 +2019,12 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     G.H2 = cfg->H2; G.W2 = cfg->W2; G.H3 = cfg->H3; G.W3 = cfg->W3;
     G.C2 = G.H2 * G.W2; G.C3 = G.H3 * G.W3; G.nb = nb; G.window = cfg->tdrop_window;
     const uint32_t nk2 = (uint32_t)(nb * G.C2), nk3 = (uint32_t)(nb * G.C3);
-    const bool have_head = cfg->head_cls_conv_W != nullptr;
+    const int head = head_kind(cfg);
+    const bool have_head = head != kHeadNone;
+    if (const char* m = head_missing(cfg)) {
+        set_error(m);
+        return SSLA_ERR_ARG;
+    }
 
     std::lock_guard<std::mutex> lock(g_ws_mu);
     if (E == 0) return SSLA_OK;
@@ -2264,12 +2303,13 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     HIPCHK(hipGetLastError());
     // ---- head ------------------------------------------------------------------
     if (have_head) {
-        HeadPtrs hp{cfg->head_cls_conv_W, cfg->head_cls_conv_b, cfg->head_cls_pred_W,
-                    cfg->head_cls_pred_b, cfg->head_reg_conv_W, cfg->head_reg_conv_b,
-                    cfg->head_reg_pred_W, cfg->head_reg_pred_b, cfg->head_obj_pred_W,
-                    cfg->head_obj_pred_b};
-        hipLaunchKernelGGL(k_head, dim3(tilesE), dim3(256), 0, st, (const int*)(w.counts + 1),
-                           w.list3, w.X4, hp, w.H7);
+        const HeadPtrs hp = head_ptrs(cfg);
+        if (head == kHeadYolox)
+            hipLaunchKernelGGL(k_head, dim3(tilesE), dim3(256), 0, st, (const int*)(w.counts + 1),
+                               w.list3, w.X4, hp, w.H7);
+        else
+            hipLaunchKernelGGL(k_head_linear, dim3(tilesE), dim3(256), 0, st,
+                               (const int*)(w.counts + 1), w.list3, w.X4, hp, w.H7);
         hipLaunchKernelGGL(k_pred_write, dim3(grid1(E, 256)), dim3(256), 0, st,
                            (const int*)(w.counts + 1), w.list3, w.owner, w.key3g, w.last3,
                            w.cnt3, w.bd, G, w.H7);

@@ -59,10 +59,11 @@ class LayerWeightsS2S3(ctypes.Structure):
                 ("qvgIn", "goW", "input_proj", "ln_gamma", "ln_beta")]
 
 
-_HEAD_FIELDS = ("head_cls_conv_W", "head_cls_conv_b", "head_cls_pred_W",
-                "head_cls_pred_b", "head_reg_conv_W", "head_reg_conv_b",
-                "head_reg_pred_W", "head_reg_pred_b", "head_obj_pred_W",
-                "head_obj_pred_b")
+# pointers of the two-branch YOLOX head in HybridS2S3Config
+HEAD_FIELDS = ("head_cls_conv_W", "head_cls_conv_b", "head_cls_pred_W",
+               "head_cls_pred_b", "head_reg_conv_W", "head_reg_conv_b",
+               "head_reg_pred_W", "head_reg_pred_b", "head_obj_pred_W",
+               "head_obj_pred_b")
 
 
 class HybridS2S3Config(ctypes.Structure):
@@ -80,7 +81,7 @@ class HybridS2S3Config(ctypes.Structure):
         ("tdrop_s3", ctypes.c_void_p * MAX_BLOCKS),
         ("head_W", ctypes.c_void_p),
         ("head_b", ctypes.c_void_p),
-    ] + [(n, ctypes.c_void_p) for n in _HEAD_FIELDS] + [
+    ] + [(n, ctypes.c_void_p) for n in HEAD_FIELDS] + [
         ("preds", ctypes.c_void_p * MAX_BLOCKS),
         ("version", ctypes.c_void_p * MAX_BLOCKS),
         ("timing", ctypes.c_void_p * MAX_BLOCKS),

@@ -112,6 +112,20 @@ def device_layouts(p: PackedLayer):
     return qvg, go, ip
 
 
+# ---- single-linear head (orin/orin/hybrid_common.py:313-325) ---------------------
+
+def build_head_weights(rng: np.random.Generator, head_out_dim: int = abi.HEAD_OUT):
+    """Random single-linear head in the draw order of the reference's
+    build_head_weights: head_W (96, head_out_dim) ~ N(0, 0.1), in the
+    device's (IN, OUT) layout (the kernel reads head_W[i*7 + o]), then
+    head_b (head_out_dim,) ~ N(0, 0.1).  The reference's live runner uses it
+    for weight directories without head keys (orin/hybrid_runner_multi.py:
+    395-423), its legacy runner always (orin/hybrid_runner.py:294-304)."""
+    W = rng.normal(scale=0.1, size=(96, head_out_dim)).astype(np.float32)
+    b = rng.normal(scale=0.1, size=(head_out_dim,)).astype(np.float32)
+    return W, b
+
+
 # ---- the drain ---------------------------------------------------------------
 
 class Drain:
@@ -126,14 +140,20 @@ class Drain:
         self._rings: List[Optional[DeviceBuffer]] = []
         self._outs: List[Optional[DeviceBuffer]] = []
         self._heads: List[Optional[DeviceBuffer]] = []
+        self._linear_head: Optional[tuple] = None
 
     # -- construction ---------------------------------------------------------
     @classmethod
     def from_weights_dir(cls, weights_dir: str, n_blocks: int = 1,
                          with_preds: bool = True,
-                         strips: Optional[Sequence[tuple]] = None) -> "Drain":
+                         strips: Optional[Sequence[tuple]] = None,
+                         linear_head: Optional[tuple] = None) -> "Drain":
         """strips: per block (x_lo, x_hi, y_lo, y_hi) owned s2 box (e.g.
-        topology.grid_topology(...)[b].owned); default the whole grid."""
+        topology.grid_topology(...)[b].owned); default the whole grid.
+        linear_head: (head_W (96, 7), head_b (7,)) bound when the directory has
+        no head keys, as the reference's live runner falls back to a
+        single-linear head (orin/hybrid_runner_multi.py:395-423); e.g.
+        build_head_weights(np.random.default_rng(seed))."""
         d = cls()
         L = lib.load()
         lib.check(L.ssla_hip_model_load(weights_dir.encode(), ctypes.byref(d._model)), "model_load")
@@ -149,10 +169,42 @@ class Drain:
         for b in range(n_blocks):
             lib.check(L.ssla_hip_state_alloc(ctypes.byref(d.cfg), b), "state_alloc")
             d._state_blocks.append(b)
-            if with_preds and d.cfg.head_cls_conv_W:
-                lib.check(L.ssla_hip_preds_alloc(ctypes.byref(d.cfg), b), "preds_alloc")
-                d._pred_blocks.append(b)
+        if linear_head is not None and not d.cfg.head_cls_conv_W:
+            d.bind_linear_head(*linear_head, with_preds=with_preds)
+        elif with_preds and d.cfg.head_cls_conv_W:
+            d.alloc_preds()
         return d
+
+    def alloc_preds(self) -> None:
+        """Prediction grids (preds, version) of every block that has none."""
+        L = lib.load()
+        for b in range(self.cfg.n_blocks):
+            if b not in self._pred_blocks:
+                lib.check(L.ssla_hip_preds_alloc(ctypes.byref(self.cfg), b), "preds_alloc")
+                self._pred_blocks.append(b)
+
+    def bind_linear_head(self, W: np.ndarray, b: np.ndarray, with_preds: bool = True) -> None:
+        """Binds the single-linear head (cfg.head_W (96, 7), cfg.head_b (7,),
+        orin/kernels/ssla_s2_s3_head_celled.cuh:1476-1481) in place of any
+        two-branch head, and allocates the prediction grids."""
+        W = np.ascontiguousarray(W, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        if W.shape != (96, abi.HEAD_OUT) or b.shape != (abi.HEAD_OUT,):
+            raise ValueError("bind_linear_head: head_W must be (96, 7) and head_b (7,)")
+        bw, bb = DeviceBuffer.from_array(W), DeviceBuffer.from_array(b)
+        self._owned += [bw, bb]
+        c = self.cfg
+        for f in abi.HEAD_FIELDS:
+            setattr(c, f, None)
+        c.head_W, c.head_b = bw.ptr, bb.ptr
+        self._linear_head = (W.copy(), b.copy())
+        if with_preds:
+            self.alloc_preds()
+
+    @property
+    def linear_head(self) -> Optional[tuple]:
+        """(head_W, head_b) host copies of a bound single-linear head."""
+        return self._linear_head
 
     @classmethod
     def from_packed(cls, layers: Sequence[PackedLayer], H2: int, W2: int, window: int,
@@ -228,6 +280,8 @@ class Drain:
     def zero_row(self) -> np.ndarray:
         """The head's raw output for an all-zero feature (the value of a cell
         no record has reached yet in the CPU pipeline)."""
+        if self._linear_head is not None:
+            return self._linear_head[1].copy()
         if not self._model:
             raise lib.SslaHipError("zero_row: no model loaded (random layers have no head)")
         x = np.zeros(96, np.float32)

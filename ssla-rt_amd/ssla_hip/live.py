@@ -25,7 +25,7 @@ from typing import Callable, Dict, Optional
 import numpy as np
 
 from . import abi, lib
-from .hybrid import Drain, HostRings, LiveDrain
+from .hybrid import Drain, HostRings, LiveDrain, build_head_weights
 from .producer import S01gAPI
 from .topology import grid_topology
 
@@ -159,7 +159,10 @@ def run_live(weights_dir: str, rate_mev: float = 2.0, duration_s: float = 8.0, n
     info = model_info(weights_dir)
     topo = grid_topology(gpu_blocks, info.W2, info.H2)
     nb = len(topo)
-    drain = Drain.from_weights_dir(weights_dir, n_blocks=nb, strips=[t.owned for t in topo])
+    # a directory without head keys gets the reference runner's random
+    # single-linear head from the run's seed (hybrid_runner_multi.py:395-423)
+    drain = Drain.from_weights_dir(weights_dir, n_blocks=nb, strips=[t.owned for t in topo],
+                                   linear_head=build_head_weights(np.random.default_rng(seed)))
     rings = HostRings(nb, ring_capacity)
     prod = S01gAPI()
     live = None
@@ -278,7 +281,7 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
                pin_core: Optional[int] = None, profile: bool = True, expect_p3=None,
                drain_timeout_s: float = 60.0, strips=None,
                speed: Optional[float] = None, group: int = 0, stages: int = 1,
-               inspect: Optional[Callable] = None) -> ReplayResult:
+               inspect: Optional[Callable] = None, seed: int = 1) -> ReplayResult:
     """Several rings live on one GPU: pre-built ring records (one array per
     ring) replayed into one ring each, one persistent workgroup per ring.
     Independent streams: rate_per_stream records/s each, round-robin.  One
@@ -289,12 +292,14 @@ def run_replay(weights_dir: str, streams, rate_per_stream: float, ring_capacity:
     time).  expect_p3 (optional, one flag array per ring) gives each ring's
     drop drift: records whose timing-slot owner flag differs from it.
     inspect(drain), when given, is called once the kernel has stopped and
-    before the state is freed.  group and stages as in run_live."""
+    before the state is freed.  group and stages as in run_live; a weight
+    directory without head keys gets a random single-linear head from seed."""
     from .producer import Replay
     nb = len(streams)
     if pin_core is None:
         pin_core, _ = pick_cores(1)
-    drain = Drain.from_weights_dir(weights_dir, n_blocks=nb, strips=strips)
+    drain = Drain.from_weights_dir(weights_dir, n_blocks=nb, strips=strips,
+                                   linear_head=build_head_weights(np.random.default_rng(seed)))
     rings = HostRings(nb, ring_capacity)
     live = rp = None
     try:

@@ -99,3 +99,14 @@ def trained_dir(tmp_path_factory):
     make_trained_checkpoint(d / "model.ckpt")
     convert.convert(str(d / "model.ckpt"), str(d / "weights"), h=64, w=80)
     return str(d / "weights")
+
+
+@pytest.fixture(scope="session")
+def headless_dir(tmp_path_factory):
+    """Stub weight directory at 80x64, seed 1, tdrop 4 with no head keys
+    (make_ssla_stub --num-head-levels 0): the layers equal stub_dir's, and
+    the reference's live runner falls back to a single-linear head."""
+    from ssla_hip import stub
+    d = tmp_path_factory.mktemp("stub_80x64_headless")
+    stub.write_stub(str(d), height=64, width=80, seed=1, tdrop=4, num_head_levels=0)
+    return str(d)

@@ -121,6 +121,45 @@ def test_live_group_single_stream(H, stub_dir, stub_npz, group, stages):
         rings.free()
 
 
+@pytest.mark.parametrize("group,stages", [(0, 1), (6, 1), (6, 2)])
+def test_live_off_grid_records(H, stub_dir, stub_npz, group, stages):
+    """Records outside the s2 grid in the live drains, including the two-
+    stage hand-off: x = W2, x = 4095, y = 4096 and 0xFFFF (whose bits would
+    reach the hand-off's flag bits if the coordinates were not masked).  They
+    change no state and produce nothing; the rest equals the oracle, which
+    skips such records."""
+    n = 3000
+    say("live off-grid records", group, stages, n)
+    rec = events.blob_records(n, seed=17)
+    bad = [(20, 3), (4095, 10), (5, 4096), (5, 0xFFFF), (0xFFFF, 0xFFFF), (19, 16)]
+    idx = np.arange(11, n, 37)
+    for k, i in enumerate(idx):
+        rec.x[i], rec.y[i] = bad[k % len(bad)]
+    recs = events.to_records(rec)
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        d.alloc_timing(4096)
+        rings = H.HostRings(1, capacity=1024)
+        live = H.LiveDrain(d, rings, idle_timeout_ms=15000, group=group, stages=stages)
+        try:
+            _produce(rings, 0, recs)
+            _wait_done(rings, 0, n)
+        finally:
+            status = live.stop()
+        assert status == 0 and int(rings.done[0]) == n
+        st, p2, p3, feat, ref7 = oracle_run(stub_npz, rec)
+        assert np.all(p2[idx] == -2)
+        ts = d.timing(0)[:n]
+        assert np.array_equal(ts["owner"], (p3 == 1).astype(np.uint32))
+        for li in range(4):
+            assert hidden_close(d.hidden(0, li), st.H[li]), li
+        td2, td3 = d.counters(0)
+        assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3)
+        check_preds(*d.preds(0), rec, p3, ref7)
+        say(f"off-grid: {idx.size} records outside the grid, group {group} stages {stages}: "
+            "state and predictions match")
+        rings.free()
+
+
 @pytest.mark.parametrize("group", [0, 6])
 def test_clock_handshake(H, stub_dir, group):
     """The live kernels answer the host's clock ping with their wall clock:
