@@ -96,11 +96,18 @@ def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20, chunk=64):
         "L7.proj": F * (N2 * C3 + S3p * 2 * C3),
         "L7.out": F * (S3pp * C3 + 2 * N3 * C3),
     }
-    # scan passes: summary reads v, g; carry touches each chunk's map and
-    # start state; apply reads v, g and writes h where consumed
+    # the recurrence h = sigmoid(g) h + v over every pair entering the layer:
+    # it must read each pair's v, g once and write h where the output is
+    # consumed.  s2 layers: one launch (k_scan, in the apply slot) does
+    # exactly that.  s3 layers: the summary pass reads v, g; carry touches
+    # each chunk's map and start state; apply reads v, g again and writes h.
     for L, pairs, need, out in (("L4", S2, S2, C2), ("L5", S2, S2p, C2),
                                 ("L6", S3p, S3p, C3), ("L7", S3p, S3pp, C3)):
         chunks = pairs / chunk
+        if out == C2:
+            byts[f"{L}.apply"] = F * (pairs * 2 * out + need * out)
+            flops[f"{L}.apply"] = 6.0 * pairs * out
+            continue
         byts[f"{L}.sum"] = F * (pairs * 2 * out + chunks * 2 * out)
         byts[f"{L}.carry"] = F * chunks * 3 * out
         byts[f"{L}.apply"] = F * (pairs * 2 * out + need * out + chunks * out)
@@ -295,9 +302,16 @@ def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20, gpu_out=None):
 PHASE_KERNEL = {"order": "ordering kernels", "head": "k_head + k_pred_*", "emit": "k_emit"}
 for _L, (_i, _o) in zip(("L4", "L5", "L6", "L7"), ((C1, C2), (C2, C2), (C2, C3), (C3, C3))):
     PHASE_KERNEL[f"{_L}.proj"] = f"k_qvg<{_i}, {_o}>"
-    PHASE_KERNEL[f"{_L}.sum"] = f"k_scan_summary<{_o}>"
-    PHASE_KERNEL[f"{_L}.carry"] = f"k_scan_carry<{_o}>"
-    PHASE_KERNEL[f"{_L}.apply"] = f"k_scan_apply<{_o}>"
+    if _o == C2:
+        # the s2 layers' recurrence is one launch (k_scan, in the apply slot);
+        # the sum slot holds the wait for its group order, carry nothing
+        PHASE_KERNEL[f"{_L}.sum"] = "(wait for k_group_order)"
+        PHASE_KERNEL[f"{_L}.carry"] = "(none)"
+        PHASE_KERNEL[f"{_L}.apply"] = f"k_scan<{_o}, {_o}>"
+    else:
+        PHASE_KERNEL[f"{_L}.sum"] = f"k_scan_summary<{_o}>"
+        PHASE_KERNEL[f"{_L}.carry"] = f"k_scan_carry<{_o}>"
+        PHASE_KERNEL[f"{_L}.apply"] = f"k_scan_apply<{_o}>"
     PHASE_KERNEL[f"{_L}.out"] = f"k_outt<{_i}, {_o}>"
 RIDGE = PEAK_FP32_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)     # FLOP/B
 

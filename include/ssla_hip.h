@@ -150,9 +150,13 @@ int ssla_hip_drain_n2(const HybridS2S3Config* cfg,
 #define SSLA_DRAIN_PHASES 23
 /* Phase order of SslaHipDrainOpts.phase_ms (one kernel launch each, except
  * 0, 21): 0 ordering (decode, sorts, tdrop decisions, chunk tables); per
- * layer a projection of v, g, the scan summary, carry and apply, then the
+ * layer a projection of v, g, the recurrence in three slots, then the
  * contraction (q, q*h, goW, residual, LayerNorm): L4 1-5, L5 6-10, L6
- * 11-15, L7 16-20; 21 head and prediction grid, 22 output slots. */
+ * 11-15, L7 16-20; 21 head and prediction grid, 22 output slots.  The
+ * recurrence of L6 and L7 is three launches (summary, carry, apply); that
+ * of L4 and L5 is one launch in the third slot (the first holds the wait
+ * for its ticket order, built beside L4's projection; the second is
+ * empty). */
 
 #define SSLA_BATCH_PHASES 32
 /* Slots of the in-kernel batch profile (batch-mode and live drains), summed
@@ -216,7 +220,7 @@ int ssla_hip_drain_batch_noalloc(const HybridS2S3Config* cfg,
                                  void* stream, int sync);
 
 /* The whole-ring drain keeps one workspace per process (device memory
- * sized for the largest call so far; about 4 KB per record).  A call with
+ * sized for the largest call so far; about 9 KB per record).  A call with
  * more records than it holds regrows it, which waits for the previous
  * drain call to finish and frees and allocates device memory.  Call this
  * once up front -- in particular before ssla_hip_persistent_start, while no

@@ -78,7 +78,7 @@ __device__ __forceinline__ int find_block(const BlockDesc* bd, int nb, int g) {
 constexpr int kDecRec = 32;          // records per 256-thread workgroup
 
 // Up to kFills int arrays set to a value each (k_decode's extra blocks).
-constexpr int kFills = 5;
+constexpr int kFills = 6;
 struct FillSet {
     int* p[kFills];
     int n[kFills];
@@ -285,6 +285,7 @@ __global__ void __launch_bounds__(kScanThreads) k_exscan(int n, int* __restrict_
 }
 
 constexpr int kCH = 64;     // pairs per scan chunk
+constexpr int kSG = 4;      // chunks per group (workgroup) of the one-pass scan
 
 // Chunk tables: one wave per key writes its chunks (ckey, cbeg, cend).
 __global__ void __launch_bounds__(256)
@@ -887,7 +888,8 @@ k_s2_tables(int n, int nbr, const uint32_t* __restrict__ keys, const uint32_t* _
             const int* __restrict__ coff, const unsigned char* __restrict__ old,
             const int* __restrict__ off, int window, unsigned char* __restrict__ pass,
             int* __restrict__ list, int* __restrict__ pos, unsigned char* __restrict__ pair_need,
-            int* __restrict__ ckey, int* __restrict__ cbeg, int* __restrict__ cend) {
+            int* __restrict__ ckey, int* __restrict__ cbeg, int* __restrict__ cend,
+            int* __restrict__ ghist, int* __restrict__ gw) {
     if ((int)blockIdx.x >= nbr) {
         const uint32_t k = (blockIdx.x - (unsigned)nbr) * 4u + (threadIdx.x >> 6);
         if (k >= nk) return;
@@ -896,6 +898,11 @@ k_s2_tables(int n, int nbr, const uint32_t* __restrict__ keys, const uint32_t* _
             ckey[c0 + q] = (int)k;
             cbeg[c0 + q] = s0 + q * kCH;
             cend[c0 + q] = min(e, s0 + (q + 1) * kCH);
+        }
+        // the key's groups of the one-pass scan (k_group_order)
+        if ((threadIdx.x & 63) == 0) {
+            const int gc = ((e - s0 + kCH - 1) / kCH + kSG - 1) / kSG;
+            if (gc > 0) gw[k] = atomicAdd(&ghist[gc], 1);
         }
         return;
     }
@@ -1272,6 +1279,285 @@ k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
                 h = fmaf(sigmoid_fast(g[u]), h, v[u]);
                 if ((use >> u) & 1ull) gstore(hp + (size_t)u * HS, h);
             }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// S in one pass (k_scan; the s2 layers L4 and L5): each pair row is read
+// once.  A cell's run of chunks is cut into groups of kSG chunks; one
+// workgroup takes one group, one wave per chunk:
+//   1. each wave loads its chunk's v, g rows into registers (sigmoid(g) in
+//      place) and composes the chunk's map h -> A h + B into LDS;
+//   2. the first wave composes the group's map (SA, SB) in chunk order and
+//      finds the group's start state: the cell's stored state for its first
+//      group, else by looking back over the cell's earlier groups -- the
+//      nearest one whose end state is published, then the maps of the groups
+//      after it, applied forward.  A group publishes its map before it waits
+//      and its end state SA h0 + SB once it has h0, so every state is the same
+//      fixed chain of fmaf's whichever word a reader happens to find: the
+//      results do not depend on timing.  The cell's last group stores the
+//      final state;
+//   3. every wave replays its chunk from registers from its start state and
+//      writes h where the pair's record needs the layer's output.
+// Workgroups draw tickets, and ticket t is glist[t] (k_group_order): every
+// cell's group 0, then every cell's group 1, ...  A group's predecessors in
+// its cell drew earlier tickets (so they have started, and none of them
+// waits for a later group), and they drew them about one rank of groups
+// earlier, so the predecessor has usually published its end state by the
+// time a group looks.  (In cell order a heavy cell's groups all ran at once
+// and waited on each other down the chain: 0.39 ms for L4 against 0.21 ms
+// without the waits.)
+// Published words hold a float and the launch's tag (value | tag << 32)
+// and are stored and loaded with relaxed device-scope atomics: a reader that
+// sees the tag sees the value, with no fence (a release fence would write
+// back the L2).  Every wait is bounded on the wall clock; a wave that runs
+// out raises *err (host memory) and goes on with a zero state.
+// ---------------------------------------------------------------------------
+constexpr int kLB = 4;       // groups looked at per look-back step
+
+__device__ __forceinline__ void sw_put(unsigned long long* p, float v, unsigned tag) {
+    __hip_atomic_store(p, ((unsigned long long)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long sw_get(const unsigned long long* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool sw_ok(unsigned long long x, unsigned tag) {
+    return (unsigned)(x >> 32) == tag;
+}
+__device__ __forceinline__ float sw_val(unsigned long long x) {
+    return __uint_as_float((unsigned)x);
+}
+
+// Start state of the group of rank r > 0 of a cell (channel cc of a lane;
+// `on` marks the lanes that carry a channel).  The cell's group of rank x
+// publishes [end | SA | SB] x OUT words at sw + (slot0 + x kSG) 3 OUT; rank
+// 0 publishes its end state without waiting.
+template <int OUT>
+__device__ float scan_lookback(const unsigned long long* __restrict__ sw, int slot0, int r, int cc,
+                               bool on, unsigned tag, unsigned long long deadline,
+                               int* __restrict__ err) {
+    auto word = [&](int x) { return sw + ((size_t)slot0 + (size_t)x * kSG) * 3 * OUT + cc; };
+    // phase 1: the nearest group whose end state every lane sees
+    int top = r - 1, found = -1;
+    float h = 0.f;
+    for (;;) {
+        unsigned long long x[kLB];
+        #pragma unroll
+        for (int q = 0; q < kLB; ++q) x[q] = sw_get(word(max(top - q, 0)));
+        #pragma unroll
+        for (int q = 0; q < kLB; ++q) {
+            const bool ok = top - q >= 0 && __all(!on || sw_ok(x[q], tag));
+            if (found < 0 && ok) {
+                found = top - q;
+                h = sw_val(x[q]);
+            }
+        }
+        if (found >= 0) break;
+        if (top - kLB >= 0) {
+            top -= kLB;                       // none of these: look further back
+            continue;
+        }
+        if ((unsigned long long)wall_clock64() > deadline) {
+            if (cc == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            return 0.f;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        top = r - 1;                          // start again from the nearest group
+    }
+    // phase 2: the maps of the groups after it, applied forward
+    for (int x0 = found + 1; x0 < r; x0 += kLB) {
+        unsigned long long a[kLB], b[kLB];
+        for (;;) {
+            #pragma unroll
+            for (int q = 0; q < kLB; ++q) {
+                const unsigned long long* p = word(min(x0 + q, r - 1));
+                a[q] = sw_get(p + OUT);
+                b[q] = sw_get(p + 2 * OUT);
+            }
+            bool ok = true;
+            #pragma unroll
+            for (int q = 0; q < kLB; ++q) ok = ok && (x0 + q >= r || (sw_ok(a[q], tag) && sw_ok(b[q], tag)));
+            if (__all(!on || ok)) break;
+            if ((unsigned long long)wall_clock64() > deadline) {
+                if (cc == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                return 0.f;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        #pragma unroll
+        for (int q = 0; q < kLB; ++q)
+            if (x0 + q < r) h = fmaf(sw_val(a[q]), h, sw_val(b[q]));
+    }
+    return h;
+}
+
+// The one-pass scan's ticket order (one workgroup): a cell's run of nc
+// chunks forms gc = ceil(nc / kSG) groups; tickets take every cell's group
+// 0, then every cell's group 1, ..., cells with more groups first.
+// ghist[v] counts the cells with gc = v and gw[k] is cell k's place among
+// them (k_s2_tables).  start[v] = cells with more than v groups (the groups
+// of rank v), base[r] = tickets before rank r; cell k, at place start[gc] +
+// gw[k] of every rank below gc, gets glist[base[r] + start[gc] + gw[k]] =
+// (k, r).  Writes the group count to *n_groups.
+__global__ void __launch_bounds__(kScanThreads)
+k_group_order(int nk, int nv, const int* __restrict__ pst, const int* __restrict__ pen,
+              const int* __restrict__ ghist, const int* __restrict__ gw, int* __restrict__ gstart,
+              int* __restrict__ gbase, int2* __restrict__ glist, int* __restrict__ n_groups) {
+    __shared__ int lds[2 * (kScanThreads / 64)];
+    int carry = 0;
+    for (int r0 = 0; r0 < nv; r0 += kScanRound) {        // start: scan of ghist from the top
+        const int i0 = r0 + (int)threadIdx.x * kScanPer;
+        int v[kScanPer], sum = 0;
+        #pragma unroll
+        for (int q = 0; q < kScanPer; ++q) {
+            v[q] = i0 + q < nv ? ghist[nv - 1 - (i0 + q)] : 0;
+            sum += v[q];
+        }
+        int total;
+        int run = carry + block_exscan(sum, lds, &total);
+        carry += total;
+        #pragma unroll
+        for (int q = 0; q < kScanPer; ++q) {
+            if (i0 + q < nv) gstart[nv - 1 - (i0 + q)] = run;
+            run += v[q];
+        }
+    }
+    __syncthreads();
+    carry = 0;
+    for (int r0 = 0; r0 < nv; r0 += kScanRound) {        // base: prefix of start
+        const int i0 = r0 + (int)threadIdx.x * kScanPer;
+        int v[kScanPer], sum = 0;
+        #pragma unroll
+        for (int q = 0; q < kScanPer; ++q) {
+            v[q] = i0 + q < nv ? gstart[i0 + q] : 0;
+            sum += v[q];
+        }
+        int total;
+        int run = carry + block_exscan(sum, lds, &total);
+        carry += total;
+        #pragma unroll
+        for (int q = 0; q < kScanPer; ++q) {
+            if (i0 + q < nv) gbase[i0 + q] = run;
+            run += v[q];
+        }
+    }
+    if (threadIdx.x == 0) *n_groups = carry;
+    __syncthreads();
+    for (int k = threadIdx.x; k < nk; k += kScanThreads) {
+        const int nc = (pen[k] - pst[k] + kCH - 1) / kCH, gc = (nc + kSG - 1) / kSG;
+        if (gc == 0) continue;
+        const int p = gstart[gc] + gw[k];
+        for (int r = 0; r < gc; ++r) glist[gbase[r] + p] = make_int2(k, r);
+    }
+}
+
+template <int OUT, int HS>
+__global__ void __launch_bounds__(kSG * 64)
+__attribute__((amdgpu_waves_per_eu(3, 8)))
+k_scan(const int* __restrict__ n_groups, int* __restrict__ ticket, unsigned tag,
+       const int2* __restrict__ glist, const int* __restrict__ cbeg, const int* __restrict__ cend,
+       const int* __restrict__ coff, const int* __restrict__ pst, const int* __restrict__ pen, int C,
+       const BlockDesc* __restrict__ bd, int li, const unsigned char* __restrict__ pair_need,
+       const float* __restrict__ QVG, float* __restrict__ Hout, unsigned long long* __restrict__ sw,
+       int* __restrict__ err, unsigned long long wait_ticks) {
+    static_assert(OUT <= 64, "one wave per chunk: a lane per channel");
+    constexpr int NC = 2 * OUT;
+    __shared__ int stk;
+    __shared__ float sA[kSG][OUT], sB[kSG][OUT], sH[kSG][OUT];
+    const int t = threadIdx.x, m = t >> 6, lane = t & 63;   // wave m: chunk m of the group
+    const bool on = lane < OUT;
+    const int cc = on ? lane : 0;
+    if (t == 0) stk = atomicAdd(ticket, 1);
+    __syncthreads();
+    const int gi = stk;
+    if (gi >= *n_groups) return;                  // uniform over the workgroup
+    const int2 kr = glist[gi];
+    const int k = kr.x, r = kr.y;
+    const int nc = (pen[k] - pst[k] + kCH - 1) / kCH;
+    const int slot0 = coff[k];                    // the cell's first chunk
+    const int c0 = slot0 + r * kSG;               // the group's first chunk
+    const int ng = min(kSG, nc - r * kSG);
+    const bool have = m < ng;
+    int s = 0, n = 0;
+    float sg[kCH], vv[kCH];
+    if (have) {
+        s = cbeg[c0 + m];
+        n = cend[c0 + m] - s;
+        // all kCH rows, eight from one base address (their offsets fit the
+        // load's immediate field; a clamped index per row cost a 64-bit
+        // address register per load).  Rows past the chunk's end stay inside
+        // the row buffer (sized for the s3 layers' 2 x 96-float rows) and are
+        // not used.
+        const float* row = QVG + (size_t)s * NC + cc;
+        #pragma unroll
+        for (int q8 = 0; q8 < kCH; q8 += 8) {
+            const float* rb = row + (size_t)q8 * NC;
+            #pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                vv[q8 + q] = __builtin_nontemporal_load(rb + q * NC);
+                sg[q8 + q] = __builtin_nontemporal_load(rb + q * NC + OUT);
+            }
+        }
+        float A = 1.f, B = 0.f;
+        #pragma unroll
+        for (int q = 0; q < kCH; ++q) {
+            sg[q] = sigmoid_fast(sg[q]);
+            if (q < n) {
+                A *= sg[q];
+                B = fmaf(sg[q], B, vv[q]);
+            }
+        }
+        if (on) {
+            sA[m][lane] = A;
+            sB[m][lane] = B;
+        }
+    }
+    __syncthreads();
+    if (m == 0) {
+        const bool last = (r + 1) * kSG >= nc;    // the cell's last group
+        float* hp0 = bd[k / C].hidden[li] + (size_t)(k % C) * OUT + cc;
+        unsigned long long* P = sw + (size_t)c0 * 3 * OUT + cc;
+        float SA = 1.f, SB = 0.f;
+        for (int q = 0; q < ng; ++q) {
+            SB = fmaf(sA[q][cc], SB, sB[q][cc]);
+            SA *= sA[q][cc];
+        }
+        float h0;
+        if (r == 0) {
+            h0 = on ? *hp0 : 0.f;
+        } else {
+            if (!last && on) {
+                sw_put(P + OUT, SA, tag);
+                sw_put(P + 2 * OUT, SB, tag);
+            }
+            h0 = scan_lookback<OUT>(sw, slot0, r, cc, on, tag,
+                                    (unsigned long long)wall_clock64() + wait_ticks, err);
+        }
+        if (on) {
+            const float hend = fmaf(SA, h0, SB);
+            if (last) *hp0 = hend;
+            else sw_put(P, hend, tag);
+        }
+        float h = h0;
+        for (int q = 0; q < ng; ++q) {
+            if (on) sH[q][lane] = h;
+            h = fmaf(sA[q][cc], h, sB[q][cc]);
+        }
+    }
+    __syncthreads();
+    if (!have) return;
+    // replay from the chunk's start state; lane l reads pair s + l's need flag
+    const unsigned long long use =
+        __ballot(lane < n && (!pair_need || pair_need[s + lane]));
+    float h = on ? sH[m][lane] : 0.f;
+    float* hp = Hout + (size_t)s * HS + cc;
+    #pragma unroll
+    for (int q = 0; q < kCH; ++q) {
+        if (q < n) {
+            h = fmaf(sg[q], h, vv[q]);
+            if (on && ((use >> q) & 1ull)) gstore(hp + (size_t)q * HS, h);
         }
     }
 }
@@ -1750,6 +2036,11 @@ struct Workspace {
     int *bh;                                   // radix-sort tile histograms
     unsigned char* old2;                       // s2 counters before the call
     float *Asum, *Bsum, *Hs;
+    unsigned long long* sw;                    // one-pass scan: published words, per group's first chunk
+    int *ghist, *gw, *gstart, *gbase;          // one-pass scan: group order tables
+    int2* glist;                               // one-pass scan: (cell, rank) of every ticket
+    int nv = 0;                                // entries of ghist / gstart / gbase
+    int* scan_err = nullptr;                   // host memory: a one-pass scan wait ran out
     float* trash;                              // sink of the projection's absent rows
     int max_chunks = 0;
     unsigned char *owner, *pass2, *pass3;
@@ -1762,8 +2053,10 @@ struct Workspace {
     hipEvent_t s2_ordered = nullptr;   // s2 tables and pass2 are complete
     hipEvent_t s3_ordered = nullptr;   // s3 tables and pass3 are complete
     hipEvent_t side_done = nullptr;    // the side stream's last work of a call
+    hipEvent_t s2_groups = nullptr;    // the one-pass scan's group order is built
     int bh_ints = 0;
     int cus = 0;                       // compute units of the device
+    int clk_khz = 0;                   // wall-clock (s_memrealtime) rate
     float* packed = nullptr;           // fragment-order weight copies (packed_weight_floats_d)
     // What `packed` was built from: the layer weight pointers and the weight
     // generation (bumped by every library call that may write device memory).
@@ -1774,6 +2067,7 @@ struct Workspace {
 
 std::mutex g_ws_mu;
 Workspace g_ws;
+unsigned g_scan_tag = 0;     // tag of the one-pass scan's last launch (under g_ws_mu)
 
 #define HIPCHK(call)                                                          \
     do {                                                                      \
@@ -1800,6 +2094,9 @@ int ensure_workspace(int E, int nkeys) {
     const int ck = std::max(nkeys, g_ws.cap_keys);
     const size_t P = (size_t)cap * kPatch;
     const size_t mc = P / kCH + (size_t)ck + 1;    // chunk bound: full chunks + one tail per key
+    // a cell's pairs come from distinct records: at most cap, so a cell has at
+    // most cap / (kCH kSG) + 2 groups of the one-pass scan
+    const size_t nv = (size_t)cap / (kCH * kSG) + 3;
     // radix-sort tile histograms: (1 << kRMaxBits) digits x tiles
     const size_t bh = ((size_t)1 << kRMaxBits) * (size_t)((cap + kRTile - 1) / kRTile);
     struct Item { void** dst; size_t bytes; };
@@ -1817,7 +2114,7 @@ int ensure_workspace(int E, int nkeys) {
         {(void**)&w.pos3, sizeof(int) * P},
         {(void**)&w.list2, sizeof(int) * (size_t)cap},
         {(void**)&w.list3, sizeof(int) * (size_t)cap},
-        {(void**)&w.counts, sizeof(int) * 8},
+        {(void**)&w.counts, sizeof(int) * 16},
         {(void**)&w.st2, sizeof(int) * (size_t)ck},
         {(void**)&w.en2, sizeof(int) * (size_t)ck},
         {(void**)&w.st3, sizeof(int) * (size_t)ck},
@@ -1857,6 +2154,12 @@ int ensure_workspace(int E, int nkeys) {
         {(void**)&w.Asum, sizeof(float) * mc * SSLA_C3},
         {(void**)&w.Bsum, sizeof(float) * mc * SSLA_C3},
         {(void**)&w.Hs, sizeof(float) * mc * SSLA_C3},
+        {(void**)&w.sw, sizeof(unsigned long long) * mc * 3 * SSLA_C2},
+        {(void**)&w.ghist, sizeof(int) * nv},
+        {(void**)&w.gstart, sizeof(int) * nv},
+        {(void**)&w.gbase, sizeof(int) * nv},
+        {(void**)&w.gw, sizeof(int) * (size_t)ck},
+        {(void**)&w.glist, sizeof(int2) * (mc / kSG + (size_t)ck + 1)},
         {(void**)&w.trash, sizeof(float) * 4 * 64},
         {(void**)&w.bd, sizeof(BlockDesc) * SSLA_MAX_BLOCKS},
     };
@@ -1869,6 +2172,13 @@ int ensure_workspace(int E, int nkeys) {
         *it.dst = p;
         p += align_up(it.bytes);
     }
+    // no stale word may carry a future launch's tag
+    HIPCHK(hipMemset(w.sw, 0, sizeof(unsigned long long) * mc * 3 * SSLA_C2));
+    w.nv = (int)nv;
+    if (!w.scan_err) {
+        HIPCHK(hipHostMalloc((void**)&w.scan_err, sizeof(int), hipHostMallocCoherent));
+        *w.scan_err = 0;
+    }
     if (!w.bd_host) {
         HIPCHK(hipHostMalloc((void**)&w.bd_host, sizeof(BlockDesc) * SSLA_MAX_BLOCKS,
                              hipHostMallocDefault));
@@ -1877,11 +2187,13 @@ int ensure_workspace(int E, int nkeys) {
         HIPCHK(hipEventCreateWithFlags(&w.s2_ordered, hipEventDisableTiming));
         HIPCHK(hipEventCreateWithFlags(&w.s3_ordered, hipEventDisableTiming));
         HIPCHK(hipEventCreateWithFlags(&w.side_done, hipEventDisableTiming));
+        HIPCHK(hipEventCreateWithFlags(&w.s2_groups, hipEventDisableTiming));
         HIPCHK(hipStreamCreateWithFlags(&w.side, hipStreamNonBlocking));
         HIPCHK(hipMalloc(&w.packed, sizeof(float) * packed_weight_floats_d()));
         int dev = 0;
         HIPCHK(hipGetDevice(&dev));
         HIPCHK(hipDeviceGetAttribute(&w.cus, hipDeviceAttributeMultiprocessorCount, dev));
+        HIPCHK(hipDeviceGetAttribute(&w.clk_khz, hipDeviceAttributeWallClockRate, dev));
     }
     w.base = base;
     w.bytes = total;
@@ -1953,7 +2265,9 @@ int zero_async(void* p, size_t nbytes, hipStream_t st) {
 
 int drain_reserve(const HybridS2S3Config* cfg, int max_records) {
     if (!cfg || cfg->n_blocks < 1 || cfg->n_blocks > SSLA_MAX_BLOCKS || cfg->H2 <= 0 ||
-        cfg->W2 <= 0 || max_records < 0 || (long long)max_records * kPatch > 0x7fffffffLL) {
+        cfg->W2 <= 0 || cfg->H2 > 65535 || cfg->W2 > 65535 || max_records < 0 ||
+        (long long)max_records * kPatch > 0x7fffffffLL ||
+        (long long)cfg->n_blocks * cfg->H2 * cfg->W2 >= 0x7fffffffLL) {
         set_error("drain_reserve: bad configuration or record count");
         return SSLA_ERR_ARG;
     }
@@ -2108,12 +2422,14 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     MARK();
     // per-call fills: run bounds of the s2 keys (k_runs writes those that
     // occur), the list and chunk counters, the prediction-grid writers
+    // one-pass scan: the group-count bound of this call's cells (see ensure_workspace)
+    const int nv2 = E / (kCH * kSG) + 3;
     FillSet f{};
     {
-        int* arr[kFills] = {w.st2, w.en2, w.counts, w.last3, w.cnt3};
-        const int len[kFills] = {(int)nk2, (int)nk2, 8, have_head ? (int)nk3 : 0,
-                                 have_head ? (int)nk3 : 0};
-        const int val[kFills] = {0, 0, 0, -1, 0};
+        int* arr[kFills] = {w.st2, w.en2, w.counts, w.last3, w.cnt3, w.ghist};
+        const int len[kFills] = {(int)nk2, (int)nk2, 16, have_head ? (int)nk3 : 0,
+                                 have_head ? (int)nk3 : 0, nv2};
+        const int val[kFills] = {0, 0, 0, -1, 0, 0};
         for (int i = 0; i < kFills; ++i) {
             f.p[i] = arr[i];
             f.n[i] = len[i];
@@ -2122,7 +2438,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     }
     // ---- decode (and the fills); stable radix sort of the records by s2 key --
     {
-        const int ndec = (int)grid1(E, kDecRec), fblk = (int)grid1(std::max<int>((int)nk2, 8), 256);
+        const int ndec = (int)grid1(E, kDecRec), fblk = (int)grid1(std::max<int>(std::max<int>((int)nk2, 16), nv2), 256);
         hipLaunchKernelGGL(k_decode, dim3(ndec + fblk * kFills), dim3(256), 0, st, E, w.bd, G,
                            w.X0, w.cell2, w.owner, w.ka, w.va, ndec, f, fblk);
     }
@@ -2180,7 +2496,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
         hipLaunchKernelGGL(k_s2_tables, dim3(nbr + grid1(nk2, 4)), dim3(256), 0, st, E, (int)nbr,
                            K2, V2, nk2, G.C2, G.W2, G.H2, w.st2, w.en2, w.pst2, w.pen2, w.coff2,
                            w.old2, w.off2, G.window, w.pass2, w.list2, w.pos2, w.pneed2, w.ckey2,
-                           w.cbeg2, w.cend2);
+                           w.cbeg2, w.cend2, w.ghist, w.gw);
     }
     // The s3 ordering needs only the s2 order, pass2 and the old counters, so
     // it runs on the side stream while L4 and L5 run here; L6 waits for it.
@@ -2205,19 +2521,56 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     const unsigned char* all = nullptr;             // every pair's record needs h
     // L4's and L5's h, compact (pairs, 48), behind their (pairs, 96) rows
     float* const Hc = w.QVG + (size_t)w.cap * kPatch * 2 * SSLA_C2;
+    // S: the recurrence of layer LI over the chunk tables of level LV (2: s2,
+    // 3: s3; n_chunks in counts[NC]), h written at HOUT (rows of HS floats)
+    // where the pair's record needs the output (NEED, or every pair): the
+    // s2 layers in one pass (k_scan, ticket counters counts[4 + LI], group
+    // count counts[6]), the s3 layers in three (summary, carry, apply).
+    const unsigned long long wait_ticks = (unsigned long long)std::max(w.clk_khz, 1) * 500ull;
+#define SCAN3(OUT, HS, LI, LV, NC, NK, CELLS, NEED, HOUT)                                             \
+    do {                                                                                            \
+        hipLaunchKernelGGL((k_scan_summary<OUT>), dim3(chunks3), dim3((OUT + 63) / 64 * 64),        \
+                           0, st, (const int*)(w.counts + NC), w.cbeg##LV, w.cend##LV, w.QVG,       \
+                           w.Asum, w.Bsum);                                                         \
+        MARK();                                                                                     \
+        hipLaunchKernelGGL((k_scan_carry<OUT>), dim3(NK),                                           \
+                           dim3(carry_threads(NK, (OUT + 63) / 64 * 64)), 0, st, CELLS, w.pst##LV,   \
+                           w.pen##LV, w.coff##LV, w.bd, LI, w.Asum, w.Bsum, w.Hs);                  \
+        MARK();                                                                                     \
+        hipLaunchKernelGGL((k_scan_apply<OUT, HS>), dim3(chunks3), dim3((OUT + 63) / 64 * 64),      \
+                           0, st, (const int*)(w.counts + NC), w.cbeg##LV, w.cend##LV, w.Hs, NEED,  \
+                           w.QVG, HOUT);                                                            \
+        MARK();                                                                                     \
+    } while (0)
+#define SCAN1(LI, NEED)                                                                             \
+    do {                                                                                            \
+        unsigned tag_ = ++g_scan_tag;                                                               \
+        if (tag_ == 0) tag_ = ++g_scan_tag;                                                         \
+        MARK();                                                                                     \
+        MARK();                                                                                     \
+        hipLaunchKernelGGL((k_scan<SSLA_C2, SSLA_C2>), dim3(groups2), dim3(kSG * 64), 0, st,        \
+                           (const int*)(w.counts + 6), w.counts + 4 + LI, tag_, w.glist, w.cbeg2,    \
+                           w.cend2, w.coff2, w.pst2, w.pen2, G.C2, w.bd, LI, NEED, w.QVG, Hc, w.sw, \
+                           w.scan_err, wait_ticks);                                                 \
+        MARK();                                                                                     \
+    } while (0)
+    // workgroups of the s3 scan passes: one per chunk, at most 9 E / kCH plus
+    // one per key (a call's own bound, not the workspace's)
+    const unsigned chunks3 = (unsigned)std::min<size_t>((size_t)E * kPatch / kCH + nk3 + 1,
+                                                        (size_t)w.max_chunks);
+    // workgroups of the s2 one-pass scan: one per group (at most one per kSG
+    // chunks plus one per key); those past the group count exit at once
+    const unsigned groups2 = (unsigned)(((size_t)E * kPatch / kCH + nk2 + 1) / kSG + nk2 + 1);
     // ---- L4: 24 -> 48, all records ----------------------------------------
     hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2, true, kTMP>), dim3(gridP4), dim3(256), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, pk.pp[0], w.QVG, w.trash);
+    // [side] the s2 one-pass scan's ticket order, beside L4's projection
+    hipLaunchKernelGGL(k_group_order, dim3(1), dim3(kScanThreads), 0, s3, (int)nk2, nv2, w.pst2,
+                       w.pen2, w.ghist, w.gw, w.gstart, w.gbase, w.glist, w.counts + 6);
+    HIPCHK(hipEventRecord(w.s2_groups, s3));
     MARK();
-    hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
-                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
-    MARK();
-    hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(carry_threads(nk2, 64)), 0, st, G.C2, w.pst2, w.pen2,
-                       w.coff2, w.bd, 0, w.Asum, w.Bsum, w.Hs);
-    MARK();
-    hipLaunchKernelGGL((k_scan_apply<48, 48>), dim3(w.max_chunks), dim3(64), 0, st,
-                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, all, w.QVG, Hc);
-    MARK();
+    HIPCHK(hipStreamWaitEvent(st, w.s2_groups, 0));
+    SCAN1(0, all);
     hipLaunchKernelGGL((k_outt<SSLA_C1, SSLA_C2, 2, 1, 3, SSLA_C2>), dim3(grid1(E, 32)), dim3(64), 0,
                        st, E, (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, Hc, pk.po[0],
                        L[0].ln_gamma, L[0].ln_beta, w.X1);
@@ -2252,15 +2605,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2, true, kTMP>), dim3(gridP5), dim3(256), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, pk.pp[1], w.QVG, w.trash);
     MARK();
-    hipLaunchKernelGGL((k_scan_summary<48>), dim3(w.max_chunks), dim3(64), 0, st,
-                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.QVG, w.Asum, w.Bsum);
-    MARK();
-    hipLaunchKernelGGL((k_scan_carry<48>), dim3(nk2), dim3(carry_threads(nk2, 64)), 0, st, G.C2, w.pst2, w.pen2,
-                       w.coff2, w.bd, 1, w.Asum, w.Bsum, w.Hs);
-    MARK();
-    hipLaunchKernelGGL((k_scan_apply<48, 48>), dim3(w.max_chunks), dim3(64), 0, st,
-                       (const int*)(w.counts + 2), w.cbeg2, w.cend2, w.Hs, w.pneed2, w.QVG, Hc);
-    MARK();
+    SCAN1(1, w.pneed2);
     hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C2, 1, 3, 1, SSLA_C2>), dim3(grid1(E, 16)), dim3(192), 0,
                        st, E, (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, Hc, pk.po[1],
                        L[1].ln_gamma, L[1].ln_beta, w.X2);
@@ -2270,15 +2615,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3, false, kTM, 2>), dim3(tilesE * 2), dim3(256), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, pk.pp[2], w.QVG, w.trash);
     MARK();
-    hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
-                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
-    MARK();
-    hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(carry_threads(nk3, 128)), 0, st, G.C3, w.pst3, w.pen3,
-                       w.coff3, w.bd, 2, w.Asum, w.Bsum, w.Hs);
-    MARK();
-    hipLaunchKernelGGL((k_scan_apply<96, 192>), dim3(w.max_chunks), dim3(128), 0, st,
-                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, all, w.QVG, w.QVG);
-    MARK();
+    SCAN3(96, 192, 2, 3, 3, nk3, G.C3, all, w.QVG);
     hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C3, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, pk.po[2],
                        L[2].ln_gamma, L[2].ln_beta, w.X3);
@@ -2287,15 +2624,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3, false, kTM, 4>), dim3(tilesE * 4), dim3(256), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, pk.pp[3], w.QVG, w.trash);
     MARK();
-    hipLaunchKernelGGL((k_scan_summary<96>), dim3(w.max_chunks), dim3(128), 0, st,
-                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.QVG, w.Asum, w.Bsum);
-    MARK();
-    hipLaunchKernelGGL((k_scan_carry<96>), dim3(nk3), dim3(carry_threads(nk3, 128)), 0, st, G.C3, w.pst3, w.pen3,
-                       w.coff3, w.bd, 3, w.Asum, w.Bsum, w.Hs);
-    MARK();
-    hipLaunchKernelGGL((k_scan_apply<96, 192>), dim3(w.max_chunks), dim3(128), 0, st,
-                       (const int*)(w.counts + 3), w.cbeg3, w.cend3, w.Hs, w.pneed3, w.QVG, w.QVG);
-    MARK();
+    SCAN3(96, 192, 3, 3, 3, nk3, G.C3, w.pneed3, w.QVG);
     hipLaunchKernelGGL((k_outt<SSLA_C3, SSLA_C3, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
                        (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, pk.po[3],
                        L[3].ln_gamma, L[3].ln_beta, w.X4);
@@ -2320,8 +2649,16 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     HIPCHK(hipGetLastError());
     MARK();
 #undef MARK
+#undef SCAN1
+#undef SCAN3
     end.finish();
-    if (sync) HIPCHK(hipStreamSynchronize(st));
+    if (sync) {
+        HIPCHK(hipStreamSynchronize(st));
+        if (__atomic_exchange_n(w.scan_err, 0, __ATOMIC_RELAXED)) {
+            set_error("drain: a wait of the one-pass scan ran out (results are invalid)");
+            return SSLA_ERR_HIP;
+        }
+    }
     if (phase_ms) {
         for (int k = 0; k < SSLA_DRAIN_PHASES; ++k) {
             if (!((pmask >> k) & 1ull) || !ev[k] || !ev[k + 1]) continue;
