@@ -2509,7 +2509,15 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     HIPCHK(hipStreamWaitEvent(s3, w.s2_ordered, 0));
     MARK();
     const LayerWeightsS2S3* L = cfg->layers[0];
-    const unsigned tilesE = grid1(E, kTM);
+    // The pass-2 and pass-3 counts stay on the device; the launches over their
+    // lists are sized by bounds the host has.  A cell's L records in a row take
+    // at most L P / 256 + 2 passes of the tdrop gate, P = ceil(256 / window)
+    // the passing counter values per 256: any 256 consecutive values hold P,
+    // and a shorter run, cut in two by the wrap, at most a1 / w + a2 / w + 2.
+    const long long Pw = G.window <= 1 ? 256 : (256 + G.window - 1) / G.window;
+    const int nmax2 = (int)std::min<long long>(E, ((long long)E * Pw + 255) / 256 + 2LL * nk2);
+    const int nmax3 = (int)std::min<long long>(nmax2, ((long long)nmax2 * Pw + 255) / 256 + 2LL * nk3);
+    const unsigned tiles2 = grid1(nmax2, kTM), tiles3 = grid1(nmax3, kTM);
     // persistent projection grids (80-record tiles loop over the workgroups):
     // measured at 200k records (2500 tiles), L4 is fastest with 6 workgroups
     // per CU, L5 with 5 (both: all resident, about two tiles each); 64-record
@@ -2554,9 +2562,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                            w.scan_err, wait_ticks);                                                 \
         MARK();                                                                                     \
     } while (0)
-    // workgroups of the s3 scan passes: one per chunk, at most 9 E / kCH plus
-    // one per key (a call's own bound, not the workspace's)
-    const unsigned chunks3 = (unsigned)std::min<size_t>((size_t)E * kPatch / kCH + nk3 + 1,
+    // workgroups of the s3 scan passes: one per chunk, at most 9 nmax2 / kCH
+    // plus one per key (a call's own bound, not the workspace's)
+    const unsigned chunks3 = (unsigned)std::min<size_t>((size_t)nmax2 * kPatch / kCH + nk3 + 1,
                                                         (size_t)w.max_chunks);
     // workgroups of the s2 one-pass scan: one per group (at most one per kSG
     // chunks plus one per key); those past the group count exit at once
@@ -2583,10 +2591,10 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL(k_keyscan<false>, dim3(1), dim3(kScanThreads), 0, s3, (int)nk3, w.t3, w.st3,
                        w.en3, (int*)nullptr, (int*)nullptr, w.n3, w.off3, w.counts + 1,
                        KeyHist{});
-    hipLaunchKernelGGL(k_place3, dim3(grid1(E, 256)), dim3(256), 0, s3, (const int*)(w.counts + 0),
+    hipLaunchKernelGGL(k_place3, dim3(grid1(nmax2, 256)), dim3(256), 0, s3, (const int*)(w.counts + 0),
                        w.list2, w.bd, G, w.cell2, w.sidx, V2, w.st2, w.en2, w.old2, w.st3, K3, V3,
                        w.key3g);
-    hipLaunchKernelGGL(k_tdrop3, dim3(grid1(E, 256)), dim3(256), 0, s3, (const int*)(w.counts + 0),
+    hipLaunchKernelGGL(k_tdrop3, dim3(grid1(nmax2, 256)), dim3(256), 0, s3, (const int*)(w.counts + 0),
                        K3, V3, nk3, G.C3, w.st3, w.off3, w.bd, G.window, w.owner,
                        have_head ? 1 : 0, w.pass3, w.list3, w.last3, w.cnt3);
     hipLaunchKernelGGL(k_keys3b, dim3(grid1(nk3, 256)), dim3(256), 0, s3, nk3, G, w.t3, w.bd,
@@ -2596,7 +2604,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (int*)nullptr, KeyHist{});
     hipLaunchKernelGGL(k_chunks, dim3(grid1(nk3, 4)), dim3(256), 0, s3, nk3, w.pst3, w.pen3,
                        w.coff3, w.ckey3, w.cbeg3, w.cend3);
-    hipLaunchKernelGGL(k_pair_rank, dim3(grid1(E, 256)), dim3(256), 0, s3, E,
+    hipLaunchKernelGGL(k_pair_rank, dim3(grid1(nmax2, 256)), dim3(256), 0, s3, E,
                        (const int*)(w.counts + 0), K3, V3, nk3, G.C3, G.W3, G.H3, w.st3, w.en3,
                        w.pst3, w.pos3, w.pneed3, w.pass3);
     HIPCHK(hipEventRecord(w.s3_ordered, s3));
@@ -2606,26 +2614,26 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, pk.pp[1], w.QVG, w.trash);
     MARK();
     SCAN1(1, w.pneed2);
-    hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C2, 1, 3, 1, SSLA_C2>), dim3(grid1(E, 16)), dim3(192), 0,
+    hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C2, 1, 3, 1, SSLA_C2>), dim3(grid1(nmax2, 16)), dim3(192), 0,
                        st, E, (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, Hc, pk.po[1],
                        L[1].ln_gamma, L[1].ln_beta, w.X2);
     MARK();
     // ---- L6: 48 -> 96, pass2 records ------------------------------------------
     HIPCHK(hipStreamWaitEvent(st, w.s3_ordered, 0));
-    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3, false, kTM, 2>), dim3(tilesE * 2), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3, false, kTM, 2>), dim3(tiles2 * 2), dim3(256), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, pk.pp[2], w.QVG, w.trash);
     MARK();
     SCAN3(96, 192, 2, 3, 3, nk3, G.C3, all, w.QVG);
-    hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C3, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
+    hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C3, 1, 3>), dim3(grid1(nmax2, 16)), dim3(192), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, pk.po[2],
                        L[2].ln_gamma, L[2].ln_beta, w.X3);
     MARK();
     // ---- L7: 96 -> 96, state for pass2, output for pass3 ----------------------
-    hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3, false, kTM, 4>), dim3(tilesE * 4), dim3(256), 0, st, E,
+    hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3, false, kTM, 4>), dim3(tiles2 * 4), dim3(256), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, pk.pp[3], w.QVG, w.trash);
     MARK();
     SCAN3(96, 192, 3, 3, 3, nk3, G.C3, w.pneed3, w.QVG);
-    hipLaunchKernelGGL((k_outt<SSLA_C3, SSLA_C3, 1, 3>), dim3(grid1(E, 16)), dim3(192), 0, st, E,
+    hipLaunchKernelGGL((k_outt<SSLA_C3, SSLA_C3, 1, 3>), dim3(grid1(nmax3, 16)), dim3(192), 0, st, E,
                        (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, pk.po[3],
                        L[3].ln_gamma, L[3].ln_beta, w.X4);
     MARK();
@@ -2634,12 +2642,12 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     if (have_head) {
         const HeadPtrs hp = head_ptrs(cfg);
         if (head == kHeadYolox)
-            hipLaunchKernelGGL(k_head, dim3(tilesE), dim3(256), 0, st, (const int*)(w.counts + 1),
+            hipLaunchKernelGGL(k_head, dim3(tiles3), dim3(256), 0, st, (const int*)(w.counts + 1),
                                w.list3, w.X4, hp, w.H7);
         else
-            hipLaunchKernelGGL(k_head_linear, dim3(tilesE), dim3(256), 0, st,
+            hipLaunchKernelGGL(k_head_linear, dim3(tiles3), dim3(256), 0, st,
                                (const int*)(w.counts + 1), w.list3, w.X4, hp, w.H7);
-        hipLaunchKernelGGL(k_pred_write, dim3(grid1(E, 256)), dim3(256), 0, st,
+        hipLaunchKernelGGL(k_pred_write, dim3(grid1(nmax3, 256)), dim3(256), 0, st,
                            (const int*)(w.counts + 1), w.list3, w.owner, w.key3g, w.last3,
                            w.cnt3, w.bd, G, w.H7);
     }
