@@ -57,7 +57,7 @@ def inbounds(x, y, H, W):
     return n
 
 
-def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20, chunk=64):
+def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20):
     """Algorithmic work of each launch of the whole-ring drain: the minimal
     MACs of the reference's skipping semantics (L5 output and L6/L7 only for
     pass2, L7 output and head for pass3) and the bytes each launch must move
@@ -97,23 +97,13 @@ def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20, chunk=64):
         "L7.out": F * (S3pp * C3 + 2 * N3 * C3),
     }
     # the recurrence h = sigmoid(g) h + v over every pair entering the layer:
-    # it must read each pair's v, g once and write h where the output is
-    # consumed.  s2 layers: one launch (k_scan, in the apply slot) does
-    # exactly that.  s3 layers: the summary pass reads v, g; carry touches
-    # each chunk's map and start state; apply reads v, g again and writes h.
+    # one launch (k_scan, in the apply slot) reads each pair's v, g once and
+    # writes h where the output is consumed (sigmoid ~ 4 FLOP, the map
+    # composition and the replay 2 FMA)
     for L, pairs, need, out in (("L4", S2, S2, C2), ("L5", S2, S2p, C2),
                                 ("L6", S3p, S3p, C3), ("L7", S3p, S3pp, C3)):
-        chunks = pairs / chunk
-        if out == C2:
-            byts[f"{L}.apply"] = F * (pairs * 2 * out + need * out)
-            flops[f"{L}.apply"] = 6.0 * pairs * out
-            continue
-        byts[f"{L}.sum"] = F * (pairs * 2 * out + chunks * 2 * out)
-        byts[f"{L}.carry"] = F * chunks * 3 * out
-        byts[f"{L}.apply"] = F * (pairs * 2 * out + need * out + chunks * out)
-        flops[f"{L}.sum"] = 4.0 * pairs * out
-        flops[f"{L}.carry"] = 2.0 * chunks * out
-        flops[f"{L}.apply"] = 4.0 * pairs * out
+        byts[f"{L}.apply"] = F * (pairs * 2 * out + need * out)
+        flops[f"{L}.apply"] = 6.0 * pairs * out
     byts["emit"] = float(N * 392)
     total_mac = sum(mac.values())
     return flops, byts, total_mac
@@ -302,31 +292,61 @@ def cpu_baseline(stub_dir, rec, budget_s=15.0, H2=16, W2=20, gpu_out=None):
 PHASE_KERNEL = {"order": "ordering kernels", "head": "k_head + k_pred_*", "emit": "k_emit"}
 for _L, (_i, _o) in zip(("L4", "L5", "L6", "L7"), ((C1, C2), (C2, C2), (C2, C3), (C3, C3))):
     PHASE_KERNEL[f"{_L}.proj"] = f"k_qvg<{_i}, {_o}>"
-    if _o == C2:
-        # the s2 layers' recurrence is one launch (k_scan, in the apply slot);
-        # the sum slot holds the wait for its group order, carry nothing
-        PHASE_KERNEL[f"{_L}.sum"] = "(wait for k_group_order)"
-        PHASE_KERNEL[f"{_L}.carry"] = "(none)"
-        PHASE_KERNEL[f"{_L}.apply"] = f"k_scan<{_o}, {_o}>"
-    else:
-        PHASE_KERNEL[f"{_L}.sum"] = f"k_scan_summary<{_o}>"
-        PHASE_KERNEL[f"{_L}.carry"] = f"k_scan_carry<{_o}>"
-        PHASE_KERNEL[f"{_L}.apply"] = f"k_scan_apply<{_o}>"
+    # the recurrence is one launch (k_scan, in the apply slot); the sum slot
+    # holds L4's wait for the s2 ticket order (L6's for the s3 one comes
+    # before its projection), carry nothing
+    PHASE_KERNEL[f"{_L}.sum"] = "(wait for k_group_order)" if _L == "L4" else "(none)"
+    PHASE_KERNEL[f"{_L}.carry"] = "(none)"
+    PHASE_KERNEL[f"{_L}.apply"] = f"k_scan<{_o}, {_o if _o == C2 else 2 * _o}>"
     PHASE_KERNEL[f"{_L}.out"] = f"k_outt<{_i}, {_o}>"
 RIDGE = PEAK_FP32_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)     # FLOP/B
 
 
-def hbm_traffic(phase: str):
-    """HBM bytes of the launch `phase` from the committed rocprofv3 PMC
-    summary (FETCH_SIZE x fetch scale + WRITE_SIZE x write scale, scales
-    from a plain copy of known size), or None when absent."""
-    f = ROOT / "profiles" / "drain_80x64_200k_hbm_traffic.json"
+def _profile(name: str):
+    f = ROOT / "profiles" / name
     if not f.exists():
         return None
     try:
-        return json.loads(f.read_text())["launches"][phase]["hbm_bytes"]
-    except (KeyError, ValueError):
+        return json.loads(f.read_text())
+    except ValueError:
         return None
+
+
+def hbm_traffic(phase: str = None):
+    """HBM bytes of the launch `phase` (None: of the whole call) from the
+    committed rocprofv3 PMC summary (FETCH_SIZE x fetch scale + WRITE_SIZE x
+    write scale, scales from a plain copy of known size), or None."""
+    p = _profile("drain_80x64_200k_hbm_traffic.json")
+    if p is None:
+        return None
+    if phase is None:
+        return int(sum(v["hbm_bytes"] for v in p["launches"].values()))
+    return p["launches"].get(phase, {}).get("hbm_bytes")
+
+
+def trace_ms(phase: str):
+    """Average duration (ms) of the launch `phase` in the committed
+    rocprofv3 --kernel-trace summary of the same workload, or None."""
+    p = _profile("drain_80x64_200k_kernel_trace.json")
+    if p is None:
+        return None
+    v = p["launches"].get(phase)
+    return None if v is None else v["avg_ms"]
+
+
+def compulsory_bytes(x, y, p2, H2=16, W2=20):
+    """HBM bytes a drain of these records cannot avoid, in the per-record
+    accounting of the reference's kernel (state kept in HBM, read and
+    written per patch): the 128 B record, the s2 hidden read-modify-write of
+    L4 and L5 (n2 patches x 48 floats x 2 layers x read + write), that of L6
+    and L7 for pass-2 records (n3 patches x 96 floats), the 392 B output
+    slot and the two uint8 counters."""
+    x = x.astype(np.int64)
+    y = y.astype(np.int64)
+    ok = (x < W2) & (y < H2)
+    n2 = np.where(ok, inbounds(x, y, H2, W2), 0)
+    n3 = np.where(p2 == 1, inbounds(x >> 1, y >> 1, H2 >> 1, W2 >> 1), 0)
+    return float(x.size * (128 + 392 + 2) + n2.sum() * 48 * 4 * 2 * 2 + n3.sum() * 96 * 4 * 2 * 2)
 
 
 def _per_batch(phase_us):
@@ -426,13 +446,26 @@ def _roofline(per, flops, byts, dom):
     fl, by = flops.get(dom, 0.0), byts.get(dom, 0.0)
     base = {"kernel": f"{kname} ({dom})", "traffic": traffic, "avg_launch_ms": round(per[dom], 5),
             "algorithmic_bytes_per_launch": int(by), "algorithmic_flops_per_launch": int(fl)}
+    tr = trace_ms(dom)
     if by > 0 and fl / by < RIDGE:
         ach = by / (per[dom] * 1e-3) / 1e9
-        return dict(base, bound="hbm", achieved=round(ach, 2), peak=PEAK_HBM_GBS, unit="GB/s",
-                    frac=round(ach / PEAK_HBM_GBS, 5))
-    ach = fl / (per[dom] * 1e-3) / 1e12
-    return dict(base, bound="mfma", achieved=round(ach, 4), peak=PEAK_FP32_TFLOPS, unit="TFLOP/s",
-                frac=round(ach / PEAK_FP32_TFLOPS, 5))
+        r = dict(base, bound="hbm", achieved=round(ach, 2), peak=PEAK_HBM_GBS, unit="GB/s",
+                 frac=round(ach / PEAK_HBM_GBS, 5))
+        if tr:
+            r["frac_kernel_trace"] = round(by / (tr * 1e-3) / 1e9 / PEAK_HBM_GBS, 5)
+    else:
+        ach = fl / (per[dom] * 1e-3) / 1e12
+        r = dict(base, bound="mfma", achieved=round(ach, 4), peak=PEAK_FP32_TFLOPS,
+                 unit="TFLOP/s", frac=round(ach / PEAK_FP32_TFLOPS, 5))
+        if tr:
+            r["frac_kernel_trace"] = round(fl / (tr * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 5)
+    if tr:
+        r["avg_launch_ms_kernel_trace"] = tr
+    r["frac_note"] = ("frac: avg_launch_ms from HIP events around this launch on the drain's "
+                      "stream over the timed steps; frac_kernel_trace: the launch's average "
+                      "duration in the committed rocprofv3 --kernel-trace summary "
+                      "(profiles/drain_80x64_200k_kernel_trace.json) of the same workload")
+    return r
 
 
 WORKLOADS = {
@@ -557,17 +590,14 @@ def batch_bench(a, d, recs, n, S, steps, warmup, desc, tmp) -> int:
 TRAFFIC_PHASES = {
     "k_qvg<24, 48>": ["L4.proj"], "k_qvg<48, 48>": ["L5.proj"], "k_qvg<48, 96>": ["L6.proj"],
     "k_qvg<96, 96>": ["L7.proj"],
-    "k_scan_summary<48>": ["L4.sum", "L5.sum"], "k_scan_carry<48>": ["L4.carry", "L5.carry"],
-    "k_scan_apply<48>": ["L4.apply", "L5.apply"],
-    "k_scan_summary<96>": ["L6.sum", "L7.sum"], "k_scan_carry<96>": ["L6.carry", "L7.carry"],
-    "k_scan_apply<96>": ["L6.apply", "L7.apply"],
+    "k_scan<48, 48>": ["L4.apply", "L5.apply"], "k_scan<96, 192>": ["L6.apply", "L7.apply"],
     "k_outt<24, 48, 2, 1>": ["L4.out"], "k_outt<48, 48, 1, 3>": ["L5.out"],
     "k_outt<48, 96, 1, 3>": ["L6.out"], "k_outt<96, 96, 1, 3>": ["L7.out"],
-    "k_head": ["head"], "k_pred_write": ["head"], "k_emit": ["emit"],
+    "k_head": ["head"], "k_head_linear": ["head"], "k_pred_write": ["head"], "k_emit": ["emit"],
 }
 ORDER_KERNELS = ("k_decode", "k_rs_hist", "k_exscan", "k_rs_scatter", "k_runs", "k_keys2",
                  "k_keyscan", "k_s2_tables", "k_pair_rank", "k_chunks", "k_keys3a", "k_place3",
-                 "k_tdrop3", "k_keys3b")
+                 "k_tdrop3", "k_keys3b", "k_group_order")
 
 
 def _traffic_key(k: str):
@@ -583,8 +613,9 @@ def _traffic_key(k: str):
 
 
 def _kname(n: str) -> str:
-    n = n.replace("ssla::(anonymous namespace)::", "").replace("ssla::", "").replace("void ", "")
-    return re.sub(r"\(.*", "", n).strip()
+    m = n.replace("ssla::(anonymous namespace)::", "").replace("ssla::", "").replace("void ", "")
+    m = re.sub(r"\(.*", "", m).strip()
+    return m or n.strip() or "(unnamed)"
 
 
 def pmc_summary(fetch_dir, write_dir, cfetch_dir, cwrite_dir, copy_bytes, command):
@@ -628,6 +659,35 @@ def pmc_summary(fetch_dir, write_dir, cfetch_dir, cwrite_dir, copy_bytes, comman
         res["launches"][ph] = {"fetch_bytes": int(f), "write_bytes": int(w),
                                "hbm_bytes": int(f + w)}
     return res
+
+
+def trace_summary(trace_dir, command):
+    """Per-launch average durations of the whole-ring drain from a rocprofv3
+    --kernel-trace run of bench.py (kernel_trace.csv), with the kernel ->
+    launch mapping of the PMC summary (a kernel launched twice per call
+    belongs to its two layers in turn)."""
+    import collections
+    import csv
+    import glob
+    f = glob.glob(f"{trace_dir}/**/*kernel_trace.csv", recursive=True)[0]
+    rs = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Dispatch_Id"]))
+    seen, tot, cnt = collections.Counter(), collections.defaultdict(float), collections.Counter()
+    for r in rs:
+        k = _kname(r["Kernel_Name"])
+        key = _traffic_key(k)
+        if key is None or k.split("<")[0] in ORDER_KERNELS:
+            continue
+        ph = TRAFFIC_PHASES[key]
+        lab = ph[seen[key] % len(ph)]
+        if lab == "head":                         # two kernels: kept apart
+            lab += ":" + k.split("<")[0]
+        seen[key] += 1
+        tot[lab] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-6
+        cnt[lab] += 1
+    return {"command": command,
+            "workload": "bench.py defaults: 200,000 ring records at 80x64, stub weights seed 1",
+            "launches": {k: {"launches": cnt[k], "avg_ms": round(tot[k] / cnt[k], 5)}
+                         for k in sorted(tot)}}
 
 
 def stats_summary(csv_path, title, workload, command, calls_note, top=30):
@@ -746,9 +806,18 @@ def main() -> int:
     ap.add_argument("--stats-summary", nargs=5,
                     metavar=("CSV", "TITLE", "WORKLOAD", "COMMAND", "CALLS"),
                     help="print a markdown table of a rocprofv3 kernel_stats.csv")
+    ap.add_argument("--trace-summary", metavar="TRACE_DIR",
+                    help="print per-launch average durations (JSON) from a rocprofv3 "
+                         "--kernel-trace output directory of bench.py")
     ap.add_argument("--sq-summary", nargs=2, metavar=("PASS_A", "PASS_B"),
                     help="print per-kernel SQ metrics from the two rocprofv3 --pmc passes")
     a = ap.parse_args()
+    if a.trace_summary:
+        print(json.dumps(trace_summary(a.trace_summary,
+                                       "rocprofv3 --kernel-trace --stats -f csv -d <dir> -- python3 "
+                                       "bench.py --steps 5 --warmup 1 --no-live --no-cpu-baseline"),
+                         indent=1))
+        return 0
     if a.sq_summary:
         print(sq_summary(*a.sq_summary))
         return 0
@@ -857,7 +926,9 @@ def main() -> int:
                                         "rows_576B_permuted": round(ceil[2], 1)}
         roof["frac_of_write_ceiling"] = round(roof["achieved"] / ceil[0], 4)
     whole = 2.0 * total_mac / (ms_step * 1e-3) / 1e12
-    hbm = sum(byts.values()) / (ms_step * 1e-3) / 1e9
+    iface = sum(byts.values())
+    comp = sum(compulsory_bytes(r.x, r.y, o["pass2"], H2, W2) for r, o in zip(recs, outs))
+    measured = hbm_traffic() if a.workload == "80x64" else None
     res = {
         "metric": METRIC, "value": round(value, 3), "unit": "kev/s", "n_gpus": 1,
         "steps": steps, "warmup": warmup, "ms_per_step": round(ms_step, 4),
@@ -868,7 +939,16 @@ def main() -> int:
         "ring_record_kev_s": round(ring_rate, 2),
         "latency_us": None,
         "whole_drain_tflops": round(whole, 4),
-        "whole_drain_algorithmic_hbm_gbs": round(hbm, 1),
+        # HBM bytes per call: the compulsory ones (records, hidden-state RMW
+        # per patch, output slots, counters) against what rocprofv3 measured
+        # for this build (committed PMC summary; 80x64 workload only)
+        "compulsory_hbm_bytes": int(comp),
+        "measured_hbm_bytes": measured,
+        "measured_over_compulsory": round(measured / comp, 3) if measured else None,
+        "whole_drain_compulsory_hbm_gbs": round(comp / (ms_step * 1e-3) / 1e9, 1),
+        # the bytes every launch moves at its interface, including the design's
+        # own intermediates (pair rows, h rows, chunk maps): not compulsory
+        "whole_drain_launch_interface_gbs": round(iface / (ms_step * 1e-3) / 1e9, 1),
         "phase_ms": {k: round(v, 5) for k, v in per.items()},
         "phase_ms_note": "HIP-event time per phase from an extra loop of the same steps with "
                          "events at every phase boundary (each adds a few us of queue time); "
@@ -876,6 +956,9 @@ def main() -> int:
         "roofline": roof,
         # every single-kernel phase against its own bound, from the per-phase
         # loop's event times (these include a few us of queue time each)
+        "roofline_by_phase_note": "per launch against its bound; HBM-bound entries are rates on "
+                                  "the launch's interface bytes, which include the design's own "
+                                  "intermediates (pair rows, h rows, chunk maps)",
         "roofline_by_phase": {
             k: {x: r[x] for x in ("bound", "achieved", "unit", "frac")}
             for k, r in ((k, _roofline(per, flops, byts, k)) for k in per

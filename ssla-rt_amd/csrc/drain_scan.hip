@@ -78,7 +78,7 @@ __device__ __forceinline__ int find_block(const BlockDesc* bd, int nb, int g) {
 constexpr int kDecRec = 32;          // records per 256-thread workgroup
 
 // Up to kFills int arrays set to a value each (k_decode's extra blocks).
-constexpr int kFills = 6;
+constexpr int kFills = 7;
 struct FillSet {
     int* p[kFills];
     int n[kFills];
@@ -285,13 +285,15 @@ __global__ void __launch_bounds__(kScanThreads) k_exscan(int n, int* __restrict_
 }
 
 constexpr int kCH = 64;     // pairs per scan chunk
-constexpr int kSG = 4;      // chunks per group (workgroup) of the one-pass scan
+constexpr int kSG = 4;      // chunks per group (workgroup) of the one-pass scan, s2 layers
+constexpr int kSG3 = 2;     // ... s3 layers (two waves per chunk)
 
-// Chunk tables: one wave per key writes its chunks (ckey, cbeg, cend).
+// Chunk tables: one wave per key writes its chunks (ckey, cbeg, cend) and
+// counts the key's groups of the one-pass scan (ghist, gw: k_group_order).
 __global__ void __launch_bounds__(256)
 k_chunks(uint32_t nk, const int* __restrict__ start, const int* __restrict__ end,
          const int* __restrict__ coff, int* __restrict__ ckey, int* __restrict__ cbeg,
-         int* __restrict__ cend) {
+         int* __restrict__ cend, int* __restrict__ ghist, int* __restrict__ gw) {
     const uint32_t k = blockIdx.x * 4u + (threadIdx.x >> 6);
     if (k >= nk) return;
     const int s = start[k], e = end[k], c0 = coff[k];
@@ -299,6 +301,10 @@ k_chunks(uint32_t nk, const int* __restrict__ start, const int* __restrict__ end
         ckey[c0 + q] = (int)k;
         cbeg[c0 + q] = s + q * kCH;
         cend[c0 + q] = min(e, s + (q + 1) * kCH);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        const int gc = ((e - s + kCH - 1) / kCH + kSG3 - 1) / kSG3;
+        if (gc > 0) gw[k] = atomicAdd(&ghist[gc], 1);
     }
 }
 
@@ -1110,204 +1116,36 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 
 // ---------------------------------------------------------------------------
 // S: the per-cell recurrence h = sigmoid(g) h + v over a cell's pairs in ring
-// order.  A cell's run is cut into chunks of kCH pairs so the work spreads
-// over many workgroups:
-//   A (k_scan_summary) per chunk: the chunk's map h -> Aj h + Bj, composed
-//                      from its (g, v) rows
-//   B (k_scan_carry)   per cell: composes its chunks' maps in order (slots
-//                      of a workgroup over contiguous ranges), records each
-//                      chunk's start state, stores the final state
-//   C (k_scan_apply)   per chunk: replays the chunk from its start state and
-//                      writes h for pairs whose record needs this layer's
-//                      output: rows of HS floats at Hout -- in place of v
-//                      (Hout = the pair rows, HS = 2 OUT) for L6 and L7, a
-//                      compact (pairs, OUT) array behind the rows for L4 and
-//                      L5, whose contractions gather h 10% faster from it
-// One lane per channel in all three passes.  Passes A and C read the v, g
-// rows with nontemporal loads: the rows are read once per pass and the
-// projection has just left up to 0.7 GB of them in the caches; streaming
-// them past the L2 made pass A 35-40% faster and pass C 2-9%.
-// ---------------------------------------------------------------------------
-template <int OUT>
-__global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
-k_scan_summary(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
-               const int* __restrict__ cend, const float* __restrict__ QVG,
-               float* __restrict__ Asum, float* __restrict__ Bsum) {
-    constexpr int NC = 2 * OUT;
-    const int j = blockIdx.x;
-    const int c = threadIdx.x;
-    if (j >= *n_chunks || c >= OUT) return;
-    const int s = cbeg[j], e = cend[j];
-    const float* row = QVG + (size_t)s * NC + c;           // v at +0, g at +OUT
-    float A = 1.f, B = 0.f;
-    constexpr int U = 32;        // pairs whose v, g are in flight together
-    for (int p0 = s; p0 < e; p0 += U, row += U * NC) {
-        float v[U], g[U];
-        #pragma unroll
-        for (int q = 0; q < U; ++q) {
-            const int k = p0 + q < e ? q : 0;
-            v[q] = __builtin_nontemporal_load(row + (size_t)k * NC);
-            g[q] = __builtin_nontemporal_load(row + (size_t)k * NC + OUT);
-        }
-        #pragma unroll
-        for (int q = 0; q < U; ++q) {
-            if (p0 + q < e) {
-                const float a = sigmoid_fast(g[q]);
-                A *= a;
-                B = fmaf(a, B, v[q]);
-            }
-        }
-    }
-    Asum[(size_t)j * OUT + c] = A;
-    Bsum[(size_t)j * OUT + c] = B;
-}
-
-// Pass B runs one workgroup per cell, cut into NW slots of whole waves (one
-// lane per channel; NW = blockDim / slot size, up to 1024 threads).  Slot w
-// takes a contiguous range of the cell's chunks: it composes their maps,
-// publishes the composition in LDS, composes the earlier slots' maps onto the
-// cell's incoming state, then walks its range again storing each chunk's start
-// state (the last slot's own composition is read by no one: it only walks).
-// At 80x64 a cell under a blob holds ~10x the mean number of chunks and one
-// walk over it set the pass's time; with thousands of cells (640x480, many
-// instances) the cells alone fill the device and one slot per cell is best.
-constexpr int kCarryThreads = 1024;
-
-// Threads per workgroup of the carry pass over `cells` cells with slots of
-// `sl` threads: slots double while the launch stays within ~8 waves per SIMD.
-int carry_threads(int cells, int sl) {
-    int nw = 1;
-    while (2 * nw * sl <= kCarryThreads && (long long)cells * 2 * nw * (sl / 64) <= 8192) nw *= 2;
-    return nw * sl;
-}
-
-template <int OUT>
-__global__ void __launch_bounds__(kCarryThreads)
-k_scan_carry(int C, const int* __restrict__ start, const int* __restrict__ end,
-             const int* __restrict__ coff, const BlockDesc* __restrict__ bd, int li,
-             const float* __restrict__ Asum,
-             const float* __restrict__ Bsum, float* __restrict__ Hs) {
-    constexpr int SL = ((OUT + 63) / 64) * 64;     // threads per slot
-    __shared__ float sA[kCarryThreads / SL][OUT], sB[kCarryThreads / SL][OUT];
-    const int NW = (int)blockDim.x / SL;           // slots per cell
-    const int k = blockIdx.x;
-    if (end[k] <= start[k]) return;                // uniform over the workgroup
-    const int w = threadIdx.x / SL, c = threadIdx.x - w * SL;
-    const bool on = c < OUT;
-    const int cc = on ? c : 0;
-    const int b = k / C, cell = k % C;
-    float* hp = bd[b].hidden[li] + (size_t)cell * OUT + cc;
-    const float h0 = on ? *hp : 0.f;                // read by every slot before the barrier
-    const int c0 = coff[k], nc = (end[k] - start[k] + kCH - 1) / kCH;
-    const int L = (nc + NW - 1) / NW;
-    const int qb = min(nc, w * L), qe = min(nc, qb + L);
-    constexpr int U = 16;        // chunks whose maps are in flight together
-    float A = 1.f, B = 0.f;
-    for (int q0 = qb; q0 < (w < NW - 1 ? qe : qb); q0 += U) {
-        float a[U], bb[U];
-        #pragma unroll
-        for (int q = 0; q < U; ++q) {
-            const size_t o = (size_t)(c0 + (q0 + q < qe ? q0 + q : q0)) * OUT + cc;
-            a[q] = gload(Asum + o);
-            bb[q] = gload(Bsum + o);
-        }
-        #pragma unroll
-        for (int q = 0; q < U; ++q) {
-            if (q0 + q < qe) {
-                A *= a[q];
-                B = fmaf(a[q], B, bb[q]);
-            }
-        }
-    }
-    if (on) {
-        sA[w][c] = A;
-        sB[w][c] = B;
-    }
-    __syncthreads();
-    float h = h0;
-    for (int v = 0; v < w; ++v) h = fmaf(sA[v][cc], h, sB[v][cc]);
-    for (int q0 = qb; q0 < qe; q0 += U) {
-        float a[U], bb[U];
-        #pragma unroll
-        for (int q = 0; q < U; ++q) {
-            const size_t o = (size_t)(c0 + (q0 + q < qe ? q0 + q : q0)) * OUT + cc;
-            a[q] = gload(Asum + o);
-            bb[q] = gload(Bsum + o);
-        }
-        #pragma unroll
-        for (int q = 0; q < U; ++q) {
-            if (on && q0 + q < qe) gstore(Hs + (size_t)(c0 + q0 + q) * OUT + c, h);
-            h = q0 + q < qe ? fmaf(a[q], h, bb[q]) : h;
-        }
-    }
-    // the last slot's range ends at the cell's last chunk
-    if (on && w == NW - 1) *hp = h;
-}
-
-template <int OUT, int HS>
-__global__ void __launch_bounds__(((OUT + 63) / 64) * 64)
-k_scan_apply(const int* __restrict__ n_chunks, const int* __restrict__ cbeg,
-             const int* __restrict__ cend, const float* __restrict__ Hs,
-             const unsigned char* __restrict__ pair_need,
-             const float* __restrict__ QVG, float* __restrict__ Hout) {
-    constexpr int NC = 2 * OUT;
-    const int j = blockIdx.x;
-    const int c = threadIdx.x;
-    if (j >= *n_chunks || c >= OUT) return;
-    const int s = cbeg[j], e = cend[j];
-    float h = Hs[(size_t)j * OUT + c];
-    const float* row = QVG + (size_t)s * NC + c;
-    float* hp = Hout + (size_t)s * HS + c;
-    constexpr int U = 16;        // pairs whose v, g are in flight together
-    static_assert(U <= 16, "the need-flag ballot below covers 16 pairs");
-    for (int p0 = s; p0 < e; p0 += U, row += U * NC, hp += U * HS) {
-        float v[U], g[U];
-        #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int k = p0 + u < e ? u : 0;
-            v[u] = __builtin_nontemporal_load(row + (size_t)k * NC);
-            g[u] = __builtin_nontemporal_load(row + (size_t)k * NC + OUT);
-        }
-        // lane l of the wave reads pair p0 + l % 16's flag; bit u of the
-        // ballot is pair p0 + u's (lanes 0..15 are active in every wave)
-        const int kf = p0 + (c & 15);
-        const unsigned long long use =
-            __ballot(kf < e && (!pair_need || pair_need[kf]));
-        #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (p0 + u < e) {
-                h = fmaf(sigmoid_fast(g[u]), h, v[u]);
-                if ((use >> u) & 1ull) gstore(hp + (size_t)u * HS, h);
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// S in one pass (k_scan; the s2 layers L4 and L5): each pair row is read
-// once.  A cell's run of chunks is cut into groups of kSG chunks; one
-// workgroup takes one group, one wave per chunk:
-//   1. each wave loads its chunk's v, g rows into registers (sigmoid(g) in
-//      place) and composes the chunk's map h -> A h + B into LDS;
-//   2. the first wave composes the group's map (SA, SB) in chunk order and
-//      finds the group's start state: the cell's stored state for its first
-//      group, else by looking back over the cell's earlier groups -- the
-//      nearest one whose end state is published, then the maps of the groups
-//      after it, applied forward.  A group publishes its map before it waits
-//      and its end state SA h0 + SB once it has h0, so every state is the same
-//      fixed chain of fmaf's whichever word a reader happens to find: the
-//      results do not depend on timing.  The cell's last group stores the
-//      final state;
+// order, in one pass (k_scan): each pair's v, g row is read once.  A cell's
+// run is cut into chunks of kCH pairs and its chunks into groups (kSG = 4 at
+// s2, kSG3 = 2 at s3); one workgroup takes one group, one wave per chunk and
+// 64 channels (two waves for the 96 channels of L6 and L7):
+//   1. each wave loads its chunk's rows into registers (sigmoid(g) in place,
+//      nontemporal loads: the projection has just left up to 0.7 GB of rows
+//      in the caches) and composes the chunk's map h -> A h + B into LDS;
+//   2. the first chunk's waves compose the group's map (SA, SB) in chunk
+//      order and find the group's start state: the cell's stored state for
+//      its first group, else by looking back over the cell's earlier groups
+//      -- the nearest one whose end state is published, then the maps of the
+//      groups after it, applied forward.  A group publishes its map before it
+//      waits and its end state SA h0 + SB once it has h0, so every state is
+//      the same fixed chain of fmaf's whichever word a reader happens to
+//      find: the results do not depend on timing.  The cell's last group
+//      stores the final state;
 //   3. every wave replays its chunk from registers from its start state and
-//      writes h where the pair's record needs the layer's output.
+//      writes h where the pair's record needs the layer's output (L4, L5: a
+//      compact (pairs, 48) array behind the rows, which their contractions
+//      gather 10% faster; L6, L7: over v in place).
 // Workgroups draw tickets, and ticket t is glist[t] (k_group_order): every
 // cell's group 0, then every cell's group 1, ...  A group's predecessors in
 // its cell drew earlier tickets (so they have started, and none of them
-// waits for a later group), and they drew them about one rank of groups
-// earlier, so the predecessor has usually published its end state by the
-// time a group looks.  (In cell order a heavy cell's groups all ran at once
-// and waited on each other down the chain: 0.39 ms for L4 against 0.21 ms
-// without the waits.)
+// waits for a later group), and about one rank of groups earlier, so the
+// predecessor has usually published its end state by the time a group
+// looks.  Measured at 200k records against the three passes it replaced
+// (summary, per-cell carry, apply): L4 0.32 -> 0.26 ms, L5 0.28 -> 0.21,
+// L6 0.14 -> 0.14, L7 0.125 -> 0.12; in cell order a cell's groups all ran at
+// once and waited on each other down the chain (L4 0.39 ms).  One chunk per
+// group at s3 (0.14, 0.13 ms), two or eight at s2 (0.27, 0.31 ms) were slower.
 // Published words hold a float and the launch's tag (value | tag << 32)
 // and are stored and loaded with relaxed device-scope atomics: a reader that
 // sees the tag sees the value, with no fence (a release fence would write
@@ -1334,11 +1172,11 @@ __device__ __forceinline__ float sw_val(unsigned long long x) {
 // `on` marks the lanes that carry a channel).  The cell's group of rank x
 // publishes [end | SA | SB] x OUT words at sw + (slot0 + x kSG) 3 OUT; rank
 // 0 publishes its end state without waiting.
-template <int OUT>
+template <int OUT, int SG>
 __device__ float scan_lookback(const unsigned long long* __restrict__ sw, int slot0, int r, int cc,
                                bool on, unsigned tag, unsigned long long deadline,
                                int* __restrict__ err) {
-    auto word = [&](int x) { return sw + ((size_t)slot0 + (size_t)x * kSG) * 3 * OUT + cc; };
+    auto word = [&](int x) { return sw + ((size_t)slot0 + (size_t)x * SG) * 3 * OUT + cc; };
     // phase 1: the nearest group whose end state every lane sees
     int top = r - 1, found = -1;
     float h = 0.f;
@@ -1401,11 +1239,15 @@ __device__ float scan_lookback(const unsigned long long* __restrict__ sw, int sl
 // of rank v), base[r] = tickets before rank r; cell k, at place start[gc] +
 // gw[k] of every rank below gc, gets glist[base[r] + start[gc] + gw[k]] =
 // (k, r).  Writes the group count to *n_groups.
+constexpr int kGroupLds = 6144;    // start / base entries k_group_order keeps in LDS
+
 __global__ void __launch_bounds__(kScanThreads)
-k_group_order(int nk, int nv, const int* __restrict__ pst, const int* __restrict__ pen,
+k_group_order(int nk, int nv, int sg, const int* __restrict__ pst, const int* __restrict__ pen,
               const int* __restrict__ ghist, const int* __restrict__ gw, int* __restrict__ gstart,
               int* __restrict__ gbase, int2* __restrict__ glist, int* __restrict__ n_groups) {
     __shared__ int lds[2 * (kScanThreads / 64)];
+    __shared__ int sst[kGroupLds], sba[kGroupLds];
+    const bool inl = nv <= kGroupLds;      // else the tables are read from global memory
     int carry = 0;
     for (int r0 = 0; r0 < nv; r0 += kScanRound) {        // start: scan of ghist from the top
         const int i0 = r0 + (int)threadIdx.x * kScanPer;
@@ -1420,7 +1262,11 @@ k_group_order(int nk, int nv, const int* __restrict__ pst, const int* __restrict
         carry += total;
         #pragma unroll
         for (int q = 0; q < kScanPer; ++q) {
-            if (i0 + q < nv) gstart[nv - 1 - (i0 + q)] = run;
+            const int i = nv - 1 - (i0 + q);
+            if (i0 + q < nv) {
+                gstart[i] = run;
+                if (inl) sst[i] = run;
+            }
             run += v[q];
         }
     }
@@ -1431,7 +1277,7 @@ k_group_order(int nk, int nv, const int* __restrict__ pst, const int* __restrict
         int v[kScanPer], sum = 0;
         #pragma unroll
         for (int q = 0; q < kScanPer; ++q) {
-            v[q] = i0 + q < nv ? gstart[i0 + q] : 0;
+            v[q] = i0 + q < nv ? (inl ? sst[i0 + q] : gstart[i0 + q]) : 0;
             sum += v[q];
         }
         int total;
@@ -1439,22 +1285,27 @@ k_group_order(int nk, int nv, const int* __restrict__ pst, const int* __restrict
         carry += total;
         #pragma unroll
         for (int q = 0; q < kScanPer; ++q) {
-            if (i0 + q < nv) gbase[i0 + q] = run;
+            if (i0 + q < nv) {
+                gbase[i0 + q] = run;
+                if (inl) sba[i0 + q] = run;
+            }
             run += v[q];
         }
     }
     if (threadIdx.x == 0) *n_groups = carry;
     __syncthreads();
+    const int* st = inl ? sst : gstart;
+    const int* ba = inl ? sba : gbase;
     for (int k = threadIdx.x; k < nk; k += kScanThreads) {
-        const int nc = (pen[k] - pst[k] + kCH - 1) / kCH, gc = (nc + kSG - 1) / kSG;
+        const int nc = (pen[k] - pst[k] + kCH - 1) / kCH, gc = (nc + sg - 1) / sg;
         if (gc == 0) continue;
-        const int p = gstart[gc] + gw[k];
-        for (int r = 0; r < gc; ++r) glist[gbase[r] + p] = make_int2(k, r);
+        const int p = st[gc] + gw[k];
+        for (int r = 0; r < gc; ++r) glist[ba[r] + p] = make_int2(k, r);
     }
 }
 
-template <int OUT, int HS>
-__global__ void __launch_bounds__(kSG * 64)
+template <int OUT, int HS, int SG>
+__global__ void __launch_bounds__(SG * ((OUT + 63) / 64) * 64)
 __attribute__((amdgpu_waves_per_eu(3, 8)))
 k_scan(const int* __restrict__ n_groups, int* __restrict__ ticket, unsigned tag,
        const int2* __restrict__ glist, const int* __restrict__ cbeg, const int* __restrict__ cend,
@@ -1462,13 +1313,15 @@ k_scan(const int* __restrict__ n_groups, int* __restrict__ ticket, unsigned tag,
        const BlockDesc* __restrict__ bd, int li, const unsigned char* __restrict__ pair_need,
        const float* __restrict__ QVG, float* __restrict__ Hout, unsigned long long* __restrict__ sw,
        int* __restrict__ err, unsigned long long wait_ticks) {
-    static_assert(OUT <= 64, "one wave per chunk: a lane per channel");
+    constexpr int WPC = (OUT + 63) / 64;          // waves per chunk (64 channels each)
     constexpr int NC = 2 * OUT;
     __shared__ int stk;
-    __shared__ float sA[kSG][OUT], sB[kSG][OUT], sH[kSG][OUT];
-    const int t = threadIdx.x, m = t >> 6, lane = t & 63;   // wave m: chunk m of the group
-    const bool on = lane < OUT;
-    const int cc = on ? lane : 0;
+    __shared__ float sA[SG][OUT], sB[SG][OUT], sH[SG][OUT];
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int m = w / WPC;                        // the wave's chunk in the group
+    const int c = (w % WPC) * 64 + lane;          // the lane's channel
+    const bool on = c < OUT;
+    const int cc = on ? c : 0;
     if (t == 0) stk = atomicAdd(ticket, 1);
     __syncthreads();
     const int gi = stk;
@@ -1477,8 +1330,8 @@ k_scan(const int* __restrict__ n_groups, int* __restrict__ ticket, unsigned tag,
     const int k = kr.x, r = kr.y;
     const int nc = (pen[k] - pst[k] + kCH - 1) / kCH;
     const int slot0 = coff[k];                    // the cell's first chunk
-    const int c0 = slot0 + r * kSG;               // the group's first chunk
-    const int ng = min(kSG, nc - r * kSG);
+    const int c0 = slot0 + r * SG;               // the group's first chunk
+    const int ng = min(SG, nc - r * SG);
     const bool have = m < ng;
     int s = 0, n = 0;
     float sg[kCH], vv[kCH];
@@ -1488,8 +1341,8 @@ k_scan(const int* __restrict__ n_groups, int* __restrict__ ticket, unsigned tag,
         // all kCH rows, eight from one base address (their offsets fit the
         // load's immediate field; a clamped index per row cost a 64-bit
         // address register per load).  Rows past the chunk's end stay inside
-        // the row buffer (sized for the s3 layers' 2 x 96-float rows) and are
-        // not used.
+        // the row buffer (kCH rows of padding past the largest row count) and
+        // are not used.
         const float* row = QVG + (size_t)s * NC + cc;
         #pragma unroll
         for (int q8 = 0; q8 < kCH; q8 += 8) {
@@ -1510,13 +1363,13 @@ k_scan(const int* __restrict__ n_groups, int* __restrict__ ticket, unsigned tag,
             }
         }
         if (on) {
-            sA[m][lane] = A;
-            sB[m][lane] = B;
+            sA[m][c] = A;
+            sB[m][c] = B;
         }
     }
     __syncthreads();
-    if (m == 0) {
-        const bool last = (r + 1) * kSG >= nc;    // the cell's last group
+    if (w < WPC) {                                // the first chunk's waves chain the group
+        const bool last = (r + 1) * SG >= nc;    // the cell's last group
         float* hp0 = bd[k / C].hidden[li] + (size_t)(k % C) * OUT + cc;
         unsigned long long* P = sw + (size_t)c0 * 3 * OUT + cc;
         float SA = 1.f, SB = 0.f;
@@ -1532,7 +1385,7 @@ k_scan(const int* __restrict__ n_groups, int* __restrict__ ticket, unsigned tag,
                 sw_put(P + OUT, SA, tag);
                 sw_put(P + 2 * OUT, SB, tag);
             }
-            h0 = scan_lookback<OUT>(sw, slot0, r, cc, on, tag,
+            h0 = scan_lookback<OUT, SG>(sw, slot0, r, cc, on, tag,
                                     (unsigned long long)wall_clock64() + wait_ticks, err);
         }
         if (on) {
@@ -1542,7 +1395,7 @@ k_scan(const int* __restrict__ n_groups, int* __restrict__ ticket, unsigned tag,
         }
         float h = h0;
         for (int q = 0; q < ng; ++q) {
-            if (on) sH[q][lane] = h;
+            if (on) sH[q][c] = h;
             h = fmaf(sA[q][cc], h, sB[q][cc]);
         }
     }
@@ -1551,7 +1404,7 @@ k_scan(const int* __restrict__ n_groups, int* __restrict__ ticket, unsigned tag,
     // replay from the chunk's start state; lane l reads pair s + l's need flag
     const unsigned long long use =
         __ballot(lane < n && (!pair_need || pair_need[s + lane]));
-    float h = on ? sH[m][lane] : 0.f;
+    float h = on ? sH[m][c] : 0.f;
     float* hp = Hout + (size_t)s * HS + cc;
     #pragma unroll
     for (int q = 0; q < kCH; ++q) {
@@ -2035,14 +1888,14 @@ struct Workspace {
     int *off2, *off3;                          // first pass-2 / pass-3 list slot of every key
     int *bh;                                   // radix-sort tile histograms
     unsigned char* old2;                       // s2 counters before the call
-    float *Asum, *Bsum, *Hs;
     unsigned long long* sw;                    // one-pass scan: published words, per group's first chunk
-    int *ghist, *gw, *gstart, *gbase;          // one-pass scan: group order tables
-    int2* glist;                               // one-pass scan: (cell, rank) of every ticket
+    int *ghist, *gw, *gstart, *gbase;          // one-pass scan: s2 group order tables
+    int2* glist;                               // one-pass scan: (cell, rank) of every s2 ticket
+    int *ghist3, *gw3, *gstart3, *gbase3;      // ... and of the s3 level
+    int2* glist3;
     int nv = 0;                                // entries of ghist / gstart / gbase
     int* scan_err = nullptr;                   // host memory: a one-pass scan wait ran out
     float* trash;                              // sink of the projection's absent rows
-    int max_chunks = 0;
     unsigned char *owner, *pass2, *pass3;
     uint32_t *ka, *kb, *va, *vb, *key3g;
     BlockDesc* bd;
@@ -2096,7 +1949,7 @@ int ensure_workspace(int E, int nkeys) {
     const size_t mc = P / kCH + (size_t)ck + 1;    // chunk bound: full chunks + one tail per key
     // a cell's pairs come from distinct records: at most cap, so a cell has at
     // most cap / (kCH kSG) + 2 groups of the one-pass scan
-    const size_t nv = (size_t)cap / (kCH * kSG) + 3;
+    const size_t nv = (size_t)cap / (kCH * std::min(kSG, kSG3)) + 3;
     // radix-sort tile histograms: (1 << kRMaxBits) digits x tiles
     const size_t bh = ((size_t)1 << kRMaxBits) * (size_t)((cap + kRTile - 1) / kRTile);
     struct Item { void** dst; size_t bytes; };
@@ -2107,7 +1960,9 @@ int ensure_workspace(int E, int nkeys) {
         {(void**)&w.X2, sizeof(float) * (size_t)cap * SSLA_C2},
         {(void**)&w.X3, sizeof(float) * (size_t)cap * SSLA_C3},
         {(void**)&w.X4, sizeof(float) * (size_t)cap * SSLA_C3},
-        {(void**)&w.QVG, sizeof(float) * P * 2 * SSLA_C3},     // [v | g] rows
+        // [v | g] rows, and kCH rows of padding that a scan chunk may read past
+        // the last one
+        {(void**)&w.QVG, sizeof(float) * (P + kCH) * 2 * SSLA_C3},
         {(void**)&w.H7, sizeof(float) * (size_t)cap * 7},
         {(void**)&w.cell2, sizeof(int) * (size_t)cap},
         {(void**)&w.pos2, sizeof(int) * P},
@@ -2151,15 +2006,17 @@ int ensure_workspace(int E, int nkeys) {
         {(void**)&w.ckey3, sizeof(int) * mc},
         {(void**)&w.cbeg3, sizeof(int) * mc},
         {(void**)&w.cend3, sizeof(int) * mc},
-        {(void**)&w.Asum, sizeof(float) * mc * SSLA_C3},
-        {(void**)&w.Bsum, sizeof(float) * mc * SSLA_C3},
-        {(void**)&w.Hs, sizeof(float) * mc * SSLA_C3},
-        {(void**)&w.sw, sizeof(unsigned long long) * mc * 3 * SSLA_C2},
+        {(void**)&w.sw, sizeof(unsigned long long) * mc * 3 * SSLA_C3},
         {(void**)&w.ghist, sizeof(int) * nv},
         {(void**)&w.gstart, sizeof(int) * nv},
         {(void**)&w.gbase, sizeof(int) * nv},
         {(void**)&w.gw, sizeof(int) * (size_t)ck},
         {(void**)&w.glist, sizeof(int2) * (mc / kSG + (size_t)ck + 1)},
+        {(void**)&w.ghist3, sizeof(int) * nv},
+        {(void**)&w.gstart3, sizeof(int) * nv},
+        {(void**)&w.gbase3, sizeof(int) * nv},
+        {(void**)&w.gw3, sizeof(int) * (size_t)ck},
+        {(void**)&w.glist3, sizeof(int2) * (mc / kSG3 + (size_t)ck + 1)},
         {(void**)&w.trash, sizeof(float) * 4 * 64},
         {(void**)&w.bd, sizeof(BlockDesc) * SSLA_MAX_BLOCKS},
     };
@@ -2173,7 +2030,7 @@ int ensure_workspace(int E, int nkeys) {
         p += align_up(it.bytes);
     }
     // no stale word may carry a future launch's tag
-    HIPCHK(hipMemset(w.sw, 0, sizeof(unsigned long long) * mc * 3 * SSLA_C2));
+    HIPCHK(hipMemset(w.sw, 0, sizeof(unsigned long long) * mc * 3 * SSLA_C3));
     w.nv = (int)nv;
     if (!w.scan_err) {
         HIPCHK(hipHostMalloc((void**)&w.scan_err, sizeof(int), hipHostMallocCoherent));
@@ -2200,7 +2057,6 @@ int ensure_workspace(int E, int nkeys) {
     w.cap = cap;
     w.cap_keys = ck;
     w.bh_ints = (int)bh;
-    w.max_chunks = (int)mc;
     return SSLA_OK;
 }
 
@@ -2423,13 +2279,13 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // per-call fills: run bounds of the s2 keys (k_runs writes those that
     // occur), the list and chunk counters, the prediction-grid writers
     // one-pass scan: the group-count bound of this call's cells (see ensure_workspace)
-    const int nv2 = E / (kCH * kSG) + 3;
+    const int nv2 = E / (kCH * kSG) + 3, nv3 = E / (kCH * kSG3) + 3;
     FillSet f{};
     {
-        int* arr[kFills] = {w.st2, w.en2, w.counts, w.last3, w.cnt3, w.ghist};
+        int* arr[kFills] = {w.st2, w.en2, w.counts, w.last3, w.cnt3, w.ghist, w.ghist3};
         const int len[kFills] = {(int)nk2, (int)nk2, 16, have_head ? (int)nk3 : 0,
-                                 have_head ? (int)nk3 : 0, nv2};
-        const int val[kFills] = {0, 0, 0, -1, 0, 0};
+                                 have_head ? (int)nk3 : 0, nv2, nv3};
+        const int val[kFills] = {0, 0, 0, -1, 0, 0, 0};
         for (int i = 0; i < kFills; ++i) {
             f.p[i] = arr[i];
             f.n[i] = len[i];
@@ -2438,7 +2294,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     }
     // ---- decode (and the fills); stable radix sort of the records by s2 key --
     {
-        const int ndec = (int)grid1(E, kDecRec), fblk = (int)grid1(std::max<int>(std::max<int>((int)nk2, 16), nv2), 256);
+        const int ndec = (int)grid1(E, kDecRec), fblk = (int)grid1(std::max<int>(std::max<int>((int)nk2, 16), nv3), 256);
         hipLaunchKernelGGL(k_decode, dim3(ndec + fblk * kFills), dim3(256), 0, st, E, w.bd, G,
                            w.X0, w.cell2, w.owner, w.ka, w.va, ndec, f, fblk);
     }
@@ -2535,50 +2391,32 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // s2 layers in one pass (k_scan, ticket counters counts[4 + LI], group
     // count counts[6]), the s3 layers in three (summary, carry, apply).
     const unsigned long long wait_ticks = (unsigned long long)std::max(w.clk_khz, 1) * 500ull;
-#define SCAN3(OUT, HS, LI, LV, NC, NK, CELLS, NEED, HOUT)                                             \
-    do {                                                                                            \
-        hipLaunchKernelGGL((k_scan_summary<OUT>), dim3(chunks3), dim3((OUT + 63) / 64 * 64),        \
-                           0, st, (const int*)(w.counts + NC), w.cbeg##LV, w.cend##LV, w.QVG,       \
-                           w.Asum, w.Bsum);                                                         \
-        MARK();                                                                                     \
-        hipLaunchKernelGGL((k_scan_carry<OUT>), dim3(NK),                                           \
-                           dim3(carry_threads(NK, (OUT + 63) / 64 * 64)), 0, st, CELLS, w.pst##LV,   \
-                           w.pen##LV, w.coff##LV, w.bd, LI, w.Asum, w.Bsum, w.Hs);                  \
-        MARK();                                                                                     \
-        hipLaunchKernelGGL((k_scan_apply<OUT, HS>), dim3(chunks3), dim3((OUT + 63) / 64 * 64),      \
-                           0, st, (const int*)(w.counts + NC), w.cbeg##LV, w.cend##LV, w.Hs, NEED,  \
-                           w.QVG, HOUT);                                                            \
-        MARK();                                                                                     \
-    } while (0)
-#define SCAN1(LI, NEED)                                                                             \
+#define SCAN1(OUT, HS, SGV, LI, LV, NG, GL, NEED, HOUT, CELLS, GRID)                                  \
     do {                                                                                            \
         unsigned tag_ = ++g_scan_tag;                                                               \
         if (tag_ == 0) tag_ = ++g_scan_tag;                                                         \
         MARK();                                                                                     \
         MARK();                                                                                     \
-        hipLaunchKernelGGL((k_scan<SSLA_C2, SSLA_C2>), dim3(groups2), dim3(kSG * 64), 0, st,        \
-                           (const int*)(w.counts + 6), w.counts + 4 + LI, tag_, w.glist, w.cbeg2,    \
-                           w.cend2, w.coff2, w.pst2, w.pen2, G.C2, w.bd, LI, NEED, w.QVG, Hc, w.sw, \
-                           w.scan_err, wait_ticks);                                                 \
+        hipLaunchKernelGGL((k_scan<OUT, HS, SGV>), dim3(GRID), dim3(SGV * ((OUT + 63) / 64) * 64), 0, \
+                           st, (const int*)(w.counts + NG), w.counts + 8 + LI, tag_, GL,             \
+                           w.cbeg##LV, w.cend##LV, w.coff##LV, w.pst##LV, w.pen##LV, CELLS, w.bd,   \
+                           LI, NEED, w.QVG, HOUT, w.sw, w.scan_err, wait_ticks);                    \
         MARK();                                                                                     \
     } while (0)
-    // workgroups of the s3 scan passes: one per chunk, at most 9 nmax2 / kCH
-    // plus one per key (a call's own bound, not the workspace's)
-    const unsigned chunks3 = (unsigned)std::min<size_t>((size_t)nmax2 * kPatch / kCH + nk3 + 1,
-                                                        (size_t)w.max_chunks);
-    // workgroups of the s2 one-pass scan: one per group (at most one per kSG
+    // workgroups of the one-pass scans: one per group (at most one per kSG
     // chunks plus one per key); those past the group count exit at once
     const unsigned groups2 = (unsigned)(((size_t)E * kPatch / kCH + nk2 + 1) / kSG + nk2 + 1);
+    const unsigned groups3 = (unsigned)(((size_t)nmax2 * kPatch / kCH + nk3 + 1) / kSG3 + nk3 + 1);
     // ---- L4: 24 -> 48, all records ----------------------------------------
     hipLaunchKernelGGL((k_qvg<SSLA_C1, SSLA_C2, true, kTMP>), dim3(gridP4), dim3(256), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, pk.pp[0], w.QVG, w.trash);
     // [side] the s2 one-pass scan's ticket order, beside L4's projection
-    hipLaunchKernelGGL(k_group_order, dim3(1), dim3(kScanThreads), 0, s3, (int)nk2, nv2, w.pst2,
+    hipLaunchKernelGGL(k_group_order, dim3(1), dim3(kScanThreads), 0, s3, (int)nk2, nv2, kSG, w.pst2,
                        w.pen2, w.ghist, w.gw, w.gstart, w.gbase, w.glist, w.counts + 6);
     HIPCHK(hipEventRecord(w.s2_groups, s3));
     MARK();
     HIPCHK(hipStreamWaitEvent(st, w.s2_groups, 0));
-    SCAN1(0, all);
+    SCAN1(SSLA_C2, SSLA_C2, kSG, 0, 2, 6, w.glist, all, Hc, G.C2, groups2);
     hipLaunchKernelGGL((k_outt<SSLA_C1, SSLA_C2, 2, 1, 3, SSLA_C2>), dim3(grid1(E, 32)), dim3(64), 0,
                        st, E, (const int*)nullptr, (const int*)nullptr, w.X0, w.pos2, Hc, pk.po[0],
                        L[0].ln_gamma, L[0].ln_beta, w.X1);
@@ -2603,7 +2441,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        w.pen3, w.coff3, w.counts + 3, (const int*)nullptr, (int*)nullptr,
                        (int*)nullptr, KeyHist{});
     hipLaunchKernelGGL(k_chunks, dim3(grid1(nk3, 4)), dim3(256), 0, s3, nk3, w.pst3, w.pen3,
-                       w.coff3, w.ckey3, w.cbeg3, w.cend3);
+                       w.coff3, w.ckey3, w.cbeg3, w.cend3, w.ghist3, w.gw3);
+    hipLaunchKernelGGL(k_group_order, dim3(1), dim3(kScanThreads), 0, s3, (int)nk3, nv3, kSG3, w.pst3,
+                       w.pen3, w.ghist3, w.gw3, w.gstart3, w.gbase3, w.glist3, w.counts + 7);
     hipLaunchKernelGGL(k_pair_rank, dim3(grid1(nmax2, 256)), dim3(256), 0, s3, E,
                        (const int*)(w.counts + 0), K3, V3, nk3, G.C3, G.W3, G.H3, w.st3, w.en3,
                        w.pst3, w.pos3, w.pneed3, w.pass3);
@@ -2613,7 +2453,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C2, true, kTMP>), dim3(gridP5), dim3(256), 0, st, E,
                        (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, pk.pp[1], w.QVG, w.trash);
     MARK();
-    SCAN1(1, w.pneed2);
+    SCAN1(SSLA_C2, SSLA_C2, kSG, 1, 2, 6, w.glist, w.pneed2, Hc, G.C2, groups2);
     hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C2, 1, 3, 1, SSLA_C2>), dim3(grid1(nmax2, 16)), dim3(192), 0,
                        st, E, (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, Hc, pk.po[1],
                        L[1].ln_gamma, L[1].ln_beta, w.X2);
@@ -2623,7 +2463,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_qvg<SSLA_C2, SSLA_C3, false, kTM, 2>), dim3(tiles2 * 2), dim3(256), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, pk.pp[2], w.QVG, w.trash);
     MARK();
-    SCAN3(96, 192, 2, 3, 3, nk3, G.C3, all, w.QVG);
+    SCAN1(SSLA_C3, 2 * SSLA_C3, kSG3, 2, 3, 7, w.glist3, all, w.QVG, G.C3, groups3);
     hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C3, 1, 3>), dim3(grid1(nmax2, 16)), dim3(192), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, pk.po[2],
                        L[2].ln_gamma, L[2].ln_beta, w.X3);
@@ -2632,7 +2472,7 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     hipLaunchKernelGGL((k_qvg<SSLA_C3, SSLA_C3, false, kTM, 4>), dim3(tiles2 * 4), dim3(256), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, pk.pp[3], w.QVG, w.trash);
     MARK();
-    SCAN3(96, 192, 3, 3, 3, nk3, G.C3, w.pneed3, w.QVG);
+    SCAN1(SSLA_C3, 2 * SSLA_C3, kSG3, 3, 3, 7, w.glist3, w.pneed3, w.QVG, G.C3, groups3);
     hipLaunchKernelGGL((k_outt<SSLA_C3, SSLA_C3, 1, 3>), dim3(grid1(nmax3, 16)), dim3(192), 0, st, E,
                        (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, pk.po[3],
                        L[3].ln_gamma, L[3].ln_beta, w.X4);
@@ -2658,7 +2498,6 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     MARK();
 #undef MARK
 #undef SCAN1
-#undef SCAN3
     end.finish();
     if (sync) {
         HIPCHK(hipStreamSynchronize(st));
