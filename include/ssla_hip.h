@@ -228,13 +228,9 @@ int ssla_hip_drain_batch_noalloc(const HybridS2S3Config* cfg,
  * max_records records in total over cfg's blocks and grid.  No counterpart
  * in the reference (its drain kernel works in shared memory only).
  *
- * The drain also keeps fragment-order copies of the layer weights
- * (reordered for the matrix cores).  They are rebuilt when a layer weight
- * pointer of cfg changes, or after any call of this library that may write
- * device memory (ssla_hip_memcpy, _memset, _free_device, _model_load,
- * _model_free).  A caller that rewrites weight memory in place by other
- * means calls ssla_hip_memset(p, 0, 0) (it writes nothing) before the next
- * drain. */
+ * Every drain call rebuilds its fragment-order copy of the layer weights
+ * (reordered for the matrix cores) from cfg's weight pointers, so weights
+ * rewritten in place, by any means, between calls are the ones used. */
 int ssla_hip_drain_reserve(const HybridS2S3Config* cfg, int max_records);
 
 /* Ticks per millisecond of the constant-rate GPU clock used by batch_clks

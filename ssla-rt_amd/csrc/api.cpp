@@ -230,7 +230,6 @@ int ssla_hip_malloc_host(size_t nbytes, void** out) {
 }
 
 int ssla_hip_free_device(void* p) {
-    weights_touched();
     if (p) API_HIP(hipFree(p));
     return SSLA_OK;
 }
@@ -241,7 +240,6 @@ int ssla_hip_free_host(void* p) {
 }
 
 int ssla_hip_memcpy(void* dst, const void* src, size_t nbytes) {
-    weights_touched();
     if (!nbytes) return SSLA_OK;
     if (!dst || !src) { set_error("null pointer"); return SSLA_ERR_ARG; }
     API_HIP(hipMemcpy(dst, src, nbytes, hipMemcpyDefault));
@@ -249,7 +247,6 @@ int ssla_hip_memcpy(void* dst, const void* src, size_t nbytes) {
 }
 
 int ssla_hip_memset(void* dst, int value, size_t nbytes) {
-    weights_touched();
     if (!nbytes) return SSLA_OK;
     if (!dst) { set_error("null pointer"); return SSLA_ERR_ARG; }
     API_HIP(hipMemsetAsync(dst, value, nbytes, nullptr));
@@ -322,7 +319,6 @@ int ssla_hip_meta_read(const char* dir, int* out) {
 
 int ssla_hip_model_load(const char* dir, SslaHipModel** out) {
     if (!dir || !out) { set_error("null argument"); return SSLA_ERR_ARG; }
-    weights_touched();
     *out = nullptr;
     ModelMeta meta;
     std::map<std::string, NpzTensor> W;
@@ -451,7 +447,6 @@ int ssla_hip_model_info(const SslaHipModel* m, SslaHipModelInfo* out) {
 
 void ssla_hip_model_free(SslaHipModel* m) {
     if (!m) return;
-    weights_touched();
     if (m->dev) (void)hipFree(m->dev);
     delete m;
 }

@@ -37,6 +37,7 @@
 #include <chrono>
 #include <cstdint>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <thread>
 #include <string>
@@ -2069,6 +2070,7 @@ struct GroupRes {
     unsigned char* tdrep = nullptr;
     float* pack = nullptr;
     float* packT = nullptr;
+    size_t xcap = 0, hcap = 0, tdcap = 0;      // bytes allocated
     void release() {
         if (xb) (void)hipFree(xb);
         if (hb) (void)hipFree(hb);
@@ -2078,6 +2080,17 @@ struct GroupRes {
         *this = GroupRes{};
     }
 };
+
+// Grows a buffer to at least `need` bytes (keeps it when large enough).
+static int grow(void** p, size_t* cap, size_t need) {
+    if (*cap >= need && *p) return SSLA_OK;
+    if (*p) LHIP(hipFree(*p));
+    *p = nullptr;
+    *cap = 0;
+    LHIP(hipMalloc(p, need));
+    *cap = need;
+    return SSLA_OK;
+}
 
 // Every member of every group must be resident at once: members wait on
 // each other.
@@ -2111,14 +2124,17 @@ static int group_setup(const HybridS2S3Config* cfg, const Geometry& G, int group
     const int nb = G.nb;
     const size_t xbytes = sizeof(unsigned long long) * kXStride * nb * stages;
     const size_t per = (size_t)(G.C2 + G.C3);
-    LHIP(hipMalloc(&r->xb, xbytes));
-    LHIP(hipMalloc(&r->tdrep, (size_t)nb * stages * (group - 1) * per));
-    LHIP(hipMalloc(&r->pack, sizeof(float) * packed_weight_floats()));
-    LHIP(hipMalloc(&r->packT, sizeof(float) * packed_weight_floats_d()));
+    // buffers are grown only when r's are too small (a cached r allocates
+    // nothing on later calls of the same or smaller sizes)
+    int rc = grow((void**)&r->xb, &r->xcap, xbytes);
+    if (!rc) rc = grow((void**)&r->tdrep, &r->tdcap, (size_t)nb * stages * (group - 1) * per);
+    if (rc) return rc;
+    if (!r->pack) LHIP(hipMalloc(&r->pack, sizeof(float) * packed_weight_floats()));
+    if (!r->packT) LHIP(hipMalloc(&r->packT, sizeof(float) * packed_weight_floats_d()));
     LHIP(hipMemsetAsync(r->xb, 0, xbytes, st));
     if (stages == 2) {
         const size_t hbytes = sizeof(unsigned long long) * kHStride * nb;
-        LHIP(hipMalloc(&r->hb, hbytes));
+        if ((rc = grow((void**)&r->hb, &r->hcap, hbytes))) return rc;
         LHIP(hipMemsetAsync(r->hb, 0, hbytes, st));
     }
     for (int b = 0; b < nb * stages; ++b)
@@ -2151,6 +2167,16 @@ static int group_setup(const HybridS2S3Config* cfg, const Geometry& G, int group
     return SSLA_OK;
 }
 
+// The group batch drain's device resources, kept per device across calls
+// (under g_bmu): after a device's first call of a size, calls allocate nothing.
+struct GroupBatchCache {
+    GroupRes r;
+    LiveDesc* desc = nullptr;                  // SSLA_MAX_BLOCKS
+    int* status = nullptr;
+    unsigned long long* prof = nullptr;        // NPROF x SSLA_MAX_BLOCKS
+};
+static std::map<int, GroupBatchCache> g_group_batch;
+
 int batch_drain_group(const HybridS2S3Config* cfg, const HybridInputRec* const* rings, const int* ns,
                       HybridS2S3OutputSlot* const* outs, float* const* head_outs, int batch,
                       int group, hipStream_t st, double* phase_us) {
@@ -2169,56 +2195,53 @@ int batch_drain_group(const HybridS2S3Config* cfg, const HybridInputRec* const* 
             return SSLA_ERR_ARG;
         }
     if ((rc = group_check(nb, group))) return rc;
+    int dev = 0;
+    LHIP(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lk(g_bmu);
-    GroupRes r;
-    LiveDesc* desc = nullptr;
-    int* status = nullptr;
-    unsigned long long* prof = nullptr;
-    auto run = [&]() -> int {
-        GroupArgs ga{};
-        int rc2 = group_setup(cfg, G, group, st, &W, &r, &ga);
-        if (rc2) return rc2;
-        LHIP(hipMalloc(&desc, sizeof(LiveDesc) * nb));
-        LHIP(hipMalloc(&status, sizeof(int)));
-        LHIP(hipMemsetAsync(status, 0, sizeof(int), st));
-        if (phase_us) LHIP(hipMalloc(&prof, sizeof(unsigned long long) * NPROF * nb));
-        std::vector<LiveDesc> hd(nb);
-        std::memset(hd.data(), 0, sizeof(LiveDesc) * nb);
-        for (int b = 0; b < nb; ++b) {
-            LiveDesc& d = hd[b];
-            live_desc_state(cfg, b, &d);
-            d.ring = rings[b];
-            d.ring_mask = ~0ull;
-            d.n = ns[b];
-            d.out = outs ? outs[b] : nullptr;
-            d.head_out = head_outs ? head_outs[b] : nullptr;
-            d.prof = prof ? prof + (size_t)NPROF * b : nullptr;
-        }
-        LHIP(hipMemcpyAsync(desc, hd.data(), sizeof(LiveDesc) * nb, hipMemcpyHostToDevice, st));
-        hipLaunchKernelGGL((k_group<false, 1>), dim3(nb * group), dim3(LT), 0, st, desc, W, G, ga,
-                           (const int*)nullptr, 0u, 0ull, batch, status);
-        LHIP(hipGetLastError());
-        LHIP(hipStreamSynchronize(st));
-        int hs = 0;
-        LHIP(hipMemcpy(&hs, status, sizeof(int), hipMemcpyDeviceToHost));
-        if (hs) {
-            set_error("group drain: a member's wait ran out (status " + std::to_string(hs) + ")");
-            return SSLA_ERR_STATE;
-        }
-        if (phase_us) {
-            std::vector<unsigned long long> h((size_t)NPROF * nb);
-            LHIP(hipMemcpy(h.data(), prof, sizeof(unsigned long long) * h.size(), hipMemcpyDeviceToHost));
-            add_profile(h.data(), nb, phase_us);
-        }
-        return SSLA_OK;
-    };
-    rc = run();
-    (void)hipStreamSynchronize(st);
-    r.release();
-    if (desc) (void)hipFree(desc);
-    if (status) (void)hipFree(status);
-    if (prof) (void)hipFree(prof);
-    return rc;
+    GroupBatchCache& c = g_group_batch[dev];
+    // every exit waits for the stream: work queued on the cached buffers must
+    // be done before the next call reuses them (also after an error)
+    struct SyncAtExit {
+        hipStream_t st;
+        ~SyncAtExit() { (void)hipStreamSynchronize(st); }
+    } sync_at_exit{st};
+    GroupArgs ga{};
+    if ((rc = group_setup(cfg, G, group, st, &W, &c.r, &ga))) return rc;
+    if (!c.desc) LHIP(hipMalloc(&c.desc, sizeof(LiveDesc) * SSLA_MAX_BLOCKS));
+    if (!c.status) LHIP(hipMalloc(&c.status, sizeof(int)));
+    if (phase_us && !c.prof)
+        LHIP(hipMalloc(&c.prof, sizeof(unsigned long long) * NPROF * SSLA_MAX_BLOCKS));
+    LHIP(hipMemsetAsync(c.status, 0, sizeof(int), st));
+    std::vector<LiveDesc> hd(nb);
+    std::memset(hd.data(), 0, sizeof(LiveDesc) * nb);
+    for (int b = 0; b < nb; ++b) {
+        LiveDesc& d = hd[b];
+        live_desc_state(cfg, b, &d);
+        d.ring = rings[b];
+        d.ring_mask = ~0ull;
+        d.n = ns[b];
+        d.out = outs ? outs[b] : nullptr;
+        d.head_out = head_outs ? head_outs[b] : nullptr;
+        d.prof = phase_us ? c.prof + (size_t)NPROF * b : nullptr;
+    }
+    LHIP(hipMemcpyAsync(c.desc, hd.data(), sizeof(LiveDesc) * nb, hipMemcpyHostToDevice, st));
+    hipLaunchKernelGGL((k_group<false, 1>), dim3(nb * group), dim3(LT), 0, st, c.desc, W, G, ga,
+                       (const int*)nullptr, 0u, 0ull, batch, c.status);
+    LHIP(hipGetLastError());
+    LHIP(hipStreamSynchronize(st));
+    int hs = 0;
+    LHIP(hipMemcpy(&hs, c.status, sizeof(int), hipMemcpyDeviceToHost));
+    if (hs) {
+        set_error("group drain: a member's wait ran out (status " + std::to_string(hs) + ")");
+        return SSLA_ERR_STATE;
+    }
+    if (phase_us) {
+        std::vector<unsigned long long> h((size_t)NPROF * nb);
+        LHIP(hipMemcpy(h.data(), c.prof, sizeof(unsigned long long) * h.size(),
+                       hipMemcpyDeviceToHost));
+        add_profile(h.data(), nb, phase_us);
+    }
+    return SSLA_OK;
 }
 
 // ---------------------------------------------------------------------------

@@ -30,9 +30,4 @@ int drain_reserve(const HybridS2S3Config* cfg, int max_records);
 // without waiting.
 int zero_async(void* p, size_t nbytes, hipStream_t st);
 
-// Marks the layer weights as possibly rewritten: the next drain rebuilds its
-// fragment-order copy.  Called by every ABI entry point that may write device
-// memory.
-void weights_touched();
-
 }  // namespace ssla

@@ -1911,10 +1911,6 @@ struct Workspace {
     int cus = 0;                       // compute units of the device
     int clk_khz = 0;                   // wall-clock (s_memrealtime) rate
     float* packed = nullptr;           // fragment-order weight copies (packed_weight_floats_d)
-    // What `packed` was built from: the layer weight pointers and the weight
-    // generation (bumped by every library call that may write device memory).
-    PackSrc packed_src = {};
-    unsigned long long packed_gen = ~0ull;
     PackedWeights pk = {};
 };
 
@@ -2086,11 +2082,7 @@ struct CallEnd {
     ~CallEnd() { finish(); }
 };
 
-std::atomic<unsigned long long> g_weights_gen{0};
-
 }  // namespace
-
-void weights_touched() { g_weights_gen.fetch_add(1, std::memory_order_relaxed); }
 
 namespace {
 // zero fill of n bytes at p (16-byte stores for the aligned body)
@@ -2258,22 +2250,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     };
 #define MARK() do { const int rc_ = mark(); if (rc_) return rc_; } while (0)
     // fragment-order copies of the layer weights for the MFMA kernels, rebuilt
-    // when a weight pointer or the weight generation has changed
-    {
-        PackSrc src{};
-        for (int i = 0; i < 4; ++i) {
-            src.qvgIn[i] = cfg->layers[0][i].qvgIn;
-            src.goW[i] = cfg->layers[0][i].goW;
-            src.ip[i] = cfg->layers[0][i].input_proj;
-        }
-        const unsigned long long gen = g_weights_gen.load(std::memory_order_relaxed);
-        if (gen != w.packed_gen || std::memcmp(&src, &w.packed_src, sizeof src) != 0) {
-            w.packed_gen = ~0ull;
-            HIPCHK(pack_weights_d(cfg->layers[0], w.packed, &w.pk, st));
-            w.packed_src = src;
-            w.packed_gen = gen;
-        }
-    }
+    // by every call (one launch of a few microseconds), so weights rewritten in
+    // place by any means are always the ones used
+    HIPCHK(pack_weights_d(cfg->layers[0], w.packed, &w.pk, st));
     const PackedWeights& pk = w.pk;
     MARK();
     // per-call fills: run bounds of the s2 keys (k_runs writes those that

@@ -476,3 +476,31 @@ def test_640x480_full_size_properties(H, stub_640):
         c2, c3 = d.counters(0)
         assert np.array_equal(c2, td2) and np.array_equal(c3, td3)
         say(f"640x480 full size: {int((d3 == 1).sum())} pass3 records")
+
+
+def test_weights_rewritten_in_place_between_calls(H, stub_dir, stub_npz, tmp_path):
+    """The whole-ring drain uses the weights the configuration points at when
+    it is called: L5's weights are rewritten in place between two drains by
+    a plain device copy (not through the drain entry points), and the second
+    drain matches the oracle with the new layer."""
+    from ssla_hip import stub
+    from ssla_hip.hybrid import upload_ptr
+    stub.write_stub(str(tmp_path), height=64, width=80, seed=2, tdrop=4)
+    L5b = O.layers_from_npz(O.load_npz(str(tmp_path)))[1]
+    ra, rb = events.blob_records(4000, seed=5), events.blob_records(4000, seed=6)
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        (a,), _ = d.drain([events.to_records(ra)])
+        st = O.S2S3(O.layers_from_npz(stub_npz), 16, 20, 4)
+        p2, p3, feat, _ = st.run(ra.x, ra.y, ra.feat1)
+        compare(a, p2, p3, feat, "weights before")
+        lw = d.cfg.layers[0][1]
+        for ptr, arr in ((lw.qvgIn, L5b.qvgIn.transpose(0, 2, 1)), (lw.goW, L5b.goW.transpose(0, 2, 1)),
+                         (lw.ln_gamma, L5b.ln_gamma), (lw.ln_beta, L5b.ln_beta)):
+            upload_ptr(ptr, np.ascontiguousarray(arr, np.float32))
+        d.reset()
+        (b,), _ = d.drain([events.to_records(rb)])
+        layers = O.layers_from_npz(stub_npz)
+        layers[1] = L5b
+        st = O.S2S3(layers, 16, 20, 4)
+        p2, p3, feat, _ = st.run(rb.x, rb.y, rb.feat1)
+        compare(b, p2, p3, feat, "weights rewritten in place")

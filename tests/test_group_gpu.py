@@ -66,6 +66,29 @@ def test_group_batch_continues_state(H, stub_dir, stub_npz):
         assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3)
 
 
+def test_group_batch_repeated_calls(H, stub_dir, stub_npz):
+    """Three group batch drains in a row, each on the resources the first
+    one sized (they are kept per device), continue one state: the
+    concatenated outputs equal the oracle run on all records."""
+    rec = events.blob_records(3000, seed=23)
+    recs = events.to_records(rec)
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        outs = []
+        for lo in (0, 1000, 2000):
+            d.load_rings([recs[lo:lo + 1000]])
+            # a device-wide sync before each call marks the call boundaries
+            # in a HIP API trace of this test
+            lib.check(lib.load().ssla_hip_device_synchronize())
+            d.run(batch=32, group=6)
+            outs.append(d.results()[0][0])
+        st, p2, p3, feat, _ = oracle_run(stub_npz, rec, head=False)
+        o = np.concatenate(outs)
+        assert np.array_equal(o["pass2"], p2.astype(np.int32))
+        assert np.array_equal(o["pass3"], p3.astype(np.int32))
+        for li in range(4):
+            assert hidden_close(d.hidden(0, li), st.H[li]), li
+
+
 def test_group_bad_sizes(H, stub_dir):
     rec = events.to_records(events.blob_records(64, seed=3))
     with H.Drain.from_weights_dir(stub_dir) as d:
