@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import subprocess
+import threading
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Dict, List, Optional, Sequence
@@ -30,7 +31,8 @@ _FP = ctypes.POINTER(ctypes.c_float)
 class OracleLayer(ctypes.Structure):
     _fields_ = [("qvgIn", _FP), ("goW", _FP), ("input_proj", _FP),
                 ("ln_gamma", _FP), ("ln_beta", _FP),
-                ("in_dim", ctypes.c_int), ("out_dim", ctypes.c_int), ("K", ctypes.c_int)]
+                ("in_dim", ctypes.c_int), ("out_dim", ctypes.c_int), ("K", ctypes.c_int),
+                ("qvgInT", _FP), ("goWT", _FP)]
 
 
 class OracleHead(ctypes.Structure):
@@ -118,6 +120,9 @@ def _f32(a) -> np.ndarray:
 
 # ---- layers -------------------------------------------------------------------
 
+_T_LOCK = threading.Lock()
+
+
 @dataclass
 class Layer:
     """Fused weights in the oracle layout (qvgIn (A, 3D, in), goW (A, D, D))."""
@@ -133,8 +138,26 @@ class Layer:
         for a in (self.qvgIn, self.goW, self.input_proj, self.ln_gamma, self.ln_beta):
             if a is not None:
                 assert a.dtype == np.float32 and a.flags.c_contiguous
+        qT, gT = self._input_major()
         return OracleLayer(_fp(self.qvgIn), _fp(self.goW), _fp(self.input_proj),
-                           _fp(self.ln_gamma), _fp(self.ln_beta), i, three_d // 3, self.K)
+                           _fp(self.ln_gamma), _fp(self.ln_beta), i, three_d // 3, self.K,
+                           _fp(qT), _fp(gT))
+
+    def _input_major(self):
+        """Input-major copies of qvgIn and goW for the fp64 step's dot
+        products (same sums, same order).  Rebuilt when the weights change;
+        every copy handed out lives as long as the layer, so structs built
+        earlier never point at freed memory."""
+        with _T_LOCK:                   # layers are shared by oracle threads
+            t = self.__dict__.get("_t")
+            if t is None or not (np.array_equal(t[0], self.qvgIn)
+                                 and np.array_equal(t[1], self.goW)):
+                self.__dict__.setdefault("_t_old", []).append(t)
+                t = (self.qvgIn.copy(), self.goW.copy(),
+                     np.ascontiguousarray(self.qvgIn.transpose(0, 2, 1)),
+                     np.ascontiguousarray(self.goW.transpose(0, 2, 1)))
+                self.__dict__["_t"] = t
+            return t[2], t[3]
 
 
 def reshape(W_in_cat, W_out_cat, qW, vW, gW, oW):

@@ -134,18 +134,60 @@ static void layernorm_f64(const double* y, int D, const float* gamma,
 /* layer_step, fp64 (ssla_ref.py:17-93)                                     */
 /* ------------------------------------------------------------------------ */
 
+/* out[r] = sum_i W[r*IN + i] * x[i] for r < rows, each sum taken in fp64 in
+ * index order i = 0..IN-1.  Eight rows run side by side so their eight
+ * dependency chains overlap; the order of every single sum is unchanged.  */
+#define ROWS_DOT_F64(NAME, XT)                                                \
+static void NAME(const float* W, int rows, int IN, const XT* x, double* out) { \
+    int r = 0;                                                                \
+    for (; r + 8 <= rows; r += 8) {                                           \
+        const float* w0 = W + (size_t)r * IN;                                 \
+        const float *w1 = w0 + IN, *w2 = w1 + IN, *w3 = w2 + IN;              \
+        const float *w4 = w3 + IN, *w5 = w4 + IN, *w6 = w5 + IN, *w7 = w6 + IN; \
+        double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;                        \
+        double s4 = 0.0, s5 = 0.0, s6 = 0.0, s7 = 0.0;                        \
+        for (int i = 0; i < IN; ++i) {                                        \
+            const double xi = (double)x[i];                                   \
+            s0 += (double)w0[i] * xi; s1 += (double)w1[i] * xi;               \
+            s2 += (double)w2[i] * xi; s3 += (double)w3[i] * xi;               \
+            s4 += (double)w4[i] * xi; s5 += (double)w5[i] * xi;               \
+            s6 += (double)w6[i] * xi; s7 += (double)w7[i] * xi;               \
+        }                                                                     \
+        out[r] = s0; out[r + 1] = s1; out[r + 2] = s2; out[r + 3] = s3;       \
+        out[r + 4] = s4; out[r + 5] = s5; out[r + 6] = s6; out[r + 7] = s7;   \
+    }                                                                         \
+    for (; r < rows; ++r) {                                                   \
+        double s = 0.0;                                                       \
+        const float* w = W + (size_t)r * IN;                                  \
+        for (int i = 0; i < IN; ++i) s += (double)w[i] * (double)x[i];        \
+        out[r] = s;                                                           \
+    }                                                                         \
+}
+ROWS_DOT_F64(rows_dot_f32in, float)
+ROWS_DOT_F64(rows_dot_f64in, double)
+
+/* The same sums over the input-major copy WT[i*rows + r]: the loop over r
+ * is innermost, so the compiler can run it on vector lanes, while each
+ * out[r] still adds its terms in the order i = 0..IN-1.                    */
+#define COLS_DOT_F64(NAME, XT)                                                \
+static void NAME(const float* WT, int rows, int IN, const XT* x, double* out) { \
+    for (int r = 0; r < rows; ++r) out[r] = 0.0;                              \
+    for (int i = 0; i < IN; ++i) {                                            \
+        const double xi = (double)x[i];                                       \
+        const float* w = WT + (size_t)i * rows;                               \
+        for (int r = 0; r < rows; ++r) out[r] += (double)w[r] * xi;           \
+    }                                                                         \
+}
+COLS_DOT_F64(cols_dot_f32in, float)
+COLS_DOT_F64(cols_dot_f64in, double)
+
 void oracle_layer_step_f64(const OracleLayer* L, const float* in,
                            float* H_all, int ev_x, int ev_y, int Hl, int Wl,
                            float* out) {
     const int IN = L->in_dim, D = L->out_dim;
     double acc[MAXD], res[MAXD], qvg[3 * MAXD], qh[MAXD];
     if (L->input_proj) {
-        for (int o = 0; o < D; ++o) {
-            double s = 0.0;
-            const float* w = L->input_proj + (size_t)o * IN;
-            for (int i = 0; i < IN; ++i) s += (double)w[i] * (double)in[i];
-            res[o] = s;
-        }
+        rows_dot_f32in(L->input_proj, D, IN, in, res);
     } else {
         for (int o = 0; o < D; ++o) res[o] = (double)in[o];
     }
@@ -155,13 +197,10 @@ void oracle_layer_step_f64(const OracleLayer* L, const float* in,
     const int np = patch_list(L->K, ev_x, ev_y, Hl, Wl, cells, deltas);
     for (int k = 0; k < np; ++k) {
         const int p = deltas[k];
-        const float* W = L->qvgIn + (size_t)p * 3 * D * IN;
-        for (int r = 0; r < 3 * D; ++r) {
-            double s = 0.0;
-            const float* w = W + (size_t)r * IN;
-            for (int i = 0; i < IN; ++i) s += (double)w[i] * (double)in[i];
-            qvg[r] = s;
-        }
+        if (L->qvgInT)
+            cols_dot_f32in(L->qvgInT + (size_t)p * 3 * D * IN, 3 * D, IN, in, qvg);
+        else
+            rows_dot_f32in(L->qvgIn + (size_t)p * 3 * D * IN, 3 * D, IN, in, qvg);
         float* h = H_all + (size_t)cells[k] * D;
         for (int o = 0; o < D; ++o) {
             const double gc = 1.0 / (1.0 + exp(-qvg[2 * D + o]));
@@ -169,13 +208,12 @@ void oracle_layer_step_f64(const OracleLayer* L, const float* in,
             h[o] = (float)hn;              /* stored back as fp32 */
             qh[o] = qvg[o] * hn;           /* q * h_new in fp64 */
         }
-        const float* G = L->goW + (size_t)p * D * D;
-        for (int o = 0; o < D; ++o) {
-            double s = 0.0;
-            const float* g = G + (size_t)o * D;
-            for (int i = 0; i < D; ++i) s += (double)g[i] * qh[i];
-            acc[o] += s;
-        }
+        double go[MAXD];
+        if (L->goWT)
+            cols_dot_f64in(L->goWT + (size_t)p * D * D, D, D, qh, go);
+        else
+            rows_dot_f64in(L->goW + (size_t)p * D * D, D, D, qh, go);
+        for (int o = 0; o < D; ++o) acc[o] += go[o];
     }
     for (int o = 0; o < D; ++o) acc[o] += res[o];
     layernorm_f64(acc, D, L->ln_gamma, L->ln_beta, out);

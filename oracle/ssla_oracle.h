@@ -59,6 +59,12 @@ typedef struct {
     int in_dim;
     int out_dim;
     int K;
+    /* Optional copies of qvgIn and goW with the last two axes swapped
+     * ((A, in, 3D) and (A, D, D) input-major), or NULL.  The fp64 step then
+     * runs its dot products over these; every sum keeps the same terms in
+     * the same order, so the results are identical either way. */
+    const float* qvgInT;
+    const float* goWT;
 } OracleLayer;
 
 /* Head of the drain.  Two-branch YOLOX head (BN already folded, PyTorch

@@ -474,9 +474,10 @@ def _check_block_preds(preds, version, x, y, own, p3, ref7, owned):
 @pytest.mark.parametrize("gpu_blocks,group,stages",
                          [(1, 0, 1), (8, 0, 1), (1, 6, 1), (8, 6, 1), (1, 6, 2), (8, 6, 2)])
 def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks, group, stages):
-    """The live configuration as stated: the producer's paced blob source at
+    """The live configuration: the producer's paced blob source at
     2.0 Mev/s -> 6 host shards for stages 0 + 1 (halo 2) -> fine-grained
-    rings -> the persistent kernel, 2 s (orin/hybrid_runner_multi.py:314-754).
+    rings -> the persistent kernel, 2 s per parametrisation
+    (orin/hybrid_runner_multi.py:314-754).
     One ownership domain (1 block) and the reference's 8-strip topology,
     one workgroup per block; one domain drained by a group of 6 workgroups
     (channel slices, exact: no halo); the 8 strips drained by a group of 6
@@ -486,10 +487,21 @@ def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks, group, 
     contents, run through the oracle with that block's ownership, give the
     kernel's pass flags (timing-slot owner flags), tdrop counters, final
     hidden state and prediction grid."""
+    _config2(stub_dir, stub_npz, gpu_blocks, group, stages, 2.0,
+             1 << 19 if gpu_blocks == 1 else 1 << 18)
+
+
+def test_config2_headline_eight_seconds(stub_dir, stub_npz):
+    """Config 2's headline run as stated: one ownership domain drained by
+    two pipelined groups of 6 workgroups, 2.0 Mev/s for 8 s (about 1M ring
+    records), every ring record checked against the oracle as above."""
+    _config2(stub_dir, stub_npz, 1, 6, 2, 8.0, 1 << 21)
+
+
+def _config2(stub_dir, stub_npz, gpu_blocks, group, stages, duration, cap):
     from ssla_hip import live as LV
-    say(f"config 2: 2.0 Mev/s, 6 shards, halo 2, 2 s, {gpu_blocks} GPU block(s), group {group}, "
-        f"stages {stages}")
-    cap = 1 << 19 if gpu_blocks == 1 else 1 << 18
+    say(f"config 2: 2.0 Mev/s, 6 shards, halo 2, {duration:g} s, {gpu_blocks} GPU block(s), "
+        f"group {group}, stages {stages}")
     seen = {}
 
     def inspect(drain, rings, heads, topo):
@@ -517,7 +529,7 @@ def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks, group, 
             _check_block_preds(pr, ver, x, y, own, p3, ref7, t.owned)
         seen["blocks"] = len(topo)
 
-    r = LV.run_live(stub_dir, rate_mev=2.0, duration_s=2.0, n_shards=6, halo=2,
+    r = LV.run_live(stub_dir, rate_mev=2.0, duration_s=duration, n_shards=6, halo=2,
                     gpu_blocks=gpu_blocks, ring_capacity=cap, timing_capacity=cap,
                     group=group, stages=stages, inspect=inspect)
     say(f"config 2: status {r.status}, {r.synth_events} events "
@@ -527,9 +539,8 @@ def test_config2_live_two_mev_six_shards(stub_dir, stub_npz, gpu_blocks, group, 
         f"p99 {r.lat_us['emit_to_done_p99']:.1f} us")
     assert r.status == 0 and seen.get("blocks") == gpu_blocks
     assert r.drained == r.ring_records > 0 and r.output_records > 0
-    # the paced source asks for 2 Mev/s; how close its one thread gets depends
-    # on the host (1.4-1.9 Mev/s measured on these boxes)
-    assert r.synth_events > 0.5 * 2.0e6 * r.duration_s
+    # the paced source asks for 2 Mev/s; the run must reach at least 1.8
+    assert r.synth_events >= 1.8e6 * r.duration_s, r.synth_events / r.duration_s
 
 
 @pytest.mark.parametrize("group,stages", [(0, 1), (6, 1), (6, 2)])

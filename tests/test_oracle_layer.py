@@ -131,6 +131,33 @@ def test_layer_step_f32_close_to_f64():
         assert np.abs(a - b).max() < 5e-5
 
 
+def test_layer_step_f64_same_on_both_weight_layouts():
+    """The fp64 step runs its dot products over input-major copies of qvgIn
+    and goW when the layer struct carries them; each sum keeps its terms and
+    their order, so outputs and states equal the row-major run bit for bit."""
+    rng = np.random.default_rng(9)
+    for in_dim, D in ((24, 48), (48, 96), (96, 96)):
+        raw = _raw(rng, in_dim, D, 9, 9)
+        qvg, go = O.reshape(**raw)
+        ip = rng.normal(0, 0.3, (D, in_dim)).astype(np.float32) if in_dim != D else None
+        layer = O.Layer(qvg, go, ip, np.ones(D, np.float32), np.zeros(D, np.float32), 3)
+        Ha = rng.normal(0, 0.3, (6 * 7, D)).astype(np.float32)
+        Hb = Ha.copy()
+        fn = O.load().oracle_layer_step_f64
+        for k in range(20):
+            x = rng.normal(0, 0.5, in_dim).astype(np.float32)
+            ex, ey = int(rng.integers(0, 7)), int(rng.integers(0, 6))
+            La = layer.c()
+            Lb = layer.c()
+            Lb.qvgInT = None
+            Lb.goWT = None
+            assert La.qvgInT and La.goWT
+            oa, ob = np.zeros(D, np.float32), np.zeros(D, np.float32)
+            fn(ctypes.byref(La), O._fp(x), O._fp(Ha), ex, ey, 6, 7, O._fp(oa))
+            fn(ctypes.byref(Lb), O._fp(x), O._fp(Hb), ex, ey, 6, 7, O._fp(ob))
+            assert np.array_equal(oa, ob) and np.array_equal(Ha, Hb), (in_dim, D, k)
+
+
 def test_zero_weights_reduce_to_layernorm_of_residual():
     D, i = 48, 24
     z = lambda *s: np.zeros(s, np.float32)
