@@ -305,6 +305,23 @@ int ssla_hip_persistent_start(const HybridS2S3Config* cfg,
                               const SslaHipLiveOpts* opts,
                               SslaHipLive** out);
 
+/* Two-ring form of ssla_hip_persistent_start: the signature of the
+ * reference's legacy live kernel k_ssla_s2s3_celled_persistent(cfg, ring0,
+ * ring1, ring_mask, tail0, tail1, stop_flag, events_done0, events_done1,
+ * spin_ns) (orin/kernels/ssla_s2_s3_head_celled.cuh:1271-1281, launched
+ * with a grid of 2 by orin/hybrid_runner.py:334-393).  cfg->n_blocks must be
+ * 2 (block b drains ring b).  As in that kernel, each block is one
+ * workgroup taking records in batches of up to 8; the idle timeout is the
+ * default 30 s.  Stop it with *stop_flag and ssla_hip_persistent_wait. */
+int ssla_hip_persistent_start2(const HybridS2S3Config* cfg,
+                               HybridInputRec* ring0, HybridInputRec* ring1,
+                               unsigned long long ring_mask,
+                               unsigned long long* tail0, unsigned long long* tail1,
+                               int* stop_flag,
+                               unsigned long long* events_done0,
+                               unsigned long long* events_done1,
+                               unsigned int spin_ns, SslaHipLive** out);
+
 /* Waits (up to timeout_ms, < 0 = forever) for the kernel to return after
  * the caller set *stop_flag, then frees the session.  *status: 0 stopped
  * by the flag, 2 ring overrun, 3 idle timeout, 4 a group member's wait

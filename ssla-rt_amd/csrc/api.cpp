@@ -737,6 +737,25 @@ int ssla_hip_persistent_start(const HybridS2S3Config* cfg, HybridInputRec* const
     return rc;
 }
 
+int ssla_hip_persistent_start2(const HybridS2S3Config* cfg, HybridInputRec* ring0,
+                               HybridInputRec* ring1, unsigned long long ring_mask,
+                               unsigned long long* tail0, unsigned long long* tail1,
+                               int* stop_flag, unsigned long long* events_done0,
+                               unsigned long long* events_done1, unsigned int spin_ns,
+                               SslaHipLive** out) {
+    if (!cfg || cfg->n_blocks != 2) {
+        set_error("the two-ring persistent drain needs cfg->n_blocks == 2");
+        return SSLA_ERR_ARG;
+    }
+    HybridInputRec* rings[2] = {ring0, ring1};
+    unsigned long long* tails[2] = {tail0, tail1};
+    unsigned long long* dones[2] = {events_done0, events_done1};
+    SslaHipLiveOpts opts{};
+    opts.max_batch = 8;
+    return ssla_hip_persistent_start(cfg, rings, ring_mask, tails, stop_flag, dones, spin_ns,
+                                     &opts, out);
+}
+
 int ssla_hip_persistent_wait(SslaHipLive* h, int timeout_ms, int* status) {
     return live_wait(reinterpret_cast<LiveSession*>(h), timeout_ms, status);
 }

@@ -63,6 +63,18 @@ struct BlockDesc {
     int                   offset;
 };
 
+// The block table travels to the device as kernel arguments: the runtime
+// copies them at launch, so a call never waits on the host for a staging
+// buffer the previous call may still be reading.
+struct BlockTable {
+    BlockDesc d[SSLA_MAX_BLOCKS];
+};
+static_assert(sizeof(BlockTable) <= 3072, "kernel argument block");
+
+__global__ void k_put_blocks(BlockTable t, BlockDesc* __restrict__ dst) {
+    if (threadIdx.x < SSLA_MAX_BLOCKS) dst[threadIdx.x] = t.d[threadIdx.x];
+}
+
 __device__ __forceinline__ int find_block(const BlockDesc* bd, int nb, int g) {
     int b = 0;
     for (int i = 1; i < nb; ++i)
@@ -1899,8 +1911,6 @@ struct Workspace {
     unsigned char *owner, *pass2, *pass3;
     uint32_t *ka, *kb, *va, *vb, *key3g;
     BlockDesc* bd;
-    BlockDesc* bd_host = nullptr;      // pinned staging of the block table
-    hipEvent_t bd_copied = nullptr;    // the last staging copy has been read
     hipEvent_t done = nullptr;         // the last drain's work on the workspace
     hipStream_t side = nullptr;        // s3 ordering, concurrent with L4 and L5
     hipEvent_t s2_ordered = nullptr;   // s2 tables and pass2 are complete
@@ -2032,10 +2042,7 @@ int ensure_workspace(int E, int nkeys) {
         HIPCHK(hipHostMalloc((void**)&w.scan_err, sizeof(int), hipHostMallocCoherent));
         *w.scan_err = 0;
     }
-    if (!w.bd_host) {
-        HIPCHK(hipHostMalloc((void**)&w.bd_host, sizeof(BlockDesc) * SSLA_MAX_BLOCKS,
-                             hipHostMallocDefault));
-        HIPCHK(hipEventCreateWithFlags(&w.bd_copied, hipEventDisableTiming));
+    if (!w.done) {
         HIPCHK(hipEventCreateWithFlags(&w.done, hipEventDisableTiming));
         HIPCHK(hipEventCreateWithFlags(&w.s2_ordered, hipEventDisableTiming));
         HIPCHK(hipEventCreateWithFlags(&w.s3_ordered, hipEventDisableTiming));
@@ -2197,7 +2204,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     Workspace& w = g_ws;
     CallEnd end{w, st};
 
-    BlockDesc hbd[SSLA_MAX_BLOCKS] = {};
+    BlockTable tab;
+    std::memset(&tab, 0, sizeof tab);
+    BlockDesc* hbd = tab.d;
     int off = 0;
     for (int b = 0; b < nb; ++b) {
         BlockDesc& d = hbd[b];
@@ -2220,12 +2229,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // Calls share one workspace: a call on another stream runs after the
     // previous call's kernels (device-side wait, the host does not block).
     HIPCHK(hipStreamWaitEvent(st, w.done, 0));
-    // The staging buffer may still be the source of the previous call's
-    // copy; wait for that copy before overwriting it.
-    HIPCHK(hipEventSynchronize(w.bd_copied));
-    std::memcpy(w.bd_host, hbd, sizeof(hbd));
-    HIPCHK(hipMemcpyAsync(w.bd, w.bd_host, sizeof(hbd), hipMemcpyHostToDevice, st));
-    HIPCHK(hipEventRecord(w.bd_copied, st));
+    hipLaunchKernelGGL(k_put_blocks, dim3(1), dim3(64), 0, st, tab, w.bd);
+    HIPCHK(hipGetLastError());
 
     // Phase timing (optional): events recorded on `st` at the boundaries of
     // the phases in pmask only -- each event costs a few microseconds of

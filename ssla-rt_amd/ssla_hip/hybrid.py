@@ -527,14 +527,24 @@ class HostRings:
 
 
 class LiveDrain:
-    """A running persistent drain over HostRings (ssla_hip_persistent_start)."""
+    """A running persistent drain over HostRings (ssla_hip_persistent_start;
+    with two_ring=True the legacy two-ring entry ssla_hip_persistent_start2,
+    orin/hybrid_runner.py:334-393, which fixes batches of 8 and one
+    workgroup per block)."""
 
     def __init__(self, drain: Drain, rings: HostRings, spin_ns: int = 200, max_batch: int = 32,
                  idle_timeout_ms: int = 30000, profile: bool = False, group: int = 0,
-                 stages: int = 1):
+                 stages: int = 1, two_ring: bool = False):
         self.rings = rings
         self.h = ctypes.c_void_p()
         bufs, tails, dones = rings.ptrs()
+        self.phase_us = None
+        if two_ring:
+            lib.check(lib.load().ssla_hip_persistent_start2(
+                ctypes.byref(drain.cfg), bufs[0], bufs[1], rings.capacity - 1, tails[0],
+                tails[1], rings.stop_ptr, dones[0], dones[1], spin_ns, ctypes.byref(self.h)),
+                "persistent_start2")
+            return
         # in-kernel phase profile, filled by wait() (abi.BATCH_PHASES order)
         self.phase_us = np.zeros(abi.N_BATCH_PHASES, np.float64) if profile else None
         opts = abi.SslaHipLiveOpts(max_batch, idle_timeout_ms)

@@ -63,6 +63,9 @@ _SIGNATURES = {
                                        ctypes.c_ulonglong, ctypes.POINTER(_VP), _VP,
                                        ctypes.POINTER(_VP), ctypes.c_uint,
                                        ctypes.POINTER(abi.SslaHipLiveOpts), ctypes.POINTER(_VP)]),
+    "ssla_hip_persistent_start2": (_I, [ctypes.POINTER(abi.HybridS2S3Config), _VP, _VP,
+                                        ctypes.c_ulonglong, _VP, _VP, _VP, _VP, _VP,
+                                        ctypes.c_uint, ctypes.POINTER(_VP)]),
     "ssla_hip_persistent_wait": (_I, [_VP, _I, ctypes.POINTER(_I)]),
     "ssla_hip_preds_snapshot": (_I, [_FP, _UP, _I, _I, _FP, _UP, _I]),
     "ssla_hip_decode_cells": (_I, [_FP, _I, _I, _I, _I, _I, _I, _I, _FP]),

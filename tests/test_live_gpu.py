@@ -212,6 +212,50 @@ def test_live_four_streams(H, stub_dir, stub_npz):
         rings.free()
 
 
+def test_live_two_ring_legacy_entry(H, stub_dir, stub_npz):
+    """The legacy two-ring persistent entry (ssla_hip_persistent_start2, the
+    signature of orin/kernels/ssla_s2_s3_head_celled.cuh:1271-1281): two
+    rings fed in turns, each block's state, counters, timing slots and
+    prediction grid equal the oracle run over its ring."""
+    n = 1500
+    say("live two-ring legacy entry", n)
+    recs = [events.blob_records(n, seed=30 + b) for b in range(2)]
+    with H.Drain.from_weights_dir(stub_dir, n_blocks=2) as d:
+        d.alloc_timing(2048)
+        rings = H.HostRings(2, capacity=512)
+        live = H.LiveDrain(d, rings, idle_timeout_ms=15000, two_ring=True)
+        try:
+            packed = [events.to_records(r) for r in recs]
+            for k in range(0, n, 100):
+                for b in range(2):
+                    _produce(rings, b, packed[b][k:k + 100])
+            for b in range(2):
+                _wait_done(rings, b, n)
+        finally:
+            status = live.stop()
+        assert status == 0
+        for b in range(2):
+            assert int(rings.done[b]) == n
+            st, p2, p3, feat, ref7 = oracle_run(stub_npz, recs[b])
+            ts = d.timing(b)[:n]
+            assert np.array_equal(ts["owner"], (p3 == 1).astype(np.uint32)), b
+            for li in range(4):
+                assert hidden_close(d.hidden(b, li), st.H[li]), (b, li)
+            td2, td3 = d.counters(b)
+            assert np.array_equal(td2, st.td2) and np.array_equal(td3, st.td3)
+            check_preds(*d.preds(b), recs[b], p3, ref7)
+        rings.free()
+
+
+def test_live_two_ring_entry_rejects_other_block_counts(H, stub_dir):
+    from ssla_hip import lib
+    with H.Drain.from_weights_dir(stub_dir, n_blocks=1) as d:
+        rings = H.HostRings(2, capacity=64)
+        with pytest.raises(lib.SslaHipError):
+            H.LiveDrain(d, rings, two_ring=True)
+        rings.free()
+
+
 def test_live_idle_timeout_exits(H, stub_dir):
     say("live idle timeout")
     with H.Drain.from_weights_dir(stub_dir) as d:
