@@ -178,7 +178,11 @@ typedef struct SslaHipDrainOpts {
                                   owned pass-3 records, zeros otherwise */
     float*        phase_ms;    /* NULL or host float[SSLA_DRAIN_PHASES]:
                                   adds the GPU time of each phase, measured
-                                  with HIP events on `stream` (needs sync) */
+                                  with HIP events on `stream`.  With sync
+                                  = 0 the times are added when a later
+                                  whole-ring call with sync set returns
+                                  (keep the array alive until then), so
+                                  timed calls can be queued back to back */
     double*       batch_phase_us; /* NULL or host double[SSLA_BATCH_PHASES]:
                                   batch mode only (needs sync); adds the
                                   in-kernel wall-clock profile */

@@ -612,7 +612,6 @@ int ssla_hip_drain_n_ex(const HybridS2S3Config* cfg, const HybridInputRec* const
     hipStream_t st = opts ? static_cast<hipStream_t>(opts->stream) : nullptr;
     const bool sync = opts ? opts->sync != 0 : true;
     float* phase_ms = opts ? opts->phase_ms : nullptr;
-    if (phase_ms && !sync) { set_error("phase_ms needs sync"); return SSLA_ERR_ARG; }
     const int batch = opts ? opts->batch : 0;
     double* bph = opts ? opts->batch_phase_us : nullptr;
     const int group = opts ? opts->group : 0;

@@ -63,17 +63,14 @@ struct BlockDesc {
     int                   offset;
 };
 
-// The block table travels to the device as kernel arguments: the runtime
-// copies them at launch, so a call never waits on the host for a staging
-// buffer the previous call may still be reading.
+// The block table travels to the device as kernel arguments of k_decode
+// (the runtime copies them at launch, so a call never waits on the host for
+// a staging buffer the previous call may still be reading); k_decode reads
+// it there and writes the copy the later kernels read.
 struct BlockTable {
     BlockDesc d[SSLA_MAX_BLOCKS];
 };
-static_assert(sizeof(BlockTable) <= 3072, "kernel argument block");
-
-__global__ void k_put_blocks(BlockTable t, BlockDesc* __restrict__ dst) {
-    if (threadIdx.x < SSLA_MAX_BLOCKS) dst[threadIdx.x] = t.d[threadIdx.x];
-}
+static_assert(sizeof(BlockTable) <= 2048, "kernel argument block");
 
 __device__ __forceinline__ int find_block(const BlockDesc* bd, int nb, int g) {
     int b = 0;
@@ -97,23 +94,40 @@ struct FillSet {
     int v[kFills];
 };
 
+// One launch for the call's set-up: blocks [0, ndec) decode the records,
+// then fblk blocks per fill array, then npk blocks rebuild the fragment-order
+// weight copies (one float per thread), and the last block writes the block
+// table for the later kernels.  Nothing in this launch reads what another of
+// its blocks writes.
 __global__ void __launch_bounds__(256)
-k_decode(int E, const BlockDesc* __restrict__ bd, Geometry G,
+k_decode(int E, BlockTable tab, BlockDesc* __restrict__ bd_out, Geometry G,
          float* __restrict__ X0, int* __restrict__ cell2,
          unsigned char* __restrict__ owner,
-         uint32_t* __restrict__ key2, uint32_t* __restrict__ val2, int ndec, FillSet f, int fblk) {
+         uint32_t* __restrict__ key2, uint32_t* __restrict__ val2, int ndec, FillSet f, int fblk,
+         PackSrc ps, float* __restrict__ pbuf, int npk) {
+    const int nfill = fblk * kFills;
     if ((int)blockIdx.x >= ndec) {
-        // the call's fills: fblk blocks of 256 per array
-        const int fb = (int)blockIdx.x - ndec, a = fb / fblk;
-        const int i = (fb - a * fblk) * 256 + (int)threadIdx.x;
-        if (i < f.n[a]) f.p[a][i] = f.v[a];
+        const int xb = (int)blockIdx.x - ndec;
+        if (xb < nfill) {
+            // the call's fills: fblk blocks of 256 per array
+            const int a = xb / fblk;
+            const int i = (xb - a * fblk) * 256 + (int)threadIdx.x;
+            if (i < f.n[a]) f.p[a][i] = f.v[a];
+        } else if (xb < nfill + npk) {
+            const size_t q = (size_t)(xb - nfill) * 256 + threadIdx.x;
+            if (q < PackLayout<true>::off[8]) pack_elem<true>(ps, pbuf, q);
+        } else if (threadIdx.x < SSLA_MAX_BLOCKS) {
+            bd_out[threadIdx.x] = tab.d[threadIdx.x];
+        }
         return;
     }
     const int g = blockIdx.x * kDecRec + (threadIdx.x >> 3);
     const int c = threadIdx.x & 7;
     if (g >= E) return;
-    const int b = find_block(bd, G.nb, g);
-    const HybridInputRec* r = bd[b].ring + (g - bd[b].offset);
+    int b = 0;
+    for (int i = 1; i < G.nb; ++i)
+        if (g >= tab.d[i].offset) b = i;
+    const HybridInputRec* r = tab.d[b].ring + (g - tab.d[b].offset);
     const float4 v = reinterpret_cast<const float4*>(r)[c];
     const int x = r->x, y = r->y;
     const bool valid = x < G.W2 && y < G.H2;
@@ -121,7 +135,7 @@ k_decode(int E, const BlockDesc* __restrict__ bd, Geometry G,
         reinterpret_cast<float4*>(X0 + (size_t)g * SSLA_C1)[c - 1] =
             valid ? v : make_float4(0.f, 0.f, 0.f, 0.f);
     if (c != 0) return;
-    const HybridStrip& s = bd[b].strip;
+    const HybridStrip& s = tab.d[b].strip;
     owner[g] = (valid && x >= s.owned_lo && x < s.owned_hi &&
                 y >= s.owned_y_lo && y < s.owned_y_hi) ? 1 : 0;
     const uint32_t none = (uint32_t)(G.nb * G.C2);
@@ -1466,6 +1480,15 @@ __device__ __forceinline__ double sum4_lanes(double v, int lane) {
     return v + xor_lanes_d(v, (lane ^ 32) << 2, false);
 }
 
+// L5-L7 contraction launch shape: 16-record tiles (RT = 1), the nine deltas
+// split over three waves (KS = 3).  Measured at 200k records: nine waves per
+// tile (one delta each) took L5.out 61 -> 91 us and L6.out 146 -> 214 us
+// (L7 spills at the 168-register cap of nine waves); two record tiles per
+// wave left L5.out unchanged and took L6.out to 161 us (L7: 202 registers,
+// one wave per SIMD).
+constexpr int kOutKS5 = 3, kOutKS6 = 3, kOutKS7 = 3;
+constexpr int kOutRT5 = 1, kOutRT6 = 1, kOutRT7 = 1;
+
 template <int IN, int OUT, int RT, int KS, int WPS = 1, int HS = 2 * OUT>
 __global__ void __launch_bounds__(64 * KS, WPS)
 k_outt(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
@@ -1922,7 +1945,42 @@ struct Workspace {
     int clk_khz = 0;                   // wall-clock (s_memrealtime) rate
     float* packed = nullptr;           // fragment-order weight copies (packed_weight_floats_d)
     PackedWeights pk = {};
+    // phase timings of calls made without sync: their events, read and added
+    // to the caller's array when a later call with sync returns
+    struct Pending {
+        hipEvent_t ev[SSLA_DRAIN_PHASES + 1];
+        float* phase_ms;
+        unsigned long long pmask;
+    };
+    std::vector<Pending> pending;
 };
+constexpr size_t kMaxPending = 256;    // more waiting calls: the oldest is waited for
+
+// Adds the phase times of the oldest `n` pending calls to their arrays and
+// frees their events (waiting for each event first).
+int flush_pending(Workspace& w, size_t n) {
+    n = std::min(n, w.pending.size());
+    int rc = SSLA_OK;
+    for (size_t i = 0; i < n; ++i) {
+        Workspace::Pending& p = w.pending[i];
+        for (int k = 0; k < SSLA_DRAIN_PHASES && rc == SSLA_OK; ++k) {
+            if (!((p.pmask >> k) & 1ull) || !p.ev[k] || !p.ev[k + 1]) continue;
+            float ms = 0.f;
+            hipError_t e = hipEventSynchronize(p.ev[k + 1]);
+            if (e == hipSuccess) e = hipEventElapsedTime(&ms, p.ev[k], p.ev[k + 1]);
+            if (e != hipSuccess) {
+                set_error(std::string("drain phase timing: ") + hipGetErrorString(e));
+                rc = SSLA_ERR_HIP;
+                break;
+            }
+            p.phase_ms[k] += ms;
+        }
+        for (int k = 0; k <= SSLA_DRAIN_PHASES; ++k)
+            if (p.ev[k]) (void)hipEventDestroy(p.ev[k]);
+    }
+    w.pending.erase(w.pending.begin(), w.pending.begin() + n);
+    return rc;
+}
 
 std::mutex g_ws_mu;
 Workspace g_ws;
@@ -2229,8 +2287,6 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // Calls share one workspace: a call on another stream runs after the
     // previous call's kernels (device-side wait, the host does not block).
     HIPCHK(hipStreamWaitEvent(st, w.done, 0));
-    hipLaunchKernelGGL(k_put_blocks, dim3(1), dim3(64), 0, st, tab, w.bd);
-    HIPCHK(hipGetLastError());
 
     // Phase timing (optional): events recorded on `st` at the boundaries of
     // the phases in pmask only -- each event costs a few microseconds of
@@ -2255,9 +2311,9 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     };
 #define MARK() do { const int rc_ = mark(); if (rc_) return rc_; } while (0)
     // fragment-order copies of the layer weights for the MFMA kernels, rebuilt
-    // by every call (one launch of a few microseconds), so weights rewritten in
-    // place by any means are always the ones used
-    HIPCHK(pack_weights_d(cfg->layers[0], w.packed, &w.pk, st));
+    // by every call (in k_decode's launch), so weights rewritten in place by
+    // any means are always the ones used
+    const PackSrc psrc = pack_setup<true>(cfg->layers[0], w.packed, &w.pk);
     const PackedWeights& pk = w.pk;
     MARK();
     // per-call fills: run bounds of the s2 keys (k_runs writes those that
@@ -2279,8 +2335,10 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     // ---- decode (and the fills); stable radix sort of the records by s2 key --
     {
         const int ndec = (int)grid1(E, kDecRec), fblk = (int)grid1(std::max<int>(std::max<int>((int)nk2, 16), nv3), 256);
-        hipLaunchKernelGGL(k_decode, dim3(ndec + fblk * kFills), dim3(256), 0, st, E, w.bd, G,
-                           w.X0, w.cell2, w.owner, w.ka, w.va, ndec, f, fblk);
+        const int npk = (int)((PackLayout<true>::off[8] + 255) / 256);
+        hipLaunchKernelGGL(k_decode, dim3(ndec + fblk * kFills + npk + 1), dim3(256), 0, st, E, tab,
+                           w.bd, G, w.X0, w.cell2, w.owner, w.ka, w.va, ndec, f, fblk, psrc,
+                           w.packed, npk);
     }
     const int bits2 = bits_for(nk2);
     const int passes = (bits2 + kRMaxBits - 1) / kRMaxBits;
@@ -2438,7 +2496,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)nullptr, (const int*)nullptr, w.X1, w.pos2, pk.pp[1], w.QVG, w.trash);
     MARK();
     SCAN1(SSLA_C2, SSLA_C2, kSG, 1, 2, 6, w.glist, w.pneed2, Hc, G.C2, groups2);
-    hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C2, 1, 3, 1, SSLA_C2>), dim3(grid1(nmax2, 16)), dim3(192), 0,
+    hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C2, kOutRT5, kOutKS5, 1, SSLA_C2>), dim3(grid1(nmax2, 16 * kOutRT5)),
+                       dim3(64 * kOutKS5), 0,
                        st, E, (const int*)(w.counts + 0), w.list2, w.X1, w.pos2, Hc, pk.po[1],
                        L[1].ln_gamma, L[1].ln_beta, w.X2);
     MARK();
@@ -2448,7 +2507,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, pk.pp[2], w.QVG, w.trash);
     MARK();
     SCAN1(SSLA_C3, 2 * SSLA_C3, kSG3, 2, 3, 7, w.glist3, all, w.QVG, G.C3, groups3);
-    hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C3, 1, 3>), dim3(grid1(nmax2, 16)), dim3(192), 0, st, E,
+    hipLaunchKernelGGL((k_outt<SSLA_C2, SSLA_C3, kOutRT6, kOutKS6>), dim3(grid1(nmax2, 16 * kOutRT6)),
+                       dim3(64 * kOutKS6), 0, st, E,
                        (const int*)(w.counts + 0), w.list2, w.X2, w.pos3, w.QVG, pk.po[2],
                        L[2].ln_gamma, L[2].ln_beta, w.X3);
     MARK();
@@ -2457,7 +2517,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
                        (const int*)(w.counts + 0), w.list2, w.X3, w.pos3, pk.pp[3], w.QVG, w.trash);
     MARK();
     SCAN1(SSLA_C3, 2 * SSLA_C3, kSG3, 3, 3, 7, w.glist3, w.pneed3, w.QVG, G.C3, groups3);
-    hipLaunchKernelGGL((k_outt<SSLA_C3, SSLA_C3, 1, 3>), dim3(grid1(nmax3, 16)), dim3(192), 0, st, E,
+    hipLaunchKernelGGL((k_outt<SSLA_C3, SSLA_C3, kOutRT7, kOutKS7>), dim3(grid1(nmax3, 16 * kOutRT7)),
+                       dim3(64 * kOutKS7), 0, st, E,
                        (const int*)(w.counts + 1), w.list3, w.X3, w.pos3, w.QVG, pk.po[3],
                        L[3].ln_gamma, L[3].ln_beta, w.X4);
     MARK();
@@ -2483,20 +2544,31 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
 #undef MARK
 #undef SCAN1
     end.finish();
+    if (phase_ms) {
+        // this call's events join the pending ones (read below when sync is
+        // set, else by a later call with sync)
+        if (w.pending.size() >= kMaxPending) {
+            const int rc = flush_pending(w, 1);
+            if (rc) return rc;
+        }
+        Workspace::Pending p;
+        for (int k = 0; k <= SSLA_DRAIN_PHASES; ++k) {
+            p.ev[k] = ev[k];
+            ev[k] = nullptr;
+        }
+        p.phase_ms = phase_ms;
+        p.pmask = pmask;
+        w.pending.push_back(p);
+    }
     if (sync) {
         HIPCHK(hipStreamSynchronize(st));
         if (__atomic_exchange_n(w.scan_err, 0, __ATOMIC_RELAXED)) {
             set_error("drain: a wait of the one-pass scan ran out (results are invalid)");
             return SSLA_ERR_HIP;
         }
-    }
-    if (phase_ms) {
-        for (int k = 0; k < SSLA_DRAIN_PHASES; ++k) {
-            if (!((pmask >> k) & 1ull) || !ev[k] || !ev[k + 1]) continue;
-            float ms = 0.f;
-            HIPCHK(hipEventElapsedTime(&ms, ev[k], ev[k + 1]));
-            phase_ms[k] += ms;
-        }
+        // every earlier call finished before this one's kernels started
+        const int rc = flush_pending(w, w.pending.size());
+        if (rc) return rc;
     }
     return SSLA_OK;
 }

@@ -225,12 +225,10 @@ __device__ __forceinline__ float out_any(const float* qvgIn, const float* goW, c
     else return out_elem<IN, OUT>(goW, ip, q);
 }
 
-// All eight copies in one launch, one thread per packed float.
+// Packed float q of all eight copies (q < PackLayout<D>::off[8]).
 template <bool D>
-__global__ void k_pack_all(PackSrc s, float* __restrict__ buf) {
+__device__ __forceinline__ void pack_elem(const PackSrc& s, float* __restrict__ buf, size_t q) {
     using L = PackLayout<D>;
-    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= L::off[8]) return;
     float v;
     if (q < L::off[1]) v = proj_elem<SSLA_C1, SSLA_C2>(s.qvgIn[0], q);
     else if (q < L::off[2]) v = out_any<SSLA_C1, SSLA_C2, D>(s.qvgIn[0], s.goW[0], s.ip[0], q - L::off[1]);
@@ -243,15 +241,22 @@ __global__ void k_pack_all(PackSrc s, float* __restrict__ buf) {
     buf[q] = v;
 }
 
+// All eight copies in one launch, one thread per packed float.
+template <bool D>
+__global__ void k_pack_all(PackSrc s, float* __restrict__ buf) {
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q < PackLayout<D>::off[8]) pack_elem<D>(s, buf, q);
+}
+
 template <bool D>
 inline size_t packed_floats() { return PackLayout<D>::off[8]; }
 
 inline size_t packed_weight_floats() { return packed_floats<false>(); }
 inline size_t packed_weight_floats_d() { return packed_floats<true>(); }
 
+// The sources of the eight copies, and where each lands in buf.
 template <bool D>
-inline hipError_t pack_all(const LayerWeightsS2S3* L, float* buf, PackedWeights* out,
-                           hipStream_t st) {
+inline PackSrc pack_setup(const LayerWeightsS2S3* L, float* buf, PackedWeights* out) {
     using PL = PackLayout<D>;
     PackSrc s{};
     for (int i = 0; i < 4; ++i) {
@@ -261,6 +266,14 @@ inline hipError_t pack_all(const LayerWeightsS2S3* L, float* buf, PackedWeights*
         out->pp[i] = buf + PL::off[2 * i];
         out->po[i] = buf + PL::off[2 * i + 1];
     }
+    return s;
+}
+
+template <bool D>
+inline hipError_t pack_all(const LayerWeightsS2S3* L, float* buf, PackedWeights* out,
+                           hipStream_t st) {
+    using PL = PackLayout<D>;
+    const PackSrc s = pack_setup<D>(L, buf, out);
     constexpr int TB = 256;
     hipLaunchKernelGGL((k_pack_all<D>), dim3((unsigned)((PL::off[8] + TB - 1) / TB)), dim3(TB), 0,
                        st, s, buf);

@@ -331,9 +331,10 @@ class Drain:
             batch: int = 0, batch_phase_us: Optional[np.ndarray] = None, group: int = 0,
             phase_mask: int = 0) -> None:
         """One drain call over the loaded rings.  phase_ms (float32 array of
-        len(abi.DRAIN_PHASES)) accumulates per-phase GPU time (needs sync) of
-        the phases in phase_mask (bit k = phase k; 0 = all).  group (batch
-        mode): workgroups per block, 3..6 (0 = one)."""
+        len(abi.DRAIN_PHASES)) accumulates per-phase GPU time of the phases
+        in phase_mask (bit k = phase k; 0 = all); a call without sync adds
+        its times when a later call with sync returns.  group (batch mode):
+        workgroups per block, 3..6 (0 = one)."""
         nb = self.cfg.n_blocks
         if len(self._rings) != nb:
             raise ValueError(f"load_rings needs {nb} rings")

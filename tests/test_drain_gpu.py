@@ -478,6 +478,34 @@ def test_640x480_full_size_properties(H, stub_640):
         say(f"640x480 full size: {int((d3 == 1).sum())} pass3 records")
 
 
+def test_phase_times_of_queued_calls(H, stub_dir, stub_npz):
+    """Phase times of calls queued without sync are added when a later call
+    with sync returns: five calls (four queued) give about five times one
+    call's phase times, and the results are the oracle's."""
+    rec = events.blob_records(20000, seed=41)
+    nph = len(abi.DRAIN_PHASES)
+    with H.Drain.from_weights_dir(stub_dir) as d:
+        d.load_rings([events.to_records(rec)])
+        one = np.zeros(nph, np.float32)
+        d.reset()
+        d.run(sync=True, phase_ms=one)
+        four = np.zeros(nph, np.float32)
+        for i in range(4):
+            d.reset(sync=False)
+            d.run(sync=False, phase_ms=four)
+            if i < 3:
+                assert np.all(four == 0), "a queued call's times were added before a sync"
+        d.reset(sync=False)
+        d.run(sync=True, phase_ms=four)
+        say(f"phase times: one call {one.sum():.3f} ms, five calls {four.sum():.3f} ms")
+        assert one.sum() > 0
+        assert 3.0 * one.sum() < four.sum() < 8.0 * one.sum()
+        (a,), _ = d.results()
+        st = O.S2S3(O.layers_from_npz(stub_npz), 16, 20, 4)
+        p2, p3, feat, _ = st.run(rec.x, rec.y, rec.feat1)
+        compare(a, p2, p3, feat, "after queued calls")
+
+
 def test_weights_rewritten_in_place_between_calls(H, stub_dir, stub_npz, tmp_path):
     """The whole-ring drain uses the weights the configuration points at when
     it is called: L5's weights are rewritten in place between two drains by
