@@ -153,10 +153,9 @@ int ssla_hip_drain_n2(const HybridS2S3Config* cfg,
  * layer a projection of v, g, the recurrence in three slots, then the
  * contraction (q, q*h, goW, residual, LayerNorm): L4 1-5, L5 6-10, L6
  * 11-15, L7 16-20; 21 head and prediction grid, 22 output slots.  The
- * recurrence of L6 and L7 is three launches (summary, carry, apply); that
- * of L4 and L5 is one launch in the third slot (the first holds the wait
- * for its ticket order, built beside L4's projection; the second is
- * empty). */
+ * recurrence of every layer is one launch, in the third of its slots; the
+ * first holds L4's wait for its ticket order (built beside L4's
+ * projection) and is empty for L5-L7, and the second is empty. */
 
 #define SSLA_BATCH_PHASES 32
 /* Slots of the in-kernel batch profile (batch-mode and live drains), summed

@@ -2398,10 +2398,10 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     }
     // The s3 ordering needs only the s2 order, pass2 and the old counters, so
     // it runs on the side stream while L4 and L5 run here; L6 waits for it.
-    // Every launch is sized by E; the pass-2 count stays on the device.  Its
-    // event sits before L4's projection: started later, the side stream's
-    // small kernels overlap L4's carry pass, a latency-bound chain per cell
-    // that they slow down by more than the event's queue gap costs here.
+    // Its launches are sized by E; the pass-2 count stays on the device.  Its
+    // event sits before L4's projection, so the side stream's small kernels
+    // start beside the projection rather than beside the latency-bound parts
+    // that follow it.
     HIPCHK(hipEventRecord(w.s2_ordered, st));
     hipStream_t s3 = w.side;
     HIPCHK(hipStreamWaitEvent(s3, w.s2_ordered, 0));
@@ -2429,9 +2429,8 @@ int scan_drain(const HybridS2S3Config* cfg, const HybridInputRec* const* rings,
     float* const Hc = w.QVG + (size_t)w.cap * kPatch * 2 * SSLA_C2;
     // S: the recurrence of layer LI over the chunk tables of level LV (2: s2,
     // 3: s3; n_chunks in counts[NC]), h written at HOUT (rows of HS floats)
-    // where the pair's record needs the output (NEED, or every pair): the
-    // s2 layers in one pass (k_scan, ticket counters counts[4 + LI], group
-    // count counts[6]), the s3 layers in three (summary, carry, apply).
+    // where the pair's record needs the output (NEED, or every pair), in one
+    // pass (k_scan; ticket counter counts[8 + LI], group count counts[NG]).
     const unsigned long long wait_ticks = (unsigned long long)std::max(w.clk_khz, 1) * 500ull;
 #define SCAN1(OUT, HS, SGV, LI, LV, NG, GL, NEED, HOUT, CELLS, GRID)                                  \
     do {                                                                                            \
