@@ -68,16 +68,24 @@ __device__ __forceinline__ float sigmoid_fast(float x) {
 // Bit 31 of a prediction cell's version marks a write in progress.
 constexpr unsigned kPredBusy = 0x80000000u;
 
+// A prediction cell's version word (fine-grained host memory) without the
+// busy bit, or 0 for none.
+__device__ __forceinline__ unsigned pred_version(const unsigned* version) {
+    return version ? __hip_atomic_load(const_cast<unsigned*>(version), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM) & ~kPredBusy
+                   : 0u;
+}
+
 // Publishes one prediction-grid cell (fine-grained host memory) for
 // concurrent host readers: the version's busy bit is set, the seven values
 // are stored between two system-scope fences, and the version ends at
 // old + count with the bit clear -- so a reader that sees the same version
 // before and after copying a cell, without the bit, has a whole cell.
-__device__ __forceinline__ void publish_pred(float* preds7, unsigned* version, const float* v7,
-                                             unsigned count) {
-    unsigned old = 0;
+// `old` is the cell's version read beforehand (pred_version): the device is
+// the cell's only writer, so the word cannot change in between.
+__device__ __forceinline__ void publish_pred_at(float* preds7, unsigned* version, const float* v7,
+                                                unsigned count, unsigned old) {
     if (version) {
-        old = __hip_atomic_load(version, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) & ~kPredBusy;
         __hip_atomic_store(version, old | kPredBusy, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         __threadfence_system();
     }
@@ -90,6 +98,11 @@ __device__ __forceinline__ void publish_pred(float* preds7, unsigned* version, c
         __hip_atomic_store(version, (old + count) & ~kPredBusy, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_SYSTEM);
     }
+}
+
+__device__ __forceinline__ void publish_pred(float* preds7, unsigned* version, const float* v7,
+                                             unsigned count) {
+    publish_pred_at(preds7, version, v7, count, pred_version(version));
 }
 
 }  // namespace ssla

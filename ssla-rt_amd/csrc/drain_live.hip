@@ -588,57 +588,93 @@ __device__ __forceinline__ void batch_layer(Lds& S, int B, const unsigned char* 
 // Two-branch YOLOX head of the nh records listed in S.ol: hidden layers
 // y = SiLU(W x + b) of both branches (one thread per weight column), then
 // the seven outputs [reg0..3, obj, cls0, cls1] (one wave per record).
+// The two-branch head of the batch's nh output records (indices in S.ol).
+// Hidden layers y = SiLU(W x + b) of both branches as 16 x 16 x 4 MFMA tiles
+// over all waves: items (row tile of 16 records, branch, 32 output
+// channels as two 16-column tiles), A = the records' features (LDS), B =
+// the (IN, OUT) row-major weights read straight from memory (lane (li, lk)
+// takes row 4 s + lk, column li of step s).  Six items per row tile, so a
+// wave's weights arrive in one load round.  Then the seven outputs, one
+// wave per record, with the output weights of the lane's channels loaded
+// before the hidden layers.
 template <class SL>
 __device__ __forceinline__ void batch_head_yolox(SL& S, int nh, const LiveWeights& W) {
-    constexpr int C = SSLA_C3;
-    const int tid = threadIdx.x;
-    if (tid < 2 * C) {
-        const int br = tid / C, o = tid - br * C;
-        const float* Wc = (br == 0 ? W.head.cls_conv_W : W.head.reg_conv_W) + o;
-        const float bias = (br == 0 ? W.head.cls_conv_b : W.head.reg_conv_b)[o];
-        for (int r0 = 0; r0 < nh; r0 += 8) {
-            int off[8];
-            float acc[8];
-            #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                off[r] = S.ol[min(r0 + r, nh - 1)] * XS;
-                acc[r] = bias;
-            }
-            coldot8<C>(Wc, C, &S.X[0][0], off, acc);
-            #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                if (r0 + r >= nh) break;
-                const int e = S.ol[r0 + r];
-                const float y = acc[r] * sigmoid_fast(acc[r]);
-                if (br == 0) S.Y[e][o] = y;
-                else S.R[e][o] = y;
+    constexpr int C = SSLA_C3, KS = C / 4, NT = C / (2 * MT);
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lk = lane >> 4;
+    float wo[2][7];
+    #pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = lane + 64 * h;
+        const bool in = i < C;
+        #pragma unroll
+        for (int k = 0; k < 4; ++k) wo[h][k] = in ? W.head.reg_pred_W[(size_t)i * 4 + k] : 0.f;
+        wo[h][4] = in ? W.head.obj_pred_W[i] : 0.f;
+        wo[h][5] = in ? W.head.cls_pred_W[(size_t)i * 2 + 0] : 0.f;
+        wo[h][6] = in ? W.head.cls_pred_W[(size_t)i * 2 + 1] : 0.f;
+    }
+    const int nit = ((nh + MT - 1) / MT) * 2 * NT;
+    for (int it = wv; it < nit; it += NW) {
+        const int mt = it / (2 * NT), rem = it - mt * 2 * NT, br = rem / NT, ot = rem - br * NT;
+        const float* Wb = (br == 0 ? W.head.cls_conv_W : W.head.reg_conv_W) + 2 * ot * MT + li;
+        const float* bb = (br == 0 ? W.head.cls_conv_b : W.head.reg_conv_b) + 2 * ot * MT + li;
+        float b0[KS], b1[KS];
+        #pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            b0[s] = Wb[(size_t)(4 * s + lk) * C];
+            b1[s] = Wb[(size_t)(4 * s + lk) * C + MT];
+        }
+        const float bias0 = bb[0], bias1 = bb[MT];
+        const float* xa = &S.X[S.ol[min(mt * MT + li, nh - 1)]][lk];
+        f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+        #pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const float x = xa[4 * s];
+            a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(x, b0[s], a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(x, b1[s], a1, 0, 0, 0);
+        }
+        // D: lane (li, lk) holds records 4 lk .. 4 lk + 3 of the tile, channel li
+        const int c0 = 2 * ot * MT + li, c1 = c0 + MT;
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r = mt * MT + 4 * lk + q;
+            if (r < nh) {
+                const int e = S.ol[r];
+                const float y0 = a0[q] + bias0, y1 = a1[q] + bias1;
+                const float v0 = y0 * sigmoid_fast(y0), v1 = y1 * sigmoid_fast(y1);
+                if (br == 0) {
+                    S.Y[e][c0] = v0;
+                    S.Y[e][c1] = v1;
+                } else {
+                    S.R[e][c0] = v0;
+                    S.R[e][c1] = v1;
+                }
             }
         }
     }
     __syncthreads();
     mark(S, PF_HEADH);
-    {
-        const int wv = tid >> 6, lane = tid & 63;
-        for (int r = wv; r < nh; r += NW) {
-            const int e = S.ol[r];
-            float part[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            for (int i = lane; i < C; i += 64) {
+    for (int r = wv; r < nh; r += NW) {
+        const int e = S.ol[r];
+        float part[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        #pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int i = lane + 64 * h;
+            if (i < C) {
                 const float yr = S.R[e][i], yc = S.Y[e][i];
                 #pragma unroll
-                for (int k = 0; k < 4; ++k) part[k] = fmaf(W.head.reg_pred_W[(size_t)i * 4 + k], yr, part[k]);
-                part[4] = fmaf(W.head.obj_pred_W[i], yr, part[4]);
-                part[5] = fmaf(W.head.cls_pred_W[(size_t)i * 2 + 0], yc, part[5]);
-                part[6] = fmaf(W.head.cls_pred_W[(size_t)i * 2 + 1], yc, part[6]);
+                for (int k = 0; k < 5; ++k) part[k] = fmaf(wo[h][k], yr, part[k]);
+                part[5] = fmaf(wo[h][5], yc, part[5]);
+                part[6] = fmaf(wo[h][6], yc, part[6]);
             }
+        }
+        #pragma unroll
+        for (int k = 0; k < 7; ++k) part[k] = wave_sumf(part[k]);
+        if (lane == 0) {
             #pragma unroll
-            for (int k = 0; k < 7; ++k) part[k] = wave_sumf(part[k]);
-            if (lane == 0) {
-                #pragma unroll
-                for (int k = 0; k < 4; ++k) S.H7[e][k] = part[k] + W.head.reg_pred_b[k];
-                S.H7[e][4] = part[4] + W.head.obj_pred_b[0];
-                S.H7[e][5] = part[5] + W.head.cls_pred_b[0];
-                S.H7[e][6] = part[6] + W.head.cls_pred_b[1];
-            }
+            for (int k = 0; k < 4; ++k) S.H7[e][k] = part[k] + W.head.reg_pred_b[k];
+            S.H7[e][4] = part[4] + W.head.obj_pred_b[0];
+            S.H7[e][5] = part[5] + W.head.cls_pred_b[0];
+            S.H7[e][6] = part[6] + W.head.cls_pred_b[1];
         }
     }
     __syncthreads();
@@ -650,8 +686,43 @@ __device__ __forceinline__ void batch_head_yolox(SL& S, int nh, const LiveWeight
 // per weight column), then the seven outputs [reg0..3, obj, cls0, cls1]
 // (one wave per record).  Single-linear head (...celled.cuh:1476-1481):
 // raw7 = head_W^T x + head_b, one wave per record.
+// Prediction-grid write of thread tid's record: the last owned pass-3
+// record of each s3 cell writes its cell (version += the cell's owned
+// pass-3 records of the batch).  The cell's version word (host memory) is
+// read here, ahead of the head, so its latency overlaps other work.
+struct PredPlan {
+    int cell = -1;
+    unsigned count = 0, old = 0;
+};
+
 template <class SL>
-__device__ __forceinline__ void batch_head(SL& S, int B, const LiveDesc& d, const LiveWeights& W) {
+__device__ __forceinline__ PredPlan pred_plan(SL& S, int B, const LiveDesc& d) {
+    PredPlan p;
+    const int tid = threadIdx.x;
+    if (tid < B && S.own[tid] && S.p3[tid]) {
+        const int e = tid, c = S.c3[e];
+        int count = 0;
+        bool last = true;
+        for (int j = 0; j < B; ++j) {
+            const bool same = S.own[j] && S.p3[j] && S.c3[j] == c;
+            count += same ? 1 : 0;
+            if (same && j > e) last = false;
+        }
+        const HybridStrip& s = d.strip;
+        const int hx = S.ex[e] - s.s3_owned_lo, hy = S.ey[e] - s.s3_owned_y_lo;
+        const int w = s.s3_owned_hi - s.s3_owned_lo, h = s.s3_owned_y_hi - s.s3_owned_y_lo;
+        if (last && hx >= 0 && hx < w && hy >= 0 && hy < h) {
+            p.cell = hy * w + hx;
+            p.count = (unsigned)count;
+            p.old = pred_version(d.version ? d.version + p.cell : nullptr);
+        }
+    }
+    return p;
+}
+
+template <class SL>
+__device__ __forceinline__ void batch_head(SL& S, int B, const LiveDesc& d, const LiveWeights& W,
+                                           const PredPlan* plan = nullptr) {
     constexpr int C = SSLA_C3;
     const int tid = threadIdx.x;
     if (tid < 64) {
@@ -660,6 +731,7 @@ __device__ __forceinline__ void batch_head(SL& S, int B, const LiveDesc& d, cons
         if (o) S.ol[__popcll(bal & ((1ull << tid) - 1ull))] = tid;
         if (tid == 0) S.nout = __popcll(bal);
     }
+    const PredPlan pp = plan ? *plan : pred_plan(S, B, d);
     __syncthreads();
     const int nh = S.nout;
     if (W.have_head == kHeadLinear) {
@@ -685,25 +757,9 @@ __device__ __forceinline__ void batch_head(SL& S, int B, const LiveDesc& d, cons
         batch_head_yolox(S, nh, W);
     }
 
-    // prediction grid: the last owned pass-3 record of each s3 cell writes
-    if (tid < B && S.own[tid] && S.p3[tid]) {
-        const int e = tid, c = S.c3[e];
-        int count = 0;
-        bool last = true;
-        for (int j = 0; j < B; ++j) {
-            const bool same = S.own[j] && S.p3[j] && S.c3[j] == c;
-            count += same ? 1 : 0;
-            if (same && j > e) last = false;
-        }
-        const HybridStrip& s = d.strip;
-        const int hx = S.ex[e] - s.s3_owned_lo, hy = S.ey[e] - s.s3_owned_y_lo;
-        const int w = s.s3_owned_hi - s.s3_owned_lo, h = s.s3_owned_y_hi - s.s3_owned_y_lo;
-        if (last && hx >= 0 && hx < w && hy >= 0 && hy < h) {
-            const int idx = hy * w + hx;
-            publish_pred(d.preds ? d.preds + (size_t)idx * 7 : nullptr,
-                         d.version ? d.version + idx : nullptr, S.H7[e], (unsigned)count);
-        }
-    }
+    if (pp.cell >= 0)
+        publish_pred_at(d.preds ? d.preds + (size_t)pp.cell * 7 : nullptr,
+                        d.version ? d.version + pp.cell : nullptr, S.H7[tid], pp.count, pp.old);
     __syncthreads();
     mark(S, PF_PREDS);
 }
@@ -1318,9 +1374,12 @@ __device__ __forceinline__ bool group_stage_b(int B, const LiveDesc& d, const Li
     if (!group_layer<SSLA_C2, SSLA_C3>(S, B, S.p2, nullptr, W.L[2], W.pk.pp[2], goT[2], ipT[2], d.hidden[2], gc, PF_L6))
         return false;
     l6_done();
+    // member 0's prediction-grid versions, read while L7 runs
+    PredPlan pp;
+    if (gc.k == 0 && W.have_head) pp = pred_plan(S, B, d);
     if (!group_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], W.pk.pp[3], goT[3], ipT[3], d.hidden[3], gc, PF_L7))
         return false;
-    if (gc.k == 0 && W.have_head) batch_head(S, B, d, W);
+    if (gc.k == 0 && W.have_head) batch_head(S, B, d, W, &pp);
     return true;
 }
 
