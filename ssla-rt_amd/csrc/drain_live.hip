@@ -210,40 +210,6 @@ __device__ __forceinline__ float wave_sumf(float v) {
 }
 
 // A float4 of an LDS row: x is 16-byte aligned and `at` a multiple of 4.
-__device__ __forceinline__ float4 lds4(const float* x, int at) {
-    return reinterpret_cast<const float4*>(__builtin_assume_aligned(x, 16))[at >> 2];
-}
-
-__device__ __forceinline__ float dot4(const float* w, float4 x, float a) {
-    a = fmaf(w[0], x.x, a);
-    a = fmaf(w[1], x.y, a);
-    a = fmaf(w[2], x.z, a);
-    return fmaf(w[3], x.w, a);
-}
-
-// acc[r] += sum_{i<K} w[i * ws] * x[off[r] + i] for eight rows of an LDS
-// array x: the weight column is read in chunks of 24 or 32 values, each
-// chunk's loads issued together and reused by the eight rows.
-template <int K>
-__device__ __forceinline__ void coldot8(const float* __restrict__ w, int ws, const float* x,
-                                        const int* off, float* acc) {
-    constexpr int KC = (K % 32 == 0) ? 32 : 24;
-    static_assert(K % KC == 0 && KC % 4 == 0, "column chunking");
-    #pragma nounroll
-    for (int k0 = 0; k0 < K; k0 += KC) {
-        float wr[KC];
-        #pragma unroll
-        for (int i = 0; i < KC; ++i) wr[i] = gload(w + (size_t)(k0 + i) * ws);
-        #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            float a = acc[r];
-            #pragma unroll
-            for (int i = 0; i < KC; i += 4) a = dot4(wr + i, lds4(x, off[r] + k0 + i), a);
-            acc[r] = a;
-        }
-    }
-}
-
 // Arrival-rank tdrop for one batch (wave 0; lane = record).  All lanes read
 // the counter in one load before the last record of each cell stores the
 // advanced value.

@@ -135,7 +135,8 @@ struct Producer {
     std::thread synth;
     std::atomic<std::uint64_t> synth_n{0};
 
-    void route(float t, float x, float y, float p, std::uint64_t t_emit) {
+    // now: the enqueue time (0: read the clock here)
+    void route(float t, float x, float y, float p, std::uint64_t t_emit, std::uint64_t now = 0) {
         const int ex = (int)x, ey = (int)y;
         if (ex < 0 || ex >= W || ey < 0 || ey >= H) {
             oob.fetch_add(1, std::memory_order_relaxed);
@@ -143,7 +144,7 @@ struct Producer {
         }
         const int home = ex / strip;
         const int owner = std::min(home, N - 1);
-        const std::uint64_t now = mono_ns();
+        if (now == 0) now = mono_ns();
         for (int k = std::max(0, home - 1); k <= std::min(N - 1, home + 1); ++k) {
             if (ex < k * strip - halo || ex >= (k + 1) * strip + halo) continue;
             Msg m{now, t_emit, t, x, y, p, (std::uint8_t)(k == owner), 0};
@@ -477,7 +478,12 @@ int submit(Producer* P, const float* ev, int n) {
 //     seed 0x9E3779B97F4A7C15 when 0; x = r mod W, y = (r >> 16) mod H,
 //     p = bit 32 of r -- the same stream for the same seed;
 //   blobs: n_blobs Gaussian blobs moving at 0.5-2 px/ms and reflecting off
-//     the sensor edges, plus bg_frac uniform background, p = +-1.
+//     the sensor edges, plus bg_frac uniform background, p = +-1.  The blob
+//     centres are recomputed every 64 events (32 us at 2 Mev/s, when a blob
+//     has moved at most 0.064 px) and the Gaussian offsets come in
+//     Box-Muller pairs from the xorshift stream: at 2 Mev/s the loop has
+//     500 ns per event, and generation, the clock and the queue pushes share
+//     them.
 void synth_loop(Producer* P, double rate_mev, int core, std::uint64_t seed, int n_blobs,
                 double sigma, double bg_frac) {
     pin_self(core);
@@ -493,7 +499,6 @@ void synth_loop(Producer* P, double rate_mev, int core, std::uint64_t seed, int 
     };
     std::mt19937_64 rng(xs);
     std::uniform_real_distribution<double> U(0.0, 1.0);
-    std::normal_distribution<double> N01(0.0, 1.0);
     struct Blob { double x0, y0, vx, vy; };
     std::vector<Blob> blobs((std::size_t)std::max(0, n_blobs));
     for (auto& b : blobs) {
@@ -510,11 +515,22 @@ void synth_loop(Producer* P, double rate_mev, int core, std::uint64_t seed, int 
         if (m < 0) m += per;
         return m > hi ? per - m : m;
     };
+    // uniform in [0, 1) and in (0, 1] from the top 53 bits of the stream
+    auto u01 = [&]() { return (double)(next_u64() >> 11) * 0x1.0p-53; };
+    auto u01_open = [&]() { return (double)((next_u64() >> 11) + 1) * 0x1.0p-53; };
+    constexpr int kRefresh = 64;
+    const std::size_t nb = blobs.size();
+    std::vector<double> cx(nb), cy(nb);
     double next = (double)mono_ns();
     float t_us = 0.f;
+    std::uint64_t count = 0;
     while (P->synth_on.load(std::memory_order_relaxed)) {
+        std::uint64_t now = mono_ns();
         if (period_ns > 0) {
-            while ((double)mono_ns() < next) cpu_relax();
+            while ((double)now < next) {
+                cpu_relax();
+                now = mono_ns();
+            }
             next += period_ns;
         }
         t_us += dt_us;
@@ -525,21 +541,28 @@ void synth_loop(Producer* P, double rate_mev, int core, std::uint64_t seed, int 
             y = (float)(int)((r >> 16) % (std::uint64_t)H);
             p = (float)((r >> 32) & 1ull);
         } else {
+            if (count % kRefresh == 0)
+                for (std::size_t i = 0; i < nb; ++i) {
+                    cx[i] = reflect(blobs[i].x0 + blobs[i].vx * t_us, W - 1);
+                    cy[i] = reflect(blobs[i].y0 + blobs[i].vy * t_us, H - 1);
+                }
             double fx, fy;
-            if (U(rng) < bg_frac) {
-                fx = std::floor(U(rng) * W);
-                fy = std::floor(U(rng) * H);
+            if (u01() < bg_frac) {
+                fx = std::floor(u01() * W);
+                fy = std::floor(u01() * H);
             } else {
-                const Blob& b = blobs[(std::size_t)(U(rng) * blobs.size()) % blobs.size()];
-                fx = std::rint(reflect(b.x0 + b.vx * t_us, W - 1) + sigma * N01(rng));
-                fy = std::rint(reflect(b.y0 + b.vy * t_us, H - 1) + sigma * N01(rng));
+                const std::size_t i = std::min(nb - 1, (std::size_t)(u01() * (double)nb));
+                const double rad = std::sqrt(-2.0 * std::log(u01_open()));
+                const double ang = 2.0 * M_PI * u01();
+                fx = std::rint(cx[i] + sigma * rad * std::cos(ang));
+                fy = std::rint(cy[i] + sigma * rad * std::sin(ang));
             }
             x = (float)std::min<double>(W - 1, std::max(0.0, fx));
             y = (float)std::min<double>(H - 1, std::max(0.0, fy));
-            p = U(rng) < 0.5 ? -1.f : 1.f;
+            p = (next_u64() >> 63) ? 1.f : -1.f;
         }
-        P->route(t_us, x, y, p, mono_ns());
-        P->synth_n.fetch_add(1, std::memory_order_relaxed);
+        P->route(t_us, x, y, p, now, now);
+        P->synth_n.store(++count, std::memory_order_relaxed);
     }
 }
 

@@ -115,9 +115,11 @@ class LiveResult:
 
 
 def pick_cores(n_shards: int):
-    """(synth_core, base_core) inside this process's CPU set: the source on
-    the first allowed core, shards on the next n_shards consecutive ones;
-    -1 (unpinned) where the set has no such run."""
+    """(synth_core, base_core) inside this process's CPU set: the shards on
+    n_shards consecutive cores after the first allowed one, the source on
+    the next allowed core after them (else on the first), so that the
+    source shares its core with neither the shards nor this process's main
+    thread; -1 (unpinned) where the set has no such run."""
     import os
     allowed = sorted(os.sched_getaffinity(0))
     if len(allowed) < n_shards + 1:
@@ -126,7 +128,8 @@ def pick_cores(n_shards: int):
     for i in range(1, len(allowed) - n_shards + 1):
         run = allowed[i:i + n_shards]
         if run[-1] - run[0] == n_shards - 1:
-            return first, run[0]
+            after = allowed[i + n_shards:]
+            return (after[0] if after else first), run[0]
     return first, -1
 
 
