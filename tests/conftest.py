@@ -32,6 +32,16 @@ def stub_npz(stub_dir):
 
 
 @pytest.fixture(scope="session")
+def stub_w1_dir(tmp_path_factory):
+    """Stub weight directory at 80x64, seed 5, tdrop window 1: every record
+    passes both gates, so every record has head outputs."""
+    from ssla_hip import stub
+    d = tmp_path_factory.mktemp("stub_80x64_w1")
+    stub.write_stub(str(d), height=64, width=80, seed=5, tdrop=1)
+    return str(d)
+
+
+@pytest.fixture(scope="session")
 def stub_640(tmp_path_factory):
     """Stub weight directory at 640x480 (s2 160 x 120), seed 1, tdrop 4."""
     from ssla_hip import stub

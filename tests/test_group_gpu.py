@@ -12,6 +12,7 @@ import ctypes
 import numpy as np
 import pytest
 
+from oracle import oracle as O
 from ssla_hip import abi, events, lib
 from test_live_gpu import (FEAT_TOL, HEAD_TOL, _produce, _wait_done, check_preds, hidden_close,
                            oracle_run, say)
@@ -87,6 +88,31 @@ def test_group_batch_repeated_calls(H, stub_dir, stub_npz):
         assert np.array_equal(o["pass3"], p3.astype(np.int32))
         for li in range(4):
             assert hidden_close(d.hidden(0, li), st.H[li]), li
+
+
+@pytest.mark.parametrize("group", [0, 6])
+def test_batch_head_with_full_batches(H, stub_w1_dir, group):
+    """Tdrop window 1: every record passes both gates and is owned, so the
+    head runs on every record of each 32-record batch (two 16-record row
+    tiles of the head's MFMA items) -- raw head rows, s3_feat, flags, state
+    and prediction grid against the oracle."""
+    rec = events.blob_records(2000, seed=27)
+    npz = O.load_npz(stub_w1_dir)
+    say(f"batch head with full batches, group {group}")
+    with H.Drain.from_weights_dir(stub_w1_dir) as d:
+        (out,), (h7,) = d.drain([events.to_records(rec)], want_head=True, batch=32, group=group)
+        st = O.S2S3(O.layers_from_npz(npz), 16, 20, 1, head=O.head_from_npz(npz))
+        p2, p3, feat, ref7 = st.run(rec.x, rec.y, rec.feat1, want_head=True)
+        assert np.all(p3 == 1)
+        assert np.array_equal(out["pass2"], p2.astype(np.int32))
+        assert np.array_equal(out["pass3"], p3.astype(np.int32))
+        df = np.abs(out["s3_feat"] - feat).max()
+        dh = np.abs(h7 - ref7).max()
+        say(f"group {group}: s3_feat max|d| {df:.3g}, head max|d| {dh:.3g}")
+        assert df <= FEAT_TOL and dh <= HEAD_TOL
+        for li in range(4):
+            assert hidden_close(d.hidden(0, li), st.H[li]), li
+        check_preds(*d.preds(0), rec, p3, ref7)
 
 
 def test_group_bad_sizes(H, stub_dir):
