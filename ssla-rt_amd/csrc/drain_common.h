@@ -10,6 +10,18 @@
 
 namespace ssla {
 
+// Global-memory accesses through address-space-1 pointers: pointers that
+// reach device code as generic values (loaded from descriptor tables) would
+// otherwise compile to flat instructions, which also count against the LDS
+// counter, so every later LDS wait would wait for them as well (a host-ring
+// read or a counter store for a PCIe or L2 round trip).
+#define SSLA_GLOBAL __attribute__((address_space(1)))
+
+template <class T>
+__device__ __forceinline__ SSLA_GLOBAL T* gmem(T* p) {
+    return (SSLA_GLOBAL T*)p;
+}
+
 constexpr int kPatch = 9;   // 3x3 patch positions, delta = (1-dy)*3 + (1-dx)
 
 struct Geometry {
@@ -71,7 +83,7 @@ constexpr unsigned kPredBusy = 0x80000000u;
 // A prediction cell's version word (fine-grained host memory) without the
 // busy bit, or 0 for none.
 __device__ __forceinline__ unsigned pred_version(const unsigned* version) {
-    return version ? __hip_atomic_load(const_cast<unsigned*>(version), __ATOMIC_RELAXED,
+    return version ? __hip_atomic_load(gmem(const_cast<unsigned*>(version)), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_SYSTEM) & ~kPredBusy
                    : 0u;
 }
@@ -86,16 +98,16 @@ __device__ __forceinline__ unsigned pred_version(const unsigned* version) {
 __device__ __forceinline__ void publish_pred_at(float* preds7, unsigned* version, const float* v7,
                                                 unsigned count, unsigned old) {
     if (version) {
-        __hip_atomic_store(version, old | kPredBusy, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(gmem(version), old | kPredBusy, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         __threadfence_system();
     }
     if (preds7) {
         #pragma unroll
-        for (int q = 0; q < 7; ++q) preds7[q] = v7[q];
+        for (int q = 0; q < 7; ++q) gmem(preds7)[q] = v7[q];
     }
     if (version) {
         __threadfence_system();
-        __hip_atomic_store(version, (old + count) & ~kPredBusy, __ATOMIC_RELAXED,
+        __hip_atomic_store(gmem(version), (old + count) & ~kPredBusy, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }

@@ -122,11 +122,13 @@ struct alignas(16) Lds {
     int pidx[LB][kPatch];                // pair of (record, delta), or -1
     int pe[LP], pc[LP], pnext[LP], lead[LP];
     unsigned pk[LB];                     // x | y << 16 of records in the pair set, else ~0
+    unsigned pbits[LB];                  // deltas of each record's pairs (bit d)
+    unsigned dmask;                      // deltas of any record's pairs
     int dcnt[kPatch], dcnto[kPatch];
     int dev[kPatch][LB];                 // records with a pair at delta
     int devo[kPatch][LB];                // ... that are output records of the layer
     int ol[LB];                          // output records of the current layer
-    int npair, nlead, nout, bsize, flag, prof_on;
+    int nlead, nout, bsize, flag, prof_on;
     unsigned long long t_pop, tprev;
     unsigned long long prof[NPROF];
 };
@@ -218,89 +220,84 @@ __device__ __forceinline__ void batch_tdrop(SL& S, int B, unsigned char* td, con
                             const unsigned char* mask, unsigned char* pass, int window) {
     if (threadIdx.x >= 64) return;
     const int e = threadIdx.x;
-    if (e >= B) return;
-    const int c = cell[e];
+    // lane j's cell when record j is live, else -1; the other lanes' keys
+    // are read from registers (the whole wave runs the loop)
+    const int c = e < B ? cell[e] : -1;
     const bool live = c >= 0 && (mask == nullptr || mask[e]);
+    const int key = live ? c : -1;
+    int rank = 0;
+    bool last = true;
+    for (int j = 0; j < B; ++j) {
+        const bool lj = __builtin_amdgcn_readlane(key, j) == key;
+        if (lj && j < e) ++rank;
+        if (lj && j > e) last = false;
+    }
+    if (e >= B) return;
     if (!live) {
         pass[e] = 0;
         return;
     }
-    int rank = 0;
-    bool last = true;
-    for (int j = 0; j < B; ++j) {
-        const bool lj = cell[j] == c && (mask == nullptr || mask[j]);
-        if (lj && j < e) ++rank;
-        if (lj && j > e) last = false;
-    }
-    const unsigned cnt = td[c];
+    const unsigned cnt = gmem(td)[c];
     const unsigned pre = (cnt + (unsigned)rank) & 255u;
     pass[e] = (window <= 1 || pre % (unsigned)window == 0u) ? 1 : 0;
-    if (last) td[c] = (unsigned char)((cnt + (unsigned)rank + 1u) & 255u);
+    if (last) gmem(td)[c] = (unsigned char)((cnt + (unsigned)rank + 1u) & 255u);
 }
 
-// (record, delta) pairs of the records in `set` on an Hl x Wl grid, in
-// record order; per-delta record lists; successor links and one leader per
-// cell.  Ends with a barrier.
-template <class SL, bool PL = false>
+// (record, delta) pairs of the records in `set` on an Hl x Wl grid.  Pair
+// (e, d) -- record e and the cell (ey + 1 - d / 3, ex + 1 - d % 3) of its
+// 3x3 patch -- has the fixed index e * 9 + d; pidx[e][d] is that index, or
+// -1 when e is not in the set or the cell is off the grid, and pbits[e] the
+// mask of e's pairs (dmask: of every record's).  LISTS: per-delta lists of
+// the records with a pair there (dev, dcnt).  Then one thread per pair: its
+// record and cell, its successor at the cell (the pair of the first later
+// record of the set whose patch holds the cell) and whether it leads the
+// cell (no earlier record's patch holds it).  Ends with a barrier.
+template <class SL, bool LISTS = true>
 __device__ __forceinline__ void build_pairs(SL& S, int B, const unsigned char* set, int Hl, int Wl) {
     const int tid = threadIdx.x;
     if (tid < 64) {
         const int e = tid;
         const bool in = e < B && set[e];
+        const int ex = in ? S.ex[e] : 0, ey = in ? S.ey[e] : 0;
         unsigned bits = 0;
         if (in) {
             #pragma unroll
             for (int d = 0; d < kPatch; ++d) {
-                const int ty = S.ey[e] + 1 - d / 3, tx = S.ex[e] + 1 - d % 3;
+                const int ty = ey + 1 - d / 3, tx = ex + 1 - d % 3;
                 if (ty >= 0 && ty < Hl && tx >= 0 && tx < Wl) bits |= 1u << d;
             }
         }
-        const int cnt = __popc(bits);
-        int incl = cnt;
-        for (int off = 1; off < 64; off <<= 1) {
-            const int v = __shfl_up(incl, off, 64);
-            if (e >= off) incl += v;
-        }
-        int k = incl - cnt;
-        int pis[kPatch];
-        #pragma unroll
-        for (int d = 0; d < kPatch; ++d) {
-            int pi = -1;
-            if (bits & (1u << d)) {
-                const int ty = S.ey[e] + 1 - d / 3, tx = S.ex[e] + 1 - d % 3;
-                S.pe[k] = e;
-                S.pc[k] = ty * Wl + tx;
-                pi = k++;
-            }
-            pis[d] = pi;
-            if (e < LB) S.pidx[e][d] = pi;
-        }
-        const unsigned long long lt = (1ull << e) - 1ull;
-        #pragma unroll
-        for (int d = 0; d < kPatch; ++d) {
-            const bool has = (bits >> d) & 1u;
-            const unsigned long long bal = __ballot(has);
-            if (has) {
-                S.dev[d][__popcll(bal & lt)] = e;
-                if constexpr (PL) S.devp[d][__popcll(bal & lt)] = pis[d];
-            }
-            if (e == 0) S.dcnt[d] = __popcll(bal);
-        }
-        const int total = __shfl(incl, 63, 64);
-        if (e < LB) S.pk[e] = in ? ((unsigned)S.ex[e] | ((unsigned)S.ey[e] << 16)) : 0xffffffffu;
         if (e == 0) {
-            S.npair = total;
+            S.dmask = 0u;
             S.nlead = 0;
+        }
+        if (e < LB) {
+            S.pbits[e] = bits;
+            S.pk[e] = in ? ((unsigned)ex | ((unsigned)ey << 16)) : 0xffffffffu;
+            #pragma unroll
+            for (int d = 0; d < kPatch; ++d) S.pidx[e][d] = ((bits >> d) & 1u) ? e * kPatch + d : -1;
+        }
+        if (bits) atomicOr(&S.dmask, bits);   // after lane 0's store: one wave, LDS order
+        if constexpr (LISTS) {
+            const unsigned long long lt = (1ull << e) - 1ull;
+            #pragma unroll
+            for (int d = 0; d < kPatch; ++d) {
+                const bool has = (bits >> d) & 1u;
+                const unsigned long long bal = __ballot(has);
+                if (has) S.dev[d][__popcll(bal & lt)] = e;
+                if (e == 0) S.dcnt[d] = __popcll(bal);
+            }
         }
     }
     __syncthreads();
-    // Links: the pair after p at p's cell belongs to the first later record
-    // of the set whose 3x3 patch holds the cell; p leads its cell when no
-    // earlier record's patch does.  O(B) per pair.
-    const int np = S.npair;
-    for (int p = tid; p < np; p += LT) {
-        const int e = S.pe[p], c = S.pc[p];
-        const int ty = c / Wl, tx = c - ty * Wl;
+    // O(B) per pair
+    for (int p = tid; p < kPatch * B; p += LT) {
+        const int e = p / kPatch, d = p - e * kPatch;
+        if (!((S.pbits[e] >> d) & 1u)) continue;
+        const unsigned ke = S.pk[e];
+        const int tx = (int)(ke & 0xffffu) + 1 - d % 3, ty = (int)(ke >> 16) + 1 - d / 3;
+        S.pe[p] = e;
+        S.pc[p] = ty * Wl + tx;
         int nx = -1;
         bool lead = true;
         for (int j = 0; j < B; ++j) {
@@ -308,7 +305,7 @@ __device__ __forceinline__ void build_pairs(SL& S, int B, const unsigned char* s
             const int dx = tx - (int)(k & 0xffffu), dy = ty - (int)(k >> 16);
             if (k == 0xffffffffu || dx < -1 || dx > 1 || dy < -1 || dy > 1) continue;
             if (j < e) lead = false;
-            else if (j > e && nx < 0) nx = S.pidx[j][(1 - dy) * 3 + (1 - dx)];
+            else if (j > e && nx < 0) nx = j * kPatch + (1 - dy) * 3 + (1 - dx);
         }
         S.pnext[p] = nx;
         if (lead) S.lead[atomicAdd(&S.nlead, 1)] = p;
@@ -665,15 +662,20 @@ template <class SL>
 __device__ __forceinline__ PredPlan pred_plan(SL& S, int B, const LiveDesc& d) {
     PredPlan p;
     const int tid = threadIdx.x;
-    if (tid < B && S.own[tid] && S.p3[tid]) {
-        const int e = tid, c = S.c3[e];
-        int count = 0;
-        bool last = true;
-        for (int j = 0; j < B; ++j) {
-            const bool same = S.own[j] && S.p3[j] && S.c3[j] == c;
-            count += same ? 1 : 0;
-            if (same && j > e) last = false;
-        }
+    if (tid >= 64) return p;
+    // lane j's s3 cell when record j is an owned pass-3 record, else -1
+    // (the whole wave runs the loop; other lanes' keys come from registers)
+    const bool mine = tid < B && S.own[tid] && S.p3[tid];
+    const int key = mine ? S.c3[tid] : -1;
+    int count = 0;
+    bool last = true;
+    for (int j = 0; j < B; ++j) {
+        const bool same = __builtin_amdgcn_readlane(key, j) == key;
+        count += same ? 1 : 0;
+        if (same && j > tid) last = false;
+    }
+    if (mine) {
+        const int e = tid;
         const HybridStrip& s = d.strip;
         const int hx = S.ex[e] - s.s3_owned_lo, hy = S.ey[e] - s.s3_owned_y_lo;
         const int w = s.s3_owned_hi - s.s3_owned_lo, h = s.s3_owned_y_hi - s.s3_owned_y_lo;
@@ -779,7 +781,7 @@ template <class SL>
 __device__ __forceinline__ void prof_end(SL& S, const LiveDesc& d, int stage = -1) {
     if (threadIdx.x == 0 && d.prof)
         for (int k = 0; k < NPROF; ++k)
-            if (stage < 0 || (stage == 1) == prof_stage_b(k)) d.prof[k] = S.prof[k];
+            if (stage < 0 || (stage == 1) == prof_stage_b(k)) gmem(d.prof)[k] = S.prof[k];
 }
 
 // Clock handshake with the host (live kernels, poll wave lane 0): when the
@@ -788,10 +790,10 @@ __device__ __forceinline__ void prof_end(SL& S, const LiveDesc& d, int stage = -
 // can bracket a GPU clock reading between its own clock readings.
 __device__ __forceinline__ void clock_sync(unsigned long long* cs, unsigned long long& last) {
     if (!cs) return;
-    const unsigned long long ping = __hip_atomic_load(cs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const unsigned long long ping = __hip_atomic_load(gmem(cs), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     if (ping != last) {
         const unsigned long long now = (unsigned long long)wall_clock64();
-        __hip_atomic_store(cs + 1, (now << 8) | (ping & 0xffull), __ATOMIC_RELAXED,
+        __hip_atomic_store(gmem(cs + 1), (now << 8) | (ping & 0xffull), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_SYSTEM);
         last = ping;
     }
@@ -811,7 +813,8 @@ __device__ __forceinline__ void load_batch(SL& S, int B, const HybridInputRec* r
     const int tid = threadIdx.x;
     if (tid < B * 8) {
         const int e = tid >> 3, q = tid & 7;
-        const uint4 v = reinterpret_cast<const uint4*>(&ring[(first + e) & mask])[q];
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 v = gmem(reinterpret_cast<const u32x4*>(&ring[(first + e) & mask]))[q];
         if (q >= 1 && q <= 6) {
             *reinterpret_cast<float4*>(&S.X[e][4 * (q - 1)]) =
                 make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
@@ -858,24 +861,24 @@ k_batch_drain(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, int ba
         // output slots and head rows
         for (int t = tid; t < B * SSLA_C3; t += LT) {
             const int e = t / SSLA_C3, i = t % SSLA_C3;
-            if (d.out) d.out[base + e].s3_feat[i] = (S.vld[e] && S.p3[e]) ? S.X[e][i] : 0.f;
+            if (d.out) gmem(d.out)[base + e].s3_feat[i] = (S.vld[e] && S.p3[e]) ? S.X[e][i] : 0.f;
         }
         if (tid < B) {
             const int e = tid;
             const bool v = S.vld[e], own = S.own[e];
             if (d.out) {
-                d.out[base + e].pass2 = !v ? -2 : (own ? (int)S.p2[e] : -1);
-                d.out[base + e].pass3 = !v ? -2 : (own ? (int)S.p3[e] : -1);
+                gmem(d.out)[base + e].pass2 = !v ? -2 : (own ? (int)S.p2[e] : -1);
+                gmem(d.out)[base + e].pass3 = !v ? -2 : (own ? (int)S.p3[e] : -1);
             }
             if (d.head_out) {
                 const bool hv = W.have_head && own && S.p3[e];
                 #pragma unroll
-                for (int k = 0; k < 7; ++k) d.head_out[(size_t)(base + e) * 7 + k] = hv ? S.H7[e][k] : 0.f;
+                for (int k = 0; k < 7; ++k) gmem(d.head_out)[(size_t)(base + e) * 7 + k] = hv ? S.H7[e][k] : 0.f;
             }
         }
         if (tid == 0 && d.batch_clk) {
-            d.batch_clk[(size_t)bi * 2 + 0] = S.t_pop;
-            d.batch_clk[(size_t)bi * 2 + 1] = (unsigned long long)wall_clock64();
+            gmem(d.batch_clk)[(size_t)bi * 2 + 0] = S.t_pop;
+            gmem(d.batch_clk)[(size_t)bi * 2 + 1] = (unsigned long long)wall_clock64();
         }
         __syncthreads();
         mark(S, PF_PUBLISH);
@@ -899,14 +902,14 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
     const int tid = threadIdx.x;
     prof_begin(S, d);
     const unsigned long long mask = d.ring_mask;
-    unsigned long long t = __hip_atomic_load(d.tail, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+    unsigned long long t = __hip_atomic_load(gmem(d.tail), __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
     unsigned long long last_work = (unsigned long long)wall_clock64();
     // The host pairs the kernel's start and end clocks with its own clock at
     // the moment it sees them, so they are stored relaxed: a release would
     // first write back the L2, and the host would see the value late by as
     // much as that takes (tens of microseconds at the end of a run).
     if (tid == 0 && d.kstart)
-        __hip_atomic_store(d.kstart, last_work, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(gmem(d.kstart), last_work, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     const int sleep_iters = (int)(spin_ns / 40u) + 1;
     unsigned long long ping_seen = 0;
     while (true) {
@@ -914,7 +917,7 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
         __syncthreads();
         // ---- poll: wave 0 probes 64 consecutive tags ------------------------------
         if (tid < 64) {
-            unsigned long long* tag = const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done);
+            SSLA_GLOBAL unsigned long long* tag = gmem(const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done));
             const unsigned long long s = __hip_atomic_load(tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             const bool ready = s == t + (unsigned long long)tid + 1ull;
             const unsigned long long bal = __ballot(ready);
@@ -941,7 +944,7 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
             if (tid == 0) {
                 if (flag > 1) atomicMax(status, flag);
                 if (d.kend)
-                    __hip_atomic_store(d.kend, (unsigned long long)wall_clock64(), __ATOMIC_RELAXED,
+                    __hip_atomic_store(gmem(d.kend), (unsigned long long)wall_clock64(), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_SYSTEM);
             }
             prof_end(S, d);
@@ -965,13 +968,13 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
         const unsigned long long t_done = (unsigned long long)wall_clock64();
         if (tid < B && d.timing) {
             const unsigned long long seq = t + (unsigned long long)tid;
-            GpuTimingSlot& ts = d.timing[seq & d.timing_mask];
-            ts.t_pop_clk = S.t_pop;
-            ts.t_done_clk = t_done;
-            ts.seq = (unsigned int)seq;
-            ts.owner = (S.own[tid] && S.p2[tid] && S.p3[tid]) ? 1u : 0u;
-            ts.t_push_ns = S.tpush[tid];
-            ts.t_emit_ns = S.temit[tid];
+            SSLA_GLOBAL GpuTimingSlot* ts = gmem(d.timing) + (seq & d.timing_mask);
+            ts->t_pop_clk = S.t_pop;
+            ts->t_done_clk = t_done;
+            ts->seq = (unsigned int)seq;
+            ts->owner = (S.own[tid] && S.p2[tid] && S.p3[tid]) ? 1u : 0u;
+            ts->t_push_ns = S.tpush[tid];
+            ts->t_emit_ns = S.temit[tid];
         }
         t += (unsigned long long)B;
         last_work = t_done;
@@ -979,9 +982,9 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
         __threadfence_system();
         __syncthreads();
         if (tid == 0) {
-            __hip_atomic_store(d.tail, t, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(gmem(d.tail), t, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
             if (d.events_done)
-                __hip_atomic_store(d.events_done, t, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(gmem(d.events_done), t, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         }
         mark(S, PF_PUBLISH);
         if (tid == 0) {
@@ -1047,11 +1050,10 @@ struct alignas(16) LdsG {
     int pidx[LB][kPatch];
     int pe[LP], pc[LP], pnext[LP], lead[LP];
     unsigned pk[LB];
-    int dcnt[kPatch], dcnto[kPatch];
-    int dev[kPatch][LB];                 // records with a pair at delta
-    int devp[kPatch][LB];                // ... and that pair
+    unsigned pbits[LB];
+    unsigned dmask;
     int ol[LB];
-    int npair, nlead, nout, bsize, flag, prof_on, abort_;
+    int nlead, nout, bsize, flag, prof_on, abort_;
     unsigned xseq;                       // exchanges done by the group
     unsigned long long t_pop, tprev;
     unsigned long long prof[NPROF];
@@ -1110,22 +1112,22 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
     }
     const int k = gc.k, G = gc.G;
     const int ns = k < NSL ? (NSL - 1 - k) / G + 1 : 0;      // own slices k, k + G, ...
-    // P: units (delta, own slice): the records with a pair at delta (A)
+    // P: units (delta, own slice): the batch's records (A, 16-record tiles)
     // times the slice's q, v and g weight columns, three MFMA chains over
-    // one A tile.  q is written for every pair; the recurrence reads it only
-    // for output pairs.
+    // one A tile; rows of the records with a pair at delta are kept.  q is
+    // written for every pair; the recurrence reads it only for output pairs.
+    const unsigned dmask = S.dmask;
     for (int u = wv; u < kPatch * ns; u += NW) {
         const int d = u / ns, js = u - d * ns;
-        const int n = S.dcnt[d];
-        if (n == 0) continue;
+        if (!((dmask >> d) & 1u)) continue;
         const int j = k + js * G;
         float bq[P::KS4 * 4], bv[P::KS4 * 4], bg[P::KS4 * 4];
         P::load(pp, d * P::T + j, lane, bq);
         P::load(pp, d * P::T + NSL + j, lane, bv);
         P::load(pp, d * P::T + 2 * NSL + j, lane, bg);
         const float* X = &S.X[0][0];
-        for (int m0 = 0; m0 < n; m0 += MT) {
-            const int xr = S.dev[d][min(m0 + li, n - 1)] * XS + lk;
+        for (int m0 = 0; m0 < B; m0 += MT) {
+            const int xr = min(m0 + li, B - 1) * XS + lk;
             f32x4 aq = {0.f, 0.f, 0.f, 0.f}, av = aq, ag = aq;
             #pragma unroll
             for (int s = 0; s < P::KS; ++s) {
@@ -1137,8 +1139,8 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
             #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int rr = m0 + 4 * lk + r;
-                if (rr < n) {
-                    float* row = S.PR[S.devp[d][rr]];
+                if (rr < B && ((S.pbits[rr] >> d) & 1u)) {
+                    float* row = S.PR[rr * kPatch + d];
                     row[js * MT + li] = aq[r];
                     row[(GSL + js) * MT + li] = av[r];
                     row[(2 * GSL + js) * MT + li] = ag[r];
@@ -1309,7 +1311,7 @@ __device__ __forceinline__ bool group_stage_a(int B, const LiveDesc& d, const Li
     batch_tdrop(S, B, td2, S.c2, nullptr, S.p2, G.window);
     __syncthreads();
     mark(S, PF_TD2);
-    build_pairs<LdsG, true>(S, B, S.vld, G.H2, G.W2);
+    build_pairs<LdsG, false>(S, B, S.vld, G.H2, G.W2);
     mark(S, PF_PAIRS2);
     if (!group_layer<SSLA_C1, SSLA_C2>(S, B, S.vld, nullptr, W.L[0], W.pk.pp[0], goT[0], ipT[0], d.hidden[0], gc, PF_L4))
         return false;
@@ -1335,7 +1337,7 @@ __device__ __forceinline__ bool group_stage_b(int B, const LiveDesc& d, const Li
     batch_tdrop(S, B, td3, S.c3, S.p2, S.p3, G.window);
     __syncthreads();
     mark(S, PF_TD3);
-    build_pairs<LdsG, true>(S, B, S.p2, G.H3, G.W3);
+    build_pairs<LdsG, false>(S, B, S.p2, G.H3, G.W3);
     mark(S, PF_PAIRS3);
     if (!group_layer<SSLA_C2, SSLA_C3>(S, B, S.p2, nullptr, W.L[2], W.pk.pp[2], goT[2], ipT[2], d.hidden[2], gc, PF_L6))
         return false;
@@ -1533,18 +1535,18 @@ __device__ __forceinline__ void group_live_stage_b(LdsG& S, const LiveDesc& d,
         if (k == 0) {
             if (tid < B && d.timing) {
                 const unsigned long long seq = t + (unsigned long long)tid;
-                GpuTimingSlot& ts = d.timing[seq & d.timing_mask];
-                ts.t_pop_clk = S.t_pop;
-                ts.t_done_clk = t_done;
-                ts.seq = (unsigned int)seq;
-                ts.owner = (S.own[tid] && S.p2[tid] && S.p3[tid]) ? 1u : 0u;
-                ts.t_push_ns = S.tpush[tid];
-                ts.t_emit_ns = S.temit[tid];
+                SSLA_GLOBAL GpuTimingSlot* ts = gmem(d.timing) + (seq & d.timing_mask);
+                ts->t_pop_clk = S.t_pop;
+                ts->t_done_clk = t_done;
+                ts->seq = (unsigned int)seq;
+                ts->owner = (S.own[tid] && S.p2[tid] && S.p3[tid]) ? 1u : 0u;
+                ts->t_push_ns = S.tpush[tid];
+                ts->t_emit_ns = S.temit[tid];
             }
             __threadfence_system();
             __syncthreads();
             if (tid == 0 && d.events_done)
-                __hip_atomic_store(d.events_done, t + (unsigned long long)B, __ATOMIC_RELEASE,
+                __hip_atomic_store(gmem(d.events_done), t + (unsigned long long)B, __ATOMIC_RELEASE,
                                    __HIP_MEMORY_SCOPE_SYSTEM);
             mark(S, PF_PUBLISH);
         }
@@ -1611,24 +1613,24 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
             if (k == 0) {
                 for (int t = tid; t < B * SSLA_C3; t += LT) {
                     const int e = t / SSLA_C3, i = t % SSLA_C3;
-                    if (d.out) d.out[base + e].s3_feat[i] = (S.vld[e] && S.p3[e]) ? S.X[e][i] : 0.f;
+                    if (d.out) gmem(d.out)[base + e].s3_feat[i] = (S.vld[e] && S.p3[e]) ? S.X[e][i] : 0.f;
                 }
                 if (tid < B) {
                     const int e = tid;
                     const bool v = S.vld[e], own = S.own[e];
                     if (d.out) {
-                        d.out[base + e].pass2 = !v ? -2 : (own ? (int)S.p2[e] : -1);
-                        d.out[base + e].pass3 = !v ? -2 : (own ? (int)S.p3[e] : -1);
+                        gmem(d.out)[base + e].pass2 = !v ? -2 : (own ? (int)S.p2[e] : -1);
+                        gmem(d.out)[base + e].pass3 = !v ? -2 : (own ? (int)S.p3[e] : -1);
                     }
                     if (d.head_out) {
                         const bool hv = W.have_head && own && S.p3[e];
                         #pragma unroll
-                        for (int q = 0; q < 7; ++q) d.head_out[(size_t)(base + e) * 7 + q] = hv ? S.H7[e][q] : 0.f;
+                        for (int q = 0; q < 7; ++q) gmem(d.head_out)[(size_t)(base + e) * 7 + q] = hv ? S.H7[e][q] : 0.f;
                     }
                 }
                 if (tid == 0 && d.batch_clk) {
-                    d.batch_clk[(size_t)bi * 2 + 0] = S.t_pop;
-                    d.batch_clk[(size_t)bi * 2 + 1] = (unsigned long long)wall_clock64();
+                    gmem(d.batch_clk)[(size_t)bi * 2 + 0] = S.t_pop;
+                    gmem(d.batch_clk)[(size_t)bi * 2 + 1] = (unsigned long long)wall_clock64();
                 }
             }
             __syncthreads();
@@ -1645,7 +1647,7 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
     unsigned long long t = d.t0;
     unsigned long long last_work = (unsigned long long)wall_clock64();
     if (k == 0 && tid == 0 && d.kstart)
-        __hip_atomic_store(d.kstart, last_work, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(gmem(d.kstart), last_work, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     const int sleep_iters = (int)(spin_ns / 40u) + 1;
     unsigned long long* bc = gc.xb + kXBc;
     unsigned bseq = 0;                   // batches broadcast
@@ -1656,7 +1658,7 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
         if (k == 0) {
             // poll: wave 0 probes 64 consecutive tags (as k_live)
             if (tid < 64) {
-                unsigned long long* tag = const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done);
+                SSLA_GLOBAL unsigned long long* tag = gmem(const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done));
                 const unsigned long long s = __hip_atomic_load(tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 const bool ready = s == t + (unsigned long long)tid + 1ull;
                 const unsigned long long bal = __ballot(ready);
@@ -1707,7 +1709,7 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
             if (tid == 0) {
                 if ((k == 0 && flag > 1) || flag == 4) atomicMax(status, flag);
                 if (k == 0 && d.kend)
-                    __hip_atomic_store(d.kend, (unsigned long long)wall_clock64(), __ATOMIC_RELAXED,
+                    __hip_atomic_store(gmem(d.kend), (unsigned long long)wall_clock64(), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_SYSTEM);
             }
             // stage B ends on the same flag once it has taken every batch
@@ -1719,7 +1721,7 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
         }
         if (k != 0 && tid < B) {
             // the producer's tags of this batch (member 0 has seen them)
-            unsigned long long* tag = const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done);
+            SSLA_GLOBAL unsigned long long* tag = gmem(const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done));
             const unsigned long long want = t + (unsigned long long)tid + 1ull;
             const unsigned long long dl = (unsigned long long)wall_clock64() + gc.wait_ticks;
             while (__hip_atomic_load(tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != want) {
@@ -1751,7 +1753,7 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
             if (tid == 0) {
                 atomicMax(status, 4);
                 if (k == 0 && d.kend)
-                    __hip_atomic_store(d.kend, (unsigned long long)wall_clock64(), __ATOMIC_RELAXED,
+                    __hip_atomic_store(gmem(d.kend), (unsigned long long)wall_clock64(), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_SYSTEM);
             }
             if (ST == 2 && k == 0) (void)handoff_put(S, hb, hseq, 0, 4, gc.wait_ticks);
@@ -1763,7 +1765,7 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
             // and the batch goes to stage B
             if (k == 0) {
                 if (tid == 0)
-                    __hip_atomic_store(d.tail, t + (unsigned long long)B, __ATOMIC_RELEASE,
+                    __hip_atomic_store(gmem(d.tail), t + (unsigned long long)B, __ATOMIC_RELEASE,
                                        __HIP_MEMORY_SCOPE_SYSTEM);
                 if (!handoff_put(S, hb, hseq, B, 0, gc.wait_ticks)) {
                     if (tid == 0) atomicMax(status, 4);
@@ -1784,20 +1786,20 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
         if (k == 0) {
             if (tid < B && d.timing) {
                 const unsigned long long seq = t + (unsigned long long)tid;
-                GpuTimingSlot& ts = d.timing[seq & d.timing_mask];
-                ts.t_pop_clk = S.t_pop;
-                ts.t_done_clk = t_done;
-                ts.seq = (unsigned int)seq;
-                ts.owner = (S.own[tid] && S.p2[tid] && S.p3[tid]) ? 1u : 0u;
-                ts.t_push_ns = S.tpush[tid];
-                ts.t_emit_ns = S.temit[tid];
+                SSLA_GLOBAL GpuTimingSlot* ts = gmem(d.timing) + (seq & d.timing_mask);
+                ts->t_pop_clk = S.t_pop;
+                ts->t_done_clk = t_done;
+                ts->seq = (unsigned int)seq;
+                ts->owner = (S.own[tid] && S.p2[tid] && S.p3[tid]) ? 1u : 0u;
+                ts->t_push_ns = S.tpush[tid];
+                ts->t_emit_ns = S.temit[tid];
             }
             __threadfence_system();
             __syncthreads();
             if (tid == 0) {
-                __hip_atomic_store(d.tail, t + (unsigned long long)B, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(gmem(d.tail), t + (unsigned long long)B, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
                 if (d.events_done)
-                    __hip_atomic_store(d.events_done, t + (unsigned long long)B, __ATOMIC_RELEASE,
+                    __hip_atomic_store(gmem(d.events_done), t + (unsigned long long)B, __ATOMIC_RELEASE,
                                        __HIP_MEMORY_SCOPE_SYSTEM);
             }
             mark(S, PF_PUBLISH);

@@ -20,6 +20,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include "drain_common.h"
 #include "ssla_abi.h"
 
 namespace ssla {
@@ -30,10 +31,6 @@ constexpr int kKSplit = 8;    // K parts of the contraction
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-// Global-memory accesses through address-space-1 pointers: pointers that
-// reach device code as generic values (loaded from descriptor tables) would
-// otherwise compile to flat instructions that also wait on the LDS counter.
-#define SSLA_GLOBAL __attribute__((address_space(1)))
 __device__ __forceinline__ float gload(const float* p) {
     return *(const SSLA_GLOBAL float*)p;
 }
