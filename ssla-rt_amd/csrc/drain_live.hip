@@ -651,15 +651,19 @@ __device__ __forceinline__ void batch_head_yolox(SL& S, int nh, const LiveWeight
 // raw7 = head_W^T x + head_b, one wave per record.
 // Prediction-grid write of thread tid's record: the last owned pass-3
 // record of each s3 cell writes its cell (version += the cell's owned
-// pass-3 records of the batch).  The cell's version word (host memory) is
-// read here, ahead of the head, so its latency overlaps other work.
+// pass-3 records of the batch).  The cell's current version comes from
+// `vsh`, a device-memory copy of the block's version words that only this
+// workgroup reads and writes (the device is the words' only writer), or,
+// without one, from the version word itself (host memory) -- read here,
+// ahead of the head.
 struct PredPlan {
     int cell = -1;
     unsigned count = 0, old = 0;
 };
 
 template <class SL>
-__device__ __forceinline__ PredPlan pred_plan(SL& S, int B, const LiveDesc& d) {
+__device__ __forceinline__ PredPlan pred_plan(SL& S, int B, const LiveDesc& d,
+                                              unsigned* vsh = nullptr) {
     PredPlan p;
     const int tid = threadIdx.x;
     if (tid >= 64) return p;
@@ -682,7 +686,12 @@ __device__ __forceinline__ PredPlan pred_plan(SL& S, int B, const LiveDesc& d) {
         if (last && hx >= 0 && hx < w && hy >= 0 && hy < h) {
             p.cell = hy * w + hx;
             p.count = (unsigned)count;
-            p.old = pred_version(d.version ? d.version + p.cell : nullptr);
+            if (vsh) {
+                p.old = gmem(vsh)[p.cell];
+                gmem(vsh)[p.cell] = (p.old + p.count) & ~kPredBusy;
+            } else {
+                p.old = pred_version(d.version ? d.version + p.cell : nullptr);
+            }
         }
     }
     return p;
@@ -800,7 +809,8 @@ __device__ __forceinline__ void clock_sync(unsigned long long* cs, unsigned long
 }
 
 
-// Loads B records starting at ring slot `first` (slots wrap with `mask`):
+// Loads records e0..B-1 of the batch at ring slot `first` (slots wrap with
+// `mask`):
 // eight threads per record, each reading one 16-byte piece of it (the ring
 // is fine-grained host memory, where every load is a PCIe read request:
 // 8 per record instead of 30 separate 4- and 8-byte ones).  Piece 0 holds
@@ -808,11 +818,12 @@ __device__ __forceinline__ void clock_sync(unsigned long long* cs, unsigned long
 // timestamps.
 template <class SL>
 __device__ __forceinline__ void load_batch(SL& S, int B, const HybridInputRec* ring, unsigned long long first,
-                           unsigned long long mask, const HybridStrip& s, const Geometry& G) {
+                           unsigned long long mask, const HybridStrip& s, const Geometry& G,
+                           int e0 = 0) {
     static_assert(sizeof(HybridInputRec) == 128, "eight 16-byte pieces per record");
     const int tid = threadIdx.x;
-    if (tid < B * 8) {
-        const int e = tid >> 3, q = tid & 7;
+    if (tid < (B - e0) * 8) {
+        const int e = e0 + (tid >> 3), q = tid & 7;
         typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
         const u32x4 v = gmem(reinterpret_cast<const u32x4*>(&ring[(first + e) & mask]))[q];
         if (q >= 1 && q <= 6) {
@@ -1053,7 +1064,7 @@ struct alignas(16) LdsG {
     unsigned pbits[LB];
     unsigned dmask;
     int ol[LB];
-    int nlead, nout, bsize, flag, prof_on, abort_;
+    int nlead, nout, bsize, flag, prof_on, abort_, nspec;
     unsigned xseq;                       // exchanges done by the group
     unsigned long long t_pop, tprev;
     unsigned long long prof[NPROF];
@@ -1325,7 +1336,7 @@ template <class F>
 __device__ __forceinline__ bool group_stage_b(int B, const LiveDesc& d, const LiveWeights& W,
                                              const Geometry& G, GroupCtx gc,
                                              const float* const* goT, const float* const* ipT,
-                                             unsigned char* td3, F l6_done) {
+                                             unsigned char* td3, unsigned* vsh, F l6_done) {
     LdsG& S = g_ldsg;
     const int tid = threadIdx.x;
     if (tid < B) {
@@ -1344,7 +1355,7 @@ __device__ __forceinline__ bool group_stage_b(int B, const LiveDesc& d, const Li
     l6_done();
     // member 0's prediction-grid versions, read while L7 runs
     PredPlan pp;
-    if (gc.k == 0 && W.have_head) pp = pred_plan(S, B, d);
+    if (gc.k == 0 && W.have_head) pp = pred_plan(S, B, d, vsh);
     if (!group_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], W.pk.pp[3], goT[3], ipT[3], d.hidden[3], gc, PF_L7))
         return false;
     if (gc.k == 0 && W.have_head) batch_head(S, B, d, W, &pp);
@@ -1356,9 +1367,9 @@ __device__ __forceinline__ bool process_group(int B, const LiveDesc& d, const Li
                                            const Geometry& G, GroupCtx gc,
                                            const float* const* goT, const float* const* ipT,
                                            unsigned char* td2,
-                                           unsigned char* td3) {
+                                           unsigned char* td3, unsigned* vsh) {
     if (!group_stage_a(B, d, W, G, gc, goT, ipT, td2)) return false;
-    return group_stage_b(B, d, W, G, gc, goT, ipT, td3, [] {});
+    return group_stage_b(B, d, W, G, gc, goT, ipT, td3, vsh, [] {});
 }
 
 // Two-stage groups (live drain): per block a group A of G workgroups runs
@@ -1387,6 +1398,7 @@ struct GroupArgs {
     unsigned long long* hb;              // hand-off words, kHStride per block (zeroed; 2 stages)
     const float* goT[4];                 // OutPackT goW fragments of L4..L7
     const float* ipT[4];                 // OutPackT input_proj fragments (L4, L6; else null)
+    unsigned* vsh;                       // prediction-version copies, C3 words per block
     unsigned long long wait_ticks;
     int G;
     int stages;                          // 1, or 2 (live drain only)
@@ -1438,7 +1450,7 @@ __device__ __forceinline__ void group_live_stage_b(LdsG& S, const LiveDesc& d,
                                                    unsigned char* td3,
                                                    unsigned long long idle_ticks,
                                                    unsigned int spin_ns, int* status,
-                                                   unsigned long long* hb) {
+                                                   unsigned long long* hb, unsigned* vsh) {
     const int tid = threadIdx.x, k = gc.k;
     const int sleep_iters = (int)(spin_ns / 40u) + 1;
     unsigned long long t = d.t0;
@@ -1523,7 +1535,7 @@ __device__ __forceinline__ void group_live_stage_b(LdsG& S, const LiveDesc& d,
         }
         // L6's exchange has every member's partial sums, so every member has
         // read the hand-off: member 0 acknowledges its slot
-        const bool ok = group_stage_b(B, d, W, G, gc, ga.goT, ga.ipT, td3, [&] {
+        const bool ok = group_stage_b(B, d, W, G, gc, ga.goT, ga.ipT, td3, vsh, [&] {
             if (k == 0 && threadIdx.x == 0) xput(hb + kHAck + (hseq & 1u), xword(0u, tag));
         });
         if (!ok) {
@@ -1585,11 +1597,20 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
         S.abort_ = 0;
         S.xseq = 0;
     }
+    // the workgroup that publishes predictions starts its copy of the
+    // block's version words
+    unsigned* vsh = nullptr;
+    if (k == 0 && stage == ST - 1 && W.have_head && d.version && ga.vsh) {
+        vsh = ga.vsh + (size_t)b * G.C3;
+        const HybridStrip& s = d.strip;
+        const int nc = (s.s3_owned_hi - s.s3_owned_lo) * (s.s3_owned_y_hi - s.s3_owned_y_lo);
+        for (int c = tid; c < nc; c += LT) gmem(vsh)[c] = pred_version(d.version + c);
+    }
     __syncthreads();
     if constexpr (ST == 2) {
         if (stage == 1) {
             group_live_stage_b(S, d, W, G, ga, gc, td3, idle_ticks, spin_ns, status,
-                               ga.hb + (size_t)b * kHStride);
+                               ga.hb + (size_t)b * kHStride, vsh);
             return;
         }
     }
@@ -1606,7 +1627,7 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
             load_batch(S, B, d.ring, (unsigned long long)base, ~0ull, d.strip, G);
             __syncthreads();
             mark(S, PF_LOAD);
-            if (!process_group(B, d, W, G, gc, ga.goT, ga.ipT, td2, td3)) {
+            if (!process_group(B, d, W, G, gc, ga.goT, ga.ipT, td2, td3, vsh)) {
                 if (tid == 0) atomicMax(status, 4);
                 return;
             }
@@ -1655,6 +1676,7 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
     unsigned long long ping_seen = 0;
     while (true) {
         __syncthreads();
+        int have = 0;                    // records of the batch already in LDS (members)
         if (k == 0) {
             // poll: wave 0 probes 64 consecutive tags (as k_live)
             if (tid < 64) {
@@ -1685,6 +1707,24 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
                 continue;
             }
         } else {
+            // the ring's ready prefix as this member sees it, loaded while
+            // member 0 decides the batch (records beyond that batch are
+            // loaded again with the next one)
+            if (tid < 64) {
+                SSLA_GLOBAL unsigned long long* tag =
+                    gmem(const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done));
+                const unsigned long long s = __hip_atomic_load(tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                const unsigned long long bal = __ballot(s == t + (unsigned long long)tid + 1ull);
+                const int lead = (int)__ffsll((long long)~bal) - 1;
+                if (tid == 0) S.nspec = min(lead < 0 ? 64 : lead, max_batch);
+            }
+            __syncthreads();
+            have = S.nspec;
+            if (have > 0) {
+                // pairs with the producer's release store of the tags
+                __atomic_thread_fence(__ATOMIC_ACQUIRE);
+                load_batch(S, have, d.ring, t, mask, d.strip, G);
+            }
             if (tid == 0) {
                 // member 0 broadcasts at least once per idle timeout (then it stops)
                 const unsigned long long dl = last_work + idle_ticks + gc.wait_ticks;
@@ -1719,8 +1759,9 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
             if (k == 0) prof_end(S, d, pstage);
             return;
         }
-        if (k != 0 && tid < B) {
-            // the producer's tags of this batch (member 0 has seen them)
+        if (k != 0 && tid >= have && tid < B) {
+            // the producer's tags of the rest of this batch (member 0 has
+            // seen them)
             SSLA_GLOBAL unsigned long long* tag = gmem(const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done));
             const unsigned long long want = t + (unsigned long long)tid + 1ull;
             const unsigned long long dl = (unsigned long long)wall_clock64() + gc.wait_ticks;
@@ -1738,17 +1779,17 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
             return;
         }
         // pairs with the producer's release store of the tags
-        __atomic_thread_fence(__ATOMIC_ACQUIRE);
+        if (B > have) __atomic_thread_fence(__ATOMIC_ACQUIRE);
         if (tid == 0) {
             S.t_pop = (unsigned long long)wall_clock64();
             S.tprev = S.t_pop;
         }
-        load_batch(S, B, d.ring, t, mask, d.strip, G);
+        if (B > have) load_batch(S, B, d.ring, t, mask, d.strip, G, have);
         __syncthreads();
         mark(S, PF_LOAD);
         bool ok;
         if constexpr (ST == 2) ok = group_stage_a(B, d, W, G, gc, ga.goT, ga.ipT, td2);
-        else ok = process_group(B, d, W, G, gc, ga.goT, ga.ipT, td2, td3);
+        else ok = process_group(B, d, W, G, gc, ga.goT, ga.ipT, td2, td3, vsh);
         if (!ok) {
             if (tid == 0) {
                 atomicMax(status, 4);
@@ -2097,8 +2138,10 @@ struct GroupRes {
     unsigned char* tdrep = nullptr;
     float* pack = nullptr;
     float* packT = nullptr;
-    size_t xcap = 0, hcap = 0, tdcap = 0;      // bytes allocated
+    unsigned* vsh = nullptr;
+    size_t xcap = 0, hcap = 0, tdcap = 0, vcap = 0;      // bytes allocated
     void release() {
+        if (vsh) (void)hipFree(vsh);
         if (xb) (void)hipFree(xb);
         if (hb) (void)hipFree(hb);
         if (tdrep) (void)hipFree(tdrep);
@@ -2155,6 +2198,7 @@ static int group_setup(const HybridS2S3Config* cfg, const Geometry& G, int group
     // nothing on later calls of the same or smaller sizes)
     int rc = grow((void**)&r->xb, &r->xcap, xbytes);
     if (!rc) rc = grow((void**)&r->tdrep, &r->tdcap, (size_t)nb * stages * (group - 1) * per);
+    if (!rc) rc = grow((void**)&r->vsh, &r->vcap, sizeof(unsigned) * nb * (size_t)G.C3);
     if (rc) return rc;
     if (!r->pack) LHIP(hipMalloc(&r->pack, sizeof(float) * packed_weight_floats()));
     if (!r->packT) LHIP(hipMalloc(&r->packT, sizeof(float) * packed_weight_floats_d()));
@@ -2177,6 +2221,7 @@ static int group_setup(const HybridS2S3Config* cfg, const Geometry& G, int group
     ga->xb = r->xb;
     ga->hb = r->hb;
     ga->tdrep = r->tdrep;
+    ga->vsh = r->vsh;
     ga->stages = stages;
     ga->goT[0] = pt.po[0] + OutPackT<SSLA_C1, SSLA_C2>::Q;
     ga->goT[1] = pt.po[1] + OutPackT<SSLA_C2, SSLA_C2>::Q;
