@@ -1102,6 +1102,47 @@ __device__ __forceinline__ unsigned long long xwait(unsigned long long* w, unsig
     return v;
 }
 
+// NCH projection chains of one wave over the batch's records (A: 16-record
+// tiles of S.X): chain c multiplies by ProjPack item it[c] (16 weight
+// columns) and its outputs go to columns cl[c] .. cl[c] + 15 of the pair
+// rows (record, dl[c]) of the records that have that pair.
+template <int IN, int OUT, int NCH>
+__device__ __forceinline__ void group_proj(LdsG& S, int B, const float* __restrict__ pp,
+                                           const int* it, const int* dl, const int* cl, int lane) {
+    using P = ProjPack<IN, OUT>;
+    const int li = lane & 15, lk = lane >> 4;
+    // the weight addresses are formed here, per call: kept out of the
+    // persistent loop's registers
+    const float* w = pp;
+    asm volatile("" : "+s"(w));
+    float b[NCH][P::KS4 * 4];
+    #pragma unroll
+    for (int c = 0; c < NCH; ++c) P::load(w, it[c], lane, b[c]);
+    const float* X = &S.X[0][0];
+    for (int m0 = 0; m0 < B; m0 += MT) {
+        const int xr = min(m0 + li, B - 1) * XS + lk;
+        f32x4 a[NCH];
+        #pragma unroll
+        for (int c = 0; c < NCH; ++c) a[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        #pragma unroll
+        for (int s = 0; s < P::KS; ++s) {
+            const float x = X[xr + s * 4];
+            #pragma unroll
+            for (int c = 0; c < NCH; ++c) a[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, b[c][s], a[c], 0, 0, 0);
+        }
+        #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int rr = m0 + 4 * lk + r;
+            if (rr < B) {
+                const unsigned pb = S.pbits[rr];
+                #pragma unroll
+                for (int c = 0; c < NCH; ++c)
+                    if ((pb >> dl[c]) & 1u) S.PR[rr * kPatch + dl[c]][cl[c] + li] = a[c][r];
+            }
+        }
+    }
+}
+
 // One layer for one member; false when a wait of the exchange ran out.
 template <int IN, int OUT>
 __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char* set,
@@ -1123,40 +1164,40 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
     }
     const int k = gc.k, G = gc.G;
     const int ns = k < NSL ? (NSL - 1 - k) / G + 1 : 0;      // own slices k, k + G, ...
-    // P: units (delta, own slice): the batch's records (A, 16-record tiles)
-    // times the slice's q, v and g weight columns, three MFMA chains over
-    // one A tile; rows of the records with a pair at delta are kept.  q is
-    // written for every pair; the recurrence reads it only for output pairs.
+    // P: the batch's records (A, 16-record tiles) times weight columns of
+    // the member's slices, one MFMA chain per (delta, q / v / g, slice);
+    // rows of the records with a pair at the delta are kept.  q is written
+    // for every pair; the recurrence reads it only for output pairs.  With
+    // one slice, wave w takes delta w's three chains and waves 1..3 one of
+    // delta 8's each, so each wave loads its weights in one round; else
+    // waves take (delta, slice) units of three chains in turn.
+    static_assert(NW == 8, "one wave per delta 0..7");
     const unsigned dmask = S.dmask;
-    for (int u = wv; u < kPatch * ns; u += NW) {
-        const int d = u / ns, js = u - d * ns;
-        if (!((dmask >> d) & 1u)) continue;
-        const int j = k + js * G;
-        float bq[P::KS4 * 4], bv[P::KS4 * 4], bg[P::KS4 * 4];
-        P::load(pp, d * P::T + j, lane, bq);
-        P::load(pp, d * P::T + NSL + j, lane, bv);
-        P::load(pp, d * P::T + 2 * NSL + j, lane, bg);
-        const float* X = &S.X[0][0];
-        for (int m0 = 0; m0 < B; m0 += MT) {
-            const int xr = min(m0 + li, B - 1) * XS + lk;
-            f32x4 aq = {0.f, 0.f, 0.f, 0.f}, av = aq, ag = aq;
-            #pragma unroll
-            for (int s = 0; s < P::KS; ++s) {
-                const float x = X[xr + s * 4];
-                aq = __builtin_amdgcn_mfma_f32_16x16x4f32(x, bq[s], aq, 0, 0, 0);
-                av = __builtin_amdgcn_mfma_f32_16x16x4f32(x, bv[s], av, 0, 0, 0);
-                ag = __builtin_amdgcn_mfma_f32_16x16x4f32(x, bg[s], ag, 0, 0, 0);
-            }
-            #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int rr = m0 + 4 * lk + r;
-                if (rr < B && ((S.pbits[rr] >> d) & 1u)) {
-                    float* row = S.PR[rr * kPatch + d];
-                    row[js * MT + li] = aq[r];
-                    row[(GSL + js) * MT + li] = av[r];
-                    row[(2 * GSL + js) * MT + li] = ag[r];
-                }
-            }
+    if (ns == 1 && dmask) {
+        const int d = wv, xo = wv - 1;
+        const bool x4 = xo >= 0 && xo < 3;
+        const int it[4] = {d * P::T + k, d * P::T + NSL + k, d * P::T + 2 * NSL + k,
+                           8 * P::T + xo * NSL + k};
+        const int dl[4] = {d, d, d, 8};
+        const int cl[4] = {0, GSL * MT, 2 * GSL * MT, xo * GSL * MT};
+        if constexpr (P::KS4 * 4 <= 16) {
+            if (x4 && ((dmask >> 8) & 1u)) group_proj<IN, OUT, 4>(S, B, pp, it, dl, cl, lane);
+            else if ((dmask >> d) & 1u) group_proj<IN, OUT, 3>(S, B, pp, it, dl, cl, lane);
+        } else {
+            // 96 inputs: the fourth chain's weights after the first three's
+            // MFMAs (four chains' weights at once would not fit the registers)
+            if ((dmask >> d) & 1u) group_proj<IN, OUT, 3>(S, B, pp, it, dl, cl, lane);
+            if (x4 && ((dmask >> 8) & 1u)) group_proj<IN, OUT, 1>(S, B, pp, it + 3, dl + 3, cl + 3, lane);
+        }
+    } else if (dmask) {
+        for (int u = wv; u < kPatch * ns; u += NW) {
+            const int d = u / ns, js = u - d * ns;
+            if (!((dmask >> d) & 1u)) continue;
+            const int j = k + js * G;
+            const int it[3] = {d * P::T + j, d * P::T + NSL + j, d * P::T + 2 * NSL + j};
+            const int dl[3] = {d, d, d};
+            const int cl[3] = {js * MT, (GSL + js) * MT, (2 * GSL + js) * MT};
+            group_proj<IN, OUT, 3>(S, B, pp, it, dl, cl, lane);
         }
     }
     __syncthreads();
