@@ -277,8 +277,8 @@ void ssla_hip_timing_free(HybridS2S3Config* cfg, int blk);
  * first loads a batch and runs tdrop_s2, L4 and L5, then hands the batch
  * (through device memory) to the second, which runs tdrop_s3, L6, L7, the
  * head and the predictions while the first takes the next batch.  The
- * ring tail advances once the first group holds a batch; events_done and
- * the timing slots once the second has finished it.
+ * ring tail, events_done and the timing slots advance once the second
+ * group has finished a batch.
  * The kernel runs on its own non-blocking stream; do not call
  * ssla_hip_device_synchronize while it runs. */
 typedef struct SslaHipLive SslaHipLive;

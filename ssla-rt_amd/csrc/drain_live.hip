@@ -993,9 +993,12 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
         __threadfence_system();
         __syncthreads();
         if (tid == 0) {
-            __hip_atomic_store(gmem(d.tail), t, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            // one release for both stores (a second release store would
+            // wait for the first to reach host memory)
+            __atomic_thread_fence(__ATOMIC_RELEASE);
+            __hip_atomic_store(gmem(d.tail), t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             if (d.events_done)
-                __hip_atomic_store(gmem(d.events_done), t, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(gmem(d.events_done), t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
         mark(S, PF_PUBLISH);
         if (tid == 0) {
@@ -1066,6 +1069,7 @@ struct alignas(16) LdsG {
     int ol[LB];
     int nlead, nout, bsize, flag, prof_on, abort_, nspec;
     unsigned xseq;                       // exchanges done by the group
+    unsigned hack;                       // stage A: hand-offs acknowledged by B, last read
     unsigned long long t_pop, tprev;
     unsigned long long prof[NPROF];
 };
@@ -1417,20 +1421,23 @@ __device__ __forceinline__ bool process_group(int B, const LiveDesc& d, const Li
 // the batch load, tdrop_s2, the s2 pairs, L4 and L5, then hands the batch
 // to a group B of G more workgroups, which runs tdrop_s3, the s3 pairs, L6,
 // L7, the head, the predictions and the timing slots -- while A takes the
-// next batch.  The hand-off goes through two slots of tagged words (as the
-// exchanges: each 64-bit word carries the hand-off's sequence number, so a
-// reader that sees the tag sees the value): a header (batch size and exit
-// flag), the batch's pop time, and per record its s2 coordinates and flags,
-// both timestamps and its L5 output row.  B's member 0 acknowledges a slot
-// once L6's exchange has completed (every member of B has read it); A's
-// member 0 writes hand-off n + 2 into the slot only after that
-// acknowledgement of hand-off n.  A advances the ring tail after its stage
-// (the ring slots are then free: A holds the records), B the events_done
-// counter after its stage.  Waits are bounded as the exchanges' are.
+// next batch.  The hand-off goes through a ring of kHSlots slots of tagged
+// words (as the exchanges: each 64-bit word carries the hand-off's sequence
+// number, so a reader that sees the tag sees the value): a header (batch
+// size and exit flag), the batch's pop time, and per record its s2
+// coordinates and flags, both timestamps and its L5 output row.  B's member
+// 0 acknowledges hand-off n (one word: the count of hand-offs taken) once
+// L6's exchange has completed (every member of B has read it); A's member 0
+// writes hand-off n into slot n mod kHSlots only when hand-off n - kHSlots
+// has been acknowledged, re-reading the word only when the count it last
+// read does not show that.  B advances the ring tail (A read the batch's
+// slots before handing it over) and the events_done counter after its
+// stage.  Waits are bounded as the exchanges' are.
 constexpr int kHRec = 5 + SSLA_C2;                  // words per record
+constexpr unsigned kHSlots = 16;                    // hand-off slots per block
 constexpr size_t kHSlot = 3 + (size_t)LB * kHRec;   // header, pop time (2), records
-constexpr size_t kHAck = 2 * kHSlot;                // two acknowledgement words
-constexpr size_t kHStride = (kHAck + 2 + 31) & ~(size_t)31;   // words per block
+constexpr size_t kHAck = kHSlots * kHSlot;          // the acknowledgement word
+constexpr size_t kHStride = (kHAck + 1 + 31) & ~(size_t)31;   // words per block
 
 struct GroupArgs {
     unsigned long long* xb;              // exchange words, kXStride per block and stage (zeroed)
@@ -1445,17 +1452,28 @@ struct GroupArgs {
     int stages;                          // 1, or 2 (live drain only)
 };
 
-// Stage A's member 0: hand-off `hseq` (slot hseq & 1) of B records, or of an
-// exit flag; false when the slot's previous acknowledgement did not arrive.
+// Stage A's member 0: hand-off `hseq` (slot hseq mod kHSlots) of B records,
+// or of an exit flag; false when the slot's previous hand-off was not
+// acknowledged in time.  S.hack holds the acknowledged count last read.
 __device__ __forceinline__ bool handoff_put(LdsG& S, unsigned long long* hb, unsigned hseq, int B,
                                             int flag, unsigned long long wait_ticks) {
     const int tid = threadIdx.x;
-    unsigned long long* hs = hb + (size_t)(hseq & 1u) * kHSlot;
+    unsigned long long* hs = hb + (size_t)(hseq % kHSlots) * kHSlot;
     if (tid == 0) {
         bool late = false;
-        if (hseq >= 2u) {
+        const unsigned need = hseq - kHSlots + 1u;       // taken count that frees the slot
+        if (hseq >= kHSlots && (int)(S.hack - need) < 0) {
             const unsigned long long dl = (unsigned long long)wall_clock64() + wait_ticks;
-            (void)xwait(hb + kHAck + (hseq & 1u), hseq - 1u, dl, late);
+            unsigned long long v = __hip_atomic_load(hb + kHAck, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            while ((int)((unsigned)(v >> 32) - need) < 0) {
+                if ((unsigned long long)wall_clock64() > dl) {
+                    late = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                v = __hip_atomic_load(hb + kHAck, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            S.hack = (unsigned)(v >> 32);
         }
         S.abort_ = late ? 1 : 0;
     }
@@ -1499,7 +1517,7 @@ __device__ __forceinline__ void group_live_stage_b(LdsG& S, const LiveDesc& d,
     unsigned hseq = 0;
     while (true) {
         __syncthreads();
-        unsigned long long* hs = hb + (size_t)(hseq & 1u) * kHSlot;
+        unsigned long long* hs = hb + (size_t)(hseq % kHSlots) * kHSlot;
         const unsigned tag = hseq + 1u;
         if (tid == 0) {
             // stage A hands off at least once per idle timeout (then it stops)
@@ -1575,9 +1593,9 @@ __device__ __forceinline__ void group_live_stage_b(LdsG& S, const LiveDesc& d,
             return;
         }
         // L6's exchange has every member's partial sums, so every member has
-        // read the hand-off: member 0 acknowledges its slot
+        // read the hand-off: member 0 acknowledges it (the count taken)
         const bool ok = group_stage_b(B, d, W, G, gc, ga.goT, ga.ipT, td3, vsh, [&] {
-            if (k == 0 && threadIdx.x == 0) xput(hb + kHAck + (hseq & 1u), xword(0u, tag));
+            if (k == 0 && threadIdx.x == 0) xput(hb + kHAck, xword(0u, tag));
         });
         if (!ok) {
             if (tid == 0) atomicMax(status, 4);
@@ -1598,9 +1616,17 @@ __device__ __forceinline__ void group_live_stage_b(LdsG& S, const LiveDesc& d,
             }
             __threadfence_system();
             __syncthreads();
-            if (tid == 0 && d.events_done)
-                __hip_atomic_store(gmem(d.events_done), t + (unsigned long long)B, __ATOMIC_RELEASE,
+            if (tid == 0) {
+                // the batch's ring slots (stage A read them before handing
+                // the batch over); one release for both stores (a second
+                // release store would wait for the first to reach host memory)
+                __atomic_thread_fence(__ATOMIC_RELEASE);
+                __hip_atomic_store(gmem(d.tail), t + (unsigned long long)B, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_SYSTEM);
+                if (d.events_done)
+                    __hip_atomic_store(gmem(d.events_done), t + (unsigned long long)B, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+            }
             mark(S, PF_PUBLISH);
         }
         t += (unsigned long long)B;
@@ -1637,6 +1663,7 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
         if (k != 0) S.prof_on = 0;
         S.abort_ = 0;
         S.xseq = 0;
+        S.hack = 0;
     }
     // the workgroup that publishes predictions starts its copy of the
     // block's version words
@@ -1843,12 +1870,8 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
             return;
         }
         if constexpr (ST == 2) {
-            // stage A: the ring slots are free (every member holds the batch),
-            // and the batch goes to stage B
+            // stage A: the batch goes to stage B
             if (k == 0) {
-                if (tid == 0)
-                    __hip_atomic_store(gmem(d.tail), t + (unsigned long long)B, __ATOMIC_RELEASE,
-                                       __HIP_MEMORY_SCOPE_SYSTEM);
                 if (!handoff_put(S, hb, hseq, B, 0, gc.wait_ticks)) {
                     if (tid == 0) atomicMax(status, 4);
                     prof_end(S, d, pstage);
@@ -1879,9 +1902,13 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
             __threadfence_system();
             __syncthreads();
             if (tid == 0) {
-                __hip_atomic_store(gmem(d.tail), t + (unsigned long long)B, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+                // one release for both stores (a second release store would
+                // wait for the first to reach host memory)
+                __atomic_thread_fence(__ATOMIC_RELEASE);
+                __hip_atomic_store(gmem(d.tail), t + (unsigned long long)B, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
                 if (d.events_done)
-                    __hip_atomic_store(gmem(d.events_done), t + (unsigned long long)B, __ATOMIC_RELEASE,
+                    __hip_atomic_store(gmem(d.events_done), t + (unsigned long long)B, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_SYSTEM);
             }
             mark(S, PF_PUBLISH);
