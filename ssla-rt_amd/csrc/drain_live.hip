@@ -215,32 +215,54 @@ __device__ __forceinline__ float wave_sumf(float v) {
 // Arrival-rank tdrop for one batch (wave 0; lane = record).  All lanes read
 // the counter in one load before the last record of each cell stores the
 // advanced value.
+// In two parts, so that other wave-0 work can run while the counters load:
+// tdrop_begin (every lane of wave 0) ranks the records and issues the
+// counter loads, tdrop_end sets the pass flags and stores the counters.
+struct TdropLane {
+    int c;
+    unsigned rank, cnt;
+    bool live, last;
+};
+
+__device__ __forceinline__ TdropLane tdrop_begin(int B, const unsigned char* td, const int* cell,
+                                                 const unsigned char* mask) {
+    const int e = threadIdx.x;
+    TdropLane r;
+    // lane j's cell when record j is live, else -1; the other lanes' keys
+    // are read from registers (the whole wave runs the loop)
+    r.c = e < B ? cell[e] : -1;
+    r.live = r.c >= 0 && (mask == nullptr || mask[e]);
+    const int key = r.live ? r.c : -1;
+    r.rank = 0;
+    r.last = true;
+    for (int j = 0; j < B; ++j) {
+        const bool lj = __builtin_amdgcn_readlane(key, j) == key;
+        if (lj && j < e) ++r.rank;
+        if (lj && j > e) r.last = false;
+    }
+    r.cnt = r.live ? (unsigned)gmem(td)[r.c] : 0u;
+    return r;
+}
+
+__device__ __forceinline__ void tdrop_end(int B, unsigned char* td, unsigned char* pass, int window,
+                                          const TdropLane& r) {
+    const int e = threadIdx.x;
+    if (e >= B) return;
+    if (!r.live) {
+        pass[e] = 0;
+        return;
+    }
+    const unsigned pre = (r.cnt + r.rank) & 255u;
+    pass[e] = (window <= 1 || pre % (unsigned)window == 0u) ? 1 : 0;
+    if (r.last) gmem(td)[r.c] = (unsigned char)((r.cnt + r.rank + 1u) & 255u);
+}
+
 template <class SL>
 __device__ __forceinline__ void batch_tdrop(SL& S, int B, unsigned char* td, const int* cell,
                             const unsigned char* mask, unsigned char* pass, int window) {
     if (threadIdx.x >= 64) return;
-    const int e = threadIdx.x;
-    // lane j's cell when record j is live, else -1; the other lanes' keys
-    // are read from registers (the whole wave runs the loop)
-    const int c = e < B ? cell[e] : -1;
-    const bool live = c >= 0 && (mask == nullptr || mask[e]);
-    const int key = live ? c : -1;
-    int rank = 0;
-    bool last = true;
-    for (int j = 0; j < B; ++j) {
-        const bool lj = __builtin_amdgcn_readlane(key, j) == key;
-        if (lj && j < e) ++rank;
-        if (lj && j > e) last = false;
-    }
-    if (e >= B) return;
-    if (!live) {
-        pass[e] = 0;
-        return;
-    }
-    const unsigned cnt = gmem(td)[c];
-    const unsigned pre = (cnt + (unsigned)rank) & 255u;
-    pass[e] = (window <= 1 || pre % (unsigned)window == 0u) ? 1 : 0;
-    if (last) gmem(td)[c] = (unsigned char)((cnt + (unsigned)rank + 1u) & 255u);
+    const TdropLane r = tdrop_begin(B, td, cell, mask);
+    tdrop_end(B, td, pass, window, r);
 }
 
 // (record, delta) pairs of the records in `set` on an Hl x Wl grid.  Pair
@@ -251,46 +273,49 @@ __device__ __forceinline__ void batch_tdrop(SL& S, int B, unsigned char* td, con
 // the records with a pair there (dev, dcnt).  Then one thread per pair: its
 // record and cell, its successor at the cell (the pair of the first later
 // record of the set whose patch holds the cell) and whether it leads the
-// cell (no earlier record's patch holds it).  Ends with a barrier.
-template <class SL, bool LISTS = true>
-__device__ __forceinline__ void build_pairs(SL& S, int B, const unsigned char* set, int Hl, int Wl) {
-    const int tid = threadIdx.x;
-    if (tid < 64) {
-        const int e = tid;
-        const bool in = e < B && set[e];
-        const int ex = in ? S.ex[e] : 0, ey = in ? S.ey[e] : 0;
-        unsigned bits = 0;
-        if (in) {
-            #pragma unroll
-            for (int d = 0; d < kPatch; ++d) {
-                const int ty = ey + 1 - d / 3, tx = ex + 1 - d % 3;
-                if (ty >= 0 && ty < Hl && tx >= 0 && tx < Wl) bits |= 1u << d;
-            }
-        }
-        if (e == 0) {
-            S.dmask = 0u;
-            S.nlead = 0;
-        }
-        if (e < LB) {
-            S.pbits[e] = bits;
-            S.pk[e] = in ? ((unsigned)ex | ((unsigned)ey << 16)) : 0xffffffffu;
-            #pragma unroll
-            for (int d = 0; d < kPatch; ++d) S.pidx[e][d] = ((bits >> d) & 1u) ? e * kPatch + d : -1;
-        }
-        if (bits) atomicOr(&S.dmask, bits);   // after lane 0's store: one wave, LDS order
-        if constexpr (LISTS) {
-            const unsigned long long lt = (1ull << e) - 1ull;
-            #pragma unroll
-            for (int d = 0; d < kPatch; ++d) {
-                const bool has = (bits >> d) & 1u;
-                const unsigned long long bal = __ballot(has);
-                if (has) S.dev[d][__popcll(bal & lt)] = e;
-                if (e == 0) S.dcnt[d] = __popcll(bal);
-            }
+// cell (no earlier record's patch holds it).  pairs_wave0: the per-record
+// part (wave 0, every lane).
+template <class SL, bool LISTS>
+__device__ __forceinline__ void pairs_wave0(SL& S, int B, const unsigned char* set, int Hl, int Wl) {
+    const int e = threadIdx.x;
+    const bool in = e < B && set[e];
+    const int ex = in ? S.ex[e] : 0, ey = in ? S.ey[e] : 0;
+    unsigned bits = 0;
+    if (in) {
+        #pragma unroll
+        for (int d = 0; d < kPatch; ++d) {
+            const int ty = ey + 1 - d / 3, tx = ex + 1 - d % 3;
+            if (ty >= 0 && ty < Hl && tx >= 0 && tx < Wl) bits |= 1u << d;
         }
     }
-    __syncthreads();
-    // O(B) per pair
+    if (e == 0) {
+        S.dmask = 0u;
+        S.nlead = 0;
+    }
+    if (e < LB) {
+        S.pbits[e] = bits;
+        S.pk[e] = in ? ((unsigned)ex | ((unsigned)ey << 16)) : 0xffffffffu;
+        #pragma unroll
+        for (int d = 0; d < kPatch; ++d) S.pidx[e][d] = ((bits >> d) & 1u) ? e * kPatch + d : -1;
+    }
+    if (bits) atomicOr(&S.dmask, bits);   // after lane 0's store: one wave, LDS order
+    if constexpr (LISTS) {
+        const unsigned long long lt = (1ull << e) - 1ull;
+        #pragma unroll
+        for (int d = 0; d < kPatch; ++d) {
+            const bool has = (bits >> d) & 1u;
+            const unsigned long long bal = __ballot(has);
+            if (has) S.dev[d][__popcll(bal & lt)] = e;
+            if (e == 0) S.dcnt[d] = __popcll(bal);
+        }
+    }
+}
+
+// The pairs' records, cells, successors and leads (after pairs_wave0 and a
+// barrier); O(B) per pair.  Ends with a barrier.
+template <class SL>
+__device__ __forceinline__ void pairs_links(SL& S, int B, int Wl) {
+    const int tid = threadIdx.x;
     for (int p = tid; p < kPatch * B; p += LT) {
         const int e = p / kPatch, d = p - e * kPatch;
         if (!((S.pbits[e] >> d) & 1u)) continue;
@@ -311,6 +336,13 @@ __device__ __forceinline__ void build_pairs(SL& S, int B, const unsigned char* s
         if (lead) S.lead[atomicAdd(&S.nlead, 1)] = p;
     }
     __syncthreads();
+}
+
+template <class SL, bool LISTS = true>
+__device__ __forceinline__ void build_pairs(SL& S, int B, const unsigned char* set, int Hl, int Wl) {
+    if (threadIdx.x < 64) pairs_wave0<SL, LISTS>(S, B, set, Hl, Wl);
+    __syncthreads();
+    pairs_links(S, B, Wl);
 }
 
 // P: scratch[pair][0, 3*OUT) = [q | v | g] of the pair's (record, delta),
@@ -711,6 +743,7 @@ __device__ __forceinline__ void batch_head(SL& S, int B, const LiveDesc& d, cons
     const PredPlan pp = plan ? *plan : pred_plan(S, B, d);
     __syncthreads();
     const int nh = S.nout;
+    if (nh == 0) return;                // no head rows and no prediction cell
     if (W.have_head == kHeadLinear) {
         const int wv = tid >> 6, lane = tid & 63;
         for (int r = wv; r < nh; r += NW) {
@@ -1305,6 +1338,14 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
     }
     if (tid == 0) xput(xh + k, xword(0u, tag));
     mark(S, slot + 2);
+    // the LayerNorm weights of the lane's channels, loaded ahead of the wait
+    float lg[2], lbt[2];
+    #pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int ch = lane + 64 * h;
+        lg[h] = ch < OUT ? gmem(L.ln_gamma)[ch] : 0.f;
+        lbt[h] = ch < OUT ? gmem(L.ln_beta)[ch] : 0.f;
+    }
     // sums of the members' partials (member order), then the identity residual
     const int ncon = (G < NSL ? G : NSL) + (IPR && NSL < G ? 1 : 0);
     const unsigned long long deadline = (unsigned long long)wall_clock64() + gc.wait_ticks;
@@ -1345,10 +1386,8 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
         const double db = lane + 64 < OUT ? (double)b - mean : 0.0;
         const double var = wave_sum(da * da + db * db) / (double)OUT;
         const double inv = 1.0 / sqrt(var + 1e-5);
-        if (lane < OUT)
-            S.X[e][lane] = (float)(da * inv * (double)L.ln_gamma[lane] + (double)L.ln_beta[lane]);
-        if (lane + 64 < OUT)
-            S.X[e][lane + 64] = (float)(db * inv * (double)L.ln_gamma[lane + 64] + (double)L.ln_beta[lane + 64]);
+        if (lane < OUT) S.X[e][lane] = (float)(da * inv * (double)lg[0] + (double)lbt[0]);
+        if (lane + 64 < OUT) S.X[e][lane + 64] = (float)(db * inv * (double)lg[1] + (double)lbt[1]);
     }
     __syncthreads();
     mark(S, slot + 3);
@@ -1364,10 +1403,15 @@ __device__ __forceinline__ bool group_stage_a(int B, const LiveDesc& d, const Li
                                              const float* const* goT, const float* const* ipT,
                                              unsigned char* td2) {
     LdsG& S = g_ldsg;
-    batch_tdrop(S, B, td2, S.c2, nullptr, S.p2, G.window);
+    // wave 0: tdrop_s2 with the per-record pair setup while its counters load
+    if (threadIdx.x < 64) {
+        const TdropLane r = tdrop_begin(B, td2, S.c2, nullptr);
+        pairs_wave0<LdsG, false>(S, B, S.vld, G.H2, G.W2);
+        tdrop_end(B, td2, S.p2, G.window, r);
+    }
     __syncthreads();
     mark(S, PF_TD2);
-    build_pairs<LdsG, false>(S, B, S.vld, G.H2, G.W2);
+    pairs_links(S, B, G.W2);
     mark(S, PF_PAIRS2);
     if (!group_layer<SSLA_C1, SSLA_C2>(S, B, S.vld, nullptr, W.L[0], W.pk.pp[0], goT[0], ipT[0], d.hidden[0], gc, PF_L4))
         return false;
@@ -1384,16 +1428,21 @@ __device__ __forceinline__ bool group_stage_b(int B, const LiveDesc& d, const Li
                                              unsigned char* td3, unsigned* vsh, F l6_done) {
     LdsG& S = g_ldsg;
     const int tid = threadIdx.x;
-    if (tid < B) {
-        S.ex[tid] >>= 1;
-        S.ey[tid] >>= 1;
-        S.c3[tid] = S.vld[tid] ? S.ey[tid] * G.W3 + S.ex[tid] : -1;
+    // wave 0 (lane = record): pooling to s3, then tdrop_s3 with the
+    // per-record pair setup while its counters load
+    if (tid < 64) {
+        if (tid < B) {
+            S.ex[tid] >>= 1;
+            S.ey[tid] >>= 1;
+            S.c3[tid] = S.vld[tid] ? S.ey[tid] * G.W3 + S.ex[tid] : -1;
+        }
+        const TdropLane r = tdrop_begin(B, td3, S.c3, S.p2);
+        pairs_wave0<LdsG, false>(S, B, S.p2, G.H3, G.W3);
+        tdrop_end(B, td3, S.p3, G.window, r);
     }
     __syncthreads();
-    batch_tdrop(S, B, td3, S.c3, S.p2, S.p3, G.window);
-    __syncthreads();
     mark(S, PF_TD3);
-    build_pairs<LdsG, false>(S, B, S.p2, G.H3, G.W3);
+    pairs_links(S, B, G.W3);
     mark(S, PF_PAIRS3);
     if (!group_layer<SSLA_C2, SSLA_C3>(S, B, S.p2, nullptr, W.L[2], W.pk.pp[2], goT[2], ipT[2], d.hidden[2], gc, PF_L6))
         return false;
