@@ -87,6 +87,7 @@ struct LiveDesc {
 namespace {
 
 constexpr int LB = kLiveBatchMax;   // records per batch, at most
+constexpr int kSpecTags = 8;        // ring slots a group member probes ahead of the batch word
 constexpr int LT = 512;             // threads per workgroup
 constexpr int NW = LT / 64;         // waves per workgroup
 constexpr int LP = kPatch * LB;     // pairs per layer, at most
@@ -1470,20 +1471,24 @@ __device__ __forceinline__ bool process_group(int B, const LiveDesc& d, const Li
 // the batch load, tdrop_s2, the s2 pairs, L4 and L5, then hands the batch
 // to a group B of G more workgroups, which runs tdrop_s3, the s3 pairs, L6,
 // L7, the head, the predictions and the timing slots -- while A takes the
-// next batch.  The hand-off goes through a ring of kHSlots slots of tagged
-// words (as the exchanges: each 64-bit word carries the hand-off's sequence
-// number, so a reader that sees the tag sees the value): a header (batch
-// size and exit flag), the batch's pop time, and per record its s2
-// coordinates and flags, both timestamps and its L5 output row.  B's member
-// 0 acknowledges hand-off n (one word: the count of hand-offs taken) once
-// L6's exchange has completed (every member of B has read it); A's member 0
-// writes hand-off n into slot n mod kHSlots only when hand-off n - kHSlots
-// has been acknowledged, re-reading the word only when the count it last
-// read does not show that.  B advances the ring tail (A read the batch's
-// slots before handing it over) and the events_done counter after its
-// stage.  Waits are bounded as the exchanges' are.
+// next batch.  The hand-off goes through kHSlots slots of tagged words (as
+// the exchanges: each 64-bit word carries the hand-off's sequence number,
+// so a reader that sees the tag sees the value): a header (batch size and
+// exit flag), the batch's pop time, and per record its s2 coordinates and
+// flags, both timestamps and its L5 output row.  B's member 0 acknowledges
+// hand-off n (one word: the count of hand-offs taken) once L6's exchange
+// has completed (every member of B has read it); A's member 0 writes
+// hand-off n into slot n mod kHSlots only when hand-off n - kHSlots has been
+// acknowledged, re-reading the word only when the count it last read does
+// not show that.  Two slots keep A at most two batches ahead of B: where B
+// is the slower stage, A then takes bigger batches instead of queueing
+// small ones in front of B (16 slots let 16 rings' B stages fall 16 batches
+// behind: push -> prediction p50 570 us against 100).  B advances the ring
+// tail (A read the batch's slots before handing it over) and the
+// events_done counter after its stage.  Waits are bounded as the
+// exchanges' are.
 constexpr int kHRec = 5 + SSLA_C2;                  // words per record
-constexpr unsigned kHSlots = 16;                    // hand-off slots per block
+constexpr unsigned kHSlots = 2;                     // hand-off slots per block
 constexpr size_t kHSlot = 3 + (size_t)LB * kHRec;   // header, pop time (2), records
 constexpr size_t kHAck = kHSlots * kHSlot;          // the acknowledgement word
 constexpr size_t kHStride = (kHAck + 1 + 31) & ~(size_t)31;   // words per block
@@ -1795,15 +1800,19 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
         __syncthreads();
         int have = 0;                    // records of the batch already in LDS (members)
         if (k == 0) {
-            // poll: wave 0 probes 64 consecutive tags (as k_live)
+            // poll: lanes 0 .. max_batch - 1 of wave 0 probe consecutive tags
+            // (one host-memory read each)
             if (tid < 64) {
-                SSLA_GLOBAL unsigned long long* tag = gmem(const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done));
-                const unsigned long long s = __hip_atomic_load(tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                const bool ready = s == t + (unsigned long long)tid + 1ull;
+                unsigned long long s = 0;
+                if (tid < max_batch) {
+                    SSLA_GLOBAL unsigned long long* tag =
+                        gmem(const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done));
+                    s = __hip_atomic_load(tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                }
+                const bool ready = tid < max_batch && s == t + (unsigned long long)tid + 1ull;
                 const unsigned long long bal = __ballot(ready);
                 const int lead = (int)__ffsll((long long)~bal) - 1;
-                int n = lead < 0 ? 64 : lead;
-                if (n > max_batch) n = max_batch;
+                const int n = lead < 0 ? 64 : lead;    // <= max_batch
                 const bool lapped = (tid == 0) && s > t + 1ull;
                 if (tid == 0) {
                     clock_sync(d.clk_sync, ping_seen);
@@ -1824,16 +1833,22 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
                 continue;
             }
         } else {
-            // the ring's ready prefix as this member sees it, loaded while
-            // member 0 decides the batch (records beyond that batch are
-            // loaded again with the next one)
+            // the ring's ready prefix as this member sees it (its first
+            // kSpecTags slots at most: each probe is a host-memory read, and
+            // every member of every block polls), loaded while member 0
+            // decides the batch (records beyond that batch are loaded again
+            // with the next one)
             if (tid < 64) {
-                SSLA_GLOBAL unsigned long long* tag =
-                    gmem(const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done));
-                const unsigned long long s = __hip_atomic_load(tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                const unsigned long long bal = __ballot(s == t + (unsigned long long)tid + 1ull);
+                const int np = min(max_batch, kSpecTags);
+                unsigned long long s = 0;
+                if (tid < np) {
+                    SSLA_GLOBAL unsigned long long* tag =
+                        gmem(const_cast<unsigned long long*>(&d.ring[(t + tid) & mask].seq_done));
+                    s = __hip_atomic_load(tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                }
+                const unsigned long long bal = __ballot(tid < np && s == t + (unsigned long long)tid + 1ull);
                 const int lead = (int)__ffsll((long long)~bal) - 1;
-                if (tid == 0) S.nspec = min(lead < 0 ? 64 : lead, max_batch);
+                if (tid == 0) S.nspec = lead < 0 ? 64 : lead;    // <= np
             }
             __syncthreads();
             have = S.nspec;
