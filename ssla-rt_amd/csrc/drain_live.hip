@@ -1189,7 +1189,8 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
                                             const float* __restrict__ goT,
                                             const float* __restrict__ ipT,
                                             float* __restrict__ hidden, const GroupCtx& gc,
-                                            int slot) {
+                                            int slot, bool may_skip = false,
+                                            unsigned long long* ack = nullptr) {
     using P = ProjPack<IN, OUT>;
     constexpr int NSL = OUT / MT;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -1240,6 +1241,13 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
     }
     __syncthreads();
     mark(S, slot + 0);
+    // ack (stage A's L5): a lane of wave 7, idle from here at live batch
+    // sizes, reads the hand-off acknowledgement count; it lands in S.hack
+    // before the layer's last barrier, so the hand-off after it rarely
+    // waits on a read of its own
+    constexpr int kAckLane = 7 * 64;
+    unsigned long long ackv = 0;
+    if (ack && tid == kAckLane) ackv = __hip_atomic_load(ack, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // S: one lane per (cell, own channel); q*h replaces q for output pairs
     {
         constexpr int CH = 8;
@@ -1277,6 +1285,19 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
     unsigned long long* xs = gc.xb + (size_t)par * kXSet;
     unsigned long long* xh = gc.xb + kXHdr + (size_t)par * kGroupMax;
     const int no = S.nout;
+    // may_skip: with no output record (every member counts the same ones)
+    // there are no partial sums to exchange and no LayerNorm; the group's
+    // exchanges stay in step, since every member skips the same ones
+    if (may_skip && no == 0) {
+        if (ack) {
+            if (tid == kAckLane && (int)((unsigned)(ackv >> 32) - S.hack) > 0) S.hack = (unsigned)(ackv >> 32);
+            __syncthreads();
+        }
+        mark(S, slot + 2);
+        mark(S, PF_XWAIT + (slot == PF_L4 ? 0 : slot == PF_L5 ? 1 : slot == PF_L6 ? 2 : 3));
+        mark(S, slot + 3);
+        return true;
+    }
     // the input_proj residual (IN != OUT) is one member's extra K slice: the
     // first member without a channel slice, else member 0
     constexpr bool IPR = IN != OUT;
@@ -1390,6 +1411,7 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
         if (lane < OUT) S.X[e][lane] = (float)(da * inv * (double)lg[0] + (double)lbt[0]);
         if (lane + 64 < OUT) S.X[e][lane + 64] = (float)(db * inv * (double)lg[1] + (double)lbt[1]);
     }
+    if (ack && tid == kAckLane && (int)((unsigned)(ackv >> 32) - S.hack) > 0) S.hack = (unsigned)(ackv >> 32);
     __syncthreads();
     mark(S, slot + 3);
     return true;
@@ -1402,7 +1424,7 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
 __device__ __forceinline__ bool group_stage_a(int B, const LiveDesc& d, const LiveWeights& W,
                                              const Geometry& G, GroupCtx gc,
                                              const float* const* goT, const float* const* ipT,
-                                             unsigned char* td2) {
+                                             unsigned char* td2, unsigned long long* ack = nullptr) {
     LdsG& S = g_ldsg;
     // wave 0: tdrop_s2 with the per-record pair setup while its counters load
     if (threadIdx.x < 64) {
@@ -1416,7 +1438,8 @@ __device__ __forceinline__ bool group_stage_a(int B, const LiveDesc& d, const Li
     mark(S, PF_PAIRS2);
     if (!group_layer<SSLA_C1, SSLA_C2>(S, B, S.vld, nullptr, W.L[0], W.pk.pp[0], goT[0], ipT[0], d.hidden[0], gc, PF_L4))
         return false;
-    return group_layer<SSLA_C2, SSLA_C2>(S, B, S.vld, S.p2, W.L[1], W.pk.pp[1], goT[1], ipT[1], d.hidden[1], gc, PF_L5);
+    return group_layer<SSLA_C2, SSLA_C2>(S, B, S.vld, S.p2, W.L[1], W.pk.pp[1], goT[1], ipT[1], d.hidden[1], gc, PF_L5,
+                                         true, ack);
 }
 
 // Stage B: pooling to s3, tdrop_s3, the s3 pairs, L6, L7 and (member 0) the
@@ -1451,7 +1474,8 @@ __device__ __forceinline__ bool group_stage_b(int B, const LiveDesc& d, const Li
     // member 0's prediction-grid versions, read while L7 runs
     PredPlan pp;
     if (gc.k == 0 && W.have_head) pp = pred_plan(S, B, d, vsh);
-    if (!group_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], W.pk.pp[3], goT[3], ipT[3], d.hidden[3], gc, PF_L7))
+    if (!group_layer<SSLA_C3, SSLA_C3>(S, B, S.p2, S.p3, W.L[3], W.pk.pp[3], goT[3], ipT[3], d.hidden[3], gc, PF_L7,
+                                       true))
         return false;
     if (gc.k == 0 && W.have_head) batch_head(S, B, d, W, &pp);
     return true;
@@ -1920,7 +1944,8 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
         __syncthreads();
         mark(S, PF_LOAD);
         bool ok;
-        if constexpr (ST == 2) ok = group_stage_a(B, d, W, G, gc, ga.goT, ga.ipT, td2);
+        if constexpr (ST == 2)
+            ok = group_stage_a(B, d, W, G, gc, ga.goT, ga.ipT, td2, k == 0 ? hb + kHAck : nullptr);
         else ok = process_group(B, d, W, G, gc, ga.goT, ga.ipT, td2, td3, vsh);
         if (!ok) {
             if (tid == 0) {
