@@ -7,9 +7,10 @@
 // workgroup-wide phases per layer:
 //   tdrop   one wave, one lane per record: arrival rank among the batch's
 //           records at the same cell (ssla_ref.py:190-195)
-//   pairs   one wave builds the (record, delta) pairs in record order and the
-//           per-delta record lists; one thread per pair finds the next pair
-//           at its cell among the later records' patches
+//   pairs   pair (record e, delta d) has the fixed index 9 e + d; one wave
+//           sets up each record's pairs and the per-delta record lists, then
+//           one thread per pair finds the next pair at its cell among the
+//           later records' patches
 //   P       q, v, g as 16 x 16 MFMA tiles: per delta, the records with a
 //           pair there times the delta's weight columns; v and g for every
 //           pair, q only for the pairs of the layer's output records
@@ -26,7 +27,10 @@
 // another.
 //
 // The live kernel polls a ring in fine-grained host memory: one wave loads
-// 64 consecutive seq_done tags and takes the ready prefix.  It stops on the
+// up to max_batch consecutive seq_done tags and takes the ready prefix
+// (groups: member 0 decides; the other members probe a few slots
+// themselves and load what they see ready before the batch word comes).
+// It stops on the
 // host's stop flag, on a ring overrun, or after an idle timeout on the
 // constant-rate wall clock, so every wave always reaches an exit.
 //
@@ -1067,10 +1071,11 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
 // Two word sets alternate by sequence parity.  A member writes exchange
 // n + 2 only after reading exchange n + 1 from every member, each of which
 // wrote it after reading exchange n, so no word is overwritten before every
-// member has read it.  Every exchange (also one without output records)
-// carries a header word per member; the L4 exchange of each batch is thus
-// a group barrier, and member 0 advances the ring tail and broadcasts the
-// next batch only after every member has loaded this one.  Every wait is
+// member has read it.  Every exchange carries a header word per member; the
+// L4 exchange of each batch is thus a group barrier, and member 0 broadcasts
+// the next batch only after every member has loaded this one.  L5's and
+// L7's exchanges are left out, by every member alike, when the batch has no
+// output record for them.  Every wait is
 // bounded on the wall clock: a member whose wait runs out sets status 4
 // and leaves, and the others' waits then run out in turn.
 // ---------------------------------------------------------------------------
