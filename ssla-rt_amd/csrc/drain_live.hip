@@ -1319,6 +1319,14 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
             f32x4 c3[3];
             #pragma unroll
             for (int q = 0; q < 3; ++q) c3[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+            // the residual's input_proj fragments load with the goW ones
+            using OT = OutPackT<IN, OUT>;
+            f32x4 ar[KG];
+            if (has_res) {
+                #pragma unroll
+                for (int t = 0; t < KG; ++t)
+                    ar[t] = ((const SSLA_GLOBAL f32x4*)ipT)[((size_t)ot * KG + t) * 64 + lane];
+            }
             for (int js = 0; js < ns; ++js) {
                 f32x4 a[kPatch];
                 #pragma unroll
@@ -1338,11 +1346,6 @@ __device__ __forceinline__ bool group_layer(LdsG& S, int B, const unsigned char*
             if (has_res) {
                 // input_proj's fragments (OutPackT order); B: the record's
                 // input, channels OutPackT::kidx(t, lk, i)
-                using OT = OutPackT<IN, OUT>;
-                f32x4 ar[KG];
-                #pragma unroll
-                for (int t = 0; t < KG; ++t)
-                    ar[t] = ((const SSLA_GLOBAL f32x4*)ipT)[((size_t)ot * KG + t) * 64 + lane];
                 #pragma unroll
                 for (int t = 0; t < KG; ++t) {
                     f32x4 v = {0.f, 0.f, 0.f, 0.f};
