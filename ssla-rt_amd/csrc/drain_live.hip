@@ -1027,8 +1027,9 @@ k_live(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, const int* st
         }
         t += (unsigned long long)B;
         last_work = t_done;
-        // predictions and timing of this batch become visible before the tail
-        __threadfence_system();
+        // predictions and timing of this batch (written by the record
+        // threads, all in wave 0) become visible before the tail
+        if (tid < 64) __threadfence_system();
         __syncthreads();
         if (tid == 0) {
             // one release for both stores (a second release store would
@@ -1700,7 +1701,9 @@ __device__ __forceinline__ void group_live_stage_b(LdsG& S, const LiveDesc& d,
                 ts->t_push_ns = S.tpush[tid];
                 ts->t_emit_ns = S.temit[tid];
             }
-            __threadfence_system();
+            // the batch's timing slots and predictions: written by the record
+            // threads, all in wave 0
+            if (tid < 64) __threadfence_system();
             __syncthreads();
             if (tid == 0) {
                 // the batch's ring slots (stage A read them before handing
@@ -1996,7 +1999,9 @@ k_group(const LiveDesc* __restrict__ ld, LiveWeights W, Geometry G, GroupArgs ga
                 ts->t_push_ns = S.tpush[tid];
                 ts->t_emit_ns = S.temit[tid];
             }
-            __threadfence_system();
+            // the batch's timing slots and predictions: written by the record
+            // threads, all in wave 0
+            if (tid < 64) __threadfence_system();
             __syncthreads();
             if (tid == 0) {
                 // one release for both stores (a second release store would
