@@ -60,9 +60,13 @@ def inbounds(x, y, H, W):
 def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20):
     """Algorithmic work of each launch of the whole-ring drain: the minimal
     MACs of the reference's skipping semantics (L5 output and L6/L7 only for
-    pass2, L7 output and head for pass3) and the bytes each launch must move
-    through HBM at its interface (rows in, rows out; weights excluded, they
-    stay in cache).  Returns ({phase: flops}, {phase: bytes}, total MACs)."""
+    pass2, L7 output and head for pass3), the algorithmic bytes of the
+    measurement's per-record accounting (each layer's input rows, the
+    hidden-state read and write per pair, the output slots; weights excluded,
+    they stay in cache) and the bytes each launch moves at its interface,
+    which also counts this design's intermediates (the projections' [v | g]
+    pair rows, the recurrence's h rows).  Returns ({phase: flops},
+    {phase: algorithmic bytes}, {phase: interface bytes}, total MACs)."""
     x = x.astype(np.int64)
     y = y.astype(np.int64)
     n2 = inbounds(x, y, H2, W2)
@@ -86,7 +90,7 @@ def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20):
         "head": int((m3 & (owner == 1)).sum()) * (2 * C3 * C3 + 7 * C3),
     }
     flops = {k: 2.0 * v for k, v in mac.items()}
-    byts = {
+    iface = {
         "L4.proj": F * (N * C1 + S2 * 2 * C2),
         "L4.out": F * (S2 * C2 + N * C1 + N * C2),
         "L5.proj": F * (N * C2 + S2 * 2 * C2),
@@ -96,17 +100,31 @@ def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20):
         "L7.proj": F * (N2 * C3 + S3p * 2 * C3),
         "L7.out": F * (S3pp * C3 + 2 * N3 * C3),
     }
-    # the recurrence h = sigmoid(g) h + v over every pair entering the layer:
-    # one launch (k_scan, in the apply slot) reads each pair's v, g once and
-    # writes h where the output is consumed (sigmoid ~ 4 FLOP, the map
-    # composition and the replay 2 FMA)
+    # algorithmic: a projection reads its layer's input rows, a contraction
+    # those and writes its output rows
+    byts = {
+        "L4.proj": F * N * C1,
+        "L4.out": F * (N * C1 + N * C2),
+        "L5.proj": F * N * C2,
+        "L5.out": F * 2 * N2 * C2,
+        "L6.proj": F * N2 * C2,
+        "L6.out": F * (N2 * C2 + N2 * C3),
+        "L7.proj": F * N2 * C3,
+        "L7.out": F * 2 * N3 * C3,
+    }
+    # the recurrence h = sigmoid(g) h + v over every pair entering the layer
+    # (sigmoid ~ 4 FLOP, the map composition and the replay 2 FMA):
+    # algorithmically the pair's hidden state is read and written; one launch
+    # (k_scan, in the apply slot) reads each pair's v, g rows once and writes
+    # h where the output is consumed
     for L, pairs, need, out in (("L4", S2, S2, C2), ("L5", S2, S2p, C2),
                                 ("L6", S3p, S3p, C3), ("L7", S3p, S3pp, C3)):
-        byts[f"{L}.apply"] = F * (pairs * 2 * out + need * out)
+        byts[f"{L}.apply"] = F * pairs * out * 2
+        iface[f"{L}.apply"] = F * (pairs * 2 * out + need * out)
         flops[f"{L}.apply"] = 6.0 * pairs * out
-    byts["emit"] = float(N * 392)
+    byts["emit"] = iface["emit"] = float(N * 392)
     total_mac = sum(mac.values())
-    return flops, byts, total_mac
+    return flops, byts, iface, total_mac
 
 
 def _cpu_model() -> str:
@@ -440,12 +458,14 @@ def _roofline_phase(per):
     return max(single, key=single.get)
 
 
-def _roofline(per, flops, byts, dom):
+def _roofline(per, flops, byts, iface, dom):
     kname = PHASE_KERNEL.get(dom, dom)
     traffic = hbm_traffic(dom)
-    fl, by = flops.get(dom, 0.0), byts.get(dom, 0.0)
+    fl, by, ib = flops.get(dom, 0.0), byts.get(dom, 0.0), iface.get(dom, 0.0)
     base = {"kernel": f"{kname} ({dom})", "traffic": traffic, "avg_launch_ms": round(per[dom], 5),
-            "algorithmic_bytes_per_launch": int(by), "algorithmic_flops_per_launch": int(fl)}
+            "algorithmic_bytes_per_launch": int(by), "algorithmic_flops_per_launch": int(fl),
+            "interface_bytes_per_launch": int(ib),
+            "interface_gbs": round(ib / (per[dom] * 1e-3) / 1e9, 1)}
     tr = trace_ms(dom)
     if by > 0 and fl / by < RIDGE:
         ach = by / (per[dom] * 1e-3) / 1e9
@@ -903,16 +923,15 @@ def main() -> int:
     ms_step = dt * 1e3 / steps
     value = n_out * steps / dt / 1e3
     ring_rate = n * S * steps / dt / 1e3
-    flops, byts, total_mac = {}, {}, 0
+    flops, byts, ibyts, total_mac = {}, {}, {}, 0
     for r, o in zip(recs, outs):
-        f_, b_, m_ = algorithmic_work(r.x, r.y, o["pass2"], o["pass3"], np.ones(n, np.int32),
-                                      H2, W2)
-        for k, v in f_.items():
-            flops[k] = flops.get(k, 0.0) + v
-        for k, v in b_.items():
-            byts[k] = byts.get(k, 0.0) + v
+        f_, b_, i_, m_ = algorithmic_work(r.x, r.y, o["pass2"], o["pass3"], np.ones(n, np.int32),
+                                          H2, W2)
+        for src, dst in ((f_, flops), (b_, byts), (i_, ibyts)):
+            for k, v in src.items():
+                dst[k] = dst.get(k, 0.0) + v
         total_mac += m_
-    roof = _roofline(per_timed, flops, byts, roof_phase)
+    roof = _roofline(per_timed, flops, byts, ibyts, roof_phase)
     if a.workload != "80x64":
         roof["traffic"] = None           # the committed PMC summary is of the 80x64 workload
     if roof.get("unit") == "GB/s":
@@ -927,9 +946,14 @@ def main() -> int:
         roof["measured_ceiling_gbs"] = {"write_stream": round(ceil[0], 1),
                                         "copy_read_write": round(ceil[1], 1),
                                         "rows_576B_permuted": round(ceil[2], 1)}
-        roof["frac_of_write_ceiling"] = round(roof["achieved"] / ceil[0], 4)
+        # the launch's interface traffic (rows included) against those ceilings
+        roof["interface_frac_of_write_ceiling"] = round(roof["interface_gbs"] / ceil[0], 4)
+    roof["bytes_note"] = ("achieved / frac: the algorithmic bytes or FLOPs of the launch (for a "
+                          "recurrence, each pair's hidden-state read and write); interface_*: "
+                          "the bytes it moves at its interface, which include this design's "
+                          "own pair rows and h rows; traffic: the committed PMC measurement")
     whole = 2.0 * total_mac / (ms_step * 1e-3) / 1e12
-    iface = sum(byts.values())
+    iface = sum(ibyts.values())
     comp = sum(compulsory_bytes(r.x, r.y, o["pass2"], H2, W2) for r, o in zip(recs, outs))
     measured = hbm_traffic() if a.workload == "80x64" else None
     res = {
@@ -959,12 +983,13 @@ def main() -> int:
         "roofline": roof,
         # every single-kernel phase against its own bound, from the per-phase
         # loop's event times (these include a few us of queue time each)
-        "roofline_by_phase_note": "per launch against its bound; HBM-bound entries are rates on "
-                                  "the launch's interface bytes, which include the design's own "
-                                  "intermediates (pair rows, h rows, chunk maps)",
+        "roofline_by_phase_note": "per launch against its bound, on its algorithmic bytes or "
+                                  "FLOPs; interface_gbs: the rate on the bytes it moves at its "
+                                  "interface, which include the design's own intermediates "
+                                  "(pair rows, h rows)",
         "roofline_by_phase": {
-            k: {x: r[x] for x in ("bound", "achieved", "unit", "frac")}
-            for k, r in ((k, _roofline(per, flops, byts, k)) for k in per
+            k: {x: r[x] for x in ("bound", "achieved", "unit", "frac", "interface_gbs")}
+            for k, r in ((k, _roofline(per, flops, byts, ibyts, k)) for k in per
                          if k not in ("order", "head") and per[k] > 0
                          and (flops.get(k, 0.0) > 0 or byts.get(k, 0.0) > 0))},
     }
