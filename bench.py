@@ -69,11 +69,12 @@ def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20):
     {phase: algorithmic bytes}, {phase: interface bytes}, total MACs)."""
     x = x.astype(np.int64)
     y = y.astype(np.int64)
-    n2 = inbounds(x, y, H2, W2)
-    m2, m3 = p2 == 1, p3 == 1
+    ok = (x >= 0) & (x < W2) & (y >= 0) & (y < H2)     # off-grid records are skipped
+    n2 = np.where(ok, inbounds(x, y, H2, W2), 0)
+    m2, m3 = ok & (p2 == 1), ok & (p3 == 1)
     n3 = inbounds(x >> 1, y >> 1, H2 >> 1, W2 >> 1)
     S2, S2p, S3p, S3pp = n2.sum(), n2[m2].sum(), n3[m2].sum(), n3[m3].sum()
-    N, N2, N3 = x.size, int(m2.sum()), int(m3.sum())
+    N, N2, N3 = int(ok.sum()), int(m2.sum()), int(m3.sum())
     F = 4.0
     # projections compute v, g for every pair entering the layer; the
     # contraction computes q for the pairs of its output records, then
@@ -122,7 +123,7 @@ def algorithmic_work(x, y, p2, p3, owner, H2=16, W2=20):
         byts[f"{L}.apply"] = F * pairs * out * 2
         iface[f"{L}.apply"] = F * (pairs * 2 * out + need * out)
         flops[f"{L}.apply"] = 6.0 * pairs * out
-    byts["emit"] = iface["emit"] = float(N * 392)
+    byts["emit"] = iface["emit"] = float(x.size * 392)     # every ring record's slot
     total_mac = sum(mac.values())
     return flops, byts, iface, total_mac
 
@@ -363,7 +364,7 @@ def compulsory_bytes(x, y, p2, H2=16, W2=20):
     y = y.astype(np.int64)
     ok = (x < W2) & (y < H2)
     n2 = np.where(ok, inbounds(x, y, H2, W2), 0)
-    n3 = np.where(p2 == 1, inbounds(x >> 1, y >> 1, H2 >> 1, W2 >> 1), 0)
+    n3 = np.where(ok & (p2 == 1), inbounds(x >> 1, y >> 1, H2 >> 1, W2 >> 1), 0)
     return float(x.size * (128 + 392 + 2) + n2.sum() * 48 * 4 * 2 * 2 + n3.sum() * 96 * 4 * 2 * 2)
 
 
