@@ -310,9 +310,9 @@ __global__ void __launch_bounds__(kScanThreads) k_exscan(int n, int* __restrict_
     }
 }
 
-constexpr int kCH = 64;     // pairs per scan chunk
-constexpr int kSG = 4;      // chunks per group (workgroup) of the one-pass scan, s2 layers
-constexpr int kSG3 = 2;     // ... s3 layers (two waves per chunk)
+constexpr int kCH = 32;     // pairs per scan chunk
+constexpr int kSG = 8;      // chunks per group (workgroup) of the one-pass scan, s2 layers
+constexpr int kSG3 = 4;     // ... s3 layers (two waves per chunk)
 
 // Chunk tables: one wave per key writes its chunks (ckey, cbeg, cend) and
 // counts the key's groups of the one-pass scan (ghist, gw: k_group_order).
@@ -1143,9 +1143,10 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 // ---------------------------------------------------------------------------
 // S: the per-cell recurrence h = sigmoid(g) h + v over a cell's pairs in ring
 // order, in one pass (k_scan): each pair's v, g row is read once.  A cell's
-// run is cut into chunks of kCH pairs and its chunks into groups (kSG = 4 at
-// s2, kSG3 = 2 at s3); one workgroup takes one group, one wave per chunk and
-// 64 channels (two waves for the 96 channels of L6 and L7):
+// run is cut into chunks of kCH = 32 pairs and its chunks into groups (kSG = 8
+// at s2, kSG3 = 4 at s3: 256 and 128 pairs); one workgroup takes one group,
+// one wave per chunk and 64 channels (two waves for the 96 channels of L6 and
+// L7):
 //   1. each wave loads its chunk's rows into registers (sigmoid(g) in place,
 //      nontemporal loads: the projection has just left up to 0.7 GB of rows
 //      in the caches) and composes the chunk's map h -> A h + B into LDS;
@@ -1171,7 +1172,11 @@ k_qvg(int n_max, const int* __restrict__ n_dev, const int* __restrict__ list,
 // (summary, per-cell carry, apply): L4 0.32 -> 0.26 ms, L5 0.28 -> 0.21,
 // L6 0.14 -> 0.14, L7 0.125 -> 0.12; in cell order a cell's groups all ran at
 // once and waited on each other down the chain (L4 0.39 ms).  One chunk per
-// group at s3 (0.14, 0.13 ms), two or eight at s2 (0.27, 0.31 ms) were slower.
+// group at s3 (0.14, 0.13 ms), two or eight at s2 (0.27, 0.31 ms) were slower
+// with 64-pair chunks.  Chunks of 32 pairs halve a wave's row registers (123
+// VGPRs, no spill, against 168 and 16 B of scratch): L4 0.27 -> 0.26 ms, L5
+// 0.21 -> 0.20, L6 0.13 -> 0.11, L7 0.107 -> 0.090 (1.86 -> 1.80 ms per call);
+// 16-chunk groups (1024 threads) and 16-pair chunks were slower.
 // Published words hold a float and the launch's tag (value | tag << 32)
 // and are stored and loaded with relaxed device-scope atomics: a reader that
 // sees the tag sees the value, with no fence (a release fence would write
